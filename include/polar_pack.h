@@ -1,0 +1,213 @@
+/*
+ * polar_pack_amd -- C ABI of the MI355X (gfx950) fused dequant-matmul decode path.
+ *
+ * Every entry point:
+ *   - takes device pointers (hipMalloc'd memory, or torch CUDA tensors' data_ptr())
+ *     plus plain sizes/strides in ELEMENTS, and a hipStream_t passed as void*;
+ *   - enqueues work on that stream and returns without synchronising;
+ *   - returns PP_OK (0) or a nonzero pp_status; pp_last_error() then returns a
+ *     thread-local message.
+ *
+ * Nothing here allocates device memory except pp_quad_gemm / pp_dual_gemm on the
+ * generic (non fast-path) layouts, which take a caller-provided workspace
+ * (see *_workspace_size) and never call hipMalloc themselves.
+ *
+ * Citations name the reference interface each entry point replaces
+ * (file:line in everymonday100/polar_pack).
+ */
+#ifndef POLAR_PACK_H
+#define POLAR_PACK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum pp_status {
+  PP_OK = 0,
+  PP_EINVAL = 1,       /* bad argument (shape, stride, pointer, enum) */
+  PP_EHIP = 2,         /* a HIP runtime call failed */
+  PP_ENOSUPPORT = 3    /* valid request this build does not implement */
+};
+
+enum pp_dtype { PP_F16 = 0, PP_F32 = 1 };
+
+/* Dual code layouts:
+ *   PP_DUAL_I16_OFFSET -- native int16 = ((amp << 10) | phase) - 32768, the
+ *                         kernel layout of polar_kernels.py:9-11;
+ *   PP_DUAL_U16_BE     -- the .dualpack file layout, big-endian uint16
+ *                         (amp << 10) | phase, polar_bitpack.py:81-88. */
+enum pp_dual_layout { PP_DUAL_I16_OFFSET = 0, PP_DUAL_U16_BE = 1 };
+
+/* Thread-local message describing the last nonzero status. */
+const char* pp_last_error(void);
+
+/* Library version string, and the gfx target it was compiled for. */
+const char* pp_version(void);
+
+/* sizeof of the ABI structs, for binding checks: out[0] = sizeof(pp_quad_proj),
+ * out[1] = sizeof(pp_quad_item).  Returns the number of values written. */
+int pp_abi_sizes(int64_t* out, int n);
+
+/* ------------------------------------------------------------------------ */
+/* Quad pack: uint32 word [norm 8 | t1 8 | t2 8 | t3 8] -> 4 models.          */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Fused decode GEMM over a (K,N) code view:
+ *   out_m[i, n] = fp16( s_m * sum_k a[i, k] * W_m[k, n] ),   m = 0..3,
+ * where W_m is decoded from codes[k*c_sk + n*c_sn] with the 7 LUTs
+ * luts = {norm, cos1, sin1, cos2, sin2, cos3, sin3} (256 entries each,
+ * lut_dtype PP_F16 or PP_F32, device memory):
+ *   w0 = r*c1, w1 = r*s1*c2, w2 = r*s1*s2*c3, w3 = r*s1*s2*s3.
+ *
+ * Replaces quad_bitpacked (quad_kernels.py:146-159) and
+ * quad_bitpacked_kernel (quad_kernels.py:53-143).
+ *
+ * Plug table (optional, plug_n may be 0): entries with
+ *   plug_idx[j] - elem_base == k*c_sk + n*c_sn
+ * replace the decoded normalised tuple of element (k, n) by the fp16 values
+ * plug_vals[4*j .. 4*j+3] (the semantics of quaternion_packer.py:187-193).
+ * plug_idx must be ascending.  Plug entries need one unit stride
+ * (c_sk == 1 or c_sn == 1).
+ *
+ * Fast paths: c_sk == 1 (container layout, codes rows are (N,K) row-major)
+ * with K % 4 == 0, 16-byte aligned rows and M <= 8.  Other layouts decode into
+ * `workspace` (4*K*N floats, see pp_quad_gemm_workspace_size) and multiply.
+ */
+int pp_quad_gemm(const void* a, int64_t a_sm, int64_t a_sk,
+                 const uint32_t* codes, int64_t c_sk, int64_t c_sn,
+                 const void* const* luts, int lut_dtype,
+                 const float* scales,
+                 const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n, int64_t elem_base,
+                 void* const* out, int64_t o_sm, int64_t o_sn,
+                 int64_t M, int64_t N, int64_t K,
+                 void* workspace, int64_t workspace_bytes,
+                 void* stream);
+
+/* Bytes of workspace pp_quad_gemm needs for this call (0 on the fast paths). */
+int64_t pp_quad_gemm_workspace_size(const void* a, int64_t a_sm, int64_t a_sk,
+                                    const uint32_t* codes, int64_t c_sk, int64_t c_sn,
+                                    int64_t plug_n, int64_t M, int64_t N, int64_t K);
+
+/*
+ * Dequantise to float32: out_m[k*N + n] = s_m * W_m[k, n] (plug applied).
+ * Parity / debug export; same operands as pp_quad_gemm.
+ * Replaces the decode half of unpack_quad (quaternion_packer.py:169-196)
+ * for one (K,N) view.
+ */
+int pp_quad_dequant(const uint32_t* codes, int64_t c_sk, int64_t c_sn,
+                    const void* const* luts, int lut_dtype, const float* scales,
+                    const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n, int64_t elem_base,
+                    float* const* out, int64_t N, int64_t K, void* stream);
+
+/*
+ * Whole-stream batch-1 decode: one launch over many projections of one
+ * .quadpack stream (the grouped whole-step launch).  All tables are device
+ * memory prepared by the host once per stream (see polar_pack_amd/stream.py):
+ *
+ *   projs  : n_proj descriptors of pp_quad_proj;
+ *   items  : n_items work items of pp_quad_item (rows of one projection, plus
+ *            their plug range in plug_idx);
+ *   luts   : 7 float32 LUTs from the header (r_max, mu);
+ *   scales : host float[4], the header RMS s_k.
+ *
+ * Rows touching stream positions >= n_codes (FP16 tails) are listed as
+ * items with flags & PP_ITEM_TAIL and decoded from tails[m] (fp16, length
+ * tail_len[m], model m's positions n_codes .. n_codes+tail_len[m]-1).
+ * Replaces the per-projection quad_bitpacked calls of a decode step and the
+ * tail restore of unpack_quad (quaternion_packer.py:201-210).
+ */
+typedef struct pp_quad_proj {
+  const uint32_t* codes;   /* code of (row 0, col 0); row r starts at codes + r*ldc */
+  int64_t ldc;             /* row stride of codes in elements (K for a packed stream) */
+  int64_t pos0;            /* stream position of (row 0, col 0) */
+  const void* x;           /* fp16 activations (M, K), row stride x_sm */
+  int64_t x_sm;
+  void* out[4];            /* fp16 outputs (M, N), row stride o_sm, unit column stride */
+  int64_t o_sm;
+  int32_t N, K;
+} pp_quad_proj;
+
+enum pp_item_flags { PP_ITEM_TAIL = 1 };
+
+/* One wavefront task: rows [row0, row0+nrows) x K slice [k0, k1) of one projection.
+ * Items of one row group that split K share a combine `group` (0..n_groups-1) and
+ * have slice = 0..n_slices-1; an item covering all of K has n_slices == 1. */
+typedef struct pp_quad_item {
+  int32_t proj;            /* index into projs */
+  int32_t row0;            /* first row */
+  int32_t nrows;           /* rows in this item, 1..pp_quad_stream_layout().rows_per_item */
+  int32_t flags;           /* PP_ITEM_*; a TAIL item is one row over all of K */
+  int32_t k0, k1;          /* K slice, multiples of 256 except k1 == K */
+  int32_t group;           /* split-K combine group, or -1 */
+  int32_t slice, n_slices;
+  int32_t pad_;
+  int64_t plug_lo;         /* plug entries [plug_lo, plug_hi) cover these rows */
+  int64_t plug_hi;
+} pp_quad_item;
+
+/* Rows per item and partial-sum floats per (group, slice) the stream decode uses for
+ * M tokens.  The split-K workspace `part` holds n_groups * max_slices * values floats;
+ * `counters` holds n_groups uint32 that must be zero before the first launch (the
+ * kernel leaves them at zero again). */
+int pp_quad_stream_layout(int64_t M, int* rows_per_item, int* values_per_slice);
+
+int pp_quad_stream(const pp_quad_proj* projs, const pp_quad_item* items, int64_t n_items,
+                   const float* const* luts, const float* scales,
+                   const uint32_t* plug_idx, const void* plug_vals,
+                   int64_t n_codes, const void* const* tails, const int64_t* tail_len,
+                   int64_t M, float* part, int64_t max_slices, uint32_t* counters,
+                   void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Dual pack: 16-bit [amp 6 | phase 10] -> 2 models.                          */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Fused decode GEMM over a (K,N) code view:
+ *   out_1[i,n] = fp16(sum_k a[i,k] * amp(k,n) * cos_lut[ph]),
+ *   out_2[i,n] = fp16(sum_k a[i,k] * amp(k,n) * sin_lut[ph]),
+ *   amp(k,n)   = amp_lut[amp_q] * bmax[g(k,n)].
+ * Group index:  chunk_size == 0 selects the kernel-layout rule
+ * g = (k*N + n) // group_size over the logical (K,N) index, whatever the strides
+ * (polar_kernels.py:70-71); chunk_size > 0 selects the container rule on the
+ * stream position p = elem_base + k*c_sk + n*c_sn, where groups restart every
+ * chunk_size positions: g = (p / chunk)*ceil(chunk/gs) + (p % chunk)/gs
+ * (polar_bitpack.py:201-203, 224-238).
+ * Replaces polar_dual_bitpacked (polar_kernels.py:98-115) and
+ * polar_dual_bitpacked_kernel (polar_kernels.py:14-95).
+ * Plug entries (optional) replace the amplitude of the pair at
+ * plug_idx[j] - elem_base by the fp16 plug_amp[j] (polar_bitpack.py:240-243).
+ */
+int pp_dual_gemm(const void* a, int64_t a_sm, int64_t a_sk,
+                 const void* codes, int code_layout, int64_t c_sk, int64_t c_sn,
+                 const void* bmax, int64_t group_size, int64_t chunk_size,
+                 const void* amp_lut, int amp_lut_n, const void* cos_lut, const void* sin_lut,
+                 int phase_n, int lut_dtype,
+                 const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n, int64_t elem_base,
+                 void* out1, void* out2, int64_t o_sm, int64_t o_sn,
+                 int64_t M, int64_t N, int64_t K,
+                 void* workspace, int64_t workspace_bytes,
+                 void* stream);
+
+int64_t pp_dual_gemm_workspace_size(const void* a, int64_t a_sm, int64_t a_sk,
+                                    const void* codes, int64_t c_sk, int64_t c_sn,
+                                    int64_t group_size, int64_t chunk_size, int64_t elem_base,
+                                    int64_t plug_n, int64_t M, int64_t N, int64_t K);
+
+/* Dequantise to float32 (w1, w2) over a (K,N) view; parity / debug export.
+ * Replaces the decode of unpack_dual_models (polar_bitpack.py:228-247). */
+int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk, int64_t c_sn,
+                    const void* bmax, int64_t group_size, int64_t chunk_size,
+                    const void* amp_lut, int amp_lut_n, const void* cos_lut, const void* sin_lut,
+                    int phase_n, int lut_dtype,
+                    const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n, int64_t elem_base,
+                    float* out1, float* out2, int64_t N, int64_t K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POLAR_PACK_H */

@@ -1,0 +1,97 @@
+"""ctypes binding of ``lib/libpolar_pack.so`` (declarations in include/polar_pack.h).
+
+The product path has no fallback: if the library is missing or cannot load,
+:func:`lib` raises, and every operator fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+from .build import LIB
+
+PP_OK, PP_EINVAL, PP_EHIP, PP_ENOSUPPORT = 0, 1, 2, 3
+PP_F16, PP_F32 = 0, 1
+PP_DUAL_I16_OFFSET, PP_DUAL_U16_BE = 0, 1
+PP_ITEM_TAIL = 1
+
+vp = C.c_void_p
+i64 = C.c_int64
+i32 = C.c_int
+
+
+class QuadProj(C.Structure):
+    """``pp_quad_proj`` (include/polar_pack.h)."""
+    _fields_ = [("codes", vp), ("ldc", i64), ("pos0", i64), ("x", vp), ("x_sm", i64),
+                ("out", vp * 4), ("o_sm", i64), ("N", C.c_int32), ("K", C.c_int32)]
+
+
+class QuadItem(C.Structure):
+    """``pp_quad_item`` (include/polar_pack.h)."""
+    _fields_ = [("proj", C.c_int32), ("row0", C.c_int32), ("nrows", C.c_int32), ("flags", C.c_int32),
+                ("k0", C.c_int32), ("k1", C.c_int32), ("group", C.c_int32), ("slice", C.c_int32),
+                ("n_slices", C.c_int32), ("pad_", C.c_int32), ("plug_lo", i64), ("plug_hi", i64)]
+
+
+EXPORTS = {
+    "pp_last_error": (C.c_char_p, []),
+    "pp_version": (C.c_char_p, []),
+    "pp_abi_sizes": (i32, [C.POINTER(i64), i32]),
+    "pp_quad_gemm": (i32, [vp, i64, i64, vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64,
+                           i64, i64, i64, vp, i64, vp]),
+    "pp_quad_gemm_workspace_size": (i64, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64]),
+    "pp_quad_dequant": (i32, [vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
+    "pp_quad_stream_layout": (i32, [i64, C.POINTER(i32), C.POINTER(i32)]),
+    "pp_quad_stream": (i32, [vp, vp, i64, vp, vp, vp, vp, i64, vp, vp, i64, vp, i64, vp, vp]),
+    "pp_dual_gemm": (i32, [vp, i64, i64, vp, i32, i64, i64, vp, i64, i64, vp, i32, vp, vp, i32, i32,
+                           vp, vp, i64, i64, vp, vp, i64, i64, i64, i64, i64, vp, i64, vp]),
+    "pp_dual_gemm_workspace_size": (i64, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64]),
+    "pp_dual_dequant": (i32, [vp, i32, i64, i64, vp, i64, i64, vp, i32, vp, vp, i32, i32, vp, vp, i64, i64,
+                              vp, vp, i64, i64, vp]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def lib_path() -> str:
+    return os.environ.get("POLAR_PACK_LIB", LIB)
+
+
+def lib() -> C.CDLL:
+    """Load the HIP library once; raise if it is absent (no fallback path exists)."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            path = lib_path()
+            if not os.path.exists(path):
+                raise RuntimeError(f"polar_pack_amd: native library {path} is missing; build it with "
+                                   "`python -m polar_pack_amd.build`")
+            h = C.CDLL(path)
+            for name, (res, args) in EXPORTS.items():
+                fn = getattr(h, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = h
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != PP_OK:
+        msg = lib().pp_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {rc}): {msg}")
+
+
+def ptr_array(ptrs, ctype=vp):
+    arr = (ctype * len(ptrs))()
+    for i, p in enumerate(ptrs):
+        arr[i] = p
+    return arr
+
+
+def float_array(vals):
+    arr = (C.c_float * len(vals))()
+    for i, v in enumerate(vals):
+        arr[i] = float(v)
+    return arr

@@ -1,0 +1,172 @@
+"""Dual-pack operators: drop-in for the reference's ``polar_kernels.py``.
+
+Same names, arguments, return values and error behaviour as the reference
+(polar_kernels.py:9-11, 98-151), computed by the gfx950 HIP library:
+
+* :func:`pack_amp_phase` -- int16 ``((amp & 63) << 10 | (phase & 1023)) - 32768``.
+* :func:`quantize_polar_bitpacked` -- per-layer packer (torch on the weights' device).
+* :func:`polar_dual_bitpacked` -- one packed pass -> 2 fp16 GEMM outputs.
+  Keyword-only extensions: ``plug=(idx, amp)`` (``.dualpack`` plug table,
+  polar_bitpack.py:240-243), ``elem_base``, ``layout`` (``"i16"`` kernel layout
+  or ``"u16be"`` file layout) and ``chunk_size`` (0 = the kernel's (k*N + n)
+  group rule, > 0 = the container's stream-position rule).
+* :func:`dual_dequant` -- float32 weights of a code view (parity export).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _native as nat
+from .quad_kernels import _check_device
+
+_LAYOUTS = {"i16": nat.PP_DUAL_I16_OFFSET, "u16be": nat.PP_DUAL_U16_BE}
+
+
+def pack_amp_phase(amp_q, phase_q):
+    """polar_kernels.py:9-11."""
+    packed = ((amp_q.to(torch.int32) & 0x3F) << 10) | (phase_q.to(torch.int32) & 0x3FF)
+    return (packed - 32768).to(torch.int16)
+
+
+def quantize_polar_bitpacked(w1, w2, amp_bits=6, num_phases=1024, mu=255, group_size=32):
+    """Per-layer dual packer (polar_kernels.py:118-151).
+
+    Returns ``(packed int16 (K,N), bmax fp16 flat, amp_lut fp16[2^amp_bits],
+    cos_lut fp16[num_phases], sin_lut fp16[num_phases])`` on w1's device.
+    """
+    K, N = w1.shape
+    amplitude = torch.sqrt(w1 ** 2 + w2 ** 2)
+    phase = torch.atan2(w2, w1)
+    phase_q = (torch.round((phase + math.pi) / (2 * math.pi) * num_phases).long() % num_phases).to(torch.int16)
+    total = K * N
+    flat = amplitude.flatten()
+    pad = (group_size - total % group_size) % group_size
+    if pad:
+        flat = torch.nn.functional.pad(flat, (0, pad))
+    grouped = flat.reshape(-1, group_size)
+    bmax = grouped.abs().max(dim=1, keepdim=True).values
+    bmax = torch.where(bmax > 1e-10, bmax, torch.ones_like(bmax))
+    norm = grouped / bmax
+    log_mu = math.log(1 + mu)
+    compressed = torch.sign(norm) * torch.log1p(mu * norm.abs()) / log_mu
+    levels = (1 << amp_bits) - 1
+    amp_q = torch.round(compressed * levels).clamp(0, levels).to(torch.int8).flatten()[:total].reshape(K, N)
+    bmax = bmax.flatten().to(torch.float16)
+    packed = pack_amp_phase(amp_q, phase_q)
+    phases = torch.linspace(-math.pi, math.pi, num_phases + 1)[:-1]
+    cos_lut = torch.cos(phases).to(torch.float16).to(w1.device)
+    sin_lut = torch.sin(phases).to(torch.float16).to(w1.device)
+    i = torch.arange(levels + 1, dtype=torch.float32)
+    amp_lut = ((torch.exp(i / levels * log_mu) - 1.0) / mu).to(torch.float16).to(w1.device)
+    return packed, bmax, amp_lut, cos_lut, sin_lut
+
+
+def _lut_dtype(*ts):
+    dt = ts[0].dtype
+    for t in ts:
+        if t.dtype != dt or not t.is_contiguous():
+            raise ValueError("dual LUTs must be contiguous tensors of one dtype")
+    if dt == torch.float16:
+        return nat.PP_F16
+    if dt == torch.float32:
+        return nat.PP_F32
+    raise TypeError(f"dual LUT dtype must be float16 or float32, got {dt}")
+
+
+def _codes_view(packed, layout):
+    if layout not in _LAYOUTS:
+        raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}")
+    if packed.element_size() != 2:
+        raise TypeError("dual codes are 16-bit (int16 kernel layout or uint16 big-endian file layout)")
+    return _LAYOUTS[layout]
+
+
+def _dual_plug(plug, device):
+    if plug is None:
+        return None, None, 0, ()
+    idx, amp = plug
+    if idx.dtype not in (torch.uint32, torch.int32) or amp.dtype != torch.float16 or amp.numel() != idx.numel():
+        raise TypeError("plug must be (uint32 idx (P,), float16 amplitude (P,))")
+    idx, amp = idx.contiguous(), amp.contiguous()
+    if idx.device != device or amp.device != device:
+        raise ValueError("plug tensors must be on the codes' device")
+    return idx.data_ptr(), amp.data_ptr(), idx.numel(), (idx, amp)
+
+
+def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases=1024, group_size=32, *,
+                         plug=None, elem_base=0, layout="i16", chunk_size=0):
+    """2 GEMMs from one packed pass (polar_kernels.py:98-115); returns ``(out1, out2)`` fp16 (M,N)."""
+    M, K = a_fp16.shape
+    K_b, N = packed.shape
+    assert K == K_b
+    dev = _check_device(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut)
+    if a_fp16.dtype != torch.float16 or bmax.dtype != torch.float16:
+        raise TypeError("a and bmax must be float16")
+    out1 = torch.empty((M, N), dtype=torch.float16, device=dev)
+    out2 = torch.empty_like(out1)
+    if M == 0 or N == 0:
+        return out1, out2
+    if K == 0:
+        out1.zero_()
+        out2.zero_()
+        return out1, out2
+    lay = _codes_view(packed, layout)
+    lut_dt = _lut_dtype(amp_lut, cos_lut, sin_lut)
+    if cos_lut.numel() != num_phases or sin_lut.numel() != num_phases:
+        raise ValueError("cos_lut / sin_lut must have num_phases entries")
+    a = a_fp16
+    if a.stride(1) != 1 or a.data_ptr() % 8 or (M > 1 and a.stride(0) % 4):
+        a = a.contiguous()
+    bmax = bmax.contiguous()
+    pi, pa, pn, keep = _dual_plug(plug, dev)
+    L = nat.lib()
+    ws_bytes = L.pp_dual_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), packed.data_ptr(),
+                                             packed.stride(0), packed.stride(1), group_size, chunk_size,
+                                             int(elem_base), pn, M, N, K)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = L.pp_dual_gemm(a.data_ptr(), a.stride(0), a.stride(1), packed.data_ptr(), lay, packed.stride(0),
+                        packed.stride(1), bmax.data_ptr(), group_size, chunk_size, amp_lut.data_ptr(),
+                        amp_lut.numel(), cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases, lut_dt, pi, pa, pn,
+                        int(elem_base), out1.data_ptr(), out2.data_ptr(), out1.stride(0), out1.stride(1), M, N, K,
+                        ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    nat.check(rc, "pp_dual_gemm")
+    del keep
+    return out1, out2
+
+
+def dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases=1024, group_size=32, *, plug=None,
+                 elem_base=0, layout="i16", chunk_size=0):
+    """float32 (K,N) weight pair ``(w1, w2)`` of a code view, plug applied."""
+    K, N = packed.shape
+    dev = _check_device(packed, bmax, amp_lut, cos_lut, sin_lut)
+    w1 = torch.empty((K, N), dtype=torch.float32, device=dev)
+    w2 = torch.empty_like(w1)
+    if K * N == 0:
+        return w1, w2
+    lay = _codes_view(packed, layout)
+    lut_dt = _lut_dtype(amp_lut, cos_lut, sin_lut)
+    pi, pa, pn, keep = _dual_plug(plug, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = nat.lib().pp_dual_dequant(packed.data_ptr(), lay, packed.stride(0), packed.stride(1),
+                                   bmax.contiguous().data_ptr(), group_size, chunk_size, amp_lut.data_ptr(),
+                                   amp_lut.numel(), cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases, lut_dt,
+                                   pi, pa, pn, int(elem_base), w1.data_ptr(), w2.data_ptr(), N, K, stream)
+    nat.check(rc, "pp_dual_dequant")
+    del keep
+    return w1, w2
+
+
+def header_luts(amp_bits=6, phase_bits=10, mu=255.0, device=None):
+    """float32 LUTs of a ``.dualpack`` header, computed in float64 and rounded once:
+    amp_lut[i] = expm1(i/levels * ln(1+mu)) / mu and the phase tables of
+    ang = i / 2^phase_bits * 2 pi - pi (polar_bitpack.py:213-215, 237, 245)."""
+    levels = 2 ** amp_bits - 1
+    i = torch.arange(levels + 1, dtype=torch.float64)
+    amp = torch.expm1(i / levels * math.log1p(mu)) / mu
+    nph = 1 << phase_bits
+    j = torch.arange(nph, dtype=torch.float64)
+    ang = j / nph * 2 * math.pi - math.pi
+    return [t.to(torch.float32).to(device) for t in (amp, torch.cos(ang), torch.sin(ang))]

@@ -1,0 +1,175 @@
+"""Quad-pack operators: drop-in for the reference's ``quad_kernels.py``.
+
+Same names, arguments, return values and error behaviour as the reference
+(quad_kernels.py:16-50, 146-159), computed by the gfx950 HIP library:
+
+* :func:`pack_quad_layer` -- 4 (K,N) weight matrices -> uint32 codes (K,N),
+  7 fp16 LUTs, 4 RMS scales (torch on the weights' device; the uint32 words
+  are assembled on the device instead of the reference's numpy round trip).
+* :func:`quad_bitpacked` -- one packed pass -> 4 fp16 GEMM outputs.
+  Keyword-only extensions: ``plug=(idx, vals)`` (the ``.quadpack`` plug table,
+  quaternion_packer.py:187-193) and ``elem_base``.
+* :func:`quad_dequant` -- float32 weights of a code view (parity export).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _native as nat
+
+MU = 255.0   # quad_kernels.py:13
+
+
+def _u32_words(nq, q1, q2, q3):
+    """Assemble [nq|q1|q2|q3] words on the device as a torch.uint32 tensor."""
+    w = (nq.to(torch.int64) << 24) | (q1.to(torch.int64) << 16) | (q2.to(torch.int64) << 8) | q3.to(torch.int64)
+    w = torch.where(w >= 2 ** 31, w - 2 ** 32, w).to(torch.int32)
+    return w.view(torch.uint32)
+
+
+def pack_quad_layer(w1, w2, w3, w4, mu=MU):
+    """Pack 4 weight matrices (K,N) into uint32 codes + LUTs (quad_kernels.py:16-50).
+
+    Returns ``(codes uint32 (K,N) on w1.device, luts [norm, cos1, sin1, cos2,
+    sin2, cos3, sin3] fp16[256] on w1.device, scales [4 floats])``.
+    """
+    ws = [w1, w2, w3, w4]
+    s = [torch.sqrt((w.float() ** 2).mean()) for w in ws]
+    wn = [w.float() / sk for w, sk in zip(ws, s)]
+    r = torch.sqrt(wn[0] ** 2 + wn[1] ** 2 + wn[2] ** 2 + wn[3] ** 2)
+    r_max = float(r.max()) * 1.001
+    log_mu = math.log1p(mu)
+    t1 = torch.atan2(torch.sqrt(wn[1] ** 2 + wn[2] ** 2 + wn[3] ** 2), wn[0])
+    t2 = torch.atan2(torch.sqrt(wn[2] ** 2 + wn[3] ** 2), wn[1])
+    t3 = torch.atan2(wn[3], wn[2]) % (2 * math.pi)
+    nq = torch.round(torch.log1p(mu * r / r_max) / log_mu * 255).clip(0, 255)
+    q1 = torch.round(t1 / math.pi * 255).clip(0, 255)
+    q2 = torch.round(t2 / math.pi * 255).clip(0, 255)
+    q3 = torch.round(t3 / (2 * math.pi) * 255).clip(0, 255)
+    codes = _u32_words(nq, q1, q2, q3)
+    i = torch.arange(256, dtype=torch.float32)
+    half_turn = i / 255 * math.pi
+    full_turn = i / 255 * 2 * math.pi
+    tables = [(torch.exp(i / 255 * log_mu) - 1) * r_max / mu,
+              torch.cos(half_turn), torch.sin(half_turn), torch.cos(half_turn), torch.sin(half_turn),
+              torch.cos(full_turn), torch.sin(full_turn)]
+    luts = [t.to(torch.float16).to(w1.device) for t in tables]
+    return codes, luts, [float(sk) for sk in s]
+
+
+def _lut_args(luts):
+    if len(luts) != 7:
+        raise ValueError("quad LUTs: expected 7 tables [norm, cos1, sin1, cos2, sin2, cos3, sin3]")
+    dt = luts[0].dtype
+    for t in luts:
+        if t.dtype != dt or t.numel() < 256 or not t.is_contiguous():
+            raise ValueError("quad LUTs must be 7 contiguous tensors of one dtype with 256 entries")
+    if dt == torch.float16:
+        code = nat.PP_F16
+    elif dt == torch.float32:
+        code = nat.PP_F32
+    else:
+        raise TypeError(f"quad LUT dtype must be float16 or float32, got {dt}")
+    return nat.ptr_array([t.data_ptr() for t in luts]), code
+
+
+def _plug_args(plug, device):
+    if plug is None:
+        return None, None, 0, ()
+    idx, vals = plug
+    if idx.dtype not in (torch.uint32, torch.int32):
+        raise TypeError("plug index must be uint32 (or int32 holding uint32 bits)")
+    if vals.dtype != torch.float16 or vals.numel() != 4 * idx.numel():
+        raise TypeError("plug values must be float16 (P, 4)")
+    idx = idx.contiguous()
+    vals = vals.contiguous()
+    if idx.device != device or vals.device != device:
+        raise ValueError("plug tensors must be on the codes' device")
+    return idx.data_ptr(), vals.data_ptr(), idx.numel(), (idx, vals)
+
+
+def _check_device(*ts):
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise ValueError("polar_pack_amd operators run on a ROCm device (tensor.device.type == 'cuda')")
+    for t in ts[1:]:
+        if t.device != dev:
+            raise ValueError("all operands must be on one device")
+    return dev
+
+
+def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
+    """4 GEMMs from one packed pass (quad_kernels.py:146-159).
+
+    ``a`` fp16 (M,K); ``codes`` uint32 (K,N) view (any strides); ``luts`` the
+    7 tables of :func:`pack_quad_layer` (fp16 or fp32); ``scales`` 4 floats.
+    Returns a list of 4 fp16 (M,N) tensors ``out_k = fp16(s_k * a @ W_k)``.
+    ``plug=(idx uint32 (P,), vals fp16 (P,4))`` replaces the normalised tuple
+    of the element at storage offset ``idx - elem_base`` of ``codes``.
+    """
+    M, K = a.shape
+    K_b, N = codes.shape
+    assert K == K_b
+    dev = _check_device(a, codes, *luts)
+    if a.dtype != torch.float16:
+        raise TypeError("a must be float16")
+    if codes.dtype not in (torch.uint32, torch.int32):
+        raise TypeError("codes must be uint32")
+    outs = [torch.empty((M, N), dtype=torch.float16, device=dev) for _ in range(4)]
+    if M == 0 or N == 0:
+        return outs
+    if K == 0:
+        for o in outs:
+            o.zero_()
+        return outs
+    if a.stride(1) != 1 or a.data_ptr() % 8 or (M > 1 and a.stride(0) % 4):
+        a = a.contiguous()
+    lut_ptrs, lut_dtype = _lut_args(luts)
+    sc = nat.float_array(scales)
+    pi, pv, pn, keep = _plug_args(plug, dev)
+    L = nat.lib()
+    ws_bytes = L.pp_quad_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), codes.data_ptr(),
+                                             codes.stride(0), codes.stride(1), pn, M, N, K)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = L.pp_quad_gemm(a.data_ptr(), a.stride(0), a.stride(1), codes.data_ptr(), codes.stride(0),
+                        codes.stride(1), lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base),
+                        nat.ptr_array([o.data_ptr() for o in outs]), outs[0].stride(0), outs[0].stride(1),
+                        M, N, K, ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    nat.check(rc, "pp_quad_gemm")
+    del keep
+    return outs
+
+
+def quad_dequant(codes, luts, scales, *, plug=None, elem_base=0):
+    """float32 (K,N) weights ``s_k * W_k`` of a code view, plug applied (4 tensors)."""
+    K, N = codes.shape
+    dev = _check_device(codes, *luts)
+    outs = [torch.empty((K, N), dtype=torch.float32, device=dev) for _ in range(4)]
+    if K * N == 0:
+        return outs
+    lut_ptrs, lut_dtype = _lut_args(luts)
+    pi, pv, pn, keep = _plug_args(plug, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = nat.lib().pp_quad_dequant(codes.data_ptr(), codes.stride(0), codes.stride(1), lut_ptrs, lut_dtype,
+                                   nat.float_array(scales), pi, pv, pn, int(elem_base),
+                                   nat.ptr_array([o.data_ptr() for o in outs]), N, K, stream)
+    nat.check(rc, "pp_quad_dequant")
+    del keep
+    return outs
+
+
+def header_luts(r_max, device=None):
+    """float32 LUTs of a ``.quadpack`` header (quaternion_packer.py:178-181), computed
+    in float64 and rounded once; cos1/sin1 and cos2/sin2 are the same half-turn table.
+    Like the reference unpacker, the module constant mu = 255 is used, not the
+    header's mu field (quaternion_packer.py:153, 178)."""
+    i = torch.arange(256, dtype=torch.float64)
+    log_mu = math.log1p(MU)
+    half = i / 255 * math.pi
+    full = i / 255 * 2 * math.pi
+    t = [(torch.exp(i / 255 * log_mu) - 1) * float(r_max) / MU,
+         torch.cos(half), torch.sin(half), torch.cos(half), torch.sin(half), torch.cos(full), torch.sin(full)]
+    return [x.to(torch.float32).to(device) for x in t]

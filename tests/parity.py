@@ -1,0 +1,49 @@
+"""Tolerance checks shared by the GPU parity tests.
+
+* dequantised weights: within 1 fp16 ulp of the float64 oracle, compared after
+  rounding both to fp16 (and the float32 value within 8 float32 ulps);
+* GEMM/GEMV outputs (fp32 accumulate, fp16 out): per element
+  |y - y_ref| <= 1e-3 * |y_ref| + 1e-5 * max|y_ref|, i.e. rel 1e-3 with a small
+  absolute floor for outputs that cancel to near zero;
+* codes, plug positions: bit-exact (checked by the tests directly).
+"""
+import numpy as np
+
+GEMV_RTOL = 1e-3
+GEMV_FLOOR = 1e-5
+
+
+def fp16_ulp_distance(a, b):
+    """|a - b| in fp16 ulps after rounding both to fp16 (ordered-integer distance)."""
+    ia = np.asarray(a, np.float64).astype(np.float16).view(np.int16).astype(np.int32)
+    ib = np.asarray(b, np.float64).astype(np.float16).view(np.int16).astype(np.int32)
+    ia = np.where(ia < 0, -32768 - ia, ia)
+    ib = np.where(ib < 0, -32768 - ib, ib)
+    return np.abs(ia - ib)
+
+
+def assert_dequant_close(got_f32, ref_f64, what=""):
+    got = np.asarray(got_f32, np.float32)
+    ref = np.asarray(ref_f64, np.float64)
+    d = fp16_ulp_distance(got, ref)
+    assert d.max() <= 1, f"{what}: dequant off by {d.max()} fp16 ulp at {np.unravel_index(d.argmax(), d.shape)}"
+    tol = 8 * np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64) + 1e-30
+    bad = np.abs(got.astype(np.float64) - ref) > tol
+    assert not bad.any(), f"{what}: float32 dequant error beyond 8 ulp at {np.argwhere(bad)[:5]}"
+
+
+def assert_gemv_close(got, ref, what="", rtol=GEMV_RTOL, floor=GEMV_FLOOR):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = np.abs(ref).max() if ref.size else 0.0
+    err = np.abs(got - ref)
+    lim = rtol * np.abs(ref) + floor * scale
+    worst = (err - lim).argmax() if ref.size else 0
+    assert np.all(err <= lim), (f"{what}: |d|={err.flat[worst]:.3e} > {lim.flat[worst]:.3e} "
+                                f"(ref {ref.flat[worst]:.4e}, got {got.flat[worst]:.4e}); "
+                                f"normwise {err.max() / max(scale, 1e-300):.2e}")
+
+
+def normwise(got, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(np.asarray(got, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-300))

@@ -1,0 +1,113 @@
+"""GPU parity of the dual decode against the float64 oracle (same seeded inputs)."""
+import numpy as np
+import pytest
+import torch
+
+import gen
+from oracle import dualpack as odp
+from oracle import layer as olay
+from parity import assert_dequant_close, assert_gemv_close
+from polar_pack_amd import polar_kernels as pk
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def u32(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).view(torch.uint32)
+
+
+def kernel_layout_layer(K, N, seed, dtype=torch.float16):
+    w1, w2 = [torch.from_numpy(w.reshape(K, N)).to(dtype) for w in gen.correlated_models(seed, [K * N] * 2)]
+    return olay.quantize_polar_bitpacked(w1, w2)
+
+
+def to_dev(*arrs):
+    return [torch.from_numpy(np.ascontiguousarray(a)).to(DEV) for a in arrs]
+
+
+@pytest.mark.parametrize("K,N", [(64, 96), (33, 40), (256, 512)])
+def test_dual_dequant_kernel_layout(K, N):
+    packed, bmax, amp_lut, cos_lut, sin_lut = kernel_layout_layer(K, N, K + N)
+    got = pk.dual_dequant(*to_dev(packed, bmax, amp_lut, cos_lut, sin_lut))
+    ref = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut)
+    for g, r in zip(got, ref):
+        assert_dequant_close(g.cpu().numpy(), r)
+
+
+def stream_pack(n1, n2, seed, cap, chunk):
+    w1, w2 = gen.correlated_models(seed, [n1, n2], delta_growth=False)
+    return odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=cap, chunk_size=chunk))
+
+
+def be_codes_tensor(dp):
+    """File-layout codes (big-endian u16 bytes) as a device int16 tensor of n_pairs elements."""
+    return torch.from_numpy(dp.codes_be.view(np.int16).copy()).to(DEV)
+
+
+@pytest.mark.parametrize("chunk", [1000, 10_001, 50_000_000])
+def test_dual_dequant_container_layout_with_plug(chunk):
+    dp = stream_pack(30_000, 27_000, 3, 0.03, chunk)
+    N, K = 120, 250                                      # 30,000 pairs viewed as a (N,K) Linear
+    codes = be_codes_tensor(dp)[:N * K].reshape(N, K).t()
+    amp, cs, sn = pk.header_luts(mu=dp.mu, device=DEV)
+    got = pk.dual_dequant(codes, torch.from_numpy(dp.scales).to(DEV), amp, cs, sn, layout="u16be",
+                          chunk_size=dp.chunk_size,
+                          plug=(u32(dp.plug_idx).to(DEV), torch.from_numpy(dp.plug_val).to(DEV)))
+    d1, d2 = odp.decode_pairs_f64(dp, 0, N * K)
+    for g, r in zip(got, (d1, d2)):
+        assert_dequant_close(g.cpu().numpy(), r.reshape(N, K).T)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("K,N", [(256, 512), (64, 96), (2048, 200)])
+def test_polar_dual_bitpacked_kernel_layout(K, N, M):
+    packed, bmax, amp_lut, cos_lut, sin_lut = kernel_layout_layer(K, N, 11 * K + N)
+    a = np.random.default_rng(M).standard_normal((M, K)).astype(np.float16)
+    o1, o2 = pk.polar_dual_bitpacked(*to_dev(a, packed, bmax, amp_lut, cos_lut, sin_lut))
+    W = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut)
+    for o, w in ((o1, W[0]), (o2, W[1])):
+        assert o.shape == (M, N) and o.dtype == torch.float16
+        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w))
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 6])
+@pytest.mark.parametrize("chunk", [4096, 10_001, 50_000_000])
+def test_polar_dual_bitpacked_container_stream(chunk, M):
+    """(N,K) Linears cut from a .dualpack stream, big-endian codes, chunked groups, plug."""
+    n1 = 3 * 2048 * 64 + 1000
+    dp = stream_pack(n1, n1 - 777, 7, 0.01, chunk)
+    amp, cs, sn = pk.header_luts(mu=dp.mu, device=DEV)
+    codes_all = be_codes_tensor(dp)
+    scales = torch.from_numpy(dp.scales).to(DEV)
+    plug = (u32(dp.plug_idx).to(DEV), torch.from_numpy(dp.plug_val).to(DEV))
+    rng = np.random.default_rng(M)
+    for base, N, K in ((0, 64, 2048), (64 * 2048, 128, 1024), (2 * 64 * 2048, 16, 8192)):
+        a = rng.standard_normal((M, K)).astype(np.float16)
+        view = codes_all[base:base + N * K].reshape(N, K).t()
+        o1, o2 = pk.polar_dual_bitpacked(torch.from_numpy(a).to(DEV), view, scales, amp, cs, sn, layout="u16be",
+                                         chunk_size=dp.chunk_size, plug=plug, elem_base=base)
+        d1, d2 = odp.decode_pairs_f64(dp, base, base + N * K)
+        for o, d in ((o1, d1), (o2, d2)):
+            assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, d.reshape(N, K).T), f"base {base}")
+
+
+@pytest.mark.parametrize("dtype,max_frac", [(torch.float16, 0.25), (torch.float32, 0.01)])
+def test_quantize_polar_bitpacked_on_gpu_matches_oracle(dtype, max_frac):
+    """The packer computes in the weights' dtype, as the reference does (polar_kernels.py:120-124).
+    With fp16 weights the phase (phase + pi) / 2pi * 1024 is rounded in fp16, where a one-ulp
+    difference between device and host atan2 moves many codes by one phase step; the
+    bound is one step (and a small fraction of codes for float32 weights)."""
+    K, N = 128, 64
+    w1, w2 = [torch.from_numpy(w.reshape(K, N)).to(dtype) for w in gen.correlated_models(5, [K * N] * 2)]
+    got = pk.quantize_polar_bitpacked(w1.to(DEV), w2.to(DEV))
+    ref = olay.quantize_polar_bitpacked(w1, w2)
+    p_got = got[0].cpu().numpy().astype(np.int32) + 32768
+    p_ref = ref[0].astype(np.int32) + 32768
+    dph = np.abs(((p_got & 1023) - (p_ref & 1023) + 512) % 1024 - 512)
+    assert (dph > 0).mean() < max_frac and dph.max() <= 1
+    assert np.abs((p_got >> 10) - (p_ref >> 10)).max() <= 1
+    db = np.abs(got[1].cpu().numpy().view(np.int16).astype(np.int32) - ref[1].view(np.int16).astype(np.int32))
+    assert db.max() <= 1                                 # group max of device sqrt: within one fp16 ulp
+    for i in (2, 3, 4):
+        np.testing.assert_array_equal(got[i].cpu().numpy().view(np.uint16), ref[i].view(np.uint16))

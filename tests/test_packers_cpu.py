@@ -1,0 +1,67 @@
+"""The product's kernel-layout packers (torch ops) against the reference-written golden
+vectors, on CPU tensors (the same code runs on the GPU inside the parity tests)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import make_golden as mg
+from polar_pack_amd import polar_kernels as pk
+from polar_pack_amd import quad_kernels as qk
+
+HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+SAME_LIBS = np.__version__ == "2.2.6" and torch.__version__.startswith("2.10.0")
+needs_same_libs = pytest.mark.skipif(not SAME_LIBS, reason="golden vectors were written with numpy 2.2.6 / torch 2.10.0")
+
+
+@needs_same_libs
+@pytest.mark.parametrize("case", mg.QUAD_LAYER_CASES, ids=[c[0] for c in mg.QUAD_LAYER_CASES])
+def test_pack_quad_layer_cpu_equals_reference(case):
+    name, K, N, seed, corr = case
+    g = np.load(os.path.join(HERE, name + ".npz"))
+    codes, luts, scales = qk.pack_quad_layer(*[torch.from_numpy(w) for w in mg.quad_layer_inputs(K, N, seed, corr)])
+    assert codes.dtype == torch.uint32 and codes.shape == (K, N)
+    np.testing.assert_array_equal(codes.view(torch.int32).numpy().view(np.uint32), g["codes"])
+    np.testing.assert_array_equal(torch.stack(luts).numpy().view(np.uint16), g["luts"].view(np.uint16))
+    assert scales == list(g["scales"])
+
+
+@needs_same_libs
+@pytest.mark.parametrize("case", mg.DUAL_LAYER_CASES, ids=[c[0] for c in mg.DUAL_LAYER_CASES])
+def test_quantize_polar_bitpacked_cpu_equals_reference(case):
+    name, K, N, seed, dt = case
+    g = np.load(os.path.join(HERE, name + ".npz"))
+    w1, w2 = [torch.from_numpy(w) for w in mg.dual_layer_inputs(K, N, seed, dt)]
+    packed, bmax, amp_lut, cos_lut, sin_lut = pk.quantize_polar_bitpacked(w1, w2)
+    np.testing.assert_array_equal(packed.numpy(), g["packed"])
+    for t, key in ((bmax, "bmax"), (amp_lut, "amp_lut"), (cos_lut, "cos_lut"), (sin_lut, "sin_lut")):
+        np.testing.assert_array_equal(t.numpy().view(np.uint16), g[key].view(np.uint16))
+
+
+def test_pack_amp_phase_closed_form():
+    amp = torch.arange(64).repeat_interleave(1024)
+    ph = torch.arange(1024).repeat(64)
+    p = pk.pack_amp_phase(amp, ph)
+    assert p.dtype == torch.int16
+    u = (p.to(torch.int32) + 32768)
+    assert torch.equal(u >> 10, amp) and torch.equal(u & 1023, ph)
+    assert int(p.min()) == -32768 and int(p.max()) == 32767
+
+
+def test_operators_reject_cpu_tensors():
+    a = torch.zeros(1, 8, dtype=torch.float16)
+    codes = torch.zeros(8, 4, dtype=torch.int32).view(torch.uint32)
+    luts = [torch.zeros(256, dtype=torch.float16)] * 7
+    with pytest.raises(ValueError, match="ROCm device"):
+        qk.quad_bitpacked(a, codes, luts, [1.0] * 4)
+
+
+def test_header_luts_closed_form():
+    l = qk.header_luts(3.0)
+    assert all(t.dtype == torch.float32 and t.numel() == 256 for t in l)
+    assert float(l[0][0]) == 0.0 and abs(float(l[0][255]) - 3.0) < 1e-6
+    assert torch.equal(l[1], l[3]) and torch.equal(l[2], l[4])
+    d = pk.header_luts()
+    assert d[0].numel() == 64 and d[1].numel() == 1024
+    assert abs(float(d[0][63]) - 1.0) < 1e-7 and float(d[1][0]) == -1.0 and float(d[2][512]) == 0.0
