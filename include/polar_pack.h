@@ -107,7 +107,7 @@ int pp_quad_dequant(const uint32_t* codes, int64_t c_sk, int64_t c_sn,
  * .quadpack stream (the grouped whole-step launch).  All tables are device
  * memory prepared by the host once per stream (see polar_pack_amd/stream.py):
  *
- *   projs  : n_proj descriptors of pp_quad_proj;
+ *   projs  : n_projs descriptors of pp_quad_proj (the first 256 are staged in LDS);
  *   items  : n_items work items of pp_quad_item (rows of one projection, plus
  *            their plug range in plug_idx);
  *   luts   : 7 float32 LUTs from the header (r_max, mu);
@@ -132,34 +132,30 @@ typedef struct pp_quad_proj {
 
 enum pp_item_flags { PP_ITEM_TAIL = 1 };
 
-/* One wavefront task: rows [row0, row0+nrows) x K slice [k0, k1) of one projection.
- * Items of one row group that split K share a combine `group` (0..n_groups-1) and
- * have slice = 0..n_slices-1; an item covering all of K has n_slices == 1. */
+/* One wavefront task: full rows [row0, row0+nrows) of one projection. */
 typedef struct pp_quad_item {
   int32_t proj;            /* index into projs */
   int32_t row0;            /* first row */
-  int32_t nrows;           /* rows in this item, 1..pp_quad_stream_layout().rows_per_item */
-  int32_t flags;           /* PP_ITEM_*; a TAIL item is one row over all of K */
-  int32_t k0, k1;          /* K slice, multiples of 256 except k1 == K */
-  int32_t group;           /* split-K combine group, or -1 */
-  int32_t slice, n_slices;
-  int32_t pad_;
+  int32_t nrows;           /* rows in this item, 1..pp_quad_stream_rows(M) */
+  int32_t flags;           /* PP_ITEM_*; a TAIL item is one row */
   int64_t plug_lo;         /* plug entries [plug_lo, plug_hi) cover these rows */
   int64_t plug_hi;
 } pp_quad_item;
 
-/* Rows per item and partial-sum floats per (group, slice) the stream decode uses for
- * M tokens.  The split-K workspace `part` holds n_groups * max_slices * values floats;
- * `counters` holds n_groups uint32 that must be zero before the first launch (the
- * kernel leaves them at zero again). */
-int pp_quad_stream_layout(int64_t M, int* rows_per_item, int* values_per_slice);
+/* Rows per item the stream decode uses for M tokens (0 and an error for bad M). */
+int pp_quad_stream_rows(int64_t M);
 
-int pp_quad_stream(const pp_quad_proj* projs, const pp_quad_item* items, int64_t n_items,
+/* Number of wavefronts pp_quad_stream launches for M tokens on the current device.
+ * wave_bounds (optional) gives wave w the items [wave_bounds[w], wave_bounds[w+1]);
+ * the host balances them by bytes.  Without it, items are split evenly by count. */
+int64_t pp_quad_stream_waves(int64_t M);
+
+int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs, const pp_quad_item* items, int64_t n_items,
+                   const int64_t* wave_bounds, int64_t n_waves,
                    const float* const* luts, const float* scales,
                    const uint32_t* plug_idx, const void* plug_vals,
                    int64_t n_codes, const void* const* tails, const int64_t* tail_len,
-                   int64_t M, float* part, int64_t max_slices, uint32_t* counters,
-                   void* stream);
+                   int64_t M, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Dual pack: 16-bit [amp 6 | phase 10] -> 2 models.                          */

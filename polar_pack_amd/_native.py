@@ -30,8 +30,7 @@ class QuadProj(C.Structure):
 class QuadItem(C.Structure):
     """``pp_quad_item`` (include/polar_pack.h)."""
     _fields_ = [("proj", C.c_int32), ("row0", C.c_int32), ("nrows", C.c_int32), ("flags", C.c_int32),
-                ("k0", C.c_int32), ("k1", C.c_int32), ("group", C.c_int32), ("slice", C.c_int32),
-                ("n_slices", C.c_int32), ("pad_", C.c_int32), ("plug_lo", i64), ("plug_hi", i64)]
+                ("plug_lo", i64), ("plug_hi", i64)]
 
 
 EXPORTS = {
@@ -42,8 +41,9 @@ EXPORTS = {
                            i64, i64, i64, vp, i64, vp]),
     "pp_quad_gemm_workspace_size": (i64, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64]),
     "pp_quad_dequant": (i32, [vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
-    "pp_quad_stream_layout": (i32, [i64, C.POINTER(i32), C.POINTER(i32)]),
-    "pp_quad_stream": (i32, [vp, vp, i64, vp, vp, vp, vp, i64, vp, vp, i64, vp, i64, vp, vp]),
+    "pp_quad_stream_rows": (i32, [i64]),
+    "pp_quad_stream_waves": (i64, [i64]),
+    "pp_quad_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, vp, vp, vp, i64, vp, vp, i64, vp]),
     "pp_dual_gemm": (i32, [vp, i64, i64, vp, i32, i64, i64, vp, i64, i64, vp, i32, vp, vp, i32, i32,
                            vp, vp, i64, i64, vp, vp, i64, i64, i64, i64, i64, vp, i64, vp]),
     "pp_dual_gemm_workspace_size": (i64, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64]),

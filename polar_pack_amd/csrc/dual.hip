@@ -220,7 +220,7 @@ __global__ __launch_bounds__(rows_threads_dual(MT)) void dual_rows_kernel(const 
         }
       }
     }
-    float mine = 0.f;
+    float mine[2] = {0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < RG; ++r)
 #pragma unroll
@@ -228,27 +228,40 @@ __global__ __launch_bounds__(rows_threads_dual(MT)) void dual_rows_kernel(const 
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
           const float v = wave_sum(acc[r][m][j]);
-          if (lane == (r * 2 + m) * MT + j) mine = v;
+          if (lane == r * MT + j) mine[m] = v;
         }
-    const int r = lane / (2 * MT), m = (lane / MT) % 2, j = lane % MT;
-    const bool owner = lane < NV && r < nrows && j < A.M;
-    f16* dst = owner ? A.out[m] + (int64_t)j * A.o_sm + (int64_t)(row0 + r) * A.o_sn : nullptr;
+    // lane r*MT + j owns (row r, token j) of both models
+    const int r = lane / MT, j = lane % MT;
+    const bool owner = lane < RG * MT && r < nrows && j < A.M;
+    const int64_t off = (int64_t)j * A.o_sm + (int64_t)(row0 + r) * A.o_sn;
     if (A.n_slices <= 1) {
-      if (owner) *dst = (f16)mine;
+      if (owner) {
+        A.out[0][off] = (f16)mine[0];
+        A.out[1][off] = (f16)mine[1];
+      }
       continue;
     }
     float* grp = A.part + (int64_t)rg * A.part_stride;
-    if (lane < NV) grp[(int64_t)slice * NV + lane] = mine;
+    if (lane < RG * MT) {
+      grp[(int64_t)slice * NV + 2 * lane] = mine[0];
+      grp[(int64_t)slice * NV + 2 * lane + 1] = mine[1];
+    }
     __threadfence();
     uint32_t prev = 0;
     if (lane == 0) prev = atomicAdd(A.counters + rg, 1u);
     prev = __shfl(prev, 0, 64);
     if (prev != (uint32_t)(A.n_slices - 1)) continue;
     __threadfence();
-    if (lane < NV) {
-      float sum = 0.f;
-      for (int s = 0; s < A.n_slices; ++s) sum += __builtin_nontemporal_load(grp + (int64_t)s * NV + lane);
-      if (owner) *dst = (f16)sum;
+    if (lane < RG * MT) {
+      float s0 = 0.f, s1 = 0.f;
+      for (int s = 0; s < A.n_slices; ++s) {
+        s0 += __builtin_nontemporal_load(grp + (int64_t)s * NV + 2 * lane);
+        s1 += __builtin_nontemporal_load(grp + (int64_t)s * NV + 2 * lane + 1);
+      }
+      if (owner) {
+        A.out[0][off] = (f16)s0;
+        A.out[1][off] = (f16)s1;
+      }
     }
     if (lane == 0) A.counters[rg] = 0u;
   }

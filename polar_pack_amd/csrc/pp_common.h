@@ -57,6 +57,25 @@ __device__ __forceinline__ u32x4 load_nt(const uint32_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  return reinterpret_cast<T*>(uniform64(reinterpret_cast<int64_t>(p)));
+}
+
+__device__ __forceinline__ int64_t lane_read64(int64_t v, int lane) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, lane);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)v >> 32), lane);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -79,14 +98,29 @@ struct QuadLuts {
   int dtype;
 };
 
+// Fill the replicated tables: thread t owns entry t % 256 and every (blockDim/256)-th
+// replica; all 7 LUT loads of a thread are issued before any LDS write, so the build
+// costs one memory round trip.  blockDim.x must be a multiple of 256.
 template <int REPL_R, int REPL_C>
 __device__ __forceinline__ void quad_build_lds(QuadLds<REPL_R, REPL_C>& T, const QuadLuts& L) {
-  for (int i = threadIdx.x; i < 256 * REPL_R; i += blockDim.x) T.r[i] = lut_at(L.p[0], L.dtype, i / REPL_R);
-  for (int i = threadIdx.x; i < 256 * REPL_C; i += blockDim.x) {
-    const int e = i / REPL_C;
-    T.cs1[i] = make_float2(lut_at(L.p[1], L.dtype, e), lut_at(L.p[2], L.dtype, e));
-    T.cs2[i] = make_float2(lut_at(L.p[3], L.dtype, e), lut_at(L.p[4], L.dtype, e));
-    T.cs3[i] = make_float2(lut_at(L.p[5], L.dtype, e), lut_at(L.p[6], L.dtype, e));
+  const int e = threadIdx.x & 255;
+  const int grp = threadIdx.x >> 8, ngrp = blockDim.x >> 8;
+  float v[7];
+  if (L.dtype == PP_F16) {
+    f16 h[7];
+#pragma unroll
+    for (int i = 0; i < 7; ++i) h[i] = reinterpret_cast<const f16*>(L.p[i])[e];
+#pragma unroll
+    for (int i = 0; i < 7; ++i) v[i] = (float)h[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 7; ++i) v[i] = reinterpret_cast<const float*>(L.p[i])[e];
+  }
+  for (int j = grp; j < REPL_R; j += ngrp) T.r[e * REPL_R + j] = v[0];
+  for (int j = grp; j < REPL_C; j += ngrp) {
+    T.cs1[e * REPL_C + j] = make_float2(v[1], v[2]);
+    T.cs2[e * REPL_C + j] = make_float2(v[3], v[4]);
+    T.cs3[e * REPL_C + j] = make_float2(v[5], v[6]);
   }
 }
 

@@ -9,16 +9,19 @@
 // Kernels:
 //   quad_rows_kernel  -- batch <= 8 decode over codes laid out (N,K) row-major (the
 //                        container stream layout).  One wavefront owns a task = up to
-//                        RG rows x a K slice: it streams the codes once with 16-byte
-//                        non-temporal loads (next segment in flight while the current
-//                        one decodes), decodes in registers against LDS tables that are
-//                        replicated so every lane of an LDS clock reads its own bank,
-//                        folds x into the norm (rx = r*x: 3 mul + 4 fma per tuple at
-//                        batch 1), reduces across the wave, and applies the plug table
-//                        as exact corrections x*(plug - decoded).  Split-K tasks publish
-//                        partial sums; the last slice to arrive adds them in slice order
-//                        (deterministic) and resets its counter.  Rows that reach FP16
-//                        tail positions are one-row tasks on a scalar path.
+//                        RG full rows.  It walks K in chunks of NSEG x 256 codes and, per
+//                        chunk, issues the activations and every 16-byte non-temporal code
+//                        load before using any of them (one memory round trip per chunk;
+//                        the other waves of the CU hide it).  Codes are decoded in
+//                        registers against LDS tables replicated so that every lane of an
+//                        LDS clock reads its own bank; x is folded into the norm
+//                        (rx = r*x: 3 mul + 4 fma per tuple at batch 1).  Plug entries of
+//                        the task are located up front and their dependent loads ride
+//                        with the first chunk; each is applied as an exact correction
+//                        x*(plug - decoded) before the wave reduction.  Rows that reach
+//                        FP16 tail positions are one-row tasks on a scalar path.  No
+//                        task spans waves, so no cross-wave combine (and no device-scope
+//                        fence, which costs an L2 writeback on this part) is needed.
 //   quad_dequant_kernel / quad_plug_scatter_kernel -- float32 weights (parity export
 //                        and the generic path); quad_ws_gemm_kernel multiplies them.
 #include "pp_common.h"
@@ -30,9 +33,6 @@ namespace pp {
 
 constexpr int QREPL_R = 32;   // norm table replicas (ds_read_b32 serves 32 lanes per clock)
 constexpr int QREPL_C = 16;   // (cos, sin) table replicas (ds_read_b64 serves 16 lanes per clock)
-// threads per workgroup: one workgroup per CU (128 KiB LDS); 8 tokens need the
-// larger register budget of 8 waves per CU
-constexpr int rows_threads(int MT) { return MT >= 8 ? 512 : 1024; }
 constexpr int QSEG = 256;     // codes per wave per row per step (64 lanes x 4)
 using QLds = QuadLds<QREPL_R, QREPL_C>;
 
@@ -46,19 +46,20 @@ struct QTask {
   int64_t o_sm, o_sn;
   int nrows, K, k0, k1;
   int64_t plug_lo, plug_hi;
-  int group, slice, n_slices;
   int tail;
 };
 
 struct QuadRowsArgs {
-  // single-projection front end (items == nullptr): task ti -> (rowgroup, slice)
+  // single-projection front end (items == nullptr): task ti -> rows [ti*rows_per_task, ...)
   pp_quad_proj proj;
   int64_t o_sn;
-  int n_slices, slice_len;
-  const int64_t* rg_plug;   // plug range start of each row group (n_rowgroups + 1), or null
+  int rows_per_task;
+  const int64_t* rg_plug;   // plug range start of each task's rows (n_tasks + 1), or null
   // stream front end
   const pp_quad_proj* projs;
+  int64_t n_projs;
   const pp_quad_item* items;
+  const int64_t* wave_bounds;  // per-wave item ranges (n_waves + 1), or null
   // common
   int64_t n_tasks;
   QuadLuts luts;
@@ -70,16 +71,65 @@ struct QuadRowsArgs {
   int64_t n_codes;          // positions >= n_codes come from the tails
   const f16* tails[4];
   int64_t tail_len[4];
-  float* part;              // split-K partial sums, group g at part + g * part_stride
-  int64_t part_stride;      // floats per combine group
-  uint32_t* counters;       // [group], zero between launches
 };
 
+// Per-token-count shape of a task: RG rows x NSEG segments of 256 codes.  Every load
+// of a task (x, all codes, the first 64 plug entries) is issued before any of it is
+// used, so a task costs one memory round trip; the plug-dependent loads (the plugged
+// code word, its fp16 values, x at its column) are issued while the codes stream in.
+#ifndef PP_ROWS1_RG
+#define PP_ROWS1_RG 4
+#endif
+#ifndef PP_ROWS1_NSEG
+#define PP_ROWS1_NSEG 4
+#endif
+#ifndef PP_ROWS1_NT
+#define PP_ROWS1_NT 1024
+#endif
+template <int MT> struct RowsCfg;
+template <> struct RowsCfg<1> { static constexpr int RG = PP_ROWS1_RG, NSEG = PP_ROWS1_NSEG, NT = PP_ROWS1_NT; };
+template <> struct RowsCfg<2> { static constexpr int RG = 2, NSEG = 4, NT = 1024; };
+template <> struct RowsCfg<4> { static constexpr int RG = 1, NSEG = 4, NT = 1024; };
+template <> struct RowsCfg<8> { static constexpr int RG = 1, NSEG = 4, NT = 512; };
+
 template <int MT, int RG>
-__device__ __forceinline__ void rows_task(const QLds& T, const QuadRowsArgs& A, const QTask& t,
+__device__ __forceinline__ void plug_apply(const QLds& T, const QuadRowsArgs& A, const QTask& t, int row,
+                                           uint32_t cw, f16x4 pv, const float (&xk)[MT], float (&acc)[RG][4][MT]) {
+  const int lane = threadIdx.x & 63;
+  float wd[4];
+  quad_decode(T, cw, lane % QREPL_R, lane % QREPL_C, wd[0], wd[1], wd[2], wd[3]);
+  const float dlt[4] = {(float)pv.x - wd[0], (float)pv.y - wd[1], (float)pv.z - wd[2], (float)pv.w - wd[3]};
+  // every row is updated with a 0/1 weight: a branch on `row` would be folded into a
+  // per-lane index into acc[], which puts the accumulators in scratch memory
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const float on = r == row ? 1.f : 0.f;
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc[r][m][j] = fmaf(on * xk[j], dlt[m], acc[r][m][j]);
+  }
+}
+
+// Locate plug entry p inside the task: row (or -1 when outside its rows) and column.
+template <int RG>
+__device__ __forceinline__ int plug_locate(const QuadRowsArgs& A, const QTask& t, int64_t p, int& k) {
+  const int64_t off = (int64_t)A.plug_idx[p] - t.pos_row0;
+  int row = 0;
+#pragma unroll
+  for (int r = 1; r < RG; ++r)
+    if (off >= (int64_t)r * t.ldc) row = r;
+  k = (int)(off - (int64_t)row * t.ldc);
+  const bool in = off >= 0 && row < t.nrows && k >= t.k0 && k < t.k1;
+  return in ? row : -1;
+}
+
+template <int MT, int RG, int NSEG>
+__device__ __forceinline__ void rows_item(const QLds& T, const QuadRowsArgs& A, const QTask& t,
                                           float (&acc)[RG][4][MT]) {
   const int lane = threadIdx.x & 63;
   const int rr = lane % QREPL_R, rc = lane % QREPL_C;
+  constexpr int CHUNK = NSEG * QSEG;
 #pragma unroll
   for (int r = 0; r < RG; ++r)
 #pragma unroll
@@ -87,106 +137,108 @@ __device__ __forceinline__ void rows_task(const QLds& T, const QuadRowsArgs& A, 
 #pragma unroll
       for (int j = 0; j < MT; ++j) acc[r][m][j] = 0.f;
 
-  const int len = t.k1 - t.k0;
-  const uint32_t* cbase = t.codes + 4 * lane;
-  const f16* xbase = t.x + t.k0 + 4 * lane;
-
-  u32x4 q[RG];
+  // first 64 plug entries of the task: positions now, dependent loads with the first chunk
+  const int64_t n_plug = t.plug_hi - t.plug_lo;
+  int prow = -1, pk = 0;
+  if (lane < n_plug) prow = plug_locate<RG>(A, t, t.plug_lo + lane, pk);
+  uint32_t pcw = 0;
+  f16x4 pv = {0, 0, 0, 0};
+  float pxk[MT];
 #pragma unroll
-  for (int r = 0; r < RG; ++r)
-    q[r] = (r < t.nrows && 4 * lane < len) ? load_nt(cbase + (int64_t)r * t.ldc) : u32x4{0u, 0u, 0u, 0u};
-  for (int kb = 0; kb < len; kb += QSEG) {
-    u32x4 qn[RG];
-    const int kn = kb + QSEG;
+  for (int j = 0; j < MT; ++j) pxk[j] = 0.f;
+
+  const f16* xbase = t.x + t.k0 + 4 * lane;
+  const uint32_t* cbase = t.codes + 4 * lane;
+  for (int kc = 0; kc < t.k1 - t.k0; kc += CHUNK) {
+    const int len = t.k1 - t.k0 - kc;   // codes of the row left from kc on
+    // all activations and codes of the chunk, issued back to back
+    f16x4 xh[MT][NSEG];
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+      const bool valid = s * QSEG + 4 * lane < len;
+#pragma unroll
+      for (int j = 0; j < MT; ++j)
+        xh[j][s] = (valid && j < A.M)
+                       ? *reinterpret_cast<const f16x4*>(xbase + (int64_t)j * t.x_sm + kc + s * QSEG)
+                       : f16x4{0, 0, 0, 0};
+    }
+    u32x4 q[RG][NSEG];
 #pragma unroll
     for (int r = 0; r < RG; ++r)
-      qn[r] = (r < t.nrows && kn + 4 * lane < len) ? load_nt(cbase + (int64_t)r * t.ldc + kn)
-                                                   : u32x4{0u, 0u, 0u, 0u};
-    const bool valid = kb + 4 * lane < len;
-    float xv[MT][4];
 #pragma unroll
-    for (int j = 0; j < MT; ++j) {
-      if (valid && j < A.M) {
-        const f16x4 h = *reinterpret_cast<const f16x4*>(xbase + (int64_t)j * t.x_sm + kb);
-        xv[j][0] = (float)h.x;
-        xv[j][1] = (float)h.y;
-        xv[j][2] = (float)h.z;
-        xv[j][3] = (float)h.w;
-      } else {
-        xv[j][0] = xv[j][1] = xv[j][2] = xv[j][3] = 0.f;
-      }
+      for (int s = 0; s < NSEG; ++s)
+        q[r][s] = (r < t.nrows && s * QSEG + 4 * lane < len)
+                      ? load_nt(cbase + (int64_t)r * t.ldc + kc + s * QSEG)
+                      : u32x4{0u, 0u, 0u, 0u};
+    if (kc == 0 && prow >= 0) {
+      pcw = t.codes[(int64_t)prow * t.ldc + (pk - t.k0)];
+      pv = *reinterpret_cast<const f16x4*>(A.plug_vals + 4 * (t.plug_lo + lane));
+#pragma unroll
+      for (int j = 0; j < MT; ++j)
+        if (j < A.M) pxk[j] = (float)t.x[(int64_t)j * t.x_sm + pk];
     }
 #pragma unroll
-    for (int r = 0; r < RG; ++r) {
-      const uint32_t cw4[4] = {q[r].x, q[r].y, q[r].z, q[r].w};
+    for (int s = 0; s < NSEG; ++s) {
+      float xv[MT][4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t cw = cw4[e];
-        const float rv = T.r[(cw >> 24) * QREPL_R + rr];
-        const float2 a = T.cs1[((cw >> 16) & 255u) * QREPL_C + rc];
-        const float2 b = T.cs2[((cw >> 8) & 255u) * QREPL_C + rc];
-        const float2 c = T.cs3[(cw & 255u) * QREPL_C + rc];
-        if constexpr (MT == 1) {
-          const float rx = rv * xv[0][e];
-          acc[r][0][0] = fmaf(rx, a.x, acc[r][0][0]);
-          const float t1 = rx * a.y;
-          acc[r][1][0] = fmaf(t1, b.x, acc[r][1][0]);
-          const float t2 = t1 * b.y;
-          acc[r][2][0] = fmaf(t2, c.x, acc[r][2][0]);
-          acc[r][3][0] = fmaf(t2, c.y, acc[r][3][0]);
-        } else {
-          const float rs = rv * a.y;
-          const float rss = rs * b.y;
-          const float w[4] = {rv * a.x, rs * b.x, rss * c.x, rss * c.y};
-#pragma unroll
-          for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int j = 0; j < MT; ++j) acc[r][m][j] = fmaf(w[m], xv[j][e], acc[r][m][j]);
-        }
+      for (int j = 0; j < MT; ++j) {
+        xv[j][0] = (float)xh[j][s].x;
+        xv[j][1] = (float)xh[j][s].y;
+        xv[j][2] = (float)xh[j][s].z;
+        xv[j][3] = (float)xh[j][s].w;
       }
-    }
-#pragma unroll
-    for (int r = 0; r < RG; ++r) q[r] = qn[r];
-  }
-}
-
-// Plug corrections for rows [0, nrows) x k in [k0, k1) of the task: lane p takes entry
-// plug_lo + p and adds x_k * (plug - decoded) to its own partial sums.
-template <int MT, int RG>
-__device__ __forceinline__ void rows_plug(const QLds& T, const QuadRowsArgs& A, const QTask& t,
-                                          float (&acc)[RG][4][MT]) {
-  const int lane = threadIdx.x & 63;
-  for (int64_t p0 = t.plug_lo; p0 < t.plug_hi; p0 += 64) {
-    const int64_t p = p0 + lane;
-    if (p >= t.plug_hi) continue;
-    const int64_t off = (int64_t)A.plug_idx[p] - t.pos_row0;
-    if (off < 0) continue;
-    const int64_t row = off / t.ldc;
-    const int k = (int)(off - row * t.ldc);
-    if (row >= t.nrows || k < t.k0 || k >= t.k1) continue;
-    float wd[4];
-    quad_decode(T, t.codes[row * t.ldc + (k - t.k0)], lane % QREPL_R, lane % QREPL_C, wd[0], wd[1], wd[2], wd[3]);
-    const f16x4 pv = *reinterpret_cast<const f16x4*>(A.plug_vals + 4 * p);
-    const float dlt[4] = {(float)pv.x - wd[0], (float)pv.y - wd[1], (float)pv.z - wd[2], (float)pv.w - wd[3]};
-#pragma unroll
-    for (int j = 0; j < MT; ++j) {
-      if (j >= A.M) break;
-      const float xk = (float)t.x[(int64_t)j * t.x_sm + k];
 #pragma unroll
       for (int r = 0; r < RG; ++r) {
-        if (r == row) {
+        const uint32_t cw4[4] = {q[r][s].x, q[r][s].y, q[r][s].z, q[r][s].w};
 #pragma unroll
-          for (int m = 0; m < 4; ++m) acc[r][m][j] = fmaf(xk, dlt[m], acc[r][m][j]);
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t cw = cw4[e];
+          const float rv = T.r[(cw >> 24) * QREPL_R + rr];
+          const float2 a = T.cs1[((cw >> 16) & 255u) * QREPL_C + rc];
+          const float2 b = T.cs2[((cw >> 8) & 255u) * QREPL_C + rc];
+          const float2 c = T.cs3[(cw & 255u) * QREPL_C + rc];
+          if constexpr (MT == 1) {
+            const float rx = rv * xv[0][e];
+            acc[r][0][0] = fmaf(rx, a.x, acc[r][0][0]);
+            const float t1 = rx * a.y;
+            acc[r][1][0] = fmaf(t1, b.x, acc[r][1][0]);
+            const float t2 = t1 * b.y;
+            acc[r][2][0] = fmaf(t2, c.x, acc[r][2][0]);
+            acc[r][3][0] = fmaf(t2, c.y, acc[r][3][0]);
+          } else {
+            const float rs = rv * a.y;
+            const float rss = rs * b.y;
+            const float w[4] = {rv * a.x, rs * b.x, rss * c.x, rss * c.y};
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+              for (int j = 0; j < MT; ++j) acc[r][m][j] = fmaf(w[m], xv[j][e], acc[r][m][j]);
+          }
         }
       }
     }
+  }
+  // plug corrections: x_k * (plug - decoded) on the lane that holds the entry
+  if (prow >= 0) plug_apply<MT, RG>(T, A, t, prow, pcw, pv, pxk, acc);
+  // tasks with more than 64 entries (dense plug tables): the rest, 64 at a time
+  for (int64_t p0 = t.plug_lo + 64; p0 < t.plug_hi; p0 += 64) {
+    const int64_t p = p0 + lane;
+    if (p >= t.plug_hi) continue;
+    int k;
+    const int row = plug_locate<RG>(A, t, p, k);
+    if (row < 0) continue;
+    float xk[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) xk[j] = j < A.M ? (float)t.x[(int64_t)j * t.x_sm + k] : 0.f;
+    plug_apply<MT, RG>(T, A, t, row, t.codes[(int64_t)row * t.ldc + (k - t.k0)],
+                       *reinterpret_cast<const f16x4*>(A.plug_vals + 4 * p), xk, acc);
   }
 }
 
 // A row that reaches FP16 tail positions (>= n_codes), element by element:
 // y_m = s_m * sum_{pos < n} x * decoded_m  +  sum_{n <= pos} x * tail_m[pos - n].
 template <int MT>
-__device__ void rows_tail_task(const QLds& T, const QuadRowsArgs& A, const QTask& t) {
+__device__ __forceinline__ void rows_tail_task(const QLds& T, const QuadRowsArgs& A, const QTask& t) {
   const int lane = threadIdx.x & 63;
   float accc[4][MT], acct[4][MT];
 #pragma unroll
@@ -249,10 +301,10 @@ __device__ void rows_tail_task(const QLds& T, const QuadRowsArgs& A, const QTask
 template <int MT, int RG>
 __device__ __forceinline__ void rows_finish(const QuadRowsArgs& A, const QTask& t, float (&acc)[RG][4][MT]) {
   const int lane = threadIdx.x & 63;
-  constexpr int NV = RG * 4 * MT;
-  static_assert(NV <= 64, "one lane per output value");
-  // butterfly: every lane ends with every sum; lane v then owns value v
-  float mine = 0.f;
+  // butterfly sums; lane r*MT + j keeps the 4 model sums of (row r, token j) and writes
+  // them through statically indexed pointers (a per-lane model index would send the
+  // pointer array to scratch memory)
+  float mine[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int r = 0; r < RG; ++r)
 #pragma unroll
@@ -260,114 +312,138 @@ __device__ __forceinline__ void rows_finish(const QuadRowsArgs& A, const QTask& 
 #pragma unroll
       for (int j = 0; j < MT; ++j) {
         const float v = wave_sum(acc[r][m][j]);
-        if (lane == (r * 4 + m) * MT + j) mine = v;
+        if (lane == r * MT + j) mine[m] = v;
       }
-  const int r = lane / (4 * MT), m = (lane / MT) % 4, j = lane % MT;
-  const bool owner = lane < NV && r < t.nrows && j < A.M;
-  if (t.n_slices <= 1) {
-    if (owner) t.out[m][(int64_t)j * t.o_sm + (int64_t)r * t.o_sn] = (f16)(mine * A.s[m]);
+  const int r = lane / MT, j = lane % MT;
+  if (lane < RG * MT && r < t.nrows && j < A.M) {
+    const int64_t off = (int64_t)j * t.o_sm + (int64_t)r * t.o_sn;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) t.out[m][off] = (f16)(mine[m] * A.s[m]);
+  }
+}
+
+constexpr int QPROJ_CACHE = 256;   // projection descriptors staged in LDS (22.5 KiB)
+
+// Task of stream item `it` on projection descriptor P (uniform values).
+template <int RG>
+__device__ __forceinline__ void task_from_item(const pp_quad_proj& P, int row0, int nrows, int flags, int64_t plo,
+                                               int64_t phi, QTask& t) {
+  const int64_t ldc = uniform64(P.ldc);
+  t.k0 = 0;
+  t.K = uniform(P.K);
+  t.k1 = t.K;
+  t.codes = uniform_ptr(P.codes) + (int64_t)row0 * ldc;
+  t.ldc = ldc;
+  t.pos_row0 = uniform64(P.pos0) + (int64_t)row0 * ldc;
+  t.x = reinterpret_cast<const f16*>(uniform_ptr(P.x));
+  t.x_sm = uniform64(P.x_sm);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) t.out[m] = reinterpret_cast<f16*>(uniform_ptr(P.out[m])) + row0;
+  t.o_sm = uniform64(P.o_sm);
+  t.o_sn = 1;
+  t.nrows = min(nrows, RG);
+  t.plug_lo = plo;
+  t.plug_hi = phi;
+  t.tail = flags & PP_ITEM_TAIL;
+}
+
+template <int MT, int RG>
+__device__ __forceinline__ void single_task(const QuadRowsArgs& A, int64_t ti, QTask& t) {
+  const pp_quad_proj& P = A.proj;
+  const int row0 = (int)ti * A.rows_per_task;
+  t.k0 = 0;
+  t.k1 = P.K;
+  t.codes = P.codes + (int64_t)row0 * P.ldc;
+  t.ldc = P.ldc;
+  t.pos_row0 = P.pos0 + (int64_t)row0 * P.ldc;
+  t.x = reinterpret_cast<const f16*>(P.x);
+  t.x_sm = P.x_sm;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) t.out[m] = reinterpret_cast<f16*>(P.out[m]) + (int64_t)row0 * A.o_sn;
+  t.o_sm = P.o_sm;
+  t.o_sn = A.o_sn;
+  t.nrows = min(A.rows_per_task, P.N - row0);
+  t.K = P.K;
+  if (A.rg_plug != nullptr) {
+    t.plug_lo = uniform64(A.rg_plug[ti]);
+    t.plug_hi = uniform64(A.rg_plug[ti + 1]);
+  } else {
+    t.plug_lo = t.plug_hi = 0;
+  }
+  t.tail = 0;
+}
+
+template <int MT, int RG, int NSEG>
+__device__ __forceinline__ void run_task(const QLds& T, const QuadRowsArgs& A, const QTask& t) {
+  if (t.tail) {
+    rows_tail_task<MT>(T, A, t);
     return;
   }
-  float* grp = A.part + (int64_t)t.group * A.part_stride;
-  if (lane < NV) grp[(int64_t)t.slice * NV + lane] = mine;
-  __threadfence();
-  uint32_t prev = 0;
-  if (lane == 0) prev = atomicAdd(A.counters + t.group, 1u);
-  prev = __shfl(prev, 0, 64);
-  if (prev != (uint32_t)(t.n_slices - 1)) return;
-  __threadfence();
-  if (lane < NV) {
-    float sum = 0.f;
-    for (int s = 0; s < t.n_slices; ++s) sum += __builtin_nontemporal_load(grp + (int64_t)s * NV + lane);
-    if (owner) t.out[m][(int64_t)j * t.o_sm + (int64_t)r * t.o_sn] = (f16)(sum * A.s[m]);
-  }
-  if (lane == 0) A.counters[t.group] = 0u;  // ready for the next launch on this stream
+  float acc[RG][4][MT];
+  rows_item<MT, RG, NSEG>(T, A, t, acc);
+  rows_finish<MT, RG>(A, t, acc);
 }
 
-template <int MT, int RG>
-__device__ __forceinline__ void resolve_task(const QuadRowsArgs& A, int64_t ti, QTask& t) {
-  if (A.items != nullptr) {
-    const pp_quad_item it = A.items[ti];
-    const pp_quad_proj& P = A.projs[it.proj];
-    t.k0 = it.k0;
-    t.k1 = it.k1;
-    t.codes = P.codes + (int64_t)it.row0 * P.ldc + it.k0;
-    t.ldc = P.ldc;
-    t.pos_row0 = P.pos0 + (int64_t)it.row0 * P.ldc;
-    t.x = reinterpret_cast<const f16*>(P.x);
-    t.x_sm = P.x_sm;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) t.out[m] = reinterpret_cast<f16*>(P.out[m]) + it.row0;
-    t.o_sm = P.o_sm;
-    t.o_sn = 1;
-    t.nrows = min(it.nrows, RG);
-    t.K = P.K;
-    t.plug_lo = it.plug_lo;
-    t.plug_hi = it.plug_hi;
-    t.group = it.group;
-    t.slice = it.slice;
-    t.n_slices = it.n_slices;
-    t.tail = it.flags & PP_ITEM_TAIL;
-  } else {
-    const pp_quad_proj& P = A.proj;
-    const int rg = (int)(ti / A.n_slices);
-    const int slice = (int)(ti % A.n_slices);
-    const int row0 = rg * RG;
-    t.k0 = slice * A.slice_len;
-    t.k1 = min(P.K, t.k0 + A.slice_len);
-    t.codes = P.codes + (int64_t)row0 * P.ldc + t.k0;
-    t.ldc = P.ldc;
-    t.pos_row0 = P.pos0 + (int64_t)row0 * P.ldc;
-    t.x = reinterpret_cast<const f16*>(P.x);
-    t.x_sm = P.x_sm;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) t.out[m] = reinterpret_cast<f16*>(P.out[m]) + (int64_t)row0 * A.o_sn;
-    t.o_sm = P.o_sm;
-    t.o_sn = A.o_sn;
-    t.nrows = min(RG, P.N - row0);
-    t.K = P.K;
-    if (A.rg_plug != nullptr) {
-      t.plug_lo = A.rg_plug[rg];
-      t.plug_hi = A.rg_plug[rg + 1];
-    } else {
-      t.plug_lo = t.plug_hi = 0;
-    }
-    t.group = rg;
-    t.slice = slice;
-    t.n_slices = A.n_slices;
-    t.tail = 0;
-  }
-}
-
-template <int MT, int RG>
-__global__ __launch_bounds__(rows_threads(MT)) void quad_rows_kernel(const QuadRowsArgs A) {
+template <int MT>
+__global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_rows_kernel(const QuadRowsArgs A) {
+  constexpr int RG = RowsCfg<MT>::RG, NSEG = RowsCfg<MT>::NSEG;
+  constexpr int WAVES = RowsCfg<MT>::NT / 64;
   __shared__ QLds T;
+  __shared__ pp_quad_proj Pc[QPROJ_CACHE];
   quad_build_lds(T, A.luts);
+  if (A.items != nullptr) {
+    const int np = (int)min<int64_t>(A.n_projs, QPROJ_CACHE);
+    constexpr int W = sizeof(pp_quad_proj) / 4;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(A.projs);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(Pc);
+    for (int i = threadIdx.x; i < np * W; i += blockDim.x) dst[i] = src[i];
+  }
   __syncthreads();
-  constexpr int WAVES = rows_threads(MT) / 64;
-  const int64_t gw = (int64_t)blockIdx.x * WAVES + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = (int64_t)blockIdx.x * WAVES + uniform(threadIdx.x >> 6);
   const int64_t nw = (int64_t)gridDim.x * WAVES;
-  const int64_t t_begin = gw * A.n_tasks / nw, t_end = (gw + 1) * A.n_tasks / nw;
-  for (int64_t ti = t_begin; ti < t_end; ++ti) {
-    QTask t;
-    resolve_task<MT, RG>(A, ti, t);
-    if (t.tail) {
-      rows_tail_task<MT>(T, A, t);
-      continue;
+  if (A.items == nullptr) {
+    const int64_t t_begin = gw * A.n_tasks / nw, t_end = (gw + 1) * A.n_tasks / nw;
+    for (int64_t ti = t_begin; ti < t_end; ++ti) {
+      QTask t;
+      single_task<MT, RG>(A, ti, t);
+      run_task<MT, RG, NSEG>(T, A, t);
     }
-    float acc[RG][4][MT];
-    rows_task<MT, RG>(T, A, t, acc);
-    if (t.plug_hi > t.plug_lo) rows_plug<MT, RG>(T, A, t, acc);
-    rows_finish<MT, RG>(A, t, acc);
+    return;
+  }
+  // Stream items: with wave_bounds, wave gw runs the contiguous range [bounds[gw], bounds[gw+1]);
+  // without, items are dealt round robin (item i to wave i % nw), which keeps the pages all
+  // waves touch at one time inside a window of nw items.
+  int64_t first, count, stride;
+  if (A.wave_bounds != nullptr) {
+    first = uniform64(A.wave_bounds[gw]);
+    count = uniform64(A.wave_bounds[gw + 1]) - first;
+    stride = 1;
+  } else {
+    first = gw;
+    count = gw < A.n_tasks ? (A.n_tasks - gw + nw - 1) / nw : 0;
+    stride = nw;
+  }
+  // item records 64 at a time, one per lane; task j of the batch is read out of lane j
+  for (int64_t b = 0; b < count; b += 64) {
+    const int nb = (int)min<int64_t>(64, count - b);
+    pp_quad_item mine = {};
+    if (lane < nb) mine = A.items[first + (b + lane) * stride];
+    for (int j = 0; j < nb; ++j) {
+      const int proj = __builtin_amdgcn_readlane(mine.proj, j);
+      const int row0 = __builtin_amdgcn_readlane(mine.row0, j);
+      const int nrows = __builtin_amdgcn_readlane(mine.nrows, j);
+      const int flags = __builtin_amdgcn_readlane(mine.flags, j);
+      const int64_t plo = lane_read64(mine.plug_lo, j), phi = lane_read64(mine.plug_hi, j);
+      QTask t;
+      if (proj < QPROJ_CACHE) task_from_item<RG>(Pc[proj], row0, nrows, flags, plo, phi, t);
+      else task_from_item<RG>(A.projs[proj], row0, nrows, flags, plo, phi, t);
+      run_task<MT, RG, NSEG>(T, A, t);
+    }
   }
 }
 
-__global__ void zero_u32_kernel(uint32_t* p, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
-}
-
-// Plug range start of each row group: first entry with idx >= pos0 + rg*RG*ldc.
+// Plug range start of each task: first entry with idx >= pos0 + task*rows_per_task*ldc.
 __global__ void rowgroup_plug_kernel(const uint32_t* plug_idx, int64_t plug_n, int64_t pos0, int64_t ldc,
                                      int rows_per_group, int n_rowgroups, int N, int64_t* rg_plug) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
@@ -487,51 +563,54 @@ static bool rows_fast_ok(const void* a, int64_t a_sm, int64_t a_sk, const uint32
          (a_sk == 1 || K == 1) && (M == 1 || a_sm % 4 == 0) && aligned(a, 8) && K > 0;
 }
 
-template <int MT, int RG>
-static int launch_rows(QuadRowsArgs& A, hipStream_t st) {
-  const int grid = device_cu_count();
-  hipLaunchKernelGGL((quad_rows_kernel<MT, RG>), dim3(grid), dim3(rows_threads(MT)), 0, st, A);
+template <int MT>
+static int launch_rows(QuadRowsArgs& A, int64_t grid, hipStream_t st) {
+  hipLaunchKernelGGL((quad_rows_kernel<MT>), dim3((unsigned)grid), dim3(RowsCfg<MT>::NT), 0, st, A);
   PP_LAUNCH_CHECK();
   return PP_OK;
 }
 
-static int dispatch_rows(QuadRowsArgs& A, int mt, hipStream_t st) {
+static int round_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+
+struct RowsShape {
+  int rg, chunk, waves_per_wg;
+};
+
+static RowsShape rows_shape(int mt) {
   switch (mt) {
-    case 1: return launch_rows<1, 4>(A, st);
-    case 2: return launch_rows<2, 2>(A, st);
-    case 4: return launch_rows<4, 1>(A, st);
-    default: return launch_rows<8, 1>(A, st);
+    case 1: return {RowsCfg<1>::RG, RowsCfg<1>::NSEG * QSEG, RowsCfg<1>::NT / 64};
+    case 2: return {RowsCfg<2>::RG, RowsCfg<2>::NSEG * QSEG, RowsCfg<2>::NT / 64};
+    case 4: return {RowsCfg<4>::RG, RowsCfg<4>::NSEG * QSEG, RowsCfg<4>::NT / 64};
+    default: return {RowsCfg<8>::RG, RowsCfg<8>::NSEG * QSEG, RowsCfg<8>::NT / 64};
   }
 }
 
-static int rows_rg(int mt) { return mt == 1 ? 4 : (mt == 2 ? 2 : 1); }
-static int round_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+static int dispatch_rows(QuadRowsArgs& A, int mt, int64_t grid, hipStream_t st) {
+  switch (mt) {
+    case 1: return launch_rows<1>(A, grid, st);
+    case 2: return launch_rows<2>(A, grid, st);
+    case 4: return launch_rows<4>(A, grid, st);
+    default: return launch_rows<8>(A, grid, st);
+  }
+}
 
 struct RowsPlan {
-  int rg, n_rowgroups, n_slices, slice_len;
-  int64_t n_tasks;
-  int64_t part_bytes, counter_bytes, plug_bytes;
-  int64_t total() const { return part_bytes + counter_bytes + plug_bytes; }
+  int rows_per_task;
+  int64_t n_tasks, grid, plug_bytes;
+  int64_t total() const { return plug_bytes; }
 };
 
-static RowsPlan plan_rows(int64_t M, int64_t N, int64_t K, int64_t plug_n) {
+// Single-projection tasks: full rows, RG per task, or 1 per task when that keeps more
+// waves busy; as many workgroups (one per CU at most: the LDS tables fill it) as tasks need.
+static RowsPlan plan_rows(int64_t M, int64_t N, int64_t plug_n) {
   RowsPlan p;
   const int mt = round_mt(M);
-  p.rg = rows_rg(mt);
-  p.n_rowgroups = (int)((N + p.rg - 1) / p.rg);
-  // split K so that the grid has several tasks per wave and a task streams >= 2048 codes per row
-  const int64_t waves = (int64_t)device_cu_count() * (rows_threads(mt) / 64);
-  const int64_t segs = (K + QSEG - 1) / QSEG;
-  int64_t want = (4 * waves + p.n_rowgroups - 1) / p.n_rowgroups;
-  want = std::max<int64_t>(1, std::min<int64_t>(want, std::max<int64_t>(1, K / 2048)));
-  const int64_t segs_per_slice = (segs + want - 1) / want;
-  p.slice_len = (int)(segs_per_slice * QSEG);
-  p.n_slices = (int)((K + p.slice_len - 1) / p.slice_len);
-  p.n_tasks = (int64_t)p.n_rowgroups * p.n_slices;
-  const int nv = p.rg * 4 * mt;
-  p.part_bytes = p.n_slices > 1 ? ((int64_t)p.n_rowgroups * p.n_slices * nv * 4 + 255) / 256 * 256 : 0;
-  p.counter_bytes = p.n_slices > 1 ? ((int64_t)p.n_rowgroups * 4 + 255) / 256 * 256 : 0;
-  p.plug_bytes = plug_n > 0 ? ((int64_t)(p.n_rowgroups + 1) * 8 + 255) / 256 * 256 : 0;
+  const RowsShape sh = rows_shape(mt);
+  const int64_t waves = (int64_t)device_cu_count() * sh.waves_per_wg;
+  p.rows_per_task = ((N + sh.rg - 1) / sh.rg >= waves) ? sh.rg : 1;
+  p.n_tasks = (N + p.rows_per_task - 1) / p.rows_per_task;
+  p.grid = std::max<int64_t>(1, std::min<int64_t>(device_cu_count(), (p.n_tasks + sh.waves_per_wg - 1) / sh.waves_per_wg));
+  p.plug_bytes = plug_n > 0 ? ((p.n_tasks + 1) * 8 + 255) / 256 * 256 : 0;
   return p;
 }
 
@@ -543,7 +622,7 @@ extern "C" int64_t pp_quad_gemm_workspace_size(const void* a, int64_t a_sm, int6
                                                int64_t c_sk, int64_t c_sn, int64_t plug_n, int64_t M, int64_t N,
                                                int64_t K) {
   if (M <= 0 || N <= 0) return 0;
-  if (rows_fast_ok(a, a_sm, a_sk, codes, c_sk, c_sn, M, K)) return plan_rows(M, N, K, plug_n).total();
+  if (rows_fast_ok(a, a_sm, a_sk, codes, c_sk, c_sn, M, K)) return plan_rows(M, N, plug_n).total();
   return 4 * N * K * (int64_t)sizeof(float);
 }
 
@@ -614,10 +693,9 @@ extern "C" int pp_quad_gemm(const void* a, int64_t a_sm, int64_t a_sk, const uin
   const int64_t need = pp_quad_gemm_workspace_size(a, a_sm, a_sk, codes, c_sk, c_sn, plug_n, M, N, K);
   const bool fast = rows_fast_ok(a, a_sm, a_sk, codes, c_sk, c_sn, M, K);
   if (fast) {
-    const RowsPlan p = plan_rows(M, N, K, plug_n);
+    const RowsPlan p = plan_rows(M, N, plug_n);
     PP_REQUIRE(workspace_bytes >= p.total() && (p.total() == 0 || workspace != nullptr),
                "workspace too small: need %lld bytes", (long long)p.total());
-    char* ws = reinterpret_cast<char*>(workspace);
     QuadRowsArgs A = {};
     A.proj.codes = codes;
     A.proj.ldc = c_sn;
@@ -629,8 +707,7 @@ extern "C" int pp_quad_gemm(const void* a, int64_t a_sm, int64_t a_sk, const uin
     A.proj.N = (int32_t)N;
     A.proj.K = (int32_t)K;
     A.o_sn = o_sn;
-    A.n_slices = p.n_slices;
-    A.slice_len = p.slice_len;
+    A.rows_per_task = p.rows_per_task;
     A.n_tasks = p.n_tasks;
     A.luts = make_luts(luts, lut_dtype);
     for (int m = 0; m < 4; ++m) A.s[m] = scales[m];
@@ -639,23 +716,14 @@ extern "C" int pp_quad_gemm(const void* a, int64_t a_sm, int64_t a_sk, const uin
     A.plug_n = plug_n;
     A.M = (int)M;
     A.n_codes = INT64_MAX;
-    A.part = p.part_bytes ? reinterpret_cast<float*>(ws) : nullptr;
-    A.counters = p.counter_bytes ? reinterpret_cast<uint32_t*>(ws + p.part_bytes) : nullptr;
-    A.part_stride = (int64_t)p.n_slices * p.rg * 4 * round_mt(M);
-    if (p.counter_bytes) {
-      // counters start at zero; a fill kernel rather than a memset node keeps graph capture safe
-      const int64_t nc = p.counter_bytes / 4;
-      hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, st, A.counters, nc);
-      PP_LAUNCH_CHECK();
-    }
     if (plug_n > 0) {
-      int64_t* rgp = reinterpret_cast<int64_t*>(ws + p.part_bytes + p.counter_bytes);
-      hipLaunchKernelGGL(rowgroup_plug_kernel, dim3((p.n_rowgroups + 1 + 255) / 256), dim3(256), 0, st, plug_idx,
-                         plug_n, elem_base, c_sn, p.rg, p.n_rowgroups, (int)N, rgp);
+      int64_t* rgp = reinterpret_cast<int64_t*>(workspace);
+      hipLaunchKernelGGL(rowgroup_plug_kernel, dim3((unsigned)((p.n_tasks + 1 + 255) / 256)), dim3(256), 0, st,
+                         plug_idx, plug_n, elem_base, c_sn, p.rows_per_task, (int)p.n_tasks, (int)N, rgp);
       PP_LAUNCH_CHECK();
       A.rg_plug = rgp;
     }
-    return dispatch_rows(A, round_mt(M), st);
+    return dispatch_rows(A, round_mt(M), p.grid, st);
   }
   // generic: dequantise into the workspace, then multiply
   PP_REQUIRE(workspace_bytes >= need && workspace != nullptr, "workspace too small: need %lld bytes",
@@ -684,30 +752,40 @@ extern "C" int pp_quad_gemm(const void* a, int64_t a_sm, int64_t a_sk, const uin
   return PP_OK;
 }
 
-extern "C" int pp_quad_stream_layout(int64_t M, int* rows_per_item, int* values_per_slice) {
-  PP_REQUIRE(M >= 1 && M <= 8, "the stream decode takes 1..8 tokens, got %lld", (long long)M);
-  const int mt = round_mt(M);
-  if (rows_per_item) *rows_per_item = rows_rg(mt);
-  if (values_per_slice) *values_per_slice = rows_rg(mt) * 4 * mt;
-  return PP_OK;
+extern "C" int pp_quad_stream_rows(int64_t M) {
+  if (M < 1 || M > 8) {
+    set_error("the stream decode takes 1..8 tokens, got %lld", (long long)M);
+    return 0;
+  }
+  return rows_shape(round_mt(M)).rg;
 }
 
-extern "C" int pp_quad_stream(const pp_quad_proj* projs, const pp_quad_item* items, int64_t n_items,
+extern "C" int64_t pp_quad_stream_waves(int64_t M) {
+  if (M < 1 || M > 8) return 0;
+  return (int64_t)device_cu_count() * rows_shape(round_mt(M)).waves_per_wg;
+}
+
+extern "C" int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs, const pp_quad_item* items, int64_t n_items,
+                              const int64_t* wave_bounds, int64_t n_waves,
                               const float* const* luts, const float* scales, const uint32_t* plug_idx,
                               const void* plug_vals, int64_t n_codes, const void* const* tails,
-                              const int64_t* tail_len, int64_t M, float* part, int64_t max_slices,
-                              uint32_t* counters, void* stream) {
+                              const int64_t* tail_len, int64_t M, void* stream) {
   PP_REQUIRE(projs && items, "projs / items are null");
   PP_REQUIRE(luts != nullptr, "luts is null");
   for (int i = 0; i < 7; ++i) PP_REQUIRE(luts[i] != nullptr, "lut %d is null", i);
   PP_REQUIRE(scales != nullptr, "scales is null");
   PP_REQUIRE(M >= 1 && M <= 8, "the stream decode takes 1..8 tokens, got %lld", (long long)M);
-  PP_REQUIRE(max_slices <= 1 || (part != nullptr && counters != nullptr), "split-K items need part / counters");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (n_items == 0) return PP_OK;
+  PP_REQUIRE(wave_bounds == nullptr || n_waves == pp_quad_stream_waves(M),
+             "wave_bounds were built for %lld waves, this device launches %lld", (long long)n_waves,
+             (long long)pp_quad_stream_waves(M));
+  PP_REQUIRE(n_projs >= 1, "no projections");
   QuadRowsArgs A = {};
   A.projs = projs;
+  A.n_projs = n_projs;
   A.items = items;
+  A.wave_bounds = wave_bounds;
   A.n_tasks = n_items;
   A.luts = make_luts(reinterpret_cast<const void* const*>(luts), PP_F32);
   for (int m = 0; m < 4; ++m) A.s[m] = scales[m];
@@ -719,9 +797,5 @@ extern "C" int pp_quad_stream(const pp_quad_proj* projs, const pp_quad_item* ite
     A.tails[m] = tails ? reinterpret_cast<const f16*>(tails[m]) : nullptr;
     A.tail_len[m] = tail_len ? tail_len[m] : 0;
   }
-  const int mt = round_mt(M);
-  A.part = part;
-  A.part_stride = std::max<int64_t>(max_slices, 1) * rows_rg(mt) * 4 * mt;
-  A.counters = counters;
-  return dispatch_rows(A, mt, st);
+  return dispatch_rows(A, round_mt(M), device_cu_count(), st);
 }

@@ -61,8 +61,7 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
         nat.check(rc, "pp_dual_gemm")
 
 
-def test_stream_layout_query():
-    r, v = C.c_int(), C.c_int()
-    assert nat.lib().pp_quad_stream_layout(1, C.byref(r), C.byref(v)) == 0
-    assert (r.value, v.value) == (4, 16)
-    assert nat.lib().pp_quad_stream_layout(9, C.byref(r), C.byref(v)) == nat.PP_EINVAL
+def test_stream_rows_query():
+    assert nat.lib().pp_quad_stream_rows(1) >= 1
+    assert nat.lib().pp_quad_stream_rows(9) == 0
+    assert b"1..8" in nat.lib().pp_last_error()
