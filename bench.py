@@ -123,10 +123,20 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=36)
-    ap.add_argument("--cpu-sample-tuples", type=int, default=25_000_000)
+    ap.add_argument("--cpu-sample-tuples", type=int, default=77_070_336)  # one layer
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 2 GiB device-to-device copy (reference for the rocprof byte counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        src = torch.ones(2 << 30, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": 2 << 30, "launches": 3}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (the decode step is a "
               "single-GPU path; see DESIGN.md for how it would shard)", file=sys.stderr)
@@ -152,7 +162,7 @@ def main():
     for x in xs:
         x.copy_(torch.randn(x.shape, generator=g, device=dev).to(torch.float16))
     st.bind(xs, outs)
-    log(f"[bench] plan: {st.n_items} items, {st.n_waves} waves, {st.n_groups} split-K groups")
+    log(f"[bench] plan: {st.n_items} items, {st.n_tail} tail items, {st.n_waves} waves")
 
     # sanity: the stream output equals the per-projection operator on a k_proj and a down_proj
     st()

@@ -113,9 +113,10 @@ int pp_quad_dequant(const uint32_t* codes, int64_t c_sk, int64_t c_sn,
  *   luts   : 7 float32 LUTs from the header (r_max, mu);
  *   scales : host float[4], the header RMS s_k.
  *
- * Rows touching stream positions >= n_codes (FP16 tails) are listed as
- * items with flags & PP_ITEM_TAIL and decoded from tails[m] (fp16, length
- * tail_len[m], model m's positions n_codes .. n_codes+tail_len[m]-1).
+ * Rows touching stream positions >= n_codes (FP16 tails) are listed apart, in
+ * tail_items (one row each, flags PP_ITEM_TAIL), and decoded from tails[m] (fp16,
+ * length tail_len[m], model m's positions n_codes .. n_codes+tail_len[m]-1) by a
+ * second, small kernel.
  * Replaces the per-projection quad_bitpacked calls of a decode step and the
  * tail restore of unpack_quad (quaternion_packer.py:201-210).
  */
@@ -151,6 +152,7 @@ int pp_quad_stream_rows(int64_t M);
 int64_t pp_quad_stream_waves(int64_t M);
 
 int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs, const pp_quad_item* items, int64_t n_items,
+                   const pp_quad_item* tail_items, int64_t n_tail,
                    const int64_t* wave_bounds, int64_t n_waves,
                    const float* const* luts, const float* scales,
                    const uint32_t* plug_idx, const void* plug_vals,

@@ -18,10 +18,11 @@
 //                        (rx = r*x: 3 mul + 4 fma per tuple at batch 1).  Plug entries of
 //                        the task are located up front and their dependent loads ride
 //                        with the first chunk; each is applied as an exact correction
-//                        x*(plug - decoded) before the wave reduction.  Rows that reach
-//                        FP16 tail positions are one-row tasks on a scalar path.  No
-//                        task spans waves, so no cross-wave combine (and no device-scope
-//                        fence, which costs an L2 writeback on this part) is needed.
+//                        x*(plug - decoded) before the wave reduction.  No task spans
+//                        waves, so no cross-wave combine (and no device-scope fence,
+//                        which costs an L2 writeback on this part) is needed.
+//   quad_tail_kernel  -- rows that reach FP16 tail positions, one row per wavefront on
+//                        a scalar path (a handful of rows per stream).
 //   quad_dequant_kernel / quad_plug_scatter_kernel -- float32 weights (parity export
 //                        and the generic path); quad_ws_gemm_kernel multiplies them.
 #include "pp_common.h"
@@ -31,22 +32,20 @@
 
 namespace pp {
 
-constexpr int QREPL_R = 32;   // norm table replicas (ds_read_b32 serves 32 lanes per clock)
-constexpr int QREPL_C = 16;   // (cos, sin) table replicas (ds_read_b64 serves 16 lanes per clock)
 constexpr int QSEG = 256;     // codes per wave per row per step (64 lanes x 4)
-using QLds = QuadLds<QREPL_R, QREPL_C>;
+constexpr int QPROJ_CACHE = 256;   // projection descriptors staged in LDS (22.5 KiB)
+using QLds = QuadLdsP;
 
+// Uniform (scalar-register) state of a task; kept small, the pipeline holds one.
 struct QTask {
-  const uint32_t* codes;  // code of (row0, k0)
-  int64_t ldc;            // row stride of codes
-  int64_t pos_row0;       // stream position of (row0, 0)
+  const uint32_t* codes;  // code of (row0, 0)
   const f16* x;           // x(0, 0)
-  int64_t x_sm;
-  f16* out[4];            // out_m(0, row0)
-  int64_t o_sm, o_sn;
-  int nrows, K, k0, k1;
+  int64_t pos_row0;       // stream position of (row0, 0)
   int64_t plug_lo, plug_hi;
-  int tail;
+  int ldc;                // row stride of codes
+  int x_sm;               // row stride of x
+  int nrows, K, tail;
+  int proj, row0;         // for the output pointers, read when the task finishes
 };
 
 struct QuadRowsArgs {
@@ -81,7 +80,7 @@ struct QuadRowsArgs {
 #define PP_ROWS1_RG 4
 #endif
 #ifndef PP_ROWS1_NSEG
-#define PP_ROWS1_NSEG 4
+#define PP_ROWS1_NSEG 2
 #endif
 #ifndef PP_ROWS1_NT
 #define PP_ROWS1_NT 1024
@@ -97,7 +96,7 @@ __device__ __forceinline__ void plug_apply(const QLds& T, const QuadRowsArgs& A,
                                            uint32_t cw, f16x4 pv, const float (&xk)[MT], float (&acc)[RG][4][MT]) {
   const int lane = threadIdx.x & 63;
   float wd[4];
-  quad_decode(T, cw, lane % QREPL_R, lane % QREPL_C, wd[0], wd[1], wd[2], wd[3]);
+  quad_decode_p(T, cw, quad_lane_offsets(lane), wd[0], wd[1], wd[2], wd[3]);
   const float dlt[4] = {(float)pv.x - wd[0], (float)pv.y - wd[1], (float)pv.z - wd[2], (float)pv.w - wd[3]};
   // every row is updated with a 0/1 weight: a branch on `row` would be folded into a
   // per-lane index into acc[], which puts the accumulators in scratch memory
@@ -120,125 +119,177 @@ __device__ __forceinline__ int plug_locate(const QuadRowsArgs& A, const QTask& t
   for (int r = 1; r < RG; ++r)
     if (off >= (int64_t)r * t.ldc) row = r;
   k = (int)(off - (int64_t)row * t.ldc);
-  const bool in = off >= 0 && row < t.nrows && k >= t.k0 && k < t.k1;
+  const bool in = off >= 0 && row < t.nrows && k < t.K;
   return in ? row : -1;
 }
 
+// One chunk of a task: RG rows x NSEG segments of 256 codes, plus the activations.
 template <int MT, int RG, int NSEG>
-__device__ __forceinline__ void rows_item(const QLds& T, const QuadRowsArgs& A, const QTask& t,
-                                          float (&acc)[RG][4][MT]) {
+struct Chunk {
+  u32x4 q[RG][NSEG];
+  f16x4 xh[MT][NSEG];
+};
+
+// Issue every load of chunk [kc, kc + NSEG*256) of task t (codes past the row, rows past
+// nrows and tokens past M read as zero).
+template <int MT, int RG, int NSEG>
+__device__ __forceinline__ void chunk_issue(const QuadRowsArgs& A, const QTask& t, int kc, Chunk<MT, RG, NSEG>& c) {
   const int lane = threadIdx.x & 63;
-  const int rr = lane % QREPL_R, rc = lane % QREPL_C;
-  constexpr int CHUNK = NSEG * QSEG;
+  const int len = t.K - kc;
+  const f16* xb = t.x + kc + 4 * lane;
+#pragma unroll
+  for (int s = 0; s < NSEG; ++s) {
+    const bool valid = s * QSEG + 4 * lane < len;
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+      c.xh[j][s] = (valid && j < A.M) ? *reinterpret_cast<const f16x4*>(xb + (int64_t)j * t.x_sm + s * QSEG)
+                                      : f16x4{0, 0, 0, 0};
+  }
+  const uint32_t* cb = t.codes + kc + 4 * lane;
 #pragma unroll
   for (int r = 0; r < RG; ++r)
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int j = 0; j < MT; ++j) acc[r][m][j] = 0.f;
+    for (int s = 0; s < NSEG; ++s)
+      c.q[r][s] = (r < t.nrows && s * QSEG + 4 * lane < len) ? load_nt(cb + (int64_t)r * t.ldc + s * QSEG)
+                                                            : u32x4{0u, 0u, 0u, 0u};
+}
 
-  // first 64 plug entries of the task: positions now, dependent loads with the first chunk
-  const int64_t n_plug = t.plug_hi - t.plug_lo;
-  int prow = -1, pk = 0;
-  if (lane < n_plug) prow = plug_locate<RG>(A, t, t.plug_lo + lane, pk);
-  uint32_t pcw = 0;
-  f16x4 pv = {0, 0, 0, 0};
-  float pxk[MT];
+// Decode a chunk and accumulate: LDS lookups addressed with one v_perm each, x folded
+// into the norm at batch 1 (3 mul + 4 fma per tuple).
+template <int MT, int RG, int NSEG>
+__device__ __forceinline__ void chunk_compute(const QLds& T, const QuadRowsArgs& A, const Chunk<MT, RG, NSEG>& c,
+                                              float (&acc)[RG][4][MT]) {
+  const QuadLaneOff lo = quad_lane_offsets(threadIdx.x & 63);
+  const char* lds = reinterpret_cast<const char*>(T.w);
 #pragma unroll
-  for (int j = 0; j < MT; ++j) pxk[j] = 0.f;
-
-  const f16* xbase = t.x + t.k0 + 4 * lane;
-  const uint32_t* cbase = t.codes + 4 * lane;
-  for (int kc = 0; kc < t.k1 - t.k0; kc += CHUNK) {
-    const int len = t.k1 - t.k0 - kc;   // codes of the row left from kc on
-    // all activations and codes of the chunk, issued back to back
-    f16x4 xh[MT][NSEG];
+  for (int s = 0; s < NSEG; ++s) {
+    float xv[MT][4];
 #pragma unroll
-    for (int s = 0; s < NSEG; ++s) {
-      const bool valid = s * QSEG + 4 * lane < len;
-#pragma unroll
-      for (int j = 0; j < MT; ++j)
-        xh[j][s] = (valid && j < A.M)
-                       ? *reinterpret_cast<const f16x4*>(xbase + (int64_t)j * t.x_sm + kc + s * QSEG)
-                       : f16x4{0, 0, 0, 0};
-    }
-    u32x4 q[RG][NSEG];
-#pragma unroll
-    for (int r = 0; r < RG; ++r)
-#pragma unroll
-      for (int s = 0; s < NSEG; ++s)
-        q[r][s] = (r < t.nrows && s * QSEG + 4 * lane < len)
-                      ? load_nt(cbase + (int64_t)r * t.ldc + kc + s * QSEG)
-                      : u32x4{0u, 0u, 0u, 0u};
-    if (kc == 0 && prow >= 0) {
-      pcw = t.codes[(int64_t)prow * t.ldc + (pk - t.k0)];
-      pv = *reinterpret_cast<const f16x4*>(A.plug_vals + 4 * (t.plug_lo + lane));
-#pragma unroll
-      for (int j = 0; j < MT; ++j)
-        if (j < A.M) pxk[j] = (float)t.x[(int64_t)j * t.x_sm + pk];
+    for (int j = 0; j < MT; ++j) {
+      xv[j][0] = (float)c.xh[j][s].x;
+      xv[j][1] = (float)c.xh[j][s].y;
+      xv[j][2] = (float)c.xh[j][s].z;
+      xv[j][3] = (float)c.xh[j][s].w;
     }
 #pragma unroll
-    for (int s = 0; s < NSEG; ++s) {
-      float xv[MT][4];
+    for (int r = 0; r < RG; ++r) {
+      const uint32_t cw4[4] = {c.q[r][s].x, c.q[r][s].y, c.q[r][s].z, c.q[r][s].w};
 #pragma unroll
-      for (int j = 0; j < MT; ++j) {
-        xv[j][0] = (float)xh[j][s].x;
-        xv[j][1] = (float)xh[j][s].y;
-        xv[j][2] = (float)xh[j][s].z;
-        xv[j][3] = (float)xh[j][s].w;
-      }
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t cw = cw4[e];
+        const float rv = *reinterpret_cast<const float*>(lds + quad_lds_addr<3>(cw, lo.r));
+        const float2 a = *reinterpret_cast<const float2*>(lds + quad_lds_addr<2>(cw, lo.c1));
+        const float2 b = *reinterpret_cast<const float2*>(lds + quad_lds_addr<1>(cw, lo.c2));
+        const float2 d = *reinterpret_cast<const float2*>(lds + quad_lds_addr<0>(cw, lo.c3));
+        if constexpr (MT == 1) {
+          const float rx = rv * xv[0][e];
+          acc[r][0][0] = fmaf(rx, a.x, acc[r][0][0]);
+          const float t1 = rx * a.y;
+          acc[r][1][0] = fmaf(t1, b.x, acc[r][1][0]);
+          const float t2 = t1 * b.y;
+          acc[r][2][0] = fmaf(t2, d.x, acc[r][2][0]);
+          acc[r][3][0] = fmaf(t2, d.y, acc[r][3][0]);
+        } else {
+          const float rs = rv * a.y;
+          const float rss = rs * b.y;
+          const float w[4] = {rv * a.x, rs * b.x, rss * d.x, rss * d.y};
 #pragma unroll
-      for (int r = 0; r < RG; ++r) {
-        const uint32_t cw4[4] = {q[r][s].x, q[r][s].y, q[r][s].z, q[r][s].w};
+          for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t cw = cw4[e];
-          const float rv = T.r[(cw >> 24) * QREPL_R + rr];
-          const float2 a = T.cs1[((cw >> 16) & 255u) * QREPL_C + rc];
-          const float2 b = T.cs2[((cw >> 8) & 255u) * QREPL_C + rc];
-          const float2 c = T.cs3[(cw & 255u) * QREPL_C + rc];
-          if constexpr (MT == 1) {
-            const float rx = rv * xv[0][e];
-            acc[r][0][0] = fmaf(rx, a.x, acc[r][0][0]);
-            const float t1 = rx * a.y;
-            acc[r][1][0] = fmaf(t1, b.x, acc[r][1][0]);
-            const float t2 = t1 * b.y;
-            acc[r][2][0] = fmaf(t2, c.x, acc[r][2][0]);
-            acc[r][3][0] = fmaf(t2, c.y, acc[r][3][0]);
-          } else {
-            const float rs = rv * a.y;
-            const float rss = rs * b.y;
-            const float w[4] = {rv * a.x, rs * b.x, rss * c.x, rss * c.y};
-#pragma unroll
-            for (int m = 0; m < 4; ++m)
-#pragma unroll
-              for (int j = 0; j < MT; ++j) acc[r][m][j] = fmaf(w[m], xv[j][e], acc[r][m][j]);
-          }
+            for (int j = 0; j < MT; ++j) acc[r][m][j] = fmaf(w[m], xv[j][e], acc[r][m][j]);
         }
       }
     }
   }
-  // plug corrections: x_k * (plug - decoded) on the lane that holds the entry
-  if (prow >= 0) plug_apply<MT, RG>(T, A, t, prow, pcw, pv, pxk, acc);
+}
+
+// Plug entries of a task: the first 64 are located when the task starts (one load of
+// their positions), their dependent loads (plugged code, fp16 values, x at the column)
+// are issued a chunk later, and all of them are applied when the task ends.
+template <int MT>
+struct PlugPre {
+  int prow, pk;
+  uint32_t pcw;
+  f16x4 pv;
+  float pxk[MT];
+};
+
+template <int MT, int RG>
+__device__ __forceinline__ void plug_locate_first(const QuadRowsArgs& A, const QTask& t, PlugPre<MT>& p) {
+  const int lane = threadIdx.x & 63;
+  p.prow = -1;
+  p.pk = 0;
+  if (lane < t.plug_hi - t.plug_lo) p.prow = plug_locate<RG>(A, t, t.plug_lo + lane, p.pk);
+}
+
+template <int MT>
+__device__ __forceinline__ void plug_issue_deps(const QuadRowsArgs& A, const QTask& t, PlugPre<MT>& p) {
+  const int lane = threadIdx.x & 63;
+  p.pcw = 0;
+  p.pv = f16x4{0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < MT; ++j) p.pxk[j] = 0.f;
+  if (p.prow >= 0) {
+    p.pcw = t.codes[(int64_t)p.prow * t.ldc + p.pk];
+    p.pv = *reinterpret_cast<const f16x4*>(A.plug_vals + 4 * (t.plug_lo + lane));
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+      if (j < A.M) p.pxk[j] = (float)t.x[(int64_t)j * t.x_sm + p.pk];
+  }
+}
+
+template <int MT, int RG>
+__device__ __forceinline__ void plug_finish(const QLds& T, const QuadRowsArgs& A, const QTask& t,
+                                            const PlugPre<MT>& p, float (&acc)[RG][4][MT]) {
+  const int lane = threadIdx.x & 63;
+  if (p.prow >= 0) plug_apply<MT, RG>(T, A, t, p.prow, p.pcw, p.pv, p.pxk, acc);
   // tasks with more than 64 entries (dense plug tables): the rest, 64 at a time
   for (int64_t p0 = t.plug_lo + 64; p0 < t.plug_hi; p0 += 64) {
-    const int64_t p = p0 + lane;
-    if (p >= t.plug_hi) continue;
+    const int64_t q = p0 + lane;
+    if (q >= t.plug_hi) continue;
     int k;
-    const int row = plug_locate<RG>(A, t, p, k);
+    const int row = plug_locate<RG>(A, t, q, k);
     if (row < 0) continue;
     float xk[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) xk[j] = j < A.M ? (float)t.x[(int64_t)j * t.x_sm + k] : 0.f;
-    plug_apply<MT, RG>(T, A, t, row, t.codes[(int64_t)row * t.ldc + (k - t.k0)],
-                       *reinterpret_cast<const f16x4*>(A.plug_vals + 4 * p), xk, acc);
+    plug_apply<MT, RG>(T, A, t, row, t.codes[(int64_t)row * t.ldc + k],
+                       *reinterpret_cast<const f16x4*>(A.plug_vals + 4 * q), xk, acc);
   }
+}
+
+// Output pointers of a task (read from the projection descriptor when the task writes).
+struct OutPtrs {
+  f16* p[4];
+  int64_t o_sm, o_sn;
+};
+
+__device__ __forceinline__ OutPtrs task_outputs(const QuadRowsArgs& A, const pp_quad_proj* Pc, const QTask& t) {
+  OutPtrs o;
+  if (t.proj < 0) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) o.p[m] = reinterpret_cast<f16*>(A.proj.out[m]) + (int64_t)t.row0 * A.o_sn;
+    o.o_sm = A.proj.o_sm;
+    o.o_sn = A.o_sn;
+  } else if (Pc != nullptr && t.proj < QPROJ_CACHE) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) o.p[m] = reinterpret_cast<f16*>(uniform_ptr(Pc[t.proj].out[m])) + t.row0;
+    o.o_sm = uniform64(Pc[t.proj].o_sm);
+    o.o_sn = 1;
+  } else {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) o.p[m] = reinterpret_cast<f16*>(A.projs[t.proj].out[m]) + t.row0;
+    o.o_sm = A.projs[t.proj].o_sm;
+    o.o_sn = 1;
+  }
+  return o;
 }
 
 // A row that reaches FP16 tail positions (>= n_codes), element by element:
 // y_m = s_m * sum_{pos < n} x * decoded_m  +  sum_{n <= pos} x * tail_m[pos - n].
 template <int MT>
-__device__ __forceinline__ void rows_tail_task(const QLds& T, const QuadRowsArgs& A, const QTask& t) {
+__device__ __forceinline__ void rows_tail_task(const QuadLds<1, 1>& T, const QuadRowsArgs& A,
+                                               const pp_quad_proj* Pc, const QTask& t) {
   const int lane = threadIdx.x & 63;
   float accc[4][MT], acct[4][MT];
 #pragma unroll
@@ -252,7 +303,7 @@ __device__ __forceinline__ void rows_tail_task(const QLds& T, const QuadRowsArgs
     for (int j = 0; j < MT; ++j) xk[j] = j < A.M ? (float)t.x[(int64_t)j * t.x_sm + k] : 0.f;
     if (pos < A.n_codes) {
       float w[4];
-      quad_decode(T, t.codes[k], lane % QREPL_R, lane % QREPL_C, w[0], w[1], w[2], w[3]);
+      quad_decode(T, t.codes[k], 0, 0, w[0], w[1], w[2], w[3]);
 #pragma unroll
       for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -275,7 +326,7 @@ __device__ __forceinline__ void rows_tail_task(const QLds& T, const QuadRowsArgs
     const int64_t k = (int64_t)A.plug_idx[p] - t.pos_row0;
     if (k < 0 || k >= t.K || t.pos_row0 + k >= A.n_codes) continue;
     float wd[4];
-    quad_decode(T, t.codes[k], lane % QREPL_R, lane % QREPL_C, wd[0], wd[1], wd[2], wd[3]);
+    quad_decode(T, t.codes[k], 0, 0, wd[0], wd[1], wd[2], wd[3]);
     const f16x4 pv = *reinterpret_cast<const f16x4*>(A.plug_vals + 4 * p);
     const float dlt[4] = {(float)pv.x - wd[0], (float)pv.y - wd[1], (float)pv.z - wd[2], (float)pv.w - wd[3]};
 #pragma unroll
@@ -286,6 +337,7 @@ __device__ __forceinline__ void rows_tail_task(const QLds& T, const QuadRowsArgs
       for (int m = 0; m < 4; ++m) accc[m][j] = fmaf(xk, dlt[m], accc[m][j]);
     }
   }
+  const OutPtrs o = task_outputs(A, Pc, t);
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     // a model whose stream ends before this row does not have the row: it reads 0
@@ -293,13 +345,14 @@ __device__ __forceinline__ void rows_tail_task(const QLds& T, const QuadRowsArgs
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
       const float v = wave_sum(accc[m][j]) * A.s[m] + wave_sum(acct[m][j]);
-      if (lane == 0 && j < A.M) t.out[m][(int64_t)j * t.o_sm] = (f16)(has ? v : 0.f);
+      if (lane == 0 && j < A.M) o.p[m][(int64_t)j * o.o_sm] = (f16)(has ? v : 0.f);
     }
   }
 }
 
 template <int MT, int RG>
-__device__ __forceinline__ void rows_finish(const QuadRowsArgs& A, const QTask& t, float (&acc)[RG][4][MT]) {
+__device__ __forceinline__ void rows_finish(const QuadRowsArgs& A, const pp_quad_proj* Pc, const QTask& t,
+                                            float (&acc)[RG][4][MT]) {
   const int lane = threadIdx.x & 63;
   // butterfly sums; lane r*MT + j keeps the 4 model sums of (row r, token j) and writes
   // them through statically indexed pointers (a per-lane model index would send the
@@ -315,55 +368,45 @@ __device__ __forceinline__ void rows_finish(const QuadRowsArgs& A, const QTask& 
         if (lane == r * MT + j) mine[m] = v;
       }
   const int r = lane / MT, j = lane % MT;
+  const OutPtrs o = task_outputs(A, Pc, t);
   if (lane < RG * MT && r < t.nrows && j < A.M) {
-    const int64_t off = (int64_t)j * t.o_sm + (int64_t)r * t.o_sn;
+    const int64_t off = (int64_t)j * o.o_sm + (int64_t)r * o.o_sn;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) t.out[m][off] = (f16)(mine[m] * A.s[m]);
+    for (int m = 0; m < 4; ++m) o.p[m][off] = (f16)(mine[m] * A.s[m]);
   }
 }
 
-constexpr int QPROJ_CACHE = 256;   // projection descriptors staged in LDS (22.5 KiB)
 
 // Task of stream item `it` on projection descriptor P (uniform values).
 template <int RG>
-__device__ __forceinline__ void task_from_item(const pp_quad_proj& P, int row0, int nrows, int flags, int64_t plo,
-                                               int64_t phi, QTask& t) {
-  const int64_t ldc = uniform64(P.ldc);
-  t.k0 = 0;
+__device__ __forceinline__ void task_from_item(const pp_quad_proj& P, int proj, int row0, int nrows, int flags,
+                                               int64_t plo, int64_t phi, QTask& t) {
+  const int ldc = uniform((int)P.ldc);
   t.K = uniform(P.K);
-  t.k1 = t.K;
   t.codes = uniform_ptr(P.codes) + (int64_t)row0 * ldc;
   t.ldc = ldc;
   t.pos_row0 = uniform64(P.pos0) + (int64_t)row0 * ldc;
   t.x = reinterpret_cast<const f16*>(uniform_ptr(P.x));
-  t.x_sm = uniform64(P.x_sm);
-#pragma unroll
-  for (int m = 0; m < 4; ++m) t.out[m] = reinterpret_cast<f16*>(uniform_ptr(P.out[m])) + row0;
-  t.o_sm = uniform64(P.o_sm);
-  t.o_sn = 1;
+  t.x_sm = uniform((int)P.x_sm);
   t.nrows = min(nrows, RG);
   t.plug_lo = plo;
   t.plug_hi = phi;
   t.tail = flags & PP_ITEM_TAIL;
+  t.proj = proj;
+  t.row0 = row0;
 }
 
 template <int MT, int RG>
 __device__ __forceinline__ void single_task(const QuadRowsArgs& A, int64_t ti, QTask& t) {
   const pp_quad_proj& P = A.proj;
   const int row0 = (int)ti * A.rows_per_task;
-  t.k0 = 0;
-  t.k1 = P.K;
+  t.K = P.K;
   t.codes = P.codes + (int64_t)row0 * P.ldc;
-  t.ldc = P.ldc;
+  t.ldc = (int)P.ldc;
   t.pos_row0 = P.pos0 + (int64_t)row0 * P.ldc;
   t.x = reinterpret_cast<const f16*>(P.x);
-  t.x_sm = P.x_sm;
-#pragma unroll
-  for (int m = 0; m < 4; ++m) t.out[m] = reinterpret_cast<f16*>(P.out[m]) + (int64_t)row0 * A.o_sn;
-  t.o_sm = P.o_sm;
-  t.o_sn = A.o_sn;
+  t.x_sm = (int)P.x_sm;
   t.nrows = min(A.rows_per_task, P.N - row0);
-  t.K = P.K;
   if (A.rg_plug != nullptr) {
     t.plug_lo = uniform64(A.rg_plug[ti]);
     t.plug_hi = uniform64(A.rg_plug[ti + 1]);
@@ -371,26 +414,64 @@ __device__ __forceinline__ void single_task(const QuadRowsArgs& A, int64_t ti, Q
     t.plug_lo = t.plug_hi = 0;
   }
   t.tail = 0;
+  t.proj = -1;
+  t.row0 = row0;
 }
 
-template <int MT, int RG, int NSEG>
-__device__ __forceinline__ void run_task(const QLds& T, const QuadRowsArgs& A, const QTask& t) {
-  if (t.tail) {
-    rows_tail_task<MT>(T, A, t);
-    return;
+// The tasks of one wavefront, in order: contiguous stream items (wave_bounds), items
+// dealt round robin, or row groups of the single-projection front end.  Stream item
+// records are read 64 at a time, one per lane, and handed out with readlane.
+struct TaskSource {
+  int64_t first, count, stride;
+  int64_t batch;       // batch of 64 records held in `rec`, -1 before the first
+  pp_quad_item rec;
+};
+
+template <int RG>
+__device__ __forceinline__ bool fetch_task(const QuadRowsArgs& A, const pp_quad_proj* Pc, TaskSource& S, int64_t i,
+                                           QTask& t) {
+  if (i >= S.count) return false;
+  if (A.items == nullptr) {
+    single_task<1, RG>(A, S.first + i, t);
+    return true;
   }
-  float acc[RG][4][MT];
-  rows_item<MT, RG, NSEG>(T, A, t, acc);
-  rows_finish<MT, RG>(A, t, acc);
+  const int lane = threadIdx.x & 63;
+  const int64_t b = i >> 6;
+  if (b != S.batch) {
+    S.batch = b;
+    const int64_t k = (b << 6) + lane;
+    S.rec = pp_quad_item{};
+    if (k < S.count) S.rec = A.items[S.first + k * S.stride];
+  }
+  const int j = (int)(i & 63);
+  const int proj = __builtin_amdgcn_readlane(S.rec.proj, j);
+  const int row0 = __builtin_amdgcn_readlane(S.rec.row0, j);
+  const int nrows = __builtin_amdgcn_readlane(S.rec.nrows, j);
+  const int flags = __builtin_amdgcn_readlane(S.rec.flags, j);
+  const int64_t plo = lane_read64(S.rec.plug_lo, j), phi = lane_read64(S.rec.plug_hi, j);
+  if (proj < QPROJ_CACHE) task_from_item<RG>(Pc[proj], proj, row0, nrows, flags, plo, phi, t);
+  else task_from_item<RG>(A.projs[proj], proj, row0, nrows, flags, plo, phi, t);
+  return true;
+}
+
+template <int MT, int RG>
+__device__ __forceinline__ void zero_acc(float (&acc)[RG][4][MT]) {
+#pragma unroll
+  for (int r = 0; r < RG; ++r)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) acc[r][m][j] = 0.f;
 }
 
 template <int MT>
 __global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_rows_kernel(const QuadRowsArgs A) {
   constexpr int RG = RowsCfg<MT>::RG, NSEG = RowsCfg<MT>::NSEG;
   constexpr int WAVES = RowsCfg<MT>::NT / 64;
+  constexpr int CHUNK = NSEG * QSEG;
   __shared__ QLds T;
   __shared__ pp_quad_proj Pc[QPROJ_CACHE];
-  quad_build_lds(T, A.luts);
+  quad_build_lds_p(T, A.luts);
   if (A.items != nullptr) {
     const int np = (int)min<int64_t>(A.n_projs, QPROJ_CACHE);
     constexpr int W = sizeof(pp_quad_proj) / 4;
@@ -399,48 +480,57 @@ __global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_rows_kernel(const QuadRo
     for (int i = threadIdx.x; i < np * W; i += blockDim.x) dst[i] = src[i];
   }
   __syncthreads();
-  const int lane = threadIdx.x & 63;
   const int64_t gw = (int64_t)blockIdx.x * WAVES + uniform(threadIdx.x >> 6);
   const int64_t nw = (int64_t)gridDim.x * WAVES;
-  if (A.items == nullptr) {
-    const int64_t t_begin = gw * A.n_tasks / nw, t_end = (gw + 1) * A.n_tasks / nw;
-    for (int64_t ti = t_begin; ti < t_end; ++ti) {
-      QTask t;
-      single_task<MT, RG>(A, ti, t);
-      run_task<MT, RG, NSEG>(T, A, t);
-    }
-    return;
-  }
-  // Stream items: with wave_bounds, wave gw runs the contiguous range [bounds[gw], bounds[gw+1]);
-  // without, items are dealt round robin (item i to wave i % nw), which keeps the pages all
-  // waves touch at one time inside a window of nw items.
-  int64_t first, count, stride;
-  if (A.wave_bounds != nullptr) {
-    first = uniform64(A.wave_bounds[gw]);
-    count = uniform64(A.wave_bounds[gw + 1]) - first;
-    stride = 1;
+  TaskSource S;
+  S.batch = -1;
+  if (A.items != nullptr && A.wave_bounds != nullptr) {
+    S.first = uniform64(A.wave_bounds[gw]);
+    S.count = uniform64(A.wave_bounds[gw + 1]) - S.first;
+    S.stride = 1;
+  } else if (A.items != nullptr) {
+    // round robin: item i to wave i % nw
+    S.first = gw;
+    S.count = gw < A.n_tasks ? (A.n_tasks - gw + nw - 1) / nw : 0;
+    S.stride = nw;
   } else {
-    first = gw;
-    count = gw < A.n_tasks ? (A.n_tasks - gw + nw - 1) / nw : 0;
-    stride = nw;
+    S.first = gw * A.n_tasks / nw;
+    S.count = (gw + 1) * A.n_tasks / nw - S.first;
+    S.stride = 1;
   }
-  // item records 64 at a time, one per lane; task j of the batch is read out of lane j
-  for (int64_t b = 0; b < count; b += 64) {
-    const int nb = (int)min<int64_t>(64, count - b);
-    pp_quad_item mine = {};
-    if (lane < nb) mine = A.items[first + (b + lane) * stride];
-    for (int j = 0; j < nb; ++j) {
-      const int proj = __builtin_amdgcn_readlane(mine.proj, j);
-      const int row0 = __builtin_amdgcn_readlane(mine.row0, j);
-      const int nrows = __builtin_amdgcn_readlane(mine.nrows, j);
-      const int flags = __builtin_amdgcn_readlane(mine.flags, j);
-      const int64_t plo = lane_read64(mine.plug_lo, j), phi = lane_read64(mine.plug_hi, j);
-      QTask t;
-      if (proj < QPROJ_CACHE) task_from_item<RG>(Pc[proj], row0, nrows, flags, plo, phi, t);
-      else task_from_item<RG>(A.projs[proj], row0, nrows, flags, plo, phi, t);
-      run_task<MT, RG, NSEG>(T, A, t);
+  QTask t;
+  for (int64_t i = 0; fetch_task<RG>(A, Pc, S, i, t); ++i) {
+    float acc[RG][4][MT];
+    zero_acc<MT, RG>(acc);
+    PlugPre<MT> pp;
+    plug_locate_first<MT, RG>(A, t, pp);
+    for (int kc = 0; kc < t.K; kc += CHUNK) {
+      Chunk<MT, RG, NSEG> c;
+      chunk_issue<MT, RG, NSEG>(A, t, kc, c);
+      if (kc == 0) plug_issue_deps<MT>(A, t, pp);
+      chunk_compute<MT, RG, NSEG>(T, A, c, acc);
     }
+    plug_finish<MT, RG>(T, A, t, pp, acc);
+    rows_finish<MT, RG>(A, Pc, t, acc);
   }
+}
+
+// Rows that reach the FP16 tails: one wavefront per tail item, compact tables.
+template <int MT>
+__global__ __launch_bounds__(256) void quad_tail_kernel(const QuadRowsArgs A) {
+  __shared__ QuadLds<1, 1> T;
+  quad_build_lds(T, A.luts);
+  __syncthreads();
+  const int64_t ti = (int64_t)blockIdx.x * 4 + uniform(threadIdx.x >> 6);
+  if (ti >= A.n_tasks) return;
+  const int lane = threadIdx.x & 63;
+  pp_quad_item rec = {};
+  if (lane == 0) rec = A.items[ti];
+  const int proj = __builtin_amdgcn_readlane(rec.proj, 0);
+  QTask t;
+  task_from_item<1>(A.projs[proj], proj, __builtin_amdgcn_readlane(rec.row0, 0), 1, PP_ITEM_TAIL,
+                    lane_read64(rec.plug_lo, 0), lane_read64(rec.plug_hi, 0), t);
+  rows_tail_task<MT>(T, A, nullptr, t);   // outputs from the global descriptor table
 }
 
 // Plug range start of each task: first entry with idx >= pos0 + task*rows_per_task*ldc.
@@ -766,27 +856,24 @@ extern "C" int64_t pp_quad_stream_waves(int64_t M) {
 }
 
 extern "C" int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs, const pp_quad_item* items, int64_t n_items,
-                              const int64_t* wave_bounds, int64_t n_waves,
-                              const float* const* luts, const float* scales, const uint32_t* plug_idx,
-                              const void* plug_vals, int64_t n_codes, const void* const* tails,
-                              const int64_t* tail_len, int64_t M, void* stream) {
-  PP_REQUIRE(projs && items, "projs / items are null");
+                              const pp_quad_item* tail_items, int64_t n_tail, const int64_t* wave_bounds,
+                              int64_t n_waves, const float* const* luts, const float* scales,
+                              const uint32_t* plug_idx, const void* plug_vals, int64_t n_codes,
+                              const void* const* tails, const int64_t* tail_len, int64_t M, void* stream) {
+  PP_REQUIRE(projs != nullptr && n_projs >= 1, "no projections");
+  PP_REQUIRE(n_items == 0 || items != nullptr, "items is null");
+  PP_REQUIRE(n_tail == 0 || tail_items != nullptr, "tail_items is null");
   PP_REQUIRE(luts != nullptr, "luts is null");
   for (int i = 0; i < 7; ++i) PP_REQUIRE(luts[i] != nullptr, "lut %d is null", i);
   PP_REQUIRE(scales != nullptr, "scales is null");
   PP_REQUIRE(M >= 1 && M <= 8, "the stream decode takes 1..8 tokens, got %lld", (long long)M);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (n_items == 0) return PP_OK;
   PP_REQUIRE(wave_bounds == nullptr || n_waves == pp_quad_stream_waves(M),
              "wave_bounds were built for %lld waves, this device launches %lld", (long long)n_waves,
              (long long)pp_quad_stream_waves(M));
-  PP_REQUIRE(n_projs >= 1, "no projections");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   QuadRowsArgs A = {};
   A.projs = projs;
   A.n_projs = n_projs;
-  A.items = items;
-  A.wave_bounds = wave_bounds;
-  A.n_tasks = n_items;
   A.luts = make_luts(reinterpret_cast<const void* const*>(luts), PP_F32);
   for (int m = 0; m < 4; ++m) A.s[m] = scales[m];
   A.plug_idx = plug_idx;
@@ -797,5 +884,25 @@ extern "C" int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs, const 
     A.tails[m] = tails ? reinterpret_cast<const f16*>(tails[m]) : nullptr;
     A.tail_len[m] = tail_len ? tail_len[m] : 0;
   }
-  return dispatch_rows(A, round_mt(M), device_cu_count(), st);
+  const int mt = round_mt(M);
+  if (n_items > 0) {
+    A.items = items;
+    A.wave_bounds = wave_bounds;
+    A.n_tasks = n_items;
+    if (int rc = dispatch_rows(A, mt, device_cu_count(), st)) return rc;
+  }
+  if (n_tail > 0) {
+    A.items = tail_items;
+    A.wave_bounds = nullptr;
+    A.n_tasks = n_tail;
+    const unsigned grid = (unsigned)((n_tail + 3) / 4);
+    switch (mt) {
+      case 1: hipLaunchKernelGGL(quad_tail_kernel<1>, dim3(grid), dim3(256), 0, st, A); break;
+      case 2: hipLaunchKernelGGL(quad_tail_kernel<2>, dim3(grid), dim3(256), 0, st, A); break;
+      case 4: hipLaunchKernelGGL(quad_tail_kernel<4>, dim3(grid), dim3(256), 0, st, A); break;
+      default: hipLaunchKernelGGL(quad_tail_kernel<8>, dim3(grid), dim3(256), 0, st, A); break;
+    }
+    PP_LAUNCH_CHECK();
+  }
+  return PP_OK;
 }

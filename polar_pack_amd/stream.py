@@ -112,8 +112,12 @@ class QuadStream:
             if k % 4 or k >= 2 ** 31 or n >= 2 ** 31:
                 raise ValueError(f"stream decode needs K % 4 == 0 (got N={n}, K={k})")
         items = plan_items(self.shapes, pack.n, pack.plug_host(), self.rows_per_item)
+        is_tail = (items["flags"] & nat.PP_ITEM_TAIL) != 0
+        self.tail_items_np = items[is_tail]
+        items = items[~is_tail]
         self.items_np = items
         self.n_items = items.size
+        self.n_tail = self.tail_items_np.size
         self.item_bytes = item_bytes(items, self.shapes, self.M)
         self.n_waves = int(L.pp_quad_stream_waves(self.M))
         if schedule not in ("interleave", "bytes"):
@@ -122,6 +126,7 @@ class QuadStream:
         self.bounds_np = wave_bounds(self.item_bytes, self.n_waves)
         dev = self.device
         self.items = torch.from_numpy(items.view(np.uint8).copy()).to(dev)
+        self.tail_items = torch.from_numpy(self.tail_items_np.view(np.uint8).copy()).to(dev)
         self.bounds = torch.from_numpy(self.bounds_np).to(dev)
         self.luts = header_luts(pack.r_max, device=dev)
         self._lut_ptrs = nat.ptr_array([t.data_ptr() for t in self.luts])
@@ -171,7 +176,9 @@ class QuadStream:
             raise RuntimeError("QuadStream.bind() must be called before launching")
         pk = self.pack
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        rc = nat.lib().pp_quad_stream(self.projs.data_ptr(), len(self.shapes), self.items.data_ptr(), self.n_items,
+        rc = nat.lib().pp_quad_stream(self.projs.data_ptr(), len(self.shapes),
+                                      self.items.data_ptr() if self.n_items else None, self.n_items,
+                                      self.tail_items.data_ptr() if self.n_tail else None, self.n_tail,
                                       self.bounds.data_ptr() if self.schedule == "bytes" else None, self.n_waves,
                                       self._lut_ptrs, self._scales,
                                       pk.plug_idx.data_ptr() if pk.plug_idx.numel() else None,
