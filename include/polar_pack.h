@@ -59,7 +59,8 @@ int pp_abi_sizes(int64_t* out, int n);
  *   out_m[i, n] = fp16( s_m * sum_k a[i, k] * W_m[k, n] ),   m = 0..3,
  * where W_m is decoded from codes[k*c_sk + n*c_sn] with the 7 LUTs
  * luts = {norm, cos1, sin1, cos2, sin2, cos3, sin3} (256 entries each,
- * lut_dtype PP_F16 or PP_F32, device memory):
+ * lut_dtype PP_F16 or PP_F32, device memory; `luts` itself is a host array of
+ * the 7 device pointers) and the host float[4] `scales`:
  *   w0 = r*c1, w1 = r*s1*c2, w2 = r*s1*s2*c3, w3 = r*s1*s2*s3.
  *
  * Replaces quad_bitpacked (quad_kernels.py:146-159) and
