@@ -162,7 +162,7 @@ def main():
     for x in xs:
         x.copy_(torch.randn(x.shape, generator=g, device=dev).to(torch.float16))
     st.bind(xs, outs)
-    log(f"[bench] plan: {st.n_items} items, {st.n_tail} tail items, {st.n_waves} waves")
+    log(f"[bench] plan: {st.n_segs} segments, {st.n_tail} tail items, {st.n_waves} waves")
 
     # sanity: the stream output equals the per-projection operator on a k_proj and a down_proj
     st()

@@ -47,7 +47,8 @@ const char* pp_last_error(void);
 const char* pp_version(void);
 
 /* sizeof of the ABI structs, for binding checks: out[0] = sizeof(pp_quad_proj),
- * out[1] = sizeof(pp_quad_item).  Returns the number of values written. */
+ * out[1] = sizeof(pp_quad_item), out[2] = sizeof(pp_quad_seg).  Returns the number of
+ * values written. */
 int pp_abi_sizes(int64_t* out, int n);
 
 /* ------------------------------------------------------------------------ */
@@ -104,20 +105,22 @@ int pp_quad_dequant(const uint32_t* codes, int64_t c_sk, int64_t c_sn,
                     float* const* out, int64_t N, int64_t K, void* stream);
 
 /*
- * Whole-stream batch-1 decode: one launch over many projections of one
- * .quadpack stream (the grouped whole-step launch).  All tables are device
- * memory prepared by the host once per stream (see polar_pack_amd/stream.py):
+ * Whole-stream decode for 1..8 tokens: one launch over many projections of one
+ * .quadpack stream (the grouped whole-step launch).  All tables are device memory
+ * prepared by the host once per stream (see polar_pack_amd/stream.py):
  *
- *   projs  : n_projs descriptors of pp_quad_proj (the first 256 are staged in LDS);
- *   items  : n_items work items of pp_quad_item (rows of one projection, plus
- *            their plug range in plug_idx);
- *   luts   : 7 float32 LUTs from the header (r_max, mu);
- *   scales : host float[4], the header RMS s_k.
+ *   projs      : n_projs descriptors of pp_quad_proj;
+ *   segs       : n_segs runs of full rows of one projection (pp_quad_seg);
+ *                wavefront w decodes segs [seg_bounds[w], seg_bounds[w+1]),
+ *                n_waves = pp_quad_stream_waves(M) (the host balances them by bytes);
+ *   luts       : 7 float32 LUTs from the header (r_max, mu);
+ *   scales     : host float[4], the header RMS s_k;
+ *   plug_idx / plug_vals : the stream's plug table (ascending positions, plug_n entries).
  *
  * Rows touching stream positions >= n_codes (FP16 tails) are listed apart, in
- * tail_items (one row each, flags PP_ITEM_TAIL), and decoded from tails[m] (fp16,
- * length tail_len[m], model m's positions n_codes .. n_codes+tail_len[m]-1) by a
- * second, small kernel.
+ * tail_items (one row each, flags PP_ITEM_TAIL, with their plug range), and decoded
+ * from tails[m] (fp16, length tail_len[m], model m's positions
+ * n_codes .. n_codes+tail_len[m]-1) by a second, small kernel.
  * Replaces the per-projection quad_bitpacked calls of a decode step and the
  * tail restore of unpack_quad (quaternion_packer.py:201-210).
  */
@@ -132,31 +135,39 @@ typedef struct pp_quad_proj {
   int32_t N, K;
 } pp_quad_proj;
 
+/* A run of full rows [row0, row1) of projection `proj`, decoded by one wavefront.
+ * plug_lo = first plug entry whose position is >= the run's first position. */
+typedef struct pp_quad_seg {
+  int32_t proj;
+  int32_t row0;
+  int32_t row1;
+  int32_t flags;           /* reserved, 0 */
+  int64_t plug_lo;
+} pp_quad_seg;
+
 enum pp_item_flags { PP_ITEM_TAIL = 1 };
 
-/* One wavefront task: full rows [row0, row0+nrows) of one projection. */
+/* One row that reaches the FP16 tails, with its plug range [plug_lo, plug_hi). */
 typedef struct pp_quad_item {
   int32_t proj;            /* index into projs */
-  int32_t row0;            /* first row */
-  int32_t nrows;           /* rows in this item, 1..pp_quad_stream_rows(M) */
-  int32_t flags;           /* PP_ITEM_*; a TAIL item is one row */
-  int64_t plug_lo;         /* plug entries [plug_lo, plug_hi) cover these rows */
+  int32_t row0;            /* the row */
+  int32_t nrows;           /* 1 */
+  int32_t flags;           /* PP_ITEM_TAIL */
+  int64_t plug_lo;
   int64_t plug_hi;
 } pp_quad_item;
 
-/* Rows per item the stream decode uses for M tokens (0 and an error for bad M). */
+/* Rows per wavefront task the stream decode uses for M tokens (0 and an error for bad M). */
 int pp_quad_stream_rows(int64_t M);
 
-/* Number of wavefronts pp_quad_stream launches for M tokens on the current device.
- * wave_bounds (optional) gives wave w the items [wave_bounds[w], wave_bounds[w+1]);
- * the host balances them by bytes.  Without it, items are split evenly by count. */
+/* Number of wavefronts pp_quad_stream launches for M tokens on the current device. */
 int64_t pp_quad_stream_waves(int64_t M);
 
-int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs, const pp_quad_item* items, int64_t n_items,
+int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs,
+                   const pp_quad_seg* segs, int64_t n_segs, const int64_t* seg_bounds, int64_t n_waves,
                    const pp_quad_item* tail_items, int64_t n_tail,
-                   const int64_t* wave_bounds, int64_t n_waves,
                    const float* const* luts, const float* scales,
-                   const uint32_t* plug_idx, const void* plug_vals,
+                   const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n,
                    int64_t n_codes, const void* const* tails, const int64_t* tail_len,
                    int64_t M, void* stream);
 

@@ -33,6 +33,12 @@ class QuadItem(C.Structure):
                 ("plug_lo", i64), ("plug_hi", i64)]
 
 
+class QuadSeg(C.Structure):
+    """``pp_quad_seg`` (include/polar_pack.h)."""
+    _fields_ = [("proj", C.c_int32), ("row0", C.c_int32), ("row1", C.c_int32), ("flags", C.c_int32),
+                ("plug_lo", i64)]
+
+
 EXPORTS = {
     "pp_last_error": (C.c_char_p, []),
     "pp_version": (C.c_char_p, []),
@@ -43,7 +49,7 @@ EXPORTS = {
     "pp_quad_dequant": (i32, [vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
     "pp_quad_stream_rows": (i32, [i64]),
     "pp_quad_stream_waves": (i64, [i64]),
-    "pp_quad_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, vp, vp, vp, i64, vp, vp, i64, vp]),
+    "pp_quad_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, vp, vp, vp, i64, i64, vp, vp, i64, vp]),
     "pp_dual_gemm": (i32, [vp, i64, i64, vp, i32, i64, i64, vp, i64, i64, vp, i32, vp, vp, i32, i32,
                            vp, vp, i64, i64, vp, vp, i64, i64, i64, i64, i64, vp, i64, vp]),
     "pp_dual_gemm_workspace_size": (i64, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64]),

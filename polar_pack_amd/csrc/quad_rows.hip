@@ -1,0 +1,1069 @@
+// Fused quad-pack decode GEMV (batch <= 8) over codes laid out (N,K) row-major, the
+// container stream layout.  Serves the whole-stream launch (pp_quad_stream) and the
+// single-projection fast path of pp_quad_gemm.
+//
+// Word [nq 8 | q1 8 | q2 8 | q3 8] (quad_kernels.py:103-106, quaternion_packer.py:173-176)
+// decodes to  w0 = r c1, w1 = r s1 c2, w2 = r s1 s2 c3, w3 = r s1 s2 s3
+// (quad_kernels.py:108-121, quaternion_packer.py:178-185); the per-model RMS s_m is
+// applied to the float32 sum at the end (quad_kernels.py:131-134).
+//
+// Structure (one workgroup per CU, persistent):
+//  * LDS tables.  gfx950's LDS serves 256 B/clk; a b64 read runs at that rate only when
+//    each 32-lane half covers all 64 banks, a b32 read when the lanes' replicas differ.
+//    When the t1 and t2 tables are equal (they always are for the reference's packers:
+//    both are cos/sin(pi i/255), quad_kernels.py:41-44), the 160 KiB layout holds
+//    32 replicas of every entry: (cos,sin)(pi i/255) and (cos,sin)(2 pi i/255) as
+//    256-byte rows, the norm as 128-byte rows.  Lane l reads replica l % 32, so every
+//    lookup is conflict-free whatever the codes are.  Otherwise a 128 KiB layout with
+//    16 replicas of four tables is used.
+//  * Work.  Each wavefront owns a list of segments: runs of full rows of one
+//    projection.  It walks a segment in tasks of RG rows and chunks of NSEG x 256
+//    columns, software-pipelined: the codes and activations of the next chunk (also
+//    across task boundaries) are in flight while the current one is decoded.  Loads are
+//    bounds-checked buffer loads, so rows past the segment, columns past K and absent
+//    plug entries read zero without branches.
+//  * Plug table.  Entries are consumed in order: a task's entries are the next ones in
+//    the sorted list whose position falls before the task's end.  Their positions are
+//    loaded one task ahead; the plugged code, its fp16 values and x at its column are
+//    loaded with the task's first chunk, and each entry is applied as the exact
+//    correction x*(plug - decoded) before the reduction (quaternion_packer.py:187-193
+//    replaces the decoded tuple by the plug tuple; the sum is the same).
+//  * Reduction.  The RG*4*MT partial sums of a lane are reduced across the wavefront by
+//    a transposing butterfly (permlane32/16 swaps, then DPP): each step halves the
+//    number of values a lane holds, so 16 sums cost ~35 instructions instead of 96
+//    shuffles; lane groups end up holding distinct (row, model, token) sums and write them.
+//  * Tails.  Rows that reach FP16 tail positions run in quad_tail_kernel, one row per
+//    wavefront (quaternion_packer.py:201-210).
+#include "quad_rows.h"
+
+#include <algorithm>
+
+namespace pp {
+
+constexpr int QSEG = 256;                 // columns per wave per row per segment (64 lanes x 4)
+constexpr uint32_t QLDS_BYTES = 0x28000;  // 160 KiB: all of a gfx950 CU's LDS
+constexpr int NT_AUX = 2;                 // non-temporal cache policy for streamed codes
+constexpr uint32_t OOB = 0x80000000u;     // buffer offset past any num_records: reads 0
+
+// Buffer resource (V#) in scalar registers: base, stride 0, num_records bytes.
+// Offsets at or past num_records read 0 and drop writes.
+typedef int rsrc_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  rsrc_t r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu));
+  r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+  r.w = 0x00020000;
+  return r;
+}
+
+// The decode loop issues its memory operations itself and counts them: the compiler
+// would otherwise wait for every outstanding load at each plug-table branch, which
+// drains the prefetched chunk.  Each result is tied (tie()) after the s_waitcnt that
+// covers it, so nothing reads or moves the register before the data has arrived.
+__device__ __forceinline__ void vload128(u32x4& d, uint32_t off, rsrc_t r) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen nt" : "=v"(d) : "v"(off), "s"(r) : "memory");
+}
+__device__ __forceinline__ void vload64(u32x2& d, uint32_t off, rsrc_t r) {
+  asm volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen" : "=v"(d) : "v"(off), "s"(r) : "memory");
+}
+__device__ __forceinline__ void vload32(uint32_t& d, uint32_t off, rsrc_t r) {
+  asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(d) : "v"(off), "s"(r) : "memory");
+}
+__device__ __forceinline__ void vload16(uint32_t& d, uint32_t off, rsrc_t r) {
+  asm volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=v"(d) : "v"(off), "s"(r) : "memory");
+}
+__device__ __forceinline__ void vstore16(uint32_t v, uint32_t off, rsrc_t r) {
+  asm volatile("buffer_store_short %0, %1, %2, 0 offen" : : "v"(v), "v"(off), "s"(r) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+template <class T>
+__device__ __forceinline__ void tie(T& v) {
+  asm volatile("" : "+v"(v) : : "memory");
+}
+__device__ __forceinline__ float h2f(uint32_t bits) { return (float)__builtin_bit_cast(f16, (unsigned short)bits); }
+
+// ------------------------------------------------------------------ LDS tables
+struct LaneOff {
+  uint32_t r, c1, c2, c3;
+};
+
+// LDS byte address of the table row of code byte B (3 = nq, 2 = q1, 1 = q2, 0 = q3):
+// byte 1 of the address is the code byte, bytes 0 and 2 come from the lane constant.
+template <int B>
+__device__ __forceinline__ uint32_t perm_addr(uint32_t cw, uint32_t lane_off) {
+  return __builtin_amdgcn_perm(cw, lane_off, 0x0C020000u | ((4u + B) << 8));
+}
+
+// q1 and q2 share one table.  [0, 64K): (cos,sin)(pi i/255) rows of 32 x 8 B;
+// [64K, 128K): (cos,sin)(2 pi i/255); [128K, 160K): norm rows of 32 x 4 B.
+struct LayShared {
+  static __device__ __forceinline__ LaneOff lane(int l) {
+    LaneOff o;
+    o.r = 0x20000u | (4u * (l & 31));
+    o.c1 = o.c2 = 8u * (l & 31);
+    o.c3 = 0x10000u | (8u * (l & 31));
+    return o;
+  }
+  static __device__ __forceinline__ uint32_t addr_r(uint32_t cw, const LaneOff& o) {
+    return ((cw >> 17) & 0x7F80u) | o.r;
+  }
+  static __device__ __forceinline__ void build(char* lds, int e, int grp, int ngrp, const float (&v)[7]) {
+    for (int j = grp; j < 32; j += ngrp) {
+      *reinterpret_cast<float*>(lds + 0x20000 + e * 128 + 4 * j) = v[0];
+      *reinterpret_cast<float2*>(lds + e * 256 + 8 * j) = make_float2(v[1], v[2]);
+      *reinterpret_cast<float2*>(lds + 0x10000 + e * 256 + 8 * j) = make_float2(v[5], v[6]);
+    }
+  }
+};
+
+// Four tables.  [0, 64K): rows [norm x 32 (4 B) | (cos3,sin3) x 16 (8 B)];
+// [64K, 128K): rows [(cos1,sin1) x 16 | (cos2,sin2) x 16].
+struct LaySplit {
+  static __device__ __forceinline__ LaneOff lane(int l) {
+    LaneOff o;
+    o.r = 4u * (l & 31);
+    o.c3 = 128u + 8u * (l & 15);
+    o.c1 = 0x10000u | (8u * (l & 15));
+    o.c2 = 0x10000u | (128u + 8u * (l & 15));
+    return o;
+  }
+  static __device__ __forceinline__ uint32_t addr_r(uint32_t cw, const LaneOff& o) { return perm_addr<3>(cw, o.r); }
+  static __device__ __forceinline__ void build(char* lds, int e, int grp, int ngrp, const float (&v)[7]) {
+    float* row0 = reinterpret_cast<float*>(lds + e * 256);
+    float* row1 = reinterpret_cast<float*>(lds + 0x10000 + e * 256);
+    for (int j = grp; j < 32; j += ngrp) row0[j] = v[0];
+    for (int j = grp; j < 16; j += ngrp) {
+      row0[32 + 2 * j] = v[5];
+      row0[33 + 2 * j] = v[6];
+      row1[2 * j] = v[1];
+      row1[2 * j + 1] = v[2];
+      row1[32 + 2 * j] = v[3];
+      row1[33 + 2 * j] = v[4];
+    }
+  }
+};
+
+template <class L>
+__device__ __forceinline__ void lookup(const char* lds, uint32_t cw, const LaneOff& o, float& r, float2& a, float2& b,
+                                       float2& c) {
+  r = *reinterpret_cast<const float*>(lds + L::addr_r(cw, o));
+  a = *reinterpret_cast<const float2*>(lds + perm_addr<2>(cw, o.c1));
+  b = *reinterpret_cast<const float2*>(lds + perm_addr<1>(cw, o.c2));
+  c = *reinterpret_cast<const float2*>(lds + perm_addr<0>(cw, o.c3));
+}
+
+// ------------------------------------------------------------------ configuration
+// Batch 1 (the decode step): 8 rows per task and 8 waves per CU measured fastest on
+// the 3B-shaped stream (vs 4 rows / 16 waves: fewer per-task reductions and stores, and
+// the lookups of 8 independent rows fill the LDS latency); 2 chunks in flight per wave.
+#ifndef PP_ROWS1_RG
+#define PP_ROWS1_RG 8
+#endif
+#ifndef PP_ROWS1_NSEG
+#define PP_ROWS1_NSEG 1
+#endif
+#ifndef PP_ROWS1_NT
+#define PP_ROWS1_NT 512
+#endif
+#ifndef PP_ROWS1_PD
+#define PP_ROWS1_PD 1
+#endif
+// RG rows per task, NSEG x 256 columns per chunk, NT threads per workgroup, PD chunks
+// prefetched ahead of the one being decoded.
+template <int MT> struct RowsCfg;
+template <> struct RowsCfg<1> {
+  static constexpr int RG = PP_ROWS1_RG, NSEG = PP_ROWS1_NSEG, NT = PP_ROWS1_NT, PD = PP_ROWS1_PD;
+};
+template <> struct RowsCfg<2> { static constexpr int RG = 2, NSEG = 2, NT = 1024, PD = 1; };
+template <> struct RowsCfg<4> { static constexpr int RG = 1, NSEG = 2, NT = 1024, PD = 1; };
+template <> struct RowsCfg<8> { static constexpr int RG = 1, NSEG = 2, NT = 512, PD = 1; };
+
+struct QuadRowsArgs {
+  // single-projection front end (segs == nullptr): wave w owns row tasks
+  // [w*n_tasks/n_waves, (w+1)*n_tasks/n_waves) of `proj`
+  pp_quad_proj proj;
+  int64_t o_sn;
+  int64_t n_tasks;
+  const int64_t* wave_plug;  // plug start of each wave's first row (n_waves + 1), or null
+  // stream front end
+  const pp_quad_proj* projs;
+  const pp_quad_seg* segs;
+  const int64_t* seg_bounds;  // wave w owns segs [seg_bounds[w], seg_bounds[w+1])
+  // common
+  QuadLuts luts;
+  float s[4];
+  const uint32_t* plug_idx;
+  const f16* plug_vals;  // (P, 4)
+  int64_t plug_n;
+  int M;
+};
+
+// Uniform state of the segment a wave is working on.
+struct SegCtx {
+  rsrc_t rc;          // codes of the segment's rows (row r at byte r*ldc*4)
+  rsrc_t rx;          // activations (token j, column k at byte (j*x_sm + k)*2)
+  int64_t pos0;       // stream position of the segment's first row
+  int ldc, K, nrows, x_sm;
+  int row0;           // projection row of the segment's first row
+  f16* out[4];        // outputs of the segment's first row
+  int64_t o_sm, o_sn;
+};
+
+template <int MT, int RG, int NSEG>
+struct Chunk {
+  u32x4 q[RG][NSEG];
+  u32x2 xr[MT][NSEG];   // fp16 x 4 per lane per segment, raw
+  static constexpr int LOADS = RG * NSEG + MT * NSEG;
+};
+
+template <int MT, int RG, int NSEG>
+__device__ __forceinline__ void chunk_tie(Chunk<MT, RG, NSEG>& c) {
+#pragma unroll
+  for (int r = 0; r < RG; ++r)
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) tie(c.q[r][s]);
+#pragma unroll
+  for (int j = 0; j < MT; ++j)
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) tie(c.xr[j][s]);
+}
+
+// Issue every load of one chunk (Chunk::LOADS instructions): RG rows x NSEG segments of
+// codes at byte offset `so` of the segment (task rows and column kc folded in), plus
+// the activations.  Past the segment's last row or past K the loads read zero.
+template <int MT, int RG, int NSEG>
+__device__ __forceinline__ void chunk_issue(const SegCtx& S, uint32_t so, int kc, const uint32_t (&voff)[RG],
+                                            int lane, Chunk<MT, RG, NSEG>& c) {
+#pragma unroll
+  for (int r = 0; r < RG; ++r)
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) vload128(c.q[r][s], voff[r] + so + 1024u * s, S.rc);
+#pragma unroll
+  for (int s = 0; s < NSEG; ++s) {
+    const int k = kc + s * QSEG + 4 * lane;
+    if constexpr (MT == 1) {
+      vload64(c.xr[0][s], 2u * (uint32_t)k, S.rx);  // past K: out of the buffer
+    } else {
+      const bool valid = k < S.K;
+#pragma unroll
+      for (int j = 0; j < MT; ++j) vload64(c.xr[j][s], valid ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
+    }
+  }
+}
+
+// Table values of one code word.
+struct Tup {
+  float r;
+  float2 a, b, c;
+};
+
+// Decode a chunk and accumulate the normalised products.  At batch 1 x is folded
+// into the norm: rx = r*x, acc0 += rx*c1, t1 = rx*s1, acc1 += t1*c2, t2 = t1*s2,
+// acc2 += t2*c3, acc3 += t2*s3 (3 mul + 4 fma per tuple).
+// The lookups run one group of GT tuples ahead of the arithmetic (the scheduler would
+// otherwise wait for each tuple's four reads before issuing the next tuple's), with
+// at most 2*4*GT LDS reads in flight (the LDS counter holds 15).
+template <int MT, int RG, int NSEG, class L>
+__device__ __forceinline__ void chunk_compute(const char* lds, const LaneOff& lo, const Chunk<MT, RG, NSEG>& c,
+                                              float (&acc)[RG][4][MT]) {
+#ifndef PP_LOOKUP_GROUP
+#define PP_LOOKUP_GROUP 2
+#endif
+  constexpr int GT = PP_LOOKUP_GROUP;       // tuples per group
+  constexpr int NT = RG * NSEG * 4;         // tuples per lane in the chunk
+  constexpr int NG = NT / GT;
+  static_assert(NT % GT == 0, "the lookup group must divide the tuples of a chunk");
+  float xv[MT][NSEG][4];
+#pragma unroll
+  for (int s = 0; s < NSEG; ++s)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      const f16x4 xh = __builtin_bit_cast(f16x4, c.xr[j][s]);
+      xv[j][s][0] = (float)xh.x;
+      xv[j][s][1] = (float)xh.y;
+      xv[j][s][2] = (float)xh.z;
+      xv[j][s][3] = (float)xh.w;
+    }
+  // tuple t: row r = t / (4*NSEG), segment s = (t / 4) % NSEG, element e = t % 4
+  auto word = [&](int t) -> uint32_t {
+    const u32x4 q = c.q[t / (4 * NSEG)][(t / 4) % NSEG];
+    const int e = t % 4;
+    return e == 0 ? q.x : e == 1 ? q.y : e == 2 ? q.z : q.w;
+  };
+  Tup buf[2][GT];
+#pragma unroll
+  for (int u = 0; u < GT; ++u) lookup<L>(lds, word(u), lo, buf[0][u].r, buf[0][u].a, buf[0][u].b, buf[0][u].c);
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (g + 1 < NG) {
+#pragma unroll
+      for (int u = 0; u < GT; ++u) {
+        Tup& T = buf[(g + 1) & 1][u];
+        lookup<L>(lds, word((g + 1) * GT + u), lo, T.r, T.a, T.b, T.c);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < GT; ++u) {
+      const int t = g * GT + u;
+      const int r = t / (4 * NSEG), s = (t / 4) % NSEG, e = t % 4;
+      const Tup& T = buf[g & 1][u];
+      if constexpr (MT == 1) {
+        const float rx = T.r * xv[0][s][e];
+        acc[r][0][0] = fmaf(rx, T.a.x, acc[r][0][0]);
+        const float t1 = rx * T.a.y;
+        acc[r][1][0] = fmaf(t1, T.b.x, acc[r][1][0]);
+        const float t2 = t1 * T.b.y;
+        acc[r][2][0] = fmaf(t2, T.c.x, acc[r][2][0]);
+        acc[r][3][0] = fmaf(t2, T.c.y, acc[r][3][0]);
+      } else {
+        const float rs = T.r * T.a.y;
+        const float rss = rs * T.b.y;
+        const float w[4] = {T.r * T.a.x, rs * T.b.x, rss * T.c.x, rss * T.c.y};
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int j = 0; j < MT; ++j) acc[r][m][j] = fmaf(w[m], xv[j][s][e], acc[r][m][j]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// ------------------------------------------------------------------ plug entries
+template <int MT>
+struct PlugSt {
+  uint32_t idx;     // stream position of entry pc + lane (loaded a task ahead)
+  int row;          // row in the task of this lane's entry, -1 when none
+  uint32_t cw;      // plugged code word
+  u32x2 pv;         // plug values (normalised tuple, fp16 x 4)
+  uint32_t xk[MT];  // x at the entry's column (fp16 bits)
+  bool dense;       // the task has >= 64 entries: the rest are applied when it ends
+  static constexpr int LOADS = 3 + MT;   // cw, pv, xk[MT], next idx
+};
+
+__device__ __forceinline__ rsrc_t plug_idx_rsrc(const QuadRowsArgs& A, int64_t pc) {
+  const int64_t left = A.plug_n - pc;
+  const uint32_t bytes = left <= 0 ? 0u : (uint32_t)std::min<int64_t>(left * 4, 0x7FFFFFF0);
+  return make_rsrc(A.plug_idx + (left > 0 ? pc : 0), bytes);
+}
+__device__ __forceinline__ rsrc_t plug_val_rsrc(const QuadRowsArgs& A, int64_t pc) {
+  const int64_t left = A.plug_n - pc;
+  const uint32_t bytes = left <= 0 ? 0u : (uint32_t)std::min<int64_t>(left * 8, 0x7FFFFFF0);
+  return make_rsrc(A.plug_vals + 4 * (left > 0 ? pc : 0), bytes);
+}
+
+// Row (or -1) and column of stream position `pos` inside the task starting at tpos0.
+template <int RG>
+__device__ __forceinline__ int plug_locate(int64_t pos, int64_t tpos0, int ldc, int K, int nr, int& k) {
+  const int64_t off = pos - tpos0;
+  int row = 0;
+#pragma unroll
+  for (int r = 1; r < RG; ++r)
+    if (off >= (int64_t)r * ldc) row = r;
+  k = (int)(off - (int64_t)row * ldc);
+  return (off >= 0 && row < nr && k < K) ? row : -1;
+}
+
+// Start of task ti (P.idx has arrived): find its entries among the 64 loaded, issue
+// their dependent loads and the next task's positions (PlugSt::LOADS instructions,
+// all lanes, out of range where there is nothing to load), advance the cursor pc.
+template <int MT, int RG>
+__device__ __forceinline__ void plug_begin(const QuadRowsArgs& A, const SegCtx& S, int ti, int lane, int64_t& pc,
+                                           PlugSt<MT>& P) {
+  const int64_t tpos0 = S.pos0 + (int64_t)ti * RG * S.ldc;
+  const int nr = min(RG, S.nrows - ti * RG);
+  const int64_t tend = tpos0 + (int64_t)nr * S.ldc;
+  const bool in = (pc + lane < A.plug_n) && ((int64_t)P.idx < tend);
+  const int cnt = __popcll(__ballot(in));
+  int k = 0;
+  const int row = in ? plug_locate<RG>((int64_t)P.idx, tpos0, S.ldc, S.K, nr, k) : -1;
+  P.row = row;
+  const bool v = row >= 0;
+  vload32(P.cw, v ? 4u * (uint32_t)((ti * RG + row) * S.ldc + k) : OOB, S.rc);
+  vload64(P.pv, in ? 8u * lane : OOB, plug_val_rsrc(A, pc));
+#pragma unroll
+  for (int j = 0; j < MT; ++j) vload16(P.xk[j], (v && j < A.M) ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
+  P.dense = cnt == 64;
+  pc += cnt;
+  vload32(P.idx, 4u * lane, plug_idx_rsrc(A, pc));
+}
+
+template <int MT>
+__device__ __forceinline__ void plug_tie(PlugSt<MT>& P) {
+  tie(P.cw);
+  tie(P.pv);
+#pragma unroll
+  for (int j = 0; j < MT; ++j) tie(P.xk[j]);
+}
+
+template <int MT, int RG, class L>
+__device__ __forceinline__ void plug_correct(const char* lds, const LaneOff& lo, int row, uint32_t cw, f16x4 pv,
+                                             const float (&xk)[MT], float (&acc)[RG][4][MT]) {
+  // the decoded tuple is rebuilt from the same tables as the chunk, so the correction
+  // cancels its contribution exactly up to float32 rounding
+  float r;
+  float2 a, b, c;
+  lookup<L>(lds, cw, lo, r, a, b, c);
+  const float rs = r * a.y, rss = rs * b.y;
+  const float dlt[4] = {(float)pv.x - r * a.x, (float)pv.y - rs * b.x, (float)pv.z - rss * c.x,
+                        (float)pv.w - rss * c.y};
+  // every row is updated with a 0/1 weight: indexing acc by a per-lane row would put
+  // the accumulators in scratch memory
+#pragma unroll
+  for (int q = 0; q < RG; ++q) {
+    const float on = q == row ? 1.f : 0.f;
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) acc[q][m][j] = fmaf(on * xk[j], dlt[m], acc[q][m][j]);
+  }
+}
+
+// End of task ti (its dependent loads have arrived): apply its entries; for a dense
+// task, the ones past the first 64 too (compiler-managed loads, waited on at once), then
+// reload the next task's positions.  Returns the number of counted loads it issued.
+template <int MT, int RG, class L>
+__device__ __forceinline__ int plug_end(const char* lds, const LaneOff& lo, const QuadRowsArgs& A, const SegCtx& S,
+                                        int ti, int lane, int64_t& pc, PlugSt<MT>& P, float (&acc)[RG][4][MT]) {
+  if (P.row >= 0) {
+    float xk[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) xk[j] = h2f(P.xk[j]);
+    plug_correct<MT, RG, L>(lds, lo, P.row, P.cw, __builtin_bit_cast(f16x4, P.pv), xk, acc);
+  }
+  if (!P.dense) return 0;
+  const int64_t tpos0 = S.pos0 + (int64_t)ti * RG * S.ldc;
+  const int nr = min(RG, S.nrows - ti * RG);
+  const int64_t tend = tpos0 + (int64_t)nr * S.ldc;
+  vm_wait<0>();            // the next task's positions were loaded at the old cursor
+  tie(P.idx);
+  const uint32_t* codes = reinterpret_cast<const uint32_t*>(
+      (static_cast<uint64_t>(static_cast<uint32_t>(S.rc.y)) << 32) | static_cast<uint32_t>(S.rc.x));
+  const f16* x = reinterpret_cast<const f16*>(
+      (static_cast<uint64_t>(static_cast<uint32_t>(S.rx.y)) << 32) | static_cast<uint32_t>(S.rx.x));
+  for (;;) {
+    const int64_t q = pc + lane;
+    const bool has = q < A.plug_n;
+    const int64_t pos = has ? (int64_t)A.plug_idx[q] : tend;
+    const bool in = pos < tend;
+    const int cnt = __popcll(__ballot(in));
+    int k = 0;
+    const int row = in ? plug_locate<RG>(pos, tpos0, S.ldc, S.K, nr, k) : -1;
+    if (row >= 0) {
+      float xk[MT];
+#pragma unroll
+      for (int j = 0; j < MT; ++j) xk[j] = j < A.M ? (float)x[(int64_t)j * S.x_sm + k] : 0.f;
+      const uint32_t cw = codes[(int64_t)(ti * RG + row) * S.ldc + k];
+      const f16x4 pv = *reinterpret_cast<const f16x4*>(A.plug_vals + 4 * q);
+      plug_correct<MT, RG, L>(lds, lo, row, cw, pv, xk, acc);
+    }
+    pc += cnt;
+    if (cnt < 64) break;
+  }
+  vload32(P.idx, 4u * lane, plug_idx_rsrc(A, pc));
+  return 1;
+}
+
+// ------------------------------------------------------------------ reduction
+template <int P>
+__device__ __forceinline__ float dpp_partner(float v) {
+  // partner across lane bit P: 3 -> row_ror:8, 2 -> row_half_mirror, 1 -> quad_perm
+  // [2,3,0,1], 0 -> quad_perm [1,0,3,2]
+  constexpr int ctrl = P == 3 ? 0x128 : P == 2 ? 0x141 : P == 1 ? 0x4E : 0xB1;
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false));
+}
+
+// One halving step over lane bit P on C values: lanes with the bit clear keep
+// v[i] + partner's v[i], lanes with it set keep v[i + C/2] + partner's v[i + C/2].
+template <int P, int C>
+__device__ __forceinline__ void halve(float* v, int lane) {
+  constexpr int H = C / 2;
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    if constexpr (P == 5) {
+      // swap(a, b): a' = (a_lo, b_lo), b' = (a_hi, b_hi) over the wave halves
+      const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + H]), false, false);
+      v[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    } else if constexpr (P == 4) {
+      // swap(a, b): a' = rows (a0, b0, a2, b2), b' = rows (a1, b1, a3, b3)
+      const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + H]), false, false);
+      v[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    } else {
+      const bool hi = (lane >> P) & 1;
+      const float send = hi ? v[i] : v[i + H];
+      const float keep = hi ? v[i + H] : v[i];
+      v[i] = keep + dpp_partner<P>(send);
+    }
+  }
+}
+
+// Sum v[0] over lane bits [0, NB).
+template <int NB>
+__device__ __forceinline__ float sum_low_bits(float v) {
+  if constexpr (NB >= 3) v += dpp_partner<2>(v);
+  if constexpr (NB >= 2) v += dpp_partner<1>(v);
+  if constexpr (NB >= 1) v += dpp_partner<0>(v);
+  return v;
+}
+
+// Reduce NV = 2^LNV values per lane over the wave; afterwards the lanes whose low
+// (6 - LNV) bits are zero hold value (lane >> (6 - LNV)) in v[0].
+template <int LNV>
+__device__ __forceinline__ float wave_transpose_reduce(float* v, int lane) {
+  static_assert(LNV >= 3 && LNV <= 6, "the reduction assumes 8..64 values per lane");
+  if constexpr (LNV >= 1) halve<5, (1 << LNV)>(v, lane);
+  if constexpr (LNV >= 2) halve<4, (1 << (LNV - 1))>(v, lane);
+  if constexpr (LNV >= 3) halve<3, (1 << (LNV - 2))>(v, lane);
+  if constexpr (LNV >= 4) halve<2, (1 << (LNV - 3))>(v, lane);
+  if constexpr (LNV >= 5) halve<1, (1 << (LNV - 4))>(v, lane);
+  if constexpr (LNV >= 6) halve<0, (1 << (LNV - 5))>(v, lane);
+  return sum_low_bits<6 - LNV>(v[0]);
+}
+
+template <int N>
+struct Log2 {
+  static constexpr int v = N <= 1 ? 0 : 1 + Log2<N / 2>::v;
+};
+template <>
+struct Log2<1> {
+  static constexpr int v = 0;
+};
+
+template <int MT, int RG>
+__device__ __forceinline__ void task_write(const QuadRowsArgs& A, const SegCtx& S, int ti, int lane,
+                                           float (&acc)[RG][4][MT]) {
+  constexpr int NV = RG * 4 * MT;
+  constexpr int LNV = Log2<NV>::v;
+  static_assert((1 << LNV) == NV, "RG*4*MT must be a power of two");
+  float v[NV];
+#pragma unroll
+  for (int r = 0; r < RG; ++r)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) v[(r * 4 + m) * MT + j] = acc[r][m][j];
+  const float y = wave_transpose_reduce<LNV>(v, lane);
+  const int idx = lane >> (6 - LNV);
+  const int r = idx / (4 * MT), m = (idx / MT) & 3, j = idx % MT;
+  const int nr = min(RG, S.nrows - ti * RG);
+  const bool wr = (lane & ((1 << (6 - LNV)) - 1)) == 0 && r < nr && j < A.M;
+  const uint32_t off = 2u * (uint32_t)((int64_t)j * S.o_sm + (int64_t)(ti * RG + r) * S.o_sn);
+  // one store per model (4 counted stores), each lane writing only its own model:
+  // selecting the pointer per lane would index the pointer array in scratch memory
+  const uint32_t obytes = 2u * (uint32_t)((int64_t)(A.M - 1) * S.o_sm + (int64_t)(S.nrows - 1) * S.o_sn + 1);
+#pragma unroll
+  for (int mm = 0; mm < 4; ++mm) {
+    const f16 h = (f16)(y * A.s[mm]);
+    vstore16((uint32_t)__builtin_bit_cast(unsigned short, h), (wr && m == mm) ? off : OOB,
+             make_rsrc(S.out[mm], obytes));
+  }
+}
+
+template <int MT, int RG>
+__device__ __forceinline__ void zero_acc(float (&acc)[RG][4][MT]) {
+#pragma unroll
+  for (int r = 0; r < RG; ++r)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) acc[r][m][j] = 0.f;
+}
+
+// ------------------------------------------------------------------ segment walk
+// Cursor over the steps (task ti, chunk ck) of a segment.
+struct Cursor {
+  int ti, ck;
+};
+
+template <int MT, int RG, int NSEG, int PD, class L>
+struct SegRunner {
+  static constexpr int CHUNK = NSEG * QSEG;
+  static constexpr int NQ = Chunk<MT, RG, NSEG>::LOADS;   // loads per prefetched chunk
+  static constexpr int NP = PlugSt<MT>::LOADS;            // loads at a task's first chunk
+  static constexpr int NS = 4;                            // stores at a task's last chunk
+  const char* lds;
+  LaneOff lo;
+  const QuadRowsArgs& A;
+  const SegCtx& S;
+  int lane, nck, ntask;
+  uint32_t voff[RG];
+  float acc[RG][4][MT];
+  PlugSt<MT> P;
+  int64_t pc;
+  Cursor lc;               // next chunk to load
+  bool pf, pl;             // the previous step issued plug loads / stores after its prefetch
+
+  __device__ __forceinline__ SegRunner(const char* l, const QuadRowsArgs& a, const SegCtx& s, int64_t plug_lo)
+      : lds(l), A(a), S(s), pc(plug_lo), pf(false), pl(false) {
+    lane = threadIdx.x & 63;
+    lo = L::lane(lane);
+    nck = (S.K + CHUNK - 1) / CHUNK;
+    ntask = (S.nrows + RG - 1) / RG;
+    lc = {0, 0};
+#pragma unroll
+    for (int r = 0; r < RG; ++r) voff[r] = 4u * (uint32_t)(r * S.ldc) + 16u * lane;
+    zero_acc<MT, RG>(acc);
+  }
+
+  __device__ __forceinline__ void advance(Cursor& c) const {
+    if (++c.ck == nck) {
+      c.ck = 0;
+      ++c.ti;
+    }
+  }
+
+  // Issue the next chunk's loads (past the last chunk: reload the last one, so every
+  // step issues exactly NQ loads).
+  __device__ __forceinline__ void prefetch(Chunk<MT, RG, NSEG>& c) {
+    const Cursor ld = lc;
+    chunk_issue<MT, RG, NSEG>(S, 4u * (uint32_t)(ld.ti * RG * S.ldc + ld.ck * CHUNK), ld.ck * CHUNK, voff, lane, c);
+    Cursor nx = lc;
+    advance(nx);
+    if (nx.ti < ntask) lc = nx;
+  }
+
+  // Wait until the chunk issued PD steps ago has arrived.  The memory operations of a
+  // step, in issue order, are  NQ prefetch loads | NP plug loads (first chunk of a task)
+  // | NS stores (last chunk of a task); they complete in order, so "everything up to the
+  // chunk issued PD steps ago" means at most PD*NQ plus the previous step's plug loads
+  // and stores still outstanding (for PD = 2; for PD = 1 the previous step's plug loads
+  // and stores precede this step's prefetch and only NS may stay outstanding... which
+  // the formula below also covers, as they are counted only when they came after the
+  // chunk in question).
+  __device__ __forceinline__ void wait_chunk() {
+    if constexpr (PD == 1) {
+      // previous step: [NQ (this chunk)] [NP?] [NS?]   this step: [NQ]
+      if (pf && pl) vm_wait<NQ + NP + NS>();
+      else if (pf) vm_wait<NQ + NP>();
+      else if (pl) vm_wait<NQ + NS>();
+      else vm_wait<NQ>();
+    } else {
+      // step-1: [NQ] [NP?] [NS?]   this step: [NQ]; the chunk came before step-1's prefetch
+      if (pf && pl) vm_wait<2 * NQ + NP + NS>();
+      else if (pf) vm_wait<2 * NQ + NP>();
+      else if (pl) vm_wait<2 * NQ + NS>();
+      else vm_wait<2 * NQ>();
+    }
+  }
+
+  // Compute the step at `cur` from `comp` while `pref` receives a later chunk.
+  __device__ __forceinline__ bool step(Cursor& cur, Chunk<MT, RG, NSEG>& comp, Chunk<MT, RG, NSEG>& pref) {
+    prefetch(pref);
+    wait_chunk();
+    chunk_tie<MT, RG, NSEG>(comp);
+    const bool first = cur.ck == 0, last = cur.ck == nck - 1;
+    // plug positions of this task were loaded at the previous task's first chunk, i.e.
+    // before the prefetch of that step; with fewer than PD+1 chunks per task that load
+    // may still be outstanding
+    if (first) {
+      if (nck <= PD) vm_wait<0>();
+      tie(P.idx);
+      plug_begin<MT, RG>(A, S, cur.ti, lane, pc, P);
+    }
+    chunk_compute<MT, RG, NSEG, L>(lds, lo, comp, acc);
+    if (last) {
+      // the dependent plug loads were issued at this task's first chunk: they are covered
+      // by the chunk wait only when that was at least PD+1 steps ago
+      if (nck <= PD + 1) vm_wait<0>();
+      plug_tie<MT>(P);
+      if (plug_end<MT, RG, L>(lds, lo, A, S, cur.ti, lane, pc, P, acc)) vm_wait<0>();
+      task_write<MT, RG>(A, S, cur.ti, lane, acc);
+      zero_acc<MT, RG>(acc);
+    }
+    pf = first;
+    pl = last;
+    advance(cur);
+    return cur.ti < ntask;
+  }
+
+  __device__ __forceinline__ void run() {
+    if (ntask <= 0 || S.K <= 0) return;
+    Chunk<MT, RG, NSEG> c0, c1, c2;
+    Cursor cur = {0, 0};
+    vload32(P.idx, 4u * lane, plug_idx_rsrc(A, pc));
+    if constexpr (PD == 1) {
+      prefetch(c0);
+      for (;;) {
+        if (!step(cur, c0, c1)) break;
+        if (!step(cur, c1, c0)) break;
+      }
+    } else {
+      prefetch(c0);
+      prefetch(c1);
+      for (;;) {
+        if (!step(cur, c0, c2)) break;
+        if (!step(cur, c1, c0)) break;
+        if (!step(cur, c2, c1)) break;
+      }
+    }
+    // drain: the last prefetches (reloads), the next positions and the stores are still
+    // in flight; their registers must stay allocated until they land
+    vm_wait<0>();
+    chunk_tie<MT, RG, NSEG>(c0);
+    chunk_tie<MT, RG, NSEG>(c1);
+    if constexpr (PD == 2) chunk_tie<MT, RG, NSEG>(c2);
+    tie(P.idx);
+    plug_tie<MT>(P);
+  }
+};
+
+// Segment context of rows [row0, row1) of projection P.  Every field goes through
+// readfirstlane: the descriptors are read from memory the kernel also writes, so the
+// compiler cannot prove them uniform, and a buffer resource in vector registers would
+// turn each load into a loop over lanes.
+__device__ __forceinline__ void seg_ctx(const pp_quad_proj& P, int64_t o_sn, int row0, int row1, int M, SegCtx& S) {
+  const int ldc = uniform((int)P.ldc), K = uniform(P.K);
+  row0 = uniform(row0);
+  row1 = uniform(row1);
+  S.ldc = ldc;
+  S.K = K;
+  S.nrows = row1 - row0;
+  S.row0 = row0;
+  S.x_sm = uniform((int)P.x_sm);
+  S.pos0 = uniform64(P.pos0) + (int64_t)row0 * ldc;
+  const uint32_t cbytes = S.nrows > 0 ? 4u * (uint32_t)((S.nrows - 1) * ldc + K) : 0u;
+  S.rc = make_rsrc(uniform_ptr(P.codes) + (int64_t)row0 * ldc, cbytes);
+  S.rx = make_rsrc(uniform_ptr(P.x), 2u * (uint32_t)((M - 1) * S.x_sm + K));
+#pragma unroll
+  for (int m = 0; m < 4; ++m) S.out[m] = reinterpret_cast<f16*>(uniform_ptr(P.out[m])) + (int64_t)row0 * o_sn;
+  S.o_sm = uniform64(P.o_sm);
+  S.o_sn = o_sn;
+}
+
+template <int MT, class L>
+__device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A) {
+  constexpr int RG = RowsCfg<MT>::RG, NSEG = RowsCfg<MT>::NSEG;
+  constexpr int WAVES = RowsCfg<MT>::NT / 64;
+  const int64_t gw = (int64_t)blockIdx.x * WAVES + uniform(threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * WAVES;
+  if (A.segs == nullptr) {
+    const int64_t t0 = gw * A.n_tasks / nw, t1 = (gw + 1) * A.n_tasks / nw;
+    const int row0 = (int)std::min<int64_t>(t0 * RG, A.proj.N), row1 = (int)std::min<int64_t>(t1 * RG, A.proj.N);
+    if (row1 <= row0) return;
+    SegCtx S;
+    seg_ctx(A.proj, A.o_sn, row0, row1, A.M, S);
+    SegRunner<MT, RG, NSEG, RowsCfg<MT>::PD, L> R(lds, A, S, A.wave_plug ? uniform64(A.wave_plug[gw]) : 0);
+    R.run();
+    return;
+  }
+  const int64_t s0 = uniform64(A.seg_bounds[gw]), s1 = uniform64(A.seg_bounds[gw + 1]);
+  for (int64_t si = s0; si < s1; ++si) {
+    const pp_quad_seg g = A.segs[si];
+    SegCtx S;
+    seg_ctx(A.projs[uniform(g.proj)], 1, g.row0, g.row1, A.M, S);
+    SegRunner<MT, RG, NSEG, RowsCfg<MT>::PD, L> R(lds, A, S, uniform64(g.plug_lo));
+    R.run();
+  }
+}
+
+template <int MT>
+__global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_rows_kernel(const QuadRowsArgs A) {
+  __shared__ __attribute__((aligned(16))) uint32_t T[QLDS_BYTES / 4];
+  char* lds = reinterpret_cast<char*>(T);
+  const int e = threadIdx.x & 255, grp = threadIdx.x >> 8, ngrp = blockDim.x >> 8;
+  float v[7];
+  if (A.luts.dtype == PP_F16) {
+#pragma unroll
+    for (int i = 0; i < 7; ++i) v[i] = (float)reinterpret_cast<const f16*>(A.luts.p[i])[e];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 7; ++i) v[i] = reinterpret_cast<const float*>(A.luts.p[i])[e];
+  }
+  const bool same = __float_as_uint(v[1]) == __float_as_uint(v[3]) && __float_as_uint(v[2]) == __float_as_uint(v[4]);
+  // workgroup-wide AND through the (not yet built) table memory: the tables fill all
+  // of LDS, so there is no room for a separate flag
+  if (threadIdx.x == 0) T[0] = 0u;
+  __syncthreads();
+  if (!same) T[0] = 1u;
+  __syncthreads();
+  const bool shared = T[0] == 0u;
+  __syncthreads();
+  if (shared) LayShared::build(lds, e, grp, ngrp, v);
+  else LaySplit::build(lds, e, grp, ngrp, v);
+  __syncthreads();
+  if (shared) rows_body<MT, LayShared>(lds, A);
+  else rows_body<MT, LaySplit>(lds, A);
+}
+
+// ------------------------------------------------------------------ tail rows
+struct QuadTailArgs {
+  const pp_quad_proj* projs;
+  const pp_quad_item* items;
+  int64_t n_items;
+  QuadLuts luts;
+  float s[4];
+  const uint32_t* plug_idx;
+  const f16* plug_vals;
+  int M;
+  int64_t n_codes;  // positions >= n_codes come from the tails
+  const f16* tails[4];
+  int64_t tail_len[4];
+};
+
+// A row that reaches FP16 tail positions, element by element:
+// y_m = s_m * sum_{pos < n} x * decoded_m  +  sum_{n <= pos} x * tail_m[pos - n].
+template <int MT>
+__global__ __launch_bounds__(256) void quad_tail_kernel(const QuadTailArgs A) {
+  __shared__ QuadLds<1, 1> T;
+  quad_build_lds(T, A.luts);
+  __syncthreads();
+  const int64_t ti = (int64_t)blockIdx.x * 4 + uniform(threadIdx.x >> 6);
+  if (ti >= A.n_items) return;
+  const int lane = threadIdx.x & 63;
+  const pp_quad_item it = A.items[ti];
+  const pp_quad_proj& P = A.projs[it.proj];
+  const int K = P.K;
+  const int64_t pos_row = P.pos0 + (int64_t)it.row0 * P.ldc;
+  const uint32_t* codes = P.codes + (int64_t)it.row0 * P.ldc;
+  const f16* x = reinterpret_cast<const f16*>(P.x);
+  float accc[4][MT], acct[4][MT];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) accc[m][j] = acct[m][j] = 0.f;
+  for (int k = lane; k < K; k += 64) {
+    const int64_t pos = pos_row + k;
+    float xk[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) xk[j] = j < A.M ? (float)x[(int64_t)j * P.x_sm + k] : 0.f;
+    if (pos < A.n_codes) {
+      float w[4];
+      quad_decode(T, codes[k], 0, 0, w[0], w[1], w[2], w[3]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int j = 0; j < MT; ++j) accc[m][j] = fmaf(w[m], xk[j], accc[m][j]);
+    } else {
+      const int64_t t = pos - A.n_codes;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (t < A.tail_len[m]) {
+          const float w = (float)A.tails[m][t];
+#pragma unroll
+          for (int j = 0; j < MT; ++j) acct[m][j] = fmaf(w, xk[j], acct[m][j]);
+        }
+      }
+    }
+  }
+  for (int64_t p0 = it.plug_lo; p0 < it.plug_hi; p0 += 64) {
+    const int64_t p = p0 + lane;
+    if (p >= it.plug_hi) continue;
+    const int64_t k = (int64_t)A.plug_idx[p] - pos_row;
+    if (k < 0 || k >= K || pos_row + k >= A.n_codes) continue;
+    float wd[4];
+    quad_decode(T, codes[k], 0, 0, wd[0], wd[1], wd[2], wd[3]);
+    const f16x4 pv = *reinterpret_cast<const f16x4*>(A.plug_vals + 4 * p);
+    const float dlt[4] = {(float)pv.x - wd[0], (float)pv.y - wd[1], (float)pv.z - wd[2], (float)pv.w - wd[3]};
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      if (j >= A.M) break;
+      const float xk = (float)x[(int64_t)j * P.x_sm + k];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) accc[m][j] = fmaf(xk, dlt[m], accc[m][j]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    // a model whose stream ends before this row does not have the row: it reads 0
+    const bool has = pos_row < A.n_codes || pos_row - A.n_codes < A.tail_len[m];
+    f16* o = reinterpret_cast<f16*>(P.out[m]) + it.row0;
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      const float v = wave_sum(accc[m][j]) * A.s[m] + wave_sum(acct[m][j]);
+      if (lane == 0 && j < A.M) o[(int64_t)j * P.o_sm] = (f16)(has ? v : 0.f);
+    }
+  }
+}
+
+// Plug start of each wave's first row: first entry with idx >= pos0 + row(g)*ldc, where
+// wave g starts at task g*n_tasks/n_waves (rows_per_task rows each).
+__global__ void wave_plug_kernel(const uint32_t* plug_idx, int64_t plug_n, int64_t pos0, int64_t ldc,
+                                 int rows_per_task, int64_t n_tasks, int64_t n_waves, int N, int64_t* wave_plug) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g > n_waves) return;
+  const int64_t row = std::min<int64_t>(g * n_tasks / n_waves * rows_per_task, N);
+  const int64_t key = pos0 + row * ldc;
+  int64_t lo = 0, hi = plug_n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)plug_idx[mid] < key) lo = mid + 1;
+    else hi = mid;
+  }
+  wave_plug[g] = lo;
+}
+
+// ------------------------------------------------------------------ host side
+static int round_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+
+static int cfg_rg(int mt) {
+  switch (mt) {
+    case 1: return RowsCfg<1>::RG;
+    case 2: return RowsCfg<2>::RG;
+    case 4: return RowsCfg<4>::RG;
+    default: return RowsCfg<8>::RG;
+  }
+}
+static int cfg_waves(int mt) {
+  switch (mt) {
+    case 1: return RowsCfg<1>::NT / 64;
+    case 2: return RowsCfg<2>::NT / 64;
+    case 4: return RowsCfg<4>::NT / 64;
+    default: return RowsCfg<8>::NT / 64;
+  }
+}
+
+static int launch_rows(const QuadRowsArgs& A, int mt, hipStream_t st) {
+  const unsigned grid = (unsigned)device_cu_count();
+  switch (mt) {
+    case 1: hipLaunchKernelGGL(quad_rows_kernel<1>, dim3(grid), dim3(RowsCfg<1>::NT), 0, st, A); break;
+    case 2: hipLaunchKernelGGL(quad_rows_kernel<2>, dim3(grid), dim3(RowsCfg<2>::NT), 0, st, A); break;
+    case 4: hipLaunchKernelGGL(quad_rows_kernel<4>, dim3(grid), dim3(RowsCfg<4>::NT), 0, st, A); break;
+    default: hipLaunchKernelGGL(quad_rows_kernel<8>, dim3(grid), dim3(RowsCfg<8>::NT), 0, st, A); break;
+  }
+  PP_LAUNCH_CHECK();
+  return PP_OK;
+}
+
+static QuadLuts make_luts(const void* const* luts, int dtype) {
+  QuadLuts L;
+  for (int i = 0; i < 7; ++i) L.p[i] = luts[i];
+  L.dtype = dtype;
+  return L;
+}
+
+bool quad_rows_ok(const void* a, int64_t a_sm, int64_t a_sk, const uint32_t* codes, int64_t c_sk, int64_t c_sn,
+                  int64_t M, int64_t N, int64_t K) {
+  // buffer offsets are 32-bit: a projection's codes and activations must stay below 2 GiB
+  return c_sk == 1 && c_sn % 4 == 0 && c_sn >= K && K % 4 == 0 && K > 0 && aligned(codes, 16) && M >= 1 &&
+         M <= 8 && (a_sk == 1 || K == 1) && (M == 1 || (a_sm % 4 == 0 && a_sm >= K)) && aligned(a, 8) &&
+         N * c_sn < (1ll << 29) && (M - 1) * a_sm + K < (1ll << 30);
+}
+
+int64_t quad_rows_workspace(int64_t M, int64_t N, int64_t plug_n) {
+  if (plug_n <= 0) return 0;
+  const int mt = round_mt(M);
+  const int64_t waves = (int64_t)device_cu_count() * cfg_waves(mt);
+  return ((waves + 1) * 8 + 255) / 256 * 256;
+}
+
+int quad_rows_single(const void* a, int64_t a_sm, const uint32_t* codes, int64_t ldc, const void* const* luts,
+                     int lut_dtype, const float* scales, const uint32_t* plug_idx, const void* plug_vals,
+                     int64_t plug_n, int64_t elem_base, void* const* out, int64_t o_sm, int64_t o_sn, int64_t M,
+                     int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, hipStream_t st) {
+  const int mt = round_mt(M);
+  const int rg = cfg_rg(mt);
+  const int64_t waves = (int64_t)device_cu_count() * cfg_waves(mt);
+  const int64_t need = quad_rows_workspace(M, N, plug_n);
+  PP_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr), "workspace too small: need %lld bytes",
+             (long long)need);
+  QuadRowsArgs A = {};
+  A.proj.codes = codes;
+  A.proj.ldc = ldc;
+  A.proj.pos0 = elem_base;
+  A.proj.x = a;
+  A.proj.x_sm = M > 1 ? a_sm : K;
+  for (int m = 0; m < 4; ++m) A.proj.out[m] = out[m];
+  A.proj.o_sm = o_sm;
+  A.proj.N = (int32_t)N;
+  A.proj.K = (int32_t)K;
+  A.o_sn = o_sn;
+  A.n_tasks = (N + rg - 1) / rg;
+  A.luts = make_luts(luts, lut_dtype);
+  for (int m = 0; m < 4; ++m) A.s[m] = scales[m];
+  A.plug_idx = plug_idx;
+  A.plug_vals = reinterpret_cast<const f16*>(plug_vals);
+  A.plug_n = plug_n;
+  A.M = (int)M;
+  if (plug_n > 0) {
+    int64_t* wp = reinterpret_cast<int64_t*>(workspace);
+    hipLaunchKernelGGL(wave_plug_kernel, dim3((unsigned)((waves + 1 + 255) / 256)), dim3(256), 0, st, plug_idx,
+                       plug_n, elem_base, ldc, rg, A.n_tasks, waves, (int)N, wp);
+    PP_LAUNCH_CHECK();
+    A.wave_plug = wp;
+  }
+  return launch_rows(A, mt, st);
+}
+
+}  // namespace pp
+
+using namespace pp;
+
+extern "C" int pp_quad_stream_rows(int64_t M) {
+  if (M < 1 || M > 8) {
+    set_error("the stream decode takes 1..8 tokens, got %lld", (long long)M);
+    return 0;
+  }
+  return cfg_rg(round_mt(M));
+}
+
+extern "C" int64_t pp_quad_stream_waves(int64_t M) {
+  if (M < 1 || M > 8) return 0;
+  return (int64_t)device_cu_count() * cfg_waves(round_mt(M));
+}
+
+extern "C" int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs, const pp_quad_seg* segs, int64_t n_segs,
+                              const int64_t* seg_bounds, int64_t n_waves, const pp_quad_item* tail_items,
+                              int64_t n_tail, const float* const* luts, const float* scales,
+                              const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n, int64_t n_codes,
+                              const void* const* tails, const int64_t* tail_len, int64_t M, void* stream) {
+  PP_REQUIRE(projs != nullptr && n_projs >= 1, "no projections");
+  PP_REQUIRE(n_segs >= 0 && (n_segs == 0 || (segs != nullptr && seg_bounds != nullptr)), "segs / seg_bounds is null");
+  PP_REQUIRE(n_tail == 0 || tail_items != nullptr, "tail_items is null");
+  PP_REQUIRE(luts != nullptr, "luts is null");
+  for (int i = 0; i < 7; ++i) PP_REQUIRE(luts[i] != nullptr, "lut %d is null", i);
+  PP_REQUIRE(scales != nullptr, "scales is null");
+  PP_REQUIRE(plug_n >= 0 && (plug_n == 0 || (plug_idx != nullptr && plug_vals != nullptr)), "plug arrays are null");
+  PP_REQUIRE(M >= 1 && M <= 8, "the stream decode takes 1..8 tokens, got %lld", (long long)M);
+  PP_REQUIRE(n_segs == 0 || n_waves == pp_quad_stream_waves(M),
+             "seg_bounds were built for %lld waves, this device launches %lld", (long long)n_waves,
+             (long long)pp_quad_stream_waves(M));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int mt = round_mt(M);
+  const QuadLuts L = make_luts(reinterpret_cast<const void* const*>(luts), PP_F32);
+  if (n_segs > 0) {
+    QuadRowsArgs A = {};
+    A.projs = projs;
+    A.segs = segs;
+    A.seg_bounds = seg_bounds;
+    A.luts = L;
+    for (int m = 0; m < 4; ++m) A.s[m] = scales[m];
+    A.plug_idx = plug_idx;
+    A.plug_vals = reinterpret_cast<const f16*>(plug_vals);
+    A.plug_n = plug_n;
+    A.M = (int)M;
+    if (int rc = launch_rows(A, mt, st)) return rc;
+  }
+  if (n_tail > 0) {
+    QuadTailArgs T = {};
+    T.projs = projs;
+    T.items = tail_items;
+    T.n_items = n_tail;
+    T.luts = L;
+    for (int m = 0; m < 4; ++m) T.s[m] = scales[m];
+    T.plug_idx = plug_idx;
+    T.plug_vals = reinterpret_cast<const f16*>(plug_vals);
+    T.M = (int)M;
+    T.n_codes = n_codes;
+    for (int m = 0; m < 4; ++m) {
+      T.tails[m] = tails ? reinterpret_cast<const f16*>(tails[m]) : nullptr;
+      T.tail_len[m] = tail_len ? tail_len[m] : 0;
+    }
+    const unsigned grid = (unsigned)((n_tail + 3) / 4);
+    switch (mt) {
+      case 1: hipLaunchKernelGGL(quad_tail_kernel<1>, dim3(grid), dim3(256), 0, st, T); break;
+      case 2: hipLaunchKernelGGL(quad_tail_kernel<2>, dim3(grid), dim3(256), 0, st, T); break;
+      case 4: hipLaunchKernelGGL(quad_tail_kernel<4>, dim3(grid), dim3(256), 0, st, T); break;
+      default: hipLaunchKernelGGL(quad_tail_kernel<8>, dim3(grid), dim3(256), 0, st, T); break;
+    }
+    PP_LAUNCH_CHECK();
+  }
+  return PP_OK;
+}

@@ -2,14 +2,17 @@
 
 A stream is the reference's flat Linear order (polar_main.py:33-43): projection p
 is an (N_p, K_p) row-major block at stream position pos_p = sum of the previous
-N*K.  :class:`QuadStream` turns the stream into wavefront tasks once:
+N*K.  :class:`QuadStream` plans the launch once:
 
-* rows fully inside the code stream -> items of up to ``rows_per_item`` full rows
-  (a wavefront walks the whole K of its rows, so nothing is combined across waves);
-* rows that reach the FP16 tails (positions >= n) -> one-row TAIL items;
-* each item carries its plug range (searchsorted of the sorted plug_idx over its
-  rows, as quaternion_packer.py:188-189 does per chunk);
-* wavefront w runs items [bounds[w], bounds[w+1]), balanced by bytes.
+* rows fully inside the code stream are cut into tasks of ``rows_per_task`` rows
+  (the kernel's row group); the tasks, in stream order, are dealt to the
+  wavefronts in contiguous runs of equal bytes;
+* each wavefront's run is split at projection boundaries into segments
+  (``pp_quad_seg``: projection, row range, first plug entry at or after the
+  segment start, found with searchsorted as quaternion_packer.py:188-189 does per
+  chunk); inside a segment the kernel finds each task's plug entries itself;
+* rows that reach the FP16 tails (positions >= n) become one-row TAIL items with
+  their plug range, decoded by a second small kernel.
 
 ``bind`` fixes the activation / output buffers, ``__call__`` launches
 ``pp_quad_stream`` on the current torch stream.
@@ -28,73 +31,92 @@ from .quad_kernels import header_luts
 
 ITEM_DTYPE = np.dtype([("proj", "<i4"), ("row0", "<i4"), ("nrows", "<i4"), ("flags", "<i4"),
                        ("plug_lo", "<i8"), ("plug_hi", "<i8")])
+SEG_DTYPE = np.dtype([("proj", "<i4"), ("row0", "<i4"), ("row1", "<i4"), ("flags", "<i4"), ("plug_lo", "<i8")])
 PROJ_DTYPE = np.dtype([("codes", "<u8"), ("ldc", "<i8"), ("pos0", "<i8"), ("x", "<u8"), ("x_sm", "<i8"),
                        ("out", "<u8", (4,)), ("o_sm", "<i8"), ("N", "<i4"), ("K", "<i4")])
-SEG = 256
 
 
-def plan_items(shapes, n, plug_host, rows_per_item):
-    """Wavefront tasks of a stream (pure host logic).
-
-    Rows fully below the code count ``n`` become items of up to ``rows_per_item``
-    full rows; rows that reach position ``n`` become one-row TAIL items.  Each item
-    carries the range of sorted plug entries that fall in its rows.
-    """
-    pos = np.cumsum([0] + [int(a) * int(b) for a, b in shapes])
-    parts = []
-    for p, ((N, K), pos0) in enumerate(zip(shapes, pos[:-1])):
-        N, K, pos0 = int(N), int(K), int(pos0)
-        r_full = int(np.clip((n - pos0) // K, 0, N))
-        if r_full > 0:
-            row0 = np.arange(0, r_full, rows_per_item)
-            it = np.zeros(row0.size, ITEM_DTYPE)
-            it["proj"] = p
-            it["row0"] = row0
-            it["nrows"] = np.minimum(rows_per_item, r_full - row0)
-            parts.append(it)
-        if r_full < N:
-            rows = np.arange(r_full, N)
-            it = np.zeros(rows.size, ITEM_DTYPE)
-            it["proj"] = p
-            it["row0"] = rows
-            it["nrows"] = 1
-            it["flags"] = nat.PP_ITEM_TAIL
-            parts.append(it)
-    items = np.concatenate(parts) if parts else np.zeros(0, ITEM_DTYPE)
-    if items.size:
-        K = np.array([k for _, k in shapes], np.int64)[items["proj"]]
-        lo = pos[:-1].astype(np.int64)[items["proj"]] + items["row0"].astype(np.int64) * K
-        hi = lo + items["nrows"].astype(np.int64) * K
-        items["plug_lo"] = np.searchsorted(plug_host, lo, side="left")
-        items["plug_hi"] = np.searchsorted(plug_host, hi, side="left")
-    return items
+def full_rows(shapes, n):
+    """Stream position of each projection and how many of its rows lie fully below ``n``."""
+    pos = np.cumsum([0] + [int(a) * int(b) for a, b in shapes]).astype(np.int64)
+    N = np.array([int(a) for a, _ in shapes], np.int64)
+    K = np.array([int(b) for _, b in shapes], np.int64)
+    r_full = np.clip((int(n) - pos[:-1]) // np.maximum(K, 1), 0, N)
+    return pos[:-1], N, K, r_full
 
 
-def item_bytes(items, shapes, M=1):
-    """Bytes each item reads (codes, activations, plug entries); TAIL rows run on a scalar
-    path and are weighted 4x."""
-    klen = np.array([k for _, k in shapes], np.int64)[items["proj"]]
-    b = 4 * items["nrows"].astype(np.int64) * klen + 2 * M * klen
-    b += 12 * (items["plug_hi"] - items["plug_lo"])
-    tail = (items["flags"] & nat.PP_ITEM_TAIL) != 0
-    b[tail] = 16 * klen[tail]
-    return b
+def plan_tasks(shapes, n, rows_per_task):
+    """Tasks (proj, row0, nrows) over the full rows of every projection, in stream order."""
+    pos0, N, K, r_full = full_rows(shapes, n)
+    counts = (r_full + rows_per_task - 1) // rows_per_task
+    proj = np.repeat(np.arange(len(shapes), dtype=np.int64), counts)
+    first = np.concatenate([[0], np.cumsum(counts)[:-1]]) if counts.size else np.zeros(0, np.int64)
+    local = np.arange(proj.size, dtype=np.int64) - np.repeat(first, counts)
+    row0 = local * rows_per_task
+    nrows = np.minimum(rows_per_task, r_full[proj] - row0) if proj.size else np.zeros(0, np.int64)
+    return proj, row0, nrows
 
 
-def wave_bounds(item_bytes_, n_waves):
-    """Item ranges per wavefront so that each gets ~1/n_waves of the bytes."""
-    starts = np.concatenate([[0], np.cumsum(item_bytes_)[:-1]]) if item_bytes_.size else np.zeros(0, np.int64)
-    total = int(item_bytes_.sum())
+def task_bytes(proj, nrows, shapes, M=1):
+    """Bytes each task reads: its codes and its activation vector(s)."""
+    K = np.array([int(b) for _, b in shapes], np.int64)[proj]
+    return 4 * nrows * K + 2 * M * K
+
+
+def wave_bounds(bytes_, n_waves):
+    """Contiguous ranges of tasks per wavefront so that each gets ~1/n_waves of the bytes."""
+    starts = np.concatenate([[0], np.cumsum(bytes_)[:-1]]) if bytes_.size else np.zeros(0, np.int64)
+    total = int(bytes_.sum())
     targets = np.arange(n_waves + 1, dtype=np.float64) * total / max(n_waves, 1)
     bounds = np.searchsorted(starts, targets, side="left").astype(np.int64)
     bounds[0] = 0
-    bounds[-1] = item_bytes_.size
+    bounds[-1] = bytes_.size
     return np.maximum.accumulate(bounds)
 
 
+def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1):
+    """Per-wave segments (SEG_DTYPE) and seg_bounds (n_waves + 1) for the rows below ``n``."""
+    proj, row0, nrows = plan_tasks(shapes, n, rows_per_task)
+    tb = wave_bounds(task_bytes(proj, nrows, shapes, M), n_waves)
+    if proj.size == 0:
+        return np.zeros(0, SEG_DTYPE), np.zeros(n_waves + 1, np.int64)
+    wave = np.searchsorted(tb, np.arange(proj.size), side="right") - 1
+    brk = np.ones(proj.size, bool)
+    brk[1:] = (wave[1:] != wave[:-1]) | (proj[1:] != proj[:-1])
+    first = np.flatnonzero(brk)
+    last = np.concatenate([first[1:], [proj.size]]) - 1
+    segs = np.zeros(first.size, SEG_DTYPE)
+    segs["proj"] = proj[first]
+    segs["row0"] = row0[first]
+    segs["row1"] = row0[last] + nrows[last]
+    pos0, _, K, _ = full_rows(shapes, n)
+    start = pos0[proj[first]] + row0[first] * K[proj[first]]
+    segs["plug_lo"] = np.searchsorted(plug_host, start, side="left")
+    seg_wave = wave[first]
+    bounds = np.searchsorted(seg_wave, np.arange(n_waves + 1), side="left").astype(np.int64)
+    return segs, bounds
+
+
+def plan_tail_items(shapes, n, plug_host):
+    """One TAIL item per row that reaches position ``n``, with its plug range."""
+    pos0, N, K, r_full = full_rows(shapes, n)
+    parts = []
+    for p in np.flatnonzero(r_full < N):
+        rows = np.arange(r_full[p], N[p])
+        it = np.zeros(rows.size, ITEM_DTYPE)
+        it["proj"] = p
+        it["row0"] = rows
+        it["nrows"] = 1
+        it["flags"] = nat.PP_ITEM_TAIL
+        lo = pos0[p] + rows * K[p]
+        it["plug_lo"] = np.searchsorted(plug_host, lo, side="left")
+        it["plug_hi"] = np.searchsorted(plug_host, lo + K[p], side="left")
+        parts.append(it)
+    return np.concatenate(parts) if parts else np.zeros(0, ITEM_DTYPE)
+
+
 class QuadStream:
-    def __init__(self, pack: QuadPackDevice, shapes: Sequence[Tuple[int, int]], M: int = 1,
-                 schedule: str = "bytes"):
+    def __init__(self, pack: QuadPackDevice, shapes: Sequence[Tuple[int, int]], M: int = 1):
         L = nat.lib()
         self.pack = pack
         self.shapes = [(int(n), int(k)) for n, k in shapes]
@@ -111,21 +133,15 @@ class QuadStream:
         for n, k in self.shapes:
             if k % 4 or k >= 2 ** 31 or n >= 2 ** 31:
                 raise ValueError(f"stream decode needs K % 4 == 0 (got N={n}, K={k})")
-        items = plan_items(self.shapes, pack.n, pack.plug_host(), self.rows_per_item)
-        is_tail = (items["flags"] & nat.PP_ITEM_TAIL) != 0
-        self.tail_items_np = items[is_tail]
-        items = items[~is_tail]
-        self.items_np = items
-        self.n_items = items.size
-        self.n_tail = self.tail_items_np.size
-        self.item_bytes = item_bytes(items, self.shapes, self.M)
+        plug = pack.plug_host()
         self.n_waves = int(L.pp_quad_stream_waves(self.M))
-        if schedule not in ("interleave", "bytes"):
-            raise ValueError("schedule must be 'interleave' or 'bytes'")
-        self.schedule = schedule
-        self.bounds_np = wave_bounds(self.item_bytes, self.n_waves)
+        self.segs_np, self.bounds_np = plan_segments(self.shapes, pack.n, plug, self.n_waves, self.rows_per_item,
+                                                     self.M)
+        self.tail_items_np = plan_tail_items(self.shapes, pack.n, plug)
+        self.n_segs = self.segs_np.size
+        self.n_tail = self.tail_items_np.size
         dev = self.device
-        self.items = torch.from_numpy(items.view(np.uint8).copy()).to(dev)
+        self.segs = torch.from_numpy(self.segs_np.view(np.uint8).copy()).to(dev)
         self.tail_items = torch.from_numpy(self.tail_items_np.view(np.uint8).copy()).to(dev)
         self.bounds = torch.from_numpy(self.bounds_np).to(dev)
         self.luts = header_luts(pack.r_max, device=dev)
@@ -177,13 +193,13 @@ class QuadStream:
         pk = self.pack
         stream = torch.cuda.current_stream(self.device).cuda_stream
         rc = nat.lib().pp_quad_stream(self.projs.data_ptr(), len(self.shapes),
-                                      self.items.data_ptr() if self.n_items else None, self.n_items,
+                                      self.segs.data_ptr() if self.n_segs else None, self.n_segs,
+                                      self.bounds.data_ptr(), self.n_waves,
                                       self.tail_items.data_ptr() if self.n_tail else None, self.n_tail,
-                                      self.bounds.data_ptr() if self.schedule == "bytes" else None, self.n_waves,
                                       self._lut_ptrs, self._scales,
                                       pk.plug_idx.data_ptr() if pk.plug_idx.numel() else None,
                                       pk.plug_vals.data_ptr() if pk.plug_vals.numel() else None,
-                                      pk.n, self._tail_ptrs, self._tail_len, self.M, stream)
+                                      int(pk.plug_idx.numel()), pk.n, self._tail_ptrs, self._tail_len, self.M, stream)
         nat.check(rc, "pp_quad_stream")
 
     # ---------------------------------------------------------------- accounting
