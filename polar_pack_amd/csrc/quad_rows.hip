@@ -45,47 +45,38 @@ constexpr uint32_t QLDS_BYTES = 0x28000;  // 160 KiB: all of a gfx950 CU's LDS
 constexpr int NT_AUX = 2;                 // non-temporal cache policy for streamed codes
 constexpr uint32_t OOB = 0x80000000u;     // buffer offset past any num_records: reads 0
 
-// Buffer resource (V#) in scalar registers: base, stride 0, num_records bytes.
-// Offsets at or past num_records read 0 and drop writes.
-typedef int rsrc_t __attribute__((ext_vector_type(4)));
+// Buffer resource (V#): base, stride 0, num_records bytes.  Offsets at or past
+// num_records read 0 and drop writes.  The fields go through readfirstlane so the
+// resource lives in scalar registers.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   const uint64_t a = reinterpret_cast<uint64_t>(p);
-  rsrc_t r;
-  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-  r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu));
-  r.z = __builtin_amdgcn_readfirstlane((int)bytes);
-  r.w = 0x00020000;
-  return r;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* u = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
 
-// The decode loop issues its memory operations itself and counts them: the compiler
-// would otherwise wait for every outstanding load at each plug-table branch, which
-// drains the prefetched chunk.  Each result is tied (tie()) after the s_waitcnt that
-// covers it, so nothing reads or moves the register before the data has arrived.
+// Loads and stores of the decode loop.  They are compiler-visible buffer operations:
+// the compiler tracks every outstanding load and waits for it before the first
+// instruction that reads the register (including any register copy it inserts), so the
+// pipeline below only has to keep the number of memory operations per step fixed and
+// avoid reading a result early.
 __device__ __forceinline__ void vload128(u32x4& d, uint32_t off, rsrc_t r) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen nt" : "=v"(d) : "v"(off), "s"(r) : "memory");
+  d = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, NT_AUX);
 }
 __device__ __forceinline__ void vload64(u32x2& d, uint32_t off, rsrc_t r) {
-  asm volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen" : "=v"(d) : "v"(off), "s"(r) : "memory");
+  d = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
 }
 __device__ __forceinline__ void vload32(uint32_t& d, uint32_t off, rsrc_t r) {
-  asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(d) : "v"(off), "s"(r) : "memory");
+  d = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
 __device__ __forceinline__ void vload16(uint32_t& d, uint32_t off, rsrc_t r) {
-  asm volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=v"(d) : "v"(off), "s"(r) : "memory");
+  d = __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
 }
 __device__ __forceinline__ void vstore16(uint32_t v, uint32_t off, rsrc_t r) {
-  asm volatile("buffer_store_short %0, %1, %2, 0 offen" : : "v"(v), "v"(off), "s"(r) : "memory");
-}
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-template <class T>
-__device__ __forceinline__ void tie(T& v) {
-  asm volatile("" : "+v"(v) : : "memory");
+  __builtin_amdgcn_raw_buffer_store_b16((unsigned short)v, r, (int)off, 0, 0);
 }
 __device__ __forceinline__ float h2f(uint32_t bits) { return (float)__builtin_bit_cast(f16, (unsigned short)bits); }
 
@@ -172,18 +163,15 @@ __device__ __forceinline__ void lookup(const char* lds, uint32_t cw, const LaneO
 #ifndef PP_ROWS1_NT
 #define PP_ROWS1_NT 512
 #endif
-#ifndef PP_ROWS1_PD
-#define PP_ROWS1_PD 1
-#endif
-// RG rows per task, NSEG x 256 columns per chunk, NT threads per workgroup, PD chunks
-// prefetched ahead of the one being decoded.
+// RG rows per task, NSEG x 256 columns per chunk, NT threads per workgroup; one chunk
+// is prefetched ahead of the one being decoded.
 template <int MT> struct RowsCfg;
 template <> struct RowsCfg<1> {
-  static constexpr int RG = PP_ROWS1_RG, NSEG = PP_ROWS1_NSEG, NT = PP_ROWS1_NT, PD = PP_ROWS1_PD;
+  static constexpr int RG = PP_ROWS1_RG, NSEG = PP_ROWS1_NSEG, NT = PP_ROWS1_NT;
 };
-template <> struct RowsCfg<2> { static constexpr int RG = 2, NSEG = 2, NT = 1024, PD = 1; };
-template <> struct RowsCfg<4> { static constexpr int RG = 1, NSEG = 2, NT = 1024, PD = 1; };
-template <> struct RowsCfg<8> { static constexpr int RG = 1, NSEG = 2, NT = 512, PD = 1; };
+template <> struct RowsCfg<2> { static constexpr int RG = 2, NSEG = 2, NT = 512; };
+template <> struct RowsCfg<4> { static constexpr int RG = 1, NSEG = 2, NT = 512; };
+template <> struct RowsCfg<8> { static constexpr int RG = 1, NSEG = 2, NT = 512; };
 
 struct QuadRowsArgs {
   // single-projection front end (segs == nullptr): wave w owns row tasks
@@ -209,6 +197,8 @@ struct QuadRowsArgs {
 struct SegCtx {
   rsrc_t rc;          // codes of the segment's rows (row r at byte r*ldc*4)
   rsrc_t rx;          // activations (token j, column k at byte (j*x_sm + k)*2)
+  const uint32_t* codes;  // the same two, as pointers
+  const f16* x;
   int64_t pos0;       // stream position of the segment's first row
   int ldc, K, nrows, x_sm;
   int row0;           // projection row of the segment's first row
@@ -223,34 +213,31 @@ struct Chunk {
   static constexpr int LOADS = RG * NSEG + MT * NSEG;
 };
 
-template <int MT, int RG, int NSEG>
-__device__ __forceinline__ void chunk_tie(Chunk<MT, RG, NSEG>& c) {
-#pragma unroll
-  for (int r = 0; r < RG; ++r)
-#pragma unroll
-    for (int s = 0; s < NSEG; ++s) tie(c.q[r][s]);
-#pragma unroll
-  for (int j = 0; j < MT; ++j)
-#pragma unroll
-    for (int s = 0; s < NSEG; ++s) tie(c.xr[j][s]);
-}
-
 // Issue every load of one chunk (Chunk::LOADS instructions): RG rows x NSEG segments of
-// codes at byte offset `so` of the segment (task rows and column kc folded in), plus
-// the activations.  Past the segment's last row or past K the loads read zero.
+// codes starting at row `row` (of the segment) and column kc, plus the activations.
+// The buffer resources are rebased to the chunk in scalar registers, so each lane's
+// offsets are fixed for the whole segment (no per-step vector address arithmetic):
+// codes resource = rows [row, nrows) from column kc, num_records ends at column K of
+// the segment's last row, so rows past the segment and columns past K of the last row
+// read 0; columns past K of other rows read the next row's codes, which meet a zero x.
 template <int MT, int RG, int NSEG>
-__device__ __forceinline__ void chunk_issue(const SegCtx& S, uint32_t so, int kc, const uint32_t (&voff)[RG],
-                                            int lane, Chunk<MT, RG, NSEG>& c) {
+__device__ __forceinline__ void chunk_issue(const SegCtx& S, int row, int kc, const uint32_t (&voff)[RG], int lane,
+                                            Chunk<MT, RG, NSEG>& c) {
+  const int64_t first = (int64_t)row * S.ldc + kc;
+  const int64_t end = (int64_t)(S.nrows - 1) * S.ldc + S.K;   // one past the last code
+  const rsrc_t rc = make_rsrc(S.codes + first, 4u * (uint32_t)(end - first));
 #pragma unroll
   for (int r = 0; r < RG; ++r)
 #pragma unroll
-    for (int s = 0; s < NSEG; ++s) vload128(c.q[r][s], voff[r] + so + 1024u * s, S.rc);
+    for (int s = 0; s < NSEG; ++s) vload128(c.q[r][s], voff[r] + 1024u * s, rc);
+  if constexpr (MT == 1) {
+    const rsrc_t rx = make_rsrc(S.x + kc, 2u * (uint32_t)(S.K - kc));   // past K: reads 0
 #pragma unroll
-  for (int s = 0; s < NSEG; ++s) {
-    const int k = kc + s * QSEG + 4 * lane;
-    if constexpr (MT == 1) {
-      vload64(c.xr[0][s], 2u * (uint32_t)k, S.rx);  // past K: out of the buffer
-    } else {
+    for (int s = 0; s < NSEG; ++s) vload64(c.xr[0][s], 8u * lane + 512u * s, rx);
+  } else {
+#pragma unroll
+    for (int s = 0; s < NSEG; ++s) {
+      const int k = kc + s * QSEG + 4 * lane;
       const bool valid = k < S.K;
 #pragma unroll
       for (int j = 0; j < MT; ++j) vload64(c.xr[j][s], valid ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
@@ -396,14 +383,6 @@ __device__ __forceinline__ void plug_begin(const QuadRowsArgs& A, const SegCtx& 
   vload32(P.idx, 4u * lane, plug_idx_rsrc(A, pc));
 }
 
-template <int MT>
-__device__ __forceinline__ void plug_tie(PlugSt<MT>& P) {
-  tie(P.cw);
-  tie(P.pv);
-#pragma unroll
-  for (int j = 0; j < MT; ++j) tie(P.xk[j]);
-}
-
 template <int MT, int RG, class L>
 __device__ __forceinline__ void plug_correct(const char* lds, const LaneOff& lo, int row, uint32_t cw, f16x4 pv,
                                              const float (&xk)[MT], float (&acc)[RG][4][MT]) {
@@ -427,9 +406,9 @@ __device__ __forceinline__ void plug_correct(const char* lds, const LaneOff& lo,
   }
 }
 
-// End of task ti (its dependent loads have arrived): apply its entries; for a dense
-// task, the ones past the first 64 too (compiler-managed loads, waited on at once), then
-// reload the next task's positions.  Returns the number of counted loads it issued.
+// Finish the plug entries of task ti: apply the ones located when it began; for a dense
+// task (>= 64 entries), the rest too (loaded and used at once: rare), then reload the
+// next task's positions at the advanced cursor.  Returns 1 when it took the dense path.
 template <int MT, int RG, class L>
 __device__ __forceinline__ int plug_end(const char* lds, const LaneOff& lo, const QuadRowsArgs& A, const SegCtx& S,
                                         int ti, int lane, int64_t& pc, PlugSt<MT>& P, float (&acc)[RG][4][MT]) {
@@ -443,12 +422,8 @@ __device__ __forceinline__ int plug_end(const char* lds, const LaneOff& lo, cons
   const int64_t tpos0 = S.pos0 + (int64_t)ti * RG * S.ldc;
   const int nr = min(RG, S.nrows - ti * RG);
   const int64_t tend = tpos0 + (int64_t)nr * S.ldc;
-  vm_wait<0>();            // the next task's positions were loaded at the old cursor
-  tie(P.idx);
-  const uint32_t* codes = reinterpret_cast<const uint32_t*>(
-      (static_cast<uint64_t>(static_cast<uint32_t>(S.rc.y)) << 32) | static_cast<uint32_t>(S.rc.x));
-  const f16* x = reinterpret_cast<const f16*>(
-      (static_cast<uint64_t>(static_cast<uint32_t>(S.rx.y)) << 32) | static_cast<uint32_t>(S.rx.x));
+  const uint32_t* codes = S.codes;
+  const f16* x = S.x;
   for (;;) {
     const int64_t q = pc + lane;
     const bool has = q < A.plug_n;
@@ -469,6 +444,9 @@ __device__ __forceinline__ int plug_end(const char* lds, const LaneOff& lo, cons
     if (cnt < 64) break;
   }
   vload32(P.idx, 4u * lane, plug_idx_rsrc(A, pc));
+  // wait for it here: a load still in flight on this rare path would make the compiler
+  // assume it may be in flight at every next use, and wait for the prefetch there
+  asm volatile("" : : "v"(P.idx));
   return 1;
 }
 
@@ -583,26 +561,24 @@ struct Cursor {
   int ti, ck;
 };
 
-template <int MT, int RG, int NSEG, int PD, class L>
+template <int MT, int RG, int NSEG, class L>
 struct SegRunner {
   static constexpr int CHUNK = NSEG * QSEG;
-  static constexpr int NQ = Chunk<MT, RG, NSEG>::LOADS;   // loads per prefetched chunk
-  static constexpr int NP = PlugSt<MT>::LOADS;            // loads at a task's first chunk
-  static constexpr int NS = 4;                            // stores at a task's last chunk
   const char* lds;
   LaneOff lo;
   const QuadRowsArgs& A;
   const SegCtx& S;
   int lane, nck, ntask;
   uint32_t voff[RG];
-  float acc[RG][4][MT];
-  PlugSt<MT> P;
+  float acc[RG][4][MT];    // the task being decoded
+  float pend[RG][4][MT];   // the previous task, finished one step late
+  int pend_ti;             // its index, -1 when none
+  PlugSt<MT> P;            // plug entries of the pending task (then of the current one)
   int64_t pc;
   Cursor lc;               // next chunk to load
-  bool pf, pl;             // the previous step issued plug loads / stores after its prefetch
 
   __device__ __forceinline__ SegRunner(const char* l, const QuadRowsArgs& a, const SegCtx& s, int64_t plug_lo)
-      : lds(l), A(a), S(s), pc(plug_lo), pf(false), pl(false) {
+      : lds(l), A(a), S(s), pend_ti(-1), pc(plug_lo) {
     lane = threadIdx.x & 63;
     lo = L::lane(lane);
     nck = (S.K + CHUNK - 1) / CHUNK;
@@ -621,97 +597,60 @@ struct SegRunner {
   }
 
   // Issue the next chunk's loads (past the last chunk: reload the last one, so every
-  // step issues exactly NQ loads).
+  // step issues the same loads).
   __device__ __forceinline__ void prefetch(Chunk<MT, RG, NSEG>& c) {
-    const Cursor ld = lc;
-    chunk_issue<MT, RG, NSEG>(S, 4u * (uint32_t)(ld.ti * RG * S.ldc + ld.ck * CHUNK), ld.ck * CHUNK, voff, lane, c);
+    chunk_issue<MT, RG, NSEG>(S, lc.ti * RG, lc.ck * CHUNK, voff, lane, c);
     Cursor nx = lc;
     advance(nx);
     if (nx.ti < ntask) lc = nx;
   }
 
-  // Wait until the chunk issued PD steps ago has arrived.  The memory operations of a
-  // step, in issue order, are  NQ prefetch loads | NP plug loads (first chunk of a task)
-  // | NS stores (last chunk of a task); they complete in order, so "everything up to the
-  // chunk issued PD steps ago" means at most PD*NQ plus the previous step's plug loads
-  // and stores still outstanding (for PD = 2; for PD = 1 the previous step's plug loads
-  // and stores precede this step's prefetch and only NS may stay outstanding... which
-  // the formula below also covers, as they are counted only when they came after the
-  // chunk in question).
-  __device__ __forceinline__ void wait_chunk() {
-    if constexpr (PD == 1) {
-      // previous step: [NQ (this chunk)] [NP?] [NS?]   this step: [NQ]
-      if (pf && pl) vm_wait<NQ + NP + NS>();
-      else if (pf) vm_wait<NQ + NP>();
-      else if (pl) vm_wait<NQ + NS>();
-      else vm_wait<NQ>();
-    } else {
-      // step-1: [NQ] [NP?] [NS?]   this step: [NQ]; the chunk came before step-1's prefetch
-      if (pf && pl) vm_wait<2 * NQ + NP + NS>();
-      else if (pf) vm_wait<2 * NQ + NP>();
-      else if (pl) vm_wait<2 * NQ + NS>();
-      else vm_wait<2 * NQ>();
-    }
+  // Finish the pending task: plug corrections, wave reduction, stores.
+  __device__ __forceinline__ void finish_pending() {
+    plug_end<MT, RG, L>(lds, lo, A, S, pend_ti, lane, pc, P, pend);
+    task_write<MT, RG>(A, S, pend_ti, lane, pend);
+    pend_ti = -1;
   }
 
-  // Compute the step at `cur` from `comp` while `pref` receives a later chunk.
+  // One step.  Memory operations are placed so that each is consumed at least one
+  // step after it was issued, and every conditional one right after the prefetch:
+  //   prefetch the next chunk | [first chunk of a task] finish the previous task (its
+  //   plug loads arrived during the previous step; its stores) and issue this task's
+  //   plug loads | decode the current chunk | [last chunk] park the sums for the next step.
+  // The compiler waits for each register before its first use; since nothing is used
+  // in the step that loaded it, no wait has to cover the prefetch just issued.
   __device__ __forceinline__ bool step(Cursor& cur, Chunk<MT, RG, NSEG>& comp, Chunk<MT, RG, NSEG>& pref) {
     prefetch(pref);
-    wait_chunk();
-    chunk_tie<MT, RG, NSEG>(comp);
-    const bool first = cur.ck == 0, last = cur.ck == nck - 1;
-    // plug positions of this task were loaded at the previous task's first chunk, i.e.
-    // before the prefetch of that step; with fewer than PD+1 chunks per task that load
-    // may still be outstanding
-    if (first) {
-      if (nck <= PD) vm_wait<0>();
-      tie(P.idx);
+    if (cur.ck == 0) {
+      if (pend_ti >= 0) finish_pending();
       plug_begin<MT, RG>(A, S, cur.ti, lane, pc, P);
     }
     chunk_compute<MT, RG, NSEG, L>(lds, lo, comp, acc);
-    if (last) {
-      // the dependent plug loads were issued at this task's first chunk: they are covered
-      // by the chunk wait only when that was at least PD+1 steps ago
-      if (nck <= PD + 1) vm_wait<0>();
-      plug_tie<MT>(P);
-      if (plug_end<MT, RG, L>(lds, lo, A, S, cur.ti, lane, pc, P, acc)) vm_wait<0>();
-      task_write<MT, RG>(A, S, cur.ti, lane, acc);
+    if (cur.ck == nck - 1) {
+#pragma unroll
+      for (int r = 0; r < RG; ++r)
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int j = 0; j < MT; ++j) pend[r][m][j] = acc[r][m][j];
       zero_acc<MT, RG>(acc);
+      pend_ti = cur.ti;
     }
-    pf = first;
-    pl = last;
     advance(cur);
     return cur.ti < ntask;
   }
 
   __device__ __forceinline__ void run() {
     if (ntask <= 0 || S.K <= 0) return;
-    Chunk<MT, RG, NSEG> c0, c1, c2;
+    Chunk<MT, RG, NSEG> c0, c1;
     Cursor cur = {0, 0};
     vload32(P.idx, 4u * lane, plug_idx_rsrc(A, pc));
-    if constexpr (PD == 1) {
-      prefetch(c0);
-      for (;;) {
-        if (!step(cur, c0, c1)) break;
-        if (!step(cur, c1, c0)) break;
-      }
-    } else {
-      prefetch(c0);
-      prefetch(c1);
-      for (;;) {
-        if (!step(cur, c0, c2)) break;
-        if (!step(cur, c1, c0)) break;
-        if (!step(cur, c2, c1)) break;
-      }
+    prefetch(c0);
+    for (;;) {
+      if (!step(cur, c0, c1)) break;
+      if (!step(cur, c1, c0)) break;
     }
-    // drain: the last prefetches (reloads), the next positions and the stores are still
-    // in flight; their registers must stay allocated until they land
-    vm_wait<0>();
-    chunk_tie<MT, RG, NSEG>(c0);
-    chunk_tie<MT, RG, NSEG>(c1);
-    if constexpr (PD == 2) chunk_tie<MT, RG, NSEG>(c2);
-    tie(P.idx);
-    plug_tie<MT>(P);
+    finish_pending();
   }
 };
 
@@ -730,8 +669,10 @@ __device__ __forceinline__ void seg_ctx(const pp_quad_proj& P, int64_t o_sn, int
   S.x_sm = uniform((int)P.x_sm);
   S.pos0 = uniform64(P.pos0) + (int64_t)row0 * ldc;
   const uint32_t cbytes = S.nrows > 0 ? 4u * (uint32_t)((S.nrows - 1) * ldc + K) : 0u;
-  S.rc = make_rsrc(uniform_ptr(P.codes) + (int64_t)row0 * ldc, cbytes);
-  S.rx = make_rsrc(uniform_ptr(P.x), 2u * (uint32_t)((M - 1) * S.x_sm + K));
+  S.codes = uniform_ptr(P.codes) + (int64_t)row0 * ldc;
+  S.x = reinterpret_cast<const f16*>(uniform_ptr(P.x));
+  S.rc = make_rsrc(S.codes, cbytes);
+  S.rx = make_rsrc(S.x, 2u * (uint32_t)((M - 1) * S.x_sm + K));
 #pragma unroll
   for (int m = 0; m < 4; ++m) S.out[m] = reinterpret_cast<f16*>(uniform_ptr(P.out[m])) + (int64_t)row0 * o_sn;
   S.o_sm = uniform64(P.o_sm);
@@ -750,7 +691,7 @@ __device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A
     if (row1 <= row0) return;
     SegCtx S;
     seg_ctx(A.proj, A.o_sn, row0, row1, A.M, S);
-    SegRunner<MT, RG, NSEG, RowsCfg<MT>::PD, L> R(lds, A, S, A.wave_plug ? uniform64(A.wave_plug[gw]) : 0);
+    SegRunner<MT, RG, NSEG, L> R(lds, A, S, A.wave_plug ? uniform64(A.wave_plug[gw]) : 0);
     R.run();
     return;
   }
@@ -759,7 +700,7 @@ __device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A
     const pp_quad_seg g = A.segs[si];
     SegCtx S;
     seg_ctx(A.projs[uniform(g.proj)], 1, g.row0, g.row1, A.M, S);
-    SegRunner<MT, RG, NSEG, RowsCfg<MT>::PD, L> R(lds, A, S, uniform64(g.plug_lo));
+    SegRunner<MT, RG, NSEG, L> R(lds, A, S, uniform64(g.plug_lo));
     R.run();
   }
 }
