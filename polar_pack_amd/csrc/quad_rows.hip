@@ -261,7 +261,7 @@ template <int MT, int RG, int NSEG, class L>
 __device__ __forceinline__ void chunk_compute(const char* lds, const LaneOff& lo, const Chunk<MT, RG, NSEG>& c,
                                               float (&acc)[RG][4][MT]) {
 #ifndef PP_LOOKUP_GROUP
-#define PP_LOOKUP_GROUP 2
+#define PP_LOOKUP_GROUP 4
 #endif
   constexpr int GT = PP_LOOKUP_GROUP;       // tuples per group
   constexpr int NT = RG * NSEG * 4;         // tuples per lane in the chunk
