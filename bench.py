@@ -12,7 +12,7 @@ Prints ONE JSON line: achieved GB/s of algorithmic bytes (value), ms per step,
 roofline (HIP-event kernel time vs 8 TB/s HBM) and the CPU baseline (the CPU
 oracle's numpy unpack + torch CPU matmul on a bounded sample, extrapolated).
 
-    python bench.py [--steps 20] [--warmup 5] [--layers 36] [--no-cpu]
+    python bench.py [--steps 30] [--warmup 10] [--layers 36] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -120,8 +120,8 @@ def read_pmc_traffic():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--cpu-sample-tuples", type=int, default=77_070_336)  # one layer
     ap.add_argument("--no-cpu", action="store_true")
