@@ -47,8 +47,8 @@ const char* pp_last_error(void);
 const char* pp_version(void);
 
 /* sizeof of the ABI structs, for binding checks: out[0] = sizeof(pp_quad_proj),
- * out[1] = sizeof(pp_quad_item), out[2] = sizeof(pp_quad_seg).  Returns the number of
- * values written. */
+ * out[1] = sizeof(pp_quad_item), out[2] = sizeof(pp_quad_seg), out[3] = sizeof(pp_dual_proj).
+ * Returns the number of values written. */
 int pp_abi_sizes(int64_t* out, int n);
 
 /* ------------------------------------------------------------------------ */
@@ -215,6 +215,44 @@ int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk, int64_t c_
                     int phase_n, int lut_dtype,
                     const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n, int64_t elem_base,
                     float* out1, float* out2, int64_t N, int64_t K, void* stream);
+
+/*
+ * Whole-stream dual decode for 1..4 tokens: every projection of a .dualpack stream in
+ * one launch.  Same segment / tail-item planning as pp_quad_stream (the structs are
+ * shared); projections are described by pp_dual_proj.  Codes are the stream's 16-bit
+ * pairs in `code_layout`; scales are the fp16 group maxima (n_groups of them) with the
+ * group rule of the file (group_size, chunk_size: groups restart every chunk);
+ * amp_lut / cos_lut / sin_lut are float32 tables from the header (64 / 1024 / 1024
+ * entries); plug entries replace the amplitude of a pair by an exact fp16 amplitude.
+ * Positions >= n_codes come from the per-model fp16 tails (tails[m], tail_len[m]): a
+ * build-defined extension for streams whose models have different lengths (the file
+ * format itself zero-pads the shorter model).
+ * Replaces the per-projection polar_dual_bitpacked calls of a decode step
+ * (polar_kernels.py:98-115) and the decode of unpack_dual_models
+ * (polar_bitpack.py:194-260).
+ */
+typedef struct pp_dual_proj {
+  const void* codes;       /* 16-bit code of (row 0, col 0); row r starts at codes + r*ldc */
+  int64_t ldc;             /* row stride in pairs */
+  int64_t pos0;            /* stream position of (row 0, col 0) */
+  const void* x;           /* fp16 activations (M, K), row stride x_sm */
+  int64_t x_sm;
+  void* out[2];            /* fp16 outputs (M, N) of the two models, row stride o_sm */
+  int64_t o_sm;
+  int32_t N, K;
+} pp_dual_proj;
+
+int pp_dual_stream_rows(int64_t M);
+int64_t pp_dual_stream_waves(int64_t M);
+
+int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs,
+                   const pp_quad_seg* segs, int64_t n_segs, const int64_t* seg_bounds, int64_t n_waves,
+                   const pp_quad_item* tail_items, int64_t n_tail,
+                   int code_layout, const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
+                   const float* amp_lut, const float* cos_lut, const float* sin_lut,
+                   const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n,
+                   int64_t n_codes, const void* const* tails, const int64_t* tail_len,
+                   int64_t M, void* stream);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,12 @@ class QuadSeg(C.Structure):
                 ("plug_lo", i64)]
 
 
+class DualProj(C.Structure):
+    """``pp_dual_proj`` (include/polar_pack.h)."""
+    _fields_ = [("codes", vp), ("ldc", i64), ("pos0", i64), ("x", vp), ("x_sm", i64),
+                ("out", vp * 2), ("o_sm", i64), ("N", C.c_int32), ("K", C.c_int32)]
+
+
 EXPORTS = {
     "pp_last_error": (C.c_char_p, []),
     "pp_version": (C.c_char_p, []),
@@ -50,6 +56,10 @@ EXPORTS = {
     "pp_quad_stream_rows": (i32, [i64]),
     "pp_quad_stream_waves": (i64, [i64]),
     "pp_quad_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, vp, vp, vp, i64, i64, vp, vp, i64, vp]),
+    "pp_dual_stream_rows": (i32, [i64]),
+    "pp_dual_stream_waves": (i64, [i64]),
+    "pp_dual_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, i32, vp, i64, i64, i64, vp, vp, vp, vp, vp, i64,
+                             i64, vp, vp, i64, vp]),
     "pp_dual_gemm": (i32, [vp, i64, i64, vp, i32, i64, i64, vp, i64, i64, vp, i32, vp, vp, i32, i32,
                            vp, vp, i64, i64, vp, vp, i64, i64, i64, i64, i64, vp, i64, vp]),
     "pp_dual_gemm_workspace_size": (i64, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64]),

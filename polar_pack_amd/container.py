@@ -198,3 +198,50 @@ class DualPackFile:
     def codes_device(self, device) -> torch.Tensor:
         """The big-endian codes as an int16 device tensor (bytes unchanged)."""
         return torch.from_numpy(self.codes_be.view(np.int16).copy()).to(device)
+
+    def to_device(self, device) -> "DualPackDevice":
+        """The stream in device memory, codes in the file's big-endian layout."""
+        return DualPackDevice(
+            n_codes=self.n_pairs, n1=self.n1, n2=self.n2, codes=self.codes_device(device), layout="u16be",
+            scales=torch.from_numpy(np.ascontiguousarray(self.scales)).to(device),
+            plug_idx=_u32_tensor(self.plug_idx).to(device),
+            plug_val=torch.from_numpy(np.ascontiguousarray(self.plug_val)).to(device),
+            amp_bits=self.amp_bits, phase_bits=self.phase_bits, mu=float(self.mu), group_size=self.group_size,
+            chunk_size=self.chunk_size, plug_idx_host=self.plug_idx.copy())
+
+
+@dataclass
+class DualPackDevice:
+    """A dual stream resident in device memory (what the stream decode reads).
+
+    ``codes`` holds ``n_codes`` 16-bit pairs, either as the file stores them
+    (``layout="u16be"``) or in the int16 kernel layout (``"i16"``).  ``tails`` is
+    this build's extension for models of different lengths: model m's weights at
+    positions ``n_codes ..`` as fp16 (the ``.dualpack`` format itself zero-pads the
+    shorter model instead, polar_bitpack.py:113-117, and has no tails).
+    """
+    n_codes: int
+    n1: int
+    n2: int
+    codes: torch.Tensor           # int16 (n_codes,)
+    layout: str
+    scales: torch.Tensor          # float16 (n_groups,)
+    plug_idx: torch.Tensor        # uint32 as int32 (P,), ascending
+    plug_val: torch.Tensor        # float16 (P,), absolute amplitude
+    amp_bits: int = 6
+    phase_bits: int = 10
+    mu: float = 255.0
+    group_size: int = 32
+    chunk_size: int = 50_000_000
+    tails: List[torch.Tensor] = field(default_factory=list)
+    plug_idx_host: Optional[np.ndarray] = None
+
+    @property
+    def tail_lengths(self):
+        t = list(self.tails) + [None] * (2 - len(self.tails))
+        return [int(x.numel()) if x is not None else 0 for x in t]
+
+    def plug_host(self) -> np.ndarray:
+        if self.plug_idx_host is None:
+            self.plug_idx_host = self.plug_idx.cpu().view(torch.int32).numpy().view(np.uint32)
+        return self.plug_idx_host

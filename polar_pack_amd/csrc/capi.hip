@@ -39,9 +39,9 @@ extern "C" const char* pp_last_error(void) { return pp::g_last_error.c_str(); }
 extern "C" const char* pp_version(void) { return "polar_pack_amd 0.1 gfx950"; }
 
 extern "C" int pp_abi_sizes(int64_t* out, int n) {
-  const int64_t v[3] = {(int64_t)sizeof(pp_quad_proj), (int64_t)sizeof(pp_quad_item),
-                        (int64_t)sizeof(pp_quad_seg)};
+  const int64_t v[4] = {(int64_t)sizeof(pp_quad_proj), (int64_t)sizeof(pp_quad_item),
+                        (int64_t)sizeof(pp_quad_seg), (int64_t)sizeof(pp_dual_proj)};
   int k = 0;
-  for (; k < n && k < 3; ++k) out[k] = v[k];
+  for (; k < n && k < 4; ++k) out[k] = v[k];
   return k;
 }

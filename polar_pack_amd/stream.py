@@ -34,6 +34,8 @@ ITEM_DTYPE = np.dtype([("proj", "<i4"), ("row0", "<i4"), ("nrows", "<i4"), ("fla
 SEG_DTYPE = np.dtype([("proj", "<i4"), ("row0", "<i4"), ("row1", "<i4"), ("flags", "<i4"), ("plug_lo", "<i8")])
 PROJ_DTYPE = np.dtype([("codes", "<u8"), ("ldc", "<i8"), ("pos0", "<i8"), ("x", "<u8"), ("x_sm", "<i8"),
                        ("out", "<u8", (4,)), ("o_sm", "<i8"), ("N", "<i4"), ("K", "<i4")])
+DUAL_PROJ_DTYPE = np.dtype([("codes", "<u8"), ("ldc", "<i8"), ("pos0", "<i8"), ("x", "<u8"), ("x_sm", "<i8"),
+                            ("out", "<u8", (2,)), ("o_sm", "<i8"), ("N", "<i4"), ("K", "<i4")])
 
 
 def full_rows(shapes, n):
@@ -57,10 +59,10 @@ def plan_tasks(shapes, n, rows_per_task):
     return proj, row0, nrows
 
 
-def task_bytes(proj, nrows, shapes, M=1):
+def task_bytes(proj, nrows, shapes, M=1, code_bytes=4):
     """Bytes each task reads: its codes and its activation vector(s)."""
     K = np.array([int(b) for _, b in shapes], np.int64)[proj]
-    return 4 * nrows * K + 2 * M * K
+    return code_bytes * nrows * K + 2 * M * K
 
 
 def wave_bounds(bytes_, n_waves):
@@ -74,10 +76,10 @@ def wave_bounds(bytes_, n_waves):
     return np.maximum.accumulate(bounds)
 
 
-def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1):
+def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=4):
     """Per-wave segments (SEG_DTYPE) and seg_bounds (n_waves + 1) for the rows below ``n``."""
     proj, row0, nrows = plan_tasks(shapes, n, rows_per_task)
-    tb = wave_bounds(task_bytes(proj, nrows, shapes, M), n_waves)
+    tb = wave_bounds(task_bytes(proj, nrows, shapes, M, code_bytes), n_waves)
     if proj.size == 0:
         return np.zeros(0, SEG_DTYPE), np.zeros(n_waves + 1, np.int64)
     wave = np.searchsorted(tb, np.arange(proj.size), side="right") - 1
@@ -213,4 +215,120 @@ class QuadStream:
             P = int(np.searchsorted(plug, hi) - np.searchsorted(plug, lo))
             tail_w = sum(max(0, min(hi, self.pack.n + t) - max(lo, self.pack.n)) for t in self.pack.tail_lengths)
             total += 4 * in_codes + 12 * P + 2 * self.M * K + 8 * self.M * N + 2 * tail_w
+        return total
+
+
+class DualStream:
+    """One-launch decode of every projection of a dual stream (``pp_dual_stream``).
+
+    Same planning as :class:`QuadStream`; positions past ``pack.n_codes`` come from the
+    per-model fp16 tails.  Projection rows and positions must be multiples of 8 pairs
+    (a lane reads 8 pairs that share one group scale).
+    """
+
+    def __init__(self, pack, shapes: Sequence[Tuple[int, int]], M: int = 1):
+        L = nat.lib()
+        self.pack = pack
+        self.shapes = [(int(n), int(k)) for n, k in shapes]
+        self.M = int(M)
+        self.device = pack.codes.device
+        self.rows_per_item = int(L.pp_dual_stream_rows(self.M))
+        nat.check(0 if self.rows_per_item > 0 else nat.PP_EINVAL, "pp_dual_stream_rows")
+        pos = np.cumsum([0] + [n * k for n, k in self.shapes])
+        self.pos0 = pos[:-1]
+        total = int(pos[-1])
+        longest = pack.n_codes + max(pack.tail_lengths)
+        if total > longest:
+            raise ValueError(f"projections cover {total} positions, the stream holds {longest}")
+        for n, k in self.shapes:
+            if k % 8 or k >= 2 ** 31 or n >= 2 ** 31:
+                raise ValueError(f"dual stream decode needs K % 8 == 0 (got N={n}, K={k})")
+        if pack.group_size < 8 or pack.group_size & (pack.group_size - 1) or pack.chunk_size % 8:
+            raise ValueError("dual stream decode needs a power-of-two group_size >= 8 and chunk_size % 8 == 0")
+        plug = pack.plug_host()
+        self.n_waves = int(L.pp_dual_stream_waves(self.M))
+        self.segs_np, self.bounds_np = plan_segments(self.shapes, pack.n_codes, plug, self.n_waves,
+                                                     self.rows_per_item, self.M, code_bytes=2)
+        self.tail_items_np = plan_tail_items(self.shapes, pack.n_codes, plug)
+        self.n_segs = self.segs_np.size
+        self.n_tail = self.tail_items_np.size
+        dev = self.device
+        self.segs = torch.from_numpy(self.segs_np.view(np.uint8).copy()).to(dev)
+        self.tail_items = torch.from_numpy(self.tail_items_np.view(np.uint8).copy()).to(dev)
+        self.bounds = torch.from_numpy(self.bounds_np).to(dev)
+        from .polar_kernels import header_luts as dual_header_luts
+        self.luts = dual_header_luts(pack.amp_bits, pack.phase_bits, pack.mu, device=dev)
+        tails = list(pack.tails) + [None] * (2 - len(pack.tails))
+        self._tail_ptrs = nat.ptr_array([t.data_ptr() if t is not None and t.numel() else 0 for t in tails])
+        self._tail_len = (C.c_int64 * 2)(*pack.tail_lengths)
+        self.code_layout = nat.PP_DUAL_U16_BE if pack.layout == "u16be" else nat.PP_DUAL_I16_OFFSET
+        self.projs = None
+
+    def make_buffers(self):
+        """One activation buffer (M, K_p) and 2 output buffers (M, N_p) per projection."""
+        xs, outs = [], []
+        for N, K in self.shapes:
+            xs.append(torch.empty((self.M, K), dtype=torch.float16, device=self.device))
+            outs.append([torch.empty((self.M, N), dtype=torch.float16, device=self.device) for _ in range(2)])
+        return xs, outs
+
+    def bind(self, xs: List[torch.Tensor], outs: List[List[torch.Tensor]]):
+        if len(xs) != len(self.shapes) or len(outs) != len(self.shapes):
+            raise ValueError("one activation and 2 outputs per projection")
+        tab = np.zeros(len(self.shapes), DUAL_PROJ_DTYPE)
+        base = self.pack.codes.data_ptr()
+        for p, ((N, K), pos0) in enumerate(zip(self.shapes, self.pos0)):
+            x, o = xs[p], outs[p]
+            if x.shape != (self.M, K) or x.dtype != torch.float16 or x.stride(1) != 1 or x.data_ptr() % 16 \
+                    or (self.M > 1 and x.stride(0) % 8):
+                raise ValueError(f"projection {p}: activations must be fp16 ({self.M}, {K}), unit stride, "
+                                 "16-byte aligned")
+            for t in o:
+                if t.shape != (self.M, N) or t.dtype != torch.float16 or t.stride(1) != 1:
+                    raise ValueError(f"projection {p}: outputs must be fp16 ({self.M}, {N}), unit stride")
+            if o[0].stride(0) != o[1].stride(0):
+                raise ValueError(f"projection {p}: the 2 outputs must share a row stride")
+            tab[p]["codes"] = base + 2 * int(pos0)
+            tab[p]["ldc"] = K
+            tab[p]["pos0"] = int(pos0)
+            tab[p]["x"] = x.data_ptr()
+            tab[p]["x_sm"] = x.stride(0)
+            tab[p]["out"] = [t.data_ptr() for t in o]
+            tab[p]["o_sm"] = o[0].stride(0)
+            tab[p]["N"] = N
+            tab[p]["K"] = K
+        self.projs = torch.from_numpy(tab.view(np.uint8).copy()).to(self.device)
+        self._bound = (xs, outs)
+
+    def __call__(self):
+        if self.projs is None:
+            raise RuntimeError("DualStream.bind() must be called before launching")
+        pk = self.pack
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        amp, cos, sin = self.luts
+        rc = nat.lib().pp_dual_stream(self.projs.data_ptr(), len(self.shapes),
+                                      self.segs.data_ptr() if self.n_segs else None, self.n_segs,
+                                      self.bounds.data_ptr(), self.n_waves,
+                                      self.tail_items.data_ptr() if self.n_tail else None, self.n_tail,
+                                      self.code_layout, pk.scales.data_ptr(), int(pk.scales.numel()),
+                                      pk.group_size, pk.chunk_size, amp.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                      pk.plug_idx.data_ptr() if pk.plug_idx.numel() else None,
+                                      pk.plug_val.data_ptr() if pk.plug_val.numel() else None,
+                                      int(pk.plug_idx.numel()), pk.n_codes, self._tail_ptrs, self._tail_len,
+                                      self.M, stream)
+        nat.check(rc, "pp_dual_stream")
+
+    def algorithmic_bytes(self) -> int:
+        """2*N*K codes + 2 B per group scale + 6 B per plug entry + 2*M*K x + 4*M*N outputs
+        + 2 B per tail weight read."""
+        plug = self.pack.plug_host()
+        gs = self.pack.group_size
+        n = self.pack.n_codes
+        total = 0
+        for (N, K), pos0 in zip(self.shapes, self.pos0):
+            lo, hi = int(pos0), int(pos0) + N * K
+            in_codes = max(0, min(hi, n) - lo)
+            P = int(np.searchsorted(plug, hi) - np.searchsorted(plug, lo))
+            tail_w = sum(max(0, min(hi, n + t) - max(lo, n)) for t in self.pack.tail_lengths)
+            total += 2 * in_codes + 2 * (-(-in_codes // gs)) + 6 * P + 2 * self.M * K + 4 * self.M * N + 2 * tail_w
         return total

@@ -1,0 +1,124 @@
+"""GPU parity of the one-launch dual stream decode (pp_dual_stream) against the float64 oracle."""
+import numpy as np
+import pytest
+import torch
+
+import gen
+from oracle import dualpack as odp
+from parity import assert_gemv_close
+from polar_pack_amd.container import DualPackDevice, DualPackFile
+from polar_pack_amd.stream import DualStream
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+# (N, K) projections in stream order, K % 8 == 0; rows of 2048-11008 pairs and short ones
+SHAPES = [(24, 1024), (8, 2048), (16, 4096), (40, 512), (12, 11008), (3, 16), (9, 520)]
+TOTAL = sum(n * k for n, k in SHAPES)
+
+
+def oracle_pairs(dp, tails=None):
+    """float64 (w1, w2) over the whole stream: codes below dp.n_pairs, tails after."""
+    w1, w2 = odp.decode_pairs_f64(dp, 0, dp.n_pairs)
+    if tails is not None:
+        t1, t2 = tails
+        w1 = np.concatenate([w1, t1.astype(np.float64), np.full(TOTAL, np.nan)])[:TOTAL]
+        w2 = np.concatenate([w2, t2.astype(np.float64), np.full(TOTAL, np.nan)])[:TOTAL]
+    return w1, w2
+
+
+def oracle_outputs(w, xs):
+    outs, pos = [], 0
+    for (N, K), x in zip(SHAPES, xs):
+        per = []
+        for m in range(2):
+            wm = w[m][pos:pos + N * K].reshape(N, K)
+            missing = np.isnan(wm[:, 0])                 # a model without the row reads 0
+            y = x.astype(np.float64) @ np.nan_to_num(wm, nan=0.0).T
+            y[:, missing] = 0.0
+            per.append(y)
+        outs.append(per)
+        pos += N * K
+    return outs
+
+
+def to_i16(codes_be_u8):
+    """File layout -> int16 kernel layout (code - 32768)."""
+    code = odp.from_be_bytes(codes_be_u8).astype(np.uint16)
+    return (code ^ np.uint16(0x8000)).view(np.int16)
+
+
+def device_pack(dp, layout, tails=None, n_codes=None):
+    f = DualPackFile(n_pairs=dp.n_pairs, n1=dp.n1, n2=dp.n2, codes_be=dp.codes_be, scales=dp.scales,
+                     plug_idx=dp.plug_idx, plug_val=dp.plug_val, amp_bits=dp.amp_bits, phase_bits=dp.phase_bits,
+                     mu=dp.mu, group_size=dp.group_size, chunk_size=dp.chunk_size)
+    pack = f.to_device(DEV)
+    if layout == "i16":
+        pack.codes = torch.from_numpy(to_i16(dp.codes_be)).to(DEV)
+        pack.layout = "i16"
+    if tails is not None:
+        pack.tails = [torch.from_numpy(np.ascontiguousarray(t)).to(DEV) for t in tails]
+    return pack
+
+
+def run_stream(pack, M, seed=5):
+    st = DualStream(pack, SHAPES, M=M)
+    xs_np = [np.random.default_rng(seed + p).standard_normal((M, k)).astype(np.float16)
+             for p, (_, k) in enumerate(SHAPES)]
+    xs = [torch.from_numpy(x).to(DEV) for x in xs_np]
+    outs = [[torch.full((M, n), float("nan"), dtype=torch.float16, device=DEV) for _ in range(2)] for n, _ in SHAPES]
+    st.bind(xs, outs)
+    return st, xs_np, outs
+
+
+@pytest.mark.parametrize("layout", ["u16be", "i16"])
+@pytest.mark.parametrize("chunk", [50_000_000, 1000])     # groups aligned / restarting mid-group
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_dual_stream_zero_padded_file(layout, chunk, M):
+    """The .dualpack format itself: model 2 shorter and zero-padded, plug cap 3%."""
+    w1, w2 = gen.correlated_models(11, [TOTAL, TOTAL - 3000], delta_growth=False)
+    dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=0.03, chunk_size=chunk))
+    assert dp.plug_idx.size > 0
+    pack = device_pack(dp, layout)
+    st, xs_np, outs = run_stream(pack, M)
+    ref = oracle_outputs(oracle_pairs(dp), xs_np)
+    for rep in range(2):
+        st()
+        torch.cuda.synchronize()
+        for p in range(len(SHAPES)):
+            for m in range(2):
+                assert_gemv_close(outs[p][m].float().cpu().numpy(), ref[p][m], f"rep {rep} proj {p} model {m}")
+
+
+@pytest.mark.parametrize("layout", ["u16be", "i16"])
+def test_dual_stream_fp16_tails(layout):
+    """Tail mode: codes cover the shorter model's length; model 1's rest is fp16 tail, model
+    2 has no weights there (rows past its end read 0, the straddling row its prefix)."""
+    n2 = TOTAL - 9 * 520 + 100          # the last projection's row 0 straddles n2
+    w1, w2 = gen.correlated_models(13, [TOTAL, n2], delta_growth=False)
+    dp = odp.pack_dual(w1[:n2], w2, odp.DualConfig(plug_cap=0.01, chunk_size=50_000_000))
+    t1 = np.asarray(w1[n2:], np.float32).astype(np.float16)
+    t2 = np.zeros(0, np.float16)
+    pack = device_pack(dp, layout, tails=(t1, t2))
+    st, xs_np, outs = run_stream(pack, 1)
+    assert st.n_tail == 9
+    ref = oracle_outputs(oracle_pairs(dp, tails=(t1, t2)), xs_np)
+    st()
+    torch.cuda.synchronize()
+    for p in range(len(SHAPES)):
+        for m in range(2):
+            assert_gemv_close(outs[p][m].float().cpu().numpy(), ref[p][m], f"proj {p} model {m}")
+
+
+def test_dual_stream_dense_plug_tasks():
+    """A plug table dense enough that tasks hold more than 64 entries."""
+    w1, w2 = gen.correlated_models(17, [TOTAL, TOTAL], delta_growth=False)
+    dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=0.2, chunk_size=50_000_000))
+    pack = device_pack(dp, "u16be")
+    st, xs_np, outs = run_stream(pack, 1)
+    ref = oracle_outputs(oracle_pairs(dp), xs_np)
+    st()
+    torch.cuda.synchronize()
+    for p in range(len(SHAPES)):
+        for m in range(2):
+            assert_gemv_close(outs[p][m].float().cpu().numpy(), ref[p][m], f"proj {p} model {m}")

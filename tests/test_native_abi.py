@@ -34,11 +34,12 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_struct_layouts_match():
-    out = (C.c_int64 * 3)()
-    assert nat.lib().pp_abi_sizes(out, 3) == 3
+    out = (C.c_int64 * 4)()
+    assert nat.lib().pp_abi_sizes(out, 4) == 4
     assert out[0] == C.sizeof(nat.QuadProj)
     assert out[1] == C.sizeof(nat.QuadItem)
     assert out[2] == C.sizeof(nat.QuadSeg)
+    assert out[3] == C.sizeof(nat.DualProj)
 
 
 def test_version_and_error_string():

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 from polar_pack_amd import _native as nat
-from polar_pack_amd.stream import (ITEM_DTYPE, SEG_DTYPE, plan_segments, plan_tail_items, plan_tasks, task_bytes,
+from polar_pack_amd.stream import (DUAL_PROJ_DTYPE, ITEM_DTYPE, SEG_DTYPE, plan_segments, plan_tail_items, plan_tasks, task_bytes,
                                    wave_bounds)
 
 SHAPES = [(2048, 2048), (256, 2048), (256, 2048), (2048, 2048), (11008, 2048), (11008, 2048), (2048, 11008)]
@@ -75,3 +75,6 @@ def test_struct_layouts_match_abi():
     assert SEG_DTYPE.itemsize == ctypes.sizeof(nat.QuadSeg) == 24
     for name, _ in nat.QuadSeg._fields_:
         assert getattr(nat.QuadSeg, name).offset == SEG_DTYPE.fields[name][1]
+    assert DUAL_PROJ_DTYPE.itemsize == ctypes.sizeof(nat.DualProj) == 72
+    for name, _ in nat.DualProj._fields_:
+        assert getattr(nat.DualProj, name).offset == DUAL_PROJ_DTYPE.fields[name][1]
