@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
 """Batch-1 decode step over a quad-pack Qwen2.5-3B-shaped Linear stream on one MI355X.
 
-Workload (one "step"): 36 layers x {q, o 2048x2048; k, v 256x2048; gate, up
-11008x2048; down 2048x11008} projections, 4 models packed in one .quadpack v2
+Default workload (one "step"): 36 layers x {q, o 2048x2048; k, v 256x2048; gate,
+up 11008x2048; down 2048x11008} projections, 4 models packed in one .quadpack v2
 stream (2,774,532,096 uint32 tuples, top 0.1% of tuples by norm in the plug table),
 one fp16 N(0,1) activation vector per projection, 4 fp16 outputs per projection,
 decoded by one pp_quad_stream launch.  Weights are synthetic: per layer-seeded
@@ -13,6 +13,22 @@ roofline (HIP-event kernel time vs 8 TB/s HBM) and the CPU baseline (the CPU
 oracle's numpy unpack + torch CPU matmul on a bounded sample, extrapolated).
 
     python bench.py [--steps 30] [--warmup 10] [--layers 36] [--no-cpu]
+
+Other workloads (``--workload``), one JSON line each:
+
+* ``dual3b``     -- dual-pack 3B-shaped stream, Student-t(df=3) base, model 2 = base +
+                    N(0, 0.004) truncated to 95% of the stream, top 1% of pairs in the plug
+                    table (largest squared amplitude error per 50M-pair chunk); model 1's
+                    last 5% are fp16 tails; one pp_dual_stream launch per step;
+* ``dual3b-pad`` -- the same weights in the .dualpack format itself (model 2 zero-padded);
+* ``dual2048``   -- one dual 2048x2048 Linear, 2 models, plug 0.1% by norm;
+* ``quadgate``   -- one quad 11008x2048 Linear (gate_proj), 4 models, plug 0.1% by norm;
+* ``sweep``      -- quad gate_proj 11008x2048 and down_proj 2048x11008 at 1, 4, 16, 64
+                    tokens per model (one line per shape and batch).
+
+Single-Linear workloads rotate enough copies of the packed weights (>= 512 MB in total)
+that no launch finds its codes in the 256 MB last-level cache, and time a HIP graph of
+one launch per copy, so the figure is device time without host launch gaps.
 """
 from __future__ import annotations
 
@@ -30,40 +46,69 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+from polar_pack_amd import polar_kernels as pk  # noqa: E402
 from polar_pack_amd import quad_kernels as qk  # noqa: E402
-from polar_pack_amd.packer import pack_quad_device  # noqa: E402
-from polar_pack_amd.stream import QuadStream  # noqa: E402
+from polar_pack_amd.packer import pack_dual_device, pack_quad_device  # noqa: E402
+from polar_pack_amd.stream import DualStream, QuadStream  # noqa: E402
 
 METRIC = "achieved HBM GB/s (% of peak) + ms per quad-pack 3B decode step, batch 1"
 PEAK_HBM_GBS = 8000.0
+PEAK_FP16_TFLOPS = 2500.0
 LAYER = [("q_proj", 2048, 2048), ("k_proj", 256, 2048), ("v_proj", 256, 2048), ("o_proj", 2048, 2048),
          ("gate_proj", 11008, 2048), ("up_proj", 11008, 2048), ("down_proj", 2048, 11008)]
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "quad_stream_3b_pmc.md")
+PMC_SUMMARY = {"quad3b": os.path.join(ROOT, "profiles", "quad_stream_3b_pmc.md"),
+               "dual3b": os.path.join(ROOT, "profiles", "dual_stream_3b_pmc.md")}
+MALL_BYTES = 512 << 20
 
 
 def seed_of(config, layer, proj):
     return 20260000 + 1000 * config + 10 * layer + proj
 
 
+def student_t(n, df, std, g, dev):
+    """Student-t(df) scaled to standard deviation ``std`` (variance of t_df is df/(df-2))."""
+    z = torch.randn(n, generator=g, device=dev)
+    chi = torch.zeros_like(z)
+    for _ in range(df):
+        chi += torch.randn(n, generator=g, device=dev) ** 2
+    return z / torch.sqrt(chi / df) * (std / math.sqrt(df / (df - 2.0)))
+
+
 def synth_models(n_layers, dev):
     """4 correlated fp16 models, flat (N,K) row-major per projection, stream order."""
     models = [[], [], [], []]
-    t_scale = 0.02 / math.sqrt(5.0 / 3.0)         # Student-t(5) has variance 5/3
     for layer in range(n_layers):
         for p, (_, n, k) in enumerate(LAYER):
             g = torch.Generator(device=dev).manual_seed(seed_of(3, layer, p))
-            z = torch.randn(n * k, generator=g, device=dev)
-            chi = torch.zeros_like(z)
-            for _ in range(5):
-                chi += torch.randn(n * k, generator=g, device=dev) ** 2
-            w0 = z / torch.sqrt(chi / 5.0) * t_scale
-            del z, chi
+            w0 = student_t(n * k, 5, 0.02, g, dev)
             for m in range(4):
                 d = torch.randn(n * k, generator=g, device=dev) * (0.002 * (m + 1))
                 models[m].append((w0 + d).to(torch.float16))
                 del d
             del w0
     return models
+
+
+def synth_dual_stream(shapes, dev, truncate=0.05):
+    """Flat fp16 model streams: model 1 = Student-t(3) base (std 0.02), model 2 = base +
+    N(0, 0.004), model 2 truncated to floor((1 - truncate) * n1) weights."""
+    n1 = sum(n * k for n, k in shapes)
+    n2 = int(math.floor((1.0 - truncate) * n1))
+    w1 = torch.empty(n1, dtype=torch.float16, device=dev)
+    w2 = torch.empty(n2, dtype=torch.float16, device=dev)
+    pos = 0
+    for i, (n, k) in enumerate(shapes):
+        layer, p = divmod(i, len(LAYER))
+        g = torch.Generator(device=dev).manual_seed(seed_of(5, layer, p))
+        w0 = student_t(n * k, 3, 0.02, g, dev)
+        w1[pos:pos + n * k] = w0.to(torch.float16)
+        d = torch.randn(n * k, generator=g, device=dev) * 0.004
+        hi = min(pos + n * k, n2)
+        if hi > pos:
+            w2[pos:hi] = (w0 + d)[:hi - pos].to(torch.float16)
+        del w0, d
+        pos += n * k
+    return w1, w2
 
 
 def cpu_baseline(pack, shapes, sample_tuples):
@@ -107,44 +152,99 @@ def cpu_baseline(pack, shapes, sample_tuples):
             "step_s": (t_unpack + t_mm) * scale, "threads": threads}
 
 
-def read_pmc_traffic():
+def cpu_baseline_dual(pack, shapes, sample_pairs):
+    """The CPU oracle's dual unpack (numpy float64, single thread) + torch CPU float32 matmul
+    on the first projections of the stream up to ~sample_pairs, extrapolated to the step."""
+    from oracle import dualpack as odp
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    take, pairs = [], 0
+    for n, k in shapes:
+        if pairs + n * k > sample_pairs and take:
+            break
+        take.append((n, k))
+        pairs += n * k
+    pairs = min(pairs, pack.n_codes)
+    be = pack.codes[:pairs].cpu().numpy().view(np.uint16)
+    if pack.layout == "i16":
+        be = (be ^ np.uint16(0x8000)).byteswap()
+    plug = pack.plug_host()
+    hi = int(np.searchsorted(plug, pairs))
+    ng = odp.n_groups_for(pairs, pack.chunk_size, pack.group_size)
+    dp = odp.DualPack(n_pairs=pairs, n1=pairs, n2=pairs, codes_be=be.view(np.uint8).copy(),
+                      scales=pack.scales[:ng].cpu().numpy(), plug_idx=plug[:hi].copy(),
+                      plug_val=pack.plug_val[:hi].cpu().numpy(), amp_bits=pack.amp_bits,
+                      phase_bits=pack.phase_bits, mu=pack.mu, group_size=pack.group_size,
+                      chunk_size=pack.chunk_size)
+    rng = np.random.default_rng(0)
+    t_unpack = t_mm = 0.0
+    pos = 0
+    for n, k in take:
+        t0 = time.perf_counter()
+        w1, w2 = odp.decode_pairs_f64(dp, pos, pos + n * k)
+        w1, w2 = w1.astype(np.float32), w2.astype(np.float32)
+        t1 = time.perf_counter()
+        x = torch.from_numpy(rng.standard_normal((1, k)).astype(np.float32))
+        for w in (w1, w2):
+            y = x @ torch.from_numpy(w.reshape(n, k)).t()
+        t2 = time.perf_counter()
+        t_unpack += t1 - t0
+        t_mm += t2 - t1
+        pos += n * k
+        del w1, w2, y
+    total = sum(n * k for n, k in shapes)
+    scale = total / pairs
+    return {"unpack_s": t_unpack, "matmul_s": t_mm, "sample": pairs, "scale": scale,
+            "step_s": (t_unpack + t_mm) * scale, "threads": threads}
+
+
+def read_pmc_traffic(path):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE), if committed."""
     try:
-        text = open(PMC_SUMMARY).read()
-    except OSError:
+        text = open(path).read()
+    except (OSError, TypeError):
         return None
     m = re.search(r"traffic_bytes_per_launch\s*[=:]\s*([0-9.eE+]+)", text)
     return float(m.group(1)) if m else None
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=30)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--layers", type=int, default=36)
-    ap.add_argument("--cpu-sample-tuples", type=int, default=77_070_336)  # one layer
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--quiet", action="store_true")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run a 2 GiB device-to-device copy (reference for the rocprof byte counters)")
-    args = ap.parse_args()
-    if args.copy_calibration:
-        src = torch.ones(2 << 30, dtype=torch.uint8, device="cuda:0")
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes": 2 << 30, "launches": 3}))
-        return
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (the decode step is a "
-              "single-GPU path; see DESIGN.md for how it would shard)", file=sys.stderr)
-        sys.exit(2)
-    log = (lambda *a: None) if args.quiet else (lambda *a: print(*a, file=sys.stderr, flush=True))
-    dev = torch.device("cuda:0")
-    shapes = [(n, k) for _ in range(args.layers) for (_, n, k) in LAYER]
+def time_events(launch, steps, warmup):
+    """HIP-event duration of each of ``steps`` launches on torch's current stream (the
+    stream the decode kernels are launched on), after ``warmup`` untimed launches."""
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        launch()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)], wall
 
+
+def line(metric, achieved, ms, args, dtype, config, traffic=None, cpu=None, extra=None):
+    out = {
+        "metric": metric, "value": round(achieved, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    if extra:
+        out.update(extra)
+    print(json.dumps(out), flush=True)
+
+
+# ---------------------------------------------------------------- 3B-shaped streams
+
+def run_quad3b(args, dev, log):
+    shapes = [(n, k) for _ in range(args.layers) for (_, n, k) in LAYER]
     t0 = time.time()
     models = synth_models(args.layers, dev)
     torch.cuda.synchronize()
@@ -179,20 +279,7 @@ def main():
             if not d <= 2e-3 * ref:
                 raise SystemExit(f"stream/single mismatch on projection {p} model {m}: {d} vs {ref}")
 
-    for _ in range(args.warmup):
-        st()
-    torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    w0 = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record()
-        st()
-        ends[i].record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - w0
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    per, wall = time_events(st, args.steps, args.warmup)
     ms = float(np.mean(per))
     algo = st.algorithmic_bytes()
     achieved = algo / (ms * 1e-3) / 1e9
@@ -210,20 +297,327 @@ def main():
                           f"float32 x@W^T x4 ({c['threads']} threads) {c['matmul_s']:.2f}s, extrapolated x"
                           f"{c['scale']:.1f} to {c['step_s']:.1f}s per step")}
 
-    traffic = read_pmc_traffic()
-    out = {
-        "metric": METRIC, "value": round(achieved, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
-        "config": {"workload": "quad-pack Qwen2.5-3B-shaped Linear stream, batch-1 decode step",
-                   "layers": args.layers, "projections": len(shapes), "models": 4, "batch": 1,
-                   "tuples": int(pack.n), "plug_entries": int(pack.plug_idx.numel()),
-                   "algorithmic_bytes": int(algo), "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic},
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(out), flush=True)
+    line(METRIC, achieved, ms, args, "fp32",
+         {"workload": "quad-pack Qwen2.5-3B-shaped Linear stream, batch-1 decode step",
+          "layers": args.layers, "projections": len(shapes), "models": 4, "batch": 1,
+          "tuples": int(pack.n), "plug_entries": int(pack.plug_idx.numel()),
+          "algorithmic_bytes": int(algo), "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2)},
+         traffic=read_pmc_traffic(PMC_SUMMARY["quad3b"]), cpu=cpu)
+
+
+def run_dual3b(args, dev, log, tails):
+    shapes = [(n, k) for _ in range(args.layers) for (_, n, k) in LAYER]
+    t0 = time.time()
+    w1, w2 = synth_dual_stream(shapes, dev)
+    torch.cuda.synchronize()
+    log(f"[bench] synthesized {w1.numel()} + {w2.numel()} fp16 weights in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    pack = pack_dual_device(w1, w2, plug_cap=0.01, select="ref", tails=tails)
+    torch.cuda.synchronize()
+    del w1, w2
+    torch.cuda.empty_cache()
+    log(f"[bench] packed: {pack.n_codes} pairs, plug {pack.plug_idx.numel()}, tails {pack.tail_lengths} "
+        f"in {time.time() - t0:.1f}s")
+
+    st = DualStream(pack, shapes, M=1)
+    xs, outs = st.make_buffers()
+    g = torch.Generator(device=dev).manual_seed(7)
+    for x in xs:
+        x.copy_(torch.randn(x.shape, generator=g, device=dev).to(torch.float16))
+    st.bind(xs, outs)
+    log(f"[bench] plan: {st.n_segs} segments, {st.n_tail} tail items, {st.n_waves} waves, "
+        f"{st.plug_windows} plug window(s) per step")
+
+    # sanity: a k_proj against the single-Linear operator; the last down_proj's rows that lie
+    # wholly in the fp16 tail against torch (model 2 has no weights there: 0)
+    st()
+    torch.cuda.synchronize()
+    amp, cos, sin = pk.header_luts(pack.amp_bits, pack.phase_bits, pack.mu, device=dev)
+    n, k = shapes[1]
+    pos = int(st.pos0[1])
+    single = pk.polar_dual_bitpacked(xs[1], pack.codes[pos:pos + n * k].reshape(n, k).t(), pack.scales, amp, cos,
+                                     sin, plug=(pack.plug_idx, pack.plug_val), elem_base=pos, layout=pack.layout,
+                                     chunk_size=pack.chunk_size)
+    checks = [(outs[1][m].float(), single[m].float(), f"k_proj model {m}") for m in range(2)]
+    if tails:
+        p = len(shapes) - 1
+        n, k = shapes[p]
+        r0 = max(0, -(-(pack.n_codes - int(st.pos0[p])) // k))     # first row wholly in the tail
+        t0_ = int(st.pos0[p]) + r0 * k - pack.n_codes
+        wt = pack.tails[0][t0_:t0_ + (n - r0) * k].float().reshape(n - r0, k)
+        ref1 = xs[p].float() @ wt.t()
+        checks.append((outs[p][0][:, r0:].float(), ref1, "tail rows model 1"))
+        checks.append((outs[p][1][:, r0:].float(), torch.zeros_like(ref1), "tail rows model 2"))
+    for got, ref, what in checks:
+        d = (got - ref).abs().max().item()
+        scale = max(ref.abs().max().item(), 1e-6)
+        if not d <= 2e-3 * scale:
+            raise SystemExit(f"dual stream sanity check failed on {what}: {d} vs {scale}")
+
+    per, wall = time_events(st, args.steps, args.warmup)
+    ms = float(np.mean(per))
+    algo = st.algorithmic_bytes()
+    achieved = algo / (ms * 1e-3) / 1e9
+    log(f"[bench] step: mean {ms:.4f} ms, median {np.median(per):.4f}, min {min(per):.4f}, wall/step "
+        f"{wall / args.steps * 1e3:.4f} ms; {algo / 1e9:.4f} GB algorithmic -> {achieved:.1f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        c = cpu_baseline_dual(pack, shapes, args.cpu_sample_tuples)
+        log(f"[bench] cpu baseline: unpack {c['unpack_s']:.2f}s + matmul {c['matmul_s']:.2f}s on "
+            f"{c['sample']} pairs -> {c['step_s']:.2f}s per step (x{c['scale']:.1f})")
+        cpu = {"value": algo / c["step_s"] / 1e9, "unit": "GB/s", "cores": c["threads"], "kind": "port",
+               "sample": (f"first {c['sample']} pairs of the stream: numpy float64 unpack_dual restatement "
+                          f"(1 thread) {c['unpack_s']:.2f}s + torch CPU float32 x@W^T x2 ({c['threads']} "
+                          f"threads) {c['matmul_s']:.2f}s, extrapolated x{c['scale']:.1f} to "
+                          f"{c['step_s']:.1f}s per step")}
+    mode = "5% of model 2 truncated, model 1's rest in fp16 tails" if tails else \
+        "model 2 truncated by 5% and zero-padded (.dualpack format)"
+    line("achieved HBM GB/s (% of peak) + ms per dual-pack 3B decode step, batch 1", achieved, ms, args, "fp32",
+         {"workload": f"dual-pack Qwen2.5-3B-shaped Linear stream, batch-1 decode step, {mode}",
+          "layers": args.layers, "projections": len(shapes), "models": 2, "batch": 1,
+          "pairs": int(pack.n_codes), "tail_weights": pack.tail_lengths,
+          "plug_entries": int(pack.plug_idx.numel()), "algorithmic_bytes": int(algo),
+          "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2)},
+         traffic=read_pmc_traffic(PMC_SUMMARY["dual3b"]) if tails else None, cpu=cpu)
+
+
+# ---------------------------------------------------------------- single Linear layers
+
+def graph_of(launches):
+    """One HIP graph that runs every launch once (captured on a side stream)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f in launches:                      # warm the code paths outside the capture
+            f()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in launches:
+            f()
+    torch.cuda.synchronize()
+    return g
+
+
+def rotated_streams(make_stream, pack, shapes, M, copies, dev, quad):
+    """``copies`` launchable single-Linear streams over distinct copies of the packed
+    weights, each with its own activations and outputs."""
+    import copy
+    sts = []
+    g = torch.Generator(device=dev).manual_seed(11)
+    for c in range(copies):
+        p = pack if c == 0 else copy.copy(pack)
+        if c:
+            p.codes = pack.codes.clone()
+            p.plug_idx = pack.plug_idx.clone()
+            if quad:
+                p.plug_vals = pack.plug_vals.clone()
+            else:
+                p.plug_val = pack.plug_val.clone()
+                p.scales = pack.scales.clone()
+        st = make_stream(p, shapes, M=M)
+        xs, outs = st.make_buffers()
+        for x in xs:
+            x.copy_(torch.randn(x.shape, generator=g, device=dev).to(torch.float16))
+        st.bind(xs, outs)
+        sts.append((st, xs, outs))
+    return sts
+
+
+def time_graph(sts, args):
+    g = graph_of([st for st, _, _ in sts])
+    per, wall = time_events(g.replay, args.steps, args.warmup)
+    return float(np.median(per)) / len(sts), per
+
+
+def run_dual2048(args, dev, log):
+    N = K = 2048
+    g = torch.Generator(device=dev).manual_seed(seed_of(1, 0, 0))
+    w0 = student_t(N * K, 5, 0.02, g, dev)
+    w1 = (w0 + torch.randn(N * K, generator=g, device=dev) * 0.002).to(torch.float16)
+    w2 = (w0 + torch.randn(N * K, generator=g, device=dev) * 0.002).to(torch.float16)
+    pack = pack_dual_device(w1, w2, plug_cap=0.001, select="norm")
+    st0 = DualStream(pack, [(N, K)], M=1)
+    copies = max(2, -(-MALL_BYTES // st0.algorithmic_bytes()))
+    sts = rotated_streams(DualStream, pack, [(N, K)], 1, copies, dev, quad=False)
+    sanity_dual_single(sts[0], pack, dev)
+    ms, per = time_graph(sts, args)
+    algo = sts[0][0].algorithmic_bytes()
+    achieved = algo / (ms * 1e-3) / 1e9
+    log(f"[bench] dual 2048x2048: {ms * 1e3:.2f} us per Linear ({copies} rotated copies) -> {achieved:.1f} GB/s")
+    cpu = None if args.no_cpu else cpu_single_dual(pack, N, K)
+    line("achieved HBM GB/s (% of peak) + us per dual-pack 2048x2048 Linear, batch 1", achieved, ms, args, "fp32",
+         {"workload": "dual-pack Linear 2048x2048, 2 models, batch 1", "N": N, "K": K, "models": 2, "batch": 1,
+          "plug_entries": int(pack.plug_idx.numel()), "rotated_copies": copies, "algorithmic_bytes": int(algo),
+          "us_per_linear": round(ms * 1e3, 3), "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2)}, cpu=cpu)
+
+
+def sanity_dual_single(entry, pack, dev):
+    st, xs, outs = entry
+    st()
+    torch.cuda.synchronize()
+    N, K = st.shapes[0]
+    amp, cos, sin = pk.header_luts(pack.amp_bits, pack.phase_bits, pack.mu, device=dev)
+    w = pk.dual_dequant(pack.codes.reshape(N, K).t(), pack.scales, amp, cos, sin, plug=(pack.plug_idx, pack.plug_val),
+                        layout=pack.layout, chunk_size=pack.chunk_size)
+    for m in range(2):
+        ref = xs[0].float() @ w[m]
+        d = (outs[0][m].float() - ref).abs().max().item()
+        if not d <= 2e-3 * ref.abs().max().item():
+            raise SystemExit(f"dual single-Linear sanity check failed on model {m}")
+
+
+def cpu_single_dual(pack, N, K):
+    from oracle import dualpack as odp
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    be = pack.codes.cpu().numpy().view(np.uint8).copy()
+    dp = odp.DualPack(n_pairs=pack.n_codes, n1=pack.n1, n2=pack.n2, codes_be=be, scales=pack.scales.cpu().numpy(),
+                      plug_idx=pack.plug_host().copy(), plug_val=pack.plug_val.cpu().numpy(), mu=pack.mu,
+                      group_size=pack.group_size, chunk_size=pack.chunk_size)
+    x = torch.from_numpy(np.random.default_rng(0).standard_normal((1, K)).astype(np.float32))
+    tu, tm = [], []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        w1, w2 = odp.decode_pairs_f64(dp)
+        w1, w2 = w1.astype(np.float32).reshape(N, K), w2.astype(np.float32).reshape(N, K)
+        t1 = time.perf_counter()
+        for w in (w1, w2):
+            x @ torch.from_numpy(w).t()
+        t2 = time.perf_counter()
+        tu.append(t1 - t0)
+        tm.append(t2 - t1)
+    s = float(np.median(tu)) + float(np.median(tm))
+    algo = 2 * N * K + 2 * -(-N * K // pack.group_size) + 6 * pack.plug_idx.numel() + 2 * K + 4 * N
+    return {"value": algo / s / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the whole Linear: numpy float64 unpack_dual restatement (1 thread) {np.median(tu):.3f}s + "
+                      f"torch CPU float32 x@W^T x2 ({threads} threads) {np.median(tm):.4f}s, median of 3"}
+
+
+def quad_linear_pack(N, K, dev, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w0 = student_t(N * K, 5, 0.02, g, dev)
+    models = [[(w0 + torch.randn(N * K, generator=g, device=dev) * (0.002 * (m + 1))).to(torch.float16)]
+              for m in range(4)]
+    return pack_quad_device(models, plug_cap=0.001, select="norm")
+
+
+def sanity_quad_single(entry, pack, dev):
+    st, xs, outs = entry
+    st()
+    torch.cuda.synchronize()
+    N, K = st.shapes[0]
+    luts = qk.header_luts(pack.r_max, device=dev)
+    w = qk.quad_dequant(pack.codes.reshape(N, K).t(), luts, list(pack.s), plug=(pack.plug_idx, pack.plug_vals))
+    for m in range(4):
+        ref = xs[0].float() @ w[m]
+        d = (outs[0][m].float() - ref).abs().max().item()
+        if not d <= 2e-3 * ref.abs().max().item():
+            raise SystemExit(f"quad single-Linear sanity check failed on model {m}")
+
+
+def cpu_single_quad(pack, N, K, M):
+    from oracle import quadpack as oqp
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    qp = oqp.QuadPack(n=pack.n, s=pack.s, r_max=pack.r_max, codes=pack.codes.cpu().view(torch.int32).numpy()
+                      .view(np.uint32), plug_idx=pack.plug_host().copy(), plug_vals=pack.plug_vals.cpu().numpy())
+    x = torch.from_numpy(np.random.default_rng(0).standard_normal((M, K)).astype(np.float32))
+    tu, tm = [], []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        ws = oqp.unpack_quad(qp)
+        t1 = time.perf_counter()
+        for w in ws:
+            x @ torch.from_numpy(w.reshape(N, K)).t()
+        t2 = time.perf_counter()
+        tu.append(t1 - t0)
+        tm.append(t2 - t1)
+        del ws
+    s = float(np.median(tu)) + float(np.median(tm))
+    algo = 4 * N * K + 12 * pack.plug_idx.numel() + 2 * M * K + 8 * M * N
+    return {"value": algo / s / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the whole Linear at {M} token(s): numpy float64 unpack_quad restatement (1 thread) "
+                      f"{np.median(tu):.3f}s + torch CPU float32 x@W^T x4 ({threads} threads) "
+                      f"{np.median(tm):.4f}s, median of 3"}
+
+
+def run_quad_single(args, dev, log, N, K, M, name, pack=None):
+    pack = pack if pack is not None else quad_linear_pack(N, K, dev, seed_of(2, 0, 0))
+    st0 = QuadStream(pack, [(N, K)], M=M)
+    copies = max(2, -(-MALL_BYTES // st0.algorithmic_bytes()))
+    sts = rotated_streams(QuadStream, pack, [(N, K)], M, copies, dev, quad=True)
+    sanity_quad_single(sts[0], pack, dev)
+    ms, per = time_graph(sts, args)
+    algo = sts[0][0].algorithmic_bytes()
+    achieved = algo / (ms * 1e-3) / 1e9
+    tflops = 8.0 * M * N * K / (ms * 1e-3) / 1e12
+    log(f"[bench] quad {name} {N}x{K} M={M}: {ms * 1e3:.2f} us per Linear ({copies} rotated copies) -> "
+        f"{achieved:.1f} GB/s, {tflops:.2f} TFLOP/s")
+    cpu = None if args.no_cpu else cpu_single_quad(pack, N, K, M)
+    line(f"achieved HBM GB/s (% of peak) + us per quad-pack {name} {N}x{K} Linear, {M} token(s)", achieved, ms,
+         args, "fp32",
+         {"workload": f"quad-pack Linear {name} {N}x{K}, 4 models, {M} token(s) per model", "N": N, "K": K,
+          "models": 4, "batch": M, "plug_entries": int(pack.plug_idx.numel()), "rotated_copies": copies,
+          "algorithmic_bytes": int(algo), "us_per_linear": round(ms * 1e3, 3),
+          "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2), "tflops": round(tflops, 3),
+          "pct_of_fp16_mfma_peak": round(100 * tflops / PEAK_FP16_TFLOPS, 3)}, cpu=cpu)
+    return pack
+
+
+def run_sweep(args, dev, log):
+    for name, N, K in (("gate_proj", 11008, 2048), ("down_proj", 2048, 11008)):
+        pack = quad_linear_pack(N, K, dev, seed_of(4, 0, 0 if name == "gate_proj" else 1))
+        for M in args.sweep_tokens:
+            if M > 8:
+                log(f"[bench] {name} M={M}: the fused decode takes up to 8 tokens per launch; skipped")
+                continue
+            run_quad_single(args, dev, log, N, K, M, name, pack=pack)
+        del pack
+        torch.cuda.empty_cache()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--workload", default="quad3b",
+                    choices=["quad3b", "dual3b", "dual3b-pad", "dual2048", "quadgate", "sweep"])
+    ap.add_argument("--sweep-tokens", type=int, nargs="+", default=[1, 4, 16, 64])
+    ap.add_argument("--cpu-sample-tuples", type=int, default=77_070_336)  # one layer
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 2 GiB device-to-device copy (reference for the rocprof byte counters)")
+    args = ap.parse_args()
+    if args.copy_calibration:
+        src = torch.ones(2 << 30, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": 2 << 30, "launches": 3}))
+        return
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (the decode step is a "
+              "single-GPU path; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+    log = (lambda *a: None) if args.quiet else (lambda *a: print(*a, file=sys.stderr, flush=True))
+    dev = torch.device("cuda:0")
+    if args.workload == "quad3b":
+        run_quad3b(args, dev, log)
+    elif args.workload in ("dual3b", "dual3b-pad"):
+        run_dual3b(args, dev, log, tails=args.workload == "dual3b")
+    elif args.workload == "dual2048":
+        run_dual2048(args, dev, log)
+    elif args.workload == "quadgate":
+        run_quad_single(args, dev, log, 11008, 2048, 1, "gate_proj")
+    else:
+        run_sweep(args, dev, log)
 
 
 if __name__ == "__main__":

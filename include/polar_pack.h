@@ -141,18 +141,22 @@ typedef struct pp_quad_seg {
   int32_t proj;
   int32_t row0;
   int32_t row1;
-  int32_t flags;           /* reserved, 0 */
+  int32_t task0;           /* dual stream: index of the run's first task in task_plug;
+                              quad stream: reserved, 0 */
   int64_t plug_lo;
 } pp_quad_seg;
 
-enum pp_item_flags { PP_ITEM_TAIL = 1 };
+enum pp_item_flags { PP_ITEM_TAIL = 1, PP_ITEM_FP16 = 2 };
 
-/* One row that reaches the FP16 tails, with its plug range [plug_lo, plug_hi). */
+/* Rows that reach the FP16 tails.  PP_ITEM_TAIL: one row, decoded element by element,
+ * with its plug range [plug_lo, plug_hi).  PP_ITEM_FP16 (dual stream only): 1..8 rows
+ * wholly past n_codes that, for each model, lie wholly inside or wholly past its tail;
+ * they need n_codes % 8 == 0, K % 8 == 0 and 16-byte aligned tails. */
 typedef struct pp_quad_item {
   int32_t proj;            /* index into projs */
-  int32_t row0;            /* the row */
-  int32_t nrows;           /* 1 */
-  int32_t flags;           /* PP_ITEM_TAIL */
+  int32_t row0;            /* first row */
+  int32_t nrows;           /* 1 (PP_ITEM_TAIL) or 1..8 (PP_ITEM_FP16) */
+  int32_t flags;           /* PP_ITEM_TAIL or PP_ITEM_FP16 */
   int64_t plug_lo;
   int64_t plug_hi;
 } pp_quad_item;
@@ -227,6 +231,11 @@ int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk, int64_t c_
  * Positions >= n_codes come from the per-model fp16 tails (tails[m], tail_len[m]): a
  * build-defined extension for streams whose models have different lengths (the file
  * format itself zero-pads the shorter model).
+ * The segments' tasks (runs of pp_dual_stream_rows(M) rows, in stream order) are
+ * numbered 0 .. n_tasks-1; segs[i].task0 is the number of the segment's first task and
+ * task_plug[2t], task_plug[2t+1] are the first plug entry at or after task t's first
+ * position and the first one past its last position.  plug_windows (1 or 2) is the
+ * number of 64-entry plug windows each decode step takes (2 for dense plug tables).
  * Replaces the per-projection polar_dual_bitpacked calls of a decode step
  * (polar_kernels.py:98-115) and the decode of unpack_dual_models
  * (polar_bitpack.py:194-260).
@@ -247,6 +256,7 @@ int64_t pp_dual_stream_waves(int64_t M);
 
 int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs,
                    const pp_quad_seg* segs, int64_t n_segs, const int64_t* seg_bounds, int64_t n_waves,
+                   const int64_t* task_plug, int64_t n_tasks, int plug_windows,
                    const pp_quad_item* tail_items, int64_t n_tail,
                    int code_layout, const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
                    const float* amp_lut, const float* cos_lut, const float* sin_lut,

@@ -15,6 +15,7 @@ PP_OK, PP_EINVAL, PP_EHIP, PP_ENOSUPPORT = 0, 1, 2, 3
 PP_F16, PP_F32 = 0, 1
 PP_DUAL_I16_OFFSET, PP_DUAL_U16_BE = 0, 1
 PP_ITEM_TAIL = 1
+PP_ITEM_FP16 = 2
 
 vp = C.c_void_p
 i64 = C.c_int64
@@ -35,7 +36,7 @@ class QuadItem(C.Structure):
 
 class QuadSeg(C.Structure):
     """``pp_quad_seg`` (include/polar_pack.h)."""
-    _fields_ = [("proj", C.c_int32), ("row0", C.c_int32), ("row1", C.c_int32), ("flags", C.c_int32),
+    _fields_ = [("proj", C.c_int32), ("row0", C.c_int32), ("row1", C.c_int32), ("task0", C.c_int32),
                 ("plug_lo", i64)]
 
 
@@ -58,7 +59,7 @@ EXPORTS = {
     "pp_quad_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, vp, vp, vp, i64, i64, vp, vp, i64, vp]),
     "pp_dual_stream_rows": (i32, [i64]),
     "pp_dual_stream_waves": (i64, [i64]),
-    "pp_dual_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, i32, vp, i64, i64, i64, vp, vp, vp, vp, vp, i64,
+    "pp_dual_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, i32, vp, i64, i32, vp, i64, i64, i64, vp, vp, vp, vp, vp, i64,
                              i64, vp, vp, i64, vp]),
     "pp_dual_gemm": (i32, [vp, i64, i64, vp, i32, i64, i64, vp, i64, i64, vp, i32, vp, vp, i32, i32,
                            vp, vp, i64, i64, vp, vp, i64, i64, i64, i64, i64, vp, i64, vp]),

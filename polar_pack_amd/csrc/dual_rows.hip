@@ -11,8 +11,8 @@
 //
 // Same structure as quad_rows.hip: one workgroup per CU, wavefronts walk segments (runs of
 // full rows of one projection) in tasks of RG rows and chunks of 512 pairs, the next chunk
-// in flight while one is decoded, plug corrections / reduction / stores of a task done in
-// the first step of the next.  Per lane and row a chunk is one 16-byte load (8 pairs that
+// in flight while one is decoded, reduction / stores of a task done in the first step of
+// the next.  Plug corrections go through a three-stage window pipeline (below).  Per lane and row a chunk is one 16-byte load (8 pairs that
 // share one group scale, so the scale multiplies a per-lane partial sum once per 8 pairs)
 // and one 2-byte scale load.
 //
@@ -25,12 +25,18 @@
 namespace pp {
 
 constexpr int DPAIRS = 512;                    // pairs per wave per row per chunk (64 lanes x 8)
-constexpr uint32_t DLDS_CS = 0;                // (cos, sin) rows: phase p at p*128 + 8*(lane % 16)
-constexpr uint32_t DLDS_AMP = 0x20000;         // amplitude rows: a at DLDS_AMP + a*128 + 4*(lane % 32)
-constexpr uint32_t DLDS_BYTES = 0x20000 + 64 * 128;
+constexpr uint32_t DLDS_AMP = 0;               // the 64 amplitudes, 4 bytes each: one per LDS bank
+constexpr uint32_t DLDS_CS = 0x400;            // (cos, sin) rows: phase p at DLDS_CS + p*128 + 8*(lane % 16)
+constexpr uint32_t DLDS_BYTES = 0x400 + 1024 * 128;
 
 template <int MT> struct DualCfg;
-template <> struct DualCfg<1> { static constexpr int RG = 8, NT = 512; };
+#ifndef PP_DUAL1_RG
+#define PP_DUAL1_RG 8
+#endif
+#ifndef PP_DUAL1_NT
+#define PP_DUAL1_NT 512
+#endif
+template <> struct DualCfg<1> { static constexpr int RG = PP_DUAL1_RG, NT = PP_DUAL1_NT; };
 template <> struct DualCfg<2> { static constexpr int RG = 4, NT = 512; };
 template <> struct DualCfg<4> { static constexpr int RG = 2, NT = 512; };
 
@@ -48,6 +54,8 @@ struct DualStreamArgs {
   const uint32_t* plug_idx;
   const f16* plug_amp;
   int64_t plug_n;
+  const int64_t* task_plug;   // per task: first plug entry in its rows, first entry past them
+  int64_t n_tasks;
   int M;
 };
 
@@ -65,23 +73,37 @@ __device__ __forceinline__ uint32_t dual_half(uint32_t h16) {
 }
 
 struct DualLane {
-  uint32_t cs, amp;   // lane offsets inside a row
+  uint32_t cs;        // the lane's replica inside a (cos, sin) row
 };
 
 __device__ __forceinline__ DualLane dual_lane(int l) {
   DualLane o;
-  o.cs = DLDS_CS | (8u * (l & 15));
-  o.amp = DLDS_AMP | (4u * (l & 31));
+  o.cs = 8u * (l & 15);
   return o;
 }
 
-// Table values of the code in the low 16 bits (H = 0) or the high 16 bits (H = 1) of w.
-template <int H>
-__device__ __forceinline__ void dual_lookup(const char* lds, uint32_t w, const DualLane& o, float& an, float2& cs) {
-  const uint32_t a_cs = (H ? ((w >> 9) & 0x1FF80u) : ((w << 7) & 0x1FF80u)) | o.cs;
-  const uint32_t a_amp = (H ? ((w >> 19) & 0x1F80u) : ((w >> 3) & 0x1F80u)) | o.amp;
-  an = *reinterpret_cast<const float*>(lds + a_amp);
-  cs = *reinterpret_cast<const float2*>(lds + a_cs);
+// Amplitude and (cos, sin) of both codes of a stored 32-bit word.  The amplitude table
+// needs no replicas (a wave's 64 reads hit distinct banks or share one address), so its
+// byte offset, 4 * amp bits, comes straight out of the stored word: byte 0 / byte 2 of
+// a big-endian word, byte 1 / byte 3 of the int16 layout, masked with 0xFC.
+template <int LAYOUT>
+__device__ __forceinline__ void dual_lookup2(const char* lds, uint32_t raw, const DualLane& o, float (&an)[2],
+                                             float2 (&cs)[2]) {
+  const uint32_t a0 = (LAYOUT == PP_DUAL_U16_BE ? raw : raw >> 8) & 0xFCu;
+  const uint32_t a1 = (raw >> (LAYOUT == PP_DUAL_U16_BE ? 16 : 24)) & 0xFCu;
+  const uint32_t w = dual_word<LAYOUT>(raw);
+  const uint32_t c0 = ((w << 7) & 0x1FF80u) | o.cs;
+  const uint32_t c1 = ((w >> 9) & 0x1FF80u) | o.cs;
+  an[0] = *reinterpret_cast<const float*>(lds + DLDS_AMP + a0);
+  an[1] = *reinterpret_cast<const float*>(lds + DLDS_AMP + a1);
+  cs[0] = *reinterpret_cast<const float2*>(lds + DLDS_CS + c0);
+  cs[1] = *reinterpret_cast<const float2*>(lds + DLDS_CS + c1);
+}
+
+// The same for one code in the table-index form (amp bits 10..15, phase 0..9).
+__device__ __forceinline__ void dual_lookup1(const char* lds, uint32_t c, const DualLane& o, float& an, float2& cs) {
+  an = *reinterpret_cast<const float*>(lds + DLDS_AMP + ((c >> 8) & 0xFCu));
+  cs = *reinterpret_cast<const float2*>(lds + DLDS_CS + (((c << 7) & 0x1FF80u) | o.cs));
 }
 
 template <int LAYOUT>
@@ -90,16 +112,14 @@ __device__ __forceinline__ void dual_build_lds(char* lds, const DualStreamArgs& 
     const int p = i >> 4, j = i & 15;
     *reinterpret_cast<float2*>(lds + DLDS_CS + p * 128 + 8 * j) = make_float2(A.cos_lut[p], A.sin_lut[p]);
   }
-  for (int i = threadIdx.x; i < 64 * 32; i += blockDim.x) {
-    const int a = i >> 5, j = i & 31;
-    const int src = LAYOUT == PP_DUAL_I16_OFFSET ? (a ^ 32) : a;
-    *reinterpret_cast<float*>(lds + DLDS_AMP + a * 128 + 4 * j) = A.amp_lut[src];
-  }
+  // the int16 layout stores code ^ 0x8000: entry a holds amplitude a ^ 32
+  for (int a = threadIdx.x; a < 64; a += blockDim.x)
+    *reinterpret_cast<float*>(lds + DLDS_AMP + 4 * a) = A.amp_lut[LAYOUT == PP_DUAL_I16_OFFSET ? (a ^ 32) : a];
 }
 
 // Uniform state of a segment.
 struct DualSeg {
-  rsrc_t rx;
+  rsrc_t rx, rcs;      // activations; the segment's codes
   const uint16_t* codes;
   const f16* x;
   int64_t pos0;        // stream position of the segment's first row
@@ -175,14 +195,18 @@ __device__ __forceinline__ void dchunk_compute(const char* lds, const DualLane& 
   }
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
-    const uint32_t w4[4] = {dual_word<LAYOUT>(c.q[r].x), dual_word<LAYOUT>(c.q[r].y), dual_word<LAYOUT>(c.q[r].z),
-                            dual_word<LAYOUT>(c.q[r].w)};
+    const uint32_t w4[4] = {c.q[r].x, c.q[r].y, c.q[r].z, c.q[r].w};
     float an[8];
     float2 cs[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      dual_lookup<0>(lds, w4[e], lo, an[2 * e], cs[2 * e]);
-      dual_lookup<1>(lds, w4[e], lo, an[2 * e + 1], cs[2 * e + 1]);
+      float a2[2];
+      float2 c2[2];
+      dual_lookup2<LAYOUT>(lds, w4[e], lo, a2, c2);
+      an[2 * e] = a2[0];
+      an[2 * e + 1] = a2[1];
+      cs[2 * e] = c2[0];
+      cs[2 * e + 1] = c2[1];
     }
     float l1[MT], l2[MT];
 #pragma unroll
@@ -204,116 +228,101 @@ __device__ __forceinline__ void dchunk_compute(const char* lds, const DualLane& 
   }
 }
 
-// Plug entries of a task (the same in-order consumption as the quad kernel).
-template <int MT>
-struct DPlug {
-  uint32_t idx;      // position of entry pc + lane
-  int row;           // row in the task, -1 when none
-  uint32_t code;     // stored 16-bit code at the entry
-  uint32_t sc;       // its group scale (fp16 bits)
-  uint32_t pa;       // plug amplitude (fp16 bits)
-  uint32_t xk[MT];   // x at its column (fp16 bits)
-  bool dense;
+// Plug entries.  The host gives every task its plug range [tlo, thi): the entries whose
+// positions lie in the task's rows.  Step ck of a task takes the window of entries
+// tlo + 64*PW*ck .. +64*PW (one entry per lane and window, filled from the front); a
+// task with more entries than its steps can take corrects the rest when it finishes.
+// A window passes through three stages, one step apart, so that every load is issued a
+// step before the step that reads it and the number of loads per step is fixed:
+//   step s-2: the entries' positions;
+//   step s-1: the stored code, the group scale, the plug amplitude and x at each entry;
+//   step s:   acc[row] += (plug amp - amp_lut[aq] * scale) * x * (cos, sin)(phase).
+// Lanes without an entry load nothing (reads of 0 make their correction 0).
+
+// Uniform description of the window of one step: its task, its first entry and the
+// number of the task's entries from there on (the window takes up to 64*PW of them).
+struct DSlot {
+  int ti;
+  int rem;
+  int64_t lo;
 };
 
-__device__ __forceinline__ rsrc_t dplug_rsrc(const void* base, int64_t plug_n, int64_t pc, int esize) {
-  const int64_t left = plug_n - pc;
-  const uint32_t bytes = left <= 0 ? 0u : (uint32_t)std::min<int64_t>(left * esize, 0x7FFFFFF0);
-  return make_rsrc(reinterpret_cast<const char*>(base) + (left > 0 ? pc : 0) * esize, bytes);
+template <int PW>
+__device__ __forceinline__ int dslot_cnt(const DSlot& s) {
+  return s.rem < 64 * PW ? s.rem : 64 * PW;
 }
 
-template <int RG>
-__device__ __forceinline__ int dplug_locate(int64_t pos, int64_t tpos0, int ldc, int K, int nr, int& k) {
-  const int64_t off = pos - tpos0;
-  int row = 0;
+template <int MT, int PW>
+struct DWin {
+  uint32_t code[PW], sc[PW], pa[PW];   // stored code, group scale, plug amplitude (16 bits)
+  uint32_t xk[PW][MT];                 // x at the entry's column (fp16 bits)
+  int q[PW];                           // row of the entry in its task, -1 for none
+};
+
+// Stage 1: the positions of the window's entries.
+template <int PW>
+__device__ __forceinline__ void dwin_positions(const DualStreamArgs& A, const DSlot& t, int lane, uint32_t (&idx)[PW]) {
+  const int cnt = dslot_cnt<PW>(t);
+  const uint32_t base = 4u * (uint32_t)t.lo;
 #pragma unroll
-  for (int r = 1; r < RG; ++r)
-    if (off >= (int64_t)r * ldc) row = r;
-  k = (int)(off - (int64_t)row * ldc);
-  return (off >= 0 && row < nr && k < K) ? row : -1;
+  for (int w = 0; w < PW; ++w)
+    vload32(idx[w], 64 * w + lane < cnt ? base + 4u * (uint32_t)(64 * w + lane) : OOB,
+            make_rsrc(A.plug_idx, 4u * (uint32_t)A.plug_n));
 }
 
-template <int MT, int RG, int SM>
-__device__ __forceinline__ void dplug_begin(const DualStreamArgs& A, const DualSeg& S, int ti, int lane, int64_t& pc,
-                                            DPlug<MT>& P) {
-  const int64_t tpos0 = S.pos0 + (int64_t)ti * RG * S.ldc;
-  const int nr = min(RG, S.nrows - ti * RG);
-  const int64_t tend = tpos0 + (int64_t)nr * S.ldc;
-  const bool in = (pc + lane < A.plug_n) && ((int64_t)P.idx < tend);
-  const int cnt = __popcll(__ballot(in));
-  int k = 0;
-  const int row = in ? dplug_locate<RG>((int64_t)P.idx, tpos0, S.ldc, S.K, nr, k) : -1;
-  P.row = row;
-  const bool v = row >= 0;
-  const int64_t first = (int64_t)ti * RG * S.ldc;
-  const int64_t end = (int64_t)(S.nrows - 1) * S.ldc + S.K;
-  const rsrc_t rc = make_rsrc(S.codes + first, 2u * (uint32_t)(end - first));
-  vload16(P.code, v ? 2u * (uint32_t)(row * S.ldc + k) : OOB, rc);
-  const uint32_t g = dual_group<SM>(A, tpos0 + (int64_t)row * S.ldc + k);
-  vload16(P.sc, v ? 2u * g : OOB, make_rsrc(A.scales, 2u * (uint32_t)A.n_groups));
-  vload16(P.pa, in ? 2u * lane : OOB, dplug_rsrc(A.plug_amp, A.plug_n, pc, 2));
+// Stage 2: per entry its row in the task, and the loads its correction needs.
+template <int MT, int RG, int PW, int SM>
+__device__ __forceinline__ void dwin_data(const DualStreamArgs& A, const DualSeg& S, const DSlot& t,
+                                          const uint32_t (&idx)[PW], int lane, DWin<MT, PW>& W) {
+  const int cnt = dslot_cnt<PW>(t);
+  const int64_t trow0 = (int64_t)t.ti * RG * S.ldc;        // task start, pairs from the segment start
+  const int64_t tpos0 = S.pos0 + trow0;
+  const int64_t span = (int64_t)min(RG, S.nrows - t.ti * RG) * S.ldc;
+  const rsrc_t rs = make_rsrc(A.scales, 2u * (uint32_t)A.n_groups);
+  const uint32_t pbase = 2u * (uint32_t)t.lo;
 #pragma unroll
-  for (int j = 0; j < MT; ++j) vload16(P.xk[j], (v && j < A.M) ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
-  P.dense = cnt == 64;
-  pc += cnt;
-  vload32(P.idx, 4u * lane, dplug_rsrc(A.plug_idx, A.plug_n, pc, 4));
+  for (int w = 0; w < PW; ++w) {
+    const int e = 64 * w + lane;
+    const int64_t off = (int64_t)idx[w] - tpos0;
+    bool v = e < cnt && off >= 0 && off < span;
+    const int o = v ? (int)off : 0;
+    int row = 0;
+#pragma unroll
+    for (int r = 1; r < RG; ++r)
+      if (o >= r * S.ldc) row = r;
+    const int k = o - row * S.ldc;
+    v = v && k < S.K;
+    W.q[w] = v ? row : -1;
+    vload16(W.code[w], v ? 2u * (uint32_t)(trow0 + o) : OOB, S.rcs);
+    vload16(W.sc[w], v ? 2u * dual_group<SM>(A, (int64_t)idx[w]) : OOB, rs);
+    vload16(W.pa[w], v ? pbase + 2u * (uint32_t)e : OOB, make_rsrc(A.plug_amp, 2u * (uint32_t)A.plug_n));
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+      vload16(W.xk[w][j], (v && j < A.M) ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
+  }
 }
 
-// Correction of one entry: the amplitude amp_lut[aq]*scale is replaced by the plug value.
-template <int MT, int RG, int LAYOUT>
-__device__ __forceinline__ void dplug_correct(const char* lds, const DualLane& lo, int row, uint32_t code16,
-                                              float sc, float pa, const float (&xk)[MT], float (&acc)[RG][2][MT]) {
-  float an;
-  float2 cs;
-  dual_lookup<0>(lds, dual_half<LAYOUT>(code16), lo, an, cs);
-  const float d = pa - an * sc;
+// Stage 3: the corrections.
+template <int MT, int RG, int PW, int LAYOUT>
+__device__ __forceinline__ void dwin_apply(const char* lds, const DualLane& lo, const DWin<MT, PW>& W,
+                                           float (&acc)[RG][2][MT]) {
 #pragma unroll
-  for (int q = 0; q < RG; ++q) {
-    const float on = q == row ? d : 0.f;
+  for (int w = 0; w < PW; ++w) {
+    float an;
+    float2 cs;
+    dual_lookup1(lds, dual_half<LAYOUT>(W.code[w]), lo, an, cs);
+    const float d = h2f(W.pa[w]) - an * h2f(W.sc[w]);
 #pragma unroll
-    for (int j = 0; j < MT; ++j) {
-      const float t = on * xk[j];
-      acc[q][0][j] = fmaf(t, cs.x, acc[q][0][j]);
-      acc[q][1][j] = fmaf(t, cs.y, acc[q][1][j]);
+    for (int q = 0; q < RG; ++q) {
+      const float on = q == W.q[w] ? d : 0.f;
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        const float t = on * h2f(W.xk[w][j]);
+        acc[q][0][j] = fmaf(t, cs.x, acc[q][0][j]);
+        acc[q][1][j] = fmaf(t, cs.y, acc[q][1][j]);
+      }
     }
   }
-}
-
-template <int MT, int RG, int LAYOUT, int SM>
-__device__ __forceinline__ void dplug_end(const char* lds, const DualLane& lo, const DualStreamArgs& A,
-                                          const DualSeg& S, int ti, int lane, int64_t& pc, DPlug<MT>& P,
-                                          float (&acc)[RG][2][MT]) {
-  if (P.row >= 0) {
-    float xk[MT];
-#pragma unroll
-    for (int j = 0; j < MT; ++j) xk[j] = h2f(P.xk[j]);
-    dplug_correct<MT, RG, LAYOUT>(lds, lo, P.row, P.code, h2f(P.sc), h2f(P.pa), xk, acc);
-  }
-  if (!P.dense) return;
-  const int64_t tpos0 = S.pos0 + (int64_t)ti * RG * S.ldc;
-  const int nr = min(RG, S.nrows - ti * RG);
-  const int64_t tend = tpos0 + (int64_t)nr * S.ldc;
-  for (;;) {
-    const int64_t q = pc + lane;
-    const bool has = q < A.plug_n;
-    const int64_t pos = has ? (int64_t)A.plug_idx[q] : tend;
-    const bool in = pos < tend;
-    const int cnt = __popcll(__ballot(in));
-    int k = 0;
-    const int row = in ? dplug_locate<RG>(pos, tpos0, S.ldc, S.K, nr, k) : -1;
-    if (row >= 0) {
-      float xk[MT];
-#pragma unroll
-      for (int j = 0; j < MT; ++j) xk[j] = j < A.M ? (float)S.x[(int64_t)j * S.x_sm + k] : 0.f;
-      const uint32_t code = S.codes[(int64_t)(ti * RG + row) * S.ldc + k];
-      const float sc = (float)A.scales[dual_group<SM>(A, pos)];
-      dplug_correct<MT, RG, LAYOUT>(lds, lo, row, code, sc, (float)A.plug_amp[q], xk, acc);
-    }
-    pc += cnt;
-    if (cnt < 64) break;
-  }
-  vload32(P.idx, 4u * lane, dplug_rsrc(A.plug_idx, A.plug_n, pc, 4));
-  asm volatile("" : : "v"(P.idx));   // wait here, not at the next (common) use
 }
 
 template <int MT, int RG>
@@ -350,23 +359,27 @@ __device__ __forceinline__ void dzero(float (&acc)[RG][2][MT]) {
     for (int j = 0; j < MT; ++j) acc[r][0][j] = acc[r][1][j] = 0.f;
 }
 
-template <int MT, int RG, int LAYOUT, int SM>
+template <int MT, int RG, int PW, int LAYOUT, int SM>
 struct DualRunner {
   const char* lds;
   DualLane lo;
   const DualStreamArgs& A;
   const DualSeg& S;
-  int lane, nck, ntask;
+  int lane, nck, ntask, task0;
   uint32_t voff[RG];
   float acc[RG][2][MT];
   float pend[RG][2][MT];
   int pend_ti;
-  DPlug<MT> P;
-  int64_t pc;
-  Cursor lc;
+  DSlot pend_left;           // entries of the parked task left after its last step
+  Cursor lc;                 // chunk to prefetch
+  DSlot s0, s1, s2;          // windows of steps s, s+1, s+2 (s = the step being computed)
+  Cursor c3;                 // step s+3, whose task plug range is in flight
+  u32x4 T;                   // that range: {tlo lo, tlo hi, thi lo, thi hi}
+  uint32_t I[PW];            // positions of the entries of step s+1's window
+  DWin<MT, PW> D;            // data of step s's window
 
-  __device__ __forceinline__ DualRunner(const char* l, const DualStreamArgs& a, const DualSeg& s, int64_t plug_lo)
-      : lds(l), A(a), S(s), pend_ti(-1), pc(plug_lo) {
+  __device__ __forceinline__ DualRunner(const char* l, const DualStreamArgs& a, const DualSeg& s, int t0)
+      : lds(l), A(a), S(s), task0(t0), pend_ti(-1) {
     lane = threadIdx.x & 63;
     lo = dual_lane(lane);
     nck = (S.K + DPAIRS - 1) / DPAIRS;
@@ -383,6 +396,27 @@ struct DualRunner {
       ++c.ti;
     }
   }
+  // Cursor for the plug windows: stops one task past the end (empty windows).
+  __device__ __forceinline__ void advance_slot(Cursor& c) const {
+    if (c.ti < ntask) advance(c);
+  }
+
+  __device__ __forceinline__ void load_range(const Cursor& c, u32x4& t) const {
+    vload128(t, c.ti < ntask ? 16u * (uint32_t)(task0 + c.ti) : OOB,
+             make_rsrc(A.task_plug, 16u * (uint32_t)A.n_tasks));
+  }
+  __device__ __forceinline__ DSlot slot_of(const Cursor& c, const u32x4& t) const {
+    const int64_t tlo =
+        (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane(t.y) << 32) | __builtin_amdgcn_readfirstlane(t.x));
+    const int64_t thi =
+        (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane(t.w) << 32) | __builtin_amdgcn_readfirstlane(t.z));
+    DSlot s;
+    s.ti = c.ti;
+    s.lo = tlo + (int64_t)(64 * PW) * c.ck;
+    const int64_t r = thi - s.lo;
+    s.rem = r <= 0 ? 0 : r >= 0x7FFFFFFF ? 0x7FFFFFFF : (int)r;
+    return s;
+  }
 
   __device__ __forceinline__ void prefetch(DChunk<MT, RG>& c) {
     dchunk_issue<MT, RG, SM>(A, S, lc.ti * RG, lc.ck * DPAIRS, voff, lane, c);
@@ -391,20 +425,31 @@ struct DualRunner {
     if (nx.ti < ntask) lc = nx;
   }
 
+  // Entries of the finished task that its steps could not take, then its outputs.
   __device__ __forceinline__ void finish_pending() {
-    dplug_end<MT, RG, LAYOUT, SM>(lds, lo, A, S, pend_ti, lane, pc, P, pend);
+    for (DSlot t = pend_left; t.rem > 0; t.lo += 64 * PW, t.rem -= 64 * PW) {
+      uint32_t idx[PW];
+      DWin<MT, PW> W;
+      dwin_positions<PW>(A, t, lane, idx);
+      dwin_data<MT, RG, PW, SM>(A, S, t, idx, lane, W);
+      dwin_apply<MT, RG, PW, LAYOUT>(lds, lo, W, pend);
+    }
     dtask_write<MT, RG>(A, S, pend_ti, lane, pend);
     pend_ti = -1;
   }
 
-  // prefetch | [first chunk] finish the previous task, this task's plug loads | decode |
-  // [last chunk] park the sums (see SegRunner in quad_rows.hip)
+  // prefetch | range of step s+2, range load for s+3 | corrections of step s | data loads
+  // for s+1 | positions for s+2 | [first chunk] finish the previous task | decode |
+  // [last chunk] park the sums
   __device__ __forceinline__ bool step(Cursor& cur, DChunk<MT, RG>& comp, DChunk<MT, RG>& pref) {
     prefetch(pref);
-    if (cur.ck == 0) {
-      if (pend_ti >= 0) finish_pending();
-      dplug_begin<MT, RG, SM>(A, S, cur.ti, lane, pc, P);
-    }
+    s2 = slot_of(c3, T);
+    advance_slot(c3);
+    load_range(c3, T);
+    if (dslot_cnt<PW>(s0) > 0) dwin_apply<MT, RG, PW, LAYOUT>(lds, lo, D, acc);
+    dwin_data<MT, RG, PW, SM>(A, S, s1, I, lane, D);
+    dwin_positions<PW>(A, s2, lane, I);
+    if (cur.ck == 0 && pend_ti >= 0) finish_pending();
     dchunk_compute<MT, RG, LAYOUT>(lds, lo, comp, acc);
     if (cur.ck == nck - 1) {
 #pragma unroll
@@ -415,16 +460,34 @@ struct DualRunner {
           for (int j = 0; j < MT; ++j) pend[r][m][j] = acc[r][m][j];
       dzero<MT, RG>(acc);
       pend_ti = cur.ti;
+      pend_left = s0;
+      pend_left.lo += 64 * PW;
+      pend_left.rem = s0.rem > 64 * PW ? s0.rem - 64 * PW : 0;
     }
+    s0 = s1;
+    s1 = s2;
     advance(cur);
     return cur.ti < ntask;
   }
 
   __device__ __forceinline__ void run() {
     if (ntask <= 0 || S.K <= 0) return;
+    // fill the window stages for steps 0 and 1, the range of step 2 in flight
+    Cursor c = {0, 0};
+    load_range(c, T);
+    s0 = slot_of(c, T);
+    advance_slot(c);
+    load_range(c, T);
+    s1 = slot_of(c, T);
+    dwin_positions<PW>(A, s0, lane, I);
+    dwin_data<MT, RG, PW, SM>(A, S, s0, I, lane, D);
+    dwin_positions<PW>(A, s1, lane, I);
+    c3 = c;
+    advance_slot(c3);
+    load_range(c3, T);
+    // c3 now names step 2; step() turns T into s2 and moves c3 to step 3
     DChunk<MT, RG> c0, c1;
     Cursor cur = {0, 0};
-    vload32(P.idx, 4u * lane, dplug_rsrc(A.plug_idx, A.plug_n, pc, 4));
     prefetch(c0);
     for (;;) {
       if (!step(cur, c0, c1)) break;
@@ -446,12 +509,13 @@ __device__ __forceinline__ void dual_seg(const pp_dual_proj& P, int row0, int ro
   S.codes = reinterpret_cast<const uint16_t*>(uniform_ptr(P.codes)) + (int64_t)row0 * ldc;
   S.x = reinterpret_cast<const f16*>(uniform_ptr(P.x));
   S.rx = make_rsrc(S.x, 2u * (uint32_t)((M - 1) * S.x_sm + K));
+  S.rcs = make_rsrc(S.codes, 2u * (uint32_t)((int64_t)(S.nrows - 1) * ldc + K));
 #pragma unroll
   for (int m = 0; m < 2; ++m) S.out[m] = reinterpret_cast<f16*>(uniform_ptr(P.out[m])) + row0;
   S.o_sm = uniform64(P.o_sm);
 }
 
-template <int MT, int LAYOUT, int SM>
+template <int MT, int PW, int LAYOUT, int SM>
 __global__ __launch_bounds__(DualCfg<MT>::NT) void dual_stream_kernel(const DualStreamArgs A) {
   constexpr int RG = DualCfg<MT>::RG, WAVES = DualCfg<MT>::NT / 64;
   __shared__ __attribute__((aligned(16))) uint32_t T[DLDS_BYTES / 4];
@@ -464,7 +528,7 @@ __global__ __launch_bounds__(DualCfg<MT>::NT) void dual_stream_kernel(const Dual
     const pp_quad_seg g = A.segs[si];
     DualSeg S;
     dual_seg(A.projs[uniform(g.proj)], g.row0, g.row1, A.M, S);
-    DualRunner<MT, RG, LAYOUT, SM> R(lds, A, S, uniform64(g.plug_lo));
+    DualRunner<MT, RG, PW, LAYOUT, SM> R(lds, A, S, uniform(g.task0));
     R.run();
   }
 }
@@ -481,9 +545,92 @@ struct DualTailArgs {
   int64_t tail_len[2];
 };
 
-// A row that reaches the FP16 tails, element by element: positions < n_codes decode
-// from the codes (with the plug entries of the row), positions >= n_codes read
-// tails[m][pos - n_codes] when model m has them.
+// Up to 8 rows that lie wholly past n_codes: for each model either wholly inside its fp16
+// tail (a plain fp16 GEMV, 16-byte loads of 8 weights per lane and row) or wholly past it
+// (outputs 0).  Needs n_codes % 8 == 0, K % 8 == 0 and 16-byte aligned tails, so that
+// every lane's 8 weights are one aligned load.
+template <int MT>
+__device__ __forceinline__ void dual_tail_rows(const DualTailArgs& T, const pp_quad_item& it, int lane) {
+  constexpr int R = 8, NV = R * 2 * MT, LNV = Log2<NV>::v;
+  const pp_dual_proj& P = T.projs[uniform(it.proj)];
+  const int K = uniform(P.K), ldc = uniform((int)P.ldc), nr = uniform(it.nrows), row0 = uniform(it.row0);
+  const int x_sm = uniform((int)P.x_sm), M = T.S.M;
+  const int64_t t0 = uniform64(P.pos0) + (int64_t)row0 * ldc - T.n_codes;   // tail index of (row0, 0)
+  const int64_t t_end = t0 + (int64_t)(nr - 1) * ldc + K;
+  rsrc_t rt[2];
+  bool has[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    has[m] = t0 >= 0 && t_end <= T.tail_len[m];
+    rt[m] = make_rsrc(has[m] ? T.tails[m] + t0 : nullptr, has[m] ? 2u * (uint32_t)(t_end - t0) : 0u);
+  }
+  const rsrc_t rx = make_rsrc(uniform_ptr(P.x), 2u * (uint32_t)((M - 1) * x_sm + K));
+  float acc[R][2][MT];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) acc[r][m][j] = 0.f;
+  for (int kc = 0; kc < K; kc += 512) {
+    const int k = kc + 8 * lane;
+    const bool kin = k < K;
+    u32x4 xr[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) vload128(xr[j], (kin && j < M) ? 2u * (uint32_t)(j * x_sm + k) : OOB, rx);
+    u32x4 wr[R][2];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+        vload128(wr[r][m], (kin && r < nr) ? 2u * (uint32_t)(r * ldc + k) : OOB, rt[m]);
+    float xv[MT][8];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      const f16x4 h0 = __builtin_bit_cast(f16x4, u32x2{xr[j].x, xr[j].y});
+      const f16x4 h1 = __builtin_bit_cast(f16x4, u32x2{xr[j].z, xr[j].w});
+      xv[j][0] = (float)h0.x; xv[j][1] = (float)h0.y; xv[j][2] = (float)h0.z; xv[j][3] = (float)h0.w;
+      xv[j][4] = (float)h1.x; xv[j][5] = (float)h1.y; xv[j][6] = (float)h1.z; xv[j][7] = (float)h1.w;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const f16x4 h0 = __builtin_bit_cast(f16x4, u32x2{wr[r][m].x, wr[r][m].y});
+        const f16x4 h1 = __builtin_bit_cast(f16x4, u32x2{wr[r][m].z, wr[r][m].w});
+        const float wv[8] = {(float)h0.x, (float)h0.y, (float)h0.z, (float)h0.w,
+                             (float)h1.x, (float)h1.y, (float)h1.z, (float)h1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+          for (int j = 0; j < MT; ++j) acc[r][m][j] = fmaf(wv[e], xv[j][e], acc[r][m][j]);
+      }
+  }
+  float v[NV];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) v[(r * 2 + m) * MT + j] = acc[r][m][j];
+  const float y = wave_transpose_reduce<LNV>(v, lane);
+  const int idx = lane >> (6 - LNV);
+  const int r = idx / (2 * MT), m = (idx / MT) & 1, j = idx % MT;
+  const bool wr_ = (lane & ((1 << (6 - LNV)) - 1)) == 0 && r < nr && j < M;
+  const int64_t o_sm = uniform64(P.o_sm);
+  const uint32_t off = 2u * (uint32_t)((int64_t)j * o_sm + row0 + r);
+  const uint32_t obytes = 2u * (uint32_t)((int64_t)(M - 1) * o_sm + P.N);
+  const f16 h = (f16)y;
+#pragma unroll
+  for (int mm = 0; mm < 2; ++mm)
+    vstore16((uint32_t)__builtin_bit_cast(unsigned short, h), (wr_ && m == mm) ? off : OOB,
+             make_rsrc(uniform_ptr(P.out[mm]), obytes));
+}
+
+// Rows that reach the FP16 tails.  PP_ITEM_FP16 items: see dual_tail_rows.  Other items
+// (one row each, straddling n_codes or the end of a model's tail) element by element:
+// positions < n_codes decode from the codes (with the plug entries of the row),
+// positions >= n_codes read tails[m][pos - n_codes] when model m has them.
 template <int MT, int LAYOUT, int SM>
 __global__ __launch_bounds__(256) void dual_tail_kernel(const DualTailArgs T) {
   const int64_t ti = (int64_t)blockIdx.x * 4 + uniform(threadIdx.x >> 6);
@@ -491,6 +638,10 @@ __global__ __launch_bounds__(256) void dual_tail_kernel(const DualTailArgs T) {
   const DualStreamArgs& A = T.S;
   const int lane = threadIdx.x & 63;
   const pp_quad_item it = T.items[ti];
+  if (uniform(it.flags) & PP_ITEM_FP16) {
+    dual_tail_rows<MT>(T, it, lane);
+    return;
+  }
   const pp_dual_proj& P = T.projs[it.proj];
   const int K = P.K;
   const int64_t pos_row = P.pos0 + (int64_t)it.row0 * P.ldc;
@@ -551,19 +702,20 @@ static int dual_stream_rg(int mt) { return mt == 1 ? DualCfg<1>::RG : mt == 2 ? 
 static int dual_stream_nt(int mt) { return mt == 1 ? DualCfg<1>::NT : mt == 2 ? DualCfg<2>::NT : DualCfg<4>::NT; }
 
 template <int MT, int LAYOUT, int SM>
-static int launch_dual_stream(const DualStreamArgs& A, hipStream_t st) {
-  hipLaunchKernelGGL((dual_stream_kernel<MT, LAYOUT, SM>), dim3((unsigned)device_cu_count()), dim3(DualCfg<MT>::NT),
-                     0, st, A);
+static int launch_dual_stream(const DualStreamArgs& A, int pw, hipStream_t st) {
+  const dim3 grid((unsigned)device_cu_count()), block(DualCfg<MT>::NT);
+  if (pw == 1) hipLaunchKernelGGL((dual_stream_kernel<MT, 1, LAYOUT, SM>), grid, block, 0, st, A);
+  else hipLaunchKernelGGL((dual_stream_kernel<MT, 2, LAYOUT, SM>), grid, block, 0, st, A);
   PP_LAUNCH_CHECK();
   return PP_OK;
 }
 
 template <int LAYOUT, int SM>
-static int dispatch_dual_stream(const DualStreamArgs& A, int mt, hipStream_t st) {
+static int dispatch_dual_stream(const DualStreamArgs& A, int mt, int pw, hipStream_t st) {
   switch (mt) {
-    case 1: return launch_dual_stream<1, LAYOUT, SM>(A, st);
-    case 2: return launch_dual_stream<2, LAYOUT, SM>(A, st);
-    default: return launch_dual_stream<4, LAYOUT, SM>(A, st);
+    case 1: return launch_dual_stream<1, LAYOUT, SM>(A, pw, st);
+    case 2: return launch_dual_stream<2, LAYOUT, SM>(A, pw, st);
+    default: return launch_dual_stream<4, LAYOUT, SM>(A, pw, st);
   }
 }
 
@@ -597,7 +749,8 @@ extern "C" int64_t pp_dual_stream_waves(int64_t M) {
 }
 
 extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const pp_quad_seg* segs, int64_t n_segs,
-                              const int64_t* seg_bounds, int64_t n_waves, const pp_quad_item* tail_items,
+                              const int64_t* seg_bounds, int64_t n_waves, const int64_t* task_plug, int64_t n_tasks,
+                              int plug_windows, const pp_quad_item* tail_items,
                               int64_t n_tail, int code_layout, const void* scales, int64_t n_groups,
                               int64_t group_size, int64_t chunk_size, const float* amp_lut, const float* cos_lut,
                               const float* sin_lut, const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n,
@@ -605,6 +758,10 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
                               void* stream) {
   PP_REQUIRE(projs != nullptr && n_projs >= 1, "no projections");
   PP_REQUIRE(n_segs >= 0 && (n_segs == 0 || (segs != nullptr && seg_bounds != nullptr)), "segs / seg_bounds is null");
+  PP_REQUIRE(n_segs == 0 || (task_plug != nullptr && n_tasks >= 1 && n_tasks < (1ll << 27)),
+             "task_plug is null or n_tasks out of range");
+  PP_REQUIRE(plug_windows == 1 || plug_windows == 2, "plug_windows must be 1 or 2");
+  PP_REQUIRE(plug_n < (1ll << 30), "the stream decode takes fewer than 2^30 plug entries");
   PP_REQUIRE(n_tail == 0 || tail_items != nullptr, "tail_items is null");
   PP_REQUIRE(code_layout == PP_DUAL_I16_OFFSET || code_layout == PP_DUAL_U16_BE, "bad code_layout");
   PP_REQUIRE(amp_lut && cos_lut && sin_lut, "lut pointers are null");
@@ -638,13 +795,17 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
   A.plug_idx = plug_idx;
   A.plug_amp = reinterpret_cast<const f16*>(plug_amp);
   A.plug_n = plug_n;
+  A.task_plug = task_plug;
+  A.n_tasks = n_tasks;
   A.M = (int)M;
   const bool be = code_layout == PP_DUAL_U16_BE;
   if (n_segs > 0) {
     int rc;
-    if (be) rc = sm == 0 ? dispatch_dual_stream<PP_DUAL_U16_BE, 0>(A, mt, st) : dispatch_dual_stream<PP_DUAL_U16_BE, 1>(A, mt, st);
-    else rc = sm == 0 ? dispatch_dual_stream<PP_DUAL_I16_OFFSET, 0>(A, mt, st)
-                      : dispatch_dual_stream<PP_DUAL_I16_OFFSET, 1>(A, mt, st);
+    const int pw = plug_windows;
+    if (be) rc = sm == 0 ? dispatch_dual_stream<PP_DUAL_U16_BE, 0>(A, mt, pw, st)
+                         : dispatch_dual_stream<PP_DUAL_U16_BE, 1>(A, mt, pw, st);
+    else rc = sm == 0 ? dispatch_dual_stream<PP_DUAL_I16_OFFSET, 0>(A, mt, pw, st)
+                      : dispatch_dual_stream<PP_DUAL_I16_OFFSET, 1>(A, mt, pw, st);
     if (rc) return rc;
   }
   if (n_tail > 0) {

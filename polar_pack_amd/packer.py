@@ -1,6 +1,6 @@
-"""Device-side packer for whole ``.quadpack`` streams (torch ops on the GPU).
+"""Device-side packers for whole ``.quadpack`` and ``.dualpack`` streams (torch ops on the GPU).
 
-Follows the three passes of pack_quad (quaternion_packer.py:52-132) on device
+:func:`pack_quad_device` follows the three passes of pack_quad (quaternion_packer.py:52-132) on device
 memory: per-model RMS over the common length (float64 accumulation, :59-68),
 global ``r_max = 1.001 * max |w/s|`` (:70-77), then codes and plug entries
 (:90-113).  Two plug selections:
@@ -15,6 +15,9 @@ Codes are computed in float32 like the reference's numpy pass; device
 transcendentals can round differently at exact ties, so a few codes may differ by
 one step from a host pack of the same weights (decode parity is unaffected: the
 decoder is checked on whatever codes the stream holds).
+
+:func:`pack_dual_device` follows pack_dual_models_packed (polar_bitpack.py:93-172)
+chunk by chunk.
 """
 from __future__ import annotations
 
@@ -24,7 +27,7 @@ from typing import List, Sequence
 import numpy as np
 import torch
 
-from .container import QuadPackDevice
+from .container import DualPackDevice, QuadPackDevice
 
 MU = 255.0
 
@@ -150,3 +153,116 @@ def _ref_threshold(models, s, sizes, r_max, plug_cap):
         words, r = quad_codes_f32(parts, r_max)
         errs.append(_rel_err_f64(parts, words, r, r_max).cpu().numpy())
     return float(np.percentile(np.concatenate(errs), (1 - plug_cap) * 100))
+
+
+def _dual_chunk(a: torch.Tensor, b: torch.Tensor, amp_bits: int, num_phases: int, mu: float, gs: int,
+                plug_cap: float, select: str):
+    """One chunk of pack_dual_models_packed (polar_bitpack.py:118-150): float32 polar
+    transform, per-group mu-law amplitude codes (quantize_amplitude_codes, :34-76) and
+    the chunk's plug entries.  Returns (16-bit codes as int32, fp16 scales, plug
+    positions within the chunk, fp16 plug amplitudes)."""
+    levels = 2 ** amp_bits - 1
+    phase_bits = 16 - amp_bits
+    amplitude = torch.sqrt(a * a + b * b)
+    phase = torch.atan2(b, a)
+    phase_idx = torch.remainder(torch.round((phase + math.pi) / (2 * math.pi) * num_phases).to(torch.int64),
+                                num_phases)
+    del phase
+    ol = amplitude.numel()
+    pad = (-ol) % gs
+    g = torch.nn.functional.pad(amplitude, (0, pad)).view(-1, gs)
+    bmax = g.abs().amax(dim=1, keepdim=True)
+    bmax = torch.where(bmax > 1e-10, bmax, torch.ones_like(bmax))
+    norm = g / bmax
+    log_mu = math.log1p(mu)
+    # float32 log1p, then the float64 division by ln(1+mu) (a float64 numpy scalar, :52-53)
+    comp = (torch.sign(norm) * torch.log1p(mu * norm.abs())).double() / log_mu
+    del norm
+    amp_q = torch.round(comp * levels).clamp(0, levels).to(torch.int64)
+    del comp
+    pidx = pval = None
+    n_plug = int(plug_cap * ol)
+    if n_plug > 0:
+        if select == "ref":       # top n_plug by squared amplitude error (:62-74)
+            decoded = torch.expm1(amp_q.double() / levels * log_mu) / mu * bmax.double()
+            err = (amplitude.double() - decoded.reshape(-1)[:ol]) ** 2
+            del decoded
+        elif select == "norm":    # top n_plug by amplitude
+            err = amplitude
+        else:
+            raise ValueError("select must be 'ref' or 'norm'")
+        pidx = torch.topk(err, n_plug, sorted=False).indices
+        del err
+        pidx = torch.sort(pidx).values
+        pval = amplitude[pidx].to(torch.float16)
+    codes = (amp_q.reshape(-1)[:ol] << phase_bits) | phase_idx
+    return codes.to(torch.int32), bmax.reshape(-1).to(torch.float16), pidx, pval
+
+
+def pack_dual_device(w1: torch.Tensor, w2: torch.Tensor, *, plug_cap: float = 0.03, select: str = "ref",
+                     amp_bits: int = 6, num_phases: int = 1024, mu: float = 255.0, group_size: int = 32,
+                     chunk_size: int = 50_000_000, tails: bool = False, layout: str = "u16be") -> DualPackDevice:
+    """Pack two flat weight streams (any float dtype, on any torch device) as
+    pack_dual_models_packed does (polar_bitpack.py:93-172), chunk by chunk.
+
+    ``tails=False`` is the ``.dualpack`` format: ``n_pairs = max(n1, n2)`` and the
+    shorter model is zero-padded (:113-117).  ``tails=True`` is this build's
+    extension: codes cover the common length rounded down to a multiple of 8
+    (``8 * (min(n1, n2) // 8)``, so that tail rows can be read with aligned 16-byte
+    loads) and each model's remaining weights are kept as its fp16 tail.
+
+    ``select="ref"`` is the reference's plug rule, the top ``int(plug_cap * L)``
+    pairs of each chunk of L pairs by squared amplitude error; ``select="norm"``
+    takes the top pairs by amplitude instead.  Codes come from float32 device
+    transcendentals: a code can differ by one step from a host pack of the same
+    weights at an exact rounding tie, and tied plug candidates may be chosen
+    differently (the decode is checked on whatever the stream holds).
+    ``layout`` is ``"u16be"`` (the file's big-endian 16-bit words) or ``"i16"``
+    (the kernel layout, code - 32768).
+    """
+    if w1.dim() != 1 or w2.dim() != 1 or w1.device != w2.device:
+        raise ValueError("w1 and w2 must be flat tensors on one device")
+    if amp_bits > 6 or 16 - amp_bits > 10 or (1 << (16 - amp_bits)) < num_phases:
+        raise ValueError("codes are 6-bit amplitude + 10-bit phase")
+    if group_size < 1 or chunk_size < 1:
+        raise ValueError("group_size and chunk_size must be positive")
+    if layout not in ("u16be", "i16"):
+        raise ValueError("layout must be 'u16be' or 'i16'")
+    n1, n2 = int(w1.numel()), int(w2.numel())
+    n = 8 * (min(n1, n2) // 8) if tails else max(n1, n2)
+    if n >= 2 ** 32:
+        raise ValueError("plug positions are uint32: the stream must hold fewer than 2^32 pairs")
+    dev = w1.device
+    codes = torch.empty(n, dtype=torch.int16, device=dev)
+    scales, pis, pvs = [], [], []
+    for start in range(0, n, chunk_size):
+        end = min(start + chunk_size, n)
+        a = w1[start:min(end, n1)].float()
+        b = w2[start:min(end, n2)].float()
+        L = end - start
+        if a.numel() < L:
+            a = torch.nn.functional.pad(a, (0, L - a.numel()))
+        if b.numel() < L:
+            b = torch.nn.functional.pad(b, (0, L - b.numel()))
+        c, sc, pidx, pval = _dual_chunk(a, b, amp_bits, num_phases, mu, group_size, plug_cap, select)
+        del a, b
+        if layout == "u16be":
+            c = ((c & 0xFF) << 8) | (c >> 8)
+        else:
+            c = c ^ 0x8000
+        codes[start:end] = torch.where(c >= 0x8000, c - 0x10000, c).to(torch.int16)
+        del c
+        scales.append(sc)
+        if pidx is not None:
+            pis.append(pidx + start)
+            pvs.append(pval)
+    pi = torch.cat(pis) if pis else torch.zeros(0, dtype=torch.int64, device=dev)
+    pv = torch.cat(pvs) if pvs else torch.zeros(0, dtype=torch.float16, device=dev)
+    pi = torch.where(pi >= 2 ** 31, pi - 2 ** 32, pi).to(torch.int32).view(torch.uint32)
+    tail_list = []
+    if tails:
+        tail_list = [w1[n:].to(torch.float16).contiguous(), w2[n:].to(torch.float16).contiguous()]
+    return DualPackDevice(n_codes=n, n1=n1, n2=n2, codes=codes, layout=layout,
+                          scales=torch.cat(scales) if scales else torch.zeros(0, dtype=torch.float16, device=dev),
+                          plug_idx=pi, plug_val=pv, amp_bits=amp_bits, phase_bits=16 - amp_bits, mu=float(mu),
+                          group_size=group_size, chunk_size=chunk_size, tails=tail_list)

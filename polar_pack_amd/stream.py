@@ -31,7 +31,7 @@ from .quad_kernels import header_luts
 
 ITEM_DTYPE = np.dtype([("proj", "<i4"), ("row0", "<i4"), ("nrows", "<i4"), ("flags", "<i4"),
                        ("plug_lo", "<i8"), ("plug_hi", "<i8")])
-SEG_DTYPE = np.dtype([("proj", "<i4"), ("row0", "<i4"), ("row1", "<i4"), ("flags", "<i4"), ("plug_lo", "<i8")])
+SEG_DTYPE = np.dtype([("proj", "<i4"), ("row0", "<i4"), ("row1", "<i4"), ("task0", "<i4"), ("plug_lo", "<i8")])
 PROJ_DTYPE = np.dtype([("codes", "<u8"), ("ldc", "<i8"), ("pos0", "<i8"), ("x", "<u8"), ("x_sm", "<i8"),
                        ("out", "<u8", (4,)), ("o_sm", "<i8"), ("N", "<i4"), ("K", "<i4")])
 DUAL_PROJ_DTYPE = np.dtype([("codes", "<u8"), ("ldc", "<i8"), ("pos0", "<i8"), ("x", "<u8"), ("x_sm", "<i8"),
@@ -91,6 +91,7 @@ def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=
     segs["proj"] = proj[first]
     segs["row0"] = row0[first]
     segs["row1"] = row0[last] + nrows[last]
+    segs["task0"] = first
     pos0, _, K, _ = full_rows(shapes, n)
     start = pos0[proj[first]] + row0[first] * K[proj[first]]
     segs["plug_lo"] = np.searchsorted(plug_host, start, side="left")
@@ -99,20 +100,61 @@ def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=
     return segs, bounds
 
 
-def plan_tail_items(shapes, n, plug_host):
-    """One TAIL item per row that reaches position ``n``, with its plug range."""
+def plan_task_plug(shapes, n, plug_host, rows_per_task):
+    """Per task (in the order of :func:`plan_tasks`): the first plug entry at or after its
+    first position and the first entry past its last position, as an (n_tasks, 2) int64
+    table, and the number of chunks (512-pair steps) of each task."""
+    proj, row0, nrows = plan_tasks(shapes, n, rows_per_task)
+    pos0, _, K, _ = full_rows(shapes, n)
+    start = pos0[proj] + row0 * K[proj]
+    tab = np.empty((proj.size, 2), np.int64)
+    tab[:, 0] = np.searchsorted(plug_host, start, side="left")
+    tab[:, 1] = np.searchsorted(plug_host, start + nrows * K[proj], side="left")
+    return tab, (K[proj] + 511) // 512
+
+
+def plan_tail_items(shapes, n, plug_host, tail_lengths=None, fp16_rows=0):
+    """Items for the rows that reach position ``n``.
+
+    By default one TAIL item per row, with its plug range.  With ``fp16_rows`` > 0 and
+    the models' ``tail_lengths``, rows that start at or past ``n`` and, for every model,
+    lie wholly inside or wholly past its tail become FP16 items of up to ``fp16_rows``
+    consecutive rows with the same status; the rest stay one-row TAIL items.
+    """
     pos0, N, K, r_full = full_rows(shapes, n)
     parts = []
     for p in np.flatnonzero(r_full < N):
-        rows = np.arange(r_full[p], N[p])
-        it = np.zeros(rows.size, ITEM_DTYPE)
-        it["proj"] = p
-        it["row0"] = rows
-        it["nrows"] = 1
-        it["flags"] = nat.PP_ITEM_TAIL
+        rows = np.arange(r_full[p], N[p], dtype=np.int64)
         lo = pos0[p] + rows * K[p]
-        it["plug_lo"] = np.searchsorted(plug_host, lo, side="left")
-        it["plug_hi"] = np.searchsorted(plug_host, lo + K[p], side="left")
+        hi = lo + K[p]
+        key = np.full(rows.size, -1, np.int64)              # -1: element by element
+        if fp16_rows > 0 and tail_lengths is not None:
+            clean = lo >= n
+            status = np.zeros(rows.size, np.int64)
+            for m, L in enumerate(tail_lengths):
+                inside = hi <= n + L
+                clean &= inside | (lo >= n + L)
+                status |= inside.astype(np.int64) << m
+            key = np.where(clean, status, -1)
+        start = np.ones(rows.size, bool)
+        start[1:] = (key[1:] != key[:-1]) | (key[1:] < 0)
+        run_id = np.cumsum(start) - 1
+        run_first = np.flatnonzero(start)
+        in_run = np.arange(rows.size) - run_first[run_id]
+        if fp16_rows > 0:
+            start |= (in_run % fp16_rows) == 0
+        first = np.flatnonzero(start)
+        count = np.diff(np.concatenate([first, [rows.size]]))
+        it = np.zeros(first.size, ITEM_DTYPE)
+        it["proj"] = p
+        it["row0"] = rows[first]
+        it["nrows"] = count
+        fp16 = key[first] >= 0
+        it["flags"] = np.where(fp16, nat.PP_ITEM_FP16, nat.PP_ITEM_TAIL)
+        plo = np.searchsorted(plug_host, lo[first], side="left")
+        phi = np.searchsorted(plug_host, hi[first], side="left")
+        it["plug_lo"] = np.where(fp16, 0, plo)
+        it["plug_hi"] = np.where(fp16, 0, phi)
         parts.append(it)
     return np.concatenate(parts) if parts else np.zeros(0, ITEM_DTYPE)
 
@@ -221,12 +263,14 @@ class QuadStream:
 class DualStream:
     """One-launch decode of every projection of a dual stream (``pp_dual_stream``).
 
-    Same planning as :class:`QuadStream`; positions past ``pack.n_codes`` come from the
-    per-model fp16 tails.  Projection rows and positions must be multiples of 8 pairs
-    (a lane reads 8 pairs that share one group scale).
+    Same planning as :class:`QuadStream`, plus each task's plug range (the kernel
+    spreads a task's plug entries over its steps, 64 or 128 per step: ``plug_windows``,
+    chosen from the table's density unless given); positions past ``pack.n_codes`` come
+    from the per-model fp16 tails.  Projection rows and positions must be multiples of
+    8 pairs (a lane reads 8 pairs that share one group scale).
     """
 
-    def __init__(self, pack, shapes: Sequence[Tuple[int, int]], M: int = 1):
+    def __init__(self, pack, shapes: Sequence[Tuple[int, int]], M: int = 1, plug_windows=None):
         L = nat.lib()
         self.pack = pack
         self.shapes = [(int(n), int(k)) for n, k in shapes]
@@ -249,10 +293,25 @@ class DualStream:
         self.n_waves = int(L.pp_dual_stream_waves(self.M))
         self.segs_np, self.bounds_np = plan_segments(self.shapes, pack.n_codes, plug, self.n_waves,
                                                      self.rows_per_item, self.M, code_bytes=2)
-        self.tail_items_np = plan_tail_items(self.shapes, pack.n_codes, plug)
+        tails = list(pack.tails) + [None] * (2 - len(pack.tails))
+        aligned = pack.n_codes % 8 == 0 and all(t is None or t.numel() == 0 or t.data_ptr() % 16 == 0
+                                                for t in tails)
+        self.tail_items_np = plan_tail_items(self.shapes, pack.n_codes, plug, pack.tail_lengths,
+                                             fp16_rows=8 if aligned else 0)
         self.n_segs = self.segs_np.size
         self.n_tail = self.tail_items_np.size
+        self.task_plug_np, nck = plan_task_plug(self.shapes, pack.n_codes, plug, self.rows_per_item)
+        self.n_tasks = self.task_plug_np.shape[0]
+        if plug_windows is None:
+            # one 64-entry window per step, two when more than 2% of the tasks would
+            # otherwise have entries left after their last step
+            left = (self.task_plug_np[:, 1] - self.task_plug_np[:, 0]) > 64 * nck
+            plug_windows = 2 if left.size and left.mean() > 0.02 else 1
+        if plug_windows not in (1, 2):
+            raise ValueError("plug_windows must be 1 or 2")
+        self.plug_windows = int(plug_windows)
         dev = self.device
+        self.task_plug = torch.from_numpy(np.ascontiguousarray(self.task_plug_np).reshape(-1)).to(dev)
         self.segs = torch.from_numpy(self.segs_np.view(np.uint8).copy()).to(dev)
         self.tail_items = torch.from_numpy(self.tail_items_np.view(np.uint8).copy()).to(dev)
         self.bounds = torch.from_numpy(self.bounds_np).to(dev)
@@ -309,6 +368,8 @@ class DualStream:
         rc = nat.lib().pp_dual_stream(self.projs.data_ptr(), len(self.shapes),
                                       self.segs.data_ptr() if self.n_segs else None, self.n_segs,
                                       self.bounds.data_ptr(), self.n_waves,
+                                      self.task_plug.data_ptr() if self.n_tasks else None, self.n_tasks,
+                                      self.plug_windows,
                                       self.tail_items.data_ptr() if self.n_tail else None, self.n_tail,
                                       self.code_layout, pk.scales.data_ptr(), int(pk.scales.numel()),
                                       pk.group_size, pk.chunk_size, amp.data_ptr(), cos.data_ptr(), sin.data_ptr(),

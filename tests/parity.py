@@ -8,6 +8,7 @@
 * codes, plug positions: bit-exact (checked by the tests directly).
 """
 import numpy as np
+import torch
 
 GEMV_RTOL = 1e-3
 GEMV_FLOOR = 1e-5
@@ -47,3 +48,34 @@ def assert_gemv_close(got, ref, what="", rtol=GEMV_RTOL, floor=GEMV_FLOOR):
 def normwise(got, ref):
     ref = np.asarray(ref, np.float64)
     return float(np.abs(np.asarray(got, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-300))
+
+
+def dual_codes_u16(pack):
+    """16-bit codes of a DualPackDevice (either layout) as uint32 numpy."""
+    raw = pack.codes.cpu().numpy().view(np.uint16).astype(np.uint32)
+    if pack.layout == "u16be":
+        return ((raw & 0xFF) << 8) | (raw >> 8)
+    return raw ^ 0x8000
+
+
+def assert_same_dual_pack(pack, dp, max_code_flips=1e-4, min_plug_overlap=0.99):
+    """Codes equal but for rare one-step flips at float32 rounding ties; scales
+    bit-exact; the same plug count, nearly the same plug set, equal values where
+    the positions agree."""
+    assert pack.n_codes == dp.n_pairs
+    got, ref = dual_codes_u16(pack), dp.codes_u16()
+    diff = np.flatnonzero(got != ref)
+    assert diff.size <= max(2, max_code_flips * got.size), f"{diff.size} of {got.size} codes differ"
+    if diff.size:
+        da = np.abs((got[diff] >> 10).astype(np.int64) - (ref[diff] >> 10).astype(np.int64))
+        dph = np.abs((got[diff] & 1023).astype(np.int64) - (ref[diff] & 1023).astype(np.int64))
+        dph = np.minimum(dph, 1024 - dph)
+        assert np.all(da + dph == 1), "a differing code is more than one step away"
+    np.testing.assert_array_equal(pack.scales.cpu().numpy().view(np.uint16), dp.scales.view(np.uint16))
+    pi = pack.plug_idx.cpu().view(torch.int32).numpy().view(np.uint32)
+    pv = pack.plug_val.cpu().numpy()
+    assert pi.size == dp.plug_idx.size
+    assert np.all(np.diff(pi.astype(np.int64)) > 0)
+    common, ia, ib = np.intersect1d(pi, dp.plug_idx, return_indices=True)
+    assert common.size >= min_plug_overlap * max(1, pi.size)
+    np.testing.assert_array_equal(pv[ia].view(np.uint16), dp.plug_val[ib].view(np.uint16))

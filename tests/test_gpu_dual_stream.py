@@ -61,8 +61,8 @@ def device_pack(dp, layout, tails=None, n_codes=None):
     return pack
 
 
-def run_stream(pack, M, seed=5):
-    st = DualStream(pack, SHAPES, M=M)
+def run_stream(pack, M, seed=5, plug_windows=None):
+    st = DualStream(pack, SHAPES, M=M, plug_windows=plug_windows)
     xs_np = [np.random.default_rng(seed + p).standard_normal((M, k)).astype(np.float16)
              for p, (_, k) in enumerate(SHAPES)]
     xs = [torch.from_numpy(x).to(DEV) for x in xs_np]
@@ -110,15 +110,87 @@ def test_dual_stream_fp16_tails(layout):
             assert_gemv_close(outs[p][m].float().cpu().numpy(), ref[p][m], f"proj {p} model {m}")
 
 
-def test_dual_stream_dense_plug_tasks():
-    """A plug table dense enough that tasks hold more than 64 entries."""
+@pytest.mark.parametrize("plug_windows", [1, 2])
+@pytest.mark.parametrize("cap,M", [(0.2, 1), (0.2, 4), (0.03, 1), (0.03, 2)])
+def test_dual_stream_dense_plug_tasks(plug_windows, cap, M):
+    """Plug tables dense enough that tasks hold more entries than their steps take
+    (64 or 128 per step): the rest is corrected when the task finishes."""
     w1, w2 = gen.correlated_models(17, [TOTAL, TOTAL], delta_growth=False)
-    dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=0.2, chunk_size=50_000_000))
+    dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=cap, chunk_size=50_000_000))
     pack = device_pack(dp, "u16be")
-    st, xs_np, outs = run_stream(pack, 1)
+    st, xs_np, outs = run_stream(pack, M, plug_windows=plug_windows)
+    n_t = st.task_plug_np[:, 1] - st.task_plug_np[:, 0]
+    nck = np.array([(-(-SHAPES[p][1] // 512)) for p in np.repeat(np.arange(len(SHAPES)),
+                                                                   [-(-n // st.rows_per_item) for n, _ in SHAPES])])
+    if cap == 0.2:
+        assert np.any(n_t > 64 * plug_windows * nck)          # the finishing path runs
     ref = oracle_outputs(oracle_pairs(dp), xs_np)
     st()
     torch.cuda.synchronize()
     for p in range(len(SHAPES)):
         for m in range(2):
             assert_gemv_close(outs[p][m].float().cpu().numpy(), ref[p][m], f"proj {p} model {m}")
+
+
+def device_pack_to_oracle(pack):
+    """The device pack as an oracle DualPack (codes as file bytes) for decode_pairs_f64."""
+    be = pack.codes.cpu().numpy().view(np.uint16)
+    if pack.layout == "i16":
+        be = (be ^ np.uint16(0x8000)).byteswap()
+    return odp.DualPack(n_pairs=pack.n_codes, n1=pack.n_codes, n2=pack.n_codes, codes_be=be.view(np.uint8).copy(),
+                        scales=pack.scales.cpu().numpy(), plug_idx=pack.plug_host().copy(),
+                        plug_val=pack.plug_val.cpu().numpy(), mu=pack.mu, group_size=pack.group_size,
+                        chunk_size=pack.chunk_size)
+
+
+@pytest.mark.parametrize("chunk", [1000, 50_000_000])
+def test_device_packer_on_gpu_matches_oracle_packer(chunk):
+    from parity import assert_same_dual_pack
+    from polar_pack_amd.packer import pack_dual_device
+    w1, w2 = gen.correlated_models(19, [60_000, 57_000], delta_growth=False)
+    pack = pack_dual_device(torch.from_numpy(w1).to(DEV), torch.from_numpy(w2).to(DEV), plug_cap=0.03,
+                            chunk_size=chunk)
+    assert_same_dual_pack(pack, odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=0.03, chunk_size=chunk)))
+
+
+@pytest.mark.parametrize("layout", ["u16be", "i16"])
+def test_device_packed_tail_stream(layout):
+    """The benchmark's pipeline at small size: device pack in tail mode (model 2 truncated),
+    stream decode, against the float64 decode of the same device pack + its fp16 tail."""
+    from polar_pack_amd.packer import pack_dual_device
+    n2 = TOTAL - 9 * 520 - 3 * 16 - 12 * 11008 + 2 * 11008 + 40      # inside the 11008-wide projection
+    w1, w2 = gen.correlated_models(23, [TOTAL, n2], delta_growth=False)
+    pack = pack_dual_device(torch.from_numpy(w1).to(DEV), torch.from_numpy(w2).to(DEV), plug_cap=0.01,
+                            select="ref", tails=True, layout=layout)
+    assert pack.n_codes == n2 and pack.tail_lengths == [TOTAL - n2, 0]
+    st, xs_np, outs = run_stream(pack, 1)
+    t1 = pack.tails[0].cpu().numpy()
+    ref = oracle_outputs(oracle_pairs(device_pack_to_oracle(pack), tails=(t1, np.zeros(0, np.float16))), xs_np)
+    st()
+    torch.cuda.synchronize()
+    for p in range(len(SHAPES)):
+        for m in range(2):
+            assert_gemv_close(outs[p][m].float().cpu().numpy(), ref[p][m], f"proj {p} model {m}")
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_dual_stream_fp16_tail_rows(M):
+    """Aligned tails (n_codes % 8 == 0): rows wholly in a tail take the vectorized fp16
+    path, with model 2's tail ending at a row boundary of one projection and inside a
+    row of a later one (that row element by element, the rows after it 0 for model 2)."""
+    n_codes = 24 * 1024 + 8 * 2048 + 16 * 4096 + 40 * 512 + 2 * 11008        # row 2 of the 12x11008 block
+    w1, w2 = gen.correlated_models(29, [TOTAL, TOTAL], delta_growth=False)
+    dp = odp.pack_dual(w1[:n_codes], w2[:n_codes], odp.DualConfig(plug_cap=0.03, chunk_size=50_000_000))
+    t1 = np.asarray(w1[n_codes:], np.float32).astype(np.float16)
+    t2 = np.asarray(w2[n_codes:n_codes + 7 * 11008 + 500], np.float32).astype(np.float16)
+    pack = device_pack(dp, "i16", tails=(t1, t2))
+    st, xs_np, outs = run_stream(pack, M)
+    flags = st.tail_items_np["flags"]
+    assert np.any(flags == 2) and np.any(flags == 1) and st.tail_items_np["nrows"].max() == 8
+    ref = oracle_outputs(oracle_pairs(dp, tails=(t1, t2)), xs_np)
+    st()
+    torch.cuda.synchronize()
+    for p in range(len(SHAPES)):
+        for m in range(2):
+            assert_gemv_close(outs[p][m].float().cpu().numpy(), ref[p][m], f"proj {p} model {m}")
+

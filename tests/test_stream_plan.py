@@ -78,3 +78,57 @@ def test_struct_layouts_match_abi():
     assert DUAL_PROJ_DTYPE.itemsize == ctypes.sizeof(nat.DualProj) == 72
     for name, _ in nat.DualProj._fields_:
         assert getattr(nat.DualProj, name).offset == DUAL_PROJ_DTYPE.fields[name][1]
+
+
+def test_task_plug_ranges_partition_the_plug_table():
+    from polar_pack_amd.stream import plan_task_plug
+    shapes = [(24, 1024), (8, 2048), (3, 16), (9, 520)]
+    total = sum(n * k for n, k in shapes)
+    n = total - 700                      # the last projection's last rows reach the tails
+    plug = np.sort(np.random.default_rng(3).choice(n, 900, replace=False)).astype(np.uint32)
+    for rg in (2, 4, 8):
+        tab, nck = plan_task_plug(shapes, n, plug, rg)
+        proj, row0, nrows = plan_tasks(shapes, n, rg)
+        assert tab.shape == (proj.size, 2) and nck.shape == (proj.size,)
+        pos = np.cumsum([0] + [a * b for a, b in shapes])
+        K = np.array([b for _, b in shapes])
+        for t in range(proj.size):
+            lo = pos[proj[t]] + row0[t] * K[proj[t]]
+            hi = lo + nrows[t] * K[proj[t]]
+            sel = plug[tab[t, 0]:tab[t, 1]].astype(np.int64)
+            assert np.all((sel >= lo) & (sel < hi))
+            assert np.count_nonzero((plug >= lo) & (plug < hi)) == sel.size
+        assert np.all(nck == (K[proj] + 511) // 512)
+    segs, _ = plan_segments(shapes, n, plug, 16, 4, code_bytes=2)
+    proj, row0, _ = plan_tasks(shapes, n, 4)
+    assert np.all(proj[segs["task0"]] == segs["proj"]) and np.all(row0[segs["task0"]] == segs["row0"])
+
+
+def test_tail_items_fp16_runs():
+    from polar_pack_amd.stream import plan_tail_items
+    shapes = [(10, 64), (20, 32), (5, 16)]
+    n = 3 * 64 + 16                    # row 3 of projection 0 straddles n
+    tails = [10 * 64 + 20 * 32 + 5 * 16 - n, 6 * 64 + 4 * 32 + 8]   # model 2's tail ends inside a row
+    plug = np.array([1, 50, 200, 205], np.uint32)
+    it = plan_tail_items(shapes, n, plug, tails, fp16_rows=4)
+    pos = np.cumsum([0] + [a * b for a, b in shapes])
+    covered = []
+    for x in it:
+        p, r0, nr, fl = int(x["proj"]), int(x["row0"]), int(x["nrows"]), int(x["flags"])
+        K = shapes[p][1]
+        lo, hi = pos[p] + r0 * K, pos[p] + (r0 + nr) * K
+        covered += [(p, r) for r in range(r0, r0 + nr)]
+        if fl == 2:
+            assert 1 <= nr <= 4 and lo >= n and x["plug_lo"] == x["plug_hi"] == 0
+            for L in tails:            # every row wholly inside or wholly past each tail
+                for r in range(nr):
+                    a, b = lo + r * K, lo + (r + 1) * K
+                    assert b <= n + L or a >= n + L
+        else:
+            assert fl == 1 and nr == 1
+            assert x["plug_lo"] == np.searchsorted(plug, lo) and x["plug_hi"] == np.searchsorted(plug, hi)
+    expect = [(p, r) for p, (N, K) in enumerate(shapes) for r in range(N) if pos[p] + (r + 1) * K > n]
+    assert covered == expect
+    assert int((it["flags"] == 1).sum()) == 2            # the row across n, the row across model 2's tail end
+    plain = plan_tail_items(shapes, n, plug)
+    assert np.all(plain["flags"] == 1) and np.all(plain["nrows"] == 1) and plain.size == len(expect)
