@@ -49,7 +49,7 @@ sys.path.insert(0, ROOT)
 from polar_pack_amd import polar_kernels as pk  # noqa: E402
 from polar_pack_amd import quad_kernels as qk  # noqa: E402
 from polar_pack_amd.packer import pack_dual_device, pack_quad_device  # noqa: E402
-from polar_pack_amd.stream import DualStream, QuadStream  # noqa: E402
+from polar_pack_amd.stream import DualStream, QuadBatch, QuadStream  # noqa: E402
 
 METRIC = "achieved HBM GB/s (% of peak) + ms per quad-pack 3B decode step, batch 1"
 PEAK_HBM_GBS = 8000.0
@@ -504,6 +504,28 @@ def quad_linear_pack(N, K, dev, seed):
     return pack_quad_device(models, plug_cap=0.001, select="norm")
 
 
+class _batch_as_stream:
+    """QuadBatch with the QuadStream interface used by the single-Linear benches."""
+
+    def __init__(self, pack, shapes, M):
+        (N, K), = shapes
+        self.qb = QuadBatch(pack, N, K, 0, M)
+        self.shapes = shapes
+
+    def make_buffers(self):
+        x, outs = self.qb.make_buffers()
+        return [x], [outs]
+
+    def bind(self, xs, outs):
+        self.qb.bind(xs[0], outs[0])
+
+    def __call__(self):
+        self.qb()
+
+    def algorithmic_bytes(self):
+        return self.qb.algorithmic_bytes()
+
+
 def sanity_quad_single(entry, pack, dev):
     st, xs, outs = entry
     st()
@@ -545,10 +567,13 @@ def cpu_single_quad(pack, N, K, M):
 
 
 def run_quad_single(args, dev, log, N, K, M, name, pack=None):
+    """Up to 8 tokens: the fused row decode (QuadStream of one projection); more: the
+    matrix-core batch decode (QuadBatch)."""
     pack = pack if pack is not None else quad_linear_pack(N, K, dev, seed_of(2, 0, 0))
-    st0 = QuadStream(pack, [(N, K)], M=M)
+    make = QuadStream if M <= 8 else _batch_as_stream
+    st0 = make(pack, [(N, K)], M=M)
     copies = max(2, -(-MALL_BYTES // st0.algorithmic_bytes()))
-    sts = rotated_streams(QuadStream, pack, [(N, K)], M, copies, dev, quad=True)
+    sts = rotated_streams(make, pack, [(N, K)], M, copies, dev, quad=True)
     sanity_quad_single(sts[0], pack, dev)
     ms, per = time_graph(sts, args)
     algo = sts[0][0].algorithmic_bytes()
@@ -571,9 +596,6 @@ def run_sweep(args, dev, log):
     for name, N, K in (("gate_proj", 11008, 2048), ("down_proj", 2048, 11008)):
         pack = quad_linear_pack(N, K, dev, seed_of(4, 0, 0 if name == "gate_proj" else 1))
         for M in args.sweep_tokens:
-            if M > 8:
-                log(f"[bench] {name} M={M}: the fused decode takes up to 8 tokens per launch; skipped")
-                continue
             run_quad_single(args, dev, log, N, K, M, name, pack=pack)
         del pack
         torch.cuda.empty_cache()

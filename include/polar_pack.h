@@ -110,9 +110,13 @@ int pp_quad_dequant(const uint32_t* codes, int64_t c_sk, int64_t c_sn,
  * prepared by the host once per stream (see polar_pack_amd/stream.py):
  *
  *   projs      : n_projs descriptors of pp_quad_proj;
- *   segs       : n_segs runs of full rows of one projection (pp_quad_seg);
+ *   segs       : n_segs runs of rows of one projection (pp_quad_seg);
  *                wavefront w decodes segs [seg_bounds[w], seg_bounds[w+1]),
  *                n_waves = pp_quad_stream_waves(M) (the host balances them by bytes);
+ *   workspace  : needed only when a segment has parts > 1: the uint32 counters (one per
+ *                task number) at its start and the float32 accumulators the segments
+ *                name; all zero before the first launch, and left zero by every launch
+ *                (launches that share a workspace must not overlap);
  *   luts       : 7 float32 LUTs from the header (r_max, mu);
  *   scales     : host float[4], the header RMS s_k;
  *   plug_idx / plug_vals : the stream's plug table (ascending positions, plug_n entries).
@@ -135,15 +139,27 @@ typedef struct pp_quad_proj {
   int32_t N, K;
 } pp_quad_proj;
 
-/* A run of full rows [row0, row1) of projection `proj`, decoded by one wavefront.
- * plug_lo = first plug entry whose position is >= the run's first position. */
+/* A run of rows [row0, row1) of projection `proj`, columns [k0, k1), decoded by one
+ * wavefront.  plug_lo = first plug entry whose position is >= the position of
+ * (row0, 0).  task0 = number of the run's first task (the runs' tasks, groups of
+ * pp_*_stream_rows(M) rows, numbered over the whole launch in stream order; the parts of
+ * one split task share its number).
+ * A run with parts == 1 covers whole rows (k0 = 0, k1 = K) and writes its outputs.
+ * A run with parts > 1 is one of `parts` column slices of its rows (split-K for
+ * projections with few rows): its float32 partial sums (scaled as the outputs are) are
+ * added into the workspace at acc_off + (m*M + j)*N + row (model m, token j), and the
+ * last of the parts of a task (counted in the workspace's uint32 counter [task]) writes
+ * the fp16 outputs and leaves the accumulators and the counter at zero. */
 typedef struct pp_quad_seg {
   int32_t proj;
   int32_t row0;
   int32_t row1;
-  int32_t task0;           /* dual stream: index of the run's first task in task_plug;
-                              quad stream: reserved, 0 */
+  int32_t task0;
   int64_t plug_lo;
+  int32_t k0, k1;          /* column range */
+  int32_t parts;           /* column slices of these rows: 1 = whole rows */
+  int32_t reserved;        /* 0 */
+  int64_t acc_off;         /* parts > 1: float offset of the projection's accumulators */
 } pp_quad_seg;
 
 enum pp_item_flags { PP_ITEM_TAIL = 1, PP_ITEM_FP16 = 2 };
@@ -161,14 +177,44 @@ typedef struct pp_quad_item {
   int64_t plug_hi;
 } pp_quad_item;
 
+/*
+ * Batch decode GEMM on the matrix cores (1..64 tokens; used for more than 8):
+ *   out_m[i, n] = fp16( s_m * sum_k a[i, k] * W_m[n, k] ),   m = 0..3,
+ * for codes laid out (N,K) row-major (row n at codes + n*ldc: the container stream
+ * layout, the reference's (K,N) view of it with c_sk == 1), K % 8 == 0.  Each 16-row
+ * tile is decoded into fp16 MFMA operands in registers; plug entries (normalised tuples,
+ * positions relative to elem_base like pp_quad_gemm) are patched into the decoded
+ * tile.  K is cut into `slices` column ranges of slice_cols (a multiple of 32) columns;
+ * row_plug[n*slices + s] (n*slices+s+1 entries follow, the last one past the end) is the
+ * first plug entry at or after position elem_base + n*ldc + s*slice_cols (searchsorted of
+ * those keys, and of elem_base + N*ldc for the last).  With slices > 1 the workspace
+ * (pp_quad_mfma_workspace_size bytes) holds float32 partial sums: zero before the first
+ * call, left zero by every call; calls that share it must not overlap.  Two launches
+ * then (the tiles, and the reduction to fp16).  No counterpart kernel in the reference
+ * (its quad_bitpacked_kernel runs every batch size through tl.dot, quad_kernels.py:53-143);
+ * this replaces that for M > 8.
+ */
+int pp_quad_mfma(const uint32_t* codes, int64_t ldc, int64_t elem_base, const void* a, int64_t a_sm,
+                 const void* const* luts, int lut_dtype, const float* scales,
+                 const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n, const int64_t* row_plug,
+                 int64_t slices, int64_t slice_cols, void* const* out, int64_t o_sm,
+                 int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream);
+int64_t pp_quad_mfma_workspace_size(int64_t M, int64_t N, int64_t slices);
+/* Wavefronts the batch decode launches (the host sizes the slices for them). */
+int64_t pp_quad_mfma_waves(void);
+
 /* Rows per wavefront task the stream decode uses for M tokens (0 and an error for bad M). */
 int pp_quad_stream_rows(int64_t M);
+/* Columns the stream decode reads per row and step for M tokens (0 for bad M): split
+ * segments (parts > 1) should cut K at multiples of it. */
+int pp_quad_stream_chunk(int64_t M);
 
 /* Number of wavefronts pp_quad_stream launches for M tokens on the current device. */
 int64_t pp_quad_stream_waves(int64_t M);
 
 int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs,
                    const pp_quad_seg* segs, int64_t n_segs, const int64_t* seg_bounds, int64_t n_waves,
+                   void* workspace,
                    const pp_quad_item* tail_items, int64_t n_tail,
                    const float* const* luts, const float* scales,
                    const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n,

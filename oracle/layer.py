@@ -85,23 +85,26 @@ def quantize_polar_bitpacked(w1, w2, amp_bits=6, num_phases=1024, mu=255, group_
             torch.cos(phases).to(torch.float16).numpy(), torch.sin(phases).to(torch.float16).numpy())
 
 
-def quad_dequant(codes, luts, scales=None):
+def quad_dequant(codes, luts, scales=None, dtype=np.float64):
     """float64 (K,N) weights for kernel-layout codes -- quad_kernels.py:103-121.
 
     The float64 formula evaluated on the LUT values the caller passes
     (``luts`` = [norm, cos1, sin1, cos2, sin2, cos3, sin3]); multiplied by
     ``scales`` when given (quad_kernels.py:131-134 applies them to the
-    accumulator, which is the same product).
+    accumulator, which is the same product).  ``dtype=np.float32`` evaluates the
+    same products in float32 (r*c1, rs = r*s1, rs*c2, rss = rs*s2, rss*c3, rss*s3, each
+    rounded once): the weights a kernel that decodes in float32 holds exactly, before
+    it rounds them to fp16 operands.
     """
     c = np.asarray(codes, dtype=np.uint32)
-    t = [np.asarray(l, dtype=np.float64) for l in luts]
+    t = [np.asarray(l, dtype=np.float64).astype(dtype) for l in luts]
     nq, q1, q2, q3 = c >> 24, (c >> 16) & 255, (c >> 8) & 255, c & 255
     r = t[0][nq]
     rs = r * t[2][q1]
     rss = rs * t[4][q2]
     w = [r * t[1][q1], rs * t[3][q2], rss * t[5][q3], rss * t[6][q3]]
     if scales is not None:
-        w = [wk * float(sk) for wk, sk in zip(w, scales)]
+        w = [wk.astype(np.float64) * float(sk) for wk, sk in zip(w, scales)]
     return w
 
 

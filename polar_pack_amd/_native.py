@@ -37,7 +37,8 @@ class QuadItem(C.Structure):
 class QuadSeg(C.Structure):
     """``pp_quad_seg`` (include/polar_pack.h)."""
     _fields_ = [("proj", C.c_int32), ("row0", C.c_int32), ("row1", C.c_int32), ("task0", C.c_int32),
-                ("plug_lo", i64)]
+                ("plug_lo", i64), ("k0", C.c_int32), ("k1", C.c_int32), ("parts", C.c_int32),
+                ("reserved", C.c_int32), ("acc_off", i64)]
 
 
 class DualProj(C.Structure):
@@ -54,9 +55,14 @@ EXPORTS = {
                            i64, i64, i64, vp, i64, vp]),
     "pp_quad_gemm_workspace_size": (i64, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64]),
     "pp_quad_dequant": (i32, [vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
+    "pp_quad_mfma": (i32, [vp, i64, i64, vp, i64, vp, i32, vp, vp, vp, i64, vp, i64, i64, vp, i64, i64, i64, i64,
+                           vp, i64, vp]),
+    "pp_quad_mfma_workspace_size": (i64, [i64, i64, i64]),
+    "pp_quad_mfma_waves": (i64, []),
     "pp_quad_stream_rows": (i32, [i64]),
+    "pp_quad_stream_chunk": (i32, [i64]),
     "pp_quad_stream_waves": (i64, [i64]),
-    "pp_quad_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, vp, vp, vp, i64, i64, vp, vp, i64, vp]),
+    "pp_quad_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, vp, i64, vp, vp, vp, vp, i64, i64, vp, vp, i64, vp]),
     "pp_dual_stream_rows": (i32, [i64]),
     "pp_dual_stream_waves": (i64, [i64]),
     "pp_dual_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, i32, vp, i64, i32, vp, i64, i64, i64, vp, vp, vp, vp, vp, i64,

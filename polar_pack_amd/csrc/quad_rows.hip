@@ -35,6 +35,7 @@
 //  * Tails.  Rows that reach FP16 tail positions run in quad_tail_kernel, one row per
 //    wavefront (quaternion_packer.py:201-210).
 #include "quad_rows.h"
+#include "quad_lds.h"
 #include "rows_common.h"
 
 #include <algorithm>
@@ -42,77 +43,6 @@
 namespace pp {
 
 constexpr int QSEG = 256;                 // columns per wave per row per segment (64 lanes x 4)
-constexpr uint32_t QLDS_BYTES = 0x28000;  // 160 KiB: all of a gfx950 CU's LDS
-// ------------------------------------------------------------------ LDS tables
-struct LaneOff {
-  uint32_t r, c1, c2, c3;
-};
-
-// LDS byte address of the table row of code byte B (3 = nq, 2 = q1, 1 = q2, 0 = q3):
-// byte 1 of the address is the code byte, bytes 0 and 2 come from the lane constant.
-template <int B>
-__device__ __forceinline__ uint32_t perm_addr(uint32_t cw, uint32_t lane_off) {
-  return __builtin_amdgcn_perm(cw, lane_off, 0x0C020000u | ((4u + B) << 8));
-}
-
-// q1 and q2 share one table.  [0, 64K): (cos,sin)(pi i/255) rows of 32 x 8 B;
-// [64K, 128K): (cos,sin)(2 pi i/255); [128K, 160K): norm rows of 32 x 4 B.
-struct LayShared {
-  static __device__ __forceinline__ LaneOff lane(int l) {
-    LaneOff o;
-    o.r = 0x20000u | (4u * (l & 31));
-    o.c1 = o.c2 = 8u * (l & 31);
-    o.c3 = 0x10000u | (8u * (l & 31));
-    return o;
-  }
-  static __device__ __forceinline__ uint32_t addr_r(uint32_t cw, const LaneOff& o) {
-    return ((cw >> 17) & 0x7F80u) | o.r;
-  }
-  static __device__ __forceinline__ void build(char* lds, int e, int grp, int ngrp, const float (&v)[7]) {
-    for (int j = grp; j < 32; j += ngrp) {
-      *reinterpret_cast<float*>(lds + 0x20000 + e * 128 + 4 * j) = v[0];
-      *reinterpret_cast<float2*>(lds + e * 256 + 8 * j) = make_float2(v[1], v[2]);
-      *reinterpret_cast<float2*>(lds + 0x10000 + e * 256 + 8 * j) = make_float2(v[5], v[6]);
-    }
-  }
-};
-
-// Four tables.  [0, 64K): rows [norm x 32 (4 B) | (cos3,sin3) x 16 (8 B)];
-// [64K, 128K): rows [(cos1,sin1) x 16 | (cos2,sin2) x 16].
-struct LaySplit {
-  static __device__ __forceinline__ LaneOff lane(int l) {
-    LaneOff o;
-    o.r = 4u * (l & 31);
-    o.c3 = 128u + 8u * (l & 15);
-    o.c1 = 0x10000u | (8u * (l & 15));
-    o.c2 = 0x10000u | (128u + 8u * (l & 15));
-    return o;
-  }
-  static __device__ __forceinline__ uint32_t addr_r(uint32_t cw, const LaneOff& o) { return perm_addr<3>(cw, o.r); }
-  static __device__ __forceinline__ void build(char* lds, int e, int grp, int ngrp, const float (&v)[7]) {
-    float* row0 = reinterpret_cast<float*>(lds + e * 256);
-    float* row1 = reinterpret_cast<float*>(lds + 0x10000 + e * 256);
-    for (int j = grp; j < 32; j += ngrp) row0[j] = v[0];
-    for (int j = grp; j < 16; j += ngrp) {
-      row0[32 + 2 * j] = v[5];
-      row0[33 + 2 * j] = v[6];
-      row1[2 * j] = v[1];
-      row1[2 * j + 1] = v[2];
-      row1[32 + 2 * j] = v[3];
-      row1[33 + 2 * j] = v[4];
-    }
-  }
-};
-
-template <class L>
-__device__ __forceinline__ void lookup(const char* lds, uint32_t cw, const LaneOff& o, float& r, float2& a, float2& b,
-                                       float2& c) {
-  r = *reinterpret_cast<const float*>(lds + L::addr_r(cw, o));
-  a = *reinterpret_cast<const float2*>(lds + perm_addr<2>(cw, o.c1));
-  b = *reinterpret_cast<const float2*>(lds + perm_addr<1>(cw, o.c2));
-  c = *reinterpret_cast<const float2*>(lds + perm_addr<0>(cw, o.c3));
-}
-
 // ------------------------------------------------------------------ configuration
 // Batch 1 (the decode step): 8 rows per task and 8 waves per CU measured fastest on
 // the 3B-shaped stream (vs 4 rows / 16 waves: fewer per-task reductions and stores, and
@@ -154,6 +84,7 @@ struct QuadRowsArgs {
   const f16* plug_vals;  // (P, 4)
   int64_t plug_n;
   int M;
+  void* ws;              // split segments: uint32 task counters, float32 accumulators
 };
 
 // Uniform state of the segment a wave is working on.
@@ -167,6 +98,11 @@ struct SegCtx {
   int row0;           // projection row of the segment's first row
   f16* out[4];        // outputs of the segment's first row
   int64_t o_sm, o_sn;
+  int kbeg, kend;     // the columns decoded: [kbeg, kend)
+  int parts;          // > 1: one of `parts` column slices, sums go through the workspace
+  int N;              // rows of the projection (accumulator stride)
+  float* acc;         // parts > 1: the projection's accumulators
+  uint32_t* cnt;      // parts > 1: counter of the segment's first task
 };
 
 template <int MT, int RG, int NSEG>
@@ -177,7 +113,8 @@ struct Chunk {
 };
 
 // Issue every load of one chunk (Chunk::LOADS instructions): RG rows x NSEG segments of
-// codes starting at row `row` (of the segment) and column kc, plus the activations.
+// codes starting at row `row` (of the segment) and column kc, plus the activations
+// (read as 0 from the segment's column end on, which also cancels the codes read there).
 // The buffer resources are rebased to the chunk in scalar registers, so each lane's
 // offsets are fixed for the whole segment (no per-step vector address arithmetic):
 // codes resource = rows [row, nrows) from column kc, num_records ends at column K of
@@ -194,14 +131,14 @@ __device__ __forceinline__ void chunk_issue(const SegCtx& S, int row, int kc, co
 #pragma unroll
     for (int s = 0; s < NSEG; ++s) vload128(c.q[r][s], voff[r] + 1024u * s, rc);
   if constexpr (MT == 1) {
-    const rsrc_t rx = make_rsrc(S.x + kc, 2u * (uint32_t)(S.K - kc));   // past K: reads 0
+    const rsrc_t rx = make_rsrc(S.x + kc, 2u * (uint32_t)(S.kend - kc));   // past kend: reads 0
 #pragma unroll
     for (int s = 0; s < NSEG; ++s) vload64(c.xr[0][s], 8u * lane + 512u * s, rx);
   } else {
 #pragma unroll
     for (int s = 0; s < NSEG; ++s) {
       const int k = kc + s * QSEG + 4 * lane;
-      const bool valid = k < S.K;
+      const bool valid = k < S.kend;
 #pragma unroll
       for (int j = 0; j < MT; ++j) vload64(c.xr[j][s], valid ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
     }
@@ -334,7 +271,8 @@ __device__ __forceinline__ void plug_begin(const QuadRowsArgs& A, const SegCtx& 
   const bool in = (pc + lane < A.plug_n) && ((int64_t)P.idx < tend);
   const int cnt = __popcll(__ballot(in));
   int k = 0;
-  const int row = in ? plug_locate<RG>((int64_t)P.idx, tpos0, S.ldc, S.K, nr, k) : -1;
+  int row = in ? plug_locate<RG>((int64_t)P.idx, tpos0, S.ldc, S.K, nr, k) : -1;
+  if (k < S.kbeg || k >= S.kend) row = -1;   // consumed with the task's rows, applied by its slice
   P.row = row;
   const bool v = row >= 0;
   vload32(P.cw, v ? 4u * (uint32_t)((ti * RG + row) * S.ldc + k) : OOB, S.rc);
@@ -394,7 +332,8 @@ __device__ __forceinline__ int plug_end(const char* lds, const LaneOff& lo, cons
     const bool in = pos < tend;
     const int cnt = __popcll(__ballot(in));
     int k = 0;
-    const int row = in ? plug_locate<RG>(pos, tpos0, S.ldc, S.K, nr, k) : -1;
+    int row = in ? plug_locate<RG>(pos, tpos0, S.ldc, S.K, nr, k) : -1;
+    if (k < S.kbeg || k >= S.kend) row = -1;
     if (row >= 0) {
       float xk[MT];
 #pragma unroll
@@ -413,9 +352,17 @@ __device__ __forceinline__ int plug_end(const char* lds, const LaneOff& lo, cons
   return 1;
 }
 
+// The reduced sum a lane holds after the transposing reduction, and where it goes.
 template <int MT, int RG>
-__device__ __forceinline__ void task_write(const QuadRowsArgs& A, const SegCtx& S, int ti, int lane,
-                                           float (&acc)[RG][4][MT]) {
+struct Reduced {
+  float y;       // normalised sum of (row r, model m, token j)
+  int r, m, j;
+  bool wr;       // this lane writes it
+};
+
+template <int MT, int RG>
+__device__ __forceinline__ Reduced<MT, RG> task_reduce(const QuadRowsArgs& A, const SegCtx& S, int ti, int lane,
+                                                       float (&acc)[RG][4][MT]) {
   constexpr int NV = RG * 4 * MT;
   constexpr int LNV = Log2<NV>::v;
   static_assert((1 << LNV) == NV, "RG*4*MT must be a power of two");
@@ -426,20 +373,67 @@ __device__ __forceinline__ void task_write(const QuadRowsArgs& A, const SegCtx& 
     for (int m = 0; m < 4; ++m)
 #pragma unroll
       for (int j = 0; j < MT; ++j) v[(r * 4 + m) * MT + j] = acc[r][m][j];
-  const float y = wave_transpose_reduce<LNV>(v, lane);
+  Reduced<MT, RG> o;
+  o.y = wave_transpose_reduce<LNV>(v, lane);
   const int idx = lane >> (6 - LNV);
-  const int r = idx / (4 * MT), m = (idx / MT) & 3, j = idx % MT;
+  o.r = idx / (4 * MT);
+  o.m = (idx / MT) & 3;
+  o.j = idx % MT;
   const int nr = min(RG, S.nrows - ti * RG);
-  const bool wr = (lane & ((1 << (6 - LNV)) - 1)) == 0 && r < nr && j < A.M;
-  const uint32_t off = 2u * (uint32_t)((int64_t)j * S.o_sm + (int64_t)(ti * RG + r) * S.o_sn);
+  o.wr = (lane & ((1 << (6 - LNV)) - 1)) == 0 && o.r < nr && o.j < A.M;
+  return o;
+}
+
+// Store value h (fp16 bits) of (row r of task ti, model m, token j) from the lanes with wr.
+template <int MT, int RG>
+__device__ __forceinline__ void task_store(const QuadRowsArgs& A, const SegCtx& S, int ti, const Reduced<MT, RG>& o,
+                                           const float (&val)[4]) {
+  const uint32_t off = 2u * (uint32_t)((int64_t)o.j * S.o_sm + (int64_t)(ti * RG + o.r) * S.o_sn);
   // one store per model (4 counted stores), each lane writing only its own model:
   // selecting the pointer per lane would index the pointer array in scratch memory
   const uint32_t obytes = 2u * (uint32_t)((int64_t)(A.M - 1) * S.o_sm + (int64_t)(S.nrows - 1) * S.o_sn + 1);
 #pragma unroll
   for (int mm = 0; mm < 4; ++mm) {
-    const f16 h = (f16)(y * A.s[mm]);
-    vstore16((uint32_t)__builtin_bit_cast(unsigned short, h), (wr && m == mm) ? off : OOB,
+    const f16 h = (f16)val[mm];
+    vstore16((uint32_t)__builtin_bit_cast(unsigned short, h), (o.wr && o.m == mm) ? off : OOB,
              make_rsrc(S.out[mm], obytes));
+  }
+}
+
+template <int MT, int RG>
+__device__ __forceinline__ void task_write(const QuadRowsArgs& A, const SegCtx& S, int ti, int lane,
+                                           float (&acc)[RG][4][MT]) {
+  const Reduced<MT, RG> o = task_reduce<MT, RG>(A, S, ti, lane, acc);
+  const float val[4] = {o.y * A.s[0], o.y * A.s[1], o.y * A.s[2], o.y * A.s[3]};
+  task_store<MT, RG>(A, S, ti, o, val);
+}
+
+// A column slice of task ti: add the scaled sums to the projection's accumulators and
+// count the part in the task's counter; the last part to arrive takes the totals
+// (swapping in zeros, so the workspace is clean for the next launch), writes the
+// outputs and clears the counter.  Every access to the workspace is a device-scope
+// atomic, performed where all CUs see it, so no cache maintenance is needed; the order
+// "sums before count" comes from a data dependence: the count added is 1 + 0 * (the
+// values the sum atomics returned), so it cannot be issued before they completed.
+template <int MT, int RG>
+__device__ __forceinline__ void task_accumulate(const QuadRowsArgs& A, const SegCtx& S, int ti, int lane,
+                                                float (&acc)[RG][4][MT]) {
+  const Reduced<MT, RG> o = task_reduce<MT, RG>(A, S, ti, lane, acc);
+  const float sm = o.m == 0 ? A.s[0] : o.m == 1 ? A.s[1] : o.m == 2 ? A.s[2] : A.s[3];
+  float* a = S.acc + ((int64_t)(o.m * A.M + o.j) * S.N + S.row0 + ti * RG + o.r);
+  float before = 0.f;
+  if (o.wr) before = __hip_atomic_fetch_add(a, o.y * sm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // a zero the compiler cannot see through, computed from the returned sums
+  uint32_t z;
+  asm volatile("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(before));
+  uint32_t old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(S.cnt + ti, 1u + z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __builtin_amdgcn_readfirstlane(old);
+  if (old + 1 == (uint32_t)S.parts) {
+    const float t = o.wr ? __hip_atomic_exchange(a, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    const float val[4] = {t, t, t, t};
+    task_store<MT, RG>(A, S, ti, o, val);
+    if (lane == 0) __hip_atomic_exchange(S.cnt + ti, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -455,7 +449,7 @@ __device__ __forceinline__ void zero_acc(float (&acc)[RG][4][MT]) {
 
 // ------------------------------------------------------------------ segment walk
 
-template <int MT, int RG, int NSEG, class L>
+template <int MT, int RG, int NSEG, class L, bool SPLIT>
 struct SegRunner {
   static constexpr int CHUNK = NSEG * QSEG;
   const char* lds;
@@ -475,7 +469,7 @@ struct SegRunner {
       : lds(l), A(a), S(s), pend_ti(-1), pc(plug_lo) {
     lane = threadIdx.x & 63;
     lo = L::lane(lane);
-    nck = (S.K + CHUNK - 1) / CHUNK;
+    nck = (S.kend - S.kbeg + CHUNK - 1) / CHUNK;
     ntask = (S.nrows + RG - 1) / RG;
     lc = {0, 0};
 #pragma unroll
@@ -493,7 +487,7 @@ struct SegRunner {
   // Issue the next chunk's loads (past the last chunk: reload the last one, so every
   // step issues the same loads).
   __device__ __forceinline__ void prefetch(Chunk<MT, RG, NSEG>& c) {
-    chunk_issue<MT, RG, NSEG>(S, lc.ti * RG, lc.ck * CHUNK, voff, lane, c);
+    chunk_issue<MT, RG, NSEG>(S, lc.ti * RG, S.kbeg + lc.ck * CHUNK, voff, lane, c);
     Cursor nx = lc;
     advance(nx);
     if (nx.ti < ntask) lc = nx;
@@ -502,7 +496,12 @@ struct SegRunner {
   // Finish the pending task: plug corrections, wave reduction, stores.
   __device__ __forceinline__ void finish_pending() {
     plug_end<MT, RG, L>(lds, lo, A, S, pend_ti, lane, pc, P, pend);
-    task_write<MT, RG>(A, S, pend_ti, lane, pend);
+    if constexpr (SPLIT) {
+      if (S.parts > 1) task_accumulate<MT, RG>(A, S, pend_ti, lane, pend);
+      else task_write<MT, RG>(A, S, pend_ti, lane, pend);
+    } else {
+      task_write<MT, RG>(A, S, pend_ti, lane, pend);
+    }
     pend_ti = -1;
   }
 
@@ -535,7 +534,7 @@ struct SegRunner {
   }
 
   __device__ __forceinline__ void run() {
-    if (ntask <= 0 || S.K <= 0) return;
+    if (ntask <= 0 || S.kend <= S.kbeg) return;
     Chunk<MT, RG, NSEG> c0, c1;
     Cursor cur = {0, 0};
     vload32(P.idx, 4u * lane, plug_idx_rsrc(A, pc));
@@ -571,9 +570,15 @@ __device__ __forceinline__ void seg_ctx(const pp_quad_proj& P, int64_t o_sn, int
   for (int m = 0; m < 4; ++m) S.out[m] = reinterpret_cast<f16*>(uniform_ptr(P.out[m])) + (int64_t)row0 * o_sn;
   S.o_sm = uniform64(P.o_sm);
   S.o_sn = o_sn;
+  S.kbeg = 0;
+  S.kend = K;
+  S.parts = 1;
+  S.N = uniform(P.N);
+  S.acc = nullptr;
+  S.cnt = nullptr;
 }
 
-template <int MT, class L>
+template <int MT, class L, bool SPLIT>
 __device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A) {
   constexpr int RG = RowsCfg<MT>::RG, NSEG = RowsCfg<MT>::NSEG;
   constexpr int WAVES = RowsCfg<MT>::NT / 64;
@@ -585,7 +590,7 @@ __device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A
     if (row1 <= row0) return;
     SegCtx S;
     seg_ctx(A.proj, A.o_sn, row0, row1, A.M, S);
-    SegRunner<MT, RG, NSEG, L> R(lds, A, S, A.wave_plug ? uniform64(A.wave_plug[gw]) : 0);
+    SegRunner<MT, RG, NSEG, L, false> R(lds, A, S, A.wave_plug ? uniform64(A.wave_plug[gw]) : 0);
     R.run();
     return;
   }
@@ -594,38 +599,27 @@ __device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A
     const pp_quad_seg g = A.segs[si];
     SegCtx S;
     seg_ctx(A.projs[uniform(g.proj)], 1, g.row0, g.row1, A.M, S);
-    SegRunner<MT, RG, NSEG, L> R(lds, A, S, uniform64(g.plug_lo));
+    const int parts = uniform(g.parts);
+    if (parts > 1) {
+      if (!SPLIT) continue;   // split segments run in the kernel that has the workspace
+      // one column slice of its rows (clamped to the projection)
+      S.kbeg = max(0, min(S.K, uniform(g.k0)));
+      S.kend = max(S.kbeg, min(S.K, uniform(g.k1)));
+      S.parts = parts;
+      S.acc = reinterpret_cast<float*>(A.ws) + uniform64(g.acc_off);
+      S.cnt = reinterpret_cast<uint32_t*>(A.ws) + uniform(g.task0);
+    }
+    SegRunner<MT, RG, NSEG, L, SPLIT> R(lds, A, S, uniform64(g.plug_lo));
     R.run();
   }
 }
 
-template <int MT>
+template <int MT, bool SPLIT>
 __global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_rows_kernel(const QuadRowsArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t T[QLDS_BYTES / 4];
-  char* lds = reinterpret_cast<char*>(T);
-  const int e = threadIdx.x & 255, grp = threadIdx.x >> 8, ngrp = blockDim.x >> 8;
-  float v[7];
-  if (A.luts.dtype == PP_F16) {
-#pragma unroll
-    for (int i = 0; i < 7; ++i) v[i] = (float)reinterpret_cast<const f16*>(A.luts.p[i])[e];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 7; ++i) v[i] = reinterpret_cast<const float*>(A.luts.p[i])[e];
-  }
-  const bool same = __float_as_uint(v[1]) == __float_as_uint(v[3]) && __float_as_uint(v[2]) == __float_as_uint(v[4]);
-  // workgroup-wide AND through the (not yet built) table memory: the tables fill all
-  // of LDS, so there is no room for a separate flag
-  if (threadIdx.x == 0) T[0] = 0u;
-  __syncthreads();
-  if (!same) T[0] = 1u;
-  __syncthreads();
-  const bool shared = T[0] == 0u;
-  __syncthreads();
-  if (shared) LayShared::build(lds, e, grp, ngrp, v);
-  else LaySplit::build(lds, e, grp, ngrp, v);
-  __syncthreads();
-  if (shared) rows_body<MT, LayShared>(lds, A);
-  else rows_body<MT, LaySplit>(lds, A);
+  const char* lds = reinterpret_cast<const char*>(T);
+  if (quad_tables(T, A.luts)) rows_body<MT, LayShared, SPLIT>(lds, A);
+  else rows_body<MT, LaySplit, SPLIT>(lds, A);
 }
 
 // ------------------------------------------------------------------ tail rows
@@ -755,14 +749,21 @@ static int cfg_waves(int mt) {
   }
 }
 
-static int launch_rows(const QuadRowsArgs& A, int mt, hipStream_t st) {
+template <bool SPLIT>
+static void launch_rows_t(const QuadRowsArgs& A, int mt, hipStream_t st) {
   const unsigned grid = (unsigned)device_cu_count();
   switch (mt) {
-    case 1: hipLaunchKernelGGL(quad_rows_kernel<1>, dim3(grid), dim3(RowsCfg<1>::NT), 0, st, A); break;
-    case 2: hipLaunchKernelGGL(quad_rows_kernel<2>, dim3(grid), dim3(RowsCfg<2>::NT), 0, st, A); break;
-    case 4: hipLaunchKernelGGL(quad_rows_kernel<4>, dim3(grid), dim3(RowsCfg<4>::NT), 0, st, A); break;
-    default: hipLaunchKernelGGL(quad_rows_kernel<8>, dim3(grid), dim3(RowsCfg<8>::NT), 0, st, A); break;
+    case 1: hipLaunchKernelGGL((quad_rows_kernel<1, SPLIT>), dim3(grid), dim3(RowsCfg<1>::NT), 0, st, A); break;
+    case 2: hipLaunchKernelGGL((quad_rows_kernel<2, SPLIT>), dim3(grid), dim3(RowsCfg<2>::NT), 0, st, A); break;
+    case 4: hipLaunchKernelGGL((quad_rows_kernel<4, SPLIT>), dim3(grid), dim3(RowsCfg<4>::NT), 0, st, A); break;
+    default: hipLaunchKernelGGL((quad_rows_kernel<8, SPLIT>), dim3(grid), dim3(RowsCfg<8>::NT), 0, st, A); break;
   }
+}
+
+// The stream launch with a workspace runs the kernel that also takes split segments.
+static int launch_rows(const QuadRowsArgs& A, int mt, hipStream_t st) {
+  if (A.ws != nullptr) launch_rows_t<true>(A, mt, st);
+  else launch_rows_t<false>(A, mt, st);
   PP_LAUNCH_CHECK();
   return PP_OK;
 }
@@ -839,13 +840,24 @@ extern "C" int pp_quad_stream_rows(int64_t M) {
   return cfg_rg(round_mt(M));
 }
 
+extern "C" int pp_quad_stream_chunk(int64_t M) {
+  if (M < 1 || M > 8) return 0;
+  switch (round_mt(M)) {
+    case 1: return RowsCfg<1>::NSEG * QSEG;
+    case 2: return RowsCfg<2>::NSEG * QSEG;
+    case 4: return RowsCfg<4>::NSEG * QSEG;
+    default: return RowsCfg<8>::NSEG * QSEG;
+  }
+}
+
 extern "C" int64_t pp_quad_stream_waves(int64_t M) {
   if (M < 1 || M > 8) return 0;
   return (int64_t)device_cu_count() * cfg_waves(round_mt(M));
 }
 
 extern "C" int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs, const pp_quad_seg* segs, int64_t n_segs,
-                              const int64_t* seg_bounds, int64_t n_waves, const pp_quad_item* tail_items,
+                              const int64_t* seg_bounds, int64_t n_waves, void* workspace,
+                              const pp_quad_item* tail_items,
                               int64_t n_tail, const float* const* luts, const float* scales,
                               const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n, int64_t n_codes,
                               const void* const* tails, const int64_t* tail_len, int64_t M, void* stream) {
@@ -874,6 +886,7 @@ extern "C" int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs, const 
     A.plug_vals = reinterpret_cast<const f16*>(plug_vals);
     A.plug_n = plug_n;
     A.M = (int)M;
+    A.ws = workspace;
     if (int rc = launch_rows(A, mt, st)) return rc;
   }
   if (n_tail > 0) {

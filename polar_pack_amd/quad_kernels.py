@@ -124,12 +124,14 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
         for o in outs:
             o.zero_()
         return outs
-    if a.stride(1) != 1 or a.data_ptr() % 8 or (M > 1 and a.stride(0) % 4):
-        a = a.contiguous()
     lut_ptrs, lut_dtype = _lut_args(luts)
     sc = nat.float_array(scales)
     pi, pv, pn, keep = _plug_args(plug, dev)
     L = nat.lib()
+    if M > 8 and _mfma_layout_ok(codes, K):
+        return _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
+    if a.stride(1) != 1 or a.data_ptr() % 8 or (M > 1 and a.stride(0) % 4):
+        a = a.contiguous()
     ws_bytes = L.pp_quad_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), codes.data_ptr(),
                                              codes.stride(0), codes.stride(1), pn, M, N, K)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
@@ -140,6 +142,43 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
                         M, N, K, ws.data_ptr() if ws is not None else None, ws_bytes, stream)
     nat.check(rc, "pp_quad_gemm")
     del keep
+    return outs
+
+
+def _mfma_layout_ok(codes, K):
+    """Codes of an (N,K) row-major block seen as (K,N): the layout the matrix-core path reads."""
+    return codes.stride(0) == 1 and codes.stride(1) >= K and codes.stride(1) % 4 == 0 and K % 8 == 0 \
+        and codes.data_ptr() % 16 == 0
+
+
+def _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
+    """More than 8 tokens: the matrix-core batch decode (pp_quad_mfma), plug starts per
+    (row, K slice) found on the device with searchsorted (quaternion_packer.py:188-189)."""
+    M, K = a.shape
+    N = codes.shape[1]
+    ldc = codes.stride(1)
+    if a.stride(1) != 1 or a.data_ptr() % 16 or (M > 1 and a.stride(0) % 8):
+        a = a.contiguous()
+    slices = max(1, min(K // 32, -(-int(L.pp_quad_mfma_waves()) // (-(-N // 16)))))
+    cols = -(-(-(-K // slices)) // 32) * 32
+    slices = -(-K // cols)
+    row_plug = None
+    if pn:
+        idx = keep[0].view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+        keys = (elem_base + torch.arange(N, device=dev, dtype=torch.int64)[:, None] * ldc
+                + torch.arange(slices, device=dev, dtype=torch.int64)[None, :] * cols).reshape(-1)
+        keys = torch.cat([keys, torch.tensor([elem_base + N * ldc], device=dev, dtype=torch.int64)])
+        row_plug = torch.searchsorted(idx, keys)
+    ws_bytes = L.pp_quad_mfma_workspace_size(M, N, slices)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = L.pp_quad_mfma(codes.data_ptr(), ldc, elem_base, a.data_ptr(), a.stride(0), lut_ptrs, lut_dtype, sc,
+                        keep[0].data_ptr() if pn else None, keep[1].data_ptr() if pn else None, pn,
+                        row_plug.data_ptr() if row_plug is not None else None, slices, cols,
+                        nat.ptr_array([o.data_ptr() for o in outs]), outs[0].stride(0), M, N, K,
+                        ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    nat.check(rc, "pp_quad_mfma")
+    del keep, row_plug, ws
     return outs
 
 

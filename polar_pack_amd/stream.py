@@ -31,7 +31,8 @@ from .quad_kernels import header_luts
 
 ITEM_DTYPE = np.dtype([("proj", "<i4"), ("row0", "<i4"), ("nrows", "<i4"), ("flags", "<i4"),
                        ("plug_lo", "<i8"), ("plug_hi", "<i8")])
-SEG_DTYPE = np.dtype([("proj", "<i4"), ("row0", "<i4"), ("row1", "<i4"), ("task0", "<i4"), ("plug_lo", "<i8")])
+SEG_DTYPE = np.dtype([("proj", "<i4"), ("row0", "<i4"), ("row1", "<i4"), ("task0", "<i4"), ("plug_lo", "<i8"),
+                      ("k0", "<i4"), ("k1", "<i4"), ("parts", "<i4"), ("reserved", "<i4"), ("acc_off", "<i8")])
 PROJ_DTYPE = np.dtype([("codes", "<u8"), ("ldc", "<i8"), ("pos0", "<i8"), ("x", "<u8"), ("x_sm", "<i8"),
                        ("out", "<u8", (4,)), ("o_sm", "<i8"), ("N", "<i4"), ("K", "<i4")])
 DUAL_PROJ_DTYPE = np.dtype([("codes", "<u8"), ("ldc", "<i8"), ("pos0", "<i8"), ("x", "<u8"), ("x_sm", "<i8"),
@@ -76,28 +77,90 @@ def wave_bounds(bytes_, n_waves):
     return np.maximum.accumulate(bounds)
 
 
-def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=4):
-    """Per-wave segments (SEG_DTYPE) and seg_bounds (n_waves + 1) for the rows below ``n``."""
+def split_factors(shapes, n, rows_per_task, n_waves, block=512):
+    """(slices, column blocks per slice) per projection, slices being whole blocks of
+    ``block`` columns (the kernel's chunk width): 1 slice when the launch has at least
+    half as many tasks as wavefronts (measured: splitting then costs more in partial-sum
+    traffic and pipeline restarts than it gains), else enough slices for about one item
+    per wavefront."""
+    proj, _, _ = plan_tasks(shapes, n, rows_per_task)
+    K = np.array([int(b) for _, b in shapes], np.int64)
+    blocks = np.maximum(1, (K + block - 1) // block)
+    if proj.size == 0 or 2 * proj.size >= n_waves:
+        return np.ones(len(shapes), np.int64), blocks
+    want = -(-n_waves // proj.size)
+    per = -(-blocks // np.minimum(want, blocks))          # blocks per slice
+    return -(-blocks // per), per
+
+
+def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=4, split=False, block=512):
+    """Per-wave segments (SEG_DTYPE), seg_bounds (n_waves + 1) and the workspace bytes
+    for the rows below ``n``.
+
+    Tasks (:func:`plan_tasks`) are the units; with ``split`` and few tasks per wavefront
+    (a single Linear with few rows) every task of a projection is cut into column slices of whole ``block``-column
+    chunks (:func:`split_factors`), the
+    slices of a projection ordered slice by slice.  The items are dealt to the wavefronts
+    in contiguous runs of equal bytes and each wavefront's run is cut into segments of
+    one projection and one slice.  The workspace of split launches holds one uint32
+    counter per task, then 4*M*N float32 accumulators per split projection.
+    """
     proj, row0, nrows = plan_tasks(shapes, n, rows_per_task)
-    tb = wave_bounds(task_bytes(proj, nrows, shapes, M, code_bytes), n_waves)
     if proj.size == 0:
-        return np.zeros(0, SEG_DTYPE), np.zeros(n_waves + 1, np.int64)
-    wave = np.searchsorted(tb, np.arange(proj.size), side="right") - 1
-    brk = np.ones(proj.size, bool)
-    brk[1:] = (wave[1:] != wave[:-1]) | (proj[1:] != proj[:-1])
+        return np.zeros(0, SEG_DTYPE), np.zeros(n_waves + 1, np.int64), 0
+    pos0, N, K, _ = full_rows(shapes, n)
+    tid = np.arange(proj.size, dtype=np.int64)
+    parts = np.ones(len(shapes), np.int64)
+    per = np.zeros(len(shapes), np.int64)
+    if split:
+        parts, per = split_factors(shapes, n, rows_per_task, n_waves, block)
+    if np.all(parts == 1):
+        it_task, it_k0, it_k1 = tid, np.zeros(proj.size, np.int64), K[proj]
+    else:
+        chunks = []
+        for p in range(len(shapes)):
+            ts = tid[proj == p]
+            if ts.size == 0:
+                continue
+            for sl in range(int(parts[p])):
+                k0 = sl * int(per[p]) * block
+                k1 = min(int(K[p]), (sl + 1) * int(per[p]) * block) if parts[p] > 1 else int(K[p])
+                chunks.append((ts, np.full(ts.size, k0, np.int64), np.full(ts.size, k1, np.int64)))
+        it_task = np.concatenate([c[0] for c in chunks])
+        it_k0 = np.concatenate([c[1] for c in chunks])
+        it_k1 = np.concatenate([c[2] for c in chunks])
+    it_proj = proj[it_task]
+    width = it_k1 - it_k0
+    ib = code_bytes * nrows[it_task] * width + 2 * M * width
+    tb = wave_bounds(ib, n_waves)
+    wave = np.searchsorted(tb, np.arange(it_task.size), side="right") - 1
+    brk = np.ones(it_task.size, bool)
+    brk[1:] = (wave[1:] != wave[:-1]) | (it_proj[1:] != it_proj[:-1]) | (it_k0[1:] != it_k0[:-1])
     first = np.flatnonzero(brk)
-    last = np.concatenate([first[1:], [proj.size]]) - 1
+    last = np.concatenate([first[1:], [it_task.size]]) - 1
     segs = np.zeros(first.size, SEG_DTYPE)
-    segs["proj"] = proj[first]
-    segs["row0"] = row0[first]
-    segs["row1"] = row0[last] + nrows[last]
-    segs["task0"] = first
-    pos0, _, K, _ = full_rows(shapes, n)
-    start = pos0[proj[first]] + row0[first] * K[proj[first]]
-    segs["plug_lo"] = np.searchsorted(plug_host, start, side="left")
+    fp = it_proj[first]
+    segs["proj"] = fp
+    segs["row0"] = row0[it_task[first]]
+    segs["row1"] = row0[it_task[last]] + nrows[it_task[last]]
+    segs["task0"] = it_task[first]
+    segs["plug_lo"] = np.searchsorted(plug_host, pos0[fp] + segs["row0"] * K[fp], side="left")
+    segs["k0"] = it_k0[first]
+    segs["k1"] = it_k1[first]
+    segs["parts"] = parts[fp]
+    ws_bytes = 0
+    if np.any(parts > 1):
+        base = (4 * proj.size + 255) // 256 * 64              # floats: after the counters, 256-byte aligned
+        acc_off = np.zeros(len(shapes), np.int64)
+        off = base
+        for p in np.flatnonzero(parts > 1):
+            acc_off[p] = off
+            off += 4 * M * int(N[p])
+        segs["acc_off"] = np.where(parts[fp] > 1, acc_off[fp], 0)
+        ws_bytes = 4 * off
     seg_wave = wave[first]
     bounds = np.searchsorted(seg_wave, np.arange(n_waves + 1), side="left").astype(np.int64)
-    return segs, bounds
+    return segs, bounds, ws_bytes
 
 
 def plan_task_plug(shapes, n, plug_host, rows_per_task):
@@ -160,7 +223,14 @@ def plan_tail_items(shapes, n, plug_host, tail_lengths=None, fp16_rows=0):
 
 
 class QuadStream:
-    def __init__(self, pack: QuadPackDevice, shapes: Sequence[Tuple[int, int]], M: int = 1):
+    """One-launch decode of many projections of a quad stream (``pp_quad_stream``).
+
+    ``split`` lets a launch with fewer row tasks than half its wavefronts (a single
+    Linear with few rows) cut its tasks into column slices whose sums meet in a
+    workspace owned by this object (so two launches of one QuadStream must not overlap).
+    """
+
+    def __init__(self, pack: QuadPackDevice, shapes: Sequence[Tuple[int, int]], M: int = 1, split: bool = True):
         L = nat.lib()
         self.pack = pack
         self.shapes = [(int(n), int(k)) for n, k in shapes]
@@ -179,12 +249,16 @@ class QuadStream:
                 raise ValueError(f"stream decode needs K % 4 == 0 (got N={n}, K={k})")
         plug = pack.plug_host()
         self.n_waves = int(L.pp_quad_stream_waves(self.M))
-        self.segs_np, self.bounds_np = plan_segments(self.shapes, pack.n, plug, self.n_waves, self.rows_per_item,
-                                                     self.M)
+        self.segs_np, self.bounds_np, ws_bytes = plan_segments(
+            self.shapes, pack.n, plug, self.n_waves, self.rows_per_item, self.M, split=split,
+            block=int(L.pp_quad_stream_chunk(self.M)))
         self.tail_items_np = plan_tail_items(self.shapes, pack.n, plug)
         self.n_segs = self.segs_np.size
         self.n_tail = self.tail_items_np.size
+        self.split = bool(np.any(self.segs_np["parts"] > 1))
         dev = self.device
+        # split launches: counters + accumulators, zero once here, left zero by every launch
+        self.workspace = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
         self.segs = torch.from_numpy(self.segs_np.view(np.uint8).copy()).to(dev)
         self.tail_items = torch.from_numpy(self.tail_items_np.view(np.uint8).copy()).to(dev)
         self.bounds = torch.from_numpy(self.bounds_np).to(dev)
@@ -239,6 +313,7 @@ class QuadStream:
         rc = nat.lib().pp_quad_stream(self.projs.data_ptr(), len(self.shapes),
                                       self.segs.data_ptr() if self.n_segs else None, self.n_segs,
                                       self.bounds.data_ptr(), self.n_waves,
+                                      self.workspace.data_ptr() if self.workspace is not None else None,
                                       self.tail_items.data_ptr() if self.n_tail else None, self.n_tail,
                                       self._lut_ptrs, self._scales,
                                       pk.plug_idx.data_ptr() if pk.plug_idx.numel() else None,
@@ -291,8 +366,8 @@ class DualStream:
             raise ValueError("dual stream decode needs a power-of-two group_size >= 8 and chunk_size % 8 == 0")
         plug = pack.plug_host()
         self.n_waves = int(L.pp_dual_stream_waves(self.M))
-        self.segs_np, self.bounds_np = plan_segments(self.shapes, pack.n_codes, plug, self.n_waves,
-                                                     self.rows_per_item, self.M, code_bytes=2)
+        self.segs_np, self.bounds_np, _ = plan_segments(self.shapes, pack.n_codes, plug, self.n_waves,
+                                                        self.rows_per_item, self.M, code_bytes=2)
         tails = list(pack.tails) + [None] * (2 - len(pack.tails))
         aligned = pack.n_codes % 8 == 0 and all(t is None or t.numel() == 0 or t.data_ptr() % 16 == 0
                                                 for t in tails)
@@ -393,3 +468,92 @@ class DualStream:
             tail_w = sum(max(0, min(hi, n + t) - max(lo, n)) for t in self.pack.tail_lengths)
             total += 2 * in_codes + 2 * (-(-in_codes // gs)) + 6 * P + 2 * self.M * K + 4 * self.M * N + 2 * tail_w
         return total
+
+
+def mfma_slices(N, K, waves):
+    """(slices, slice_cols) for the batch decode of an (N, K) projection: enough K slices
+    of whole 32-column steps for about one 16-row x slice item per wavefront."""
+    tiles = -(-int(N) // 16)
+    s = max(1, min(int(K) // 32, -(-int(waves) // tiles)))
+    cols = -(-int(K) // s)
+    cols = -(-cols // 32) * 32
+    return -(-int(K) // cols), cols
+
+
+def mfma_row_plug(plug_host, pos0, N, K, ldc, slices, cols):
+    """First plug entry at or after each (row, slice) start, then the end of the projection."""
+    keys = (int(pos0) + np.arange(int(N), dtype=np.int64)[:, None] * int(ldc)
+            + np.arange(int(slices), dtype=np.int64)[None, :] * int(cols)).reshape(-1)
+    keys = np.concatenate([keys, [int(pos0) + int(N) * int(ldc)]])
+    return np.searchsorted(plug_host, keys, side="left").astype(np.int64)
+
+
+class QuadBatch:
+    """Batch decode of one projection of a quad stream on the matrix cores
+    (``pp_quad_mfma``, 1..64 tokens): the (N, K) block at stream position ``pos0``.
+
+    The K slices and their plug starts are planned once; with several slices the float32
+    accumulators live in a workspace owned by this object (two launches of one QuadBatch
+    must not overlap).
+    """
+
+    def __init__(self, pack: QuadPackDevice, N: int, K: int, pos0: int = 0, M: int = 16, slices=None):
+        L = nat.lib()
+        self.pack = pack
+        self.N, self.K, self.pos0, self.M = int(N), int(K), int(pos0), int(M)
+        if not 1 <= self.M <= 64:
+            raise ValueError("the batch decode takes 1..64 tokens")
+        if self.K % 8 or self.pos0 + self.N * self.K > pack.n:
+            raise ValueError("needs K % 8 == 0 and the projection inside the coded stream")
+        self.device = pack.codes.device
+        if slices is None:
+            self.slices, self.cols = mfma_slices(self.N, self.K, int(L.pp_quad_mfma_waves()))
+        else:
+            self.slices = int(slices)
+            cols = -(-self.K // self.slices)
+            self.cols = -(-cols // 32) * 32
+            self.slices = -(-self.K // self.cols)
+        plug = pack.plug_host()
+        self.row_plug = torch.from_numpy(mfma_row_plug(plug, self.pos0, self.N, self.K, self.K, self.slices,
+                                                       self.cols)).to(self.device)
+        lo, hi = np.searchsorted(plug, [self.pos0, self.pos0 + self.N * self.K])
+        self.n_plug = int(hi - lo)
+        ws = int(L.pp_quad_mfma_workspace_size(self.M, self.N, self.slices))
+        self.workspace = torch.zeros(ws, dtype=torch.uint8, device=self.device) if ws else None
+        self.luts = header_luts(pack.r_max, device=self.device)
+        self._lut_ptrs = nat.ptr_array([t.data_ptr() for t in self.luts])
+        self._scales = nat.float_array(pack.s)
+        self.x = self.outs = None
+
+    def make_buffers(self):
+        x = torch.empty((self.M, self.K), dtype=torch.float16, device=self.device)
+        return x, [torch.empty((self.M, self.N), dtype=torch.float16, device=self.device) for _ in range(4)]
+
+    def bind(self, x: torch.Tensor, outs: List[torch.Tensor]):
+        if x.shape != (self.M, self.K) or x.dtype != torch.float16 or x.stride(1) != 1 or x.data_ptr() % 16 \
+                or (self.M > 1 and x.stride(0) % 8):
+            raise ValueError(f"activations must be fp16 ({self.M}, {self.K}), unit stride, 16-byte aligned rows")
+        if len(outs) != 4 or any(o.shape != (self.M, self.N) or o.dtype != torch.float16 or o.stride(1) != 1
+                                 or o.stride(0) != outs[0].stride(0) for o in outs):
+            raise ValueError(f"4 fp16 outputs ({self.M}, {self.N}) with one row stride")
+        self.x, self.outs = x, outs
+        self._out_ptrs = nat.ptr_array([o.data_ptr() for o in outs])
+
+    def __call__(self):
+        if self.x is None:
+            raise RuntimeError("QuadBatch.bind() must be called before launching")
+        pk = self.pack
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        rc = nat.lib().pp_quad_mfma(pk.codes.data_ptr() + 4 * self.pos0, self.K, self.pos0, self.x.data_ptr(),
+                                    self.x.stride(0), self._lut_ptrs, nat.PP_F32, self._scales,
+                                    pk.plug_idx.data_ptr() if pk.plug_idx.numel() else None,
+                                    pk.plug_vals.data_ptr() if pk.plug_vals.numel() else None,
+                                    int(pk.plug_idx.numel()), self.row_plug.data_ptr(), self.slices, self.cols,
+                                    self._out_ptrs, self.outs[0].stride(0), self.M, self.N, self.K,
+                                    self.workspace.data_ptr() if self.workspace is not None else None,
+                                    int(self.workspace.numel()) if self.workspace is not None else 0, stream)
+        nat.check(rc, "pp_quad_mfma")
+
+    def algorithmic_bytes(self) -> int:
+        """4*N*K codes + 12 B per plug entry + 2*M*K x + 8*M*N outputs."""
+        return 4 * self.N * self.K + 12 * self.n_plug + 2 * self.M * self.K + 8 * self.M * self.N

@@ -6,7 +6,7 @@ import torch
 import gen
 from oracle import layer as olay
 from oracle import quadpack as oqp
-from parity import assert_dequant_close, assert_gemv_close
+from parity import normwise, assert_dequant_close, assert_gemv_close
 from polar_pack_amd import quad_kernels as qk
 
 pytestmark = pytest.mark.gpu
@@ -99,9 +99,20 @@ def test_quad_gemm_matches_oracle(K, N, layout, M):
     a = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
     outs = qk.quad_bitpacked(a.to(DEV), view, [l.to(DEV) for l in luts], scales)
     W = oracle_w(codes, luts, scales)
+    # more than 8 tokens on (N,K) rows: the matrix-core path, fp16 weights into the dot
+    # product (as the reference's tl.dot); held to the fp16-rounded decode + the fp32
+    # dot-product bound (see test_gpu_mfma.py)
+    mfma = M > 8 and layout == "nk" and K % 8 == 0
+    W32 = olay.quad_dequant(codes, [l.float().numpy() for l in luts], dtype=np.float32) if mfma else None
     for k in range(4):
         assert outs[k].shape == (M, N) and outs[k].dtype == torch.float16
-        assert_gemv_close(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), W[k]), f"model {k}")
+        w = W[k]
+        bound = None
+        if mfma:
+            w = W32[k].astype(np.float16).astype(np.float64) * float(np.float32(scales[k]))
+            bound = 2.0 ** -18 * (np.abs(a.numpy().astype(np.float64)) @ np.abs(w))
+            assert normwise(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), W[k])) <= 1e-3
+        assert_gemv_close(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), w), f"model {k}", bound=bound)
 
 
 @pytest.mark.parametrize("M", [1, 4, 8])

@@ -44,14 +44,16 @@ def oracle_outputs(qp, xs):
     return outs
 
 
+@pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
-def test_stream_matches_oracle_with_plug_and_tails(tmp_path, M):
+def test_stream_matches_oracle_with_plug_and_tails(tmp_path, M, split):
     tails = (0, 12 * 512 - 5 * 512 - 100 + 7, 1000, 12 * 512 - 5 * 512 - 100)
     qp, path = make_file(tmp_path, tails)
     f = QuadPackFile.read(path)
     assert f.n == qp.n and f.plug_idx.size == qp.plug_idx.size > 0
     pack = f.to_device(DEV)
-    st = QuadStream(pack, SHAPES, M=M)
+    st = QuadStream(pack, SHAPES, M=M, split=split)
+    assert st.split == split                      # few tasks per wavefront: the planner splits
     xs_np = [np.random.default_rng(100 + p).standard_normal((M, k)).astype(np.float16) for p, (_, k) in enumerate(SHAPES)]
     xs = [torch.from_numpy(x).to(DEV) for x in xs_np]
     outs = [[torch.full((M, n), float("nan"), dtype=torch.float16, device=DEV) for _ in range(4)] for n, _ in SHAPES]
@@ -106,3 +108,30 @@ def test_container_file_round_trip_and_validation(tmp_path):
     bad.write_bytes(path.read_bytes()[:-3])
     with pytest.raises(ValueError, match="shorter|implies"):
         QuadPackFile.read(bad)
+
+
+@pytest.mark.parametrize("shape", [(256, 2048), (64, 11008), (1000, 1000), (512, 1536)])
+@pytest.mark.parametrize("M", [1, 2, 8])
+def test_single_linear_split_k(shape, M):
+    """One projection, its tasks cut into column slices that meet in the workspace: equal
+    to the oracle, on repeated launches, and the workspace is left zero."""
+    N, K = shape
+    models = gen.correlated_models(7, [N * K] * 4)
+    qp = oqp.pack_quad(models, threshold=0.004)
+    pack = QuadPackFile(n=qp.n, s=qp.s, r_max=qp.r_max, codes=qp.codes, plug_idx=qp.plug_idx,
+                        plug_vals=qp.plug_vals).to_device(DEV)
+    st = QuadStream(pack, [shape], M=M)
+    assert st.split and st.workspace is not None
+    x_np = np.random.default_rng(5).standard_normal((M, K)).astype(np.float16)
+    xs = [torch.from_numpy(x_np).to(DEV)]
+    outs = [[torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV) for _ in range(4)]]
+    st.bind(xs, outs)
+    W = oqp.unpack_quad_f64(qp, 0, N * K)
+    for rep in range(3):
+        st()
+        torch.cuda.synchronize()
+        for m in range(4):
+            ref = x_np.astype(np.float64) @ W[m].reshape(N, K).T
+            assert_gemv_close(outs[0][m].float().cpu().numpy(), ref, f"rep {rep} model {m}")
+        assert int(torch.count_nonzero(st.workspace)) == 0
+

@@ -213,6 +213,30 @@ def test_quad_layer_dequant_matches_container_decode():
         np.testing.assert_allclose(a[k][0], b[k], rtol=1e-12, atol=1e-15)
 
 
+def test_quad_layer_dequant_float32_mode_is_the_rounded_float64():
+    """The float32 evaluation is the float64 decode up to the 3 roundings of its products
+    (and the float32 LUTs), and every value is exactly a float32 product chain."""
+    c = all_codes_sample(20000)
+    i = np.arange(256, dtype=np.float64)
+    r_max = 6.25
+    luts64 = [(np.exp(i / 255 * math.log1p(255.0)) - 1) * r_max / 255.0,
+              np.cos(i / 255 * np.pi), np.sin(i / 255 * np.pi), np.cos(i / 255 * np.pi), np.sin(i / 255 * np.pi),
+              np.cos(i / 255 * 2 * np.pi), np.sin(i / 255 * 2 * np.pi)]
+    luts32 = [l.astype(np.float32) for l in luts64]
+    a = olay.quad_dequant(c.reshape(1, -1), luts32, dtype=np.float32)
+    b = olay.quad_dequant(c.reshape(1, -1), luts32)                    # float64 on the same LUTs
+    for k in range(4):
+        assert a[k].dtype == np.float32
+        np.testing.assert_allclose(a[k], b[k], rtol=4 * 2.0 ** -24, atol=1e-30)
+    # spot-check one word against an explicit float32 chain
+    w = int(c[123])
+    nq, q1, q2, q3 = w >> 24, (w >> 16) & 255, (w >> 8) & 255, w & 255
+    r = luts32[0][nq]
+    rs = np.float32(r * luts32[2][q1])
+    rss = np.float32(rs * luts32[4][q2])
+    assert a[2][0, 123] == np.float32(rss * luts32[5][q3]) and a[1][0, 123] == np.float32(rs * luts32[3][q2])
+
+
 def test_dual_layer_dequant_group_index_and_offset():
     K, N = 5, 40
     rng = np.random.default_rng(2)

@@ -23,7 +23,7 @@ def seg_coverage(segs, shapes):
 def test_segments_cover_every_row_once(rpt, waves):
     shapes = [(37, 2048), (5, 11008), (8, 256), (3, 4100)]
     n = sum(a * b for a, b in shapes)
-    segs, bounds = plan_segments(shapes, n, np.zeros(0, np.uint32), waves, rpt)
+    segs, bounds, _ = plan_segments(shapes, n, np.zeros(0, np.uint32), waves, rpt)
     for c in seg_coverage(segs, shapes):
         assert c.min() == 1 and c.max() == 1
     assert bounds.size == waves + 1 and bounds[0] == 0 and bounds[-1] == segs.size
@@ -38,7 +38,7 @@ def test_tail_rows_and_plug_ranges():
     shapes = [(4, 100), (6, 64)]
     n = 4 * 100 + 2 * 64 + 10           # projection 1: rows 0-1 in codes, row 2 straddles, rows 3-5 tail
     plug = np.array([5, 99, 100, 399, 400, 463, 464, 527, 528, 537], np.uint32)
-    segs, bounds = plan_segments(shapes, n, plug, 3, 4)
+    segs, bounds, _ = plan_segments(shapes, n, plug, 3, 4)
     tail = plan_tail_items(shapes, n, plug)
     assert list(tail["proj"]) == [1, 1, 1, 1] and list(tail["row0"]) == [2, 3, 4, 5]
     assert np.all(tail["flags"] == nat.PP_ITEM_TAIL) and np.all(tail["nrows"] == 1)
@@ -72,7 +72,7 @@ def test_struct_layouts_match_abi():
     assert ITEM_DTYPE.itemsize == ctypes.sizeof(nat.QuadItem) == 32
     for name, _ in nat.QuadItem._fields_:
         assert getattr(nat.QuadItem, name).offset == ITEM_DTYPE.fields[name][1]
-    assert SEG_DTYPE.itemsize == ctypes.sizeof(nat.QuadSeg) == 24
+    assert SEG_DTYPE.itemsize == ctypes.sizeof(nat.QuadSeg) == 48
     for name, _ in nat.QuadSeg._fields_:
         assert getattr(nat.QuadSeg, name).offset == SEG_DTYPE.fields[name][1]
     assert DUAL_PROJ_DTYPE.itemsize == ctypes.sizeof(nat.DualProj) == 72
@@ -99,7 +99,7 @@ def test_task_plug_ranges_partition_the_plug_table():
             assert np.all((sel >= lo) & (sel < hi))
             assert np.count_nonzero((plug >= lo) & (plug < hi)) == sel.size
         assert np.all(nck == (K[proj] + 511) // 512)
-    segs, _ = plan_segments(shapes, n, plug, 16, 4, code_bytes=2)
+    segs, _, _ = plan_segments(shapes, n, plug, 16, 4, code_bytes=2)
     proj, row0, _ = plan_tasks(shapes, n, 4)
     assert np.all(proj[segs["task0"]] == segs["proj"]) and np.all(row0[segs["task0"]] == segs["row0"])
 
@@ -132,3 +132,44 @@ def test_tail_items_fp16_runs():
     assert int((it["flags"] == 1).sum()) == 2            # the row across n, the row across model 2's tail end
     plain = plan_tail_items(shapes, n, plug)
     assert np.all(plain["flags"] == 1) and np.all(plain["nrows"] == 1) and plain.size == len(expect)
+
+
+@pytest.mark.parametrize("shape,waves", [((11008, 2048), 8192), ((2048, 11008), 2048), ((256, 2048), 2048),
+                                         ((40, 1000), 64)])
+def test_split_segments_cover_every_task_slice_once(shape, waves):
+    N, K = shape
+    shapes = [shape]
+    n = N * K
+    plug = np.sort(np.random.default_rng(1).choice(n, 500, replace=False)).astype(np.uint32)
+    rpt = 8
+    segs, bounds, ws = plan_segments(shapes, n, plug, waves, rpt, split=True)
+    parts = int(segs["parts"][0])
+    assert np.all(segs["parts"] == parts) and parts > 1
+    ntask = -(-N // rpt)
+    assert ws >= 4 * ntask + 4 * 4 * N
+    # every (task, column) pair covered exactly once, slices on 512-column boundaries
+    cover = np.zeros((ntask, K), np.int32)
+    for g in segs:
+        assert g["k0"] % 512 == 0 and (g["k1"] % 512 == 0 or g["k1"] == K) and g["k0"] < g["k1"] <= K
+        t0 = g["row0"] // rpt
+        assert g["task0"] == t0 and g["plug_lo"] == np.searchsorted(plug, g["row0"] * K)
+        for t in range(t0, -(-g["row1"] // rpt)):
+            cover[t, g["k0"]:g["k1"]] += 1
+        assert g["acc_off"] * 4 >= 4 * ntask and g["acc_off"] % 64 == 0
+        assert (g["acc_off"] + 4 * N) * 4 <= ws
+    assert np.all(cover == 1)
+    # each task is cut into exactly `parts` slices
+    slices = {}
+    for g in segs:
+        for t in range(g["row0"] // rpt, -(-g["row1"] // rpt)):
+            slices.setdefault(t, set()).add(int(g["k0"]))
+    assert all(len(v) == parts for v in slices.values())
+    assert np.all(np.diff(bounds) >= 0) and bounds[-1] == segs.size
+
+
+def test_large_streams_are_not_split():
+    shapes = [(2048, 2048), (11008, 2048)] * 20
+    n = sum(a * b for a, b in shapes)
+    segs, _, ws = plan_segments(shapes, n, np.zeros(0, np.uint32), 2048, 8, split=True)
+    assert np.all(segs["parts"] == 1) and ws == 0
+    assert np.all(segs["k0"] == 0) and np.all(segs["k1"] == np.array([b for _, b in shapes])[segs["proj"]])
