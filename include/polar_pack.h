@@ -181,7 +181,7 @@ typedef struct pp_quad_item {
  * Batch decode GEMM on the matrix cores (1..64 tokens; used for more than 8):
  *   out_m[i, n] = fp16( s_m * sum_k a[i, k] * W_m[n, k] ),   m = 0..3,
  * for codes laid out (N,K) row-major (row n at codes + n*ldc: the container stream
- * layout, the reference's (K,N) view of it with c_sk == 1), K % 8 == 0.  Each 16-row
+ * layout, the reference's (K,N) view of it with c_sk == 1), K % 32 == 0.  Each 16-row
  * tile is decoded into fp16 MFMA operands in registers; plug entries (normalised tuples,
  * positions relative to elem_base like pp_quad_gemm) are patched into the decoded
  * tile.  K is cut into `slices` column ranges of slice_cols (a multiple of 32) columns;
@@ -200,8 +200,8 @@ int pp_quad_mfma(const uint32_t* codes, int64_t ldc, int64_t elem_base, const vo
                  int64_t slices, int64_t slice_cols, void* const* out, int64_t o_sm,
                  int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream);
 int64_t pp_quad_mfma_workspace_size(int64_t M, int64_t N, int64_t slices);
-/* Wavefronts the batch decode launches (the host sizes the slices for them). */
-int64_t pp_quad_mfma_waves(void);
+/* Wavefronts the batch decode launches for M tokens (the host sizes the slices for them). */
+int64_t pp_quad_mfma_waves(int64_t M);
 
 /* Rows per wavefront task the stream decode uses for M tokens (0 and an error for bad M). */
 int pp_quad_stream_rows(int64_t M);

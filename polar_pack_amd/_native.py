@@ -58,7 +58,7 @@ EXPORTS = {
     "pp_quad_mfma": (i32, [vp, i64, i64, vp, i64, vp, i32, vp, vp, vp, i64, vp, i64, i64, vp, i64, i64, i64, i64,
                            vp, i64, vp]),
     "pp_quad_mfma_workspace_size": (i64, [i64, i64, i64]),
-    "pp_quad_mfma_waves": (i64, []),
+    "pp_quad_mfma_waves": (i64, [i64]),
     "pp_quad_stream_rows": (i32, [i64]),
     "pp_quad_stream_chunk": (i32, [i64]),
     "pp_quad_stream_waves": (i64, [i64]),

@@ -175,10 +175,10 @@ __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const Dual
   }
   if constexpr (MT == 1) {
     const rsrc_t rx = make_rsrc(S.x + kc, 2u * (uint32_t)(S.K - kc));
-    vload128(c.xr[0], 16u * lane, rx);
+    vload128c(c.xr[0], 16u * lane, rx);
   } else {
 #pragma unroll
-    for (int j = 0; j < MT; ++j) vload128(c.xr[j], k < S.K ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
+    for (int j = 0; j < MT; ++j) vload128c(c.xr[j], k < S.K ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
   }
 }
 
@@ -577,7 +577,7 @@ __device__ __forceinline__ void dual_tail_rows(const DualTailArgs& T, const pp_q
     const bool kin = k < K;
     u32x4 xr[MT];
 #pragma unroll
-    for (int j = 0; j < MT; ++j) vload128(xr[j], (kin && j < M) ? 2u * (uint32_t)(j * x_sm + k) : OOB, rx);
+    for (int j = 0; j < MT; ++j) vload128c(xr[j], (kin && j < M) ? 2u * (uint32_t)(j * x_sm + k) : OOB, rx);
     u32x4 wr[R][2];
 #pragma unroll
     for (int r = 0; r < R; ++r)

@@ -20,8 +20,8 @@
 // replaces the decoded tuple by the plug values before rounding.
 // Slices: with one slice a wave writes its fp16 outputs; otherwise it adds its scaled
 // sums into float32 accumulators [m][n][j] with device-scope atomics (no return, so
-// nothing waits on them) and quad_mfma_finish_kernel, launched after, swaps the totals
-// out (leaving zeros for the next launch) and writes the outputs.
+// nothing waits on them) and quad_mfma_finish_kernel, launched after, reads the totals,
+// writes the outputs and leaves zeros for the next launch.
 #include "quad_lds.h"
 #include "rows_common.h"
 
@@ -30,7 +30,17 @@ namespace pp {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int MF_NT = 512;   // threads per workgroup: 8 waves, one workgroup per CU (the tables take all of LDS)
+// Threads per workgroup (one workgroup per CU: the tables take all of LDS), by token
+// tiles: as many waves as the registers allow (4, 3, 2 per SIMD for 1, 2, 4 tiles), for
+// the memory parallelism of a latency-bound walk.
+// SUB: 32-column MFMA steps per stage.  A stage is what one load step brings in: SUB x 2
+// KiB of codes per wave; 1 step (2 KiB) per stage left the waves waiting a full HBM round
+// trip per step, 4 steps (8 KiB, as much as the row kernel keeps in flight) hide it.
+// With 4 token tiles the x operands of 4 steps would not fit in registers: 2.
+template <int T> struct MfCfg {
+  static constexpr int NT = 512;
+  static constexpr int SUB = T == 4 ? 2 : 4;
+};
 
 struct QuadMfmaArgs {
   const uint32_t* codes;   // code of (row 0, col 0); row n at codes + n*ldc
@@ -54,69 +64,171 @@ struct QuadMfmaArgs {
 
 template <int T>
 struct MStage {
-  u32x4 c0, c1;            // 8 code words of the lane's row
-  u32x4 xb[T];             // 8 fp16 x of token 16t + l%16
+  static constexpr int SUB = MfCfg<T>::SUB;
+  u32x4 c[SUB][2];         // per step: 8 code words of the lane's row
+  u32x4 xb[SUB][T];        // per step: 8 fp16 x of token 16t + l%16
 };
 
+// Issue the loads of the step at column k0.  Each lane's offsets are fixed for the item
+// (voc for its row's codes, vox[t] for token 16t + l%16; OOB for rows or tokens past the
+// end); the buffer resources are rebased to k0 in scalar registers, so a step needs no
+// vector address arithmetic.  K and the slices are multiples of 32 columns, so every
+// lane's 8 columns of a step are in range (a step past the slice end reads data it never
+// uses).
 template <int T>
-__device__ __forceinline__ void mstage_issue(const QuadMfmaArgs& A, rsrc_t rc, rsrc_t rx, int ri, int q, bool rowok,
-                                             int k0, int ke, MStage<T>& S) {
-  const int kk = k0 + 8 * q;
-  const bool valid = kk < ke;
-  const uint32_t co = (rowok && valid) ? 4u * (uint32_t)(ri * A.ldc + kk) : OOB;
-  vload128(S.c0, co, rc);
-  vload128(S.c1, co == OOB ? OOB : co + 16u, rc);
+__device__ __forceinline__ void mstage_issue(const QuadMfmaArgs& A, const uint32_t* ctile, int nrows, uint32_t voc,
+                                             const uint32_t (&vox)[T], int k0, MStage<T>& S) {
+  constexpr int SUB = MfCfg<T>::SUB;
+  k0 = min(k0, A.K);   // look-ahead past the end: rebase at K (nothing read there is used)
+  const rsrc_t rc = make_rsrc(ctile + k0, 4u * (uint32_t)((int64_t)(nrows - 1) * A.ldc + (A.K - k0)));
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    const int j = 16 * t + ri;
-    vload128(S.xb[t], (valid && j < A.M) ? 2u * (uint32_t)(j * A.x_sm + kk) : OOB, rx);
+  for (int u = 0; u < SUB; ++u) {
+    vload128(S.c[u][0], voc + 128u * u, rc);
+    vload128(S.c[u][1], voc + 128u * u + 16u, rc);
   }
+  const rsrc_t rx = make_rsrc(A.x + k0, 2u * (uint32_t)((int64_t)(A.M - 1) * A.x_sm + (A.K - k0)));
+#pragma unroll
+  for (int u = 0; u < SUB; ++u)
+#pragma unroll
+    for (int t = 0; t < T; ++t) vload128c(S.xb[u][t], vox[t] + 64u * u, rx);
 }
 
-// The lane's window of 4 plug entries of its row: columns (INT_MAX past the end) and values.
+// The lane's window of 4 plug entries of its row: columns (INT_MAX past the end, INT_MIN
+// once applied) and values.
 struct MPlug {
   int k[4];
   u32x2 v[4];
   int64_t next, end;       // next entry to load, end of the row's entries in the slice
 };
 
-__device__ __forceinline__ void mplug_fill(const QuadMfmaArgs& A, int64_t rowpos, MPlug& P) {
+// Load the next 4 entries of the row (bounds-checked buffer loads, nothing past `end`).
+__device__ __forceinline__ void mplug_issue(const QuadMfmaArgs& A, MPlug& P, uint32_t (&idx)[4]) {
+  const rsrc_t ri = make_rsrc(A.plug_idx, 4u * (uint32_t)A.plug_n);
+  const rsrc_t rv = make_rsrc(A.plug_vals, 8u * (uint32_t)A.plug_n);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t e = P.next + i;
     const bool has = e < P.end;
-    P.k[i] = has ? (int)((int64_t)A.plug_idx[e] - rowpos) : 0x7FFFFFFF;
-    P.v[i] = has ? *reinterpret_cast<const u32x2*>(A.plug_vals + 4 * e) : u32x2{0u, 0u};
+    vload32(idx[i], has ? 4u * (uint32_t)e : OOB, ri);
+    vload64(P.v[i], has ? 8u * (uint32_t)e : OOB, rv);
   }
+}
+__device__ __forceinline__ void mplug_take(MPlug& P, const uint32_t (&idx)[4], int64_t rowpos) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) P.k[i] = P.next + i < P.end ? (int)((int64_t)idx[i] - rowpos) : 0x7FFFFFFF;
   P.next += 4;
 }
 
+// Decode 8 code words into the fp16 A operands of the 4 models (each tuple rounded
+// once, as soon as it is decoded: the fp32 values are not kept).
 template <class L>
 __device__ __forceinline__ void decode8(const char* lds, const LaneOff& lo, const u32x4& c0, const u32x4& c1,
-                                        float (&w)[4][8]) {
+                                        h8 (&a)[4]) {
   const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float r;
-    float2 a, b, c;
-    lookup<L>(lds, cw[e], lo, r, a, b, c);
-    const float rs = r * a.y, rss = rs * b.y;
-    w[0][e] = r * a.x;
-    w[1][e] = rs * b.x;
-    w[2][e] = rss * c.x;
-    w[3][e] = rss * c.y;
+    float2 ta, tb, tc;
+    lookup<L>(lds, cw[e], lo, r, ta, tb, tc);
+    const float rs = r * ta.y, rss = rs * tb.y;
+    a[0][e] = (_Float16)(r * ta.x);
+    a[1][e] = (_Float16)(rs * tb.x);
+    a[2][e] = (_Float16)(rss * tc.x);
+    a[3][e] = (_Float16)(rss * tc.y);
   }
 }
+
+// The slice walk of one item: step(cur, pre, k0) issues the loads of step k0 + 32 into
+// pre, decodes cur (step k0) into the MFMA operands, patches the plug entries and
+// accumulates; returns false after the last step.  Called alternately on two stage
+// buffers (the shape of the row kernel's walk), so every load is consumed one step after
+// it was issued.  (A ring of 4 stages measured no faster: the compiler's waits still
+// drained it to one step ahead.)
+template <int T, class L>
+struct MRun {
+  const char* lds;
+  LaneOff lo;
+  const QuadMfmaArgs& A;
+  const uint32_t* ctile;
+  int nrows;
+  uint32_t voc;
+  uint32_t vox[T];
+  int q;
+  int ke;
+  int64_t rowpos;
+  MPlug P;
+  f4 C[4][T];
+
+  __device__ __forceinline__ bool step(const MStage<T>& cur, MStage<T>& pre, int& k0) {
+    constexpr int SUB = MfCfg<T>::SUB;
+    mstage_issue<T>(A, ctile, nrows, voc, vox, k0 + 32 * SUB, pre);
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) {
+      const int ks = k0 + 32 * u;
+      if (ks >= ke) break;   // the slice ends inside the stage (wave-uniform)
+      h8 a[4];
+      decode8<L>(lds, lo, cur.c[u][0], cur.c[u][1], a);
+      const int kk = ks + 8 * q;
+      // entries in this lane's 8 columns: replace the operands by the plug values, one
+      // entry per pass (two in one lane's 8 columns of one step are rare); a window used
+      // up within the step is refilled
+      for (;;) {
+        int hit = -1;
+#pragma unroll
+        for (int i = 3; i >= 0; --i) hit = (unsigned)(P.k[i] - kk) < 8u ? i : hit;
+        if (__ballot(hit >= 0)) {
+          const int e = hit >= 0 ? (hit == 0 ? P.k[0] : hit == 1 ? P.k[1] : hit == 2 ? P.k[2] : P.k[3]) - kk : -1;
+          const u32x2 pv2 = hit == 0 ? P.v[0] : hit == 1 ? P.v[1] : hit == 2 ? P.v[2] : P.v[3];
+          const f16x4 pv = __builtin_bit_cast(f16x4, pv2);
+          const _Float16 v[4] = {(_Float16)pv.x, (_Float16)pv.y, (_Float16)pv.z, (_Float16)pv.w};
+#pragma unroll
+          for (int ee = 0; ee < 8; ++ee)
+#pragma unroll
+            for (int m = 0; m < 4; ++m) a[m][ee] = e == ee ? v[m] : a[m][ee];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) P.k[i] = hit == i ? (int)0x80000000 : P.k[i];
+          continue;
+        }
+        const bool refill = P.k[3] < ks + 32 && P.next < P.end;
+        if (!__ballot(refill)) break;
+        // rare: load and wait here, so no load is left in flight past this branch (a
+        // possibly pending load would make every later wait drain the prefetch too)
+        uint32_t idx[4];
+        MPlug R = P;
+        mplug_issue(A, R, idx);
+        asm volatile("" : : "v"(idx[0]), "v"(idx[1]), "v"(idx[2]), "v"(idx[3]), "v"(R.v[0]), "v"(R.v[1]),
+                     "v"(R.v[2]), "v"(R.v[3]));
+        mplug_take(R, idx, rowpos);
+        if (refill) P = R;
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const h8 b = __builtin_bit_cast(h8, cur.xb[u][t]);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) C[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b, C[m][t], 0, 0, 0);
+      }
+    }
+    k0 += 32 * MfCfg<T>::SUB;
+    return k0 < ke;
+  }
+};
 
 template <int T, class L>
 __device__ __forceinline__ void mfma_body(const char* lds, const QuadMfmaArgs& A) {
   const int lane = threadIdx.x & 63, ri = lane & 15, q = lane >> 4;
   const LaneOff lo = L::lane(lane);
-  constexpr int WAVES = MF_NT / 64;
-  const int64_t gw = (int64_t)blockIdx.x * WAVES + uniform(threadIdx.x >> 6);
+  constexpr int WAVES = MfCfg<T>::NT / 64;
+  // items are dealt round-robin over the workgroups (item i to workgroup i % grid), so a
+  // launch with fewer items than wavefronts still spreads them over every CU
+  const int64_t gw = (int64_t)uniform(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
   const int64_t nw = (int64_t)gridDim.x * WAVES;
   const int64_t items = A.tiles * A.slices;
-  const rsrc_t rx = make_rsrc(A.x, 2u * (uint32_t)((int64_t)(A.M - 1) * A.x_sm + A.K));
+  uint32_t vox[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int j = 16 * t + ri;
+    vox[t] = j < A.M ? 2u * (uint32_t)(j * A.x_sm + 8 * q) : OOB;
+  }
   for (int64_t it = gw; it < items; it += nw) {
     const int tile = (int)uniform64(it / A.slices), sl = (int)uniform64(it % A.slices);
     const int n0 = tile * 16;
@@ -124,68 +236,31 @@ __device__ __forceinline__ void mfma_body(const char* lds, const QuadMfmaArgs& A
     const int nrows = min(16, A.N - n0);
     const int n = n0 + ri;
     const bool rowok = ri < nrows;
-    const rsrc_t rc = make_rsrc(A.codes + (int64_t)n0 * A.ldc, 4u * (uint32_t)((int64_t)(nrows - 1) * A.ldc + A.K));
-    MStage<T> s0, s1;
-    mstage_issue<T>(A, rc, rx, ri, q, rowok, kb, ke, s0);
-    // the row's plug entries in this slice
+    const uint32_t* ctile = A.codes + (int64_t)n0 * A.ldc;
+    const uint32_t voc = rowok ? 4u * (uint32_t)(ri * A.ldc + 8 * q) : OOB;
+    // the row's plug entries in this slice: the first window, then the first step's loads
     MPlug P;
     P.next = rowok && A.plug_n > 0 ? A.row_plug[(int64_t)n * A.slices + sl] : 0;
     P.end = rowok && A.plug_n > 0 ? A.row_plug[(int64_t)n * A.slices + sl + 1] : 0;
     const int64_t rowpos = A.pos0 + (int64_t)n * A.ldc;
-    mplug_fill(A, rowpos, P);
-    f4 C[4][T];
+    uint32_t pidx[4];
+    mplug_issue(A, P, pidx);
+    MStage<T> s0, s1;
+    mstage_issue<T>(A, ctile, nrows, voc, vox, kb, s0);
+    mplug_take(P, pidx, rowpos);
+    MRun<T, L> R{lds, lo, A, ctile, nrows, voc, {}, q, ke, rowpos, P};
+#pragma unroll
+    for (int t = 0; t < T; ++t) R.vox[t] = vox[t];
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
-      for (int t = 0; t < T; ++t) C[m][t] = f4{0.f, 0.f, 0.f, 0.f};
-    auto step = [&](const MStage<T>& cur, MStage<T>& nxt, int k0) {
-      mstage_issue<T>(A, rc, rx, ri, q, rowok, k0 + 32, ke, nxt);
-      float w[4][8];
-      decode8<L>(lds, lo, cur.c0, cur.c1, w);
-      const int kk = k0 + 8 * q;
-      for (;;) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int e = P.k[i] - kk;
-          const bool hit = e >= 0 && e < 8;
-          if (__ballot(hit)) {
-            const f16x4 pv = __builtin_bit_cast(f16x4, P.v[i]);
-            const float v[4] = {(float)pv.x, (float)pv.y, (float)pv.z, (float)pv.w};
-#pragma unroll
-            for (int ee = 0; ee < 8; ++ee) {
-              const bool sel = hit && e == ee;
-#pragma unroll
-              for (int m = 0; m < 4; ++m) w[m][ee] = sel ? v[m] : w[m][ee];
-            }
-          }
-        }
-        // the window is used up within this step: take the row's next 4 (rare) and patch
-        // again (lanes that keep their window re-apply the same values: no change)
-        const bool refill = P.k[3] < k0 + 32 && P.next < P.end;
-        if (!__ballot(refill)) break;
-        if (refill) mplug_fill(A, rowpos, P);
-      }
-      h8 a[4];
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int ee = 0; ee < 8; ++ee) a[m][ee] = (_Float16)w[m][ee];
-#pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const h8 b = __builtin_bit_cast(h8, cur.xb[t]);
-#pragma unroll
-        for (int m = 0; m < 4; ++m) C[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b, C[m][t], 0, 0, 0);
-      }
-    };
+      for (int t = 0; t < T; ++t) R.C[m][t] = f4{0.f, 0.f, 0.f, 0.f};
     int k0 = kb;
     for (;;) {
-      if (k0 >= ke) break;
-      step(s0, s1, k0);
-      k0 += 32;
-      if (k0 >= ke) break;
-      step(s1, s0, k0);
-      k0 += 32;
+      if (!R.step(s0, s1, k0)) break;
+      if (!R.step(s1, s0, k0)) break;
     }
+    const f4 (&C)[4][T] = R.C;
     // epilogue: lane holds rows n0 + 4q + r of token 16t + ri
     if (A.slices == 1) {
 #pragma unroll
@@ -222,33 +297,63 @@ __device__ __forceinline__ void mfma_body(const char* lds, const QuadMfmaArgs& A
 }
 
 template <int T>
-__global__ __launch_bounds__(MF_NT) void quad_mfma_kernel(const QuadMfmaArgs A) {
+__global__ __launch_bounds__(MfCfg<T>::NT) void quad_mfma_kernel(const QuadMfmaArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t Tb[QLDS_BYTES / 4];
   const char* lds = reinterpret_cast<const char*>(Tb);
   if (quad_tables(Tb, A.luts)) mfma_body<T, LayShared>(lds, A);
   else mfma_body<T, LaySplit>(lds, A);
 }
 
-// Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero.
+// Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero.  This launch starts
+// after the tile kernel has completed, so its atomics are visible to plain loads and
+// plain stores clear the sums for the next launch: each thread takes 4 consecutive sums
+// (M % 4 == 0: one 16-byte load; otherwise one at a time).
 __global__ __launch_bounds__(256) void quad_mfma_finish_kernel(const QuadMfmaArgs A) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t total = 4ll * A.N * A.M;
-  if (i >= total) return;
-  const int j = (int)(i % A.M);
-  const int64_t mn = i / A.M;
-  const int row = (int)(mn % A.N), m = (int)(mn / A.N);
-  const float v = __hip_atomic_exchange(A.acc + i, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  f16* o = m == 0 ? A.out[0] : m == 1 ? A.out[1] : m == 2 ? A.out[2] : A.out[3];
-  o[(int64_t)j * A.o_sm + row] = (f16)v;
+  const int64_t i0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+  if (i0 >= total) return;
+  float v[4];
+  if (A.M % 4 == 0) {
+    const float4 t = *reinterpret_cast<const float4*>(A.acc + i0);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    *reinterpret_cast<float4*>(A.acc + i0) = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = i0 + e < total ? A.acc[i0 + e] : 0.f;
+      if (i0 + e < total) A.acc[i0 + e] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t i = i0 + e;
+    if (i >= total) break;
+    const int j = (int)(i % A.M);
+    const int64_t mn = i / A.M;
+    const int row = (int)(mn % A.N), m = (int)(mn / A.N);
+    f16* o = m == 0 ? A.out[0] : m == 1 ? A.out[1] : m == 2 ? A.out[2] : A.out[3];
+    o[(int64_t)j * A.o_sm + row] = (f16)v[e];
+  }
 }
 
 static int mfma_tiles_t(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
+
+static int mfma_nt(int64_t M) {
+  switch (mfma_tiles_t(M)) {
+    case 1: return MfCfg<1>::NT;
+    case 2: return MfCfg<2>::NT;
+    default: return MfCfg<4>::NT;
+  }
+}
 
 }  // namespace pp
 
 using namespace pp;
 
-extern "C" int64_t pp_quad_mfma_waves(void) { return (int64_t)device_cu_count() * (MF_NT / 64); }
+extern "C" int64_t pp_quad_mfma_waves(int64_t M) {
+  if (M < 1 || M > 64) return 0;
+  return (int64_t)device_cu_count() * (mfma_nt(M) / 64);
+}
 
 extern "C" int64_t pp_quad_mfma_workspace_size(int64_t M, int64_t N, int64_t slices) {
   if (slices <= 1) return 0;
@@ -266,7 +371,7 @@ extern "C" int pp_quad_mfma(const uint32_t* codes, int64_t ldc, int64_t elem_bas
   for (int i = 0; i < 7; ++i) PP_REQUIRE(luts[i] != nullptr, "lut %d is null", i);
   PP_REQUIRE(lut_dtype == PP_F16 || lut_dtype == PP_F32, "bad lut_dtype");
   PP_REQUIRE(M >= 1 && M <= 64, "the matrix-core path takes 1..64 tokens, got %lld", (long long)M);
-  PP_REQUIRE(N >= 1 && K >= 8 && K % 8 == 0, "needs N >= 1 and K a multiple of 8 (N=%lld, K=%lld)", (long long)N,
+  PP_REQUIRE(N >= 1 && K >= 32 && K % 32 == 0, "needs N >= 1 and K a multiple of 32 (N=%lld, K=%lld)", (long long)N,
              (long long)K);
   PP_REQUIRE(ldc >= K && ldc % 4 == 0 && aligned(codes, 16), "codes must be 16-byte aligned rows of ldc >= K words");
   PP_REQUIRE(aligned(a, 16) && (M == 1 || (a_sm >= K && a_sm % 8 == 0)),
@@ -305,17 +410,17 @@ extern "C" int pp_quad_mfma(const uint32_t* codes, int64_t ldc, int64_t elem_bas
   A.acc = reinterpret_cast<float*>(workspace);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t items = A.tiles * slices;
-  const int64_t waves = MF_NT / 64;
-  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(device_cu_count(), (items + waves - 1) / waves));
+  const int nt = mfma_nt(M);
+  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(device_cu_count(), items));
   switch (mfma_tiles_t(M)) {
-    case 1: hipLaunchKernelGGL(quad_mfma_kernel<1>, dim3(grid), dim3(MF_NT), 0, st, A); break;
-    case 2: hipLaunchKernelGGL(quad_mfma_kernel<2>, dim3(grid), dim3(MF_NT), 0, st, A); break;
-    default: hipLaunchKernelGGL(quad_mfma_kernel<4>, dim3(grid), dim3(MF_NT), 0, st, A); break;
+    case 1: hipLaunchKernelGGL(quad_mfma_kernel<1>, dim3(grid), dim3(nt), 0, st, A); break;
+    case 2: hipLaunchKernelGGL(quad_mfma_kernel<2>, dim3(grid), dim3(nt), 0, st, A); break;
+    default: hipLaunchKernelGGL(quad_mfma_kernel<4>, dim3(grid), dim3(nt), 0, st, A); break;
   }
   PP_LAUNCH_CHECK();
   if (slices > 1) {
     const int64_t total = 4 * N * M;
-    hipLaunchKernelGGL(quad_mfma_finish_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, A);
+    hipLaunchKernelGGL(quad_mfma_finish_kernel, dim3((unsigned)((total / 4 + 255) / 256 + 1)), dim3(256), 0, st, A);
     PP_LAUNCH_CHECK();
   }
   return PP_OK;

@@ -33,6 +33,11 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
 __device__ __forceinline__ void vload128(u32x4& d, uint32_t off, rsrc_t r) {
   d = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, NT_AUX);
 }
+// The same without the streaming cache policy: for data that many wavefronts re-read
+// (activations), which should stay in the caches.
+__device__ __forceinline__ void vload128c(u32x4& d, uint32_t off, rsrc_t r) {
+  d = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
 __device__ __forceinline__ void vload64(u32x2& d, uint32_t off, rsrc_t r) {
   d = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
 }

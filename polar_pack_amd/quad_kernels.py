@@ -147,7 +147,7 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
 
 def _mfma_layout_ok(codes, K):
     """Codes of an (N,K) row-major block seen as (K,N): the layout the matrix-core path reads."""
-    return codes.stride(0) == 1 and codes.stride(1) >= K and codes.stride(1) % 4 == 0 and K % 8 == 0 \
+    return codes.stride(0) == 1 and codes.stride(1) >= K and codes.stride(1) % 4 == 0 and K % 32 == 0 \
         and codes.data_ptr() % 16 == 0
 
 
@@ -159,9 +159,8 @@ def _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, 
     ldc = codes.stride(1)
     if a.stride(1) != 1 or a.data_ptr() % 16 or (M > 1 and a.stride(0) % 8):
         a = a.contiguous()
-    slices = max(1, min(K // 32, -(-int(L.pp_quad_mfma_waves()) // (-(-N // 16)))))
-    cols = -(-(-(-K // slices)) // 32) * 32
-    slices = -(-K // cols)
+    from .stream import mfma_slices
+    slices, cols = mfma_slices(N, K, int(L.pp_quad_mfma_waves(M)))
     row_plug = None
     if pn:
         idx = keep[0].view(torch.int32).to(torch.int64) & 0xFFFFFFFF

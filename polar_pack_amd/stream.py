@@ -471,10 +471,12 @@ class DualStream:
 
 
 def mfma_slices(N, K, waves):
-    """(slices, slice_cols) for the batch decode of an (N, K) projection: enough K slices
-    of whole 32-column steps for about one 16-row x slice item per wavefront."""
+    """(slices, slice_cols) for the batch decode of an (N, K) projection: as many K slices
+    of whole 32-column steps as keep the 16-row x slice items within one per wavefront
+    (one item more than the wavefronts would double the launch for the waves that take
+    two)."""
     tiles = -(-int(N) // 16)
-    s = max(1, min(int(K) // 32, -(-int(waves) // tiles)))
+    s = max(1, min(int(K) // 32, int(waves) // tiles))
     cols = -(-int(K) // s)
     cols = -(-cols // 32) * 32
     return -(-int(K) // cols), cols
@@ -503,11 +505,11 @@ class QuadBatch:
         self.N, self.K, self.pos0, self.M = int(N), int(K), int(pos0), int(M)
         if not 1 <= self.M <= 64:
             raise ValueError("the batch decode takes 1..64 tokens")
-        if self.K % 8 or self.pos0 + self.N * self.K > pack.n:
-            raise ValueError("needs K % 8 == 0 and the projection inside the coded stream")
+        if self.K % 32 or self.pos0 + self.N * self.K > pack.n:
+            raise ValueError("needs K % 32 == 0 and the projection inside the coded stream")
         self.device = pack.codes.device
         if slices is None:
-            self.slices, self.cols = mfma_slices(self.N, self.K, int(L.pp_quad_mfma_waves()))
+            self.slices, self.cols = mfma_slices(self.N, self.K, int(L.pp_quad_mfma_waves(self.M)))
         else:
             self.slices = int(slices)
             cols = -(-self.K // self.slices)

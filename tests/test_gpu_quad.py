@@ -102,7 +102,7 @@ def test_quad_gemm_matches_oracle(K, N, layout, M):
     # more than 8 tokens on (N,K) rows: the matrix-core path, fp16 weights into the dot
     # product (as the reference's tl.dot); held to the fp16-rounded decode + the fp32
     # dot-product bound (see test_gpu_mfma.py)
-    mfma = M > 8 and layout == "nk" and K % 8 == 0
+    mfma = M > 8 and layout == "nk" and K % 32 == 0
     W32 = olay.quad_dequant(codes, [l.float().numpy() for l in luts], dtype=np.float32) if mfma else None
     for k in range(4):
         assert outs[k].shape == (M, N) and outs[k].dtype == torch.float16
