@@ -282,6 +282,11 @@ int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk, int64_t c_
  * task_plug[2t], task_plug[2t+1] are the first plug entry at or after task t's first
  * position and the first one past its last position.  plug_windows (1 or 2) is the
  * number of 64-entry plug windows each decode step takes (2 for dense plug tables).
+ * Split segments (parts > 1, columns cut at multiples of pp_dual_stream_chunk(M)) work
+ * as in pp_quad_stream: their float32 partial sums go to the workspace (uint32 counter
+ * per task, accumulators at acc_off + (m*M + j)*N + row for model m = 0, 1), which must
+ * be zero before the first launch and is left zero by each; launches that share it must
+ * not overlap.  A null workspace skips split segments.
  * Replaces the per-projection polar_dual_bitpacked calls of a decode step
  * (polar_kernels.py:98-115) and the decode of unpack_dual_models
  * (polar_bitpack.py:194-260).
@@ -298,11 +303,13 @@ typedef struct pp_dual_proj {
 } pp_dual_proj;
 
 int pp_dual_stream_rows(int64_t M);
+/* Pairs the dual stream decode reads per row and step for M tokens (0 for bad M). */
+int pp_dual_stream_chunk(int64_t M);
 int64_t pp_dual_stream_waves(int64_t M);
 
 int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs,
                    const pp_quad_seg* segs, int64_t n_segs, const int64_t* seg_bounds, int64_t n_waves,
-                   const int64_t* task_plug, int64_t n_tasks, int plug_windows,
+                   void* workspace, const int64_t* task_plug, int64_t n_tasks, int plug_windows,
                    const pp_quad_item* tail_items, int64_t n_tail,
                    int code_layout, const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
                    const float* amp_lut, const float* cos_lut, const float* sin_lut,

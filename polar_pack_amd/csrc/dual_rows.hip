@@ -57,6 +57,7 @@ struct DualStreamArgs {
   const int64_t* task_plug;   // per task: first plug entry in its rows, first entry past them
   int64_t n_tasks;
   int M;
+  void* ws;                   // split launches: per-task counters, then float32 accumulators
 };
 
 // Stored 32-bit word (two pairs) -> two codes in the table-index form: the file layout is
@@ -106,15 +107,29 @@ __device__ __forceinline__ void dual_lookup1(const char* lds, uint32_t c, const 
   cs = *reinterpret_cast<const float2*>(lds + DLDS_CS + (((c << 7) & 0x1FF80u) | o.cs));
 }
 
-template <int LAYOUT>
+// (cos, sin) rows as 16-byte units (two replicas) in address order, so that a wavefront's
+// stores fill consecutive banks; every LUT load of a thread is issued before its stores.
+template <int LAYOUT, int NT>
 __device__ __forceinline__ void dual_build_lds(char* lds, const DualStreamArgs& A) {
-  for (int i = threadIdx.x; i < 1024 * 16; i += blockDim.x) {
-    const int p = i >> 4, j = i & 15;
-    *reinterpret_cast<float2*>(lds + DLDS_CS + p * 128 + 8 * j) = make_float2(A.cos_lut[p], A.sin_lut[p]);
+  constexpr int KU = (8192 + NT - 1) / NT;
+  float c[KU], s[KU];
+#pragma unroll
+  for (int k = 0; k < KU; ++k) {
+    const int u = threadIdx.x + k * NT;
+    if (u < 8192) {
+      c[k] = A.cos_lut[u >> 3];
+      s[k] = A.sin_lut[u >> 3];
+    }
   }
   // the int16 layout stores code ^ 0x8000: entry a holds amplitude a ^ 32
-  for (int a = threadIdx.x; a < 64; a += blockDim.x)
-    *reinterpret_cast<float*>(lds + DLDS_AMP + 4 * a) = A.amp_lut[LAYOUT == PP_DUAL_I16_OFFSET ? (a ^ 32) : a];
+  if (threadIdx.x < 64)
+    *reinterpret_cast<float*>(lds + DLDS_AMP + 4 * threadIdx.x) =
+        A.amp_lut[LAYOUT == PP_DUAL_I16_OFFSET ? (threadIdx.x ^ 32) : threadIdx.x];
+#pragma unroll
+  for (int k = 0; k < KU; ++k) {
+    const int u = threadIdx.x + k * NT;
+    if (u < 8192) *reinterpret_cast<float4*>(lds + DLDS_CS + 16 * u) = make_float4(c[k], s[k], c[k], s[k]);
+  }
 }
 
 // Uniform state of a segment.
@@ -126,6 +141,10 @@ struct DualSeg {
   int ldc, K, nrows, x_sm;
   f16* out[2];
   int64_t o_sm;
+  int kbeg, kend;      // the column slice the segment covers
+  int parts, N, row0;  // slices of its rows; the projection's rows; the first row
+  float* acc;          // parts > 1: the projection's accumulators [2][M][N]
+  uint32_t* cnt;       // parts > 1: the counters of the segment's tasks
 };
 
 // Group (scale index) of stream position p.  SM = 0: chunk is a multiple of gs, so
@@ -161,7 +180,7 @@ __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const Dual
   const int64_t base = S.pos0 + first;   // stream position of (row, kc): uniform
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
-    const bool in = (row + r) < S.nrows && k < S.K;
+    const bool in = (row + r) < S.nrows && k < S.kend;
     const int64_t br = base + (int64_t)r * S.ldc;
     uint32_t g;
     if constexpr (SM == 0) {
@@ -174,11 +193,12 @@ __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const Dual
     vload16(c.sc[r], in ? 2u * g : OOB, rs);
   }
   if constexpr (MT == 1) {
-    const rsrc_t rx = make_rsrc(S.x + kc, 2u * (uint32_t)(S.K - kc));
+    // columns past the slice read x = 0, so the codes loaded there add nothing
+    const rsrc_t rx = make_rsrc(S.x + kc, 2u * (uint32_t)(S.kend - kc));
     vload128c(c.xr[0], 16u * lane, rx);
   } else {
 #pragma unroll
-    for (int j = 0; j < MT; ++j) vload128c(c.xr[j], k < S.K ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
+    for (int j = 0; j < MT; ++j) vload128c(c.xr[j], k < S.kend ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
   }
 }
 
@@ -291,7 +311,7 @@ __device__ __forceinline__ void dwin_data(const DualStreamArgs& A, const DualSeg
     for (int r = 1; r < RG; ++r)
       if (o >= r * S.ldc) row = r;
     const int k = o - row * S.ldc;
-    v = v && k < S.K;
+    v = v && k >= S.kbeg && k < S.kend;   // entries of the task's other column slices are theirs
     W.q[w] = v ? row : -1;
     vload16(W.code[w], v ? 2u * (uint32_t)(trow0 + o) : OOB, S.rcs);
     vload16(W.sc[w], v ? 2u * dual_group<SM>(A, (int64_t)idx[w]) : OOB, rs);
@@ -325,9 +345,16 @@ __device__ __forceinline__ void dwin_apply(const char* lds, const DualLane& lo, 
   }
 }
 
+// The task's sums reduced over the wave: lane `wr` holds (row r, model m, token j).
+struct DReduced {
+  float y;
+  int r, m, j;
+  bool wr;
+};
+
 template <int MT, int RG>
-__device__ __forceinline__ void dtask_write(const DualStreamArgs& A, const DualSeg& S, int ti, int lane,
-                                            float (&acc)[RG][2][MT]) {
+__device__ __forceinline__ DReduced dtask_reduce(const DualStreamArgs& A, const DualSeg& S, int ti, int lane,
+                                                 float (&acc)[RG][2][MT]) {
   constexpr int NV = RG * 2 * MT;
   constexpr int LNV = Log2<NV>::v;
   static_assert((1 << LNV) == NV, "RG*2*MT must be a power of two");
@@ -338,17 +365,60 @@ __device__ __forceinline__ void dtask_write(const DualStreamArgs& A, const DualS
     for (int m = 0; m < 2; ++m)
 #pragma unroll
       for (int j = 0; j < MT; ++j) v[(r * 2 + m) * MT + j] = acc[r][m][j];
-  const float y = wave_transpose_reduce<LNV>(v, lane);
+  DReduced o;
+  o.y = wave_transpose_reduce<LNV>(v, lane);
   const int idx = lane >> (6 - LNV);
-  const int r = idx / (2 * MT), m = (idx / MT) & 1, j = idx % MT;
+  o.r = idx / (2 * MT);
+  o.m = (idx / MT) & 1;
+  o.j = idx % MT;
   const int nr = min(RG, S.nrows - ti * RG);
-  const bool wr = (lane & ((1 << (6 - LNV)) - 1)) == 0 && r < nr && j < A.M;
-  const uint32_t off = 2u * (uint32_t)((int64_t)j * S.o_sm + (int64_t)(ti * RG + r));
+  o.wr = (lane & ((1 << (6 - LNV)) - 1)) == 0 && o.r < nr && o.j < A.M;
+  return o;
+}
+
+template <int RG>
+__device__ __forceinline__ void dtask_store(const DualStreamArgs& A, const DualSeg& S, int ti, const DReduced& o,
+                                            float y) {
+  const uint32_t off = 2u * (uint32_t)((int64_t)o.j * S.o_sm + (int64_t)(ti * RG + o.r));
   const uint32_t obytes = 2u * (uint32_t)((int64_t)(A.M - 1) * S.o_sm + (int64_t)S.nrows);
   const f16 h = (f16)y;
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm)
-    vstore16((uint32_t)__builtin_bit_cast(unsigned short, h), (wr && m == mm) ? off : OOB, make_rsrc(S.out[mm], obytes));
+    vstore16((uint32_t)__builtin_bit_cast(unsigned short, h), (o.wr && o.m == mm) ? off : OOB,
+             make_rsrc(S.out[mm], obytes));
+}
+
+template <int MT, int RG>
+__device__ __forceinline__ void dtask_write(const DualStreamArgs& A, const DualSeg& S, int ti, int lane,
+                                            float (&acc)[RG][2][MT]) {
+  const DReduced o = dtask_reduce<MT, RG>(A, S, ti, lane, acc);
+  dtask_store<RG>(A, S, ti, o, o.y);
+}
+
+// A column slice of task ti: add the sums to the projection's accumulators and count the
+// part in the task's counter; the last part to arrive takes the totals (swapping in
+// zeros, so the workspace is clean for the next launch), writes the outputs and clears
+// the counter.  Every workspace access is a device-scope atomic, performed where all CUs
+// see it; "sums before count" comes from a data dependence (the count added is
+// 1 + 0 * the values the sum atomics returned).
+template <int MT, int RG>
+__device__ __forceinline__ void dtask_accumulate(const DualStreamArgs& A, const DualSeg& S, int ti, int lane,
+                                                 float (&acc)[RG][2][MT]) {
+  const DReduced o = dtask_reduce<MT, RG>(A, S, ti, lane, acc);
+  float* a = S.acc + ((int64_t)(o.m * A.M + o.j) * S.N + S.row0 + ti * RG + o.r);
+  float before = 0.f;
+  if (o.wr) before = __hip_atomic_fetch_add(a, o.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // a zero the compiler cannot see through, computed from the returned sums
+  uint32_t z;
+  asm volatile("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(before));
+  uint32_t old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(S.cnt + ti, 1u + z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __builtin_amdgcn_readfirstlane(old);
+  if (old + 1 == (uint32_t)S.parts) {
+    const float t = o.wr ? __hip_atomic_exchange(a, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    dtask_store<RG>(A, S, ti, o, t);
+    if (lane == 0) __hip_atomic_exchange(S.cnt + ti, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 template <int MT, int RG>
@@ -359,7 +429,7 @@ __device__ __forceinline__ void dzero(float (&acc)[RG][2][MT]) {
     for (int j = 0; j < MT; ++j) acc[r][0][j] = acc[r][1][j] = 0.f;
 }
 
-template <int MT, int RG, int PW, int LAYOUT, int SM>
+template <int MT, int RG, int PW, int LAYOUT, int SM, bool SPLIT>
 struct DualRunner {
   const char* lds;
   DualLane lo;
@@ -382,7 +452,7 @@ struct DualRunner {
       : lds(l), A(a), S(s), task0(t0), pend_ti(-1) {
     lane = threadIdx.x & 63;
     lo = dual_lane(lane);
-    nck = (S.K + DPAIRS - 1) / DPAIRS;
+    nck = (S.kend - S.kbeg + DPAIRS - 1) / DPAIRS;
     ntask = (S.nrows + RG - 1) / RG;
     lc = {0, 0};
 #pragma unroll
@@ -419,7 +489,7 @@ struct DualRunner {
   }
 
   __device__ __forceinline__ void prefetch(DChunk<MT, RG>& c) {
-    dchunk_issue<MT, RG, SM>(A, S, lc.ti * RG, lc.ck * DPAIRS, voff, lane, c);
+    dchunk_issue<MT, RG, SM>(A, S, lc.ti * RG, S.kbeg + lc.ck * DPAIRS, voff, lane, c);
     Cursor nx = lc;
     advance(nx);
     if (nx.ti < ntask) lc = nx;
@@ -434,7 +504,8 @@ struct DualRunner {
       dwin_data<MT, RG, PW, SM>(A, S, t, idx, lane, W);
       dwin_apply<MT, RG, PW, LAYOUT>(lds, lo, W, pend);
     }
-    dtask_write<MT, RG>(A, S, pend_ti, lane, pend);
+    if (SPLIT && S.parts > 1) dtask_accumulate<MT, RG>(A, S, pend_ti, lane, pend);
+    else dtask_write<MT, RG>(A, S, pend_ti, lane, pend);
     pend_ti = -1;
   }
 
@@ -471,7 +542,7 @@ struct DualRunner {
   }
 
   __device__ __forceinline__ void run() {
-    if (ntask <= 0 || S.K <= 0) return;
+    if (ntask <= 0 || S.kend <= S.kbeg) return;
     // fill the window stages for steps 0 and 1, the range of step 2 in flight
     Cursor c = {0, 0};
     load_range(c, T);
@@ -513,22 +584,41 @@ __device__ __forceinline__ void dual_seg(const pp_dual_proj& P, int row0, int ro
 #pragma unroll
   for (int m = 0; m < 2; ++m) S.out[m] = reinterpret_cast<f16*>(uniform_ptr(P.out[m])) + row0;
   S.o_sm = uniform64(P.o_sm);
+  S.kbeg = 0;
+  S.kend = K;
+  S.parts = 1;
+  S.N = uniform(P.N);
+  S.row0 = row0;
+  S.acc = nullptr;
+  S.cnt = nullptr;
 }
 
-template <int MT, int PW, int LAYOUT, int SM>
+template <int MT, int PW, int LAYOUT, int SM, bool SPLIT>
 __global__ __launch_bounds__(DualCfg<MT>::NT) void dual_stream_kernel(const DualStreamArgs A) {
   constexpr int RG = DualCfg<MT>::RG, WAVES = DualCfg<MT>::NT / 64;
   __shared__ __attribute__((aligned(16))) uint32_t T[DLDS_BYTES / 4];
   char* lds = reinterpret_cast<char*>(T);
-  dual_build_lds<LAYOUT>(lds, A);
-  __syncthreads();
   const int64_t gw = (int64_t)blockIdx.x * WAVES + uniform(threadIdx.x >> 6);
-  const int64_t s0 = uniform64(A.seg_bounds[gw]), s1 = uniform64(A.seg_bounds[gw + 1]);
+  SegRange sr;
+  sr.issue(A.seg_bounds, gw, (int64_t)gridDim.x * WAVES);
+  dual_build_lds<LAYOUT, DualCfg<MT>::NT>(lds, A);
+  __syncthreads();
+  const int64_t s0 = sr.lo(), s1 = sr.hi();
   for (int64_t si = s0; si < s1; ++si) {
     const pp_quad_seg g = A.segs[si];
     DualSeg S;
     dual_seg(A.projs[uniform(g.proj)], g.row0, g.row1, A.M, S);
-    DualRunner<MT, RG, PW, LAYOUT, SM> R(lds, A, S, uniform(g.task0));
+    const int parts = uniform(g.parts);
+    if (parts > 1) {
+      if (!SPLIT) continue;   // split segments run in the kernel that has the workspace
+      // one column slice of its rows (clamped to the projection)
+      S.kbeg = max(0, min(S.K, uniform(g.k0)));
+      S.kend = max(S.kbeg, min(S.K, uniform(g.k1)));
+      S.parts = parts;
+      S.acc = reinterpret_cast<float*>(A.ws) + uniform64(g.acc_off);
+      S.cnt = reinterpret_cast<uint32_t*>(A.ws) + uniform(g.task0);
+    }
+    DualRunner<MT, RG, PW, LAYOUT, SM, SPLIT> R(lds, A, S, uniform(g.task0));
     R.run();
   }
 }
@@ -704,8 +794,13 @@ static int dual_stream_nt(int mt) { return mt == 1 ? DualCfg<1>::NT : mt == 2 ? 
 template <int MT, int LAYOUT, int SM>
 static int launch_dual_stream(const DualStreamArgs& A, int pw, hipStream_t st) {
   const dim3 grid((unsigned)device_cu_count()), block(DualCfg<MT>::NT);
-  if (pw == 1) hipLaunchKernelGGL((dual_stream_kernel<MT, 1, LAYOUT, SM>), grid, block, 0, st, A);
-  else hipLaunchKernelGGL((dual_stream_kernel<MT, 2, LAYOUT, SM>), grid, block, 0, st, A);
+  if (A.ws != nullptr) {
+    if (pw == 1) hipLaunchKernelGGL((dual_stream_kernel<MT, 1, LAYOUT, SM, true>), grid, block, 0, st, A);
+    else hipLaunchKernelGGL((dual_stream_kernel<MT, 2, LAYOUT, SM, true>), grid, block, 0, st, A);
+  } else {
+    if (pw == 1) hipLaunchKernelGGL((dual_stream_kernel<MT, 1, LAYOUT, SM, false>), grid, block, 0, st, A);
+    else hipLaunchKernelGGL((dual_stream_kernel<MT, 2, LAYOUT, SM, false>), grid, block, 0, st, A);
+  }
   PP_LAUNCH_CHECK();
   return PP_OK;
 }
@@ -743,13 +838,16 @@ extern "C" int pp_dual_stream_rows(int64_t M) {
   return dual_stream_rg(dual_stream_mt(M));
 }
 
+extern "C" int pp_dual_stream_chunk(int64_t M) { return M < 1 || M > 4 ? 0 : DPAIRS; }
+
 extern "C" int64_t pp_dual_stream_waves(int64_t M) {
   if (M < 1 || M > 4) return 0;
   return (int64_t)device_cu_count() * (dual_stream_nt(dual_stream_mt(M)) / 64);
 }
 
 extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const pp_quad_seg* segs, int64_t n_segs,
-                              const int64_t* seg_bounds, int64_t n_waves, const int64_t* task_plug, int64_t n_tasks,
+                              const int64_t* seg_bounds, int64_t n_waves, void* workspace, const int64_t* task_plug,
+                              int64_t n_tasks,
                               int plug_windows, const pp_quad_item* tail_items,
                               int64_t n_tail, int code_layout, const void* scales, int64_t n_groups,
                               int64_t group_size, int64_t chunk_size, const float* amp_lut, const float* cos_lut,
@@ -798,6 +896,7 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
   A.task_plug = task_plug;
   A.n_tasks = n_tasks;
   A.M = (int)M;
+  A.ws = workspace;
   const bool be = code_layout == PP_DUAL_U16_BE;
   if (n_segs > 0) {
     int rc;

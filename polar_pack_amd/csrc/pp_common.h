@@ -140,77 +140,4 @@ __device__ __forceinline__ void quad_decode(const QuadLds<REPL_R, REPL_C>& T, ui
   w3 = rss * c.y;
 }
 
-// Byte-addressed layout of the same tables for the hot loop: two 64 KiB regions of
-// 256-byte rows, row e holding entry e of two tables,
-//   region 0: [norm x 32 replicas (4 B)] [cos3,sin3 x 16 replicas (8 B)]
-//   region 1: [cos1,sin1 x 16 replicas]   [cos2,sin2 x 16 replicas]
-// so the LDS byte address of a lookup is  region<<16 | code_byte<<8 | lane_offset,
-// one v_perm_b32 of the code word and a per-lane constant.
-struct QuadLdsP {
-  uint32_t w[2 * 256 * 64];
-};
-
-// per-lane constants: byte 0 = offset of this lane's replica in the row, byte 2 = region
-struct QuadLaneOff {
-  uint32_t r, c1, c2, c3;
-};
-
-__device__ __forceinline__ QuadLaneOff quad_lane_offsets(int lane) {
-  QuadLaneOff o;
-  o.r = 4u * (lane & 31);
-  o.c3 = 128u + 8u * (lane & 15);
-  o.c1 = (1u << 16) | (8u * (lane & 15));
-  o.c2 = (1u << 16) | (128u + 8u * (lane & 15));
-  return o;
-}
-
-__device__ __forceinline__ void quad_build_lds_p(QuadLdsP& T, const QuadLuts& L) {
-  const int e = threadIdx.x & 255;
-  const int grp = threadIdx.x >> 8, ngrp = blockDim.x >> 8;
-  float v[7];
-  if (L.dtype == PP_F16) {
-    f16 h[7];
-#pragma unroll
-    for (int i = 0; i < 7; ++i) h[i] = reinterpret_cast<const f16*>(L.p[i])[e];
-#pragma unroll
-    for (int i = 0; i < 7; ++i) v[i] = (float)h[i];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 7; ++i) v[i] = reinterpret_cast<const float*>(L.p[i])[e];
-  }
-  float* f = reinterpret_cast<float*>(T.w);
-  float* row0 = f + e * 64;              // region 0, row e
-  float* row1 = f + 256 * 64 + e * 64;   // region 1, row e
-  for (int j = grp; j < 32; j += ngrp) row0[j] = v[0];
-  for (int j = grp; j < 16; j += ngrp) {
-    row0[32 + 2 * j] = v[5];
-    row0[33 + 2 * j] = v[6];
-    row1[2 * j] = v[1];
-    row1[2 * j + 1] = v[2];
-    row1[32 + 2 * j] = v[3];
-    row1[33 + 2 * j] = v[4];
-  }
-}
-
-// LDS byte address of the lookup of code byte `b` (3 = norm, 2 = q1, 1 = q2, 0 = q3)
-template <int B>
-__device__ __forceinline__ uint32_t quad_lds_addr(uint32_t cw, uint32_t lane_off) {
-  return __builtin_amdgcn_perm(cw, lane_off, 0x0C020000u | ((4u + B) << 8));
-}
-
-__device__ __forceinline__ void quad_decode_p(const QuadLdsP& T, uint32_t cw, const QuadLaneOff& o, float& w0,
-                                              float& w1, float& w2, float& w3) {
-  const char* base = reinterpret_cast<const char*>(T.w);
-  const float r = *reinterpret_cast<const float*>(base + quad_lds_addr<3>(cw, o.r));
-  const float2 a = *reinterpret_cast<const float2*>(base + quad_lds_addr<2>(cw, o.c1));
-  const float2 b = *reinterpret_cast<const float2*>(base + quad_lds_addr<1>(cw, o.c2));
-  const float2 c = *reinterpret_cast<const float2*>(base + quad_lds_addr<0>(cw, o.c3));
-  const float rs = r * a.y;
-  const float rss = rs * b.y;
-  w0 = r * a.x;
-  w1 = rs * b.x;
-  w2 = rss * c.x;
-  w3 = rss * c.y;
-}
-
 }  // namespace pp

@@ -7,7 +7,7 @@
 
 namespace pp {
 
-constexpr uint32_t QLDS_BYTES = 0x28000;  // 160 KiB: all of a gfx950 CU's LDS  // 160 KiB: all of a gfx950 CU's LDS
+constexpr uint32_t QLDS_BYTES = 0x28000;  // 160 KiB: all of a gfx950 CU's LDS
 // ------------------------------------------------------------------ LDS tables
 struct LaneOff {
   uint32_t r, c1, c2, c3;
@@ -18,6 +18,12 @@ struct LaneOff {
 template <int B>
 __device__ __forceinline__ uint32_t perm_addr(uint32_t cw, uint32_t lane_off) {
   return __builtin_amdgcn_perm(cw, lane_off, 0x0C020000u | ((4u + B) << 8));
+}
+
+// Entry e of header LUT i, stored as E (fp16 or float32).
+template <typename E>
+__device__ __forceinline__ float lut_val(const QuadLuts& L, int i, int e) {
+  return (float)reinterpret_cast<const E*>(L.p[i])[e];
 }
 
 // q1 and q2 share one table.  [0, 64K): (cos,sin)(pi i/255) rows of 32 x 8 B;
@@ -33,13 +39,38 @@ struct LayShared {
   static __device__ __forceinline__ uint32_t addr_r(uint32_t cw, const LaneOff& o) {
     return ((cw >> 17) & 0x7F80u) | o.r;
   }
-  static __device__ __forceinline__ void build(char* lds, int e, int grp, int ngrp, const float (&v)[7]) {
-    for (int j = grp; j < 32; j += ngrp) {
-      *reinterpret_cast<float*>(lds + 0x20000 + e * 128 + 4 * j) = v[0];
-      *reinterpret_cast<float2*>(lds + e * 256 + 8 * j) = make_float2(v[1], v[2]);
-      *reinterpret_cast<float2*>(lds + 0x10000 + e * 256 + 8 * j) = make_float2(v[5], v[6]);
+  // 16-byte units in address order, so that a wavefront's 64 stores fill 1 KiB of
+  // consecutive banks (a row-per-thread order puts all 64 lanes of a store on one bank).
+  // The LUT loads (load) are issued before the layout check, the stores (store) after.
+  template <int NT>
+  struct Units {
+    static constexpr int KN = 2048 / NT, KC = 4096 / NT;       // norm: 8 units per entry, (cos, sin): 16
+    float r[KN], c1[KC], s1[KC], c3[KC], s3[KC];
+    template <typename E>
+    __device__ __forceinline__ void load(const QuadLuts& L) {
+#pragma unroll
+      for (int k = 0; k < KN; ++k) r[k] = lut_val<E>(L, 0, (threadIdx.x + k * NT) >> 3);
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        const int e = (threadIdx.x + k * NT) >> 4;
+        c1[k] = lut_val<E>(L, 1, e);
+        s1[k] = lut_val<E>(L, 2, e);
+        c3[k] = lut_val<E>(L, 5, e);
+        s3[k] = lut_val<E>(L, 6, e);
+      }
     }
-  }
+    __device__ __forceinline__ void store(char* lds) const {
+#pragma unroll
+      for (int k = 0; k < KN; ++k)
+        *reinterpret_cast<float4*>(lds + 0x20000 + 16 * (threadIdx.x + k * NT)) = make_float4(r[k], r[k], r[k], r[k]);
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        const int u = threadIdx.x + k * NT;
+        *reinterpret_cast<float4*>(lds + 16 * u) = make_float4(c1[k], s1[k], c1[k], s1[k]);
+        *reinterpret_cast<float4*>(lds + 0x10000 + 16 * u) = make_float4(c3[k], s3[k], c3[k], s3[k]);
+      }
+    }
+  };
 };
 
 // Four tables.  [0, 64K): rows [norm x 32 (4 B) | (cos3,sin3) x 16 (8 B)];
@@ -54,17 +85,22 @@ struct LaySplit {
     return o;
   }
   static __device__ __forceinline__ uint32_t addr_r(uint32_t cw, const LaneOff& o) { return perm_addr<3>(cw, o.r); }
-  static __device__ __forceinline__ void build(char* lds, int e, int grp, int ngrp, const float (&v)[7]) {
-    float* row0 = reinterpret_cast<float*>(lds + e * 256);
-    float* row1 = reinterpret_cast<float*>(lds + 0x10000 + e * 256);
-    for (int j = grp; j < 32; j += ngrp) row0[j] = v[0];
-    for (int j = grp; j < 16; j += ngrp) {
-      row0[32 + 2 * j] = v[5];
-      row0[33 + 2 * j] = v[6];
-      row1[2 * j] = v[1];
-      row1[2 * j + 1] = v[2];
-      row1[32 + 2 * j] = v[3];
-      row1[33 + 2 * j] = v[4];
+  template <int NT, typename E>
+  static __device__ __forceinline__ void build(char* lds, const QuadLuts& L) {
+    constexpr int KU = 8192 / NT;                                // 16 units per row, in address order
+    float a[KU], b[KU];
+#pragma unroll
+    for (int k = 0; k < KU; ++k) {
+      const int u = threadIdx.x + k * NT;
+      const int reg = u >> 12, e = (u >> 4) & 255, c = u & 15;
+      const int t = reg == 0 ? (c < 8 ? 0 : 5) : (c < 8 ? 1 : 3);
+      a[k] = lut_val<E>(L, t, e);
+      b[k] = lut_val<E>(L, t == 0 ? 0 : t + 1, e);
+    }
+#pragma unroll
+    for (int k = 0; k < KU; ++k) {
+      const int u = threadIdx.x + k * NT;
+      *reinterpret_cast<float4*>(lds + ((u >> 12) << 16) + 16 * (u & 4095)) = make_float4(a[k], b[k], a[k], b[k]);
     }
   }
 };
@@ -78,21 +114,21 @@ __device__ __forceinline__ void lookup(const char* lds, uint32_t cw, const LaneO
   c = *reinterpret_cast<const float2*>(lds + perm_addr<0>(cw, o.c3));
 }
 
-// Build the tables of a workgroup (all of its threads; blockDim.x a multiple of 256) from
-// the 7 header LUTs (256 entries each, fp16 or fp32) into T (QLDS_BYTES).  Returns true
-// for the shared layout (the t1 and t2 tables equal), false for the split one.
-__device__ __forceinline__ bool quad_tables(uint32_t* T, const QuadLuts& luts) {
+// Build the tables of a workgroup (all NT threads; NT a multiple of 256) from the 7
+// header LUTs (256 entries each, of type E) into T (QLDS_BYTES).  Returns true for the
+// shared layout (the t1 and t2 tables equal), false for the split one.  Every load of
+// the shared layout is issued before the layout check.
+template <int NT, typename E>
+__device__ __forceinline__ bool quad_tables_of(uint32_t* T, const QuadLuts& luts) {
+  static_assert(NT % 256 == 0, "the table build takes a multiple of 256 threads");
   char* lds = reinterpret_cast<char*>(T);
-  const int e = threadIdx.x & 255, grp = threadIdx.x >> 8, ngrp = blockDim.x >> 8;
-  float v[7];
-  if (luts.dtype == PP_F16) {
+  const int e = threadIdx.x & 255;
+  float v[4];
 #pragma unroll
-    for (int i = 0; i < 7; ++i) v[i] = (float)reinterpret_cast<const f16*>(luts.p[i])[e];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 7; ++i) v[i] = reinterpret_cast<const float*>(luts.p[i])[e];
-  }
-  const bool same = __float_as_uint(v[1]) == __float_as_uint(v[3]) && __float_as_uint(v[2]) == __float_as_uint(v[4]);
+  for (int i = 0; i < 4; ++i) v[i] = lut_val<E>(luts, 1 + i, e);
+  LayShared::Units<NT> U;
+  U.template load<E>(luts);
+  const bool same = __float_as_uint(v[0]) == __float_as_uint(v[2]) && __float_as_uint(v[1]) == __float_as_uint(v[3]);
   // workgroup-wide AND through the (not yet built) table memory: the tables fill all
   // of LDS, so there is no room for a separate flag
   if (threadIdx.x == 0) T[0] = 0u;
@@ -101,10 +137,15 @@ __device__ __forceinline__ bool quad_tables(uint32_t* T, const QuadLuts& luts) {
   __syncthreads();
   const bool shared = T[0] == 0u;
   __syncthreads();
-  if (shared) LayShared::build(lds, e, grp, ngrp, v);
-  else LaySplit::build(lds, e, grp, ngrp, v);
+  if (shared) U.store(lds);
+  else LaySplit::build<NT, E>(lds, luts);
   __syncthreads();
   return shared;
+}
+
+template <int NT>
+__device__ __forceinline__ bool quad_tables(uint32_t* T, const QuadLuts& luts) {
+  return luts.dtype == PP_F16 ? quad_tables_of<NT, f16>(T, luts) : quad_tables_of<NT, float>(T, luts);
 }
 
 }  // namespace pp

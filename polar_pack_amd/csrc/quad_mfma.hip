@@ -300,7 +300,7 @@ template <int T>
 __global__ __launch_bounds__(MfCfg<T>::NT) void quad_mfma_kernel(const QuadMfmaArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t Tb[QLDS_BYTES / 4];
   const char* lds = reinterpret_cast<const char*>(Tb);
-  if (quad_tables(Tb, A.luts)) mfma_body<T, LayShared>(lds, A);
+  if (quad_tables<MfCfg<T>::NT>(Tb, A.luts)) mfma_body<T, LayShared>(lds, A);
   else mfma_body<T, LaySplit>(lds, A);
 }
 

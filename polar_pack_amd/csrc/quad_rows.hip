@@ -578,11 +578,11 @@ __device__ __forceinline__ void seg_ctx(const pp_quad_proj& P, int64_t o_sn, int
   S.cnt = nullptr;
 }
 
+// Wave gw of the launch; [s0, s1) its segments (stream front end).
 template <int MT, class L, bool SPLIT>
-__device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A) {
+__device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A, int64_t gw, int64_t s0, int64_t s1) {
   constexpr int RG = RowsCfg<MT>::RG, NSEG = RowsCfg<MT>::NSEG;
   constexpr int WAVES = RowsCfg<MT>::NT / 64;
-  const int64_t gw = (int64_t)blockIdx.x * WAVES + uniform(threadIdx.x >> 6);
   const int64_t nw = (int64_t)gridDim.x * WAVES;
   if (A.segs == nullptr) {
     const int64_t t0 = gw * A.n_tasks / nw, t1 = (gw + 1) * A.n_tasks / nw;
@@ -594,7 +594,6 @@ __device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A
     R.run();
     return;
   }
-  const int64_t s0 = uniform64(A.seg_bounds[gw]), s1 = uniform64(A.seg_bounds[gw + 1]);
   for (int64_t si = s0; si < s1; ++si) {
     const pp_quad_seg g = A.segs[si];
     SegCtx S;
@@ -618,8 +617,11 @@ template <int MT, bool SPLIT>
 __global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_rows_kernel(const QuadRowsArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t T[QLDS_BYTES / 4];
   const char* lds = reinterpret_cast<const char*>(T);
-  if (quad_tables(T, A.luts)) rows_body<MT, LayShared, SPLIT>(lds, A);
-  else rows_body<MT, LaySplit, SPLIT>(lds, A);
+  const int64_t gw = (int64_t)blockIdx.x * (RowsCfg<MT>::NT / 64) + uniform(threadIdx.x >> 6);
+  SegRange sr;
+  if (A.segs != nullptr) sr.issue(A.seg_bounds, gw, (int64_t)gridDim.x * (RowsCfg<MT>::NT / 64));
+  if (quad_tables<RowsCfg<MT>::NT>(T, A.luts)) rows_body<MT, LayShared, SPLIT>(lds, A, gw, sr.lo(), sr.hi());
+  else rows_body<MT, LaySplit, SPLIT>(lds, A, gw, sr.lo(), sr.hi());
 }
 
 // ------------------------------------------------------------------ tail rows

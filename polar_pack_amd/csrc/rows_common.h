@@ -117,6 +117,21 @@ struct Log2<1> {
   static constexpr int v = 0;
 };
 
+// A wavefront's segment range [seg_bounds[gw], seg_bounds[gw + 1]) (seg_bounds holds
+// n_waves + 1 entries).  issue() starts vector loads, so the round trip runs under the
+// LDS table build instead of before it (a scalar load there would be waited for by the
+// kernel-argument loads that follow it); lo() / hi() wait for them.
+struct SegRange {
+  u32x2 b0 = {0u, 0u}, b1 = {0u, 0u};
+  __device__ __forceinline__ void issue(const int64_t* seg_bounds, int64_t gw, int64_t n_waves) {
+    const rsrc_t r = make_rsrc(seg_bounds, 8u * (uint32_t)(n_waves + 1));
+    vload64(b0, 8u * (uint32_t)gw, r);
+    vload64(b1, 8u * (uint32_t)gw + 8u, r);
+  }
+  __device__ __forceinline__ int64_t lo() const { return uniform64((int64_t)(((uint64_t)b0[1] << 32) | b0[0])); }
+  __device__ __forceinline__ int64_t hi() const { return uniform64((int64_t)(((uint64_t)b1[1] << 32) | b1[0])); }
+};
+
 // Cursor over the steps (task ti, chunk ck) of a segment.
 struct Cursor {
   int ti, ck;

@@ -342,10 +342,12 @@ class DualStream:
     spreads a task's plug entries over its steps, 64 or 128 per step: ``plug_windows``,
     chosen from the table's density unless given); positions past ``pack.n_codes`` come
     from the per-model fp16 tails.  Projection rows and positions must be multiples of
-    8 pairs (a lane reads 8 pairs that share one group scale).
+    8 pairs (a lane reads 8 pairs that share one group scale).  ``split`` as for
+    :class:`QuadStream` (column slices for launches with few row tasks, summed in a
+    workspace owned by this object: two launches of one DualStream must not overlap).
     """
 
-    def __init__(self, pack, shapes: Sequence[Tuple[int, int]], M: int = 1, plug_windows=None):
+    def __init__(self, pack, shapes: Sequence[Tuple[int, int]], M: int = 1, plug_windows=None, split: bool = True):
         L = nat.lib()
         self.pack = pack
         self.shapes = [(int(n), int(k)) for n, k in shapes]
@@ -366,8 +368,12 @@ class DualStream:
             raise ValueError("dual stream decode needs a power-of-two group_size >= 8 and chunk_size % 8 == 0")
         plug = pack.plug_host()
         self.n_waves = int(L.pp_dual_stream_waves(self.M))
-        self.segs_np, self.bounds_np, _ = plan_segments(self.shapes, pack.n_codes, plug, self.n_waves,
-                                                        self.rows_per_item, self.M, code_bytes=2)
+        self.segs_np, self.bounds_np, ws_bytes = plan_segments(
+            self.shapes, pack.n_codes, plug, self.n_waves, self.rows_per_item, self.M, code_bytes=2, split=split,
+            block=int(L.pp_dual_stream_chunk(self.M)))
+        self.split = bool(np.any(self.segs_np["parts"] > 1))
+        # split launches: counters + accumulators, zero once here, left zero by every launch
+        self.workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=self.device) if ws_bytes else None
         tails = list(pack.tails) + [None] * (2 - len(pack.tails))
         aligned = pack.n_codes % 8 == 0 and all(t is None or t.numel() == 0 or t.data_ptr() % 16 == 0
                                                 for t in tails)
@@ -443,6 +449,7 @@ class DualStream:
         rc = nat.lib().pp_dual_stream(self.projs.data_ptr(), len(self.shapes),
                                       self.segs.data_ptr() if self.n_segs else None, self.n_segs,
                                       self.bounds.data_ptr(), self.n_waves,
+                                      self.workspace.data_ptr() if self.workspace is not None else None,
                                       self.task_plug.data_ptr() if self.n_tasks else None, self.n_tasks,
                                       self.plug_windows,
                                       self.tail_items.data_ptr() if self.n_tail else None, self.n_tail,

@@ -61,8 +61,10 @@ def device_pack(dp, layout, tails=None, n_codes=None):
     return pack
 
 
-def run_stream(pack, M, seed=5, plug_windows=None):
-    st = DualStream(pack, SHAPES, M=M, plug_windows=plug_windows)
+def run_stream(pack, M, seed=5, plug_windows=None, split=True):
+    st = DualStream(pack, SHAPES, M=M, plug_windows=plug_windows, split=split)
+    # these streams hold few row tasks, so split=True cuts the K > 512 projections into slices
+    assert st.split == split
     xs_np = [np.random.default_rng(seed + p).standard_normal((M, k)).astype(np.float16)
              for p, (_, k) in enumerate(SHAPES)]
     xs = [torch.from_numpy(x).to(DEV) for x in xs_np]
@@ -74,13 +76,14 @@ def run_stream(pack, M, seed=5, plug_windows=None):
 @pytest.mark.parametrize("layout", ["u16be", "i16"])
 @pytest.mark.parametrize("chunk", [50_000_000, 1000])     # groups aligned / restarting mid-group
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
-def test_dual_stream_zero_padded_file(layout, chunk, M):
+@pytest.mark.parametrize("split", [False, True])
+def test_dual_stream_zero_padded_file(layout, chunk, M, split):
     """The .dualpack format itself: model 2 shorter and zero-padded, plug cap 3%."""
     w1, w2 = gen.correlated_models(11, [TOTAL, TOTAL - 3000], delta_growth=False)
     dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=0.03, chunk_size=chunk))
     assert dp.plug_idx.size > 0
     pack = device_pack(dp, layout)
-    st, xs_np, outs = run_stream(pack, M)
+    st, xs_np, outs = run_stream(pack, M, split=split)
     ref = oracle_outputs(oracle_pairs(dp), xs_np)
     for rep in range(2):
         st()
@@ -88,6 +91,8 @@ def test_dual_stream_zero_padded_file(layout, chunk, M):
         for p in range(len(SHAPES)):
             for m in range(2):
                 assert_gemv_close(outs[p][m].float().cpu().numpy(), ref[p][m], f"rep {rep} proj {p} model {m}")
+        if st.workspace is not None:
+            assert int(torch.count_nonzero(st.workspace)) == 0
 
 
 @pytest.mark.parametrize("layout", ["u16be", "i16"])
@@ -112,13 +117,15 @@ def test_dual_stream_fp16_tails(layout):
 
 @pytest.mark.parametrize("plug_windows", [1, 2])
 @pytest.mark.parametrize("cap,M", [(0.2, 1), (0.2, 4), (0.03, 1), (0.03, 2)])
-def test_dual_stream_dense_plug_tasks(plug_windows, cap, M):
+@pytest.mark.parametrize("split", [False, True])
+def test_dual_stream_dense_plug_tasks(plug_windows, cap, M, split):
     """Plug tables dense enough that tasks hold more entries than their steps take
-    (64 or 128 per step): the rest is corrected when the task finishes."""
+    (64 or 128 per step): the rest is corrected when the task finishes (with column
+    slices, each slice walks its task's entries and applies those in its columns)."""
     w1, w2 = gen.correlated_models(17, [TOTAL, TOTAL], delta_growth=False)
     dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=cap, chunk_size=50_000_000))
     pack = device_pack(dp, "u16be")
-    st, xs_np, outs = run_stream(pack, M, plug_windows=plug_windows)
+    st, xs_np, outs = run_stream(pack, M, plug_windows=plug_windows, split=split)
     n_t = st.task_plug_np[:, 1] - st.task_plug_np[:, 0]
     nck = np.array([(-(-SHAPES[p][1] // 512)) for p in np.repeat(np.arange(len(SHAPES)),
                                                                    [-(-n // st.rows_per_item) for n, _ in SHAPES])])
@@ -194,3 +201,30 @@ def test_dual_stream_fp16_tail_rows(M):
         for m in range(2):
             assert_gemv_close(outs[p][m].float().cpu().numpy(), ref[p][m], f"proj {p} model {m}")
 
+
+
+@pytest.mark.parametrize("shape", [(256, 2048), (64, 11008), (1000, 1000), (2048, 520)])
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_single_linear_split_k(shape, M):
+    """One projection whose tasks are cut into column slices that meet in the workspace:
+    equal to the oracle on repeated launches, and the workspace is left zero."""
+    N, K = shape
+    w1, w2 = gen.correlated_models(19, [N * K, N * K], delta_growth=False)
+    dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=0.01, chunk_size=50_000_000))
+    pack = device_pack(dp, "i16")
+    st = DualStream(pack, [shape], M=M)
+    # slices when the launch has fewer than half as many row tasks as wavefronts
+    assert st.split == (K > 512 and 2 * -(-N // st.rows_per_item) < st.n_waves)
+    assert (st.workspace is not None) == st.split
+    x_np = np.random.default_rng(23).standard_normal((M, K)).astype(np.float16)
+    outs = [[torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV) for _ in range(2)]]
+    st.bind([torch.from_numpy(x_np).to(DEV)], outs)
+    w = odp.decode_pairs_f64(dp, 0, N * K)
+    for rep in range(3):
+        st()
+        torch.cuda.synchronize()
+        for m in range(2):
+            ref = x_np.astype(np.float64) @ w[m].reshape(N, K).T
+            assert_gemv_close(outs[0][m].float().cpu().numpy(), ref, f"rep {rep} model {m}")
+        if st.workspace is not None:
+            assert int(torch.count_nonzero(st.workspace)) == 0
