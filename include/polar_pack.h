@@ -274,6 +274,9 @@ int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk, int64_t c_
  * group rule of the file (group_size, chunk_size: groups restart every chunk);
  * amp_lut / cos_lut / sin_lut are float32 tables from the header (64 / 1024 / 1024
  * entries); plug entries replace the amplitude of a pair by an exact fp16 amplitude.
+ * plug_aux (plug_n words, from pp_dual_plug_aux on the same codes and scales) holds each
+ * entry's stored code and group scale, so the kernel reads them with the plug table
+ * instead of gathering them from the code stream.
  * Positions >= n_codes come from the per-model fp16 tails (tails[m], tail_len[m]): a
  * build-defined extension for streams whose models have different lengths (the file
  * format itself zero-pads the shorter model).
@@ -313,9 +316,20 @@ int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs,
                    const pp_quad_item* tail_items, int64_t n_tail,
                    int code_layout, const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
                    const float* amp_lut, const float* cos_lut, const float* sin_lut,
-                   const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n,
+                   const uint32_t* plug_idx, const void* plug_amp, const uint32_t* plug_aux, int64_t plug_n,
                    int64_t n_codes, const void* const* tails, const int64_t* tail_len,
                    int64_t M, void* stream);
+
+/*
+ * Plug side table of a dual stream (built once per stream, on the stream's device):
+ * aux[j] = the stored 16-bit code of pair plug_idx[j] (in the codes' layout) | the fp16
+ * bits of its group scale << 16, with the group rule of pp_dual_stream; 0 for an entry
+ * at or past n_codes.  No counterpart in the reference: it is a cache of values of its
+ * code and scale arrays (polar_bitpack.py:205-211) for the plug correction.
+ */
+int pp_dual_plug_aux(const void* codes, int64_t n_codes, const void* scales, int64_t n_groups,
+                     int64_t group_size, int64_t chunk_size, const uint32_t* plug_idx, int64_t plug_n,
+                     uint32_t* aux, void* stream);
 
 #ifdef __cplusplus
 }

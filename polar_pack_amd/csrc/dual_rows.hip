@@ -53,6 +53,7 @@ struct DualStreamArgs {
   int log2gs;
   const uint32_t* plug_idx;
   const f16* plug_amp;
+  const uint32_t* plug_aux;   // per entry: its pair's stored code | group scale bits << 16
   int64_t plug_n;
   const int64_t* task_plug;   // per task: first plug entry in its rows, first entry past them
   int64_t n_tasks;
@@ -255,7 +256,9 @@ __device__ __forceinline__ void dchunk_compute(const char* lds, const DualLane& 
 // A window passes through three stages, one step apart, so that every load is issued a
 // step before the step that reads it and the number of loads per step is fixed:
 //   step s-2: the entries' positions;
-//   step s-1: the stored code, the group scale, the plug amplitude and x at each entry;
+//   step s-1: the stored code and group scale (one word of the side table plug_aux, so
+//             that nothing is gathered from the code stream), the plug amplitude and x
+//             at each entry;
 //   step s:   acc[row] += (plug amp - amp_lut[aq] * scale) * x * (cos, sin)(phase).
 // Lanes without an entry load nothing (reads of 0 make their correction 0).
 
@@ -274,7 +277,7 @@ __device__ __forceinline__ int dslot_cnt(const DSlot& s) {
 
 template <int MT, int PW>
 struct DWin {
-  uint32_t code[PW], sc[PW], pa[PW];   // stored code, group scale, plug amplitude (16 bits)
+  uint32_t aux[PW], pa[PW];            // stored code | group scale << 16, plug amplitude (16 bits)
   uint32_t xk[PW][MT];                 // x at the entry's column (fp16 bits)
   int q[PW];                           // row of the entry in its task, -1 for none
 };
@@ -298,7 +301,6 @@ __device__ __forceinline__ void dwin_data(const DualStreamArgs& A, const DualSeg
   const int64_t trow0 = (int64_t)t.ti * RG * S.ldc;        // task start, pairs from the segment start
   const int64_t tpos0 = S.pos0 + trow0;
   const int64_t span = (int64_t)min(RG, S.nrows - t.ti * RG) * S.ldc;
-  const rsrc_t rs = make_rsrc(A.scales, 2u * (uint32_t)A.n_groups);
   const uint32_t pbase = 2u * (uint32_t)t.lo;
 #pragma unroll
   for (int w = 0; w < PW; ++w) {
@@ -313,8 +315,7 @@ __device__ __forceinline__ void dwin_data(const DualStreamArgs& A, const DualSeg
     const int k = o - row * S.ldc;
     v = v && k >= S.kbeg && k < S.kend;   // entries of the task's other column slices are theirs
     W.q[w] = v ? row : -1;
-    vload16(W.code[w], v ? 2u * (uint32_t)(trow0 + o) : OOB, S.rcs);
-    vload16(W.sc[w], v ? 2u * dual_group<SM>(A, (int64_t)idx[w]) : OOB, rs);
+    vload32(W.aux[w], v ? 2u * pbase + 4u * (uint32_t)e : OOB, make_rsrc(A.plug_aux, 4u * (uint32_t)A.plug_n));
     vload16(W.pa[w], v ? pbase + 2u * (uint32_t)e : OOB, make_rsrc(A.plug_amp, 2u * (uint32_t)A.plug_n));
 #pragma unroll
     for (int j = 0; j < MT; ++j)
@@ -330,8 +331,8 @@ __device__ __forceinline__ void dwin_apply(const char* lds, const DualLane& lo, 
   for (int w = 0; w < PW; ++w) {
     float an;
     float2 cs;
-    dual_lookup1(lds, dual_half<LAYOUT>(W.code[w]), lo, an, cs);
-    const float d = h2f(W.pa[w]) - an * h2f(W.sc[w]);
+    dual_lookup1(lds, dual_half<LAYOUT>(W.aux[w]), lo, an, cs);
+    const float d = h2f(W.pa[w]) - an * h2f(W.aux[w] >> 16);
 #pragma unroll
     for (int q = 0; q < RG; ++q) {
       const float on = q == W.q[w] ? d : 0.f;
@@ -786,6 +787,23 @@ __global__ __launch_bounds__(256) void dual_tail_kernel(const DualTailArgs T) {
   }
 }
 
+// Side table of the plug entries: aux[j] = stored 16-bit code of pair plug_idx[j] |
+// fp16 bits of its group scale << 16 (0 for an entry at or past n_codes).
+__global__ __launch_bounds__(256) void dual_plug_aux_kernel(const uint16_t* codes, const f16* scales, int64_t n_groups,
+                                                            int64_t gs, int64_t chunk, const uint32_t* plug_idx,
+                                                            int64_t plug_n, int64_t n_codes, uint32_t* aux) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= plug_n) return;
+  const int64_t p = plug_idx[j];
+  uint32_t v = 0;
+  if (p < n_codes) {
+    const int64_t g = (p / chunk) * ((chunk + gs - 1) / gs) + (p % chunk) / gs;
+    const uint32_t sc = g < n_groups ? (uint32_t)__builtin_bit_cast(unsigned short, scales[g]) : 0u;
+    v = (uint32_t)codes[p] | (sc << 16);
+  }
+  aux[j] = v;
+}
+
 // ------------------------------------------------------------------ host side
 static int dual_stream_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
 static int dual_stream_rg(int mt) { return mt == 1 ? DualCfg<1>::RG : mt == 2 ? DualCfg<2>::RG : DualCfg<4>::RG; }
@@ -838,6 +856,22 @@ extern "C" int pp_dual_stream_rows(int64_t M) {
   return dual_stream_rg(dual_stream_mt(M));
 }
 
+extern "C" int pp_dual_plug_aux(const void* codes, int64_t n_codes, const void* scales, int64_t n_groups,
+                                int64_t group_size, int64_t chunk_size, const uint32_t* plug_idx, int64_t plug_n,
+                                uint32_t* aux, void* stream) {
+  PP_REQUIRE(plug_n >= 0 && plug_n < (1ll << 31), "plug_n out of range");
+  if (plug_n == 0) return PP_OK;
+  PP_REQUIRE(codes != nullptr && scales != nullptr && plug_idx != nullptr && aux != nullptr, "null pointer");
+  PP_REQUIRE(n_codes >= 0 && n_groups >= 1, "bad n_codes / n_groups");
+  PP_REQUIRE(group_size >= 1 && chunk_size >= 1, "bad group_size / chunk_size");
+  hipLaunchKernelGGL(dual_plug_aux_kernel, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const uint16_t*>(codes),
+                     reinterpret_cast<const f16*>(scales), n_groups, group_size, chunk_size, plug_idx, plug_n, n_codes,
+                     aux);
+  PP_LAUNCH_CHECK();
+  return PP_OK;
+}
+
 extern "C" int pp_dual_stream_chunk(int64_t M) { return M < 1 || M > 4 ? 0 : DPAIRS; }
 
 extern "C" int64_t pp_dual_stream_waves(int64_t M) {
@@ -851,7 +885,8 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
                               int plug_windows, const pp_quad_item* tail_items,
                               int64_t n_tail, int code_layout, const void* scales, int64_t n_groups,
                               int64_t group_size, int64_t chunk_size, const float* amp_lut, const float* cos_lut,
-                              const float* sin_lut, const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n,
+                              const float* sin_lut, const uint32_t* plug_idx, const void* plug_amp,
+                              const uint32_t* plug_aux, int64_t plug_n,
                               int64_t n_codes, const void* const* tails, const int64_t* tail_len, int64_t M,
                               void* stream) {
   PP_REQUIRE(projs != nullptr && n_projs >= 1, "no projections");
@@ -868,6 +903,7 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
              "the stream decode needs a power-of-two group_size >= 8");
   PP_REQUIRE(chunk_size >= 8 && chunk_size % 8 == 0, "the stream decode needs chunk_size % 8 == 0");
   PP_REQUIRE(plug_n >= 0 && (plug_n == 0 || (plug_idx != nullptr && plug_amp != nullptr)), "plug arrays are null");
+  PP_REQUIRE(plug_n == 0 || n_segs == 0 || plug_aux != nullptr, "plug_aux is null (build it with pp_dual_plug_aux)");
   PP_REQUIRE(M >= 1 && M <= 4, "the dual stream decode takes 1..4 tokens, got %lld", (long long)M);
   PP_REQUIRE(n_segs == 0 || n_waves == pp_dual_stream_waves(M),
              "seg_bounds were built for %lld waves, this device launches %lld", (long long)n_waves,
@@ -892,6 +928,7 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
   while ((1ll << A.log2gs) < group_size) ++A.log2gs;
   A.plug_idx = plug_idx;
   A.plug_amp = reinterpret_cast<const f16*>(plug_amp);
+  A.plug_aux = plug_aux;
   A.plug_n = plug_n;
   A.task_plug = task_plug;
   A.n_tasks = n_tasks;

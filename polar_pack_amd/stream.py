@@ -402,6 +402,15 @@ class DualStream:
         self._tail_ptrs = nat.ptr_array([t.data_ptr() if t is not None and t.numel() else 0 for t in tails])
         self._tail_len = (C.c_int64 * 2)(*pack.tail_lengths)
         self.code_layout = nat.PP_DUAL_U16_BE if pack.layout == "u16be" else nat.PP_DUAL_I16_OFFSET
+        # each plug entry's stored code and group scale, gathered once here (pp_dual_plug_aux)
+        P = int(pack.plug_idx.numel())
+        self.plug_aux = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
+        if P:
+            rc = L.pp_dual_plug_aux(pack.codes.data_ptr(), pack.n_codes, pack.scales.data_ptr(),
+                                    int(pack.scales.numel()), pack.group_size, pack.chunk_size,
+                                    pack.plug_idx.data_ptr(), P, self.plug_aux.data_ptr(),
+                                    torch.cuda.current_stream(dev).cuda_stream)
+            nat.check(rc, "pp_dual_plug_aux")
         self.projs = None
 
     def make_buffers(self):
@@ -457,6 +466,7 @@ class DualStream:
                                       pk.group_size, pk.chunk_size, amp.data_ptr(), cos.data_ptr(), sin.data_ptr(),
                                       pk.plug_idx.data_ptr() if pk.plug_idx.numel() else None,
                                       pk.plug_val.data_ptr() if pk.plug_val.numel() else None,
+                                      self.plug_aux.data_ptr(),
                                       int(pk.plug_idx.numel()), pk.n_codes, self._tail_ptrs, self._tail_len,
                                       self.M, stream)
         nat.check(rc, "pp_dual_stream")

@@ -228,3 +228,20 @@ def test_single_linear_split_k(shape, M):
             assert_gemv_close(outs[0][m].float().cpu().numpy(), ref, f"rep {rep} model {m}")
         if st.workspace is not None:
             assert int(torch.count_nonzero(st.workspace)) == 0
+
+
+@pytest.mark.parametrize("layout", ["u16be", "i16"])
+@pytest.mark.parametrize("chunk", [50_000_000, 1000])
+def test_plug_side_table(layout, chunk):
+    """pp_dual_plug_aux: each entry's stored code | its group's fp16 scale bits << 16,
+    with groups restarting every chunk (polar_bitpack.py:201-203)."""
+    w1, w2 = gen.correlated_models(31, [TOTAL, TOTAL], delta_growth=False)
+    dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=0.03, chunk_size=chunk))
+    pack = device_pack(dp, layout)
+    st = DualStream(pack, SHAPES, M=1)
+    stored = pack.codes.cpu().numpy().view(np.uint16).astype(np.uint32)
+    p = dp.plug_idx.astype(np.int64)
+    g = (p // chunk) * (-(-chunk // dp.group_size)) + (p % chunk) // dp.group_size
+    want = stored[p] | (dp.scales.view(np.uint16)[g].astype(np.uint32) << 16)
+    got = st.plug_aux.cpu().numpy().view(np.uint32)[:p.size]
+    np.testing.assert_array_equal(got, want)
