@@ -217,9 +217,20 @@ int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs,
                    void* workspace,
                    const pp_quad_item* tail_items, int64_t n_tail,
                    const float* const* luts, const float* scales,
-                   const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n,
+                   const uint32_t* plug_idx, const void* plug_vals, const uint32_t* plug_code, int64_t plug_n,
                    int64_t n_codes, const void* const* tails, const int64_t* tail_len,
                    int64_t M, void* stream);
+
+/*
+ * Plug side table of a quad stream (built once per stream, on the stream's device):
+ * code[j] = the code word at stream position plug_idx[j] (0 at or past n_codes).  Given to
+ * pp_quad_stream as plug_code, the plug corrections read the plugged words with the plug
+ * table instead of gathering them from the code stream (null: they gather).  No
+ * counterpart in the reference: a cache of values of its code array
+ * (quaternion_packer.py:155-157).
+ */
+int pp_quad_plug_codes(const uint32_t* codes, int64_t n_codes, const uint32_t* plug_idx, int64_t plug_n,
+                       uint32_t* code, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Dual pack: 16-bit [amp 6 | phase 10] -> 2 models.                          */

@@ -82,6 +82,7 @@ struct QuadRowsArgs {
   float s[4];
   const uint32_t* plug_idx;
   const f16* plug_vals;  // (P, 4)
+  const uint32_t* plug_code;  // per entry: the code word at its position, or null (gathered)
   int64_t plug_n;
   int M;
   void* ws;              // split segments: uint32 task counters, float32 accumulators
@@ -241,6 +242,11 @@ __device__ __forceinline__ rsrc_t plug_idx_rsrc(const QuadRowsArgs& A, int64_t p
   const uint32_t bytes = left <= 0 ? 0u : (uint32_t)std::min<int64_t>(left * 4, 0x7FFFFFF0);
   return make_rsrc(A.plug_idx + (left > 0 ? pc : 0), bytes);
 }
+__device__ __forceinline__ rsrc_t plug_code_rsrc(const QuadRowsArgs& A, int64_t pc) {
+  const int64_t left = A.plug_n - pc;
+  const uint32_t bytes = left <= 0 ? 0u : (uint32_t)std::min<int64_t>(left * 4, 0x7FFFFFF0);
+  return make_rsrc(A.plug_code + (left > 0 ? pc : 0), bytes);
+}
 __device__ __forceinline__ rsrc_t plug_val_rsrc(const QuadRowsArgs& A, int64_t pc) {
   const int64_t left = A.plug_n - pc;
   const uint32_t bytes = left <= 0 ? 0u : (uint32_t)std::min<int64_t>(left * 8, 0x7FFFFFF0);
@@ -275,7 +281,10 @@ __device__ __forceinline__ void plug_begin(const QuadRowsArgs& A, const SegCtx& 
   if (k < S.kbeg || k >= S.kend) row = -1;   // consumed with the task's rows, applied by its slice
   P.row = row;
   const bool v = row >= 0;
-  vload32(P.cw, v ? 4u * (uint32_t)((ti * RG + row) * S.ldc + k) : OOB, S.rc);
+  // the plugged word from the side table (entry pc + lane) or, without one, from the codes
+  const bool tab = A.plug_code != nullptr;
+  vload32(P.cw, v ? (tab ? 4u * lane : 4u * (uint32_t)((ti * RG + row) * S.ldc + k)) : OOB,
+          tab ? plug_code_rsrc(A, pc) : S.rc);
   vload64(P.pv, in ? 8u * lane : OOB, plug_val_rsrc(A, pc));
 #pragma unroll
   for (int j = 0; j < MT; ++j) vload16(P.xk[j], (v && j < A.M) ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
@@ -338,7 +347,7 @@ __device__ __forceinline__ int plug_end(const char* lds, const LaneOff& lo, cons
       float xk[MT];
 #pragma unroll
       for (int j = 0; j < MT; ++j) xk[j] = j < A.M ? (float)x[(int64_t)j * S.x_sm + k] : 0.f;
-      const uint32_t cw = codes[(int64_t)(ti * RG + row) * S.ldc + k];
+      const uint32_t cw = A.plug_code ? A.plug_code[q] : codes[(int64_t)(ti * RG + row) * S.ldc + k];
       const f16x4 pv = *reinterpret_cast<const f16x4*>(A.plug_vals + 4 * q);
       plug_correct<MT, RG, L>(lds, lo, row, cw, pv, xk, acc);
     }
@@ -419,7 +428,12 @@ template <int MT, int RG>
 __device__ __forceinline__ void task_accumulate(const QuadRowsArgs& A, const SegCtx& S, int ti, int lane,
                                                 float (&acc)[RG][4][MT]) {
   const Reduced<MT, RG> o = task_reduce<MT, RG>(A, S, ti, lane, acc);
-  const float sm = o.m == 0 ? A.s[0] : o.m == 1 ? A.s[1] : o.m == 2 ? A.s[2] : A.s[3];
+  // the scale of the lane's model, selected among values: a select among the loads
+  // A.s[0..3] would become an indexed load, which puts the kernel arguments in scratch
+  float sc[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) sc[m] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(A.s[m])));
+  const float sm = o.m == 0 ? sc[0] : o.m == 1 ? sc[1] : o.m == 2 ? sc[2] : sc[3];
   float* a = S.acc + ((int64_t)(o.m * A.M + o.j) * S.N + S.row0 + ti * RG + o.r);
   float before = 0.f;
   if (o.wr) before = __hip_atomic_fetch_add(a, o.y * sm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -857,12 +871,34 @@ extern "C" int64_t pp_quad_stream_waves(int64_t M) {
   return (int64_t)device_cu_count() * cfg_waves(round_mt(M));
 }
 
+// Side table of the plug entries: code[j] = the code word at stream position plug_idx[j]
+// (0 for an entry at or past n_codes).
+__global__ __launch_bounds__(256) void quad_plug_code_kernel(const uint32_t* codes, int64_t n_codes,
+                                                             const uint32_t* plug_idx, int64_t plug_n, uint32_t* code) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= plug_n) return;
+  const int64_t p = plug_idx[j];
+  code[j] = p < n_codes ? codes[p] : 0u;
+}
+
+extern "C" int pp_quad_plug_codes(const uint32_t* codes, int64_t n_codes, const uint32_t* plug_idx, int64_t plug_n,
+                                  uint32_t* code, void* stream) {
+  PP_REQUIRE(plug_n >= 0 && plug_n < (1ll << 31), "plug_n out of range");
+  if (plug_n == 0) return PP_OK;
+  PP_REQUIRE(codes != nullptr && plug_idx != nullptr && code != nullptr && n_codes >= 0, "null pointer or bad n_codes");
+  hipLaunchKernelGGL(quad_plug_code_kernel, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), codes, n_codes, plug_idx, plug_n, code);
+  PP_LAUNCH_CHECK();
+  return PP_OK;
+}
+
 extern "C" int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs, const pp_quad_seg* segs, int64_t n_segs,
                               const int64_t* seg_bounds, int64_t n_waves, void* workspace,
                               const pp_quad_item* tail_items,
                               int64_t n_tail, const float* const* luts, const float* scales,
-                              const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n, int64_t n_codes,
-                              const void* const* tails, const int64_t* tail_len, int64_t M, void* stream) {
+                              const uint32_t* plug_idx, const void* plug_vals, const uint32_t* plug_code,
+                              int64_t plug_n, int64_t n_codes, const void* const* tails, const int64_t* tail_len,
+                              int64_t M, void* stream) {
   PP_REQUIRE(projs != nullptr && n_projs >= 1, "no projections");
   PP_REQUIRE(n_segs >= 0 && (n_segs == 0 || (segs != nullptr && seg_bounds != nullptr)), "segs / seg_bounds is null");
   PP_REQUIRE(n_tail == 0 || tail_items != nullptr, "tail_items is null");
@@ -886,6 +922,7 @@ extern "C" int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs, const 
     for (int m = 0; m < 4; ++m) A.s[m] = scales[m];
     A.plug_idx = plug_idx;
     A.plug_vals = reinterpret_cast<const f16*>(plug_vals);
+    A.plug_code = plug_code;
     A.plug_n = plug_n;
     A.M = (int)M;
     A.ws = workspace;

@@ -267,6 +267,13 @@ class QuadStream:
         self._scales = nat.float_array(pack.s)
         self._tail_ptrs = nat.ptr_array([t.data_ptr() if t.numel() else 0 for t in pack.tails])
         self._tail_len = (C.c_int64 * 4)(*pack.tail_lengths)
+        # each plug entry's code word, gathered once here (pp_quad_plug_codes)
+        P = int(pack.plug_idx.numel())
+        self.plug_code = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
+        if P:
+            rc = L.pp_quad_plug_codes(pack.codes.data_ptr(), pack.n, pack.plug_idx.data_ptr(), P,
+                                      self.plug_code.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+            nat.check(rc, "pp_quad_plug_codes")
         self.projs = None
 
     # ---------------------------------------------------------------- buffers
@@ -318,6 +325,7 @@ class QuadStream:
                                       self._lut_ptrs, self._scales,
                                       pk.plug_idx.data_ptr() if pk.plug_idx.numel() else None,
                                       pk.plug_vals.data_ptr() if pk.plug_vals.numel() else None,
+                                      self.plug_code.data_ptr(),
                                       int(pk.plug_idx.numel()), pk.n, self._tail_ptrs, self._tail_len, self.M, stream)
         nat.check(rc, "pp_quad_stream")
 

@@ -135,3 +135,14 @@ def test_single_linear_split_k(shape, M):
             assert_gemv_close(outs[0][m].float().cpu().numpy(), ref, f"rep {rep} model {m}")
         assert int(torch.count_nonzero(st.workspace)) == 0
 
+
+
+def test_plug_side_table(tmp_path):
+    """pp_quad_plug_codes: each plug entry's code word (0 for an entry past n)."""
+    qp, path = make_file(tmp_path, tails=(0, 12 * 512 - 5 * 512 - 100, 0, 7))
+    pack = QuadPackFile.read(path).to_device(DEV)
+    assert qp.plug_idx.size > 0
+    st = QuadStream(pack, SHAPES, M=1)
+    want = qp.codes[qp.plug_idx.astype(np.int64)]
+    got = st.plug_code.cpu().numpy().view(np.uint32)[:want.size]
+    np.testing.assert_array_equal(got, want)
