@@ -285,9 +285,10 @@ int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk, int64_t c_
  * group rule of the file (group_size, chunk_size: groups restart every chunk);
  * amp_lut / cos_lut / sin_lut are float32 tables from the header (64 / 1024 / 1024
  * entries); plug entries replace the amplitude of a pair by an exact fp16 amplitude.
- * plug_aux (plug_n words, from pp_dual_plug_aux on the same codes and scales) holds each
- * entry's stored code and group scale, so the kernel reads them with the plug table
- * instead of gathering them from the code stream.
+ * plug_ent (3 words per entry, from pp_dual_plug_table for the same projections and
+ * pp_dual_stream_rows(M)) is each entry's record, read with the plug window instead of
+ * gathering the entry's code and scale from the stream; the kernel takes the plug
+ * amplitudes from it (plug_amp is read by the tail rows).
  * Positions >= n_codes come from the per-model fp16 tails (tails[m], tail_len[m]): a
  * build-defined extension for streams whose models have different lengths (the file
  * format itself zero-pads the shorter model).
@@ -327,20 +328,26 @@ int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs,
                    const pp_quad_item* tail_items, int64_t n_tail,
                    int code_layout, const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
                    const float* amp_lut, const float* cos_lut, const float* sin_lut,
-                   const uint32_t* plug_idx, const void* plug_amp, const uint32_t* plug_aux, int64_t plug_n,
+                   const uint32_t* plug_idx, const void* plug_amp, const uint32_t* plug_ent, int64_t plug_n,
                    int64_t n_codes, const void* const* tails, const int64_t* tail_len,
                    int64_t M, void* stream);
 
 /*
- * Plug side table of a dual stream (built once per stream, on the stream's device):
- * aux[j] = the stored 16-bit code of pair plug_idx[j] (in the codes' layout) | the fp16
- * bits of its group scale << 16, with the group rule of pp_dual_stream; 0 for an entry
- * at or past n_codes.  No counterpart in the reference: it is a cache of values of its
- * code and scale arrays (polar_bitpack.py:205-211) for the plug correction.
+ * Plug records of a dual stream (built once per stream plan, on the stream's device):
+ * for entry j at stream position p = plug_idx[j],
+ *   ent[3j]   = (row of p in its task of rows_per_task rows) << 24 | column of p,
+ *               where projection i covers [proj_pos0[i], proj_pos0[i+1]) with rows of
+ *               proj_k[i] < 2^24 columns (proj_pos0 has n_projs + 1 entries), 0 outside;
+ *   ent[3j+1] = the stored 16-bit code of pair p (in the codes' layout) | the fp16 bits
+ *               of its group scale << 16 (group rule of pp_dual_stream), 0 at or past n_codes;
+ *   ent[3j+2] = the fp16 bits of plug_amp[j].
+ * No counterpart in the reference: an index over its code, scale and plug arrays
+ * (polar_bitpack.py:205-211) for the plug correction.
  */
-int pp_dual_plug_aux(const void* codes, int64_t n_codes, const void* scales, int64_t n_groups,
-                     int64_t group_size, int64_t chunk_size, const uint32_t* plug_idx, int64_t plug_n,
-                     uint32_t* aux, void* stream);
+int pp_dual_plug_table(const void* codes, int64_t n_codes, const void* scales, int64_t n_groups,
+                       int64_t group_size, int64_t chunk_size, const uint32_t* plug_idx, const void* plug_amp,
+                       int64_t plug_n, const int64_t* proj_pos0, const int32_t* proj_k, int64_t n_projs,
+                       int64_t rows_per_task, uint32_t* ent, void* stream);
 
 #ifdef __cplusplus
 }

@@ -53,7 +53,8 @@ struct DualStreamArgs {
   int log2gs;
   const uint32_t* plug_idx;
   const f16* plug_amp;
-  const uint32_t* plug_aux;   // per entry: its pair's stored code | group scale bits << 16
+  const uint32_t* plug_ent;   // per entry 3 words: row in its task << 24 | column; stored code |
+                              // group scale bits << 16; plug amplitude bits
   int64_t plug_n;
   const int64_t* task_plug;   // per task: first plug entry in its rows, first entry past them
   int64_t n_tasks;
@@ -250,15 +251,15 @@ __device__ __forceinline__ void dchunk_compute(const char* lds, const DualLane& 
 }
 
 // Plug entries.  The host gives every task its plug range [tlo, thi): the entries whose
-// positions lie in the task's rows.  Step ck of a task takes the window of entries
+// positions lie in the task's rows, and every entry its 12-byte record plug_ent (row in
+// its task and column, the stored code and group scale of its pair, the plug amplitude),
+// so a window needs one contiguous load and the x gather, and no position arithmetic.  Step ck of a task takes the window of entries
 // tlo + 64*PW*ck .. +64*PW (one entry per lane and window, filled from the front); a
 // task with more entries than its steps can take corrects the rest when it finishes.
 // A window passes through three stages, one step apart, so that every load is issued a
 // step before the step that reads it and the number of loads per step is fixed:
-//   step s-2: the entries' positions;
-//   step s-1: the stored code and group scale (one word of the side table plug_aux, so
-//             that nothing is gathered from the code stream), the plug amplitude and x
-//             at each entry;
+//   step s-2: the entries' records;
+//   step s-1: x at each entry's column;
 //   step s:   acc[row] += (plug amp - amp_lut[aq] * scale) * x * (cos, sin)(phase).
 // Lanes without an entry load nothing (reads of 0 make their correction 0).
 
@@ -282,41 +283,34 @@ struct DWin {
   int q[PW];                           // row of the entry in its task, -1 for none
 };
 
-// Stage 1: the positions of the window's entries.
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+
+// Stage 1: the records of the window's entries.
 template <int PW>
-__device__ __forceinline__ void dwin_positions(const DualStreamArgs& A, const DSlot& t, int lane, uint32_t (&idx)[PW]) {
+__device__ __forceinline__ void dwin_positions(const DualStreamArgs& A, const DSlot& t, int lane, u32x3 (&ent)[PW]) {
   const int cnt = dslot_cnt<PW>(t);
-  const uint32_t base = 4u * (uint32_t)t.lo;
+  const uint32_t base = 12u * (uint32_t)t.lo;
+  const rsrc_t r = make_rsrc(A.plug_ent, 12u * (uint32_t)A.plug_n);
 #pragma unroll
   for (int w = 0; w < PW; ++w)
-    vload32(idx[w], 64 * w + lane < cnt ? base + 4u * (uint32_t)(64 * w + lane) : OOB,
-            make_rsrc(A.plug_idx, 4u * (uint32_t)A.plug_n));
+    ent[w] = __builtin_amdgcn_raw_buffer_load_b96(
+        r, (int)(64 * w + lane < cnt ? base + 12u * (uint32_t)(64 * w + lane) : OOB), 0, 0);
 }
 
-// Stage 2: per entry its row in the task, and the loads its correction needs.
+// Stage 2: per entry its row in the task, and x at its column.
 template <int MT, int RG, int PW, int SM>
 __device__ __forceinline__ void dwin_data(const DualStreamArgs& A, const DualSeg& S, const DSlot& t,
-                                          const uint32_t (&idx)[PW], int lane, DWin<MT, PW>& W) {
+                                          const u32x3 (&ent)[PW], int lane, DWin<MT, PW>& W) {
   const int cnt = dslot_cnt<PW>(t);
-  const int64_t trow0 = (int64_t)t.ti * RG * S.ldc;        // task start, pairs from the segment start
-  const int64_t tpos0 = S.pos0 + trow0;
-  const int64_t span = (int64_t)min(RG, S.nrows - t.ti * RG) * S.ldc;
-  const uint32_t pbase = 2u * (uint32_t)t.lo;
 #pragma unroll
   for (int w = 0; w < PW; ++w) {
     const int e = 64 * w + lane;
-    const int64_t off = (int64_t)idx[w] - tpos0;
-    bool v = e < cnt && off >= 0 && off < span;
-    const int o = v ? (int)off : 0;
-    int row = 0;
-#pragma unroll
-    for (int r = 1; r < RG; ++r)
-      if (o >= r * S.ldc) row = r;
-    const int k = o - row * S.ldc;
-    v = v && k >= S.kbeg && k < S.kend;   // entries of the task's other column slices are theirs
+    const int row = (int)(ent[w].x >> 24), k = (int)(ent[w].x & 0xFFFFFFu);
+    // entries of the task's other column slices are theirs
+    const bool v = e < cnt && k >= S.kbeg && k < S.kend;
     W.q[w] = v ? row : -1;
-    vload32(W.aux[w], v ? 2u * pbase + 4u * (uint32_t)e : OOB, make_rsrc(A.plug_aux, 4u * (uint32_t)A.plug_n));
-    vload16(W.pa[w], v ? pbase + 2u * (uint32_t)e : OOB, make_rsrc(A.plug_amp, 2u * (uint32_t)A.plug_n));
+    W.aux[w] = ent[w].y;
+    W.pa[w] = ent[w].z;
 #pragma unroll
     for (int j = 0; j < MT; ++j)
       vload16(W.xk[w][j], (v && j < A.M) ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
@@ -446,7 +440,7 @@ struct DualRunner {
   DSlot s0, s1, s2;          // windows of steps s, s+1, s+2 (s = the step being computed)
   Cursor c3;                 // step s+3, whose task plug range is in flight
   u32x4 T;                   // that range: {tlo lo, tlo hi, thi lo, thi hi}
-  uint32_t I[PW];            // positions of the entries of step s+1's window
+  u32x3 I[PW];               // records of the entries of step s+1's window
   DWin<MT, PW> D;            // data of step s's window
 
   __device__ __forceinline__ DualRunner(const char* l, const DualStreamArgs& a, const DualSeg& s, int t0)
@@ -499,7 +493,7 @@ struct DualRunner {
   // Entries of the finished task that its steps could not take, then its outputs.
   __device__ __forceinline__ void finish_pending() {
     for (DSlot t = pend_left; t.rem > 0; t.lo += 64 * PW, t.rem -= 64 * PW) {
-      uint32_t idx[PW];
+      u32x3 idx[PW];
       DWin<MT, PW> W;
       dwin_positions<PW>(A, t, lane, idx);
       dwin_data<MT, RG, PW, SM>(A, S, t, idx, lane, W);
@@ -787,21 +781,38 @@ __global__ __launch_bounds__(256) void dual_tail_kernel(const DualTailArgs T) {
   }
 }
 
-// Side table of the plug entries: aux[j] = stored 16-bit code of pair plug_idx[j] |
-// fp16 bits of its group scale << 16 (0 for an entry at or past n_codes).
-__global__ __launch_bounds__(256) void dual_plug_aux_kernel(const uint16_t* codes, const f16* scales, int64_t n_groups,
-                                                            int64_t gs, int64_t chunk, const uint32_t* plug_idx,
-                                                            int64_t plug_n, int64_t n_codes, uint32_t* aux) {
+// Records of the plug entries for the stream decode (see DualStreamArgs::plug_ent).
+// Projection p covers stream positions [proj_pos0[p], proj_pos0[p] + N_p * proj_k[p]);
+// proj_pos0 has n_projs + 1 entries (the last one the end of the stream's projections).
+__global__ __launch_bounds__(256) void dual_plug_table_kernel(const uint16_t* codes, int64_t n_codes, const f16* scales,
+                                                              int64_t n_groups, int64_t gs, int64_t chunk,
+                                                              const uint32_t* plug_idx, const f16* plug_amp,
+                                                              int64_t plug_n, const int64_t* proj_pos0,
+                                                              const int32_t* proj_k, int n_projs, int rows_per_task,
+                                                              uint32_t* ent) {
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= plug_n) return;
   const int64_t p = plug_idx[j];
-  uint32_t v = 0;
+  uint32_t w0 = 0, w1 = 0;
   if (p < n_codes) {
     const int64_t g = (p / chunk) * ((chunk + gs - 1) / gs) + (p % chunk) / gs;
     const uint32_t sc = g < n_groups ? (uint32_t)__builtin_bit_cast(unsigned short, scales[g]) : 0u;
-    v = (uint32_t)codes[p] | (sc << 16);
+    w1 = (uint32_t)codes[p] | (sc << 16);
   }
-  aux[j] = v;
+  if (p >= proj_pos0[0] && p < proj_pos0[n_projs]) {
+    int lo = 0, hi = n_projs - 1;                   // last projection starting at or before p
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (proj_pos0[mid] <= p) lo = mid;
+      else hi = mid - 1;
+    }
+    const int64_t local = p - proj_pos0[lo], K = proj_k[lo];
+    const int64_t row = local / K;
+    w0 = ((uint32_t)(row % rows_per_task) << 24) | (uint32_t)(local - row * K);
+  }
+  ent[3 * j] = w0;
+  ent[3 * j + 1] = w1;
+  ent[3 * j + 2] = (uint32_t)__builtin_bit_cast(unsigned short, plug_amp[j]);
 }
 
 // ------------------------------------------------------------------ host side
@@ -856,18 +867,22 @@ extern "C" int pp_dual_stream_rows(int64_t M) {
   return dual_stream_rg(dual_stream_mt(M));
 }
 
-extern "C" int pp_dual_plug_aux(const void* codes, int64_t n_codes, const void* scales, int64_t n_groups,
-                                int64_t group_size, int64_t chunk_size, const uint32_t* plug_idx, int64_t plug_n,
-                                uint32_t* aux, void* stream) {
-  PP_REQUIRE(plug_n >= 0 && plug_n < (1ll << 31), "plug_n out of range");
+extern "C" int pp_dual_plug_table(const void* codes, int64_t n_codes, const void* scales, int64_t n_groups,
+                                  int64_t group_size, int64_t chunk_size, const uint32_t* plug_idx,
+                                  const void* plug_amp, int64_t plug_n, const int64_t* proj_pos0,
+                                  const int32_t* proj_k, int64_t n_projs, int64_t rows_per_task, uint32_t* ent,
+                                  void* stream) {
+  PP_REQUIRE(plug_n >= 0 && plug_n < (1ll << 28), "the stream decode takes fewer than 2^28 plug entries");
   if (plug_n == 0) return PP_OK;
-  PP_REQUIRE(codes != nullptr && scales != nullptr && plug_idx != nullptr && aux != nullptr, "null pointer");
-  PP_REQUIRE(n_codes >= 0 && n_groups >= 1, "bad n_codes / n_groups");
-  PP_REQUIRE(group_size >= 1 && chunk_size >= 1, "bad group_size / chunk_size");
-  hipLaunchKernelGGL(dual_plug_aux_kernel, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const uint16_t*>(codes),
-                     reinterpret_cast<const f16*>(scales), n_groups, group_size, chunk_size, plug_idx, plug_n, n_codes,
-                     aux);
+  PP_REQUIRE(codes && scales && plug_idx && plug_amp && proj_pos0 && proj_k && ent, "null pointer");
+  PP_REQUIRE(n_codes >= 0 && n_groups >= 1 && group_size >= 1 && chunk_size >= 1, "bad sizes");
+  PP_REQUIRE(n_projs >= 1 && n_projs < (1ll << 30), "bad n_projs");
+  PP_REQUIRE(rows_per_task >= 1 && rows_per_task <= 255, "bad rows_per_task");
+  hipLaunchKernelGGL(dual_plug_table_kernel, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const uint16_t*>(codes), n_codes,
+                     reinterpret_cast<const f16*>(scales), n_groups, group_size, chunk_size, plug_idx,
+                     reinterpret_cast<const f16*>(plug_amp), plug_n, proj_pos0, proj_k, (int)n_projs,
+                     (int)rows_per_task, ent);
   PP_LAUNCH_CHECK();
   return PP_OK;
 }
@@ -886,7 +901,7 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
                               int64_t n_tail, int code_layout, const void* scales, int64_t n_groups,
                               int64_t group_size, int64_t chunk_size, const float* amp_lut, const float* cos_lut,
                               const float* sin_lut, const uint32_t* plug_idx, const void* plug_amp,
-                              const uint32_t* plug_aux, int64_t plug_n,
+                              const uint32_t* plug_ent, int64_t plug_n,
                               int64_t n_codes, const void* const* tails, const int64_t* tail_len, int64_t M,
                               void* stream) {
   PP_REQUIRE(projs != nullptr && n_projs >= 1, "no projections");
@@ -894,7 +909,7 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
   PP_REQUIRE(n_segs == 0 || (task_plug != nullptr && n_tasks >= 1 && n_tasks < (1ll << 27)),
              "task_plug is null or n_tasks out of range");
   PP_REQUIRE(plug_windows == 1 || plug_windows == 2, "plug_windows must be 1 or 2");
-  PP_REQUIRE(plug_n < (1ll << 30), "the stream decode takes fewer than 2^30 plug entries");
+  PP_REQUIRE(plug_n < (1ll << 28), "the stream decode takes fewer than 2^28 plug entries");
   PP_REQUIRE(n_tail == 0 || tail_items != nullptr, "tail_items is null");
   PP_REQUIRE(code_layout == PP_DUAL_I16_OFFSET || code_layout == PP_DUAL_U16_BE, "bad code_layout");
   PP_REQUIRE(amp_lut && cos_lut && sin_lut, "lut pointers are null");
@@ -903,7 +918,7 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
              "the stream decode needs a power-of-two group_size >= 8");
   PP_REQUIRE(chunk_size >= 8 && chunk_size % 8 == 0, "the stream decode needs chunk_size % 8 == 0");
   PP_REQUIRE(plug_n >= 0 && (plug_n == 0 || (plug_idx != nullptr && plug_amp != nullptr)), "plug arrays are null");
-  PP_REQUIRE(plug_n == 0 || n_segs == 0 || plug_aux != nullptr, "plug_aux is null (build it with pp_dual_plug_aux)");
+  PP_REQUIRE(plug_n == 0 || n_segs == 0 || plug_ent != nullptr, "plug_ent is null (build it with pp_dual_plug_table)");
   PP_REQUIRE(M >= 1 && M <= 4, "the dual stream decode takes 1..4 tokens, got %lld", (long long)M);
   PP_REQUIRE(n_segs == 0 || n_waves == pp_dual_stream_waves(M),
              "seg_bounds were built for %lld waves, this device launches %lld", (long long)n_waves,
@@ -928,7 +943,7 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
   while ((1ll << A.log2gs) < group_size) ++A.log2gs;
   A.plug_idx = plug_idx;
   A.plug_amp = reinterpret_cast<const f16*>(plug_amp);
-  A.plug_aux = plug_aux;
+  A.plug_ent = plug_ent;
   A.plug_n = plug_n;
   A.task_plug = task_plug;
   A.n_tasks = n_tasks;

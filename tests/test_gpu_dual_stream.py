@@ -232,9 +232,10 @@ def test_single_linear_split_k(shape, M):
 
 @pytest.mark.parametrize("layout", ["u16be", "i16"])
 @pytest.mark.parametrize("chunk", [50_000_000, 1000])
-def test_plug_side_table(layout, chunk):
-    """pp_dual_plug_aux: each entry's stored code | its group's fp16 scale bits << 16,
-    with groups restarting every chunk (polar_bitpack.py:201-203)."""
+def test_plug_records(layout, chunk):
+    """pp_dual_plug_table: each entry's row in its task and column, its pair's stored code
+    | its group's fp16 scale bits << 16 (groups restart every chunk, polar_bitpack.py:201-203),
+    and its plug amplitude."""
     w1, w2 = gen.correlated_models(31, [TOTAL, TOTAL], delta_growth=False)
     dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=0.03, chunk_size=chunk))
     pack = device_pack(dp, layout)
@@ -242,6 +243,11 @@ def test_plug_side_table(layout, chunk):
     stored = pack.codes.cpu().numpy().view(np.uint16).astype(np.uint32)
     p = dp.plug_idx.astype(np.int64)
     g = (p // chunk) * (-(-chunk // dp.group_size)) + (p % chunk) // dp.group_size
-    want = stored[p] | (dp.scales.view(np.uint16)[g].astype(np.uint32) << 16)
-    got = st.plug_aux.cpu().numpy().view(np.uint32)[:p.size]
-    np.testing.assert_array_equal(got, want)
+    pos0 = np.cumsum([0] + [n * k for n, k in SHAPES])
+    proj = np.searchsorted(pos0, p, side="right") - 1
+    K = np.array([k for _, k in SHAPES])[proj]
+    row, col = (p - pos0[proj]) // K, (p - pos0[proj]) % K
+    ent = st.plug_ent.cpu().numpy().view(np.uint32)[:3 * p.size].reshape(-1, 3)
+    np.testing.assert_array_equal(ent[:, 0], ((row % st.rows_per_item) << 24) | col)
+    np.testing.assert_array_equal(ent[:, 1], stored[p] | (dp.scales.view(np.uint16)[g].astype(np.uint32) << 16))
+    np.testing.assert_array_equal(ent[:, 2], dp.plug_val.view(np.uint16))
