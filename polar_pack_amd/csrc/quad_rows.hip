@@ -24,8 +24,9 @@
 //    plug entries read zero without branches.
 //  * Plug table.  Entries are consumed in order: a task's entries are the next ones in
 //    the sorted list whose position falls before the task's end.  Their positions are
-//    loaded one task ahead; the plugged code, its fp16 values and x at its column are
-//    loaded with the task's first chunk, and each entry is applied as the exact
+//    loaded one task ahead; the plugged code (from the side table plug_code when the
+//    caller built one, else from the code stream), its fp16 values and x at its column
+//    are loaded with the task's first chunk, and each entry is applied as the exact
 //    correction x*(plug - decoded) before the reduction (quaternion_packer.py:187-193
 //    replaces the decoded tuple by the plug tuple; the sum is the same).
 //  * Reduction.  The RG*4*MT partial sums of a lane are reduced across the wavefront by
