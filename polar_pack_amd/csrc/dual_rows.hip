@@ -657,23 +657,29 @@ __device__ __forceinline__ void dual_tail_rows(const DualTailArgs& T, const pp_q
     for (int m = 0; m < 2; ++m)
 #pragma unroll
       for (int j = 0; j < MT; ++j) acc[r][m][j] = 0.f;
-  for (int kc = 0; kc < K; kc += 512) {
+  // 512 columns per step, the next step's loads in flight while one is summed (columns
+  // past K read 0)
+  struct Step {
+    u32x4 xr[MT];
+    u32x4 wr[R][2];
+  };
+  auto issue = [&](int kc, Step& c) {
     const int k = kc + 8 * lane;
     const bool kin = k < K;
-    u32x4 xr[MT];
 #pragma unroll
-    for (int j = 0; j < MT; ++j) vload128c(xr[j], (kin && j < M) ? 2u * (uint32_t)(j * x_sm + k) : OOB, rx);
-    u32x4 wr[R][2];
+    for (int j = 0; j < MT; ++j) vload128c(c.xr[j], (kin && j < M) ? 2u * (uint32_t)(j * x_sm + k) : OOB, rx);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int m = 0; m < 2; ++m)
-        vload128(wr[r][m], (kin && r < nr) ? 2u * (uint32_t)(r * ldc + k) : OOB, rt[m]);
+        vload128(c.wr[r][m], (kin && r < nr) ? 2u * (uint32_t)(r * ldc + k) : OOB, rt[m]);
+  };
+  auto sum = [&](const Step& c) {
     float xv[MT][8];
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
-      const f16x4 h0 = __builtin_bit_cast(f16x4, u32x2{xr[j].x, xr[j].y});
-      const f16x4 h1 = __builtin_bit_cast(f16x4, u32x2{xr[j].z, xr[j].w});
+      const f16x4 h0 = __builtin_bit_cast(f16x4, u32x2{c.xr[j].x, c.xr[j].y});
+      const f16x4 h1 = __builtin_bit_cast(f16x4, u32x2{c.xr[j].z, c.xr[j].w});
       xv[j][0] = (float)h0.x; xv[j][1] = (float)h0.y; xv[j][2] = (float)h0.z; xv[j][3] = (float)h0.w;
       xv[j][4] = (float)h1.x; xv[j][5] = (float)h1.y; xv[j][6] = (float)h1.z; xv[j][7] = (float)h1.w;
     }
@@ -681,8 +687,8 @@ __device__ __forceinline__ void dual_tail_rows(const DualTailArgs& T, const pp_q
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        const f16x4 h0 = __builtin_bit_cast(f16x4, u32x2{wr[r][m].x, wr[r][m].y});
-        const f16x4 h1 = __builtin_bit_cast(f16x4, u32x2{wr[r][m].z, wr[r][m].w});
+        const f16x4 h0 = __builtin_bit_cast(f16x4, u32x2{c.wr[r][m].x, c.wr[r][m].y});
+        const f16x4 h1 = __builtin_bit_cast(f16x4, u32x2{c.wr[r][m].z, c.wr[r][m].w});
         const float wv[8] = {(float)h0.x, (float)h0.y, (float)h0.z, (float)h0.w,
                              (float)h1.x, (float)h1.y, (float)h1.z, (float)h1.w};
 #pragma unroll
@@ -690,6 +696,15 @@ __device__ __forceinline__ void dual_tail_rows(const DualTailArgs& T, const pp_q
 #pragma unroll
           for (int j = 0; j < MT; ++j) acc[r][m][j] = fmaf(wv[e], xv[j][e], acc[r][m][j]);
       }
+  };
+  Step c0, c1;
+  issue(0, c0);
+  for (int kc = 0; kc < K; kc += 1024) {
+    issue(kc + 512, c1);
+    sum(c0);
+    if (kc + 512 >= K) break;
+    issue(kc + 1024, c0);
+    sum(c1);
   }
   float v[NV];
 #pragma unroll

@@ -63,8 +63,14 @@ template <int MT> struct RowsCfg;
 template <> struct RowsCfg<1> {
   static constexpr int RG = PP_ROWS1_RG, NSEG = PP_ROWS1_NSEG, NT = PP_ROWS1_NT;
 };
+#ifndef PP_ROWS4_RG
+#define PP_ROWS4_RG 1
+#endif
+#ifndef PP_ROWS4_NSEG
+#define PP_ROWS4_NSEG 2
+#endif
 template <> struct RowsCfg<2> { static constexpr int RG = 2, NSEG = 2, NT = 512; };
-template <> struct RowsCfg<4> { static constexpr int RG = 1, NSEG = 2, NT = 512; };
+template <> struct RowsCfg<4> { static constexpr int RG = PP_ROWS4_RG, NSEG = PP_ROWS4_NSEG, NT = 512; };
 template <> struct RowsCfg<8> { static constexpr int RG = 1, NSEG = 2, NT = 512; };
 
 struct QuadRowsArgs {
