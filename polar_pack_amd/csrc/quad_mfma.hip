@@ -30,16 +30,17 @@ namespace pp {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-// Threads per workgroup (one workgroup per CU: the tables take all of LDS), by token
-// tiles: as many waves as the registers allow (4, 3, 2 per SIMD for 1, 2, 4 tiles), for
-// the memory parallelism of a latency-bound walk.
+// Threads per workgroup: 8 waves (one workgroup per CU: the tables take all of LDS).
 // SUB: 32-column MFMA steps per stage.  A stage is what one load step brings in: SUB x 2
 // KiB of codes per wave; 1 step (2 KiB) per stage left the waves waiting a full HBM round
 // trip per step, 4 steps (8 KiB, as much as the row kernel keeps in flight) hide it.
-// With 4 token tiles the x operands of 4 steps would not fit in registers: 2.
+// With 2 or 4 token tiles the x operands take the registers: 2 steps (measured faster
+// than 4 with 2 tiles: 49.5 vs 53.3 us on an 11008x2048 Linear at 32 tokens).
+// (Running the LDS lookups a group of tuples ahead of their arithmetic, as the row
+// kernel does, measured no faster here.)
 template <int T> struct MfCfg {
   static constexpr int NT = 512;
-  static constexpr int SUB = T == 4 ? 2 : 4;
+  static constexpr int SUB = T == 1 ? 4 : 2;
 };
 
 struct QuadMfmaArgs {
