@@ -164,12 +164,14 @@ struct Tup {
 // acc2 += t2*c3, acc3 += t2*s3 (3 mul + 4 fma per tuple).
 // The lookups run one group of GT tuples ahead of the arithmetic (the scheduler would
 // otherwise wait for each tuple's four reads before issuing the next tuple's), with
-// at most 2*4*GT LDS reads in flight (the LDS counter holds 15).
+// at most 2*4*GT LDS reads in flight (the LDS counter holds 15).  GT = 2 measured 0.4%
+// faster than 4 on the 3B-shaped stream (1.796 vs 1.802 ms, means of 4-6 runs on three
+// boxes); 8 spills.
 template <int MT, int RG, int NSEG, class L>
 __device__ __forceinline__ void chunk_compute(const char* lds, const LaneOff& lo, const Chunk<MT, RG, NSEG>& c,
                                               float (&acc)[RG][4][MT]) {
 #ifndef PP_LOOKUP_GROUP
-#define PP_LOOKUP_GROUP 4
+#define PP_LOOKUP_GROUP 2
 #endif
   constexpr int GT = PP_LOOKUP_GROUP;       // tuples per group
   constexpr int NT = RG * NSEG * 4;         // tuples per lane in the chunk
