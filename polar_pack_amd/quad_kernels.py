@@ -129,7 +129,13 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
     pi, pv, pn, keep = _plug_args(plug, dev)
     L = nat.lib()
     if M > 8 and _mfma_layout_ok(codes, K):
-        return _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
+        # the matrix-core path takes up to 64 tokens per launch: larger batches (the
+        # reference's prefill sizes, quad_kernels.py:166-189) run in blocks of 64 rows
+        for i0 in range(0, M, 64):
+            i1 = min(M, i0 + 64)
+            _quad_mfma(a[i0:i1], codes, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base),
+                       [o[i0:i1] for o in outs], L, dev)
+        return outs
     if a.stride(1) != 1 or a.data_ptr() % 8 or (M > 1 and a.stride(0) % 4):
         a = a.contiguous()
     ws_bytes = L.pp_quad_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), codes.data_ptr(),

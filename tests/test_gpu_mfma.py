@@ -105,8 +105,9 @@ def test_dense_plug_rows_refill_the_window():
     check(outs, oracle(qp, 0, 32, 512, x_np), "dense")
 
 
-@pytest.mark.parametrize("M", [12, 64])
+@pytest.mark.parametrize("M", [12, 64, 100, 130])
 def test_drop_in_operator_takes_the_matrix_cores_for_large_batches(M):
+    """9..64 tokens in one launch; more (the reference's prefill sizes) in blocks of 64."""
     qp, pack = packed(SHAPES, 35, threshold=0.015)
     N, K = SHAPES[1]
     pos = SHAPES[0][0] * SHAPES[0][1]
