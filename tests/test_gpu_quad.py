@@ -202,3 +202,28 @@ def test_pack_quad_layer_on_gpu_matches_oracle():
         assert abs(scales[k] - rs[k]) <= 1e-6 * rs[k]
     for i in range(1, 7):
         np.testing.assert_array_equal(luts[i].cpu().numpy().view(np.uint16), rl[i].view(np.uint16))
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6])
+@pytest.mark.parametrize("K,N,plug", [(2048, 1000, 0), (2048, 1000, 700), (64, 96, 0), (520, 4096, 300)])
+def test_quad_gemm_kn_layout_fast_path(K, N, plug, M):
+    """Contiguous (K,N) codes, the layout pack_quad_layer returns: the fused (K,N) kernel
+    (256-column items, K slices whose partial sums a finish pass adds, plug corrections
+    per entry; blocks of 4 tokens), against the float64 oracle."""
+    seed = K + N + plug + M
+    codes = random_codes((K, N), seed)
+    luts, scales = fp16_luts(seed)
+    rng = np.random.default_rng(seed)
+    base = 1000
+    flat = np.sort(rng.choice(K * N, plug, replace=False)).astype(np.uint32)
+    vals = (rng.standard_normal((plug, 4)) * 0.5).astype(np.float16)
+    a = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
+    kw = {}
+    if plug:
+        kw = dict(plug=(u32(flat + base).to(DEV), torch.from_numpy(vals).to(DEV)), elem_base=base)
+    outs = qk.quad_bitpacked(a.to(DEV), u32(codes).to(DEV), [l.to(DEV) for l in luts], scales, **kw)
+    W = oracle_w(codes, luts, scales)
+    kk, nn = flat // N, flat % N
+    for k in range(4):
+        W[k][kk, nn] = vals[:, k].astype(np.float64) * scales[k]
+        assert_gemv_close(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), W[k]), f"model {k}")
