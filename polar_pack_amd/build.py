@@ -16,7 +16,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libpolar_pack.so")
-SOURCES = ["capi.hip", "quad.hip", "quad_rows.hip", "quad_mfma.hip", "quad_kn.hip", "dual.hip", "dual_rows.hip"]
+SOURCES = ["capi.hip", "quad.hip", "quad_rows.hip", "quad_mfma.hip", "quad_kn.hip", "dual.hip", "dual_rows.hip", "dual_kn.hip"]
 ARCH = "gfx950"
 
 # Packed FP32 instructions are disabled for all device code (their results have been

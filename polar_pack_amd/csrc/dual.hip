@@ -13,9 +13,12 @@
 //                         group scale, so the scale multiplies a per-lane partial sum once
 //                         per 8 pairs (x * amp_lut, then 2 fma per pair).  Plug entries
 //                         replace the amplitude as exact corrections.
+//   dual_kn_gemm       -- (dual_kn.hip) codes (K,N) with unit column stride, the layout
+//                         quantize_polar_bitpacked returns, in blocks of up to 4 tokens.
 //   dual_dequant_kernel / dual_plug_scatter_kernel / dual_ws_gemm_kernel -- generic path
 //                         and parity export (any strides, both group-index modes).
-#include "pp_common.h"
+#include "dual_kn.h"
+#include "dual_lds.h"
 
 #include <algorithm>
 
@@ -25,12 +28,6 @@ constexpr int DREPL_A = 32;   // amplitude table replicas (b32 reads)
 constexpr int DREPL_C = 16;   // (cos, sin) table replicas (b64 reads)
 constexpr int DSEG = 512;     // codes per wave per row per step (64 lanes x 8)
 constexpr int rows_threads_dual(int MT) { return MT >= 4 ? 512 : 1024; }
-
-struct DualLuts {
-  const void* amp;
-  const void* cs[2];  // cos, sin
-  int amp_n, phase_n, dtype;
-};
 
 struct DualLds {
   float amp[64 * DREPL_A];
@@ -472,6 +469,9 @@ extern "C" int64_t pp_dual_gemm_workspace_size(const void* a, int64_t a_sm, int6
   if (M <= 0 || N <= 0) return 0;
   if (dual_fast_ok(a, a_sm, a_sk, codes, c_sk, c_sn, elem_base, chunk_size, group_size, M, K))
     return dual_plan(M, N, K, plug_n).total();
+  // (K,N) codes: blocks of up to 4 tokens, one after another, sharing the workspace
+  if (dual_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, group_size, chunk_size, std::min<int64_t>(M, 4), N, K))
+    return dual_kn_workspace(std::min<int64_t>(M, 4), N, K, plug_n);
   return 2 * N * K * (int64_t)sizeof(float);
 }
 
@@ -591,6 +591,16 @@ extern "C" int pp_dual_gemm(const void* a, int64_t a_sm, int64_t a_sk, const voi
     }
     return code_layout == PP_DUAL_U16_BE ? dispatch_dual_rows<PP_DUAL_U16_BE>(A, mt, st)
                                          : dispatch_dual_rows<PP_DUAL_I16_OFFSET>(A, mt, st);
+  }
+  if (dual_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, group_size, chunk_size, std::min<int64_t>(M, 4), N, K)) {
+    for (int64_t i0 = 0; i0 < M; i0 += 4) {
+      void* o[2] = {reinterpret_cast<f16*>(out1) + i0 * o_sm, reinterpret_cast<f16*>(out2) + i0 * o_sm};
+      if (int rc = dual_kn_gemm(reinterpret_cast<const f16*>(a) + i0 * a_sm, a_sm, codes, code_layout, c_sk, bmax,
+                                group_size, L, plug_idx, plug_amp, plug_n, elem_base, o, o_sm, o_sn,
+                                std::min<int64_t>(4, M - i0), N, K, workspace, workspace_bytes, st))
+        return rc;
+    }
+    return PP_OK;
   }
   const int64_t need = 2 * N * K * (int64_t)sizeof(float);
   PP_REQUIRE(workspace != nullptr && workspace_bytes >= need, "workspace too small: need %lld bytes",

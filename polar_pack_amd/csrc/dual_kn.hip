@@ -1,0 +1,361 @@
+// Fused dual-pack decode GEMV for codes laid out (K,N) with unit column stride: the
+// layout quantize_polar_bitpacked returns (polar_kernels.py:118-140) and
+// polar_dual_bitpacked_kernel reads (polar_kernels.py:27-95), for 1..4 tokens per launch.
+//
+//   out_m[j, n] = fp16( sum_k a[j, k] * W_m[k, n] ),   m = 1, 2,
+//   W_1 = amp cos_lut[phase],  W_2 = amp sin_lut[phase],
+//   amp = amp_lut[amp_q] * bmax[(k*N + n) / gs]            (polar_kernels.py:64-79)
+//
+// with the LDS tables of dual_lds.h.  Work item = 512 columns x one slice of rows, one
+// wavefront: lane l owns columns n0 + 8l .. +7 (one 16-byte load per row), 8 rows per step,
+// the next step's loads in flight while one is decoded.  The 8 codes of a lane and row
+// share one group scale (gs is a power of two >= 8 and N % 8 == 0, so (k*N + n) / gs is
+// the same for the 8 columns), one 2-byte load per row; the activations of a row are the
+// same for every lane (one 16-byte load of 8 rows per token).  Each lane keeps its own 8
+// columns' sums, so no cross-lane reduction.  With one slice and no plug table the wave
+// writes its fp16 outputs; otherwise every slice stores its float32 partial sums
+// [slice][m][j][n], plug corrections are added to slice 0 by dual_kn_plug_kernel (one
+// thread per entry) and dual_kn_finish_kernel sums the slices into the fp16 outputs.
+#include "dual_kn.h"
+#include "dual_lds.h"
+#include "rows_common.h"
+
+namespace pp {
+
+constexpr int DKN_COLS = 512;  // columns per item: 64 lanes x 8
+constexpr int DKN_R = 8;       // rows per step
+constexpr int DKN_NT = 512;    // threads per workgroup (one per CU: the tables take most of LDS)
+
+struct DualKnArgs {
+  const uint16_t* codes;   // code of (row 0, col 0); row k at codes + k*ldk
+  int64_t ldk;
+  const f16* a;            // (M, K), row stride a_sm, unit column stride
+  int64_t a_sm;
+  f16* out[2];             // (M, N): element (j, n) at out + j*o_sm + n*o_sn
+  int64_t o_sm, o_sn;
+  int M, N, K;
+  int slices, ks;          // K slices of ks rows (a multiple of DKN_R)
+  int64_t nblk;            // ceil(N / DKN_COLS)
+  const f16* scales;       // bmax, one per group of gs consecutive (k*N + n)
+  int64_t n_groups;
+  int log2gs;
+  DualLuts luts;
+  float* part;             // partial sums [slice][2][M][N] (slices > 1 or plug), else null
+};
+
+// Tables from the caller's LUTs (fp16 or float32): every LUT load of a thread is issued
+// before its stores, the (cos, sin) rows written as 16-byte units in address order.
+template <int LAYOUT, typename E>
+__device__ __forceinline__ void dkn_tables_of(char* lds, const DualLuts& L) {
+  constexpr int KU = (8192 + DKN_NT - 1) / DKN_NT;
+  const E* cp = reinterpret_cast<const E*>(L.cs[0]);
+  const E* sp = reinterpret_cast<const E*>(L.cs[1]);
+  float c[KU], s[KU];
+#pragma unroll
+  for (int k = 0; k < KU; ++k) {
+    const int p = (threadIdx.x + k * DKN_NT) >> 3;
+    c[k] = p < L.phase_n ? (float)cp[p] : 0.f;
+    s[k] = p < L.phase_n ? (float)sp[p] : 0.f;
+  }
+  float amp = 0.f;
+  if (threadIdx.x < 64) {
+    // the int16 layout stores code ^ 0x8000: entry a holds amplitude a ^ 32
+    const int e = LAYOUT == PP_DUAL_I16_OFFSET ? (threadIdx.x ^ 32) : threadIdx.x;
+    amp = e < L.amp_n ? (float)reinterpret_cast<const E*>(L.amp)[e] : 0.f;
+    *reinterpret_cast<float*>(lds + DLDS_AMP + 4 * threadIdx.x) = amp;
+  }
+#pragma unroll
+  for (int k = 0; k < KU; ++k)
+    *reinterpret_cast<float4*>(lds + DLDS_CS + 16 * (threadIdx.x + k * DKN_NT)) = make_float4(c[k], s[k], c[k], s[k]);
+}
+
+template <int MT>
+struct DknStep {
+  u32x4 q[DKN_R];        // 8 codes (columns) per row
+  uint32_t sc[DKN_R];    // their group scale (fp16 bits)
+  u32x4 x[MT];           // 8 fp16 activations (the step's rows) per token
+};
+
+template <int MT>
+__device__ __forceinline__ void dkn_issue(const DualKnArgs& A, int k, int kend, int n, uint32_t voff,
+                                          DknStep<MT>& S) {
+  // rows [k, kend) of the slice: the resource ends at row kend, so rows past it read 0
+  const int rows = max(0, kend - k);
+  const rsrc_t rc = make_rsrc(A.codes + (int64_t)min(k, kend) * A.ldk, 2u * (uint32_t)((int64_t)rows * A.ldk));
+#pragma unroll
+  for (int r = 0; r < DKN_R; ++r) vload128(S.q[r], voff + 2u * (uint32_t)(r * A.ldk), rc);
+  const rsrc_t rs = make_rsrc(A.scales, 2u * (uint32_t)A.n_groups);
+#pragma unroll
+  for (int r = 0; r < DKN_R; ++r) {
+    // group of (k + r, n .. n+7); K*N < 2^32 on this path
+    const uint32_t p = (uint32_t)(k + r) * (uint32_t)A.N + (uint32_t)n;
+    vload16(S.sc[r], r < rows && n < A.N ? 2u * (p >> A.log2gs) : OOB, rs);
+  }
+#pragma unroll
+  for (int j = 0; j < MT; ++j) {
+    // 8 activations of the step's rows: past kend they read 0 (with the codes, they add 0)
+    const rsrc_t rx = make_rsrc(A.a + (int64_t)j * A.a_sm + min(k, kend), 2u * (uint32_t)rows);
+    vload128c(S.x[j], j < A.M ? 0u : OOB, rx);
+  }
+}
+
+template <int MT, int LAYOUT>
+__device__ __forceinline__ void dkn_compute(const char* lds, const DualLane& lo, const DknStep<MT>& S,
+                                            float (&acc)[8][2][MT]) {
+  float xv[MT][DKN_R];
+#pragma unroll
+  for (int j = 0; j < MT; ++j) {
+    const f16x4 h0 = __builtin_bit_cast(f16x4, u32x2{S.x[j].x, S.x[j].y});
+    const f16x4 h1 = __builtin_bit_cast(f16x4, u32x2{S.x[j].z, S.x[j].w});
+    xv[j][0] = (float)h0.x; xv[j][1] = (float)h0.y; xv[j][2] = (float)h0.z; xv[j][3] = (float)h0.w;
+    xv[j][4] = (float)h1.x; xv[j][5] = (float)h1.y; xv[j][6] = (float)h1.z; xv[j][7] = (float)h1.w;
+  }
+#pragma unroll
+  for (int r = 0; r < DKN_R; ++r) {
+    const float sc = h2f(S.sc[r]);
+    float xs[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) xs[j] = xv[j][r] * sc;
+    const uint32_t w4[4] = {S.q[r].x, S.q[r].y, S.q[r].z, S.q[r].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float an[2];
+      float2 cs[2];
+      dual_lookup2<LAYOUT>(lds, w4[e], lo, an, cs);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          const float t = an[h] * xs[j];
+          acc[2 * e + h][0][j] = fmaf(t, cs[h].x, acc[2 * e + h][0][j]);
+          acc[2 * e + h][1][j] = fmaf(t, cs[h].y, acc[2 * e + h][1][j]);
+        }
+    }
+  }
+}
+
+template <int MT, int LAYOUT>
+__device__ __forceinline__ void dkn_body(const char* lds, const DualKnArgs& A) {
+  constexpr int WAVES = DKN_NT / 64;
+  const int lane = threadIdx.x & 63;
+  const DualLane lo = dual_lane(lane);
+  // items dealt round-robin over the workgroups, so a launch with fewer items than
+  // wavefronts still spreads them over every CU
+  const int64_t gw = (int64_t)uniform(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
+  const int64_t nw = (int64_t)gridDim.x * WAVES;
+  const int64_t items = A.nblk * A.slices;
+  for (int64_t it = gw; it < items; it += nw) {
+    const int blk = (int)uniform64(it / A.slices), sl = (int)uniform64(it % A.slices);
+    const int n = blk * DKN_COLS + 8 * lane;           // the lane's first column
+    const int k0 = sl * A.ks, k1 = min(A.K, k0 + A.ks);
+    const uint32_t voff = n < A.N ? 2u * (uint32_t)n : OOB;
+    float acc[8][2][MT];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) acc[c][0][j] = acc[c][1][j] = 0.f;
+    DknStep<MT> s0, s1;
+    dkn_issue<MT>(A, k0, k1, n, voff, s0);
+    for (int k = k0; k < k1; k += 2 * DKN_R) {
+      dkn_issue<MT>(A, k + DKN_R, k1, n, voff, s1);
+      dkn_compute<MT, LAYOUT>(lds, lo, s0, acc);
+      if (k + DKN_R >= k1) break;
+      dkn_issue<MT>(A, k + 2 * DKN_R, k1, n, voff, s0);
+      dkn_compute<MT, LAYOUT>(lds, lo, s1, acc);
+    }
+    if (A.part == nullptr) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const rsrc_t ro = make_rsrc(A.out[m], 2u * (uint32_t)((int64_t)(A.M - 1) * A.o_sm + (int64_t)(A.N - 1) * A.o_sn + 1));
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const f16 h = (f16)acc[c][m][j];
+            const bool ok = n + c < A.N && j < A.M;
+            vstore16((uint32_t)__builtin_bit_cast(unsigned short, h),
+                     ok ? 2u * (uint32_t)((int64_t)j * A.o_sm + (int64_t)(n + c) * A.o_sn) : OOB, ro);
+          }
+      }
+    } else {
+      // partials [sl][m][j][n .. n+7] as two 16-byte stores (N % 8 == 0 on this path)
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+          if (n < A.N && j < A.M) {
+            float4* p = reinterpret_cast<float4*>(A.part + (((int64_t)sl * 2 + m) * A.M + j) * A.N + n);
+            p[0] = make_float4(acc[0][m][j], acc[1][m][j], acc[2][m][j], acc[3][m][j]);
+            p[1] = make_float4(acc[4][m][j], acc[5][m][j], acc[6][m][j], acc[7][m][j]);
+          }
+    }
+  }
+}
+
+template <int MT, int LAYOUT>
+__global__ __launch_bounds__(DKN_NT) void dual_kn_kernel(const DualKnArgs A) {
+  __shared__ __attribute__((aligned(16))) char T[DLDS_BYTES];
+  if (A.luts.dtype == PP_F16) dkn_tables_of<LAYOUT, f16>(T, A.luts);
+  else dkn_tables_of<LAYOUT, float>(T, A.luts);
+  __syncthreads();
+  dkn_body<MT, LAYOUT>(T, A);
+}
+
+// Plug corrections, one entry per thread, added to slice 0's partial sums after the
+// tile kernel: x * (plug amp - amp_lut[amp_q] * bmax) * (cos, sin)(phase) for every token
+// (the plug amplitude replaces the decoded one, polar_bitpack.py:240-243).  Positions are
+// relative to elem_base in the (K,N) storage, row stride ldk.
+struct DualKnPlugArgs {
+  DualKnArgs T;
+  int layout;
+  const uint32_t* plug_idx;
+  const f16* plug_amp;
+  int64_t plug_n, elem_base;
+};
+
+__global__ __launch_bounds__(256) void dual_kn_plug_kernel(const DualKnPlugArgs P) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= P.plug_n) return;
+  const DualKnArgs& A = P.T;
+  const int64_t pos = (int64_t)P.plug_idx[e] - P.elem_base;
+  if (pos < 0) return;
+  const int64_t k = pos / A.ldk, n = pos % A.ldk;
+  if (k >= A.K || n >= A.N) return;
+  const uint32_t raw = A.codes[pos];
+  const uint32_t code = P.layout == PP_DUAL_U16_BE ? (((raw & 0xFFu) << 8) | (raw >> 8)) : (raw ^ 0x8000u);
+  const int aq = (int)((code >> 10) & 63u), ph = (int)(code & 1023u);
+  const DualLuts& L = A.luts;
+  const float an = aq < L.amp_n ? lut_at(L.amp, L.dtype, aq) : 0.f;
+  const float c = ph < L.phase_n ? lut_at(L.cs[0], L.dtype, ph) : 0.f;
+  const float s = ph < L.phase_n ? lut_at(L.cs[1], L.dtype, ph) : 0.f;
+  const float sc = (float)A.scales[(k * A.N + n) >> A.log2gs];
+  const float d = (float)P.plug_amp[e] - an * sc;
+  for (int j = 0; j < A.M; ++j) {
+    const float xd = (float)A.a[(int64_t)j * A.a_sm + k] * d;
+    atomicAdd(A.part + (int64_t)j * A.N + n, xd * c);
+    atomicAdd(A.part + ((int64_t)A.M + j) * A.N + n, xd * s);
+  }
+}
+
+// out_m[j, n] = fp16(sum over slices of part[sl][m][j][n]), 4 consecutive columns per
+// thread (N % 8 == 0 on this path).
+__global__ __launch_bounds__(256) void dual_kn_finish_kernel(const DualKnArgs A) {
+  const int64_t total = 2ll * A.M * A.N;
+  const int64_t i0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+  if (i0 >= total) return;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+  for (int sl = 0; sl < A.slices; ++sl) {
+    const float4 t = *reinterpret_cast<const float4*>(A.part + (int64_t)sl * total + i0);
+    v.x += t.x;
+    v.y += t.y;
+    v.z += t.z;
+    v.w += t.w;
+  }
+  const int64_t mj = i0 / A.N;
+  const int n = (int)(i0 % A.N), j = (int)(mj % A.M), m = (int)(mj / A.M);
+  f16* o = m == 0 ? A.out[0] : A.out[1];
+  const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) o[(int64_t)j * A.o_sm + (int64_t)(n + c) * A.o_sn] = (f16)vv[c];
+}
+
+// ------------------------------------------------------------------ host side
+#ifndef PP_DKN_MIN_ROWS
+#define PP_DKN_MIN_ROWS 64
+#endif
+
+struct DknPlan {
+  int slices, ks;
+  int64_t nblk;
+};
+
+static DknPlan dkn_plan(int64_t N, int64_t K) {
+  DknPlan p;
+  p.nblk = (N + DKN_COLS - 1) / DKN_COLS;
+  const int64_t waves = (int64_t)device_cu_count() * (DKN_NT / 64);
+  // about one item per wavefront, slices of at least PP_DKN_MIN_ROWS rows
+  int64_t s = std::max<int64_t>(
+      1, std::min<int64_t>(waves / std::max<int64_t>(p.nblk, 1), (K + PP_DKN_MIN_ROWS - 1) / PP_DKN_MIN_ROWS));
+  int64_t ks = (K + s - 1) / s;
+  ks = (ks + DKN_R - 1) / DKN_R * DKN_R;
+  p.ks = (int)std::max<int64_t>(ks, DKN_R);
+  p.slices = (int)((K + p.ks - 1) / p.ks);
+  return p;
+}
+
+bool dual_kn_ok(const void* a, int64_t a_sm, int64_t a_sk, const void* codes, int64_t c_sk, int64_t c_sn,
+                int64_t group_size, int64_t chunk_size, int64_t M, int64_t N, int64_t K) {
+  return c_sn == 1 && c_sk >= N && c_sk % 8 == 0 && N % 8 == 0 && N > 0 && K > 0 && K % 8 == 0 && M >= 1 &&
+         M <= 4 && aligned(codes, 16) && chunk_size == 0 && group_size >= 8 && (group_size & (group_size - 1)) == 0 &&
+         a_sk == 1 && (M == 1 || a_sm % 8 == 0) && aligned(a, 16) && K * N < (1ll << 32) &&
+         2 * c_sk * K < (1ll << 31);
+}
+
+int64_t dual_kn_workspace(int64_t M, int64_t N, int64_t K, int64_t plug_n) {
+  const DknPlan p = dkn_plan(N, K);
+  if (p.slices == 1 && plug_n == 0) return 0;
+  return (int64_t)p.slices * 2 * M * N * (int64_t)sizeof(float);
+}
+
+int dual_kn_gemm(const void* a, int64_t a_sm, const void* codes, int code_layout, int64_t ldk, const void* bmax,
+                 int64_t group_size, const DualLuts& luts, const uint32_t* plug_idx, const void* plug_amp,
+                 int64_t plug_n, int64_t elem_base, void* const* out, int64_t o_sm, int64_t o_sn, int64_t M,
+                 int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, hipStream_t st) {
+  const DknPlan p = dkn_plan(N, K);
+  const int64_t need = dual_kn_workspace(M, N, K, plug_n);
+  PP_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), "workspace too small: need %lld bytes",
+             (long long)need);
+  DualKnArgs A = {};
+  A.codes = reinterpret_cast<const uint16_t*>(codes);
+  A.ldk = ldk;
+  A.a = reinterpret_cast<const f16*>(a);
+  A.a_sm = a_sm;
+  A.out[0] = reinterpret_cast<f16*>(out[0]);
+  A.out[1] = reinterpret_cast<f16*>(out[1]);
+  A.o_sm = o_sm;
+  A.o_sn = o_sn;
+  A.M = (int)M;
+  A.N = (int)N;
+  A.K = (int)K;
+  A.slices = p.slices;
+  A.ks = p.ks;
+  A.nblk = p.nblk;
+  A.scales = reinterpret_cast<const f16*>(bmax);
+  A.n_groups = (K * N + group_size - 1) / group_size;
+  A.log2gs = 0;
+  while ((1ll << A.log2gs) < group_size) ++A.log2gs;
+  A.luts = luts;
+  A.part = need > 0 ? reinterpret_cast<float*>(workspace) : nullptr;
+  const int64_t items = p.nblk * p.slices;
+  const unsigned grid = (unsigned)std::min<int64_t>(device_cu_count(), (items + DKN_NT / 64 - 1) / (DKN_NT / 64));
+  const bool be = code_layout == PP_DUAL_U16_BE;
+  switch ((M <= 1 ? 1 : M <= 2 ? 2 : 4) * 2 + (be ? 1 : 0)) {
+    case 2: hipLaunchKernelGGL((dual_kn_kernel<1, PP_DUAL_I16_OFFSET>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    case 3: hipLaunchKernelGGL((dual_kn_kernel<1, PP_DUAL_U16_BE>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    case 4: hipLaunchKernelGGL((dual_kn_kernel<2, PP_DUAL_I16_OFFSET>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    case 5: hipLaunchKernelGGL((dual_kn_kernel<2, PP_DUAL_U16_BE>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    case 8: hipLaunchKernelGGL((dual_kn_kernel<4, PP_DUAL_I16_OFFSET>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    default: hipLaunchKernelGGL((dual_kn_kernel<4, PP_DUAL_U16_BE>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+  }
+  PP_LAUNCH_CHECK();
+  if (A.part != nullptr) {
+    if (plug_n > 0) {
+      DualKnPlugArgs P;
+      P.T = A;
+      P.layout = code_layout;
+      P.plug_idx = plug_idx;
+      P.plug_amp = reinterpret_cast<const f16*>(plug_amp);
+      P.plug_n = plug_n;
+      P.elem_base = elem_base;
+      hipLaunchKernelGGL(dual_kn_plug_kernel, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0, st, P);
+      PP_LAUNCH_CHECK();
+    }
+    const int64_t total = 2 * M * N;
+    hipLaunchKernelGGL(dual_kn_finish_kernel, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0, st, A);
+    PP_LAUNCH_CHECK();
+  }
+  return PP_OK;
+}
+
+}  // namespace pp

@@ -16,18 +16,14 @@
 // share one group scale, so the scale multiplies a per-lane partial sum once per 8 pairs)
 // and one 2-byte scale load.
 //
-// LDS tables (136 KiB): (cos, sin) of the 1024 phases in 128-byte rows of 16 replicas,
-// the 64 amplitudes in 128-byte rows of 32 replicas.  For the int16 layout the amplitude
-// rows are stored at index amp_q ^ 32, so the stored bits index them directly.
-#include "pp_common.h"
+// LDS tables (129 KiB, dual_lds.h): (cos, sin) of the 1024 phases in 128-byte rows of 16
+// replicas, the 64 amplitudes one per bank.
+#include "dual_lds.h"
 #include "rows_common.h"
 
 namespace pp {
 
 constexpr int DPAIRS = 512;                    // pairs per wave per row per chunk (64 lanes x 8)
-constexpr uint32_t DLDS_AMP = 0;               // the 64 amplitudes, 4 bytes each: one per LDS bank
-constexpr uint32_t DLDS_CS = 0x400;            // (cos, sin) rows: phase p at DLDS_CS + p*128 + 8*(lane % 16)
-constexpr uint32_t DLDS_BYTES = 0x400 + 1024 * 128;
 
 template <int MT> struct DualCfg;
 #ifndef PP_DUAL1_RG
@@ -61,53 +57,6 @@ struct DualStreamArgs {
   int M;
   void* ws;                   // split launches: per-task counters, then float32 accumulators
 };
-
-// Stored 32-bit word (two pairs) -> two codes in the table-index form: the file layout is
-// byte-swapped per half, the int16 layout is used as stored.
-template <int LAYOUT>
-__device__ __forceinline__ uint32_t dual_word(uint32_t w) {
-  if constexpr (LAYOUT == PP_DUAL_U16_BE) return __builtin_amdgcn_perm(w, w, 0x02030001u);
-  else return w;
-}
-template <int LAYOUT>
-__device__ __forceinline__ uint32_t dual_half(uint32_t h16) {
-  if constexpr (LAYOUT == PP_DUAL_U16_BE) return ((h16 & 0xFFu) << 8) | ((h16 >> 8) & 0xFFu);
-  else return h16 & 0xFFFFu;
-}
-
-struct DualLane {
-  uint32_t cs;        // the lane's replica inside a (cos, sin) row
-};
-
-__device__ __forceinline__ DualLane dual_lane(int l) {
-  DualLane o;
-  o.cs = 8u * (l & 15);
-  return o;
-}
-
-// Amplitude and (cos, sin) of both codes of a stored 32-bit word.  The amplitude table
-// needs no replicas (a wave's 64 reads hit distinct banks or share one address), so its
-// byte offset, 4 * amp bits, comes straight out of the stored word: byte 0 / byte 2 of
-// a big-endian word, byte 1 / byte 3 of the int16 layout, masked with 0xFC.
-template <int LAYOUT>
-__device__ __forceinline__ void dual_lookup2(const char* lds, uint32_t raw, const DualLane& o, float (&an)[2],
-                                             float2 (&cs)[2]) {
-  const uint32_t a0 = (LAYOUT == PP_DUAL_U16_BE ? raw : raw >> 8) & 0xFCu;
-  const uint32_t a1 = (raw >> (LAYOUT == PP_DUAL_U16_BE ? 16 : 24)) & 0xFCu;
-  const uint32_t w = dual_word<LAYOUT>(raw);
-  const uint32_t c0 = ((w << 7) & 0x1FF80u) | o.cs;
-  const uint32_t c1 = ((w >> 9) & 0x1FF80u) | o.cs;
-  an[0] = *reinterpret_cast<const float*>(lds + DLDS_AMP + a0);
-  an[1] = *reinterpret_cast<const float*>(lds + DLDS_AMP + a1);
-  cs[0] = *reinterpret_cast<const float2*>(lds + DLDS_CS + c0);
-  cs[1] = *reinterpret_cast<const float2*>(lds + DLDS_CS + c1);
-}
-
-// The same for one code in the table-index form (amp bits 10..15, phase 0..9).
-__device__ __forceinline__ void dual_lookup1(const char* lds, uint32_t c, const DualLane& o, float& an, float2& cs) {
-  an = *reinterpret_cast<const float*>(lds + DLDS_AMP + ((c >> 8) & 0xFCu));
-  cs = *reinterpret_cast<const float2*>(lds + DLDS_CS + (((c << 7) & 0x1FF80u) | o.cs));
-}
 
 // (cos, sin) rows as 16-byte units (two replicas) in address order, so that a wavefront's
 // stores fill consecutive banks; every LUT load of a thread is issued before its stores.

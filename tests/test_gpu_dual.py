@@ -111,3 +111,55 @@ def test_quantize_polar_bitpacked_on_gpu_matches_oracle(dtype, max_frac, max_ste
     assert db.max() <= 1                                 # group max of device sqrt: within one fp16 ulp
     for i in (2, 3, 4):
         np.testing.assert_array_equal(got[i].cpu().numpy().view(np.uint16), ref[i].view(np.uint16))
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6])
+@pytest.mark.parametrize("K,N,plug", [(2048, 1000 - 1000 % 8, 0), (2048, 1000 - 1000 % 8, 700), (64, 96, 0),
+                                      (520, 4096, 300), (4096, 4096, 0)])
+def test_polar_dual_bitpacked_kn_fast_path(K, N, plug, M):
+    """Contiguous (K,N) codes, the layout quantize_polar_bitpacked returns: the fused (K,N)
+    kernel (512-column items, K slices whose partial sums a finish pass adds, plug entries
+    replacing the amplitude; blocks of 4 tokens), against the float64 oracle."""
+    seed = K + N + plug + M
+    packed, bmax, amp_lut, cos_lut, sin_lut = kernel_layout_layer(K, N, seed)
+    rng = np.random.default_rng(seed)
+    base = 1000
+    flat = np.sort(rng.choice(K * N, plug, replace=False)).astype(np.uint32)
+    vals = np.abs(rng.standard_normal(plug) * 0.05).astype(np.float16)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    kw = {}
+    if plug:
+        kw = dict(plug=(u32(flat + base).to(DEV), torch.from_numpy(vals).to(DEV)), elem_base=base)
+    o1, o2 = pk.polar_dual_bitpacked(*to_dev(a, packed, bmax, amp_lut, cos_lut, sin_lut), **kw)
+    W = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut)
+    ph = (packed.astype(np.int32) + 32768) & 1023
+    kk, nn = flat // N, flat % N
+    for w, lut in ((W[0], cos_lut), (W[1], sin_lut)):
+        w[kk, nn] = vals.astype(np.float64) * np.asarray(lut, np.float64)[ph[kk, nn]]
+    for o, w in ((o1, W[0]), (o2, W[1])):
+        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w))
+
+
+def test_polar_dual_bitpacked_kn_output_view():
+    """Outputs written through a strided (transposed) view on the direct-store path."""
+    K, N, M = 512, 1024, 2
+    packed, bmax, amp_lut, cos_lut, sin_lut = kernel_layout_layer(K, N, 77)
+    a = np.random.default_rng(1).standard_normal((M, K)).astype(np.float16)
+    W = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut)
+    from polar_pack_amd import _native as nat
+    dev = to_dev(a, packed, bmax, amp_lut, cos_lut, sin_lut)
+    o = torch.full((2, N, M), float("nan"), dtype=torch.float16, device=DEV)
+    o1, o2 = o[0].t(), o[1].t()                   # (M, N) views with o_sm = 1, o_sn = M
+    L = nat.lib()
+    x, p, b, al, cl, sl = dev
+    ws_bytes = L.pp_dual_gemm_workspace_size(x.data_ptr(), K, 1, p.data_ptr(), N, 1, 32, 0, 0, 0, M, N, K)
+    ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    lut_dt = 0 if al.dtype == torch.float16 else 1
+    rc = L.pp_dual_gemm(x.data_ptr(), K, 1, p.data_ptr(), 0, N, 1, b.data_ptr(), 32, 0, al.data_ptr(), al.numel(),
+                        cl.data_ptr(), sl.data_ptr(), 1024, lut_dt, None, None, 0, 0, o1.data_ptr(), o2.data_ptr(),
+                        o1.stride(0), o1.stride(1), M, N, K, ws.data_ptr(), ws_bytes,
+                        torch.cuda.current_stream().cuda_stream)
+    nat.check(rc, "pp_dual_gemm")
+    torch.cuda.synchronize()
+    for out, w in ((o1, W[0]), (o2, W[1])):
+        assert_gemv_close(out.float().cpu().numpy(), olay.gemm_f64(a, w))
