@@ -105,6 +105,17 @@ int pp_quad_dequant(const uint32_t* codes, int64_t c_sk, int64_t c_sn,
                     float* const* out, int64_t N, int64_t K, void* stream);
 
 /*
+ * The same into fp16: out_m[k*N + n] = fp16(s_m * W_m[k, n]), the rounded weights the
+ * reference kernel feeds its dot products (quad_kernels.py:117-126, with s_m folded in).
+ * For batches large enough that the matmul is compute-bound (the reference's prefill
+ * sizes, quad_kernels.py:175-189): decode once, then a library fp16 GEMM.
+ */
+int pp_quad_dequant_f16(const uint32_t* codes, int64_t c_sk, int64_t c_sn,
+                        const void* const* luts, int lut_dtype, const float* scales,
+                        const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n, int64_t elem_base,
+                        void* const* out, int64_t N, int64_t K, void* stream);
+
+/*
  * Whole-stream decode for 1..8 tokens: one launch over many projections of one
  * .quadpack stream (the grouped whole-step launch).  All tables are device memory
  * prepared by the host once per stream (see polar_pack_amd/stream.py):
@@ -276,6 +287,16 @@ int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk, int64_t c_
                     int phase_n, int lut_dtype,
                     const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n, int64_t elem_base,
                     float* out1, float* out2, int64_t N, int64_t K, void* stream);
+
+/* The same into fp16 (w1, w2): the rounded weights polar_dual_bitpacked_kernel feeds its
+ * dot products (polar_kernels.py:78-82), for a library GEMM at prefill batch sizes
+ * (polar_kernels.py:165-184). */
+int pp_dual_dequant_f16(const void* codes, int code_layout, int64_t c_sk, int64_t c_sn,
+                        const void* bmax, int64_t group_size, int64_t chunk_size,
+                        const void* amp_lut, int amp_lut_n, const void* cos_lut, const void* sin_lut,
+                        int phase_n, int lut_dtype,
+                        const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n, int64_t elem_base,
+                        void* out1, void* out2, int64_t N, int64_t K, void* stream);
 
 /*
  * Whole-stream dual decode for 1..4 tokens: every projection of a .dualpack stream in

@@ -55,6 +55,7 @@ EXPORTS = {
                            i64, i64, i64, vp, i64, vp]),
     "pp_quad_gemm_workspace_size": (i64, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64]),
     "pp_quad_dequant": (i32, [vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
+    "pp_quad_dequant_f16": (i32, [vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
     "pp_quad_mfma": (i32, [vp, i64, i64, vp, i64, vp, i32, vp, vp, vp, i64, vp, i64, i64, vp, i64, i64, i64, i64,
                            vp, i64, vp]),
     "pp_quad_mfma_workspace_size": (i64, [i64, i64, i64]),
@@ -75,6 +76,8 @@ EXPORTS = {
     "pp_dual_gemm_workspace_size": (i64, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64]),
     "pp_dual_dequant": (i32, [vp, i32, i64, i64, vp, i64, i64, vp, i32, vp, vp, i32, i32, vp, vp, i64, i64,
                               vp, vp, i64, i64, vp]),
+    "pp_dual_dequant_f16": (i32, [vp, i32, i64, i64, vp, i64, i64, vp, i32, vp, vp, i32, i32, vp, vp, i64, i64,
+                                  vp, vp, i64, i64, vp]),
 }
 
 _lock = threading.Lock()

@@ -273,26 +273,50 @@ struct DualDequantArgs {
   const f16* scales;
   DualGroup grp;
   DualLuts luts;
-  float* out[2];
+  void* out[2];   // O[K*N] each
   int64_t N, K;
 };
 
+// Small decode tables for the element-wise kernel: a wave's random reads conflict in a
+// few banks, which costs less than the three global gathers per element they replace.
+struct DualDqLds {
+  float amp[64];
+  float2 cs[1024];
+};
+
+template <typename O>
+__device__ __forceinline__ void dual_dequant_at(const DualDqLds& T, const DualDequantArgs& A, int64_t e, int64_t k,
+                                                int64_t n, int64_t g) {
+  const int64_t off = k * A.c_sk + n * A.c_sn;
+  const uint32_t raw = reinterpret_cast<const uint16_t*>(A.codes)[off];
+  const uint32_t code = A.layout == PP_DUAL_U16_BE ? (((raw & 0xFFu) << 8) | (raw >> 8)) : (raw ^ 0x8000u);
+  if (g < 0) g = A.grp.of_pos(A.elem_base + off);
+  const float amp = T.amp[(code >> 10) & 63u] * (float)A.scales[g];
+  const float2 cs = T.cs[code & 1023u];
+  reinterpret_cast<O*>(A.out[0])[e] = (O)(amp * cs.x);
+  reinterpret_cast<O*>(A.out[1])[e] = (O)(amp * cs.y);
+}
+
+template <typename O>
 __global__ __launch_bounds__(256) void dual_dequant_kernel(const DualDequantArgs A) {
-  const uint16_t* c16 = reinterpret_cast<const uint16_t*>(A.codes);
+  __shared__ DualDqLds T;
+  const DualLuts& L = A.luts;
+  for (int i = threadIdx.x; i < 1024; i += blockDim.x) {
+    T.cs[i] = i < L.phase_n ? make_float2(lut_at(L.cs[0], L.dtype, i), lut_at(L.cs[1], L.dtype, i))
+                            : make_float2(0.f, 0.f);
+    if (i < 64) T.amp[i] = i < L.amp_n ? lut_at(L.amp, L.dtype, i) : 0.f;
+  }
+  __syncthreads();
   const int64_t total = A.N * A.K;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t k = e / A.N, n = e - k * A.N;
-    const int64_t off = k * A.c_sk + n * A.c_sn;
-    const uint32_t raw = c16[off];
-    const uint32_t code = A.layout == PP_DUAL_U16_BE ? (((raw & 0xFFu) << 8) | (raw >> 8)) : (raw ^ 0x8000u);
-    const int aq = (int)((code >> 10) & 63u), ph = (int)(code & 1023u);
-    const int64_t g = A.grp.chunk == 0 ? (k * A.N + n) / A.grp.gs : A.grp.of_pos(A.elem_base + off);
-    const float an = aq < A.luts.amp_n ? lut_at(A.luts.amp, A.luts.dtype, aq) : 0.f;
-    const float amp = an * (float)A.scales[g];
-    const float c = ph < A.luts.phase_n ? lut_at(A.luts.cs[0], A.luts.dtype, ph) : 0.f;
-    const float s = ph < A.luts.phase_n ? lut_at(A.luts.cs[1], A.luts.dtype, ph) : 0.f;
-    A.out[0][e] = amp * c;
-    A.out[1][e] = amp * s;
+  if (total < (1ll << 32) && A.grp.chunk == 0 && (A.grp.gs & (A.grp.gs - 1)) == 0) {
+    // 32-bit index arithmetic (a 64-bit division per element costs more than the decode)
+    const uint32_t N = (uint32_t)A.N, tot = (uint32_t)total;
+    for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < tot; e += gridDim.x * blockDim.x)
+      dual_dequant_at<O>(T, A, e, e / N, e % N, e >> A.grp.log2gs);
+  } else {
+    // e = k*N + n: the kernel rule's group is e / gs; g < 0 asks for the chunked rule
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x)
+      dual_dequant_at<O>(T, A, e, e / A.N, e % A.N, A.grp.chunk == 0 ? e / A.grp.gs : -1);
   }
 }
 
@@ -304,10 +328,11 @@ struct DualPlugScatterArgs {
   const f16* plug_amp;
   int64_t plug_n;
   DualLuts luts;
-  float* out[2];
+  void* out[2];
   int64_t N, K;
 };
 
+template <typename O>
 __global__ void dual_plug_scatter_kernel(const DualPlugScatterArgs A) {
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= A.plug_n) return;
@@ -328,8 +353,8 @@ __global__ void dual_plug_scatter_kernel(const DualPlugScatterArgs A) {
   const float amp = (float)A.plug_amp[j];
   const float c = ph < A.luts.phase_n ? lut_at(A.luts.cs[0], A.luts.dtype, ph) : 0.f;
   const float s = ph < A.luts.phase_n ? lut_at(A.luts.cs[1], A.luts.dtype, ph) : 0.f;
-  A.out[0][k * A.N + n] = amp * c;
-  A.out[1][k * A.N + n] = amp * s;
+  reinterpret_cast<O*>(A.out[0])[k * A.N + n] = (O)(amp * c);
+  reinterpret_cast<O*>(A.out[1])[k * A.N + n] = (O)(amp * s);
 }
 
 struct DualWsGemmArgs {
@@ -475,11 +500,12 @@ extern "C" int64_t pp_dual_gemm_workspace_size(const void* a, int64_t a_sm, int6
   return 2 * N * K * (int64_t)sizeof(float);
 }
 
-extern "C" int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk, int64_t c_sn, const void* bmax,
+template <typename O>
+static int dual_dequant_to(const void* codes, int code_layout, int64_t c_sk, int64_t c_sn, const void* bmax,
                                int64_t group_size, int64_t chunk_size, const void* amp_lut, int amp_lut_n,
                                const void* cos_lut, const void* sin_lut, int phase_n, int lut_dtype,
                                const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n, int64_t elem_base,
-                               float* out1, float* out2, int64_t N, int64_t K, void* stream) {
+                               void* out1, void* out2, int64_t N, int64_t K, void* stream) {
   if (int rc = dual_common_checks(codes, code_layout, group_size, chunk_size, amp_lut, amp_lut_n, cos_lut, sin_lut,
                                   phase_n, lut_dtype, plug_n, plug_idx, plug_amp, c_sk, c_sn, N, K))
     return rc;
@@ -497,13 +523,14 @@ extern "C" int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk,
   A.grp.chunk = chunk_size;
   A.grp.per_chunk = chunk_size > 0 ? (chunk_size + group_size - 1) / group_size : 0;
   A.grp.log2gs = 0;
+  while ((1ll << A.grp.log2gs) < group_size) ++A.grp.log2gs;
   A.luts = make_dual_luts(amp_lut, amp_lut_n, cos_lut, sin_lut, phase_n, lut_dtype);
   A.out[0] = out1;
   A.out[1] = out2;
   A.N = N;
   A.K = K;
   const int64_t blocks = std::min<int64_t>((N * K + 255) / 256, (int64_t)device_cu_count() * 16);
-  hipLaunchKernelGGL(dual_dequant_kernel, dim3((unsigned)blocks), dim3(256), 0, st, A);
+  hipLaunchKernelGGL(dual_dequant_kernel<O>, dim3((unsigned)blocks), dim3(256), 0, st, A);
   PP_LAUNCH_CHECK();
   if (plug_n > 0) {
     DualPlugScatterArgs P;
@@ -520,10 +547,30 @@ extern "C" int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk,
     P.out[1] = out2;
     P.N = N;
     P.K = K;
-    hipLaunchKernelGGL(dual_plug_scatter_kernel, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0, st, P);
+    hipLaunchKernelGGL(dual_plug_scatter_kernel<O>, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0, st, P);
     PP_LAUNCH_CHECK();
   }
   return PP_OK;
+}
+
+extern "C" int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk, int64_t c_sn, const void* bmax,
+                               int64_t group_size, int64_t chunk_size, const void* amp_lut, int amp_lut_n,
+                               const void* cos_lut, const void* sin_lut, int phase_n, int lut_dtype,
+                               const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n, int64_t elem_base,
+                               float* out1, float* out2, int64_t N, int64_t K, void* stream) {
+  return dual_dequant_to<float>(codes, code_layout, c_sk, c_sn, bmax, group_size, chunk_size, amp_lut, amp_lut_n,
+                                cos_lut, sin_lut, phase_n, lut_dtype, plug_idx, plug_amp, plug_n, elem_base, out1,
+                                out2, N, K, stream);
+}
+
+extern "C" int pp_dual_dequant_f16(const void* codes, int code_layout, int64_t c_sk, int64_t c_sn,
+                                   const void* bmax, int64_t group_size, int64_t chunk_size, const void* amp_lut,
+                                   int amp_lut_n, const void* cos_lut, const void* sin_lut, int phase_n,
+                                   int lut_dtype, const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n,
+                                   int64_t elem_base, void* out1, void* out2, int64_t N, int64_t K, void* stream) {
+  return dual_dequant_to<f16>(codes, code_layout, c_sk, c_sn, bmax, group_size, chunk_size, amp_lut, amp_lut_n,
+                              cos_lut, sin_lut, phase_n, lut_dtype, plug_idx, plug_amp, plug_n, elem_base, out1,
+                              out2, N, K, stream);
 }
 
 extern "C" int pp_dual_gemm(const void* a, int64_t a_sm, int64_t a_sk, const void* codes, int code_layout,

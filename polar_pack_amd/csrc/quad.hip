@@ -22,27 +22,40 @@
 
 namespace pp {
 
-// Generic path: float32 weights out_m[k*N + n] = s_m * W_m[k, n], then a GEMM.
+// Generic path: weights out_m[k*N + n] = s_m * W_m[k, n] (float32 for the workspace GEMM,
+// fp16 for a caller's library GEMM), then a GEMM.
 struct QuadDequantArgs {
   const uint32_t* codes;
   int64_t c_sk, c_sn;
   QuadLuts luts;
   float s[4];
-  float* out[4];
+  void* out[4];   // O[K*N] each
   int64_t N, K;
 };
 
+template <typename O>
+__device__ __forceinline__ void quad_dequant_at(const QuadLds<1, 1>& T, const QuadDequantArgs& A, int64_t e,
+                                                int64_t k, int64_t n) {
+  float w[4];
+  quad_decode(T, A.codes[k * A.c_sk + n * A.c_sn], 0, 0, w[0], w[1], w[2], w[3]);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) reinterpret_cast<O*>(A.out[m])[e] = (O)(w[m] * A.s[m]);
+}
+
+template <typename O>
 __global__ __launch_bounds__(256) void quad_dequant_kernel(const QuadDequantArgs A) {
   __shared__ QuadLds<1, 1> T;
   quad_build_lds(T, A.luts);
   __syncthreads();
   const int64_t total = A.N * A.K;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t k = e / A.N, n = e - k * A.N;
-    float w[4];
-    quad_decode(T, A.codes[k * A.c_sk + n * A.c_sn], 0, 0, w[0], w[1], w[2], w[3]);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) A.out[m][e] = w[m] * A.s[m];
+  if (total < (1ll << 32)) {
+    // 32-bit index arithmetic (a 64-bit division per element costs more than the decode)
+    const uint32_t N = (uint32_t)A.N, tot = (uint32_t)total;
+    for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < tot; e += gridDim.x * blockDim.x)
+      quad_dequant_at<O>(T, A, e, e / N, e % N);
+  } else {
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x)
+      quad_dequant_at<O>(T, A, e, e / A.N, e % A.N);
   }
 }
 
@@ -52,11 +65,12 @@ struct QuadPlugScatterArgs {
   int64_t plug_n, elem_base;
   int64_t c_sk, c_sn;
   float s[4];
-  float* out[4];
+  void* out[4];
   int64_t N, K;
 };
 
 // Entries are unique positions, so the scatter has no write conflicts.
+template <typename O>
 __global__ void quad_plug_scatter_kernel(const QuadPlugScatterArgs A) {
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= A.plug_n) return;
@@ -73,7 +87,7 @@ __global__ void quad_plug_scatter_kernel(const QuadPlugScatterArgs A) {
   if (k >= A.K || n >= A.N) return;
   const int64_t e = k * A.N + n;
 #pragma unroll
-  for (int m = 0; m < 4; ++m) A.out[m][e] = (float)A.plug_vals[4 * j + m] * A.s[m];
+  for (int m = 0; m < 4; ++m) reinterpret_cast<O*>(A.out[m])[e] = (O)((float)A.plug_vals[4 * j + m] * A.s[m]);
 }
 
 struct QuadWsGemmArgs {
@@ -133,9 +147,10 @@ extern "C" int64_t pp_quad_gemm_workspace_size(const void* a, int64_t a_sm, int6
   return 4 * N * K * (int64_t)sizeof(float);
 }
 
-extern "C" int pp_quad_dequant(const uint32_t* codes, int64_t c_sk, int64_t c_sn, const void* const* luts,
+template <typename O>
+static int quad_dequant_to(const uint32_t* codes, int64_t c_sk, int64_t c_sn, const void* const* luts,
                                int lut_dtype, const float* scales, const uint32_t* plug_idx, const void* plug_vals,
-                               int64_t plug_n, int64_t elem_base, float* const* out, int64_t N, int64_t K,
+                               int64_t plug_n, int64_t elem_base, void* const* out, int64_t N, int64_t K,
                                void* stream) {
   if (int rc = check_luts(luts, lut_dtype)) return rc;
   PP_REQUIRE(N >= 0 && K >= 0, "negative shape");
@@ -159,7 +174,7 @@ extern "C" int pp_quad_dequant(const uint32_t* codes, int64_t c_sk, int64_t c_sn
   A.N = N;
   A.K = K;
   const int64_t blocks = std::min<int64_t>((N * K + 255) / 256, (int64_t)device_cu_count() * 16);
-  hipLaunchKernelGGL(quad_dequant_kernel, dim3((unsigned)blocks), dim3(256), 0, st, A);
+  hipLaunchKernelGGL(quad_dequant_kernel<O>, dim3((unsigned)blocks), dim3(256), 0, st, A);
   PP_LAUNCH_CHECK();
   if (plug_n > 0) {
     QuadPlugScatterArgs P;
@@ -175,10 +190,26 @@ extern "C" int pp_quad_dequant(const uint32_t* codes, int64_t c_sk, int64_t c_sn
     }
     P.N = N;
     P.K = K;
-    hipLaunchKernelGGL(quad_plug_scatter_kernel, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0, st, P);
+    hipLaunchKernelGGL(quad_plug_scatter_kernel<O>, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0, st, P);
     PP_LAUNCH_CHECK();
   }
   return PP_OK;
+}
+
+extern "C" int pp_quad_dequant(const uint32_t* codes, int64_t c_sk, int64_t c_sn, const void* const* luts,
+                               int lut_dtype, const float* scales, const uint32_t* plug_idx, const void* plug_vals,
+                               int64_t plug_n, int64_t elem_base, float* const* out, int64_t N, int64_t K,
+                               void* stream) {
+  return quad_dequant_to<float>(codes, c_sk, c_sn, luts, lut_dtype, scales, plug_idx, plug_vals, plug_n, elem_base,
+                                reinterpret_cast<void* const*>(out), N, K, stream);
+}
+
+extern "C" int pp_quad_dequant_f16(const uint32_t* codes, int64_t c_sk, int64_t c_sn, const void* const* luts,
+                                   int lut_dtype, const float* scales, const uint32_t* plug_idx,
+                                   const void* plug_vals, int64_t plug_n, int64_t elem_base, void* const* out,
+                                   int64_t N, int64_t K, void* stream) {
+  return quad_dequant_to<f16>(codes, c_sk, c_sn, luts, lut_dtype, scales, plug_idx, plug_vals, plug_n, elem_base,
+                              out, N, K, stream);
 }
 
 extern "C" int pp_quad_gemm(const void* a, int64_t a_sm, int64_t a_sk, const uint32_t* codes, int64_t c_sk,

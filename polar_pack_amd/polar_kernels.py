@@ -10,7 +10,11 @@ Same names, arguments, return values and error behaviour as the reference
   polar_bitpack.py:240-243), ``elem_base``, ``layout`` (``"i16"`` kernel layout
   or ``"u16be"`` file layout) and ``chunk_size`` (0 = the kernel's (k*N + n)
   group rule, > 0 = the container's stream-position rule).
-* :func:`dual_dequant` -- float32 weights of a code view (parity export).
+* :func:`dual_dequant` -- float32 (or fp16) weights of a code view.
+
+Batches of 1-4 tokens run on the fused decode kernels; larger ones decode once into
+fp16 weights (the values the reference's kernel rounds its weights to,
+polar_kernels.py:78-82) and run a library fp16 GEMM (hipBLASLt through torch.matmul).
 """
 from __future__ import annotations
 
@@ -122,6 +126,12 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
     bmax = bmax.contiguous()
     pi, pa, pn, keep = _dual_plug(plug, dev)
     L = nat.lib()
+    if M > FUSED_MAX_M:
+        w1, w2 = dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug=plug,
+                              elem_base=elem_base, layout=layout, chunk_size=chunk_size, dtype=torch.float16)
+        torch.matmul(a_fp16, w1, out=out1)
+        torch.matmul(a_fp16, w2, out=out2)
+        return out1, out2
     ws_bytes = L.pp_dual_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), packed.data_ptr(),
                                              packed.stride(0), packed.stride(1), group_size, chunk_size,
                                              int(elem_base), pn, M, N, K)
@@ -137,12 +147,18 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
     return out1, out2
 
 
+FUSED_MAX_M = 4   # larger batches decode once and run a library GEMM
+
+
 def dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases=1024, group_size=32, *, plug=None,
-                 elem_base=0, layout="i16", chunk_size=0):
-    """float32 (K,N) weight pair ``(w1, w2)`` of a code view, plug applied."""
+                 elem_base=0, layout="i16", chunk_size=0, dtype=torch.float32):
+    """(K,N) weight pair ``(w1, w2)`` of a code view, plug applied, float32 or float16
+    (``dtype``)."""
     K, N = packed.shape
     dev = _check_device(packed, bmax, amp_lut, cos_lut, sin_lut)
-    w1 = torch.empty((K, N), dtype=torch.float32, device=dev)
+    if dtype not in (torch.float32, torch.float16):
+        raise TypeError("dtype must be torch.float32 or torch.float16")
+    w1 = torch.empty((K, N), dtype=dtype, device=dev)
     w2 = torch.empty_like(w1)
     if K * N == 0:
         return w1, w2
@@ -150,10 +166,10 @@ def dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases=1024, group
     lut_dt = _lut_dtype(amp_lut, cos_lut, sin_lut)
     pi, pa, pn, keep = _dual_plug(plug, dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
-    rc = nat.lib().pp_dual_dequant(packed.data_ptr(), lay, packed.stride(0), packed.stride(1),
-                                   bmax.contiguous().data_ptr(), group_size, chunk_size, amp_lut.data_ptr(),
-                                   amp_lut.numel(), cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases, lut_dt,
-                                   pi, pa, pn, int(elem_base), w1.data_ptr(), w2.data_ptr(), N, K, stream)
+    fn = nat.lib().pp_dual_dequant if dtype == torch.float32 else nat.lib().pp_dual_dequant_f16
+    rc = fn(packed.data_ptr(), lay, packed.stride(0), packed.stride(1), bmax.contiguous().data_ptr(), group_size,
+            chunk_size, amp_lut.data_ptr(), amp_lut.numel(), cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases,
+            lut_dt, pi, pa, pn, int(elem_base), w1.data_ptr(), w2.data_ptr(), N, K, stream)
     nat.check(rc, "pp_dual_dequant")
     del keep
     return w1, w2

@@ -9,7 +9,14 @@ Same names, arguments, return values and error behaviour as the reference
 * :func:`quad_bitpacked` -- one packed pass -> 4 fp16 GEMM outputs.
   Keyword-only extensions: ``plug=(idx, vals)`` (the ``.quadpack`` plug table,
   quaternion_packer.py:187-193) and ``elem_base``.
-* :func:`quad_dequant` -- float32 weights of a code view (parity export).
+* :func:`quad_dequant` -- float32 (or fp16) weights of a code view.
+
+Batches: 1-8 tokens run on the fused decode kernels; 9-256 tokens on the matrix-core
+decode when the codes are an (N,K) block seen as (K,N) (the container layout); larger
+batches, and more than 8 tokens on other layouts, decode once into fp16 weights (the
+values the reference's kernel rounds its weights to, quad_kernels.py:117-126) and run a
+library fp16 GEMM (hipBLASLt through torch.matmul), where the matmul's compute, not the
+weight stream, bounds the time.
 """
 from __future__ import annotations
 
@@ -128,7 +135,11 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
     sc = nat.float_array(scales)
     pi, pv, pn, keep = _plug_args(plug, dev)
     L = nat.lib()
-    if M > 8 and _mfma_layout_ok(codes, K):
+    if M > PREFILL_M or (M > 8 and not _mfma_layout_ok(codes, K)):
+        _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base), outs, L, dev)
+        del keep
+        return outs
+    if M > 8:
         # the matrix-core path takes up to 64 tokens per launch: larger batches (the
         # reference's prefill sizes, quad_kernels.py:166-189) run in blocks of 64 rows
         for i0 in range(0, M, 64):
@@ -149,6 +160,21 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
     nat.check(rc, "pp_quad_gemm")
     del keep
     return outs
+
+
+PREFILL_M = 256   # batches above this decode once and run a library GEMM on every layout
+
+
+def _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, elem_base, outs, L, dev):
+    """Decode into fp16 (K,N) weights s_m * W_m (plug applied), then 4 fp16 GEMMs."""
+    K, N = codes.shape
+    w = torch.empty((4, K, N), dtype=torch.float16, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = L.pp_quad_dequant_f16(codes.data_ptr(), codes.stride(0), codes.stride(1), lut_ptrs, lut_dtype, sc, pi, pv,
+                               pn, elem_base, nat.ptr_array([w[m].data_ptr() for m in range(4)]), N, K, stream)
+    nat.check(rc, "pp_quad_dequant_f16")
+    for m in range(4):
+        torch.matmul(a, w[m], out=outs[m])
 
 
 def _mfma_layout_ok(codes, K):
@@ -187,19 +213,22 @@ def _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, 
     return outs
 
 
-def quad_dequant(codes, luts, scales, *, plug=None, elem_base=0):
-    """float32 (K,N) weights ``s_k * W_k`` of a code view, plug applied (4 tensors)."""
+def quad_dequant(codes, luts, scales, *, plug=None, elem_base=0, dtype=torch.float32):
+    """(K,N) weights ``s_k * W_k`` of a code view, plug applied (4 tensors), float32 or
+    float16 (``dtype``)."""
     K, N = codes.shape
     dev = _check_device(codes, *luts)
-    outs = [torch.empty((K, N), dtype=torch.float32, device=dev) for _ in range(4)]
+    if dtype not in (torch.float32, torch.float16):
+        raise TypeError("dtype must be torch.float32 or torch.float16")
+    outs = [torch.empty((K, N), dtype=dtype, device=dev) for _ in range(4)]
     if K * N == 0:
         return outs
     lut_ptrs, lut_dtype = _lut_args(luts)
     pi, pv, pn, keep = _plug_args(plug, dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
-    rc = nat.lib().pp_quad_dequant(codes.data_ptr(), codes.stride(0), codes.stride(1), lut_ptrs, lut_dtype,
-                                   nat.float_array(scales), pi, pv, pn, int(elem_base),
-                                   nat.ptr_array([o.data_ptr() for o in outs]), N, K, stream)
+    fn = nat.lib().pp_quad_dequant if dtype == torch.float32 else nat.lib().pp_quad_dequant_f16
+    rc = fn(codes.data_ptr(), codes.stride(0), codes.stride(1), lut_ptrs, lut_dtype, nat.float_array(scales), pi, pv,
+            pn, int(elem_base), nat.ptr_array([o.data_ptr() for o in outs]), N, K, stream)
     nat.check(rc, "pp_quad_dequant")
     del keep
     return outs

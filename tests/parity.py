@@ -51,6 +51,17 @@ def assert_gemv_close(got, ref, what="", rtol=GEMV_RTOL, floor=GEMV_FLOOR, bound
                                 f"normwise {err.max() / max(scale, 1e-300):.2e}")
 
 
+def fp16_weight_bound(a, w):
+    """Per-output allowance for weights rounded to fp16 before an fp32-accumulated dot
+    product, as the reference kernels do (quad_kernels.py:117-126, polar_kernels.py:78-82)
+    and the large-batch path (fp16 decode + library GEMM) does: each weight moves by at
+    most 2^-11 of itself (2^-25 absolute below fp16's normal range), and the sum adds the
+    float32 dot-product bound 2^-18 * sum_k |w_k x_k|."""
+    a = np.abs(np.asarray(a, np.float64))
+    w = np.abs(np.asarray(w, np.float64))
+    return (2.0 ** -11 + 2.0 ** -18) * (a @ w) + 2.0 ** -25 * a.sum(axis=1, keepdims=True)
+
+
 def normwise(got, ref):
     ref = np.asarray(ref, np.float64)
     return float(np.abs(np.asarray(got, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-300))

@@ -6,7 +6,7 @@ import torch
 import gen
 from oracle import dualpack as odp
 from oracle import layer as olay
-from parity import assert_dequant_close, assert_gemv_close
+from parity import fp16_ulp_distance, assert_dequant_close, assert_gemv_close, fp16_weight_bound
 from polar_pack_amd import polar_kernels as pk
 
 pytestmark = pytest.mark.gpu
@@ -20,6 +20,12 @@ def u32(a):
 def kernel_layout_layer(K, N, seed, dtype=torch.float16):
     w1, w2 = [torch.from_numpy(w.reshape(K, N)).to(dtype) for w in gen.correlated_models(seed, [K * N] * 2)]
     return olay.quantize_polar_bitpacked(w1, w2)
+
+
+def prefill_bound(a, w):
+    """More than 4 tokens: fp16 decode + library GEMM, weights rounded to fp16 as the
+    reference's kernel rounds them (polar_kernels.py:78-82)."""
+    return fp16_weight_bound(a, w) if a.shape[0] > pk.FUSED_MAX_M else None
 
 
 def to_dev(*arrs):
@@ -68,7 +74,7 @@ def test_polar_dual_bitpacked_kernel_layout(K, N, M):
     W = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut)
     for o, w in ((o1, W[0]), (o2, W[1])):
         assert o.shape == (M, N) and o.dtype == torch.float16
-        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w))
+        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), bound=prefill_bound(a, w))
 
 
 @pytest.mark.parametrize("M", [1, 2, 4, 6])
@@ -89,7 +95,8 @@ def test_polar_dual_bitpacked_container_stream(chunk, M):
                                          chunk_size=dp.chunk_size, plug=plug, elem_base=base)
         d1, d2 = odp.decode_pairs_f64(dp, base, base + N * K)
         for o, d in ((o1, d1), (o2, d2)):
-            assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, d.reshape(N, K).T), f"base {base}")
+            w = d.reshape(N, K).T
+            assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), f"base {base}", bound=prefill_bound(a, w))
 
 
 @pytest.mark.parametrize("dtype,max_frac,max_step", [(torch.float16, 0.25, 2), (torch.float32, 0.01, 1)])
@@ -137,7 +144,7 @@ def test_polar_dual_bitpacked_kn_fast_path(K, N, plug, M):
     for w, lut in ((W[0], cos_lut), (W[1], sin_lut)):
         w[kk, nn] = vals.astype(np.float64) * np.asarray(lut, np.float64)[ph[kk, nn]]
     for o, w in ((o1, W[0]), (o2, W[1])):
-        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w))
+        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), bound=prefill_bound(a, w))
 
 
 def test_polar_dual_bitpacked_kn_output_view():
@@ -163,3 +170,22 @@ def test_polar_dual_bitpacked_kn_output_view():
     torch.cuda.synchronize()
     for out, w in ((o1, W[0]), (o2, W[1])):
         assert_gemv_close(out.float().cpu().numpy(), olay.gemm_f64(a, w))
+
+
+@pytest.mark.parametrize("layout", ["i16", "u16be"])
+def test_dual_dequant_f16_is_rounded_f32(layout):
+    """The fp16 decode (the large-batch path's weights) is the float32 decode rounded to fp16."""
+    K, N = 256, 512
+    packed, bmax, amp_lut, cos_lut, sin_lut = kernel_layout_layer(K, N, 9)
+    codes = torch.from_numpy(packed).to(DEV)
+    if layout == "u16be":
+        codes = torch.from_numpy(((packed.view(np.uint16) ^ 0x8000).byteswap()).view(np.int16)).to(DEV)
+    args = to_dev(bmax, amp_lut, cos_lut, sin_lut)
+    w32 = pk.dual_dequant(codes, *args, layout=layout)
+    w16 = pk.dual_dequant(codes, *args, layout=layout, dtype=torch.float16)
+    for a32, a16 in zip(w32, w16):
+        assert a16.dtype == torch.float16
+        # the fp16 store may round the exact product once (a mixed-precision multiply)
+        # where the float32 path rounds twice: at most 1 ulp apart, and rarely
+        d = fp16_ulp_distance(a16.cpu().numpy(), a32.cpu().numpy())
+        assert d.max() <= 1 and (d > 0).mean() < 1e-3
