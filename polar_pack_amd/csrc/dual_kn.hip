@@ -134,8 +134,71 @@ __device__ __forceinline__ void dkn_compute(const char* lds, const DualLane& lo,
   }
 }
 
+// A wave's item: its 512 columns and row slice.
+struct DknItem {
+  int n, k0, k1, sl;
+  uint32_t voff;
+};
+
+__device__ __forceinline__ DknItem dkn_item(const DualKnArgs& A, int64_t it, int lane) {
+  DknItem I;
+  const int blk = (int)uniform64(it / A.slices);
+  I.sl = (int)uniform64(it % A.slices);
+  I.n = blk * DKN_COLS + 8 * lane;          // the lane's first column
+  I.k0 = I.sl * A.ks;
+  I.k1 = min(A.K, I.k0 + A.ks);
+  I.voff = I.n < A.N ? 2u * (uint32_t)I.n : OOB;
+  return I;
+}
+
+// One item, its first step already issued into s0.
 template <int MT, int LAYOUT>
-__device__ __forceinline__ void dkn_body(const char* lds, const DualKnArgs& A) {
+__device__ __forceinline__ void dkn_run(const char* lds, const DualLane& lo, const DualKnArgs& A, const DknItem& I,
+                                        DknStep<MT>& s0, DknStep<MT>& s1) {
+  float acc[8][2][MT];
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[c][0][j] = acc[c][1][j] = 0.f;
+  for (int k = I.k0; k < I.k1; k += 2 * DKN_R) {
+    dkn_issue<MT>(A, k + DKN_R, I.k1, I.n, I.voff, s1);
+    dkn_compute<MT, LAYOUT>(lds, lo, s0, acc);
+    if (k + DKN_R >= I.k1) break;
+    dkn_issue<MT>(A, k + 2 * DKN_R, I.k1, I.n, I.voff, s0);
+    dkn_compute<MT, LAYOUT>(lds, lo, s1, acc);
+  }
+  const int n = I.n;
+  if (A.part == nullptr) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const rsrc_t ro = make_rsrc(A.out[m], 2u * (uint32_t)((int64_t)(A.M - 1) * A.o_sm + (int64_t)(A.N - 1) * A.o_sn + 1));
+#pragma unroll
+      for (int j = 0; j < MT; ++j)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const f16 h = (f16)acc[c][m][j];
+          const bool ok = n + c < A.N && j < A.M;
+          vstore16((uint32_t)__builtin_bit_cast(unsigned short, h),
+                   ok ? 2u * (uint32_t)((int64_t)j * A.o_sm + (int64_t)(n + c) * A.o_sn) : OOB, ro);
+        }
+    }
+  } else {
+    // partials [sl][m][j][n .. n+7] as two 16-byte stores (N % 8 == 0 on this path)
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int j = 0; j < MT; ++j)
+        if (n < A.N && j < A.M) {
+          float4* p = reinterpret_cast<float4*>(A.part + (((int64_t)I.sl * 2 + m) * A.M + j) * A.N + n);
+          p[0] = make_float4(acc[0][m][j], acc[1][m][j], acc[2][m][j], acc[3][m][j]);
+          p[1] = make_float4(acc[4][m][j], acc[5][m][j], acc[6][m][j], acc[7][m][j]);
+        }
+  }
+}
+
+template <int MT, int LAYOUT>
+__global__ __launch_bounds__(DKN_NT) void dual_kn_kernel(const DualKnArgs A) {
+  __shared__ __attribute__((aligned(16))) char T[DLDS_BYTES];
   constexpr int WAVES = DKN_NT / 64;
   const int lane = threadIdx.x & 63;
   const DualLane lo = dual_lane(lane);
@@ -144,61 +207,20 @@ __device__ __forceinline__ void dkn_body(const char* lds, const DualKnArgs& A) {
   const int64_t gw = (int64_t)uniform(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
   const int64_t nw = (int64_t)gridDim.x * WAVES;
   const int64_t items = A.nblk * A.slices;
-  for (int64_t it = gw; it < items; it += nw) {
-    const int blk = (int)uniform64(it / A.slices), sl = (int)uniform64(it % A.slices);
-    const int n = blk * DKN_COLS + 8 * lane;           // the lane's first column
-    const int k0 = sl * A.ks, k1 = min(A.K, k0 + A.ks);
-    const uint32_t voff = n < A.N ? 2u * (uint32_t)n : OOB;
-    float acc[8][2][MT];
-#pragma unroll
-    for (int c = 0; c < 8; ++c)
-#pragma unroll
-      for (int j = 0; j < MT; ++j) acc[c][0][j] = acc[c][1][j] = 0.f;
-    DknStep<MT> s0, s1;
-    dkn_issue<MT>(A, k0, k1, n, voff, s0);
-    for (int k = k0; k < k1; k += 2 * DKN_R) {
-      dkn_issue<MT>(A, k + DKN_R, k1, n, voff, s1);
-      dkn_compute<MT, LAYOUT>(lds, lo, s0, acc);
-      if (k + DKN_R >= k1) break;
-      dkn_issue<MT>(A, k + 2 * DKN_R, k1, n, voff, s0);
-      dkn_compute<MT, LAYOUT>(lds, lo, s1, acc);
-    }
-    if (A.part == nullptr) {
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const rsrc_t ro = make_rsrc(A.out[m], 2u * (uint32_t)((int64_t)(A.M - 1) * A.o_sm + (int64_t)(A.N - 1) * A.o_sn + 1));
-#pragma unroll
-        for (int j = 0; j < MT; ++j)
-#pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            const f16 h = (f16)acc[c][m][j];
-            const bool ok = n + c < A.N && j < A.M;
-            vstore16((uint32_t)__builtin_bit_cast(unsigned short, h),
-                     ok ? 2u * (uint32_t)((int64_t)j * A.o_sm + (int64_t)(n + c) * A.o_sn) : OOB, ro);
-          }
-      }
-    } else {
-      // partials [sl][m][j][n .. n+7] as two 16-byte stores (N % 8 == 0 on this path)
-#pragma unroll
-      for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int j = 0; j < MT; ++j)
-          if (n < A.N && j < A.M) {
-            float4* p = reinterpret_cast<float4*>(A.part + (((int64_t)sl * 2 + m) * A.M + j) * A.N + n);
-            p[0] = make_float4(acc[0][m][j], acc[1][m][j], acc[2][m][j], acc[3][m][j]);
-            p[1] = make_float4(acc[4][m][j], acc[5][m][j], acc[6][m][j], acc[7][m][j]);
-          }
-    }
-  }
-}
-
-template <int MT, int LAYOUT>
-__global__ __launch_bounds__(DKN_NT) void dual_kn_kernel(const DualKnArgs A) {
-  __shared__ __attribute__((aligned(16))) char T[DLDS_BYTES];
+  // the first item's first loads travel while the tables are built
+  DknStep<MT> s0, s1;
+  DknItem I = dkn_item(A, gw < items ? gw : 0, lane);
+  if (gw < items) dkn_issue<MT>(A, I.k0, I.k1, I.n, I.voff, s0);
   if (A.luts.dtype == PP_F16) dkn_tables_of<LAYOUT, f16>(T, A.luts);
   else dkn_tables_of<LAYOUT, float>(T, A.luts);
   __syncthreads();
-  dkn_body<MT, LAYOUT>(T, A);
+  for (int64_t it = gw; it < items; it += nw) {
+    if (it != gw) {
+      I = dkn_item(A, it, lane);
+      dkn_issue<MT>(A, I.k0, I.k1, I.n, I.voff, s0);
+    }
+    dkn_run<MT, LAYOUT>(T, lo, A, I, s0, s1);
+  }
 }
 
 // Plug corrections, one entry per thread, added to slice 0's partial sums after the
@@ -237,16 +259,33 @@ __global__ __launch_bounds__(256) void dual_kn_plug_kernel(const DualKnPlugArgs 
   }
 }
 
-// out_m[j, n] = fp16(sum over slices of part[sl][m][j][n]), 4 consecutive columns per
-// thread (N % 8 == 0 on this path).
-__global__ __launch_bounds__(256) void dual_kn_finish_kernel(const DualKnArgs A) {
+// out_m[j, n] = fp16(sum over slices of part[sl][m][j][n]): a workgroup takes 64 runs of
+// 4 consecutive columns (N % 8 == 0 on this path), its 8 wavefronts every 8th slice each,
+// summed through LDS, so the slices' loads are in flight together.
+constexpr int KN_FIN_NT = 512;
+
+__global__ __launch_bounds__(KN_FIN_NT) void dual_kn_finish_kernel(const DualKnArgs A) {
+  __shared__ float4 red[KN_FIN_NT / 64][64];
+  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int64_t total = 2ll * A.M * A.N;
-  const int64_t i0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
-  if (i0 >= total) return;
+  const int64_t i0 = 4 * ((int64_t)blockIdx.x * 64 + lane);
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-  for (int sl = 0; sl < A.slices; ++sl) {
-    const float4 t = *reinterpret_cast<const float4*>(A.part + (int64_t)sl * total + i0);
+  if (i0 < total) {
+#pragma unroll 4
+    for (int sl = grp; sl < A.slices; sl += KN_FIN_NT / 64) {
+      const float4 t = *reinterpret_cast<const float4*>(A.part + (int64_t)sl * total + i0);
+      v.x += t.x;
+      v.y += t.y;
+      v.z += t.z;
+      v.w += t.w;
+    }
+  }
+  red[grp][lane] = v;
+  __syncthreads();
+  if (grp != 0 || i0 >= total) return;
+#pragma unroll
+  for (int g = 1; g < KN_FIN_NT / 64; ++g) {
+    const float4 t = red[g][lane];
     v.x += t.x;
     v.y += t.y;
     v.z += t.z;
@@ -262,7 +301,7 @@ __global__ __launch_bounds__(256) void dual_kn_finish_kernel(const DualKnArgs A)
 
 // ------------------------------------------------------------------ host side
 #ifndef PP_DKN_MIN_ROWS
-#define PP_DKN_MIN_ROWS 64
+#define PP_DKN_MIN_ROWS 16   // slices of at least this many rows (4096x4096: 1..4 tokens measured best)
 #endif
 
 struct DknPlan {
@@ -352,7 +391,7 @@ int dual_kn_gemm(const void* a, int64_t a_sm, const void* codes, int code_layout
       PP_LAUNCH_CHECK();
     }
     const int64_t total = 2 * M * N;
-    hipLaunchKernelGGL(dual_kn_finish_kernel, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0, st, A);
+    hipLaunchKernelGGL(dual_kn_finish_kernel, dim3((unsigned)((total / 4 + 63) / 64)), dim3(KN_FIN_NT), 0, st, A);
     PP_LAUNCH_CHECK();
   }
   return PP_OK;

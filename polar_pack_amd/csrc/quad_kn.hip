@@ -122,63 +122,85 @@ __device__ __forceinline__ void kn_compute(const char* lds, const LaneOff& lo, c
   }
 }
 
+// A wave's item: its 256 columns and row slice.
+struct KnItem {
+  int n, k0, k1, sl;
+  uint32_t voff;
+};
+
+__device__ __forceinline__ KnItem kn_item(const QuadKnArgs& A, int64_t it, int lane) {
+  KnItem I;
+  const int blk = (int)uniform64(it / A.slices);
+  I.sl = (int)uniform64(it % A.slices);
+  I.n = blk * KN_COLS + 4 * lane;           // the lane's first column
+  I.k0 = I.sl * A.ks;
+  I.k1 = min(A.K, I.k0 + A.ks);
+  I.voff = I.n < A.N ? 4u * (uint32_t)I.n : OOB;
+  return I;
+}
+
+// One item, its first step already issued into s0.
 template <int MT, class L>
-__device__ __forceinline__ void kn_body(const char* lds, const QuadKnArgs& A) {
-  constexpr int WAVES = KN_NT / 64;
-  const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void kn_run(const char* lds, const LaneOff& lo, const QuadKnArgs& A, const KnItem& I,
+                                       KnStep<MT>& s0, KnStep<MT>& s1) {
+  float acc[4][4][MT];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) acc[c][m][j] = 0.f;
+  for (int k = I.k0; k < I.k1; k += 2 * KN_R) {
+    kn_issue<MT>(A, k + KN_R, I.k1, I.voff, s1);
+    kn_compute<MT, L>(lds, lo, s0, acc);
+    if (k + KN_R >= I.k1) break;
+    kn_issue<MT>(A, k + 2 * KN_R, I.k1, I.voff, s0);
+    kn_compute<MT, L>(lds, lo, s1, acc);
+  }
+  const int n = I.n;
+  if (A.part == nullptr) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const rsrc_t ro = make_rsrc(A.out[m], 2u * (uint32_t)((int64_t)(A.M - 1) * A.o_sm + (int64_t)(A.N - 1) * A.o_sn + 1));
+#pragma unroll
+      for (int j = 0; j < MT; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f16 h = (f16)(acc[c][m][j] * A.s[m]);
+          const bool ok = n + c < A.N && j < A.M;
+          vstore16((uint32_t)__builtin_bit_cast(unsigned short, h),
+                   ok ? 2u * (uint32_t)((int64_t)j * A.o_sm + (int64_t)(n + c) * A.o_sn) : OOB, ro);
+        }
+    }
+  } else {
+    // partials [sl][m][j][n .. n+3] as one 16-byte store (N % 4 == 0 on this path)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int j = 0; j < MT; ++j)
+        if (n < A.N && j < A.M) {
+          float4* p = reinterpret_cast<float4*>(A.part + (((int64_t)I.sl * 4 + m) * A.M + j) * A.N + n);
+          *p = make_float4(acc[0][m][j] * A.s[m], acc[1][m][j] * A.s[m], acc[2][m][j] * A.s[m],
+                           acc[3][m][j] * A.s[m]);
+        }
+  }
+}
+
+// With 4 tokens the early loads would stay live through the table build and spill.
+template <int MT>
+constexpr bool kn_early() { return MT <= 2; }
+
+template <int MT, class L>
+__device__ __forceinline__ void kn_items(const char* lds, const QuadKnArgs& A, int64_t gw, int64_t nw, int lane,
+                                         KnItem I, KnStep<MT>& s0, KnStep<MT>& s1) {
   const LaneOff lo = L::lane(lane);
-  // items dealt round-robin over the workgroups, so a launch with fewer items than
-  // wavefronts still spreads them over every CU
-  const int64_t gw = (int64_t)uniform(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
-  const int64_t nw = (int64_t)gridDim.x * WAVES;
   const int64_t items = A.nblk * A.slices;
   for (int64_t it = gw; it < items; it += nw) {
-    const int blk = (int)uniform64(it / A.slices), sl = (int)uniform64(it % A.slices);
-    const int n = blk * KN_COLS + 4 * lane;           // the lane's first column
-    const int k0 = sl * A.ks, k1 = min(A.K, k0 + A.ks);
-    const uint32_t voff = n < A.N ? 4u * (uint32_t)n : OOB;
-    float acc[4][4][MT];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int j = 0; j < MT; ++j) acc[c][m][j] = 0.f;
-    KnStep<MT> s0, s1;
-    kn_issue<MT>(A, k0, k1, voff, s0);
-    for (int k = k0; k < k1; k += 2 * KN_R) {
-      kn_issue<MT>(A, k + KN_R, k1, voff, s1);
-      kn_compute<MT, L>(lds, lo, s0, acc);
-      if (k + KN_R >= k1) break;
-      kn_issue<MT>(A, k + 2 * KN_R, k1, voff, s0);
-      kn_compute<MT, L>(lds, lo, s1, acc);
+    if (it != gw || !kn_early<MT>()) {
+      I = kn_item(A, it, lane);
+      kn_issue<MT>(A, I.k0, I.k1, I.voff, s0);
     }
-    if (A.part == nullptr) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const rsrc_t ro = make_rsrc(A.out[m], 2u * (uint32_t)((int64_t)(A.M - 1) * A.o_sm + (int64_t)(A.N - 1) * A.o_sn + 1));
-#pragma unroll
-        for (int j = 0; j < MT; ++j)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const f16 h = (f16)(acc[c][m][j] * A.s[m]);
-            const bool ok = n + c < A.N && j < A.M;
-            vstore16((uint32_t)__builtin_bit_cast(unsigned short, h),
-                     ok ? 2u * (uint32_t)((int64_t)j * A.o_sm + (int64_t)(n + c) * A.o_sn) : OOB, ro);
-          }
-      }
-    } else {
-      // partials [sl][m][j][n .. n+3] as one 16-byte store (N % 4 == 0 on this path)
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int j = 0; j < MT; ++j)
-          if (n < A.N && j < A.M) {
-            float4* p = reinterpret_cast<float4*>(A.part + (((int64_t)sl * 4 + m) * A.M + j) * A.N + n);
-            *p = make_float4(acc[0][m][j] * A.s[m], acc[1][m][j] * A.s[m], acc[2][m][j] * A.s[m],
-                             acc[3][m][j] * A.s[m]);
-          }
-    }
+    kn_run<MT, L>(lds, lo, A, I, s0, s1);
   }
 }
 
@@ -186,8 +208,19 @@ template <int MT>
 __global__ __launch_bounds__(KN_NT) void quad_kn_kernel(const QuadKnArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t T[QLDS_BYTES / 4];
   const char* lds = reinterpret_cast<const char*>(T);
-  if (quad_tables<KN_NT>(T, A.luts)) kn_body<MT, LayShared>(lds, A);
-  else kn_body<MT, LaySplit>(lds, A);
+  constexpr int WAVES = KN_NT / 64;
+  const int lane = threadIdx.x & 63;
+  // items dealt round-robin over the workgroups, so a launch with fewer items than
+  // wavefronts still spreads them over every CU
+  const int64_t gw = (int64_t)uniform(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
+  const int64_t nw = (int64_t)gridDim.x * WAVES;
+  const int64_t items = A.nblk * A.slices;
+  // the first item's first loads travel while the tables are built (1-2 tokens)
+  KnStep<MT> s0, s1;
+  const KnItem I = kn_item(A, gw < items ? gw : 0, lane);
+  if (kn_early<MT>() && gw < items) kn_issue<MT>(A, I.k0, I.k1, I.voff, s0);
+  if (quad_tables<KN_NT>(T, A.luts)) kn_items<MT, LayShared>(lds, A, gw, nw, lane, I, s0, s1);
+  else kn_items<MT, LaySplit>(lds, A, gw, nw, lane, I, s0, s1);
 }
 
 // Plug corrections, one entry per thread, added to slice 0's partial sums after the
@@ -237,16 +270,33 @@ __global__ __launch_bounds__(256) void quad_kn_plug_kernel(const QuadKnPlugArgs 
   }
 }
 
-// out_m[j, n] = fp16(sum over slices of part[sl][m][j][n]), 4 consecutive columns per
-// thread (N % 4 == 0 on this path).
-__global__ __launch_bounds__(256) void quad_kn_finish_kernel(const QuadKnArgs A) {
+// out_m[j, n] = fp16(sum over slices of part[sl][m][j][n]): a workgroup takes 64 runs of
+// 4 consecutive columns (N % 4 == 0 on this path), its 8 wavefronts every 8th slice each,
+// summed through LDS, so the slices' loads are in flight together.
+constexpr int KN_FIN_NT = 512;
+
+__global__ __launch_bounds__(KN_FIN_NT) void quad_kn_finish_kernel(const QuadKnArgs A) {
+  __shared__ float4 red[KN_FIN_NT / 64][64];
+  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int64_t total = 4ll * A.M * A.N;
-  const int64_t i0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
-  if (i0 >= total) return;
+  const int64_t i0 = 4 * ((int64_t)blockIdx.x * 64 + lane);
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-  for (int sl = 0; sl < A.slices; ++sl) {
-    const float4 t = *reinterpret_cast<const float4*>(A.part + (int64_t)sl * total + i0);
+  if (i0 < total) {
+#pragma unroll 4
+    for (int sl = grp; sl < A.slices; sl += KN_FIN_NT / 64) {
+      const float4 t = *reinterpret_cast<const float4*>(A.part + (int64_t)sl * total + i0);
+      v.x += t.x;
+      v.y += t.y;
+      v.z += t.z;
+      v.w += t.w;
+    }
+  }
+  red[grp][lane] = v;
+  __syncthreads();
+  if (grp != 0 || i0 >= total) return;
+#pragma unroll
+  for (int g = 1; g < KN_FIN_NT / 64; ++g) {
+    const float4 t = red[g][lane];
     v.x += t.x;
     v.y += t.y;
     v.z += t.z;
@@ -261,6 +311,10 @@ __global__ __launch_bounds__(256) void quad_kn_finish_kernel(const QuadKnArgs A)
 }
 
 // ------------------------------------------------------------------ host side
+#ifndef PP_KN_MIN_ROWS
+#define PP_KN_MIN_ROWS 32   // slices of at least this many rows (4096x4096: 1..4 tokens measured best)
+#endif
+
 struct KnPlan {
   int slices, ks;
   int64_t nblk;
@@ -270,8 +324,9 @@ static KnPlan kn_plan(int64_t N, int64_t K) {
   KnPlan p;
   p.nblk = (N + KN_COLS - 1) / KN_COLS;
   const int64_t waves = (int64_t)device_cu_count() * (KN_NT / 64);
-  // about one item per wavefront, slices of at least 64 rows
-  int64_t s = std::max<int64_t>(1, std::min<int64_t>(waves / std::max<int64_t>(p.nblk, 1), (K + 63) / 64));
+  // about one item per wavefront, slices of at least PP_KN_MIN_ROWS rows
+  int64_t s = std::max<int64_t>(
+      1, std::min<int64_t>(waves / std::max<int64_t>(p.nblk, 1), (K + PP_KN_MIN_ROWS - 1) / PP_KN_MIN_ROWS));
   int64_t ks = (K + s - 1) / s;
   ks = (ks + KN_R - 1) / KN_R * KN_R;
   p.ks = (int)std::max<int64_t>(ks, KN_R);
@@ -340,7 +395,7 @@ int quad_kn_gemm(const void* a, int64_t a_sm, const uint32_t* codes, int64_t ldk
       PP_LAUNCH_CHECK();
     }
     const int64_t total = 4 * M * N;
-    hipLaunchKernelGGL(quad_kn_finish_kernel, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0, st, A);
+    hipLaunchKernelGGL(quad_kn_finish_kernel, dim3((unsigned)((total / 4 + 63) / 64)), dim3(KN_FIN_NT), 0, st, A);
     PP_LAUNCH_CHECK();
   }
   return PP_OK;
