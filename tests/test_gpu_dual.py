@@ -189,3 +189,18 @@ def test_dual_dequant_f16_is_rounded_f32(layout):
         # where the float32 path rounds twice: at most 1 ulp apart, and rarely
         d = fp16_ulp_distance(a16.cpu().numpy(), a32.cpu().numpy())
         assert d.max() <= 1 and (d > 0).mean() < 1e-3
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_polar_dual_bitpacked_kn_file_layout(M):
+    """Big-endian (file-layout) codes in a contiguous (K,N) tensor with the kernel's group
+    rule (chunk_size 0): the (K,N) kernel reads either layout."""
+    K, N = 256, 1024
+    packed, bmax, amp_lut, cos_lut, sin_lut = kernel_layout_layer(K, N, 21)
+    be = ((packed.view(np.uint16) ^ 0x8000).byteswap()).view(np.int16)
+    a = np.random.default_rng(M).standard_normal((M, K)).astype(np.float16)
+    x, c16, b, al, cl, sl = to_dev(a, be, bmax, amp_lut, cos_lut, sin_lut)
+    o1, o2 = pk.polar_dual_bitpacked(x, c16, b, al, cl, sl, layout="u16be")
+    W = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut)
+    for o, w in ((o1, W[0]), (o2, W[1])):
+        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w))
