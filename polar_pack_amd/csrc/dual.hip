@@ -320,6 +320,61 @@ __global__ __launch_bounds__(256) void dual_dequant_kernel(const DualDequantArgs
   }
 }
 
+// Rows contiguous across columns (c_sn == 1, N % 8 == 0, 16-byte aligned rows) and the
+// kernel's group rule with gs a power of two >= 8: a thread decodes 8 consecutive
+// columns of one row (one 16-byte code load, one group scale, two stores of 8 values).
+template <typename O>
+__global__ __launch_bounds__(256) void dual_dequant_vec_kernel(const DualDequantArgs A) {
+  __shared__ DualDqLds T;
+  const DualLuts& L = A.luts;
+  for (int i = threadIdx.x; i < 1024; i += blockDim.x) {
+    T.cs[i] = i < L.phase_n ? make_float2(lut_at(L.cs[0], L.dtype, i), lut_at(L.cs[1], L.dtype, i))
+                            : make_float2(0.f, 0.f);
+    if (i < 64) T.amp[i] = i < L.amp_n ? lut_at(L.amp, L.dtype, i) : 0.f;
+  }
+  __syncthreads();
+  const uint32_t N8 = (uint32_t)(A.N / 8), tot8 = (uint32_t)(A.N * A.K / 8);
+  for (uint32_t v = blockIdx.x * blockDim.x + threadIdx.x; v < tot8; v += gridDim.x * blockDim.x) {
+    const uint32_t k = v / N8, n = 8u * (v - k * N8), e = 8u * v;
+    const u32x4 q = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(A.codes) +
+                                                    (int64_t)k * A.c_sk + n);
+    const float sc = (float)A.scales[e >> A.grp.log2gs];
+    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+    float o1[8], o2[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t raw = (w4[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+      const uint32_t code = A.layout == PP_DUAL_U16_BE ? (((raw & 0xFFu) << 8) | (raw >> 8)) : (raw ^ 0x8000u);
+      const float amp = T.amp[(code >> 10) & 63u] * sc;
+      const float2 cs = T.cs[code & 1023u];
+      o1[i] = amp * cs.x;
+      o2[i] = amp * cs.y;
+    }
+    if constexpr (sizeof(O) == 2) {
+      // 8 fp16 values as one 16-byte store per output
+      u32x4 h1, h2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t a = __builtin_bit_cast(unsigned short, (f16)o1[2 * i]);
+        const uint32_t b = __builtin_bit_cast(unsigned short, (f16)o1[2 * i + 1]);
+        const uint32_t c = __builtin_bit_cast(unsigned short, (f16)o2[2 * i]);
+        const uint32_t d = __builtin_bit_cast(unsigned short, (f16)o2[2 * i + 1]);
+        h1[i] = a | (b << 16);
+        h2[i] = c | (d << 16);
+      }
+      *reinterpret_cast<u32x4*>(reinterpret_cast<O*>(A.out[0]) + e) = h1;
+      *reinterpret_cast<u32x4*>(reinterpret_cast<O*>(A.out[1]) + e) = h2;
+    } else {
+      float4* d1 = reinterpret_cast<float4*>(reinterpret_cast<O*>(A.out[0]) + e);
+      float4* d2 = reinterpret_cast<float4*>(reinterpret_cast<O*>(A.out[1]) + e);
+      d1[0] = make_float4(o1[0], o1[1], o1[2], o1[3]);
+      d1[1] = make_float4(o1[4], o1[5], o1[6], o1[7]);
+      d2[0] = make_float4(o2[0], o2[1], o2[2], o2[3]);
+      d2[1] = make_float4(o2[4], o2[5], o2[6], o2[7]);
+    }
+  }
+}
+
 struct DualPlugScatterArgs {
   const void* codes;
   int layout;
@@ -529,8 +584,16 @@ static int dual_dequant_to(const void* codes, int code_layout, int64_t c_sk, int
   A.out[1] = out2;
   A.N = N;
   A.K = K;
-  const int64_t blocks = std::min<int64_t>((N * K + 255) / 256, (int64_t)device_cu_count() * 16);
-  hipLaunchKernelGGL(dual_dequant_kernel<O>, dim3((unsigned)blocks), dim3(256), 0, st, A);
+  const bool vec = c_sn == 1 && c_sk % 8 == 0 && N % 8 == 0 && aligned(codes, 16) && chunk_size == 0 &&
+                   group_size >= 8 && (group_size & (group_size - 1)) == 0 && N * K < (1ll << 32) &&
+                   aligned(out1, 16) && aligned(out2, 16);
+  if (vec) {
+    const int64_t blocks = std::min<int64_t>((N * K / 8 + 255) / 256, (int64_t)device_cu_count() * 8);
+    hipLaunchKernelGGL(dual_dequant_vec_kernel<O>, dim3((unsigned)blocks), dim3(256), 0, st, A);
+  } else {
+    const int64_t blocks = std::min<int64_t>((N * K + 255) / 256, (int64_t)device_cu_count() * 16);
+    hipLaunchKernelGGL(dual_dequant_kernel<O>, dim3((unsigned)blocks), dim3(256), 0, st, A);
+  }
   PP_LAUNCH_CHECK();
   if (plug_n > 0) {
     DualPlugScatterArgs P;

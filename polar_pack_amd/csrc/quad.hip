@@ -59,6 +59,42 @@ __global__ __launch_bounds__(256) void quad_dequant_kernel(const QuadDequantArgs
   }
 }
 
+// Rows contiguous across columns (c_sn == 1, N % 4 == 0, 16-byte aligned rows): a
+// thread decodes 4 consecutive columns of one row (one 16-byte code load, one store of 4
+// values per model).
+template <typename O>
+__global__ __launch_bounds__(256) void quad_dequant_vec_kernel(const QuadDequantArgs A) {
+  __shared__ QuadLds<1, 1> T;
+  quad_build_lds(T, A.luts);
+  __syncthreads();
+  const uint32_t N4 = (uint32_t)(A.N / 4), tot4 = (uint32_t)(A.N * A.K / 4);
+  for (uint32_t v = blockIdx.x * blockDim.x + threadIdx.x; v < tot4; v += gridDim.x * blockDim.x) {
+    const uint32_t k = v / N4, n = 4u * (v - k * N4), e = 4u * v;
+    const u32x4 q = *reinterpret_cast<const u32x4*>(A.codes + (int64_t)k * A.c_sk + n);
+    const uint32_t cw[4] = {q.x, q.y, q.z, q.w};
+    float w[4][4];   // [column][model]
+#pragma unroll
+    for (int c = 0; c < 4; ++c) quad_decode(T, cw[c], 0, 0, w[c][0], w[c][1], w[c][2], w[c][3]);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      O* d = reinterpret_cast<O*>(A.out[m]) + e;
+      if constexpr (sizeof(O) == 2) {
+        u32x2 h;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const uint32_t a = __builtin_bit_cast(unsigned short, (f16)(w[2 * i][m] * A.s[m]));
+          const uint32_t b = __builtin_bit_cast(unsigned short, (f16)(w[2 * i + 1][m] * A.s[m]));
+          h[i] = a | (b << 16);
+        }
+        *reinterpret_cast<u32x2*>(d) = h;
+      } else {
+        *reinterpret_cast<float4*>(d) =
+            make_float4(w[0][m] * A.s[m], w[1][m] * A.s[m], w[2][m] * A.s[m], w[3][m] * A.s[m]);
+      }
+    }
+  }
+}
+
 struct QuadPlugScatterArgs {
   const uint32_t* plug_idx;
   const f16* plug_vals;
@@ -173,8 +209,15 @@ static int quad_dequant_to(const uint32_t* codes, int64_t c_sk, int64_t c_sn, co
   }
   A.N = N;
   A.K = K;
-  const int64_t blocks = std::min<int64_t>((N * K + 255) / 256, (int64_t)device_cu_count() * 16);
-  hipLaunchKernelGGL(quad_dequant_kernel<O>, dim3((unsigned)blocks), dim3(256), 0, st, A);
+  bool vec = c_sn == 1 && c_sk % 4 == 0 && N % 4 == 0 && aligned(codes, 16) && N * K < (1ll << 32);
+  for (int m = 0; m < 4; ++m) vec = vec && aligned(out[m], 16);
+  if (vec) {
+    const int64_t blocks = std::min<int64_t>((N * K / 4 + 255) / 256, (int64_t)device_cu_count() * 8);
+    hipLaunchKernelGGL(quad_dequant_vec_kernel<O>, dim3((unsigned)blocks), dim3(256), 0, st, A);
+  } else {
+    const int64_t blocks = std::min<int64_t>((N * K + 255) / 256, (int64_t)device_cu_count() * 16);
+    hipLaunchKernelGGL(quad_dequant_kernel<O>, dim3((unsigned)blocks), dim3(256), 0, st, A);
+  }
   PP_LAUNCH_CHECK();
   if (plug_n > 0) {
     QuadPlugScatterArgs P;
