@@ -99,6 +99,30 @@ __device__ __forceinline__ void dkn_issue(const DualKnArgs& A, int k, int kend, 
   }
 }
 
+// Table entries of one row's 8 codes.
+struct DknRowLk {
+  float an[8];
+  float2 cs[8];
+};
+
+template <int LAYOUT>
+__device__ __forceinline__ void dkn_lookup_row(const char* lds, const DualLane& lo, const u32x4& q, DknRowLk& L) {
+  const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float an[2];
+    float2 cs[2];
+    dual_lookup2<LAYOUT>(lds, w4[e], lo, an, cs);
+    L.an[2 * e] = an[0];
+    L.an[2 * e + 1] = an[1];
+    L.cs[2 * e] = cs[0];
+    L.cs[2 * e + 1] = cs[1];
+  }
+}
+
+// The lookups of row r + 1 are issued before the arithmetic of row r (the barrier keeps
+// the compiler from moving them back behind it), so a wave has a row of LDS reads in
+// flight while it multiplies.
 template <int MT, int LAYOUT>
 __device__ __forceinline__ void dkn_compute(const char* lds, const DualLane& lo, const DknStep<MT>& S,
                                             float (&acc)[8][2][MT]) {
@@ -110,27 +134,25 @@ __device__ __forceinline__ void dkn_compute(const char* lds, const DualLane& lo,
     xv[j][0] = (float)h0.x; xv[j][1] = (float)h0.y; xv[j][2] = (float)h0.z; xv[j][3] = (float)h0.w;
     xv[j][4] = (float)h1.x; xv[j][5] = (float)h1.y; xv[j][6] = (float)h1.z; xv[j][7] = (float)h1.w;
   }
+  DknRowLk buf[2];
+  dkn_lookup_row<LAYOUT>(lds, lo, S.q[0], buf[0]);
 #pragma unroll
   for (int r = 0; r < DKN_R; ++r) {
+    if (r + 1 < DKN_R) dkn_lookup_row<LAYOUT>(lds, lo, S.q[r + 1], buf[(r + 1) & 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    const DknRowLk& L = buf[r & 1];
     const float sc = h2f(S.sc[r]);
     float xs[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) xs[j] = xv[j][r] * sc;
-    const uint32_t w4[4] = {S.q[r].x, S.q[r].y, S.q[r].z, S.q[r].w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float an[2];
-      float2 cs[2];
-      dual_lookup2<LAYOUT>(lds, w4[e], lo, an, cs);
+    for (int c = 0; c < 8; ++c)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int j = 0; j < MT; ++j) {
-          const float t = an[h] * xs[j];
-          acc[2 * e + h][0][j] = fmaf(t, cs[h].x, acc[2 * e + h][0][j]);
-          acc[2 * e + h][1][j] = fmaf(t, cs[h].y, acc[2 * e + h][1][j]);
-        }
-    }
+      for (int j = 0; j < MT; ++j) {
+        const float t = L.an[c] * xs[j];
+        acc[c][0][j] = fmaf(t, L.cs[c].x, acc[c][0][j]);
+        acc[c][1][j] = fmaf(t, L.cs[c].y, acc[c][1][j]);
+      }
   }
 }
 
@@ -207,15 +229,17 @@ __global__ __launch_bounds__(DKN_NT) void dual_kn_kernel(const DualKnArgs A) {
   const int64_t gw = (int64_t)uniform(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
   const int64_t nw = (int64_t)gridDim.x * WAVES;
   const int64_t items = A.nblk * A.slices;
-  // the first item's first loads travel while the tables are built
+  // the first item's first loads travel while the tables are built (1-2 tokens: with 4
+  // they would stay live through the build and spill)
+  constexpr bool early = MT <= 2;
   DknStep<MT> s0, s1;
   DknItem I = dkn_item(A, gw < items ? gw : 0, lane);
-  if (gw < items) dkn_issue<MT>(A, I.k0, I.k1, I.n, I.voff, s0);
+  if (early && gw < items) dkn_issue<MT>(A, I.k0, I.k1, I.n, I.voff, s0);
   if (A.luts.dtype == PP_F16) dkn_tables_of<LAYOUT, f16>(T, A.luts);
   else dkn_tables_of<LAYOUT, float>(T, A.luts);
   __syncthreads();
   for (int64_t it = gw; it < items; it += nw) {
-    if (it != gw) {
+    if (it != gw || !early) {
       I = dkn_item(A, it, lane);
       dkn_issue<MT>(A, I.k0, I.k1, I.n, I.voff, s0);
     }
