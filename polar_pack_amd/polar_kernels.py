@@ -127,10 +127,14 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
     pi, pa, pn, keep = _dual_plug(plug, dev)
     L = nat.lib()
     if M > FUSED_MAX_M:
-        w1, w2 = dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug=plug,
-                              elem_base=elem_base, layout=layout, chunk_size=chunk_size, dtype=torch.float16)
-        torch.matmul(a_fp16, w1, out=out1)
-        torch.matmul(a_fp16, w2, out=out2)
+        # decode along the storage: K-contiguous codes (container rows) into (N,K) weights,
+        # multiplied as their transpose; the kernel rule's groups need the (K,N) indices
+        nk = packed.stride(0) == 1 and packed.stride(1) != 1 and chunk_size > 0
+        w1, w2 = dual_dequant(packed.t() if nk else packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size,
+                              plug=plug, elem_base=elem_base, layout=layout, chunk_size=chunk_size,
+                              dtype=torch.float16)
+        torch.matmul(a_fp16, w1.t() if nk else w1, out=out1)
+        torch.matmul(a_fp16, w2.t() if nk else w2, out=out2)
         return out1, out2
     ws_bytes = L.pp_dual_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), packed.data_ptr(),
                                              packed.stride(0), packed.stride(1), group_size, chunk_size,

@@ -11,7 +11,7 @@ Same names, arguments, return values and error behaviour as the reference
   quaternion_packer.py:187-193) and ``elem_base``.
 * :func:`quad_dequant` -- float32 (or fp16) weights of a code view.
 
-Batches: 1-8 tokens run on the fused decode kernels; 9-256 tokens on the matrix-core
+Batches: 1-8 tokens run on the fused decode kernels; 9-128 tokens on the matrix-core
 decode when the codes are an (N,K) block seen as (K,N) (the container layout); larger
 batches, and more than 8 tokens on other layouts, decode once into fp16 weights (the
 values the reference's kernel rounds its weights to, quad_kernels.py:117-126) and run a
@@ -162,19 +162,23 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
     return outs
 
 
-PREFILL_M = 256   # batches above this decode once and run a library GEMM on every layout
+PREFILL_M = 128   # batches above this decode once and run a library GEMM on every layout
 
 
 def _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, elem_base, outs, L, dev):
-    """Decode into fp16 (K,N) weights s_m * W_m (plug applied), then 4 fp16 GEMMs."""
-    K, N = codes.shape
-    w = torch.empty((4, K, N), dtype=torch.float16, device=dev)
+    """Decode into fp16 weights s_m * W_m (plug applied), then 4 fp16 GEMMs.  The decode
+    follows the storage: codes with K contiguous (an (N,K) buffer seen as (K,N)) decode
+    into (N,K) weights, multiplied as their transpose, so both its reads and its writes
+    run along memory."""
+    view = codes.t() if codes.stride(0) == 1 and codes.stride(1) != 1 else codes
+    R, C = view.shape
+    w = torch.empty((4, R, C), dtype=torch.float16, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
-    rc = L.pp_quad_dequant_f16(codes.data_ptr(), codes.stride(0), codes.stride(1), lut_ptrs, lut_dtype, sc, pi, pv,
-                               pn, elem_base, nat.ptr_array([w[m].data_ptr() for m in range(4)]), N, K, stream)
+    rc = L.pp_quad_dequant_f16(view.data_ptr(), view.stride(0), view.stride(1), lut_ptrs, lut_dtype, sc, pi, pv, pn,
+                               elem_base, nat.ptr_array([w[m].data_ptr() for m in range(4)]), C, R, stream)
     nat.check(rc, "pp_quad_dequant_f16")
     for m in range(4):
-        torch.matmul(a, w[m], out=outs[m])
+        torch.matmul(a, w[m] if view is codes else w[m].t(), out=outs[m])
 
 
 def _mfma_layout_ok(codes, K):
