@@ -177,9 +177,11 @@ extern "C" int64_t pp_quad_gemm_workspace_size(const void* a, int64_t a_sm, int6
                                                int64_t K) {
   if (M <= 0 || N <= 0) return 0;
   if (quad_rows_ok(a, a_sm, a_sk, codes, c_sk, c_sn, M, N, K)) return quad_rows_workspace(M, N, plug_n);
-  // (K,N) codes: blocks of up to 4 tokens, one after another, sharing the workspace
-  if (quad_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, std::min<int64_t>(M, 4), N, K))
-    return quad_kn_workspace(std::min<int64_t>(M, 4), N, K, plug_n);
+  // (K,N) codes: blocks of up to 8 tokens, one after another, sharing the workspace (the
+  // last block may have 1..7 tokens: the larger of the 4- and 8-token needs covers it)
+  if (quad_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, std::min<int64_t>(M, 8), N, K))
+    return std::max(quad_kn_workspace(std::min<int64_t>(M, 8), N, K, plug_n),
+                    quad_kn_workspace(std::min<int64_t>(M, 4), N, K, plug_n));
   return 4 * N * K * (int64_t)sizeof(float);
 }
 
@@ -275,13 +277,13 @@ extern "C" int pp_quad_gemm(const void* a, int64_t a_sm, int64_t a_sk, const uin
   if (quad_rows_ok(a, a_sm, a_sk, codes, c_sk, c_sn, M, N, K))
     return quad_rows_single(a, a_sm, codes, c_sn, luts, lut_dtype, scales, plug_idx, plug_vals, plug_n, elem_base,
                             out, o_sm, o_sn, M, N, K, workspace, workspace_bytes, st);
-  if (quad_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, std::min<int64_t>(M, 4), N, K)) {
-    for (int64_t i0 = 0; i0 < M; i0 += 4) {
+  if (quad_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, std::min<int64_t>(M, 8), N, K)) {
+    for (int64_t i0 = 0; i0 < M; i0 += 8) {
       void* o[4];
       for (int m = 0; m < 4; ++m) o[m] = reinterpret_cast<f16*>(out[m]) + i0 * o_sm;
       if (int rc = quad_kn_gemm(reinterpret_cast<const f16*>(a) + i0 * a_sm, a_sm, codes, c_sk, luts, lut_dtype,
                                 scales, plug_idx, plug_vals, plug_n, elem_base, o, o_sm, o_sn,
-                                std::min<int64_t>(4, M - i0), N, K, workspace, workspace_bytes, st))
+                                std::min<int64_t>(8, M - i0), N, K, workspace, workspace_bytes, st))
         return rc;
     }
     return PP_OK;

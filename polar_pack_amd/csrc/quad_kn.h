@@ -6,7 +6,7 @@
 
 namespace pp {
 
-// True when quad_kn_gemm can serve this view for M (1..4) tokens: codes (K,N) with
+// True when quad_kn_gemm can serve this view for M (1..8) tokens: codes (K,N) with
 // c_sn == 1, rows of a multiple of 4 words, 16-byte aligned; N % 4 == 0, K % 8 == 0;
 // contiguous, 16-byte aligned fp16 activations.
 bool quad_kn_ok(const void* a, int64_t a_sm, int64_t a_sk, const uint32_t* codes, int64_t c_sk, int64_t c_sn,

@@ -1,6 +1,6 @@
 // Fused quad-pack decode GEMV for codes laid out (K,N) with unit column stride: the
 // layout pack_quad_layer returns (quad_kernels.py:35-37) and quad_bitpacked_kernel reads
-// (quad_kernels.py:53-143), for 1..4 tokens per launch.
+// (quad_kernels.py:53-143), for 1..8 tokens per launch.
 //
 //   out_m[j, n] = fp16( s_m * sum_k a[j, k] * W_m[k, n] ),   m = 0..3,
 //
@@ -20,7 +20,6 @@
 
 namespace pp {
 
-constexpr int KN_COLS = 256;   // columns per item: 64 lanes x 4
 constexpr int KN_R = 8;        // rows per step
 constexpr int KN_NT = 512;     // threads per workgroup (one per CU: the tables take all of LDS)
 
@@ -33,25 +32,34 @@ struct QuadKnArgs {
   int64_t o_sm, o_sn;
   int M, N, K;
   int slices, ks;          // K slices of ks rows (a multiple of KN_R)
-  int64_t nblk;            // ceil(N / KN_COLS)
+  int64_t nblk;            // ceil(N / (64 * columns per lane))
   QuadLuts luts;
   float s[4];
   float* part;             // partial sums [slice][4][M][N] (slices > 1 or plug), else null
 };
 
-template <int MT>
+// CL columns (code words) per lane and row: 4 (16-byte loads) for 1-4 tokens, 2 (8-byte
+// loads) for 8 tokens, where the accumulators of 4 columns would not fit in registers.
+template <int CL> struct KnVec;
+template <> struct KnVec<4> { typedef u32x4 T; };
+template <> struct KnVec<2> { typedef u32x2 T; };
+
+template <int MT, int CL>
 struct KnStep {
-  u32x4 q[KN_R];     // 4 words (columns) per row
-  u32x4 x[MT];       // 8 fp16 activations (the step's rows) per token
+  typename KnVec<CL>::T q[KN_R];   // CL words (columns) per row
+  u32x4 x[MT];                      // 8 fp16 activations (the step's rows) per token
 };
 
-template <int MT>
-__device__ __forceinline__ void kn_issue(const QuadKnArgs& A, int k, int kend, uint32_t voff, KnStep<MT>& S) {
+template <int MT, int CL>
+__device__ __forceinline__ void kn_issue(const QuadKnArgs& A, int k, int kend, uint32_t voff, KnStep<MT, CL>& S) {
   // rows [k, kend) of the slice: the resource ends at row kend, so rows past it read 0
   const int rows = max(0, kend - k);
   const rsrc_t rc = make_rsrc(A.codes + (int64_t)min(k, kend) * A.ldk, 4u * (uint32_t)((int64_t)rows * A.ldk));
 #pragma unroll
-  for (int r = 0; r < KN_R; ++r) vload128(S.q[r], voff + 4u * (uint32_t)(r * A.ldk), rc);
+  for (int r = 0; r < KN_R; ++r) {
+    if constexpr (CL == 4) vload128(S.q[r], voff + 4u * (uint32_t)(r * A.ldk), rc);
+    else S.q[r] = __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(voff + 4u * (uint32_t)(r * A.ldk)), 0, NT_AUX);
+  }
 #pragma unroll
   for (int j = 0; j < MT; ++j) {
     // 8 activations of the step's rows: past kend they read 0 (with the codes, they add 0)
@@ -66,24 +74,29 @@ struct KnTup {
   float2 a, b, c;
 };
 
-template <int MT, class L>
-__device__ __forceinline__ void kn_compute(const char* lds, const LaneOff& lo, const KnStep<MT>& S,
-                                           float (&acc)[4][4][MT]) {
-  float xv[MT][KN_R];
-#pragma unroll
-  for (int j = 0; j < MT; ++j) {
-    const f16x4 h0 = __builtin_bit_cast(f16x4, u32x2{S.x[j].x, S.x[j].y});
-    const f16x4 h1 = __builtin_bit_cast(f16x4, u32x2{S.x[j].z, S.x[j].w});
-    xv[j][0] = (float)h0.x; xv[j][1] = (float)h0.y; xv[j][2] = (float)h0.z; xv[j][3] = (float)h0.w;
-    xv[j][4] = (float)h1.x; xv[j][5] = (float)h1.y; xv[j][6] = (float)h1.z; xv[j][7] = (float)h1.w;
-  }
-  // tuple t = row r * 4 + column c; lookups two tuples ahead of the arithmetic
+// Activation of token j, row r of the step (fp16 -> float on use: 8 tokens' converted
+// rows would not fit in registers next to their accumulators).
+template <int MT>
+__device__ __forceinline__ float kn_x(const u32x4 (&x)[MT], int j, int r) {
+  const uint32_t w = r < 2 ? x[j].x : r < 4 ? x[j].y : r < 6 ? x[j].z : x[j].w;
+  return h2f((r & 1) ? (w >> 16) : (w & 0xFFFFu));
+}
+
+template <int MT, int CL, class L>
+__device__ __forceinline__ void kn_compute(const char* lds, const LaneOff& lo, const KnStep<MT, CL>& S,
+                                           float (&acc)[CL][4][MT]) {
+  // tuple t = row r * CL + column c; lookups two tuples ahead of the arithmetic
   auto word = [&](int t) -> uint32_t {
-    const u32x4& q = S.q[t / 4];
-    const int c = t % 4;
-    return c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w;
+    const int c = t % CL;
+    if constexpr (CL == 4) {
+      const u32x4& q = S.q[t / 4];
+      return c == 0 ? q.x : c == 1 ? q.y : c == 2 ? q.z : q.w;
+    } else {
+      const u32x2& q = S.q[t / 2];
+      return c == 0 ? q.x : q.y;
+    }
   };
-  constexpr int GT = 2, NTUP = KN_R * 4, NG = NTUP / GT;
+  constexpr int GT = 2, NTUP = KN_R * CL, NG = NTUP / GT;
   KnTup buf[2][GT];
 #pragma unroll
   for (int u = 0; u < GT; ++u) lookup<L>(lds, word(u), lo, buf[0][u].r, buf[0][u].a, buf[0][u].b, buf[0][u].c);
@@ -99,10 +112,10 @@ __device__ __forceinline__ void kn_compute(const char* lds, const LaneOff& lo, c
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < GT; ++u) {
-      const int t = g * GT + u, r = t / 4, c = t % 4;
+      const int t = g * GT + u, r = t / CL, c = t % CL;
       const KnTup& T = buf[g & 1][u];
       if constexpr (MT == 1) {
-        const float rx = T.r * xv[0][r];
+        const float rx = T.r * kn_x<MT>(S.x, 0, r);
         acc[c][0][0] = fmaf(rx, T.a.x, acc[c][0][0]);
         const float t1 = rx * T.a.y;
         acc[c][1][0] = fmaf(t1, T.b.x, acc[c][1][0]);
@@ -114,25 +127,28 @@ __device__ __forceinline__ void kn_compute(const char* lds, const LaneOff& lo, c
         const float rss = rs * T.b.y;
         const float w[4] = {T.r * T.a.x, rs * T.b.x, rss * T.c.x, rss * T.c.y};
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int j = 0; j < MT; ++j) {
+          const float xj = kn_x<MT>(S.x, j, r);
 #pragma unroll
-          for (int j = 0; j < MT; ++j) acc[c][m][j] = fmaf(w[m], xv[j][r], acc[c][m][j]);
+          for (int m = 0; m < 4; ++m) acc[c][m][j] = fmaf(w[m], xj, acc[c][m][j]);
+        }
       }
     }
   }
 }
 
-// A wave's item: its 256 columns and row slice.
+// A wave's item: its 64 * CL columns and row slice.
 struct KnItem {
   int n, k0, k1, sl;
   uint32_t voff;
 };
 
+template <int CL>
 __device__ __forceinline__ KnItem kn_item(const QuadKnArgs& A, int64_t it, int lane) {
   KnItem I;
   const int blk = (int)uniform64(it / A.slices);
   I.sl = (int)uniform64(it % A.slices);
-  I.n = blk * KN_COLS + 4 * lane;           // the lane's first column
+  I.n = blk * 64 * CL + CL * lane;          // the lane's first column
   I.k0 = I.sl * A.ks;
   I.k1 = min(A.K, I.k0 + A.ks);
   I.voff = I.n < A.N ? 4u * (uint32_t)I.n : OOB;
@@ -140,22 +156,22 @@ __device__ __forceinline__ KnItem kn_item(const QuadKnArgs& A, int64_t it, int l
 }
 
 // One item, its first step already issued into s0.
-template <int MT, class L>
+template <int MT, int CL, class L>
 __device__ __forceinline__ void kn_run(const char* lds, const LaneOff& lo, const QuadKnArgs& A, const KnItem& I,
-                                       KnStep<MT>& s0, KnStep<MT>& s1) {
-  float acc[4][4][MT];
+                                       KnStep<MT, CL>& s0, KnStep<MT, CL>& s1) {
+  float acc[CL][4][MT];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < CL; ++c)
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
       for (int j = 0; j < MT; ++j) acc[c][m][j] = 0.f;
   for (int k = I.k0; k < I.k1; k += 2 * KN_R) {
-    kn_issue<MT>(A, k + KN_R, I.k1, I.voff, s1);
-    kn_compute<MT, L>(lds, lo, s0, acc);
+    kn_issue<MT, CL>(A, k + KN_R, I.k1, I.voff, s1);
+    kn_compute<MT, CL, L>(lds, lo, s0, acc);
     if (k + KN_R >= I.k1) break;
-    kn_issue<MT>(A, k + 2 * KN_R, I.k1, I.voff, s0);
-    kn_compute<MT, L>(lds, lo, s1, acc);
+    kn_issue<MT, CL>(A, k + 2 * KN_R, I.k1, I.voff, s0);
+    kn_compute<MT, CL, L>(lds, lo, s1, acc);
   }
   const int n = I.n;
   if (A.part == nullptr) {
@@ -165,7 +181,7 @@ __device__ __forceinline__ void kn_run(const char* lds, const LaneOff& lo, const
 #pragma unroll
       for (int j = 0; j < MT; ++j)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < CL; ++c) {
           const f16 h = (f16)(acc[c][m][j] * A.s[m]);
           const bool ok = n + c < A.N && j < A.M;
           vstore16((uint32_t)__builtin_bit_cast(unsigned short, h),
@@ -173,15 +189,18 @@ __device__ __forceinline__ void kn_run(const char* lds, const LaneOff& lo, const
         }
     }
   } else {
-    // partials [sl][m][j][n .. n+3] as one 16-byte store (N % 4 == 0 on this path)
+    // partials [sl][m][j][n .. n+CL-1] as one 16- or 8-byte store (N % 4 == 0 on this path)
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
       for (int j = 0; j < MT; ++j)
         if (n < A.N && j < A.M) {
-          float4* p = reinterpret_cast<float4*>(A.part + (((int64_t)I.sl * 4 + m) * A.M + j) * A.N + n);
-          *p = make_float4(acc[0][m][j] * A.s[m], acc[1][m][j] * A.s[m], acc[2][m][j] * A.s[m],
-                           acc[3][m][j] * A.s[m]);
+          float* p = A.part + (((int64_t)I.sl * 4 + m) * A.M + j) * A.N + n;
+          if constexpr (CL == 4)
+            *reinterpret_cast<float4*>(p) = make_float4(acc[0][m][j] * A.s[m], acc[1][m][j] * A.s[m],
+                                                        acc[2][m][j] * A.s[m], acc[3][m][j] * A.s[m]);
+          else
+            *reinterpret_cast<float2*>(p) = make_float2(acc[0][m][j] * A.s[m], acc[1][m][j] * A.s[m]);
         }
   }
 }
@@ -190,21 +209,21 @@ __device__ __forceinline__ void kn_run(const char* lds, const LaneOff& lo, const
 template <int MT>
 constexpr bool kn_early() { return MT <= 2; }
 
-template <int MT, class L>
+template <int MT, int CL, class L>
 __device__ __forceinline__ void kn_items(const char* lds, const QuadKnArgs& A, int64_t gw, int64_t nw, int lane,
-                                         KnItem I, KnStep<MT>& s0, KnStep<MT>& s1) {
+                                         KnItem I, KnStep<MT, CL>& s0, KnStep<MT, CL>& s1) {
   const LaneOff lo = L::lane(lane);
   const int64_t items = A.nblk * A.slices;
   for (int64_t it = gw; it < items; it += nw) {
     if (it != gw || !kn_early<MT>()) {
-      I = kn_item(A, it, lane);
-      kn_issue<MT>(A, I.k0, I.k1, I.voff, s0);
+      I = kn_item<CL>(A, it, lane);
+      kn_issue<MT, CL>(A, I.k0, I.k1, I.voff, s0);
     }
-    kn_run<MT, L>(lds, lo, A, I, s0, s1);
+    kn_run<MT, CL, L>(lds, lo, A, I, s0, s1);
   }
 }
 
-template <int MT>
+template <int MT, int CL>
 __global__ __launch_bounds__(KN_NT) void quad_kn_kernel(const QuadKnArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t T[QLDS_BYTES / 4];
   const char* lds = reinterpret_cast<const char*>(T);
@@ -216,11 +235,11 @@ __global__ __launch_bounds__(KN_NT) void quad_kn_kernel(const QuadKnArgs A) {
   const int64_t nw = (int64_t)gridDim.x * WAVES;
   const int64_t items = A.nblk * A.slices;
   // the first item's first loads travel while the tables are built (1-2 tokens)
-  KnStep<MT> s0, s1;
-  const KnItem I = kn_item(A, gw < items ? gw : 0, lane);
-  if (kn_early<MT>() && gw < items) kn_issue<MT>(A, I.k0, I.k1, I.voff, s0);
-  if (quad_tables<KN_NT>(T, A.luts)) kn_items<MT, LayShared>(lds, A, gw, nw, lane, I, s0, s1);
-  else kn_items<MT, LaySplit>(lds, A, gw, nw, lane, I, s0, s1);
+  KnStep<MT, CL> s0, s1;
+  const KnItem I = kn_item<CL>(A, gw < items ? gw : 0, lane);
+  if (kn_early<MT>() && gw < items) kn_issue<MT, CL>(A, I.k0, I.k1, I.voff, s0);
+  if (quad_tables<KN_NT>(T, A.luts)) kn_items<MT, CL, LayShared>(lds, A, gw, nw, lane, I, s0, s1);
+  else kn_items<MT, CL, LaySplit>(lds, A, gw, nw, lane, I, s0, s1);
 }
 
 // Plug corrections, one entry per thread, added to slice 0's partial sums after the
@@ -320,9 +339,13 @@ struct KnPlan {
   int64_t nblk;
 };
 
-static KnPlan kn_plan(int64_t N, int64_t K) {
+// Columns per lane for a block of M tokens.
+static int kn_cl(int64_t M) { return M <= 4 ? 4 : 2; }
+
+static KnPlan kn_plan(int64_t M, int64_t N, int64_t K) {
   KnPlan p;
-  p.nblk = (N + KN_COLS - 1) / KN_COLS;
+  const int64_t cols = 64 * kn_cl(M);
+  p.nblk = (N + cols - 1) / cols;
   const int64_t waves = (int64_t)device_cu_count() * (KN_NT / 64);
   // about one item per wavefront, slices of at least PP_KN_MIN_ROWS rows
   int64_t s = std::max<int64_t>(
@@ -336,13 +359,13 @@ static KnPlan kn_plan(int64_t N, int64_t K) {
 
 bool quad_kn_ok(const void* a, int64_t a_sm, int64_t a_sk, const uint32_t* codes, int64_t c_sk, int64_t c_sn,
                 int64_t M, int64_t N, int64_t K) {
-  return c_sn == 1 && c_sk >= N && c_sk % 4 == 0 && N % 4 == 0 && N > 0 && K > 0 && K % 8 == 0 && M >= 1 && M <= 4 &&
+  return c_sn == 1 && c_sk >= N && c_sk % 4 == 0 && N % 4 == 0 && N > 0 && K > 0 && K % 8 == 0 && M >= 1 && M <= 8 &&
          aligned(codes, 16) && a_sk == 1 && (M == 1 || a_sm % 8 == 0) && aligned(a, 16) &&
          K < (1ll << 30) && c_sk * K < (1ll << 30);
 }
 
 int64_t quad_kn_workspace(int64_t M, int64_t N, int64_t K, int64_t plug_n) {
-  const KnPlan p = kn_plan(N, K);
+  const KnPlan p = kn_plan(M, N, K);
   if (p.slices == 1 && plug_n == 0) return 0;
   return (int64_t)p.slices * 4 * M * N * (int64_t)sizeof(float);
 }
@@ -351,7 +374,7 @@ int quad_kn_gemm(const void* a, int64_t a_sm, const uint32_t* codes, int64_t ldk
                  int lut_dtype, const float* scales, const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n,
                  int64_t elem_base, void* const* out, int64_t o_sm, int64_t o_sn, int64_t M, int64_t N, int64_t K,
                  void* workspace, int64_t workspace_bytes, hipStream_t st) {
-  const KnPlan p = kn_plan(N, K);
+  const KnPlan p = kn_plan(M, N, K);
   const int64_t need = quad_kn_workspace(M, N, K, plug_n);
   PP_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), "workspace too small: need %lld bytes",
              (long long)need);
@@ -377,10 +400,11 @@ int quad_kn_gemm(const void* a, int64_t a_sm, const uint32_t* codes, int64_t ldk
   A.part = need > 0 ? reinterpret_cast<float*>(workspace) : nullptr;
   const int64_t items = p.nblk * p.slices;
   const unsigned grid = (unsigned)std::min<int64_t>(device_cu_count(), (items + KN_NT / 64 - 1) / (KN_NT / 64));
-  switch (M <= 1 ? 1 : M <= 2 ? 2 : 4) {
-    case 1: hipLaunchKernelGGL(quad_kn_kernel<1>, dim3(grid), dim3(KN_NT), 0, st, A); break;
-    case 2: hipLaunchKernelGGL(quad_kn_kernel<2>, dim3(grid), dim3(KN_NT), 0, st, A); break;
-    default: hipLaunchKernelGGL(quad_kn_kernel<4>, dim3(grid), dim3(KN_NT), 0, st, A); break;
+  switch (M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8) {
+    case 1: hipLaunchKernelGGL((quad_kn_kernel<1, 4>), dim3(grid), dim3(KN_NT), 0, st, A); break;
+    case 2: hipLaunchKernelGGL((quad_kn_kernel<2, 4>), dim3(grid), dim3(KN_NT), 0, st, A); break;
+    case 4: hipLaunchKernelGGL((quad_kn_kernel<4, 4>), dim3(grid), dim3(KN_NT), 0, st, A); break;
+    default: hipLaunchKernelGGL((quad_kn_kernel<8, 2>), dim3(grid), dim3(KN_NT), 0, st, A); break;
   }
   PP_LAUNCH_CHECK();
   if (A.part != nullptr) {

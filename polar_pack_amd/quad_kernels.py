@@ -11,9 +11,10 @@ Same names, arguments, return values and error behaviour as the reference
   quaternion_packer.py:187-193) and ``elem_base``.
 * :func:`quad_dequant` -- float32 (or fp16) weights of a code view.
 
-Batches: 1-8 tokens run on the fused decode kernels; 9-128 tokens on the matrix-core
-decode when the codes are an (N,K) block seen as (K,N) (the container layout); larger
-batches, and more than 8 tokens on other layouts, decode once into fp16 weights (the
+Batches: 1-8 tokens run on the fused decode kernels (16 in two passes on (K,N) storage);
+9-128 tokens on the matrix-core decode when the codes are an (N,K) block seen as (K,N)
+(the container layout); larger batches, and more tokens on other layouts, decode once
+into fp16 weights (the
 values the reference's kernel rounds its weights to, quad_kernels.py:117-126) and run a
 library fp16 GEMM (hipBLASLt through torch.matmul), where the matmul's compute, not the
 weight stream, bounds the time.
@@ -135,11 +136,12 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
     sc = nat.float_array(scales)
     pi, pv, pn, keep = _plug_args(plug, dev)
     L = nat.lib()
-    if M > PREFILL_M or (M > 8 and not _mfma_layout_ok(codes, K)):
+    kn = _kn_layout_ok(codes, K, N)
+    if M > PREFILL_M or (M > 8 and not _mfma_layout_ok(codes, K) and not (kn and M <= KN_MAX_M)):
         _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base), outs, L, dev)
         del keep
         return outs
-    if M > 8:
+    if M > 8 and not kn:
         # the matrix-core path takes up to 64 tokens per launch: larger batches (the
         # reference's prefill sizes, quad_kernels.py:166-189) run in blocks of 64 rows
         for i0 in range(0, M, 64):
@@ -147,7 +149,7 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
             _quad_mfma(a[i0:i1], codes, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base),
                        [o[i0:i1] for o in outs], L, dev)
         return outs
-    if a.stride(1) != 1 or a.data_ptr() % 8 or (M > 1 and a.stride(0) % 4):
+    if a.stride(1) != 1 or a.data_ptr() % 16 or (M > 1 and a.stride(0) % 8):
         a = a.contiguous()
     ws_bytes = L.pp_quad_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), codes.data_ptr(),
                                              codes.stride(0), codes.stride(1), pn, M, N, K)
@@ -163,6 +165,14 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
 
 
 PREFILL_M = 128   # batches above this decode once and run a library GEMM on every layout
+KN_MAX_M = 16     # (K,N) storage: up to two 8-token passes of the fused kernel, then the GEMM
+
+
+def _kn_layout_ok(codes, K, N):
+    """Codes (K,N) with unit column stride (as pack_quad_layer returns): the fused (K,N)
+    kernel's layout."""
+    return codes.stride(1) == 1 and codes.stride(0) >= N and codes.stride(0) % 4 == 0 and N % 4 == 0 \
+        and K % 8 == 0 and codes.data_ptr() % 16 == 0
 
 
 def _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, elem_base, outs, L, dev):

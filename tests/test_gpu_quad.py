@@ -118,7 +118,8 @@ def test_quad_gemm_matches_oracle(K, N, layout, M):
     # product (as the reference's tl.dot); held to the fp16-rounded decode + the fp32
     # dot-product bound (see test_gpu_mfma.py)
     mfma = M > 8 and layout == "nk" and K % 32 == 0
-    prefill = M > 8 and not mfma                 # fp16 decode + library GEMM
+    kn = layout == "kn" and N % 4 == 0 and K % 8 == 0 and M <= qk.KN_MAX_M   # fused (K,N) passes
+    prefill = M > 8 and not mfma and not kn      # fp16 decode + library GEMM
     W32 = olay.quad_dequant(codes, [l.float().numpy() for l in luts], dtype=np.float32) if mfma else None
     for k in range(4):
         assert outs[k].shape == (M, N) and outs[k].dtype == torch.float16
@@ -223,12 +224,13 @@ def test_pack_quad_layer_on_gpu_matches_oracle():
         np.testing.assert_array_equal(luts[i].cpu().numpy().view(np.uint16), rl[i].view(np.uint16))
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 6])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6, 8, 13])
 @pytest.mark.parametrize("K,N,plug", [(2048, 1000, 0), (2048, 1000, 700), (64, 96, 0), (520, 4096, 300)])
 def test_quad_gemm_kn_layout_fast_path(K, N, plug, M):
     """Contiguous (K,N) codes, the layout pack_quad_layer returns: the fused (K,N) kernel
-    (256-column items, K slices whose partial sums a finish pass adds, plug corrections
-    per entry; blocks of 4 tokens), against the float64 oracle."""
+    (256-column items for 1-4 tokens, 128-column items for 5-8, K slices whose partial
+    sums a finish pass adds, plug corrections per entry; blocks of 8 tokens), against the
+    float64 oracle."""
     seed = K + N + plug + M
     codes = random_codes((K, N), seed)
     luts, scales = fp16_luts(seed)
