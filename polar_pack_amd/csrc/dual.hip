@@ -14,7 +14,7 @@
 //                         per 8 pairs (x * amp_lut, then 2 fma per pair).  Plug entries
 //                         replace the amplitude as exact corrections.
 //   dual_kn_gemm       -- (dual_kn.hip) codes (K,N) with unit column stride, the layout
-//                         quantize_polar_bitpacked returns, in blocks of up to 4 tokens.
+//                         quantize_polar_bitpacked returns, in blocks of up to 8 tokens.
 //   dual_dequant_kernel / dual_plug_scatter_kernel / dual_ws_gemm_kernel -- generic path
 //                         and parity export (any strides, both group-index modes).
 #include "dual_kn.h"
@@ -549,9 +549,11 @@ extern "C" int64_t pp_dual_gemm_workspace_size(const void* a, int64_t a_sm, int6
   if (M <= 0 || N <= 0) return 0;
   if (dual_fast_ok(a, a_sm, a_sk, codes, c_sk, c_sn, elem_base, chunk_size, group_size, M, K))
     return dual_plan(M, N, K, plug_n).total();
-  // (K,N) codes: blocks of up to 4 tokens, one after another, sharing the workspace
-  if (dual_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, group_size, chunk_size, std::min<int64_t>(M, 4), N, K))
-    return dual_kn_workspace(std::min<int64_t>(M, 4), N, K, plug_n);
+  // (K,N) codes: blocks of up to 8 tokens, one after another, sharing the workspace (the
+  // last block may have 1..7 tokens: the larger of the 4- and 8-token needs covers it)
+  if (dual_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, group_size, chunk_size, std::min<int64_t>(M, 8), N, K))
+    return std::max(dual_kn_workspace(std::min<int64_t>(M, 8), N, K, plug_n),
+                    dual_kn_workspace(std::min<int64_t>(M, 4), N, K, plug_n));
   return 2 * N * K * (int64_t)sizeof(float);
 }
 
@@ -702,12 +704,12 @@ extern "C" int pp_dual_gemm(const void* a, int64_t a_sm, int64_t a_sk, const voi
     return code_layout == PP_DUAL_U16_BE ? dispatch_dual_rows<PP_DUAL_U16_BE>(A, mt, st)
                                          : dispatch_dual_rows<PP_DUAL_I16_OFFSET>(A, mt, st);
   }
-  if (dual_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, group_size, chunk_size, std::min<int64_t>(M, 4), N, K)) {
-    for (int64_t i0 = 0; i0 < M; i0 += 4) {
+  if (dual_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, group_size, chunk_size, std::min<int64_t>(M, 8), N, K)) {
+    for (int64_t i0 = 0; i0 < M; i0 += 8) {
       void* o[2] = {reinterpret_cast<f16*>(out1) + i0 * o_sm, reinterpret_cast<f16*>(out2) + i0 * o_sm};
       if (int rc = dual_kn_gemm(reinterpret_cast<const f16*>(a) + i0 * a_sm, a_sm, codes, code_layout, c_sk, bmax,
                                 group_size, L, plug_idx, plug_amp, plug_n, elem_base, o, o_sm, o_sn,
-                                std::min<int64_t>(4, M - i0), N, K, workspace, workspace_bytes, st))
+                                std::min<int64_t>(8, M - i0), N, K, workspace, workspace_bytes, st))
         return rc;
     }
     return PP_OK;

@@ -8,7 +8,7 @@ namespace pp {
 
 struct DualLuts;
 
-// True when dual_kn_gemm can serve this view for M (1..4) tokens: codes (K,N) with
+// True when dual_kn_gemm can serve this view for M (1..8) tokens: codes (K,N) with
 // c_sn == 1, rows of a multiple of 8 codes, 16-byte aligned; N % 8 == 0, K % 8 == 0;
 // groups by the kernel rule (k*N + n) / gs (chunk_size 0) with gs a power of two >= 8;
 // contiguous, 16-byte aligned fp16 activations.

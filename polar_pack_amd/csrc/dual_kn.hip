@@ -1,13 +1,14 @@
 // Fused dual-pack decode GEMV for codes laid out (K,N) with unit column stride: the
 // layout quantize_polar_bitpacked returns (polar_kernels.py:118-140) and
-// polar_dual_bitpacked_kernel reads (polar_kernels.py:27-95), for 1..4 tokens per launch.
+// polar_dual_bitpacked_kernel reads (polar_kernels.py:27-95), for 1..8 tokens per launch.
 //
 //   out_m[j, n] = fp16( sum_k a[j, k] * W_m[k, n] ),   m = 1, 2,
 //   W_1 = amp cos_lut[phase],  W_2 = amp sin_lut[phase],
 //   amp = amp_lut[amp_q] * bmax[(k*N + n) / gs]            (polar_kernels.py:64-79)
 //
 // with the LDS tables of dual_lds.h.  Work item = 512 columns x one slice of rows, one
-// wavefront: lane l owns columns n0 + 8l .. +7 (one 16-byte load per row), 8 rows per step,
+// wavefront: lane l owns columns n0 + 8l .. +7 (one 16-byte load per row; 8 tokens: 256
+// columns, 4 per lane, so the accumulators fit in registers), 8 rows per step,
 // the next step's loads in flight while one is decoded.  The 8 codes of a lane and row
 // share one group scale (gs is a power of two >= 8 and N % 8 == 0, so (k*N + n) / gs is
 // the same for the 8 columns), one 2-byte load per row; the activations of a row are the
@@ -22,7 +23,6 @@
 
 namespace pp {
 
-constexpr int DKN_COLS = 512;  // columns per item: 64 lanes x 8
 constexpr int DKN_R = 8;       // rows per step
 constexpr int DKN_NT = 512;    // threads per workgroup (one per CU: the tables take most of LDS)
 
@@ -35,7 +35,7 @@ struct DualKnArgs {
   int64_t o_sm, o_sn;
   int M, N, K;
   int slices, ks;          // K slices of ks rows (a multiple of DKN_R)
-  int64_t nblk;            // ceil(N / DKN_COLS)
+  int64_t nblk;            // ceil(N / (64 * codes per lane))
   const f16* scales;       // bmax, one per group of gs consecutive (k*N + n)
   int64_t n_groups;
   int log2gs;
@@ -69,25 +69,34 @@ __device__ __forceinline__ void dkn_tables_of(char* lds, const DualLuts& L) {
     *reinterpret_cast<float4*>(lds + DLDS_CS + 16 * (threadIdx.x + k * DKN_NT)) = make_float4(c[k], s[k], c[k], s[k]);
 }
 
-template <int MT>
+// CL codes (columns) per lane and row: 8 (16-byte loads) for 1-4 tokens, 4 (8-byte
+// loads) for 8 tokens, where the accumulators of 8 columns would not fit in registers.
+template <int CL> struct DknVec;
+template <> struct DknVec<8> { typedef u32x4 T; };
+template <> struct DknVec<4> { typedef u32x2 T; };
+
+template <int MT, int CL>
 struct DknStep {
-  u32x4 q[DKN_R];        // 8 codes (columns) per row
-  uint32_t sc[DKN_R];    // their group scale (fp16 bits)
-  u32x4 x[MT];           // 8 fp16 activations (the step's rows) per token
+  typename DknVec<CL>::T q[DKN_R];   // CL codes (columns) per row
+  uint32_t sc[DKN_R];                 // their group scale (fp16 bits)
+  u32x4 x[MT];                        // 8 fp16 activations (the step's rows) per token
 };
 
-template <int MT>
+template <int MT, int CL>
 __device__ __forceinline__ void dkn_issue(const DualKnArgs& A, int k, int kend, int n, uint32_t voff,
-                                          DknStep<MT>& S) {
+                                          DknStep<MT, CL>& S) {
   // rows [k, kend) of the slice: the resource ends at row kend, so rows past it read 0
   const int rows = max(0, kend - k);
   const rsrc_t rc = make_rsrc(A.codes + (int64_t)min(k, kend) * A.ldk, 2u * (uint32_t)((int64_t)rows * A.ldk));
 #pragma unroll
-  for (int r = 0; r < DKN_R; ++r) vload128(S.q[r], voff + 2u * (uint32_t)(r * A.ldk), rc);
+  for (int r = 0; r < DKN_R; ++r) {
+    if constexpr (CL == 8) vload128(S.q[r], voff + 2u * (uint32_t)(r * A.ldk), rc);
+    else S.q[r] = __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(voff + 2u * (uint32_t)(r * A.ldk)), 0, NT_AUX);
+  }
   const rsrc_t rs = make_rsrc(A.scales, 2u * (uint32_t)A.n_groups);
 #pragma unroll
   for (int r = 0; r < DKN_R; ++r) {
-    // group of (k + r, n .. n+7); K*N < 2^32 on this path
+    // group of (k + r, n .. n+CL-1); K*N < 2^32 on this path
     const uint32_t p = (uint32_t)(k + r) * (uint32_t)A.N + (uint32_t)n;
     vload16(S.sc[r], r < rows && n < A.N ? 2u * (p >> A.log2gs) : OOB, rs);
   }
@@ -99,20 +108,21 @@ __device__ __forceinline__ void dkn_issue(const DualKnArgs& A, int k, int kend, 
   }
 }
 
-// Table entries of one row's 8 codes.
+// Table entries of one row's CL codes.
+template <int CL>
 struct DknRowLk {
-  float an[8];
-  float2 cs[8];
+  float an[CL];
+  float2 cs[CL];
 };
 
-template <int LAYOUT>
-__device__ __forceinline__ void dkn_lookup_row(const char* lds, const DualLane& lo, const u32x4& q, DknRowLk& L) {
-  const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+template <int LAYOUT, int CL>
+__device__ __forceinline__ void dkn_lookup_row(const char* lds, const DualLane& lo,
+                                               const typename DknVec<CL>::T& q, DknRowLk<CL>& L) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int e = 0; e < CL / 2; ++e) {
     float an[2];
     float2 cs[2];
-    dual_lookup2<LAYOUT>(lds, w4[e], lo, an, cs);
+    dual_lookup2<LAYOUT>(lds, q[e], lo, an, cs);
     L.an[2 * e] = an[0];
     L.an[2 * e + 1] = an[1];
     L.cs[2 * e] = cs[0];
@@ -120,33 +130,32 @@ __device__ __forceinline__ void dkn_lookup_row(const char* lds, const DualLane& 
   }
 }
 
+// Activation of token j, row r of the step, converted on use.
+template <int MT>
+__device__ __forceinline__ float dkn_x(const u32x4 (&x)[MT], int j, int r) {
+  const uint32_t w = r < 2 ? x[j].x : r < 4 ? x[j].y : r < 6 ? x[j].z : x[j].w;
+  return h2f((r & 1) ? (w >> 16) : (w & 0xFFFFu));
+}
+
 // The lookups of row r + 1 are issued before the arithmetic of row r (the barrier keeps
 // the compiler from moving them back behind it), so a wave has a row of LDS reads in
 // flight while it multiplies.
-template <int MT, int LAYOUT>
-__device__ __forceinline__ void dkn_compute(const char* lds, const DualLane& lo, const DknStep<MT>& S,
-                                            float (&acc)[8][2][MT]) {
-  float xv[MT][DKN_R];
-#pragma unroll
-  for (int j = 0; j < MT; ++j) {
-    const f16x4 h0 = __builtin_bit_cast(f16x4, u32x2{S.x[j].x, S.x[j].y});
-    const f16x4 h1 = __builtin_bit_cast(f16x4, u32x2{S.x[j].z, S.x[j].w});
-    xv[j][0] = (float)h0.x; xv[j][1] = (float)h0.y; xv[j][2] = (float)h0.z; xv[j][3] = (float)h0.w;
-    xv[j][4] = (float)h1.x; xv[j][5] = (float)h1.y; xv[j][6] = (float)h1.z; xv[j][7] = (float)h1.w;
-  }
-  DknRowLk buf[2];
-  dkn_lookup_row<LAYOUT>(lds, lo, S.q[0], buf[0]);
+template <int MT, int CL, int LAYOUT>
+__device__ __forceinline__ void dkn_compute(const char* lds, const DualLane& lo, const DknStep<MT, CL>& S,
+                                            float (&acc)[CL][2][MT]) {
+  DknRowLk<CL> buf[2];
+  dkn_lookup_row<LAYOUT, CL>(lds, lo, S.q[0], buf[0]);
 #pragma unroll
   for (int r = 0; r < DKN_R; ++r) {
-    if (r + 1 < DKN_R) dkn_lookup_row<LAYOUT>(lds, lo, S.q[r + 1], buf[(r + 1) & 1]);
+    if (r + 1 < DKN_R) dkn_lookup_row<LAYOUT, CL>(lds, lo, S.q[r + 1], buf[(r + 1) & 1]);
     __builtin_amdgcn_sched_barrier(0);
-    const DknRowLk& L = buf[r & 1];
+    const DknRowLk<CL>& L = buf[r & 1];
     const float sc = h2f(S.sc[r]);
     float xs[MT];
 #pragma unroll
-    for (int j = 0; j < MT; ++j) xs[j] = xv[j][r] * sc;
+    for (int j = 0; j < MT; ++j) xs[j] = dkn_x<MT>(S.x, j, r) * sc;
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+    for (int c = 0; c < CL; ++c)
 #pragma unroll
       for (int j = 0; j < MT; ++j) {
         const float t = L.an[c] * xs[j];
@@ -156,17 +165,18 @@ __device__ __forceinline__ void dkn_compute(const char* lds, const DualLane& lo,
   }
 }
 
-// A wave's item: its 512 columns and row slice.
+// A wave's item: its 64 * CL columns and row slice.
 struct DknItem {
   int n, k0, k1, sl;
   uint32_t voff;
 };
 
+template <int CL>
 __device__ __forceinline__ DknItem dkn_item(const DualKnArgs& A, int64_t it, int lane) {
   DknItem I;
   const int blk = (int)uniform64(it / A.slices);
   I.sl = (int)uniform64(it % A.slices);
-  I.n = blk * DKN_COLS + 8 * lane;          // the lane's first column
+  I.n = blk * 64 * CL + CL * lane;          // the lane's first column
   I.k0 = I.sl * A.ks;
   I.k1 = min(A.K, I.k0 + A.ks);
   I.voff = I.n < A.N ? 2u * (uint32_t)I.n : OOB;
@@ -174,20 +184,20 @@ __device__ __forceinline__ DknItem dkn_item(const DualKnArgs& A, int64_t it, int
 }
 
 // One item, its first step already issued into s0.
-template <int MT, int LAYOUT>
+template <int MT, int CL, int LAYOUT>
 __device__ __forceinline__ void dkn_run(const char* lds, const DualLane& lo, const DualKnArgs& A, const DknItem& I,
-                                        DknStep<MT>& s0, DknStep<MT>& s1) {
-  float acc[8][2][MT];
+                                        DknStep<MT, CL>& s0, DknStep<MT, CL>& s1) {
+  float acc[CL][2][MT];
 #pragma unroll
-  for (int c = 0; c < 8; ++c)
+  for (int c = 0; c < CL; ++c)
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[c][0][j] = acc[c][1][j] = 0.f;
   for (int k = I.k0; k < I.k1; k += 2 * DKN_R) {
-    dkn_issue<MT>(A, k + DKN_R, I.k1, I.n, I.voff, s1);
-    dkn_compute<MT, LAYOUT>(lds, lo, s0, acc);
+    dkn_issue<MT, CL>(A, k + DKN_R, I.k1, I.n, I.voff, s1);
+    dkn_compute<MT, CL, LAYOUT>(lds, lo, s0, acc);
     if (k + DKN_R >= I.k1) break;
-    dkn_issue<MT>(A, k + 2 * DKN_R, I.k1, I.n, I.voff, s0);
-    dkn_compute<MT, LAYOUT>(lds, lo, s1, acc);
+    dkn_issue<MT, CL>(A, k + 2 * DKN_R, I.k1, I.n, I.voff, s0);
+    dkn_compute<MT, CL, LAYOUT>(lds, lo, s1, acc);
   }
   const int n = I.n;
   if (A.part == nullptr) {
@@ -197,7 +207,7 @@ __device__ __forceinline__ void dkn_run(const char* lds, const DualLane& lo, con
 #pragma unroll
       for (int j = 0; j < MT; ++j)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int c = 0; c < CL; ++c) {
           const f16 h = (f16)acc[c][m][j];
           const bool ok = n + c < A.N && j < A.M;
           vstore16((uint32_t)__builtin_bit_cast(unsigned short, h),
@@ -205,20 +215,21 @@ __device__ __forceinline__ void dkn_run(const char* lds, const DualLane& lo, con
         }
     }
   } else {
-    // partials [sl][m][j][n .. n+7] as two 16-byte stores (N % 8 == 0 on this path)
+    // partials [sl][m][j][n .. n+CL-1] as 16-byte stores (N % 8 == 0 on this path)
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
       for (int j = 0; j < MT; ++j)
         if (n < A.N && j < A.M) {
           float4* p = reinterpret_cast<float4*>(A.part + (((int64_t)I.sl * 2 + m) * A.M + j) * A.N + n);
-          p[0] = make_float4(acc[0][m][j], acc[1][m][j], acc[2][m][j], acc[3][m][j]);
-          p[1] = make_float4(acc[4][m][j], acc[5][m][j], acc[6][m][j], acc[7][m][j]);
+#pragma unroll
+          for (int h = 0; h < CL / 4; ++h)
+            p[h] = make_float4(acc[4 * h][m][j], acc[4 * h + 1][m][j], acc[4 * h + 2][m][j], acc[4 * h + 3][m][j]);
         }
   }
 }
 
-template <int MT, int LAYOUT>
+template <int MT, int CL, int LAYOUT>
 __global__ __launch_bounds__(DKN_NT) void dual_kn_kernel(const DualKnArgs A) {
   __shared__ __attribute__((aligned(16))) char T[DLDS_BYTES];
   constexpr int WAVES = DKN_NT / 64;
@@ -229,21 +240,21 @@ __global__ __launch_bounds__(DKN_NT) void dual_kn_kernel(const DualKnArgs A) {
   const int64_t gw = (int64_t)uniform(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
   const int64_t nw = (int64_t)gridDim.x * WAVES;
   const int64_t items = A.nblk * A.slices;
-  // the first item's first loads travel while the tables are built (1-2 tokens: with 4
-  // they would stay live through the build and spill)
+  // the first item's first loads travel while the tables are built (1-2 tokens: with
+  // more they would stay live through the build and spill)
   constexpr bool early = MT <= 2;
-  DknStep<MT> s0, s1;
-  DknItem I = dkn_item(A, gw < items ? gw : 0, lane);
-  if (early && gw < items) dkn_issue<MT>(A, I.k0, I.k1, I.n, I.voff, s0);
+  DknStep<MT, CL> s0, s1;
+  DknItem I = dkn_item<CL>(A, gw < items ? gw : 0, lane);
+  if (early && gw < items) dkn_issue<MT, CL>(A, I.k0, I.k1, I.n, I.voff, s0);
   if (A.luts.dtype == PP_F16) dkn_tables_of<LAYOUT, f16>(T, A.luts);
   else dkn_tables_of<LAYOUT, float>(T, A.luts);
   __syncthreads();
   for (int64_t it = gw; it < items; it += nw) {
     if (it != gw || !early) {
-      I = dkn_item(A, it, lane);
-      dkn_issue<MT>(A, I.k0, I.k1, I.n, I.voff, s0);
+      I = dkn_item<CL>(A, it, lane);
+      dkn_issue<MT, CL>(A, I.k0, I.k1, I.n, I.voff, s0);
     }
-    dkn_run<MT, LAYOUT>(T, lo, A, I, s0, s1);
+    dkn_run<MT, CL, LAYOUT>(T, lo, A, I, s0, s1);
   }
 }
 
@@ -333,9 +344,13 @@ struct DknPlan {
   int64_t nblk;
 };
 
-static DknPlan dkn_plan(int64_t N, int64_t K) {
+// Codes (columns) per lane for a block of M tokens.
+static int dkn_cl(int64_t M) { return M <= 4 ? 8 : 4; }
+
+static DknPlan dkn_plan(int64_t M, int64_t N, int64_t K) {
   DknPlan p;
-  p.nblk = (N + DKN_COLS - 1) / DKN_COLS;
+  const int64_t cols = 64 * dkn_cl(M);
+  p.nblk = (N + cols - 1) / cols;
   const int64_t waves = (int64_t)device_cu_count() * (DKN_NT / 64);
   // about one item per wavefront, slices of at least PP_DKN_MIN_ROWS rows
   int64_t s = std::max<int64_t>(
@@ -350,13 +365,13 @@ static DknPlan dkn_plan(int64_t N, int64_t K) {
 bool dual_kn_ok(const void* a, int64_t a_sm, int64_t a_sk, const void* codes, int64_t c_sk, int64_t c_sn,
                 int64_t group_size, int64_t chunk_size, int64_t M, int64_t N, int64_t K) {
   return c_sn == 1 && c_sk >= N && c_sk % 8 == 0 && N % 8 == 0 && N > 0 && K > 0 && K % 8 == 0 && M >= 1 &&
-         M <= 4 && aligned(codes, 16) && chunk_size == 0 && group_size >= 8 && (group_size & (group_size - 1)) == 0 &&
+         M <= 8 && aligned(codes, 16) && chunk_size == 0 && group_size >= 8 && (group_size & (group_size - 1)) == 0 &&
          a_sk == 1 && (M == 1 || a_sm % 8 == 0) && aligned(a, 16) && K * N < (1ll << 32) &&
          2 * c_sk * K < (1ll << 31);
 }
 
 int64_t dual_kn_workspace(int64_t M, int64_t N, int64_t K, int64_t plug_n) {
-  const DknPlan p = dkn_plan(N, K);
+  const DknPlan p = dkn_plan(M, N, K);
   if (p.slices == 1 && plug_n == 0) return 0;
   return (int64_t)p.slices * 2 * M * N * (int64_t)sizeof(float);
 }
@@ -365,7 +380,7 @@ int dual_kn_gemm(const void* a, int64_t a_sm, const void* codes, int code_layout
                  int64_t group_size, const DualLuts& luts, const uint32_t* plug_idx, const void* plug_amp,
                  int64_t plug_n, int64_t elem_base, void* const* out, int64_t o_sm, int64_t o_sn, int64_t M,
                  int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, hipStream_t st) {
-  const DknPlan p = dkn_plan(N, K);
+  const DknPlan p = dkn_plan(M, N, K);
   const int64_t need = dual_kn_workspace(M, N, K, plug_n);
   PP_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), "workspace too small: need %lld bytes",
              (long long)need);
@@ -393,13 +408,15 @@ int dual_kn_gemm(const void* a, int64_t a_sm, const void* codes, int code_layout
   const int64_t items = p.nblk * p.slices;
   const unsigned grid = (unsigned)std::min<int64_t>(device_cu_count(), (items + DKN_NT / 64 - 1) / (DKN_NT / 64));
   const bool be = code_layout == PP_DUAL_U16_BE;
-  switch ((M <= 1 ? 1 : M <= 2 ? 2 : 4) * 2 + (be ? 1 : 0)) {
-    case 2: hipLaunchKernelGGL((dual_kn_kernel<1, PP_DUAL_I16_OFFSET>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
-    case 3: hipLaunchKernelGGL((dual_kn_kernel<1, PP_DUAL_U16_BE>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
-    case 4: hipLaunchKernelGGL((dual_kn_kernel<2, PP_DUAL_I16_OFFSET>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
-    case 5: hipLaunchKernelGGL((dual_kn_kernel<2, PP_DUAL_U16_BE>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
-    case 8: hipLaunchKernelGGL((dual_kn_kernel<4, PP_DUAL_I16_OFFSET>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
-    default: hipLaunchKernelGGL((dual_kn_kernel<4, PP_DUAL_U16_BE>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+  switch ((M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8) * 2 + (be ? 1 : 0)) {
+    case 2: hipLaunchKernelGGL((dual_kn_kernel<1, 8, PP_DUAL_I16_OFFSET>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    case 3: hipLaunchKernelGGL((dual_kn_kernel<1, 8, PP_DUAL_U16_BE>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    case 4: hipLaunchKernelGGL((dual_kn_kernel<2, 8, PP_DUAL_I16_OFFSET>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    case 5: hipLaunchKernelGGL((dual_kn_kernel<2, 8, PP_DUAL_U16_BE>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    case 8: hipLaunchKernelGGL((dual_kn_kernel<4, 8, PP_DUAL_I16_OFFSET>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    case 9: hipLaunchKernelGGL((dual_kn_kernel<4, 8, PP_DUAL_U16_BE>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    case 16: hipLaunchKernelGGL((dual_kn_kernel<8, 4, PP_DUAL_I16_OFFSET>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
+    default: hipLaunchKernelGGL((dual_kn_kernel<8, 4, PP_DUAL_U16_BE>), dim3(grid), dim3(DKN_NT), 0, st, A); break;
   }
   PP_LAUNCH_CHECK();
   if (A.part != nullptr) {

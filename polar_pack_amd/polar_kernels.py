@@ -12,7 +12,8 @@ Same names, arguments, return values and error behaviour as the reference
   group rule, > 0 = the container's stream-position rule).
 * :func:`dual_dequant` -- float32 (or fp16) weights of a code view.
 
-Batches of 1-4 tokens run on the fused decode kernels; larger ones decode once into
+Batches of 1-4 tokens (1-8 on the (K,N) kernel layout) run on the fused decode kernels;
+larger ones decode once into
 fp16 weights (the values the reference's kernel rounds its weights to,
 polar_kernels.py:78-82) and run a library fp16 GEMM (hipBLASLt through torch.matmul).
 """
@@ -121,12 +122,15 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
     if cos_lut.numel() != num_phases or sin_lut.numel() != num_phases:
         raise ValueError("cos_lut / sin_lut must have num_phases entries")
     a = a_fp16
-    if a.stride(1) != 1 or a.data_ptr() % 8 or (M > 1 and a.stride(0) % 4):
+    if a.stride(1) != 1 or a.data_ptr() % 16 or (M > 1 and a.stride(0) % 8):
         a = a.contiguous()
     bmax = bmax.contiguous()
     pi, pa, pn, keep = _dual_plug(plug, dev)
     L = nat.lib()
-    if M > FUSED_MAX_M:
+    kn = packed.stride(1) == 1 and packed.stride(0) >= N and packed.stride(0) % 8 == 0 and N % 8 == 0 \
+        and K % 8 == 0 and chunk_size == 0 and group_size >= 8 and group_size & (group_size - 1) == 0 \
+        and packed.data_ptr() % 16 == 0
+    if M > (KN_MAX_M if kn else FUSED_MAX_M):
         # decode along the storage: K-contiguous codes (container rows) into (N,K) weights,
         # multiplied as their transpose; the kernel rule's groups need the (K,N) indices
         nk = packed.stride(0) == 1 and packed.stride(1) != 1 and chunk_size > 0
@@ -152,6 +156,7 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
 
 
 FUSED_MAX_M = 4   # larger batches decode once and run a library GEMM
+KN_MAX_M = 8      # on the (K,N) kernel layout the fused kernel takes up to 8 tokens
 
 
 def dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases=1024, group_size=32, *, plug=None,

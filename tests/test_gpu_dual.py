@@ -120,7 +120,7 @@ def test_quantize_polar_bitpacked_on_gpu_matches_oracle(dtype, max_frac, max_ste
         np.testing.assert_array_equal(got[i].cpu().numpy().view(np.uint16), ref[i].view(np.uint16))
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 6])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6, 8, 11])
 @pytest.mark.parametrize("K,N,plug", [(2048, 1000 - 1000 % 8, 0), (2048, 1000 - 1000 % 8, 700), (64, 96, 0),
                                       (520, 4096, 300), (4096, 4096, 0)])
 def test_polar_dual_bitpacked_kn_fast_path(K, N, plug, M):
