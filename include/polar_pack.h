@@ -75,8 +75,11 @@ int pp_abi_sizes(int64_t* out, int n);
  * (c_sk == 1 or c_sn == 1).
  *
  * Fast paths: c_sk == 1 (container layout, codes rows are (N,K) row-major)
- * with K % 4 == 0, 16-byte aligned rows and M <= 8.  Other layouts decode into
- * `workspace` (4*K*N floats, see pp_quad_gemm_workspace_size) and multiply.
+ * with K % 4 == 0, 16-byte aligned rows and M <= 8; c_sn == 1 (the contiguous
+ * (K,N) tensor pack_quad_layer returns) with N % 4 == 0, K % 8 == 0, 16-byte
+ * aligned rows, in blocks of 8 tokens over a K-slice workspace.  Other layouts
+ * decode into `workspace` (4*K*N floats) and multiply.  The caller sizes the
+ * workspace with pp_quad_gemm_workspace_size.
  */
 int pp_quad_gemm(const void* a, int64_t a_sm, int64_t a_sk,
                  const uint32_t* codes, int64_t c_sk, int64_t c_sn,
@@ -262,6 +265,11 @@ int pp_quad_plug_codes(const uint32_t* codes, int64_t n_codes, const uint32_t* p
  * polar_dual_bitpacked_kernel (polar_kernels.py:14-95).
  * Plug entries (optional) replace the amplitude of the pair at
  * plug_idx[j] - elem_base by the fp16 plug_amp[j] (polar_bitpack.py:240-243).
+ * Fast paths: c_sk == 1 (container layout) with chunk_size > 0 and M <= 4;
+ * c_sn == 1 (the int16 (K,N) tensor quantize_polar_bitpacked returns) with
+ * chunk_size == 0, a power-of-two group_size >= 8, N % 8 == 0, K % 8 == 0, in
+ * blocks of 8 tokens over a K-slice workspace.  Other layouts decode into the
+ * workspace (2*K*N floats); size it with pp_dual_gemm_workspace_size.
  */
 int pp_dual_gemm(const void* a, int64_t a_sm, int64_t a_sk,
                  const void* codes, int code_layout, int64_t c_sk, int64_t c_sn,
