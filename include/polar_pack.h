@@ -236,6 +236,14 @@ int pp_quad_stream(const pp_quad_proj* projs, int64_t n_projs,
                    int64_t M, void* stream);
 
 /*
+ * Transpose quad codes from a (K,N) tensor (row stride ldk >= N, as pack_quad_layer
+ * returns) to (N,K) rows: out[n*K + k] = codes[k*ldk + n].  No counterpart in the
+ * reference: it lets batches of 9-64 tokens on the reference's (K,N) layout run on the
+ * matrix-core decode (pp_quad_mfma), which reads (N,K) rows.
+ */
+int pp_quad_codes_nk(const uint32_t* codes, int64_t ldk, int64_t K, int64_t N, uint32_t* out, void* stream);
+
+/*
  * Plug side table of a quad stream (built once per stream, on the stream's device):
  * code[j] = the code word at stream position plug_idx[j] (0 at or past n_codes).  Given to
  * pp_quad_stream as plug_code, the plug corrections read the plugged words with the plug

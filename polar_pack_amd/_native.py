@@ -65,6 +65,7 @@ EXPORTS = {
     "pp_quad_stream_waves": (i64, [i64]),
     "pp_quad_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, vp, i64, vp, vp, vp, vp, vp, i64, i64, vp, vp, i64, vp]),
     "pp_quad_plug_codes": (i32, [vp, i64, vp, i64, vp, vp]),
+    "pp_quad_codes_nk": (i32, [vp, i64, i64, i64, vp, vp]),
     "pp_dual_stream_rows": (i32, [i64]),
     "pp_dual_stream_chunk": (i32, [i64]),
     "pp_dual_stream_waves": (i64, [i64]),

@@ -329,6 +329,29 @@ __global__ __launch_bounds__(KN_FIN_NT) void quad_kn_finish_kernel(const QuadKnA
   for (int c = 0; c < 4; ++c) o[(int64_t)j * A.o_sm + (int64_t)(n + c) * A.o_sn] = (f16)vv[c];
 }
 
+// Codes (K,N), row stride ldk  ->  (N,K) rows (out[n*K + k]): the layout the matrix-core
+// batch decode reads.  64 x 64 tiles through LDS (a padded row so the column reads of the
+// transposed write hit distinct banks); reads run along n, writes along k.
+constexpr int KN_TT = 64;
+
+__global__ __launch_bounds__(256) void quad_codes_nk_kernel(const uint32_t* codes, int64_t ldk, int K, int N,
+                                                            uint32_t* out) {
+  __shared__ uint32_t tile[KN_TT][KN_TT + 1];
+  const int n0 = blockIdx.x * KN_TT, k0 = blockIdx.y * KN_TT;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;   // 64 x 4 threads
+#pragma unroll
+  for (int i = 0; i < KN_TT; i += 4) {
+    const int k = k0 + ty + i, n = n0 + tx;
+    if (k < K && n < N) tile[ty + i][tx] = codes[(int64_t)k * ldk + n];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < KN_TT; i += 4) {
+    const int n = n0 + ty + i, k = k0 + tx;
+    if (k < K && n < N) out[(int64_t)n * K + k] = tile[tx][ty + i];
+  }
+}
+
 // ------------------------------------------------------------------ host side
 #ifndef PP_KN_MIN_ROWS
 #define PP_KN_MIN_ROWS 32   // slices of at least this many rows (4096x4096: 1..4 tokens measured best)
@@ -426,3 +449,17 @@ int quad_kn_gemm(const void* a, int64_t a_sm, const uint32_t* codes, int64_t ldk
 }
 
 }  // namespace pp
+
+extern "C" int pp_quad_codes_nk(const uint32_t* codes, int64_t ldk, int64_t K, int64_t N, uint32_t* out,
+                                void* stream) {
+  PP_REQUIRE(K >= 0 && N >= 0 && ldk >= N, "bad shape / row stride");
+  if (K == 0 || N == 0) return PP_OK;
+  PP_REQUIRE(codes != nullptr && out != nullptr, "null pointer");
+  PP_REQUIRE(K < (1ll << 31) && N < (1ll << 31) && (K + pp::KN_TT - 1) / pp::KN_TT < 65536,
+             "K / N out of range");
+  const dim3 grid((unsigned)((N + pp::KN_TT - 1) / pp::KN_TT), (unsigned)((K + pp::KN_TT - 1) / pp::KN_TT));
+  hipLaunchKernelGGL(pp::quad_codes_nk_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream), codes, ldk,
+                     (int)K, (int)N, out);
+  PP_LAUNCH_CHECK();
+  return PP_OK;
+}

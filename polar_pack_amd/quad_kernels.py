@@ -11,10 +11,11 @@ Same names, arguments, return values and error behaviour as the reference
   quaternion_packer.py:187-193) and ``elem_base``.
 * :func:`quad_dequant` -- float32 (or fp16) weights of a code view.
 
-Batches: 1-8 tokens run on the fused decode kernels (16 in two passes on (K,N) storage);
-9-128 tokens on the matrix-core decode when the codes are an (N,K) block seen as (K,N)
-(the container layout); larger batches, and more tokens on other layouts, decode once
-into fp16 weights (the
+Batches: 1-8 tokens run on the fused decode kernels; 9-128 tokens on the matrix-core
+decode when the codes are an (N,K) block seen as (K,N) (the container layout), 9-64 on
+(K,N) storage after a transpose of the codes (two 8-token fused passes up to 16 tokens
+when K % 32 != 0); larger batches, and more tokens on other layouts, decode once into
+fp16 weights (the
 values the reference's kernel rounds its weights to, quad_kernels.py:117-126) and run a
 library fp16 GEMM (hipBLASLt through torch.matmul), where the matmul's compute, not the
 weight stream, bounds the time.
@@ -137,6 +138,10 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
     pi, pv, pn, keep = _plug_args(plug, dev)
     L = nat.lib()
     kn = _kn_layout_ok(codes, K, N)
+    if kn and 8 < M <= KN_MFMA_MAX_M and K % 32 == 0:
+        _quad_kn_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
+        del keep
+        return outs
     if M > PREFILL_M or (M > 8 and not _mfma_layout_ok(codes, K) and not (kn and M <= KN_MAX_M)):
         _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base), outs, L, dev)
         del keep
@@ -165,7 +170,35 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
 
 
 PREFILL_M = 128   # batches above this decode once and run a library GEMM on every layout
-KN_MAX_M = 16     # (K,N) storage: up to two 8-token passes of the fused kernel, then the GEMM
+KN_MAX_M = 16     # (K,N) storage, K % 32 != 0: up to two 8-token passes of the fused kernel
+KN_MFMA_MAX_M = 64   # (K,N) storage, K % 32 == 0: codes transposed to (N,K), matrix cores
+
+
+def _quad_kn_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
+    """9-64 tokens on (K,N) storage: transpose the codes to (N,K) rows (pp_quad_codes_nk,
+    one read and one write of the codes) and run the matrix-core decode on them; plug
+    positions are moved to the transposed storage and re-sorted."""
+    K, N = codes.shape
+    ldk = codes.stride(0)
+    cnk = torch.empty((N, K), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    nat.check(L.pp_quad_codes_nk(codes.data_ptr(), ldk, K, N, cnk.data_ptr(), stream), "pp_quad_codes_nk")
+    view = cnk.view(torch.uint32).t()
+    keep2, pn2 = (), 0
+    if pn:
+        idx = (keep[0].view(torch.int32).to(torch.int64) & 0xFFFFFFFF) - elem_base
+        vals = keep[1].reshape(-1, 4)
+        k, n = idx // ldk, idx % ldk
+        ok = (idx >= 0) & (k < K) & (n < N)
+        pos = (n * K + k)[ok]
+        order = torch.argsort(pos)
+        pos = pos[order]
+        keep2 = (torch.where(pos >= 2 ** 31, pos - 2 ** 32, pos).to(torch.int32).contiguous(),
+                 vals[ok][order].contiguous())
+        pn2 = int(pos.numel())
+    for i0 in range(0, a.shape[0], 64):
+        i1 = min(a.shape[0], i0 + 64)
+        _quad_mfma(a[i0:i1], view, lut_ptrs, lut_dtype, sc, keep2, pn2, 0, [o[i0:i1] for o in outs], L, dev)
 
 
 def _kn_layout_ok(codes, K, N):
