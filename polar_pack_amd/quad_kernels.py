@@ -174,6 +174,21 @@ KN_MAX_M = 16     # (K,N) storage, K % 32 != 0: up to two 8-token passes of the 
 KN_MFMA_MAX_M = 64   # (K,N) storage, K % 32 == 0: codes transposed to (N,K), matrix cores
 
 
+def transposed_plug(idx, vals, elem_base, ldk, K, N):
+    """Plug entries of a (K,N) code tensor (row stride ``ldk``, positions relative to
+    ``elem_base``) moved to its (N,K) transpose: position k*ldk + n becomes n*K + k, entries
+    outside the K x N block dropped, re-sorted (the matrix-core path searches them).
+    Returns (int32 tensor holding the uint32 positions, (P', 4) fp16 values)."""
+    p = (idx.view(torch.int32).to(torch.int64) & 0xFFFFFFFF) - elem_base
+    k, n = p // ldk, p % ldk
+    ok = (p >= 0) & (k < K) & (n < N)
+    pos = (n * K + k)[ok]
+    order = torch.argsort(pos)
+    pos = pos[order]
+    return (torch.where(pos >= 2 ** 31, pos - 2 ** 32, pos).to(torch.int32).contiguous(),
+            vals.reshape(-1, 4)[ok][order].contiguous())
+
+
 def _quad_kn_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
     """9-64 tokens on (K,N) storage: transpose the codes to (N,K) rows (pp_quad_codes_nk,
     one read and one write of the codes) and run the matrix-core decode on them; plug
@@ -186,16 +201,8 @@ def _quad_kn_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, 
     view = cnk.view(torch.uint32).t()
     keep2, pn2 = (), 0
     if pn:
-        idx = (keep[0].view(torch.int32).to(torch.int64) & 0xFFFFFFFF) - elem_base
-        vals = keep[1].reshape(-1, 4)
-        k, n = idx // ldk, idx % ldk
-        ok = (idx >= 0) & (k < K) & (n < N)
-        pos = (n * K + k)[ok]
-        order = torch.argsort(pos)
-        pos = pos[order]
-        keep2 = (torch.where(pos >= 2 ** 31, pos - 2 ** 32, pos).to(torch.int32).contiguous(),
-                 vals[ok][order].contiguous())
-        pn2 = int(pos.numel())
+        keep2 = transposed_plug(keep[0], keep[1], elem_base, ldk, K, N)
+        pn2 = int(keep2[0].numel())
     for i0 in range(0, a.shape[0], 64):
         i1 = min(a.shape[0], i0 + 64)
         _quad_mfma(a[i0:i1], view, lut_ptrs, lut_dtype, sc, keep2, pn2, 0, [o[i0:i1] for o in outs], L, dev)

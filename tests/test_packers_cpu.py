@@ -65,3 +65,21 @@ def test_header_luts_closed_form():
     d = pk.header_luts()
     assert d[0].numel() == 64 and d[1].numel() == 1024
     assert abs(float(d[0][63]) - 1.0) < 1e-7 and float(d[1][0]) == -1.0 and float(d[2][512]) == 0.0
+
+
+def test_transposed_plug_positions():
+    """Plug entries of a (K,N) tensor moved to its (N,K) transpose (the matrix-core route
+    for (K,N) storage): positions remapped, out-of-block entries dropped, re-sorted."""
+    import torch
+    from polar_pack_amd.quad_kernels import transposed_plug
+    K, N, ldk, base = 6, 5, 8, 100
+    rng = np.random.default_rng(0)
+    pos = np.sort(rng.choice(K * ldk + 20, 25, replace=False)).astype(np.int64) - 10   # some below 0, past the end
+    vals = rng.standard_normal((pos.size, 4)).astype(np.float16)
+    idx = torch.from_numpy((pos + base).astype(np.int64)).to(torch.int32)
+    got_pos, got_vals = transposed_plug(idx, torch.from_numpy(vals), base, ldk, K, N)
+    keep = [(p, v) for p, v in zip(pos, vals) if p >= 0 and p // ldk < K and p % ldk < N]
+    want = sorted(((p % ldk) * K + p // ldk, tuple(v)) for p, v in keep)
+    assert got_pos.dtype == torch.int32
+    np.testing.assert_array_equal(got_pos.numpy(), [w[0] for w in want])
+    np.testing.assert_array_equal(got_vals.numpy(), np.array([w[1] for w in want], np.float16).reshape(-1, 4))
