@@ -690,7 +690,8 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (the decode step is a "
-              "single-GPU path; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "single-GPU path; a sharded step would run the same kernel on a row slice of every "
+              "projection per GPU)", file=sys.stderr)
         sys.exit(2)
     log = (lambda *a: None) if args.quiet else (lambda *a: print(*a, file=sys.stderr, flush=True))
     dev = torch.device("cuda:0")
