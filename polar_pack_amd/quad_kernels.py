@@ -138,7 +138,7 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
     pi, pv, pn, keep = _plug_args(plug, dev)
     L = nat.lib()
     kn = _kn_layout_ok(codes, K, N)
-    if kn and 8 < M <= KN_MFMA_MAX_M and K % 32 == 0:
+    if kn and 8 < M <= (KN_MFMA_MAX_M if N > K else PREFILL_M) and K % 32 == 0:
         _quad_kn_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
         del keep
         return outs
@@ -171,7 +171,10 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
 
 PREFILL_M = 128   # batches above this decode once and run a library GEMM on every layout
 KN_MAX_M = 16     # (K,N) storage, K % 32 != 0: up to two 8-token passes of the fused kernel
-KN_MFMA_MAX_M = 64   # (K,N) storage, K % 32 == 0: codes transposed to (N,K), matrix cores
+# (K,N) storage, K % 32 == 0: codes transposed to (N,K) for the matrix cores, up to 64
+# tokens, or up to PREFILL_M when N <= K (measured: 4096x4096 and 11008x2048 gain at 65-128
+# tokens, 2048x11008 loses to the fp16 decode + GEMM route there)
+KN_MFMA_MAX_M = 64
 
 
 def transposed_plug(idx, vals, elem_base, ldk, K, N):

@@ -119,7 +119,8 @@ def test_quad_gemm_matches_oracle(K, N, layout, M):
     # dot-product bound (see test_gpu_mfma.py)
     kn_ok = layout == "kn" and N % 4 == 0 and K % 8 == 0
     # matrix cores: (N,K) rows, or (K,N) storage transposed for them
-    mfma = M > 8 and K % 32 == 0 and (layout == "nk" or (kn_ok and M <= qk.KN_MFMA_MAX_M))
+    kn_mfma_max = qk.KN_MFMA_MAX_M if N > K else qk.PREFILL_M
+    mfma = M > 8 and K % 32 == 0 and (layout == "nk" or (kn_ok and M <= kn_mfma_max))
     kn = kn_ok and M <= qk.KN_MAX_M and not mfma                          # fused (K,N) passes
     prefill = M > 8 and not mfma and not kn      # fp16 decode + library GEMM
     W32 = olay.quad_dequant(codes, [l.float().numpy() for l in luts], dtype=np.float32) if mfma else None
@@ -226,7 +227,7 @@ def test_pack_quad_layer_on_gpu_matches_oracle():
         np.testing.assert_array_equal(luts[i].cpu().numpy().view(np.uint16), rl[i].view(np.uint16))
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 6, 8, 13, 40, 64])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6, 8, 13, 40, 64, 100])
 @pytest.mark.parametrize("K,N,plug", [(2048, 1000, 0), (2048, 1000, 700), (64, 96, 0), (520, 4096, 300)])
 def test_quad_gemm_kn_layout_fast_path(K, N, plug, M):
     """Contiguous (K,N) codes, the layout pack_quad_layer returns: the fused (K,N) kernel
