@@ -116,6 +116,43 @@ def synth_dual_stream(shapes, dev, truncate=0.05):
     return w1, w2
 
 
+def stream_shapes(layers):
+    """(N, K) of every projection of the 3B-shaped stream, in stream order."""
+    return [(n, k) for _ in range(layers) for (_, n, k) in LAYER]
+
+
+def quad3b_pack(layers, dev):
+    """The quad 3B-shaped workload's stream: synthesized weights packed on the device, plug
+    table = top 0.1% of tuples by norm."""
+    models = synth_models(layers, dev)
+    pack = pack_quad_device(models, plug_cap=0.001, select="norm")
+    del models
+    torch.cuda.empty_cache()
+    return pack
+
+
+def dual3b_pack(layers, dev, tails):
+    """The dual 3B-shaped heavy-tail workload's stream (model 2 truncated by 5%): top 1% of
+    pairs by squared amplitude error per chunk in the plug table; ``tails`` keeps model 1's
+    last weights as fp16 tails, otherwise the shorter model is zero-padded."""
+    w1, w2 = synth_dual_stream(stream_shapes(layers), dev)
+    pack = pack_dual_device(w1, w2, plug_cap=0.01, select="ref", tails=tails)
+    del w1, w2
+    torch.cuda.empty_cache()
+    return pack
+
+
+def dual2048_pack(dev):
+    """The dual 2048x2048 Linear: Student-t(5) base with std 0.02, each model base + N(0,
+    0.002), plug table = top 0.1% of pairs by amplitude."""
+    N = K = 2048
+    g = torch.Generator(device=dev).manual_seed(seed_of(1, 0, 0))
+    w0 = student_t(N * K, 5, 0.02, g, dev)
+    w1 = (w0 + torch.randn(N * K, generator=g, device=dev) * 0.002).to(torch.float16)
+    w2 = (w0 + torch.randn(N * K, generator=g, device=dev) * 0.002).to(torch.float16)
+    return pack_dual_device(w1, w2, plug_cap=0.001, select="norm")
+
+
 def cpu_baseline(pack, shapes, sample_tuples):
     """The CPU oracle's unpack (numpy float64, single thread) + torch CPU float32 matmul,
     on the first projections of the stream up to ~sample_tuples, extrapolated to the step."""
@@ -249,17 +286,12 @@ def line(metric, achieved, ms, args, dtype, config, traffic=None, cpu=None, extr
 # ---------------------------------------------------------------- 3B-shaped streams
 
 def run_quad3b(args, dev, log):
-    shapes = [(n, k) for _ in range(args.layers) for (_, n, k) in LAYER]
+    shapes = stream_shapes(args.layers)
     t0 = time.time()
-    models = synth_models(args.layers, dev)
+    pack = quad3b_pack(args.layers, dev)
     torch.cuda.synchronize()
-    log(f"[bench] synthesized 4 x {sum(n * k for n, k in shapes)} fp16 weights in {time.time() - t0:.1f}s")
-    t0 = time.time()
-    pack = pack_quad_device(models, plug_cap=0.001, select="norm")
-    torch.cuda.synchronize()
-    del models
-    torch.cuda.empty_cache()
-    log(f"[bench] packed: n={pack.n} plug={pack.plug_idx.numel()} r_max={pack.r_max:.4f} in {time.time() - t0:.1f}s")
+    log(f"[bench] synthesized and packed: n={pack.n} plug={pack.plug_idx.numel()} r_max={pack.r_max:.4f} in "
+        f"{time.time() - t0:.1f}s")
 
     st = QuadStream(pack, shapes, M=1)
     xs, outs = st.make_buffers()
@@ -311,18 +343,12 @@ def run_quad3b(args, dev, log):
 
 
 def run_dual3b(args, dev, log, tails):
-    shapes = [(n, k) for _ in range(args.layers) for (_, n, k) in LAYER]
+    shapes = stream_shapes(args.layers)
     t0 = time.time()
-    w1, w2 = synth_dual_stream(shapes, dev)
+    pack = dual3b_pack(args.layers, dev, tails)
     torch.cuda.synchronize()
-    log(f"[bench] synthesized {w1.numel()} + {w2.numel()} fp16 weights in {time.time() - t0:.1f}s")
-    t0 = time.time()
-    pack = pack_dual_device(w1, w2, plug_cap=0.01, select="ref", tails=tails)
-    torch.cuda.synchronize()
-    del w1, w2
-    torch.cuda.empty_cache()
-    log(f"[bench] packed: {pack.n_codes} pairs, plug {pack.plug_idx.numel()}, tails {pack.tail_lengths} "
-        f"in {time.time() - t0:.1f}s")
+    log(f"[bench] synthesized and packed: {pack.n_codes} pairs, plug {pack.plug_idx.numel()}, tails "
+        f"{pack.tail_lengths} in {time.time() - t0:.1f}s")
 
     st = DualStream(pack, shapes, M=1)
     xs, outs = st.make_buffers()
@@ -439,11 +465,7 @@ def time_graph(sts, args):
 
 def run_dual2048(args, dev, log):
     N = K = 2048
-    g = torch.Generator(device=dev).manual_seed(seed_of(1, 0, 0))
-    w0 = student_t(N * K, 5, 0.02, g, dev)
-    w1 = (w0 + torch.randn(N * K, generator=g, device=dev) * 0.002).to(torch.float16)
-    w2 = (w0 + torch.randn(N * K, generator=g, device=dev) * 0.002).to(torch.float16)
-    pack = pack_dual_device(w1, w2, plug_cap=0.001, select="norm")
+    pack = dual2048_pack(dev)
     st0 = DualStream(pack, [(N, K)], M=1)
     copies = max(2, -(-MALL_BYTES // st0.algorithmic_bytes()))
     sts = rotated_streams(DualStream, pack, [(N, K)], 1, copies, dev, quad=False)

@@ -192,7 +192,7 @@ def decode_pairs_f64(dp: DualPack, lo=0, hi=None):
     levels = 2 ** dp.amp_bits - 1
     log_mu = np.log1p(dp.mu)
     phase_mask = (1 << dp.phase_bits) - 1
-    codes = dp.codes_u16()[lo:hi]
+    codes = from_be_bytes(dp.codes_be[2 * lo:2 * hi])     # = dp.codes_u16()[lo:hi]
     amp_q = (codes >> dp.phase_bits) & levels
     phase_idx = codes & phase_mask
     pos = np.arange(lo, hi, dtype=np.int64)

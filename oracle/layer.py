@@ -53,16 +53,36 @@ def pack_amp_phase(amp_q, phase_q):
     return (((a & 0x3F) << 10) | (p & 0x3FF)) - 32768
 
 
-def quantize_polar_bitpacked(w1, w2, amp_bits=6, num_phases=1024, mu=255, group_size=32):
+def _opmath(x, op, c):
+    """``x op c`` as torch's GPU elementwise kernels evaluate a tensor-scalar operation: in
+    float32 with the scalar as float32 (a division multiplies by the float32 reciprocal),
+    rounded once to the tensor's dtype."""
+    c32 = torch.tensor(c, dtype=torch.float32)
+    y = x.float() + c32 if op == "+" else x.float() * (torch.tensor(1.0, dtype=torch.float32) / c32)
+    return y.to(x.dtype)
+
+
+def quantize_polar_bitpacked(w1, w2, amp_bits=6, num_phases=1024, mu=255, group_size=32, gpu_scalars=False):
     """Per-layer dual packer -- polar_kernels.py:118-151 (torch, CPU).
 
     Returns ``(packed int16 (K,N), bmax fp16 flat, amp_lut fp16[64],
     cos_lut fp16[1024], sin_lut fp16[1024])`` as numpy arrays.
+
+    The reference function is torch code that runs on whichever device holds the weights,
+    and torch rounds Python scalars differently there: on the CPU, ``fp16 + pi`` first
+    rounds pi to fp16 (3.140625), while the GPU kernels keep scalars in float32 and
+    divide by a scalar through its reciprocal.  ``gpu_scalars=True`` evaluates the
+    scalar operations of the phase and amplitude codes the GPU's way (the reference's result for
+    weights on a GPU); the default is the CPU's (the golden vectors were written there).
     """
     K, N = w1.shape
     amplitude = torch.sqrt(w1 ** 2 + w2 ** 2)
     phase = torch.atan2(w2, w1)
-    phase_q = (torch.round((phase + math.pi) / (2 * math.pi) * num_phases).long() % num_phases).to(torch.int16)
+    if gpu_scalars:
+        turns = _opmath(_opmath(phase, "+", math.pi), "/", 2 * math.pi)
+    else:
+        turns = (phase + math.pi) / (2 * math.pi)
+    phase_q = (torch.round(turns * num_phases).long() % num_phases).to(torch.int16)
     total = K * N
     flat = amplitude.flatten()
     pad = (group_size - total % group_size) % group_size
@@ -73,7 +93,8 @@ def quantize_polar_bitpacked(w1, w2, amp_bits=6, num_phases=1024, mu=255, group_
     bmax = torch.where(bmax > 1e-10, bmax, torch.ones_like(bmax))
     norm = grouped / bmax
     log_mu = math.log(1 + mu)
-    compressed = torch.sign(norm) * torch.log1p(mu * norm.abs()) / log_mu
+    compressed = torch.sign(norm) * torch.log1p(mu * norm.abs())
+    compressed = _opmath(compressed, "/", log_mu) if gpu_scalars else compressed / log_mu
     levels = (1 << amp_bits) - 1
     amp_q = torch.round(compressed * levels).clamp(0, levels).to(torch.int8).flatten()[:total].reshape(K, N)
     bmax = bmax.flatten().to(torch.float16)

@@ -11,11 +11,13 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libpolar_pack.so")
+OBJ_DIR = os.path.join(LIB_DIR, "obj")
 SOURCES = ["capi.hip", "quad.hip", "quad_rows.hip", "quad_mfma.hip", "quad_kn.hip", "dual.hip", "dual_rows.hip", "dual_kn.hip"]
 ARCH = "gfx950"
 
@@ -33,10 +35,7 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build polar_pack_amd)")
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp] + [os.path.join(CSRC, s) for s in SOURCES]
+def _run(cmd, verbose):
     proc = subprocess.run(cmd, cwd=CSRC, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (proc.stderr or "").splitlines() if noise not in l)
@@ -44,6 +43,19 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{' '.join(cmd)}\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    """Compile every source to an object (in parallel), then link the shared library."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    objs = [os.path.join(OBJ_DIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    cmds = [[hipcc(), *compile_flags, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+    jobs = jobs or min(len(cmds), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        list(pool.map(lambda c: _run(c, verbose), cmds))
+    tmp = LIB + ".tmp"
+    _run([hipcc(), *HIPCC_FLAGS, "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB)
     return LIB
 

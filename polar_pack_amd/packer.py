@@ -11,10 +11,12 @@ global ``r_max = 1.001 * max |w/s|`` (:70-77), then codes and plug entries
 * ``select="norm"`` -- the top ``plug_cap`` fraction of tuples by norm (threshold
   from a strided sample), as the decode-step benchmark specifies.
 
-Codes are computed in float32 like the reference's numpy pass; device
-transcendentals can round differently at exact ties, so a few codes may differ by
-one step from a host pack of the same weights (decode parity is unaffected: the
-decoder is checked on whatever codes the stream holds).
+Codes are computed in float32 like the reference's numpy pass, with the same
+operation order and IEEE divisions (never a multiply by a reciprocal); device
+transcendentals can still round differently at exact ties, so a few codes may differ
+by one step from a host pack of the same weights (decode parity is unaffected: the
+decoder is checked on whatever codes the stream holds).  Models of unequal length
+keep their positions past the common length as fp16 tails, as the reference does.
 
 :func:`pack_dual_device` follows pack_dual_models_packed (polar_bitpack.py:93-172)
 chunk by chunk.
@@ -36,6 +38,12 @@ def _f32(x: float) -> float:
     return float(np.float32(x))
 
 
+def _div(x: torch.Tensor, c: float) -> torch.Tensor:
+    """x / float32(c), an element-wise IEEE division like numpy's (a Python-scalar divisor
+    makes torch on the GPU multiply by its reciprocal instead, which rounds differently)."""
+    return x / torch.tensor(c, dtype=torch.float32, device=x.device)
+
+
 def quad_codes_f32(wn: Sequence[torch.Tensor], r_max: float):
     """uint32 words (int64 tensor) and float32 norm of normalised float32 tuples
     (quaternion_packer.py:22-39)."""
@@ -45,10 +53,10 @@ def quad_codes_f32(wn: Sequence[torch.Tensor], r_max: float):
     t1 = torch.atan2(torch.sqrt(w2 ** 2 + w3 ** 2 + w4 ** 2), w1)
     t2 = torch.atan2(torch.sqrt(w3 ** 2 + w4 ** 2), w2)
     t3 = torch.remainder(torch.atan2(w4, w3), 2 * math.pi)
-    nq = torch.round(torch.log1p(MU * r / r_max) / log_mu * 255).clamp(0, 255).to(torch.int64)
-    q1 = torch.round(t1 / math.pi * 255).clamp(0, 255).to(torch.int64)
-    q2 = torch.round(t2 / math.pi * 255).clamp(0, 255).to(torch.int64)
-    q3 = torch.round(t3 / (2 * math.pi) * 255).clamp(0, 255).to(torch.int64)
+    nq = torch.round(_div(torch.log1p(_div(MU * r, r_max)), log_mu) * 255).clamp(0, 255).to(torch.int64)
+    q1 = torch.round(_div(t1, math.pi) * 255).clamp(0, 255).to(torch.int64)
+    q2 = torch.round(_div(t2, math.pi) * 255).clamp(0, 255).to(torch.int64)
+    q3 = torch.round(_div(t3, 2 * math.pi) * 255).clamp(0, 255).to(torch.int64)
     return (nq << 24) | (q1 << 16) | (q2 << 8) | q3, r
 
 
@@ -66,63 +74,99 @@ def _rel_err_f64(wn, words, r, r_max):
     return torch.sqrt(e) / torch.clamp(r.double(), min=1e-12)
 
 
+class _Flat:
+    """A model given as a list of flat tensors, read as one stream by position."""
+
+    def __init__(self, parts: Sequence[torch.Tensor]):
+        self.parts = [t.reshape(-1) for t in parts]
+        self.offs = np.concatenate([[0], np.cumsum([int(t.numel()) for t in self.parts])]).astype(np.int64)
+
+    def __len__(self):
+        return int(self.offs[-1])
+
+    def slice(self, a: int, b: int) -> torch.Tensor:
+        """Positions [a, b) (one view when they lie in one part)."""
+        i = int(np.searchsorted(self.offs, a, side="right")) - 1
+        pieces = []
+        while a < b:
+            lo, hi = int(self.offs[i]), int(self.offs[i + 1])
+            take = min(b, hi)
+            if take > a:
+                pieces.append(self.parts[i][a - lo:take - lo])
+                a = take
+            i += 1
+        return pieces[0] if len(pieces) == 1 else torch.cat(pieces)
+
+
 def pack_quad_device(models: List[List[torch.Tensor]], plug_cap: float = 0.001, select: str = "norm",
-                     sample: int = 4_000_000) -> QuadPackDevice:
-    """Pack 4 models given as lists of flat fp16/fp32 device tensors (one per projection,
-    stream order; all 4 lists have the same lengths) into a device-resident stream."""
-    if len(models) != 4 or len({len(m) for m in models}) != 1:
-        raise ValueError("need 4 models with the same projection list")
-    sizes = [int(t.numel()) for t in models[0]]
-    for m in models:
-        if [int(t.numel()) for t in m] != sizes:
-            raise ValueError("per-model tails are not produced by the device packer; use equal lengths")
-    n = sum(sizes)
+                     sample: int = 4_000_000, threshold=None) -> QuadPackDevice:
+    """Pack 4 models, each a list of flat fp16/fp32 device tensors (one per projection, stream
+    order), into a device-resident stream.
+
+    As quaternion_packer.py:54-56 and 121-126: ``n`` = the shortest model's length, every
+    model's positions past ``n`` are kept as its fp16 tail.  The models' lists may cut the
+    stream at different places; the work proceeds over the pieces between all of their
+    cuts below ``n``.  ``threshold`` (``select="ref"`` only) replaces the sampled relative-error
+    threshold, for streams of at most 1,000,000 tuples where the reference's window sampler
+    cannot run."""
+    if len(models) != 4:
+        raise ValueError("need 4 models")
+    flats = [_Flat(m) for m in models]
+    lengths = [len(f) for f in flats]
+    n = min(lengths)
+    if n == 0:
+        raise ValueError("every model must hold at least one weight")
     if n >= 2 ** 32:
         raise ValueError("a .quadpack stream indexes plug entries with uint32: n must be < 2^32")
-    dev = models[0][0].device
-    # pass A: RMS per model over the stream (float64 accumulation)
+    dev = flats[0].parts[0].device
+    cuts = np.unique(np.concatenate([f.offs[(f.offs > 0) & (f.offs < n)] for f in flats] + [[0, n]]))
+    pieces = list(zip(cuts[:-1].tolist(), cuts[1:].tolist()))
+    # pass A: RMS per model over the common length (float64 accumulation, quaternion_packer.py:59-68)
     s = []
-    for m in models:
+    for f in flats:
         acc = torch.zeros((), dtype=torch.float64, device=dev)
-        for t in m:
-            acc += (t.double() ** 2).sum()
+        for a, b in pieces:
+            acc += (f.slice(a, b).double() ** 2).sum()
         s.append(math.sqrt(float(acc) / n))
-    # pass B: r_max, plus a strided norm sample for the 'norm' threshold
+    s32 = [torch.tensor(sk, dtype=torch.float32, device=dev) for sk in s]
+
+    def normalised(a, b):
+        return [f.slice(a, b).float() / sk for f, sk in zip(flats, s32)]
+
+    # pass B: r_max (:70-77), plus a strided norm sample for the 'norm' threshold
     r_max = 0.0
     samples = []
     stride = max(1, n // sample)
-    for p in range(len(sizes)):
-        wn = [models[k][p].float() / s[k] for k in range(4)]
+    for a, b in pieces:
+        wn = normalised(a, b)
         r = torch.sqrt(wn[0] ** 2 + wn[1] ** 2 + wn[2] ** 2 + wn[3] ** 2)
         r_max = max(r_max, float(r.max()))
         if select == "norm":
-            samples.append(r[::stride].clone())
+            samples.append(r[(-a) % stride::stride].clone())
     r_max *= 1.001
     if select == "norm":
         allr = torch.cat(samples)
         k = max(1, int(round(allr.numel() * (1.0 - plug_cap))))
         thr = float(torch.kthvalue(allr.cpu(), min(k, allr.numel())).values) if plug_cap > 0 else float("inf")
     elif select == "ref":
-        thr = _ref_threshold(models, s, sizes, r_max, plug_cap)
+        thr = _ref_threshold(normalised, n, r_max, plug_cap) if threshold is None else float(threshold)
     else:
         raise ValueError("select must be 'norm' or 'ref'")
-    # pass C: codes + plug
+    # pass C: codes + plug (:90-113)
     codes = torch.empty(n, dtype=torch.int32, device=dev)
     pidx, pvals = [], []
-    pos = 0
-    for p, size in enumerate(sizes):
-        wn = [models[k][p].float() / s[k] for k in range(4)]
+    for a, b in pieces:
+        wn = normalised(a, b)
         words, r = quad_codes_f32(wn, r_max)
-        codes[pos:pos + size] = torch.where(words >= 2 ** 31, words - 2 ** 32, words).to(torch.int32)
+        codes[a:b] = torch.where(words >= 2 ** 31, words - 2 ** 32, words).to(torch.int32)
         if select == "norm":
             mask = r > thr
         else:
             mask = _rel_err_f64(wn, words, r, r_max) > thr
         nz = torch.nonzero(mask).flatten()
         if nz.numel():
-            pidx.append((nz + pos).to(torch.int64))
+            pidx.append((nz + a).to(torch.int64))
             pvals.append(torch.stack([w[nz] for w in wn], dim=1).to(torch.float16))
-        pos += size
     if pidx:
         pi = torch.cat(pidx)
         pi = torch.where(pi >= 2 ** 31, pi - 2 ** 32, pi).to(torch.int32).view(torch.uint32)
@@ -130,26 +174,22 @@ def pack_quad_device(models: List[List[torch.Tensor]], plug_cap: float = 0.001, 
     else:
         pi = torch.zeros(0, dtype=torch.int32, device=dev).view(torch.uint32)
         pv = torch.zeros((0, 4), dtype=torch.float16, device=dev)
+    # per-model fp16 tails (:121-126)
+    tails = [f.slice(n, L).to(torch.float16).contiguous() if L > n else torch.zeros(0, dtype=torch.float16, device=dev)
+             for f, L in zip(flats, lengths)]
     return QuadPackDevice(n=n, s=tuple(_f32(x) for x in s), r_max=_f32(r_max), codes=codes.view(torch.uint32),
-                          plug_idx=pi, plug_vals=pv, tails=[torch.zeros(0, dtype=torch.float16, device=dev)] * 4)
+                          plug_idx=pi, plug_vals=pv, tails=tails)
 
 
-def _ref_threshold(models, s, sizes, r_max, plug_cap):
-    """Percentile of the relative error over the reference's 100 seeded windows."""
-    n = sum(sizes)
+def _ref_threshold(normalised, n, r_max, plug_cap):
+    """Percentile of the relative error over the reference's 100 seeded windows of 1,000,000
+    tuples (quaternion_packer.py:79-87; like the reference, needs n > 1,000,000)."""
+    if n <= 1_000_000:
+        raise ValueError("the reference's plug threshold samples windows of 1,000,000 tuples: n must exceed that")
     starts = np.random.default_rng(42).integers(0, n - 1_000_000, 100)
-    offs = np.concatenate([[0], np.cumsum(sizes)])
     errs = []
     for st in starts:
-        parts = []
-        for k in range(4):
-            seg = []
-            lo, hi = int(st), int(st) + 1_000_000
-            for p in range(len(sizes)):
-                a, b = max(lo, offs[p]), min(hi, offs[p + 1])
-                if a < b:
-                    seg.append(models[k][p][a - offs[p]:b - offs[p]].float())
-            parts.append(torch.cat(seg) / s[k])
+        parts = normalised(int(st), int(st) + 1_000_000)
         words, r = quad_codes_f32(parts, r_max)
         errs.append(_rel_err_f64(parts, words, r, r_max).cpu().numpy())
     return float(np.percentile(np.concatenate(errs), (1 - plug_cap) * 100))

@@ -39,18 +39,30 @@ DUAL_PROJ_DTYPE = np.dtype([("codes", "<u8"), ("ldc", "<i8"), ("pos0", "<i8"), (
                             ("out", "<u8", (2,)), ("o_sm", "<i8"), ("N", "<i4"), ("K", "<i4")])
 
 
-def full_rows(shapes, n):
+def stream_positions(shapes, positions=None):
+    """Stream position of each projection: ``positions`` when given (ascending, the
+    projections not overlapping), else back to back from 0."""
+    sizes = np.array([int(a) * int(b) for a, b in shapes], np.int64)
+    if positions is None:
+        return np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64) if sizes.size else np.zeros(0, np.int64)
+    pos = np.asarray(positions, np.int64).reshape(-1)
+    if pos.size != sizes.size or (pos.size and (pos[0] < 0 or np.any(pos[1:] < pos[:-1] + sizes[:-1]))):
+        raise ValueError("projection positions must be >= 0, ascending and not overlapping")
+    return pos
+
+
+def full_rows(shapes, n, positions=None):
     """Stream position of each projection and how many of its rows lie fully below ``n``."""
-    pos = np.cumsum([0] + [int(a) * int(b) for a, b in shapes]).astype(np.int64)
+    pos = stream_positions(shapes, positions)
     N = np.array([int(a) for a, _ in shapes], np.int64)
     K = np.array([int(b) for _, b in shapes], np.int64)
-    r_full = np.clip((int(n) - pos[:-1]) // np.maximum(K, 1), 0, N)
-    return pos[:-1], N, K, r_full
+    r_full = np.clip((int(n) - pos) // np.maximum(K, 1), 0, N)
+    return pos, N, K, r_full
 
 
-def plan_tasks(shapes, n, rows_per_task):
+def plan_tasks(shapes, n, rows_per_task, positions=None):
     """Tasks (proj, row0, nrows) over the full rows of every projection, in stream order."""
-    pos0, N, K, r_full = full_rows(shapes, n)
+    pos0, N, K, r_full = full_rows(shapes, n, positions)
     counts = (r_full + rows_per_task - 1) // rows_per_task
     proj = np.repeat(np.arange(len(shapes), dtype=np.int64), counts)
     first = np.concatenate([[0], np.cumsum(counts)[:-1]]) if counts.size else np.zeros(0, np.int64)
@@ -77,13 +89,13 @@ def wave_bounds(bytes_, n_waves):
     return np.maximum.accumulate(bounds)
 
 
-def split_factors(shapes, n, rows_per_task, n_waves, block=512):
+def split_factors(shapes, n, rows_per_task, n_waves, block=512, positions=None):
     """(slices, column blocks per slice) per projection, slices being whole blocks of
     ``block`` columns (the kernel's chunk width): 1 slice when the launch has at least
     half as many tasks as wavefronts (measured: splitting then costs more in partial-sum
     traffic and pipeline restarts than it gains), else enough slices for about one item
     per wavefront."""
-    proj, _, _ = plan_tasks(shapes, n, rows_per_task)
+    proj, _, _ = plan_tasks(shapes, n, rows_per_task, positions)
     K = np.array([int(b) for _, b in shapes], np.int64)
     blocks = np.maximum(1, (K + block - 1) // block)
     if proj.size == 0 or 2 * proj.size >= n_waves:
@@ -93,7 +105,8 @@ def split_factors(shapes, n, rows_per_task, n_waves, block=512):
     return -(-blocks // per), per
 
 
-def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=4, split=False, block=512):
+def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=4, split=False, block=512,
+                  positions=None):
     """Per-wave segments (SEG_DTYPE), seg_bounds (n_waves + 1) and the workspace bytes
     for the rows below ``n``.
 
@@ -105,15 +118,15 @@ def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=
     one projection and one slice.  The workspace of split launches holds one uint32
     counter per task, then 4*M*N float32 accumulators per split projection.
     """
-    proj, row0, nrows = plan_tasks(shapes, n, rows_per_task)
+    proj, row0, nrows = plan_tasks(shapes, n, rows_per_task, positions)
     if proj.size == 0:
         return np.zeros(0, SEG_DTYPE), np.zeros(n_waves + 1, np.int64), 0
-    pos0, N, K, _ = full_rows(shapes, n)
+    pos0, N, K, _ = full_rows(shapes, n, positions)
     tid = np.arange(proj.size, dtype=np.int64)
     parts = np.ones(len(shapes), np.int64)
     per = np.zeros(len(shapes), np.int64)
     if split:
-        parts, per = split_factors(shapes, n, rows_per_task, n_waves, block)
+        parts, per = split_factors(shapes, n, rows_per_task, n_waves, block, positions)
     if np.all(parts == 1):
         it_task, it_k0, it_k1 = tid, np.zeros(proj.size, np.int64), K[proj]
     else:
@@ -163,12 +176,12 @@ def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=
     return segs, bounds, ws_bytes
 
 
-def plan_task_plug(shapes, n, plug_host, rows_per_task):
+def plan_task_plug(shapes, n, plug_host, rows_per_task, positions=None):
     """Per task (in the order of :func:`plan_tasks`): the first plug entry at or after its
     first position and the first entry past its last position, as an (n_tasks, 2) int64
     table, and the number of chunks (512-pair steps) of each task."""
-    proj, row0, nrows = plan_tasks(shapes, n, rows_per_task)
-    pos0, _, K, _ = full_rows(shapes, n)
+    proj, row0, nrows = plan_tasks(shapes, n, rows_per_task, positions)
+    pos0, _, K, _ = full_rows(shapes, n, positions)
     start = pos0[proj] + row0 * K[proj]
     tab = np.empty((proj.size, 2), np.int64)
     tab[:, 0] = np.searchsorted(plug_host, start, side="left")
@@ -176,7 +189,7 @@ def plan_task_plug(shapes, n, plug_host, rows_per_task):
     return tab, (K[proj] + 511) // 512
 
 
-def plan_tail_items(shapes, n, plug_host, tail_lengths=None, fp16_rows=0):
+def plan_tail_items(shapes, n, plug_host, tail_lengths=None, fp16_rows=0, positions=None):
     """Items for the rows that reach position ``n``.
 
     By default one TAIL item per row, with its plug range.  With ``fp16_rows`` > 0 and
@@ -184,7 +197,7 @@ def plan_tail_items(shapes, n, plug_host, tail_lengths=None, fp16_rows=0):
     lie wholly inside or wholly past its tail become FP16 items of up to ``fp16_rows``
     consecutive rows with the same status; the rest stay one-row TAIL items.
     """
-    pos0, N, K, r_full = full_rows(shapes, n)
+    pos0, N, K, r_full = full_rows(shapes, n, positions)
     parts = []
     for p in np.flatnonzero(r_full < N):
         rows = np.arange(r_full[p], N[p], dtype=np.int64)
@@ -222,6 +235,32 @@ def plan_tail_items(shapes, n, plug_host, tail_lengths=None, fp16_rows=0):
     return np.concatenate(parts) if parts else np.zeros(0, ITEM_DTYPE)
 
 
+def layer_map_projections(layer_info, model=None):
+    """The projections of the reference's layer map (collect_weights, polar_main.py:33-46:
+    dicts with ``name``, ``shape`` = [N, K] and ``numel``, in stream order) as
+    ``(names, shapes, positions)``.  Each entry advances the stream position by its
+    ``numel``; entries that are not an (N, K) Linear -- a shape that is not 2-D or does not
+    hold ``numel`` weights, or, with ``model`` given, a name that is not an ``nn.Linear``
+    of that size there -- are skipped, as replace_model_weights does
+    (polar_packer.py:297-305)."""
+    names, shapes, positions = [], [], []
+    pos = 0
+    for info in layer_info:
+        numel = int(info["numel"])
+        shape = [int(v) for v in info["shape"]]
+        ok = len(shape) == 2 and shape[0] * shape[1] == numel and numel > 0
+        if ok and model is not None:
+            from .linear import _module_at
+            _, module = _module_at(model, info["name"])
+            ok = isinstance(module, torch.nn.Linear) and module.weight.numel() == numel
+        if ok:
+            names.append(info["name"])
+            shapes.append((shape[0], shape[1]))
+            positions.append(pos)
+        pos += numel
+    return names, shapes, positions
+
+
 class QuadStream:
     """One-launch decode of many projections of a quad stream (``pp_quad_stream``).
 
@@ -230,7 +269,8 @@ class QuadStream:
     workspace owned by this object (so two launches of one QuadStream must not overlap).
     """
 
-    def __init__(self, pack: QuadPackDevice, shapes: Sequence[Tuple[int, int]], M: int = 1, split: bool = True):
+    def __init__(self, pack: QuadPackDevice, shapes: Sequence[Tuple[int, int]], M: int = 1, split: bool = True,
+                 positions=None):
         L = nat.lib()
         self.pack = pack
         self.shapes = [(int(n), int(k)) for n, k in shapes]
@@ -238,9 +278,9 @@ class QuadStream:
         self.device = pack.codes.device
         self.rows_per_item = int(L.pp_quad_stream_rows(self.M))
         nat.check(0 if self.rows_per_item > 0 else nat.PP_EINVAL, "pp_quad_stream_rows")
-        pos = np.cumsum([0] + [n * k for n, k in self.shapes])
-        self.pos0 = pos[:-1]
-        total = int(pos[-1])
+        self.pos0 = stream_positions(self.shapes, positions)
+        self.positions = self.pos0 if positions is not None else None
+        total = int(self.pos0[-1]) + self.shapes[-1][0] * self.shapes[-1][1] if self.shapes else 0
         longest = pack.n + max(pack.tail_lengths)
         if total > longest:
             raise ValueError(f"projections cover {total} positions, the stream holds {longest}")
@@ -251,8 +291,8 @@ class QuadStream:
         self.n_waves = int(L.pp_quad_stream_waves(self.M))
         self.segs_np, self.bounds_np, ws_bytes = plan_segments(
             self.shapes, pack.n, plug, self.n_waves, self.rows_per_item, self.M, split=split,
-            block=int(L.pp_quad_stream_chunk(self.M)))
-        self.tail_items_np = plan_tail_items(self.shapes, pack.n, plug)
+            block=int(L.pp_quad_stream_chunk(self.M)), positions=self.positions)
+        self.tail_items_np = plan_tail_items(self.shapes, pack.n, plug, positions=self.positions)
         self.n_segs = self.segs_np.size
         self.n_tail = self.tail_items_np.size
         self.split = bool(np.any(self.segs_np["parts"] > 1))
@@ -275,6 +315,15 @@ class QuadStream:
                                       self.plug_code.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
             nat.check(rc, "pp_quad_plug_codes")
         self.projs = None
+
+    @classmethod
+    def from_layer_map(cls, pack: QuadPackDevice, layer_info, M: int = 1, model=None, split: bool = True):
+        """The stream of every Linear of a reference layer map (:func:`layer_map_projections`);
+        ``names`` lists them in projection order."""
+        names, shapes, positions = layer_map_projections(layer_info, model)
+        st = cls(pack, shapes, M=M, split=split, positions=positions)
+        st.names = names
+        return st
 
     # ---------------------------------------------------------------- buffers
     def make_buffers(self):
@@ -355,7 +404,8 @@ class DualStream:
     workspace owned by this object: two launches of one DualStream must not overlap).
     """
 
-    def __init__(self, pack, shapes: Sequence[Tuple[int, int]], M: int = 1, plug_windows=None, split: bool = True):
+    def __init__(self, pack, shapes: Sequence[Tuple[int, int]], M: int = 1, plug_windows=None, split: bool = True,
+                 positions=None):
         L = nat.lib()
         self.pack = pack
         self.shapes = [(int(n), int(k)) for n, k in shapes]
@@ -363,9 +413,9 @@ class DualStream:
         self.device = pack.codes.device
         self.rows_per_item = int(L.pp_dual_stream_rows(self.M))
         nat.check(0 if self.rows_per_item > 0 else nat.PP_EINVAL, "pp_dual_stream_rows")
-        pos = np.cumsum([0] + [n * k for n, k in self.shapes])
-        self.pos0 = pos[:-1]
-        total = int(pos[-1])
+        self.pos0 = stream_positions(self.shapes, positions)
+        self.positions = self.pos0 if positions is not None else None
+        total = int(self.pos0[-1]) + self.shapes[-1][0] * self.shapes[-1][1] if self.shapes else 0
         longest = pack.n_codes + max(pack.tail_lengths)
         if total > longest:
             raise ValueError(f"projections cover {total} positions, the stream holds {longest}")
@@ -378,7 +428,7 @@ class DualStream:
         self.n_waves = int(L.pp_dual_stream_waves(self.M))
         self.segs_np, self.bounds_np, ws_bytes = plan_segments(
             self.shapes, pack.n_codes, plug, self.n_waves, self.rows_per_item, self.M, code_bytes=2, split=split,
-            block=int(L.pp_dual_stream_chunk(self.M)))
+            block=int(L.pp_dual_stream_chunk(self.M)), positions=self.positions)
         self.split = bool(np.any(self.segs_np["parts"] > 1))
         # split launches: counters + accumulators, zero once here, left zero by every launch
         self.workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=self.device) if ws_bytes else None
@@ -386,10 +436,10 @@ class DualStream:
         aligned = pack.n_codes % 8 == 0 and all(t is None or t.numel() == 0 or t.data_ptr() % 16 == 0
                                                 for t in tails)
         self.tail_items_np = plan_tail_items(self.shapes, pack.n_codes, plug, pack.tail_lengths,
-                                             fp16_rows=8 if aligned else 0)
+                                             fp16_rows=8 if aligned else 0, positions=self.positions)
         self.n_segs = self.segs_np.size
         self.n_tail = self.tail_items_np.size
-        self.task_plug_np, nck = plan_task_plug(self.shapes, pack.n_codes, plug, self.rows_per_item)
+        self.task_plug_np, nck = plan_task_plug(self.shapes, pack.n_codes, plug, self.rows_per_item, self.positions)
         self.n_tasks = self.task_plug_np.shape[0]
         if plug_windows is None:
             # one 64-entry window per step, two when more than 2% of the tasks would
@@ -425,6 +475,15 @@ class DualStream:
                                       torch.cuda.current_stream(dev).cuda_stream)
             nat.check(rc, "pp_dual_plug_table")
         self.projs = None
+
+    @classmethod
+    def from_layer_map(cls, pack, layer_info, M: int = 1, model=None, split: bool = True, plug_windows=None):
+        """The stream of every Linear of a reference layer map (:func:`layer_map_projections`);
+        ``names`` lists them in projection order."""
+        names, shapes, positions = layer_map_projections(layer_info, model)
+        st = cls(pack, shapes, M=M, split=split, positions=positions, plug_windows=plug_windows)
+        st.names = names
+        return st
 
     def make_buffers(self):
         """One activation buffer (M, K_p) and 2 output buffers (M, N_p) per projection."""

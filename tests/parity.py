@@ -3,8 +3,9 @@
 * dequantised weights: within 1 fp16 ulp of the float64 oracle, compared after
   rounding both to fp16 (and the float32 value within 8 float32 ulps);
 * GEMM/GEMV outputs (fp32 accumulate, fp16 out): per element
-  |y - y_ref| <= 1e-3 * |y_ref| + 1e-5 * max|y_ref|, i.e. rel 1e-3 with a small
-  absolute floor for outputs that cancel to near zero; products summed on the matrix
+  |y - y_ref| <= 1e-3 * |y_ref| + 1e-5 * max|y_ref| + 2^-25, i.e. rel 1e-3 with a small
+  absolute floor for outputs that cancel to near zero, and the fp16 output's own rounding
+  below its normal range (half its smallest subnormal); products summed on the matrix
   cores (fp16 operands, fp32 sums: ~1e-6 of sum |w x| measured) add the dot-product
   bound 2^-18 * sum_k |w_k x_k|;
 * codes, plug positions: bit-exact (checked by the tests directly).
@@ -14,6 +15,7 @@ import torch
 
 GEMV_RTOL = 1e-3
 GEMV_FLOOR = 1e-5
+FP16_OUT_FLOOR = 2.0 ** -25    # an fp16 output rounds values below 2^-14 to a multiple of 2^-24
 
 
 def fp16_ulp_distance(a, b):
@@ -42,7 +44,7 @@ def assert_gemv_close(got, ref, what="", rtol=GEMV_RTOL, floor=GEMV_FLOOR, bound
     ref = np.asarray(ref, np.float64)
     scale = np.abs(ref).max() if ref.size else 0.0
     err = np.abs(got - ref)
-    lim = rtol * np.abs(ref) + floor * scale
+    lim = rtol * np.abs(ref) + floor * scale + FP16_OUT_FLOOR
     if bound is not None:
         lim = lim + bound
     worst = (err - lim).argmax() if ref.size else 0

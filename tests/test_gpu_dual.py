@@ -99,20 +99,20 @@ def test_polar_dual_bitpacked_container_stream(chunk, M):
             assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), f"base {base}", bound=prefill_bound(a, w))
 
 
-@pytest.mark.parametrize("dtype,max_frac,max_step", [(torch.float16, 0.25, 2), (torch.float32, 0.01, 1)])
-def test_quantize_polar_bitpacked_on_gpu_matches_oracle(dtype, max_frac, max_step):
-    """The packer computes in the weights' dtype, as the reference does (polar_kernels.py:120-124).
-    With fp16 weights the phase (phase + pi) / 2pi * 1024 is rounded in fp16, where a one-ulp
-    difference between device and host atan2, carried through three fp16 roundings, moves
-    many codes by one or two phase steps; with float32 weights only a few move, by one."""
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_quantize_polar_bitpacked_on_gpu_matches_oracle(dtype):
+    """The packer computes in the weights' dtype, as the reference does (polar_kernels.py:120-124),
+    with torch's GPU rule for Python scalars (kept in float32, division through the
+    reciprocal; the oracle's ``gpu_scalars`` mode): codes equal but for rare one-step flips
+    where device and host transcendentals round apart."""
     K, N = 128, 64
     w1, w2 = [torch.from_numpy(w.reshape(K, N)).to(dtype) for w in gen.correlated_models(5, [K * N] * 2)]
     got = pk.quantize_polar_bitpacked(w1.to(DEV), w2.to(DEV))
-    ref = olay.quantize_polar_bitpacked(w1, w2)
+    ref = olay.quantize_polar_bitpacked(w1, w2, gpu_scalars=True)
     p_got = got[0].cpu().numpy().astype(np.int32) + 32768
     p_ref = ref[0].astype(np.int32) + 32768
     dph = np.abs(((p_got & 1023) - (p_ref & 1023) + 512) % 1024 - 512)
-    assert (dph > 0).mean() < max_frac and dph.max() <= max_step
+    assert (dph > 0).mean() < 0.01 and dph.max() <= 1, ((dph > 0).mean(), dph.max())
     assert np.abs((p_got >> 10) - (p_ref >> 10)).max() <= 1
     db = np.abs(got[1].cpu().numpy().view(np.int16).astype(np.int32) - ref[1].view(np.int16).astype(np.int32))
     assert db.max() <= 1                                 # group max of device sqrt: within one fp16 ulp

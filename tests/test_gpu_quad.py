@@ -1,4 +1,6 @@
 """GPU parity of the quad decode against the float64 oracle (same seeded inputs)."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -134,6 +136,7 @@ def test_quad_gemm_matches_oracle(K, N, layout, M):
             assert normwise(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), W[k])) <= 1e-3
         if prefill:
             bound = fp16_weight_bound(a.numpy(), w)
+            assert normwise(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), W[k])) <= 1e-3
         assert_gemv_close(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), w), f"model {k}", bound=bound)
 
 
@@ -155,6 +158,8 @@ def test_quad_gemm_real_pack_with_plug_fast_path(M):
     for k in range(4):
         w = W[k].reshape(N, K).T
         bound = fp16_weight_bound(a.numpy(), w) if M > qk.PREFILL_M else None   # fp16 decode + library GEMM
+        if bound is not None:
+            assert normwise(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), w)) <= 1e-3
         assert_gemv_close(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), w), f"model {k}", bound=bound)
 
 
@@ -227,13 +232,53 @@ def test_pack_quad_layer_on_gpu_matches_oracle():
         np.testing.assert_array_equal(luts[i].cpu().numpy().view(np.uint16), rl[i].view(np.uint16))
 
 
+def kn_route(K, N, M):
+    """Which kernel quad_bitpacked runs for contiguous (K,N) codes: 'fused' (the (K,N)
+    decode kernel), 'mfma' (codes transposed for the matrix cores) or 'prefill' (fp16
+    decode + library GEMM)."""
+    if M <= 8 or (K % 32 != 0 and M <= qk.KN_MAX_M):
+        return "fused"
+    if K % 32 == 0 and M <= (qk.KN_MFMA_MAX_M if N > K else qk.PREFILL_M):
+        return "mfma"
+    return "prefill"
+
+
+def check_route(outs, a, codes, luts, scales, route, plug_at=None, plug_vals=None, what=""):
+    """Outputs of one route against the float64 oracle: the exact decode for the fused
+    kernels (rel 1e-3); for the matrix cores the fp16 operands they multiply (the float32
+    decode rounded once, plug tuples substituted) with the float32 dot-product bound, and
+    normwise 1e-3 against the exact decode; for the fp16 decode + GEMM the fp16-weight
+    bound, and normwise 1e-3."""
+    an = a.numpy() if torch.is_tensor(a) else a
+    W = oracle_w(codes, luts, scales)
+    W32 = olay.quad_dequant(codes, [l.float().numpy() for l in luts], dtype=np.float32) if route == "mfma" else None
+    for k in range(4):
+        if plug_at is not None:
+            W[k][plug_at] = plug_vals[:, k].astype(np.float64) * scales[k]
+        got = outs[k].float().cpu().numpy()
+        exact = olay.gemm_f64(an, W[k])
+        if route == "fused":
+            assert_gemv_close(got, exact, f"{what} model {k}")
+            continue
+        assert normwise(got, exact) <= 1e-3, f"{what} model {k}: normwise {normwise(got, exact):.2e}"
+        if route == "mfma":
+            h = W32[k].astype(np.float16)
+            if plug_at is not None:
+                h[plug_at] = plug_vals[:, k]
+            w = h.astype(np.float64) * float(np.float32(scales[k]))
+            bound = 2.0 ** -18 * (np.abs(an.astype(np.float64)) @ np.abs(w))
+            assert_gemv_close(got, olay.gemm_f64(an, w), f"{what} model {k}", bound=bound)
+        else:
+            assert_gemv_close(got, exact, f"{what} model {k}", bound=fp16_weight_bound(an, W[k]))
+
+
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 6, 8, 13, 40, 64, 100])
 @pytest.mark.parametrize("K,N,plug", [(2048, 1000, 0), (2048, 1000, 700), (64, 96, 0), (520, 4096, 300)])
 def test_quad_gemm_kn_layout_fast_path(K, N, plug, M):
     """Contiguous (K,N) codes, the layout pack_quad_layer returns: the fused (K,N) kernel
     (256-column items for 1-4 tokens, 128-column items for 5-8, K slices whose partial
-    sums a finish pass adds, plug corrections per entry; blocks of 8 tokens), against the
-    float64 oracle."""
+    sums a finish pass adds, plug corrections per entry; blocks of 8 tokens), the codes
+    transposed for the matrix cores, or the fp16 decode + GEMM, each against its oracle."""
     seed = K + N + plug + M
     codes = random_codes((K, N), seed)
     luts, scales = fp16_luts(seed)
@@ -246,12 +291,78 @@ def test_quad_gemm_kn_layout_fast_path(K, N, plug, M):
     if plug:
         kw = dict(plug=(u32(flat + base).to(DEV), torch.from_numpy(vals).to(DEV)), elem_base=base)
     outs = qk.quad_bitpacked(a.to(DEV), u32(codes).to(DEV), [l.to(DEV) for l in luts], scales, **kw)
-    W = oracle_w(codes, luts, scales)
-    kk, nn = flat // N, flat % N
-    # beyond the fused passes (codes transposed for the matrix cores, or the fp16 decode +
-    # GEMM), fp16 weights meet the dot product
-    fused = M <= 8 or (K % 32 != 0 and M <= qk.KN_MAX_M)
+    check_route(outs, a, codes, luts, scales, kn_route(K, N, M), (flat // N, flat % N), vals, f"M={M}")
+
+
+@pytest.mark.parametrize("M", [4, 40, 200])
+def test_quad_gemm_kn_layout_wider_row_stride(M):
+    """(K,N) codes that are a column slice of a wider tensor (row stride ldk > N, ldk % 4 ==
+    0): plug entries in the block are applied, entries in the columns past N are not."""
+    K, N, ldk = 1024, 500, 520
+    seed = 71 + M
+    wide = random_codes((K, ldk), seed)
+    luts, scales = fp16_luts(seed)
+    rng = np.random.default_rng(seed)
+    base = 333
+    inside = rng.choice(K * N, 260, replace=False)
+    kk_in, nn_in = inside // N, inside % N
+    pad_k = rng.integers(0, K, 40)
+    pad_n = rng.integers(N, ldk, 40)
+    pos = np.concatenate([kk_in * ldk + nn_in, pad_k * ldk + pad_n])
+    order = np.argsort(pos)
+    pos = pos[order]
+    pos, first = np.unique(pos, return_index=True)
+    vals = (rng.standard_normal((pos.size, 4)) * 0.5).astype(np.float16)
+    view = u32(wide).to(DEV)[:, :N]
+    assert view.stride(0) == ldk
+    a = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
+    outs = qk.quad_bitpacked(a.to(DEV), view, [l.to(DEV) for l in luts], scales,
+                             plug=(u32((pos + base).astype(np.uint32)).to(DEV), torch.from_numpy(vals).to(DEV)),
+                             elem_base=base)
+    in_block = (pos % ldk) < N
+    check_route(outs, a, wide[:, :N], luts, scales, kn_route(K, N, M), (pos[in_block] // ldk, pos[in_block] % ldk),
+                vals[in_block], f"ldk={ldk} M={M}")
+
+
+def split_luts(seed):
+    """fp16 LUTs whose q2 tables (cos2, sin2) differ from the q1 ones: the decode kernels'
+    four-table LDS layout (the reference's 7-table interface allows any tables)."""
+    luts, scales = fp16_luts(seed)
+    ang = torch.arange(256, dtype=torch.float64) / 255 * math.pi * 0.93 + 0.07
+    luts = list(luts)
+    luts[3] = torch.cos(ang).to(torch.float16)
+    luts[4] = torch.sin(ang).to(torch.float16)
+    assert not torch.equal(luts[1], luts[3])
+    return luts, scales
+
+
+@pytest.mark.parametrize("layout,M", [("nk", 1), ("nk", 3), ("nk", 8), ("kn", 1), ("kn", 5), ("nk", 16), ("nk", 64),
+                                      ("kn", 40)])
+def test_quad_split_tables_every_route(layout, M):
+    K, N = 1024, 384
+    seed = 90 + M
+    codes = random_codes((K, N), seed)
+    luts, scales = split_luts(seed)
+    rng = np.random.default_rng(seed)
+    flat = np.sort(rng.choice(K * N, 150, replace=False)).astype(np.uint32)
+    vals = (rng.standard_normal((150, 4)) * 0.5).astype(np.float16)
+    if layout == "kn":
+        view = u32(codes).to(DEV)
+        idx = flat
+        at = (flat // N, flat % N)
+        route = kn_route(K, N, M)
+    else:
+        view = u32(np.ascontiguousarray(codes.T)).to(DEV).t()
+        nn, kk = flat // K, flat % K          # storage offsets of (N,K) rows
+        idx = flat
+        at = (kk, nn)
+        route = "fused" if M <= 8 else "mfma"
+    a = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
+    L = [l.to(DEV) for l in luts]
+    outs = qk.quad_bitpacked(a.to(DEV), view, L, scales, plug=(u32(idx).to(DEV), torch.from_numpy(vals).to(DEV)))
+    check_route(outs, a, codes, luts, scales, route, at, vals, f"{layout} M={M}")
+    w = qk.quad_dequant(view, L, scales, plug=(u32(idx).to(DEV), torch.from_numpy(vals).to(DEV)))
+    ref = oracle_w(codes, luts, scales)
     for k in range(4):
-        W[k][kk, nn] = vals[:, k].astype(np.float64) * scales[k]
-        bound = None if fused else fp16_weight_bound(a.numpy(), W[k])
-        assert_gemv_close(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), W[k]), f"model {k}", bound=bound)
+        ref[k][at] = vals[:, k].astype(np.float64) * scales[k]
+        assert_dequant_close(w[k].cpu().numpy(), ref[k], f"dequant model {k}")

@@ -274,3 +274,32 @@ def test_pack_quad_layer_luts_closed_form():
     wn = [x.double().numpy() / s for x, s in zip(w, scales)]
     rmax = 1.001 * np.sqrt(sum(x ** 2 for x in wn)).max()
     assert abs(float(luts[0][255]) - rmax) <= 2 ** -10 * rmax
+
+
+def test_dual_layer_packer_scalar_rounding_modes():
+    """The oracle's two scalar-rounding modes of quantize_polar_bitpacked: float32 weights
+    give the same codes either way but for float32 reciprocal roundings (a few codes, one
+    step); fp16 weights under the CPU rule equal an explicit chain with pi rounded to fp16
+    for the add; under the GPU rule, an explicit float32 chain rounded to fp16 per op."""
+    import math
+    import torch
+    from oracle import layer as olay
+    import gen
+    K, N = 64, 96
+    ws = gen.correlated_models(21, [K * N] * 2)
+    w32 = [torch.from_numpy(w.reshape(K, N)) for w in ws]
+    a = olay.quantize_polar_bitpacked(*w32)[0].astype(np.int32)
+    b = olay.quantize_polar_bitpacked(*w32, gpu_scalars=True)[0].astype(np.int32)
+    d = np.abs((((a & 1023) - (b & 1023)) + 512) % 1024 - 512)
+    assert (d > 0).sum() <= 10 and d.max() <= 1 and np.array_equal(a >> 10, b >> 10)
+    w16 = [w.half() for w in w32]
+    ph = torch.atan2(w16[1].float(), w16[0].float()).half().float()
+    pi16 = float(torch.tensor(math.pi, dtype=torch.float16))
+    cpu = torch.round((((ph + pi16).half().float() / (2 * math.pi)).half().float() * 1024).half()).long() % 1024
+    inv = np.float32(1.0) / np.float32(2 * math.pi)
+    gpu = torch.round((((ph + np.float32(math.pi)).half().float() * float(inv)).half().float() * 1024).half()).long() % 1024
+    got_cpu = (olay.quantize_polar_bitpacked(*w16)[0].astype(np.int32) + 32768) & 1023
+    got_gpu = (olay.quantize_polar_bitpacked(*w16, gpu_scalars=True)[0].astype(np.int32) + 32768) & 1023
+    np.testing.assert_array_equal(got_cpu, cpu.numpy())
+    np.testing.assert_array_equal(got_gpu, gpu.numpy())
+    assert (got_cpu != got_gpu).mean() > 0.05       # the two rules really differ for fp16 weights

@@ -83,3 +83,45 @@ def test_transposed_plug_positions():
     assert got_pos.dtype == torch.int32
     np.testing.assert_array_equal(got_pos.numpy(), [w[0] for w in want])
     np.testing.assert_array_equal(got_vals.numpy(), np.array([w[1] for w in want], np.float16).reshape(-1, 4))
+
+
+def test_pack_quad_device_tails_and_threshold_rule_match_the_oracle():
+    """Models of unequal length (per-model fp16 tails, quaternion_packer.py:54-56, 121-126),
+    given as lists cut at different places, with the reference's relative-error plug rule
+    at a fixed threshold: the oracle packer's header, codes, plug table and tails."""
+    import gen
+    from oracle import quadpack as oqp
+    from polar_pack_amd.packer import pack_quad_device
+    n, tails = 60_000, (0, 517, 1031, 13)
+    models = gen.correlated_models(61, [n + t for t in tails])
+    cuts = [[], [1000, 30_000], [n], [7, 59_999, 60_500]]
+    lists = [[torch.from_numpy(p) for p in np.split(m, c)] for m, c in zip(models, cuts)]
+    pack = pack_quad_device(lists, select="ref", threshold=0.006)
+    qp = oqp.pack_quad(models, threshold=0.006)
+    assert pack.n == qp.n == n and pack.tail_lengths == list(tails)
+    assert pack.s == qp.s and pack.r_max == qp.r_max
+    got = pack.codes.view(torch.int32).numpy().view(np.uint32)
+    flips = np.flatnonzero(got != qp.codes)
+    assert flips.size <= 6, f"{flips.size} codes differ"
+    for f in flips:            # a flip moves one byte field by one step (a rounding tie)
+        d = [abs(int(got[f] >> s & 255) - int(qp.codes[f] >> s & 255)) for s in (24, 16, 8, 0)]
+        assert sorted(d) == [0, 0, 0, 1] or sorted(d)[-1] == 255
+    pi = pack.plug_idx.view(torch.int32).numpy().view(np.uint32)
+    common, ia, ib = np.intersect1d(pi, qp.plug_idx, return_indices=True)
+    assert qp.plug_idx.size > 100 and common.size >= 0.99 * max(pi.size, qp.plug_idx.size)
+    np.testing.assert_array_equal(pack.plug_vals.numpy()[ia].view(np.uint16), qp.plug_vals[ib].view(np.uint16))
+    for k in range(4):
+        np.testing.assert_array_equal(pack.tails[k].numpy().view(np.uint16), qp.tails[k].view(np.uint16))
+
+
+def test_pack_quad_device_list_cuts_do_not_change_the_pack():
+    import gen
+    from polar_pack_amd.packer import pack_quad_device
+    models = gen.correlated_models(62, [30_000] * 4)
+    one = pack_quad_device([[torch.from_numpy(m)] for m in models], plug_cap=0.01)
+    cut = pack_quad_device([[torch.from_numpy(p) for p in np.split(m, [100 * (k + 1), 20_000])]
+                            for k, m in enumerate(models)], plug_cap=0.01)
+    assert one.s == cut.s and one.r_max == cut.r_max
+    assert torch.equal(one.codes.view(torch.int32), cut.codes.view(torch.int32))
+    assert torch.equal(one.plug_idx.view(torch.int32), cut.plug_idx.view(torch.int32))
+    assert torch.equal(one.plug_vals, cut.plug_vals)

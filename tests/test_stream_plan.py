@@ -173,3 +173,56 @@ def test_large_streams_are_not_split():
     segs, _, ws = plan_segments(shapes, n, np.zeros(0, np.uint32), 2048, 8, split=True)
     assert np.all(segs["parts"] == 1) and ws == 0
     assert np.all(segs["k0"] == 0) and np.all(segs["k1"] == np.array([b for _, b in shapes])[segs["proj"]])
+
+
+def test_layer_map_projections_skip_non_linear_entries():
+    """Every entry advances the stream position by its numel; entries that are not an
+    (N, K) Linear are skipped (polar_packer.py:297-305)."""
+    from polar_pack_amd.stream import layer_map_projections
+    info = [{"name": "model.layers.0.q", "shape": [8, 16], "numel": 128},
+            {"name": "model.norm", "shape": [16], "numel": 16},
+            {"name": "model.layers.0.k", "shape": [4, 16], "numel": 64},
+            {"name": "bad", "shape": [4, 4], "numel": 20},
+            {"name": "lm_head", "shape": [12, 16], "numel": 192}]
+    names, shapes, pos = layer_map_projections(info)
+    assert names == ["model.layers.0.q", "model.layers.0.k", "lm_head"]
+    assert shapes == [(8, 16), (4, 16), (12, 16)]
+    assert pos == [0, 144, 228]
+
+
+def test_layer_map_projections_with_a_model():
+    import torch
+    from polar_pack_amd.stream import layer_map_projections
+    m = torch.nn.Sequential(torch.nn.Linear(16, 8), torch.nn.SiLU(), torch.nn.Embedding(4, 16), torch.nn.Linear(16, 6))
+    info = [{"name": "0", "shape": [8, 16], "numel": 128}, {"name": "2", "shape": [4, 16], "numel": 64},
+            {"name": "3", "shape": [5, 16], "numel": 80}]        # a size that does not match the module
+    names, shapes, pos = layer_map_projections(info, model=m)
+    assert names == ["0"] and pos == [0]
+
+
+def test_positioned_plans_match_back_to_back_plans_shifted():
+    """Projections at explicit positions (gaps between them, as skipped layer-map entries
+    leave) plan the same segments as back-to-back ones, with plug starts and tail items
+    found at the real positions."""
+    shapes = [(37, 2048), (5, 1024), (8, 256)]
+    gaps = [0, 300, 17]
+    pos = np.cumsum([g + (shapes[i - 1][0] * shapes[i - 1][1] if i else 0) for i, g in enumerate(gaps)])
+    end = int(pos[-1]) + 8 * 256
+    n = end - 3 * 256 - 5                 # the last projection's last rows reach the tails
+    rng = np.random.default_rng(0)
+    plug = np.sort(rng.choice(end, 400, replace=False)).astype(np.uint32)
+    segs, bounds, _ = plan_segments(shapes, n, plug, 16, 4, positions=pos)
+    cov = seg_coverage(segs, shapes)
+    assert [c.tolist() for c in cov[:2]] == [[1] * 37, [1] * 5]
+    assert cov[2].tolist() == [1] * 4 + [0] * 4
+    for s in segs:
+        start = int(pos[int(s["proj"])]) + int(s["row0"]) * shapes[int(s["proj"])][1]
+        assert int(s["plug_lo"]) == int(np.searchsorted(plug, start))
+    tail = plan_tail_items(shapes, n, plug, positions=pos)
+    assert list(tail["proj"]) == [2] * 4 and list(tail["row0"]) == [4, 5, 6, 7]
+    for it in tail:
+        lo = int(pos[2]) + int(it["row0"]) * 256
+        expect = np.nonzero((plug >= lo) & (plug < lo + 256))[0]
+        np.testing.assert_array_equal(np.arange(int(it["plug_lo"]), int(it["plug_hi"])), expect)
+    with pytest.raises(ValueError):
+        plan_segments(shapes, n, plug, 16, 4, positions=[0, 10, 20])       # overlapping
