@@ -8,9 +8,9 @@
  *   - returns PP_OK (0) or a nonzero pp_status; pp_last_error() then returns a
  *     thread-local message.
  *
- * Nothing here allocates device memory except pp_quad_gemm / pp_dual_gemm on the
- * generic (non fast-path) layouts, which take a caller-provided workspace
- * (see *_workspace_size) and never call hipMalloc themselves.
+ * Nothing here allocates device memory: entry points that need scratch memory take a
+ * caller-provided workspace (see *_workspace_size), or, for pp_quad_gemm_noalloc, use a
+ * fixed device array inside the library.
  *
  * Citations name the reference interface each entry point replaces
  * (file:line in everymonday100/polar_pack).
@@ -95,6 +95,28 @@ int pp_quad_gemm(const void* a, int64_t a_sm, int64_t a_sk,
 int64_t pp_quad_gemm_workspace_size(const void* a, int64_t a_sm, int64_t a_sk,
                                     const uint32_t* codes, int64_t c_sk, int64_t c_sn,
                                     int64_t plug_n, int64_t M, int64_t N, int64_t K);
+
+/*
+ * pp_quad_gemm without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference: it exists for those callers.
+ * Same operands, results and fast paths as pp_quad_gemm; the workspace is a device array
+ * of PP_NOALLOC_SCRATCH_BYTES inside the library (one per GPU, held until the process
+ * ends).  Calls whose pp_quad_gemm_workspace_size exceeds it fail with PP_EINVAL (the
+ * generic layouts above 4M weights; the fast paths need at most 32 MiB below 500K output
+ * columns).  It calls no hipMalloc,
+ * hipFree or allocating library routine.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU race.
+ */
+#define PP_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int pp_quad_gemm_noalloc(const void* a, int64_t a_sm, int64_t a_sk,
+                         const uint32_t* codes, int64_t c_sk, int64_t c_sn,
+                         const void* const* luts, int lut_dtype,
+                         const float* scales,
+                         const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n, int64_t elem_base,
+                         void* const* out, int64_t o_sm, int64_t o_sn,
+                         int64_t M, int64_t N, int64_t K,
+                         void* stream);
 
 /*
  * Dequantise to float32: out_m[k*N + n] = s_m * W_m[k, n] (plug applied).

@@ -54,6 +54,8 @@ EXPORTS = {
     "pp_quad_gemm": (i32, [vp, i64, i64, vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64,
                            i64, i64, i64, vp, i64, vp]),
     "pp_quad_gemm_workspace_size": (i64, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64]),
+    "pp_quad_gemm_noalloc": (i32, [vp, i64, i64, vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64,
+                                   i64, i64, i64, vp]),
     "pp_quad_dequant": (i32, [vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
     "pp_quad_dequant_f16": (i32, [vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
     "pp_quad_mfma": (i32, [vp, i64, i64, vp, i64, vp, i32, vp, vp, vp, i64, vp, i64, i64, vp, i64, i64, i64, i64,
