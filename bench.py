@@ -153,9 +153,22 @@ def dual2048_pack(dev):
     return pack_dual_device(w1, w2, plug_cap=0.001, select="norm")
 
 
-def cpu_baseline(pack, shapes, sample_tuples):
+def check_close(got, ref, what, rtol=1e-3, floor=1e-5):
+    """|got - ref| <= rtol |ref| + floor max|ref| + 2^-25 per element (fp16 outputs)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    lim = rtol * np.abs(ref) + floor * np.abs(ref).max() + 2.0 ** -25
+    if not np.all(err <= lim):
+        raise SystemExit(f"parity check failed on {what}: max |d| {err.max():.3e}, max |ref| {np.abs(ref).max():.3e}")
+    return float(err.max() / max(np.abs(ref).max(), 1e-300))
+
+
+def cpu_baseline(pack, shapes, sample_tuples, xs=None, outs=None):
     """The CPU oracle's unpack (numpy float64, single thread) + torch CPU float32 matmul,
-    on the first projections of the stream up to ~sample_tuples, extrapolated to the step."""
+    on the first projections of the stream up to ~sample_tuples, extrapolated to the step.
+    With the GPU run's activations ``xs`` and outputs ``outs``, the CPU products are also
+    the check of those projections' GPU outputs (rel 1e-3)."""
     from oracle import quadpack as oqp
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
@@ -173,30 +186,35 @@ def cpu_baseline(pack, shapes, sample_tuples):
     rng = np.random.default_rng(0)
     t_unpack = t_mm = 0.0
     pos = 0
-    for n, k in take:
+    worst = 0.0
+    for p, (n, k) in enumerate(take):
         sub = oqp.QuadPack(n=n * k, s=qp.s, r_max=qp.r_max, codes=qp.codes[pos:pos + n * k],
                            plug_idx=(qp.plug_idx[(qp.plug_idx >= pos) & (qp.plug_idx < pos + n * k)] - pos).astype(np.uint32),
                            plug_vals=qp.plug_vals[(qp.plug_idx >= pos) & (qp.plug_idx < pos + n * k)])
         t0 = time.perf_counter()
         ws = oqp.unpack_quad(sub)
         t1 = time.perf_counter()
-        x = torch.from_numpy(rng.standard_normal((1, k)).astype(np.float32))
-        for w in ws:
-            y = x @ torch.from_numpy(w.reshape(n, k)).t()
+        x = xs[p].float() if xs is not None else torch.from_numpy(rng.standard_normal((1, k)).astype(np.float32))
+        ys = [x @ torch.from_numpy(w.reshape(n, k)).t() for w in ws]
         t2 = time.perf_counter()
         t_unpack += t1 - t0
         t_mm += t2 - t1
+        if outs is not None:
+            for m in range(4):
+                worst = max(worst, check_close(outs[p][m].float().numpy(), ys[m].numpy(), f"projection {p} model {m}"))
         pos += n * k
-        del ws, y
+        del ws, ys
     total_tuples = sum(n * k for n, k in shapes)
     scale = total_tuples / tuples
     return {"unpack_s": t_unpack, "matmul_s": t_mm, "sample_tuples": tuples, "scale": scale,
-            "step_s": (t_unpack + t_mm) * scale, "threads": threads}
+            "step_s": (t_unpack + t_mm) * scale, "threads": threads, "checked": len(take) if outs else 0,
+            "worst_normwise": worst}
 
 
-def cpu_baseline_dual(pack, shapes, sample_pairs):
+def cpu_baseline_dual(pack, shapes, sample_pairs, xs=None, outs=None):
     """The CPU oracle's dual unpack (numpy float64, single thread) + torch CPU float32 matmul
-    on the first projections of the stream up to ~sample_pairs, extrapolated to the step."""
+    on the first projections of the stream up to ~sample_pairs, extrapolated to the step;
+    with the GPU run's activations and outputs, also the check of those projections."""
     from oracle import dualpack as odp
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
@@ -221,23 +239,27 @@ def cpu_baseline_dual(pack, shapes, sample_pairs):
     rng = np.random.default_rng(0)
     t_unpack = t_mm = 0.0
     pos = 0
-    for n, k in take:
+    worst = 0.0
+    for p, (n, k) in enumerate(take):
         t0 = time.perf_counter()
         w1, w2 = odp.decode_pairs_f64(dp, pos, pos + n * k)
         w1, w2 = w1.astype(np.float32), w2.astype(np.float32)
         t1 = time.perf_counter()
-        x = torch.from_numpy(rng.standard_normal((1, k)).astype(np.float32))
-        for w in (w1, w2):
-            y = x @ torch.from_numpy(w.reshape(n, k)).t()
+        x = xs[p].float() if xs is not None else torch.from_numpy(rng.standard_normal((1, k)).astype(np.float32))
+        ys = [x @ torch.from_numpy(w.reshape(n, k)).t() for w in (w1, w2)]
         t2 = time.perf_counter()
         t_unpack += t1 - t0
         t_mm += t2 - t1
+        if outs is not None:
+            for m in range(2):
+                worst = max(worst, check_close(outs[p][m].float().numpy(), ys[m].numpy(), f"projection {p} model {m}"))
         pos += n * k
-        del w1, w2, y
+        del w1, w2, ys
     total = sum(n * k for n, k in shapes)
     scale = total / pairs
     return {"unpack_s": t_unpack, "matmul_s": t_mm, "sample": pairs, "scale": scale,
-            "step_s": (t_unpack + t_mm) * scale, "threads": threads}
+            "step_s": (t_unpack + t_mm) * scale, "threads": threads, "checked": len(take) if outs else 0,
+            "worst_normwise": worst}
 
 
 def read_pmc_traffic(path):
@@ -301,20 +323,22 @@ def run_quad3b(args, dev, log):
     st.bind(xs, outs)
     log(f"[bench] plan: {st.n_segs} segments, {st.n_tail} tail items, {st.n_waves} waves")
 
-    # sanity: the stream output equals the per-projection operator on a k_proj and a down_proj
+    # sanity: a k_proj and a down_proj of the stream against another kernel's decode (the
+    # element-wise quad_dequant) times torch's float32 matmul; the CPU baseline below checks
+    # layer 0 against the oracle
     st()
     torch.cuda.synchronize()
+    first = [[o.cpu() for o in outs[p]] for p in range(len(LAYER))]
     luts = qk.header_luts(pack.r_max, device=dev)
     for p in (1, 6):
         n, k = shapes[p]
         pos = int(st.pos0[p])
-        single = qk.quad_bitpacked(xs[p], pack.codes[pos:pos + n * k].reshape(n, k).t(), luts, list(pack.s),
-                                   plug=(pack.plug_idx, pack.plug_vals), elem_base=pos)
+        w = qk.quad_dequant(pack.codes[pos:pos + n * k].reshape(n, k).t(), luts, list(pack.s),
+                            plug=(pack.plug_idx, pack.plug_vals), elem_base=pos)
         for m in range(4):
-            d = (outs[p][m].float() - single[m].float()).abs().max().item()
-            ref = single[m].float().abs().max().item()
-            if not d <= 2e-3 * ref:
-                raise SystemExit(f"stream/single mismatch on projection {p} model {m}: {d} vs {ref}")
+            check_close(outs[p][m].float().cpu().numpy(), (xs[p].float() @ w[m]).cpu().numpy(),
+                        f"projection {p} model {m} vs the element-wise decode")
+        del w
 
     per, wall = time_events(st, args.steps, args.warmup)
     ms = float(np.mean(per))
@@ -325,14 +349,16 @@ def run_quad3b(args, dev, log):
 
     cpu = None
     if not args.no_cpu:
-        c = cpu_baseline(pack, shapes, args.cpu_sample_tuples)
+        c = cpu_baseline(pack, shapes, args.cpu_sample_tuples, xs=[x.cpu() for x in xs[:len(first)]], outs=first)
         log(f"[bench] cpu baseline: unpack {c['unpack_s']:.2f}s + matmul {c['matmul_s']:.2f}s on "
-            f"{c['sample_tuples']} tuples -> {c['step_s']:.2f}s per step (x{c['scale']:.1f})")
+            f"{c['sample_tuples']} tuples -> {c['step_s']:.2f}s per step (x{c['scale']:.1f}); GPU outputs of "
+            f"{c['checked']} projections match it (normwise {c['worst_normwise']:.1e})")
         cpu = {"value": algo / c["step_s"] / 1e9, "unit": "GB/s", "cores": c["threads"], "kind": "port",
                "sample": (f"first {c['sample_tuples']} tuples of the stream ({c['sample_tuples'] / pack.n:.2%}): "
                           f"numpy float64 unpack_quad restatement (1 thread) {c['unpack_s']:.2f}s + torch CPU "
                           f"float32 x@W^T x4 ({c['threads']} threads) {c['matmul_s']:.2f}s, extrapolated x"
-                          f"{c['scale']:.1f} to {c['step_s']:.1f}s per step")}
+                          f"{c['scale']:.1f} to {c['step_s']:.1f}s per step; the GPU outputs of those "
+                          f"{c['checked']} projections match it within rel 1e-3")}
 
     line(METRIC, achieved, ms, args, "fp32",
          {"workload": "quad-pack Qwen2.5-3B-shaped Linear stream, batch-1 decode step",
@@ -360,9 +386,11 @@ def run_dual3b(args, dev, log, tails):
         f"{st.plug_windows} plug window(s) per step")
 
     # sanity: a k_proj against the single-Linear operator; the last down_proj's rows that lie
-    # wholly in the fp16 tail against torch (model 2 has no weights there: 0)
+    # wholly in the fp16 tail against torch (model 2 has no weights there: 0); the CPU
+    # baseline below checks layer 0 against the oracle
     st()
     torch.cuda.synchronize()
+    first = [[o.cpu() for o in outs[p]] for p in range(len(LAYER))]
     amp, cos, sin = pk.header_luts(pack.amp_bits, pack.phase_bits, pack.mu, device=dev)
     n, k = shapes[1]
     pos = int(st.pos0[1])
@@ -394,14 +422,17 @@ def run_dual3b(args, dev, log, tails):
 
     cpu = None
     if not args.no_cpu:
-        c = cpu_baseline_dual(pack, shapes, args.cpu_sample_tuples)
+        c = cpu_baseline_dual(pack, shapes, args.cpu_sample_tuples, xs=[x.cpu() for x in xs[:len(first)]],
+                              outs=first)
         log(f"[bench] cpu baseline: unpack {c['unpack_s']:.2f}s + matmul {c['matmul_s']:.2f}s on "
-            f"{c['sample']} pairs -> {c['step_s']:.2f}s per step (x{c['scale']:.1f})")
+            f"{c['sample']} pairs -> {c['step_s']:.2f}s per step (x{c['scale']:.1f}); GPU outputs of "
+            f"{c['checked']} projections match it (normwise {c['worst_normwise']:.1e})")
         cpu = {"value": algo / c["step_s"] / 1e9, "unit": "GB/s", "cores": c["threads"], "kind": "port",
                "sample": (f"first {c['sample']} pairs of the stream: numpy float64 unpack_dual restatement "
                           f"(1 thread) {c['unpack_s']:.2f}s + torch CPU float32 x@W^T x2 ({c['threads']} "
                           f"threads) {c['matmul_s']:.2f}s, extrapolated x{c['scale']:.1f} to "
-                          f"{c['step_s']:.1f}s per step")}
+                          f"{c['step_s']:.1f}s per step; the GPU outputs of those {c['checked']} projections "
+                          f"match it within rel 1e-3")}
     mode = "5% of model 2 truncated, model 1's rest in fp16 tails" if tails else \
         "model 2 truncated by 5% and zero-padded (.dualpack format)"
     line("achieved HBM GB/s (% of peak) + ms per dual-pack 3B decode step, batch 1", achieved, ms, args, "fp32",

@@ -12,9 +12,10 @@ Same names, arguments, return values and error behaviour as the reference
 * :func:`quad_dequant` -- float32 (or fp16) weights of a code view.
 
 Batches: 1-8 tokens run on the fused decode kernels; 9-128 tokens on the matrix-core
-decode when the codes are an (N,K) block seen as (K,N) (the container layout), 9-64 on
-(K,N) storage after a transpose of the codes (two 8-token fused passes up to 16 tokens
-when K % 32 != 0); larger batches, and more tokens on other layouts, decode once into
+decode when the codes are an (N,K) block seen as (K,N) (the container layout), 9-64
+(9-128 when N <= K) on (K,N) storage after a transpose of the codes (two 8-token fused
+passes up to 16 tokens when K % 32 != 0); larger batches, and more tokens on other
+layouts, decode once into
 fp16 weights (the
 values the reference's kernel rounds its weights to, quad_kernels.py:117-126) and run a
 library fp16 GEMM (hipBLASLt through torch.matmul), where the matmul's compute, not the
@@ -23,12 +24,14 @@ weight stream, bounds the time.
 from __future__ import annotations
 
 import math
+import os
 
 import torch
 
 from . import _native as nat
 
 MU = 255.0   # quad_kernels.py:13
+_CHECK_PLUG = os.environ.get("POLAR_PACK_CHECK_PLUG", "0") == "1"   # verify plug order (one sync per call)
 
 
 def _u32_words(nq, q1, q2, q3):
@@ -96,6 +99,10 @@ def _plug_args(plug, device):
     vals = vals.contiguous()
     if idx.device != device or vals.device != device:
         raise ValueError("plug tensors must be on the codes' device")
+    if _CHECK_PLUG and idx.numel() > 1:
+        pos = idx.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+        if not bool(torch.all(pos[1:] > pos[:-1])):
+            raise ValueError("plug positions must be strictly ascending")
     return idx.data_ptr(), vals.data_ptr(), idx.numel(), (idx, vals)
 
 
@@ -116,7 +123,9 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
     7 tables of :func:`pack_quad_layer` (fp16 or fp32); ``scales`` 4 floats.
     Returns a list of 4 fp16 (M,N) tensors ``out_k = fp16(s_k * a @ W_k)``.
     ``plug=(idx uint32 (P,), vals fp16 (P,4))`` replaces the normalised tuple
-    of the element at storage offset ``idx - elem_base`` of ``codes``.
+    of the element at storage offset ``idx - elem_base`` of ``codes``; ``idx`` must be
+    strictly ascending, as a ``.quadpack`` file stores it (quaternion_packer.py:104-113):
+    checked on the host when ``POLAR_PACK_CHECK_PLUG=1``.
     """
     M, K = a.shape
     K_b, N = codes.shape

@@ -78,15 +78,42 @@ def task_bytes(proj, nrows, shapes, M=1, code_bytes=4):
     return code_bytes * nrows * K + 2 * M * K
 
 
-def wave_bounds(bytes_, n_waves):
-    """Contiguous ranges of tasks per wavefront so that each gets ~1/n_waves of the bytes."""
+def wave_bounds(bytes_, n_waves, weights=None):
+    """Contiguous ranges of tasks per wavefront so that each gets ~1/n_waves of the bytes, or
+    a share proportional to ``weights`` (n_waves values) when given."""
     starts = np.concatenate([[0], np.cumsum(bytes_)[:-1]]) if bytes_.size else np.zeros(0, np.int64)
     total = int(bytes_.sum())
-    targets = np.arange(n_waves + 1, dtype=np.float64) * total / max(n_waves, 1)
+    if weights is None:
+        targets = np.arange(n_waves + 1, dtype=np.float64) * total / max(n_waves, 1)
+    else:
+        w = np.asarray(weights, np.float64)
+        targets = np.concatenate([[0.0], np.cumsum(w)]) * (total / max(w.sum(), 1e-300))
     bounds = np.searchsorted(starts, targets, side="left").astype(np.int64)
     bounds[0] = 0
     bounds[-1] = bytes_.size
     return np.maximum.accumulate(bounds)
+
+
+# Waves w and w + 4 of a workgroup of 8 share a SIMD and the older one wins instruction
+# issue: measured on the quad 3B stream, waves 4-7 of every workgroup take 7.4% longer for
+# the same bytes, so equal shares leave the first four idle at the end (8.6-9.9% of the
+# wave-time idle; 5.2% with these weights, and the launch 2.7% shorter).
+SLOT_FACTOR = 1.074
+DUAL_SLOT_FACTOR = 1.10
+
+
+def slot_weights(n_waves, waves_per_group, factor=SLOT_FACTOR):
+    """Planner weights of the launch's wavefronts (numbered workgroup by workgroup): the
+    younger half of each workgroup's waves gets 1/factor of the older half's share."""
+    w = np.ones(int(n_waves))
+    if waves_per_group >= 2:
+        w[(np.arange(int(n_waves)) % waves_per_group) >= waves_per_group // 2] /= factor
+    return w
+
+
+def _waves_per_group(n_waves, device):
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    return max(1, int(n_waves) // max(1, cus))
 
 
 def split_factors(shapes, n, rows_per_task, n_waves, block=512, positions=None):
@@ -106,7 +133,7 @@ def split_factors(shapes, n, rows_per_task, n_waves, block=512, positions=None):
 
 
 def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=4, split=False, block=512,
-                  positions=None):
+                  positions=None, wave_weights=None, task_cost=0):
     """Per-wave segments (SEG_DTYPE), seg_bounds (n_waves + 1) and the workspace bytes
     for the rows below ``n``.
 
@@ -114,8 +141,9 @@ def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=
     (a single Linear with few rows) every task of a projection is cut into column slices of whole ``block``-column
     chunks (:func:`split_factors`), the
     slices of a projection ordered slice by slice.  The items are dealt to the wavefronts
-    in contiguous runs of equal bytes and each wavefront's run is cut into segments of
-    one projection and one slice.  The workspace of split launches holds one uint32
+    in contiguous runs of equal cost (bytes read, plus ``task_cost`` bytes for each item's
+    reduction and stores), or of cost proportional to ``wave_weights``, and each
+    wavefront's run is cut into segments of one projection and one slice.  The workspace of split launches holds one uint32
     counter per task, then 4*M*N float32 accumulators per split projection.
     """
     proj, row0, nrows = plan_tasks(shapes, n, rows_per_task, positions)
@@ -144,8 +172,8 @@ def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=
         it_k1 = np.concatenate([c[2] for c in chunks])
     it_proj = proj[it_task]
     width = it_k1 - it_k0
-    ib = code_bytes * nrows[it_task] * width + 2 * M * width
-    tb = wave_bounds(ib, n_waves)
+    ib = code_bytes * nrows[it_task] * width + 2 * M * width + int(task_cost)
+    tb = wave_bounds(ib, n_waves, wave_weights)
     wave = np.searchsorted(tb, np.arange(it_task.size), side="right") - 1
     brk = np.ones(it_task.size, bool)
     brk[1:] = (wave[1:] != wave[:-1]) | (it_proj[1:] != it_proj[:-1]) | (it_k0[1:] != it_k0[:-1])
@@ -267,10 +295,12 @@ class QuadStream:
     ``split`` lets a launch with fewer row tasks than half its wavefronts (a single
     Linear with few rows) cut its tasks into column slices whose sums meet in a
     workspace owned by this object (so two launches of one QuadStream must not overlap).
+    ``wave_weights``: per-wave shares of the work ("slots": :func:`slot_weights`; None:
+    equal bytes); ``task_cost``: bytes charged per task for its reduction and stores.
     """
 
     def __init__(self, pack: QuadPackDevice, shapes: Sequence[Tuple[int, int]], M: int = 1, split: bool = True,
-                 positions=None):
+                 positions=None, wave_weights="slots", task_cost=0):
         L = nat.lib()
         self.pack = pack
         self.shapes = [(int(n), int(k)) for n, k in shapes]
@@ -289,9 +319,12 @@ class QuadStream:
                 raise ValueError(f"stream decode needs K % 4 == 0 (got N={n}, K={k})")
         plug = pack.plug_host()
         self.n_waves = int(L.pp_quad_stream_waves(self.M))
+        if isinstance(wave_weights, str) and wave_weights == "slots":
+            wave_weights = slot_weights(self.n_waves, _waves_per_group(self.n_waves, self.device))
         self.segs_np, self.bounds_np, ws_bytes = plan_segments(
             self.shapes, pack.n, plug, self.n_waves, self.rows_per_item, self.M, split=split,
-            block=int(L.pp_quad_stream_chunk(self.M)), positions=self.positions)
+            block=int(L.pp_quad_stream_chunk(self.M)), positions=self.positions, wave_weights=wave_weights,
+            task_cost=task_cost)
         self.tail_items_np = plan_tail_items(self.shapes, pack.n, plug, positions=self.positions)
         self.n_segs = self.segs_np.size
         self.n_tail = self.tail_items_np.size
@@ -405,7 +438,7 @@ class DualStream:
     """
 
     def __init__(self, pack, shapes: Sequence[Tuple[int, int]], M: int = 1, plug_windows=None, split: bool = True,
-                 positions=None):
+                 positions=None, wave_weights="slots", task_cost=0):
         L = nat.lib()
         self.pack = pack
         self.shapes = [(int(n), int(k)) for n, k in shapes]
@@ -426,9 +459,12 @@ class DualStream:
             raise ValueError("dual stream decode needs a power-of-two group_size >= 8 and chunk_size % 8 == 0")
         plug = pack.plug_host()
         self.n_waves = int(L.pp_dual_stream_waves(self.M))
+        if isinstance(wave_weights, str) and wave_weights == "slots":
+            wave_weights = slot_weights(self.n_waves, _waves_per_group(self.n_waves, self.device), DUAL_SLOT_FACTOR)
         self.segs_np, self.bounds_np, ws_bytes = plan_segments(
             self.shapes, pack.n_codes, plug, self.n_waves, self.rows_per_item, self.M, code_bytes=2, split=split,
-            block=int(L.pp_dual_stream_chunk(self.M)), positions=self.positions)
+            block=int(L.pp_dual_stream_chunk(self.M)), positions=self.positions, wave_weights=wave_weights,
+            task_cost=task_cost)
         self.split = bool(np.any(self.segs_np["parts"] > 1))
         # split launches: counters + accumulators, zero once here, left zero by every launch
         self.workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=self.device) if ws_bytes else None
