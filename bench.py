@@ -695,11 +695,24 @@ def run_refbench(args, dev, log):
             tf = (time.perf_counter() - t0) / 100
             per, _ = time_events(lambda: op(a), 30, 5)
             ev = float(np.median(per)) * 1e-3
-            rows.append({"M": M, "packed_ms": round(tq * 1e3, 4), "fp16_matmul_ms": round(tf * 1e3, 4),
-                         "speedup_vs_fp16": round(tf / tq, 3), "packed_event_ms": round(ev * 1e3, 4),
-                         "gbs_event": round(algo(M) / ev / 1e9, 1)})
+            row = {"M": M, "packed_ms": round(tq * 1e3, 4), "fp16_matmul_ms": round(tf * 1e3, 4),
+                   "speedup_vs_fp16": round(tf / tq, 3), "packed_event_ms": round(ev * 1e3, 4),
+                   "gbs_event": round(algo(M) / ev / 1e9, 1)}
+            extra = ""
+            if name == "quad" and M > qk.BIG_MIN_M:
+                # the fused large-batch kernel at every size (the operator's default above
+                # BIG_MAX_M tokens is the fp16 decode + one batched GEMM)
+                fz = lambda: qk.quad_bitpacked(a, codes, luts, scales, fused=True)
+                for o, r in zip(fz(), want):
+                    d = (o.float() - r.float()).abs().max().item()
+                    if not d <= 0.05 * r.float().abs().max().item():
+                        raise SystemExit(f"refbench fused M={M}: max |diff| {d} vs fp16 matmul")
+                per, _ = time_events(fz, 30, 5)
+                row["fused_event_ms"] = round(float(np.median(per)), 4)
+                extra = f", fused kernel {row['fused_event_ms']:.3f} ms"
+            rows.append(row)
             log(f"[bench] refbench {name} M={M}: {tq * 1e3:.3f} ms (events {ev * 1e3:.3f} ms) vs fp16 "
-                f"{tf * 1e3:.3f} ms -> {tf / tq:.2f}x")
+                f"{tf * 1e3:.3f} ms -> {tf / tq:.2f}x{extra}")
         first = rows[0]
         achieved = algo(1) / (first["packed_event_ms"] * 1e-3) / 1e9
         line(f"ms per {name} drop-in call on 4096x4096 weights vs fp16 matmul (the reference's own benchmark)",

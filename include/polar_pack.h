@@ -239,6 +239,36 @@ int64_t pp_quad_mfma_workspace_size(int64_t M, int64_t N, int64_t slices);
 /* Wavefronts the batch decode launches for M tokens (the host sizes the slices for them). */
 int64_t pp_quad_mfma_waves(int64_t M);
 
+/*
+ * Large-batch decode GEMM on the matrix cores (any M >= 1; used for more than 64 tokens):
+ * the same product as pp_quad_mfma, fused, replacing the reference's tl.dot path for
+ * its prefill batch sizes (quad_kernels.py:53-67, 123-134, 166-189), with no weight
+ * written to memory.  Each code word is decoded once per 128 tokens.
+ *   layout PP_QUAD_NK: codes (N,K) row-major, row n at codes + n*ldc (ldc >= K, a
+ *                      multiple of 4, 16-byte aligned): the container stream layout;
+ *   layout PP_QUAD_KN: codes (K,N), row k at codes + k*ldc (ldc >= N): the layout
+ *                      pack_quad_layer returns (quad_kernels.py:46-50).
+ * K % 32 == 0.  Plug entries (sorted positions, normalised fp16 tuples) are read in an
+ * (N,K) frame: the entry of (row n, column k) has position plug_pos0 + n*plug_ld + k
+ * (for PP_QUAD_NK storage elem_base and ldc; for PP_QUAD_KN the host moves the positions
+ * of the (K,N) storage there and sorts them).  row_plug[n*slices + s] (N*slices + 1
+ * entries) is the first entry at or after plug_pos0 + n*plug_ld + s*slice_cols, the last
+ * one plug_pos0 + N*plug_ld.  slices / slice_cols come from pp_quad_big_plan; with
+ * slices > 1 the workspace (pp_quad_big_workspace_size bytes) holds float32 partial sums:
+ * zero before the first call, left zero by every call; calls that share it must not
+ * overlap.  No counterpart kernel in the reference.
+ */
+enum pp_quad_layout { PP_QUAD_NK = 0, PP_QUAD_KN = 1 };
+int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const void* a, int64_t a_sm,
+                const void* const* luts, int lut_dtype, const float* scales,
+                const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n, const int64_t* row_plug,
+                int64_t plug_pos0, int64_t plug_ld, int64_t slices, int64_t slice_cols,
+                void* const* out, int64_t o_sm, int64_t M, int64_t N, int64_t K,
+                void* workspace, int64_t workspace_bytes, void* stream);
+/* K slices for pp_quad_big at this shape on the current device. */
+int pp_quad_big_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* slice_cols);
+int64_t pp_quad_big_workspace_size(int64_t M, int64_t N, int64_t slices);
+
 /* Rows per wavefront task the stream decode uses for M tokens (0 and an error for bad M). */
 int pp_quad_stream_rows(int64_t M);
 /* Columns the stream decode reads per row and step for M tokens (0 for bad M): split

@@ -14,6 +14,7 @@ from .build import LIB
 PP_OK, PP_EINVAL, PP_EHIP, PP_ENOSUPPORT = 0, 1, 2, 3
 PP_F16, PP_F32 = 0, 1
 PP_DUAL_I16_OFFSET, PP_DUAL_U16_BE = 0, 1
+PP_QUAD_NK, PP_QUAD_KN = 0, 1
 PP_ITEM_TAIL = 1
 PP_ITEM_FP16 = 2
 
@@ -62,6 +63,10 @@ EXPORTS = {
                            vp, i64, vp]),
     "pp_quad_mfma_workspace_size": (i64, [i64, i64, i64]),
     "pp_quad_mfma_waves": (i64, [i64]),
+    "pp_quad_big": (i32, [vp, i32, i64, vp, i64, vp, i32, vp, vp, vp, i64, vp, i64, i64, i64, i64, vp, i64, i64, i64,
+                          i64, vp, i64, vp]),
+    "pp_quad_big_plan": (i32, [i64, i64, i64, vp, vp]),
+    "pp_quad_big_workspace_size": (i64, [i64, i64, i64]),
     "pp_quad_stream_rows": (i32, [i64]),
     "pp_quad_stream_chunk": (i32, [i64]),
     "pp_quad_stream_waves": (i64, [i64]),

@@ -1,0 +1,410 @@
+// Quad-pack decode GEMM for large batches (more than 64 tokens) on the matrix cores: one
+// fused pass produces the 4 models' outputs
+//   out_m[j, n] = fp16( s_m * sum_k x[j, k] * W_m[n, k] )
+// (quad_kernels.py:123-134) with W_m decoded from the codes in registers
+// (quad_kernels.py:103-121, quaternion_packer.py:173-185), the plug table patched into
+// the decoded operands (quaternion_packer.py:187-193), and no weight ever written to
+// memory.
+//
+// Work item = 16 weight rows x 128 tokens x one K slice, one wavefront,
+// v_mfma_f32_16x16x32_f16 (operand layouts as in quad_mfma.hip):
+//  * per 32-column step a lane decodes 8 code words of its row (n0 + i, i = lane % 16,
+//    columns k0 + 8(lane/16) .. +7), so each code word is decoded once per 128 tokens and
+//    feeds 4 models x 8 token tiles of products;
+//  * x is the B operand as stored: lane l reads tokens 16t + l%16 at the same 8 columns;
+//  * 4 models x 8 token tiles of 16 x 16 fp32 sums stay in registers, with two buffers
+//    each of codes (loaded a step ahead), of x (loaded a step before the products that
+//    use it) and of decoded operands: a wavefront takes a SIMD's register file (4 waves per
+//    workgroup, one workgroup per CU: the decode tables fill the LDS);
+//  * the products of step s - 1 are issued between the arithmetic of step s (the only
+//    wave on its SIMD has no other wave to overlap them with), after step s's LDS lookups.
+// Codes in either storage: (N,K) rows (the stream container, K contiguous: two 16-byte
+// loads per step) or (K,N) (pack_quad_layer, N contiguous: 8 four-byte loads per step,
+// each a 64-byte run over 16 lanes).  Plug positions are read in an (N,K) frame (position
+// ppos0 + n*pld + k): for (K,N) storage the host moves them there first.
+// Slices: with one slice a wave writes its fp16 outputs; otherwise it adds its scaled sums
+// into float32 accumulators [m][n][j] with device-scope atomics and quad_big_finish_kernel
+// writes the outputs and leaves zeros for the next launch.
+#include "quad_mfma.h"
+
+namespace pp {
+
+constexpr int QB_NT = 256;      // 4 waves, one per SIMD
+constexpr int QB_WAVES = QB_NT / 64;
+constexpr int QB_ROWS = 16;     // weight rows per item
+constexpr int QB_TT = 8;        // 16-token tiles per item
+constexpr int QB_GROUP = 2;     // steps per loop pass (2 code buffers, 2 x buffers, 2 operand sets)
+
+struct QuadBigArgs {
+  const uint32_t* codes;
+  int64_t ldc;             // (N,K) storage: words between rows n; (K,N): words between rows k
+  const f16* x;            // (M, K), row stride x_sm
+  int64_t x_sm;
+  f16* out[4];             // (M, N), row stride o_sm
+  int64_t o_sm;
+  int N, K, M;
+  int tiles, tblocks;      // ceil(N / 16), ceil(M / 128)
+  int slices, ks;          // K slices of ks columns (a multiple of 32)
+  QuadLuts luts;
+  float s[4];
+  PlugSrc plug;
+  const int64_t* row_plug; // [n*slices + s]: first plug entry of (row n, slice s); N*slices + 1 entries
+  int64_t ppos0, pld;      // plug position of (row n, column k): ppos0 + n*pld + k
+  float* acc;              // slices > 1: [4][N][M] float32, zero on entry
+  int xcd_remap;           // grid a multiple of 8: consecutive items on the workgroups of one XCD
+  int vec_out;             // outputs 8-byte aligned with o_sm % 4 == 0: 4 rows per store
+};
+
+struct QbCodes {
+  u32x4 c[2];              // 8 code words of the lane's row
+};
+struct QbX {
+  u32x4 xb[QB_TT];         // 8 fp16 x of token 16t + l%16
+};
+
+// Issue the code loads of the step at column k0 (clamped to the last step: a step past the
+// slice end reads valid codes whose products are zero).  voc: the lane's code offset (OOB
+// for a row past N).  (K,N) storage: the 8 columns' rows are 4*ldc bytes apart, an offset
+// carried in the scalar operand.
+template <bool KN>
+__device__ __forceinline__ void qb_codes(const QuadBigArgs& A, const uint32_t* ctile, int n0, int k0, uint32_t voc,
+                                         QbCodes& S) {
+  k0 = min(k0, A.K - 32);
+  if constexpr (!KN) {
+    const int nr = min(QB_ROWS, A.N - n0);
+    const rsrc_t rc = make_rsrc(ctile + k0, 4u * (uint32_t)((int64_t)(nr - 1) * A.ldc + (A.K - k0)));
+    vload128(S.c[0], voc, rc);
+    vload128(S.c[1], voc + 16u, rc);
+  } else {
+    const rsrc_t rc = make_rsrc(ctile + (int64_t)k0 * A.ldc,
+                                4u * (uint32_t)((int64_t)(A.K - 1 - k0) * A.ldc + (A.N - n0)));
+    const int st = (int)(4 * A.ldc);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) S.c[e >> 2][e & 3] = __builtin_amdgcn_raw_buffer_load_b32(rc, (int)voc, e * st, NT_AUX);
+  }
+}
+
+// Issue the x loads of the step at column k0: vox, the lane's offsets per token tile (OOB
+// past M).  A step at or past the slice end ke (the walk runs whole groups of steps) reads
+// through an empty buffer record, i.e. zeros, so its products add nothing.
+__device__ __forceinline__ void qb_x(const QuadBigArgs& A, int k0, int ke, const uint32_t (&vox)[QB_TT],
+                                     const f16* xblk, int j0, QbX& S) {
+  const uint32_t xrec = k0 < ke ? 2u * (uint32_t)((int64_t)(A.M - 1 - j0) * A.x_sm + (ke - k0)) : 0u;
+  const rsrc_t rx = make_rsrc(xblk + min(k0, A.K - 32), xrec);
+#pragma unroll
+  for (int t = 0; t < QB_TT; ++t) vload128c(S.xb[t], vox[t], rx);
+}
+
+// The LDS lookups of 8 code words, issued together, and the arithmetic on them.
+struct Look8 {
+  float r[8];
+  float2 a[8], b[8], c[8];
+};
+
+template <class L>
+__device__ __forceinline__ void look8(const char* lds, const LaneOff& lo, const u32x4& c0, const u32x4& c1,
+                                      Look8& o) {
+  const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) lookup<L>(lds, cw[e], lo, o.r[e], o.a[e], o.b[e], o.c[e]);
+}
+
+__device__ __forceinline__ void math8(const Look8& o, h8 (&a)[4]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float rs = o.r[e] * o.a[e].y, rss = rs * o.b[e].y;
+    a[0][e] = (_Float16)(o.r[e] * o.a[e].x);
+    a[1][e] = (_Float16)(rs * o.b[e].x);
+    a[2][e] = (_Float16)(rss * o.c[e].x);
+    a[3][e] = (_Float16)(rss * o.c[e].y);
+  }
+}
+
+template <bool KN, bool PLUG, class L>
+struct QbRun {
+  const char* lds;
+  LaneOff lo;
+  const QuadBigArgs& A;
+  const uint32_t* ctile;
+  const f16* xblk;
+  int n0, j0, q, ke;
+  uint32_t voc;
+  uint32_t vox[QB_TT];
+  int64_t rowpos;
+  MPlug P;
+  f4 C[4][QB_TT];
+
+  __device__ __forceinline__ void mfma(const h8 (&a)[4], const QbX& S) {
+#pragma unroll
+    for (int t = 0; t < QB_TT; ++t) {
+      const h8 b = __builtin_bit_cast(h8, S.xb[t]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) C[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b, C[m][t], 0, 0, 0);
+    }
+  }
+
+  // Step at k0: issue the code loads of k0 + 32 into nxt and the x loads of k0 into xnow
+  // (used by the next step), look up cur's codes, then the products of the previous step
+  // (operands aprev, x in xprev) interleaved with the arithmetic of this one into anew.
+  __device__ __forceinline__ void step(const QbCodes& cur, QbCodes& nxt, QbX& xnow, const QbX& xprev,
+                                       const h8 (&aprev)[4], h8 (&anew)[4], int k0) {
+    qb_codes<KN>(A, ctile, n0, k0 + 32, voc, nxt);
+    qb_x(A, k0, ke, vox, xblk, j0, xnow);
+    Look8 lk;
+    look8<L>(lds, lo, cur.c[0], cur.c[1], lk);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma(aprev, xprev);
+    math8(lk, anew);
+    // 32 products, 64 arithmetic instructions: one product, then two
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PLUG) mplug_patch(A.plug, P, rowpos, k0 + 8 * q, k0, anew);
+  }
+};
+
+template <bool KN, bool PLUG, class L>
+__device__ __forceinline__ void qb_body(const char* lds, const QuadBigArgs& A) {
+  const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+  const LaneOff lo = L::lane(lane);
+  int b = blockIdx.x;
+  if (A.xcd_remap) b = (b & 7) * (int)(gridDim.x >> 3) + (b >> 3);
+  const int64_t gw = (int64_t)b * QB_WAVES + uniform(threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * QB_WAVES;
+  // Items in groups of QB_WAVES row tiles that share a token block and K slice, one group
+  // per workgroup (its waves read the same x, through the CU's L1); groups ordered slice,
+  // token block, row tiles, so the workgroups of one XCD (consecutive after the remap)
+  // share row tiles (codes) and token blocks (x) through its L2.
+  const int64_t tgroups = (A.tiles + QB_WAVES - 1) / QB_WAVES;
+  const int64_t items = tgroups * QB_WAVES * A.tblocks * A.slices;
+  for (int64_t it = gw; it < items; it += nw) {
+    const int64_t w = uniform64(it / QB_WAVES);
+    const int tile = (int)(uniform64(w / ((int64_t)A.slices * A.tblocks)) * QB_WAVES + it % QB_WAVES);
+    const int sl = (int)(w % A.slices), tb = (int)((w / A.slices) % A.tblocks);
+    if (tile >= A.tiles) continue;
+    const int n0 = tile * QB_ROWS, j0 = tb * 16 * QB_TT;
+    const int kb = sl * A.ks, ke = min(A.K, kb + A.ks);
+    QbRun<KN, PLUG, L> R{lds, lo, A, KN ? A.codes + n0 : A.codes + (int64_t)n0 * A.ldc,
+                         A.x + (int64_t)j0 * A.x_sm, n0, j0, q, ke};
+#pragma unroll
+    for (int t = 0; t < QB_TT; ++t) {
+      const int jl = 16 * t + i;
+      R.vox[t] = j0 + jl < A.M ? 2u * (uint32_t)(jl * A.x_sm + 8 * q) : OOB;
+    }
+    const int n = n0 + i;
+    const bool ok = n < A.N;
+    R.voc = !ok ? OOB : KN ? 4u * (uint32_t)(8 * q * A.ldc + i) : 4u * (uint32_t)(i * A.ldc + 8 * q);
+    uint32_t pidx[4];
+    if constexpr (PLUG) {
+      R.rowpos = A.ppos0 + (int64_t)n * A.pld;
+      R.P.next = ok ? A.row_plug[(int64_t)n * A.slices + sl] : 0;
+      R.P.end = ok ? A.row_plug[(int64_t)n * A.slices + sl + 1] : 0;
+      mplug_issue(A.plug, R.P, pidx);
+    }
+    QbCodes C0, C1;
+    QbX X0, X1;
+    qb_codes<KN>(A, R.ctile, n0, kb, R.voc, C0);
+    if constexpr (PLUG) mplug_take(R.P, pidx, R.rowpos);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int t = 0; t < QB_TT; ++t) R.C[m][t] = f4{0.f, 0.f, 0.f, 0.f};
+    // step s reads code buffer s % 2, loads x buffer s % 2 and writes operand set s % 2;
+    // the "previous step" of the first one multiplies zeros
+    h8 Aa[4], Ab[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) Ab[m] = h8{};
+#pragma unroll
+    for (int t = 0; t < QB_TT; ++t) X1.xb[t] = u32x4{0u, 0u, 0u, 0u};
+    // whole groups of steps with no exit between them, so that each load is issued in the
+    // step that starts it (not moved by the compiler towards the block that reads it)
+    int k0 = kb;
+    for (; k0 < ke; k0 += 32 * QB_GROUP) {
+      R.step(C0, C1, X0, X1, Ab, Aa, k0);
+      R.step(C1, C0, X1, X0, Aa, Ab, k0 + 32);
+    }
+    R.mfma(Ab, X1);   // the last step's products
+    // epilogue: lane holds rows n0 + 4q + r, r = 0..3, of token j0 + 16t + i
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int t = 0; t < QB_TT; ++t) {
+        const int j = j0 + 16 * t + i;
+        const int nn = n0 + 4 * q;
+        const f4 c = R.C[m][t] * A.s[m];
+        if (j >= A.M || nn >= A.N) continue;
+        if (A.slices == 1) {
+          f16* o = A.out[m] + (int64_t)j * A.o_sm + nn;
+          if (A.vec_out && nn + 3 < A.N) {
+            const f16x4 h = {(f16)c[0], (f16)c[1], (f16)c[2], (f16)c[3]};
+            *reinterpret_cast<f16x4*>(o) = h;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (nn + r < A.N) o[r] = (f16)c[r];
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (nn + r < A.N)
+              __hip_atomic_fetch_add(A.acc + ((int64_t)m * A.N + nn + r) * A.M + j, c[r], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+  }
+}
+
+template <bool KN>
+__global__ __launch_bounds__(QB_NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void quad_big_kernel(
+    const QuadBigArgs A) {
+  __shared__ __attribute__((aligned(16))) uint32_t Tb[QLDS_BYTES / 4];
+  const char* lds = reinterpret_cast<const char*>(Tb);
+  const bool shared = quad_tables<QB_NT>(Tb, A.luts);
+  if (A.plug.n > 0) {
+    if (shared) qb_body<KN, true, LayShared>(lds, A);
+    else qb_body<KN, true, LaySplit>(lds, A);
+  } else {
+    if (shared) qb_body<KN, false, LayShared>(lds, A);
+    else qb_body<KN, false, LaySplit>(lds, A);
+  }
+}
+
+// Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero.  Runs after the
+// item kernel has completed, so its atomics are visible to plain loads.  Thread = 4
+// consecutive tokens of one (model, row).
+__global__ __launch_bounds__(256) void quad_big_finish_kernel(float* acc, f16* o0, f16* o1, f16* o2, f16* o3,
+                                                              int64_t o_sm, int N, int M) {
+  const int64_t total = 4ll * N * M;
+  const int64_t i0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+  if (i0 >= total) return;
+  float v[4];
+  if (M % 4 == 0) {
+    const float4 t = *reinterpret_cast<const float4*>(acc + i0);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    *reinterpret_cast<float4*>(acc + i0) = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = i0 + e < total ? acc[i0 + e] : 0.f;
+      if (i0 + e < total) acc[i0 + e] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t idx = i0 + e;
+    if (idx >= total) break;
+    const int j = (int)(idx % M);
+    const int64_t mn = idx / M;
+    const int row = (int)(mn % N), m = (int)(mn / N);
+    f16* o = m == 0 ? o0 : m == 1 ? o1 : m == 2 ? o2 : o3;
+    o[(int64_t)j * o_sm + row] = (f16)v[e];
+  }
+}
+
+
+// K slices for an (N, K) product at M tokens: as many whole 32-column slices as keep the
+// items within one per wavefront.
+static void qb_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* cols) {
+  const int64_t waves = (int64_t)device_cu_count() * QB_WAVES;
+  const int64_t units = ((N + QB_ROWS - 1) / QB_ROWS) * ((M + 16 * QB_TT - 1) / (16 * QB_TT));
+  int64_t s = std::max<int64_t>(1, std::min<int64_t>(K / 32, waves / std::max<int64_t>(1, units)));
+  const int64_t per = (K + s - 1) / s;
+  int64_t c = (per + 32 * QB_GROUP - 1) / (32 * QB_GROUP) * (32 * QB_GROUP);   // whole groups of steps
+  if ((K + c - 1) / c != s) c = (per + 31) / 32 * 32;
+  *cols = c;
+  *slices = (K + c - 1) / c;
+}
+
+}  // namespace pp
+
+using namespace pp;
+
+extern "C" int pp_quad_big_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* slice_cols) {
+  PP_REQUIRE(slices != nullptr && slice_cols != nullptr, "null pointer argument");
+  PP_REQUIRE(M >= 1 && N >= 1 && K >= 32, "needs M, N >= 1 and K >= 32");
+  qb_plan(M, N, K, slices, slice_cols);
+  return PP_OK;
+}
+
+extern "C" int64_t pp_quad_big_workspace_size(int64_t M, int64_t N, int64_t slices) {
+  if (slices <= 1) return 0;
+  return (4 * N * M * 4 + 255) / 256 * 256;
+}
+
+extern "C" int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const void* a, int64_t a_sm,
+                           const void* const* luts, int lut_dtype, const float* scales, const uint32_t* plug_idx,
+                           const void* plug_vals, int64_t plug_n, const int64_t* row_plug, int64_t plug_pos0,
+                           int64_t plug_ld, int64_t slices, int64_t slice_cols, void* const* out, int64_t o_sm,
+                           int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
+  PP_REQUIRE(codes != nullptr && a != nullptr && out != nullptr && luts != nullptr && scales != nullptr,
+             "null pointer argument");
+  for (int m = 0; m < 4; ++m) PP_REQUIRE(out[m] != nullptr, "out[%d] is null", m);
+  for (int i = 0; i < 7; ++i) PP_REQUIRE(luts[i] != nullptr, "lut %d is null", i);
+  PP_REQUIRE(lut_dtype == PP_F16 || lut_dtype == PP_F32, "bad lut_dtype");
+  PP_REQUIRE(layout == PP_QUAD_NK || layout == PP_QUAD_KN, "layout must be PP_QUAD_NK or PP_QUAD_KN");
+  PP_REQUIRE(M >= 1 && N >= 1 && K >= 32 && K % 32 == 0, "needs M, N >= 1 and K a multiple of 32 (N=%lld, K=%lld)",
+             (long long)N, (long long)K);
+  const bool kn = layout == PP_QUAD_KN;
+  PP_REQUIRE(kn ? ldc >= N : (ldc >= K && ldc % 4 == 0 && aligned(codes, 16)),
+             "codes: (N,K) rows must be 16-byte aligned with ldc >= K words (a multiple of 4); (K,N) rows need "
+             "ldc >= N");
+  PP_REQUIRE(aligned(codes, 4), "codes must be 4-byte aligned");
+  PP_REQUIRE(aligned(a, 16) && (M == 1 || (a_sm >= K && a_sm % 8 == 0)),
+             "activations must be 16-byte aligned with a row stride that is a multiple of 8");
+  PP_REQUIRE(o_sm >= N, "o_sm must be >= N");
+  PP_REQUIRE(slices >= 1 && slice_cols >= 32 && slice_cols % 32 == 0 && slices * slice_cols >= K &&
+                 (slices - 1) * slice_cols < K,
+             "slices x slice_cols must cover K in multiples of 32 columns");
+  PP_REQUIRE(plug_n >= 0 && (plug_n == 0 || (plug_idx && plug_vals && row_plug)), "plug arrays are null");
+  PP_REQUIRE(plug_n < (1ll << 28), "at most 2^28 plug entries");
+  PP_REQUIRE((kn ? K * ldc * 4 : QB_ROWS * ldc * 4) < (1ll << 31) && (M - 1) * a_sm + K < (1ll << 30),
+             "the codes a launch walks and the activations must each stay below 2 GiB");
+  const int64_t need = pp_quad_big_workspace_size(M, N, slices);
+  PP_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), "workspace too small: need %lld bytes",
+             (long long)need);
+  QuadBigArgs A = {};
+  A.codes = codes;
+  A.ldc = ldc;
+  A.x = reinterpret_cast<const f16*>(a);
+  A.x_sm = M > 1 ? a_sm : K;
+  bool vec = o_sm % 4 == 0;
+  for (int m = 0; m < 4; ++m) {
+    A.out[m] = reinterpret_cast<f16*>(out[m]);
+    vec = vec && aligned(out[m], 8);
+  }
+  A.vec_out = vec;
+  A.o_sm = o_sm;
+  A.N = (int)N;
+  A.K = (int)K;
+  A.M = (int)M;
+  A.tiles = (int)((N + QB_ROWS - 1) / QB_ROWS);
+  A.tblocks = (int)((M + 16 * QB_TT - 1) / (16 * QB_TT));
+  A.slices = (int)slices;
+  A.ks = (int)slice_cols;
+  for (int i = 0; i < 7; ++i) A.luts.p[i] = luts[i];
+  A.luts.dtype = lut_dtype;
+  for (int m = 0; m < 4; ++m) A.s[m] = scales[m];
+  A.plug = PlugSrc{plug_idx, reinterpret_cast<const f16*>(plug_vals), plug_n};
+  A.row_plug = row_plug;
+  A.ppos0 = plug_pos0;
+  A.pld = plug_ld;
+  A.acc = reinterpret_cast<float*>(workspace);
+  const int64_t groups = (int64_t)(A.tiles + QB_WAVES - 1) / QB_WAVES * A.tblocks * slices;
+  const int64_t cus = device_cu_count();
+  int64_t grid = std::min<int64_t>(cus, groups);
+  A.xcd_remap = grid % 8 == 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (kn) hipLaunchKernelGGL((quad_big_kernel<true>), dim3((unsigned)grid), dim3(QB_NT), 0, st, A);
+  else hipLaunchKernelGGL((quad_big_kernel<false>), dim3((unsigned)grid), dim3(QB_NT), 0, st, A);
+  PP_LAUNCH_CHECK();
+  if (slices > 1) {
+    const int64_t total = 4 * N * M;
+    hipLaunchKernelGGL(quad_big_finish_kernel, dim3((unsigned)((total / 4 + 255) / 256 + 1)), dim3(256), 0, st,
+                       A.acc, A.out[0], A.out[1], A.out[2], A.out[3], o_sm, A.N, A.M);
+    PP_LAUNCH_CHECK();
+  }
+  return PP_OK;
+}

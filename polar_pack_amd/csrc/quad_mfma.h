@@ -1,0 +1,104 @@
+// Device helpers shared by the matrix-core quad decode kernels (quad_mfma.hip: 1..64
+// tokens, quad_big.hip: larger batches): the decode of 8 code words into the fp16 A
+// operands of v_mfma_f32_16x16x32_f16 for the 4 models, and the per-lane window of plug
+// entries patched into those operands (quaternion_packer.py:187-193).
+#pragma once
+
+#include "quad_lds.h"
+#include "rows_common.h"
+
+namespace pp {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// The plug table: sorted stream positions and (P, 4) normalised fp16 values.
+struct PlugSrc {
+  const uint32_t* idx;
+  const f16* vals;
+  int64_t n;
+};
+
+// The lane's window of 4 plug entries of its row: columns (INT_MAX past the end, INT_MIN
+// once applied) and values.
+struct MPlug {
+  int k[4];
+  u32x2 v[4];
+  int64_t next, end;       // next entry to load, end of the row's entries in the slice
+};
+
+// Load the next 4 entries of the row (bounds-checked buffer loads, nothing past `end`).
+__device__ __forceinline__ void mplug_issue(const PlugSrc& S, MPlug& P, uint32_t (&idx)[4]) {
+  const rsrc_t ri = make_rsrc(S.idx, 4u * (uint32_t)S.n);
+  const rsrc_t rv = make_rsrc(S.vals, 8u * (uint32_t)S.n);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t e = P.next + i;
+    const bool has = e < P.end;
+    vload32(idx[i], has ? 4u * (uint32_t)e : OOB, ri);
+    vload64(P.v[i], has ? 8u * (uint32_t)e : OOB, rv);
+  }
+}
+__device__ __forceinline__ void mplug_take(MPlug& P, const uint32_t (&idx)[4], int64_t rowpos) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) P.k[i] = P.next + i < P.end ? (int)((int64_t)idx[i] - rowpos) : 0x7FFFFFFF;
+  P.next += 4;
+}
+
+// Decode 8 code words into the fp16 A operands of the 4 models (each tuple rounded
+// once, as soon as it is decoded: the fp32 values are not kept).
+template <class L>
+__device__ __forceinline__ void decode8(const char* lds, const LaneOff& lo, const u32x4& c0, const u32x4& c1,
+                                        h8 (&a)[4]) {
+  const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float r;
+    float2 ta, tb, tc;
+    lookup<L>(lds, cw[e], lo, r, ta, tb, tc);
+    const float rs = r * ta.y, rss = rs * tb.y;
+    a[0][e] = (_Float16)(r * ta.x);
+    a[1][e] = (_Float16)(rs * tb.x);
+    a[2][e] = (_Float16)(rss * tc.x);
+    a[3][e] = (_Float16)(rss * tc.y);
+  }
+}
+
+// Patch the plug entries of the lane's 8 columns kk .. kk+7 (step columns ks .. ks+31)
+// into its operands: the decoded tuple is replaced by the plug values, one entry per
+// pass (two in one lane's 8 columns of one step are rare); a window used up within the
+// step is refilled.  Wave-uniform control flow: the common case is one compare per
+// window entry and one ballot.
+__device__ __forceinline__ void mplug_patch(const PlugSrc& S, MPlug& P, int64_t rowpos, int kk, int ks, h8 (&a)[4]) {
+  for (;;) {
+    int hit = -1;
+#pragma unroll
+    for (int i = 3; i >= 0; --i) hit = (unsigned)(P.k[i] - kk) < 8u ? i : hit;
+    if (__ballot(hit >= 0)) {
+      const int e = hit >= 0 ? (hit == 0 ? P.k[0] : hit == 1 ? P.k[1] : hit == 2 ? P.k[2] : P.k[3]) - kk : -1;
+      const u32x2 pv2 = hit == 0 ? P.v[0] : hit == 1 ? P.v[1] : hit == 2 ? P.v[2] : P.v[3];
+      const f16x4 pv = __builtin_bit_cast(f16x4, pv2);
+      const _Float16 v[4] = {(_Float16)pv.x, (_Float16)pv.y, (_Float16)pv.z, (_Float16)pv.w};
+#pragma unroll
+      for (int ee = 0; ee < 8; ++ee)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) a[m][ee] = e == ee ? v[m] : a[m][ee];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) P.k[i] = hit == i ? (int)0x80000000 : P.k[i];
+      continue;
+    }
+    const bool refill = P.k[3] < ks + 32 && P.next < P.end;
+    if (!__ballot(refill)) break;
+    // rare: load and wait here, so no load is left in flight past this branch (a
+    // possibly pending load would make every later wait drain the prefetch too)
+    uint32_t idx[4];
+    MPlug R = P;
+    mplug_issue(S, R, idx);
+    asm volatile("" : : "v"(idx[0]), "v"(idx[1]), "v"(idx[2]), "v"(idx[3]), "v"(R.v[0]), "v"(R.v[1]), "v"(R.v[2]),
+                 "v"(R.v[3]));
+    mplug_take(R, idx, rowpos);
+    if (refill) P = R;
+  }
+}
+
+}  // namespace pp

@@ -23,6 +23,7 @@ weight stream, bounds the time.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 import os
 
@@ -116,7 +117,7 @@ def _check_device(*ts):
     return dev
 
 
-def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
+def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None):
     """4 GEMMs from one packed pass (quad_kernels.py:146-159).
 
     ``a`` fp16 (M,K); ``codes`` uint32 (K,N) view (any strides); ``luts`` the
@@ -126,6 +127,10 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
     of the element at storage offset ``idx - elem_base`` of ``codes``; ``idx`` must be
     strictly ascending, as a ``.quadpack`` file stores it (quaternion_packer.py:104-113):
     checked on the host when ``POLAR_PACK_CHECK_PLUG=1``.
+    ``fused`` (batches above 64 tokens on (N,K) or (K,N) storage): True runs the fused
+    large-batch kernel at any size, False decodes fp16 weights and runs a library GEMM,
+    None (default) picks by size (the fused kernel up to BIG_MAX_M tokens, where it is
+    the faster; above, the decode + GEMM, which needs 8 bytes of scratch per code word).
     """
     M, K = a.shape
     K_b, N = codes.shape
@@ -147,11 +152,16 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
     pi, pv, pn, keep = _plug_args(plug, dev)
     L = nat.lib()
     kn = _kn_layout_ok(codes, K, N)
-    if kn and 8 < M <= (KN_MFMA_MAX_M if N > K else PREFILL_M) and K % 32 == 0:
+    big = _big_layout(codes, K, N) if M > BIG_MIN_M else None
+    if big is not None and (fused or (fused is None and M <= BIG_MAX_M)):
+        _quad_big(a, codes, big, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
+        del keep
+        return outs
+    if big is None and kn and 8 < M <= (KN_MFMA_MAX_M if N > K else PREFILL_M) and K % 32 == 0:
         _quad_kn_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
         del keep
         return outs
-    if M > PREFILL_M or (M > 8 and not _mfma_layout_ok(codes, K) and not (kn and M <= KN_MAX_M)):
+    if M > PREFILL_M or big is not None or (M > 8 and not _mfma_layout_ok(codes, K) and not (kn and M <= KN_MAX_M)):
         _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base), outs, L, dev)
         del keep
         return outs
@@ -178,7 +188,11 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0):
     return outs
 
 
-PREFILL_M = 128   # batches above this decode once and run a library GEMM on every layout
+BIG_MIN_M = 64    # larger batches on (N,K) or (K,N) storage run the fused large-batch kernel ...
+BIG_MAX_M = 128   # ... up to this size by default; above, the fp16 decode + one library GEMM is
+# faster (4096x4096 layer, measured: fused 87.5 us at 128 tokens against 128 us for 4 fp16
+# matmuls; at 1024 tokens fused 291 us, decode 32 us + one batched GEMM 113 us)
+PREFILL_M = 128   # other layouts: batches above this decode once and run a library GEMM
 KN_MAX_M = 16     # (K,N) storage, K % 32 != 0: up to two 8-token passes of the fused kernel
 # (K,N) storage, K % 32 == 0: codes transposed to (N,K) for the matrix cores, up to 64
 # tokens, or up to PREFILL_M when N <= K (measured: 4096x4096 and 11008x2048 gain at 65-128
@@ -227,11 +241,67 @@ def _kn_layout_ok(codes, K, N):
         and K % 8 == 0 and codes.data_ptr() % 16 == 0
 
 
+def _big_layout(codes, K, N):
+    """The storage the large-batch kernel reads: PP_QUAD_NK for (N,K) rows seen as (K,N)
+    (the stream container), PP_QUAD_KN for (K,N) rows with unit column stride
+    (pack_quad_layer); None for other strides or K % 32 != 0."""
+    if K % 32:
+        return None
+    if _mfma_layout_ok(codes, K):
+        return nat.PP_QUAD_NK
+    if codes.stride(1) == 1 and codes.stride(0) >= N:
+        return nat.PP_QUAD_KN
+    return None
+
+
+def _quad_big(a, codes, layout, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
+    """More than 64 tokens on (N,K) or (K,N) storage: the fused large-batch decode
+    (pp_quad_big).  Plug entries are located per (row, K slice) with searchsorted
+    (quaternion_packer.py:188-189); on (K,N) storage they are first moved to the (N,K)
+    frame the kernel reads them in."""
+    M, K = a.shape
+    N = codes.shape[1]
+    if a.stride(1) != 1 or a.data_ptr() % 16 or (M > 1 and a.stride(0) % 8):
+        a = a.contiguous()
+    plan = (ctypes.c_int64 * 2)()
+    nat.check(L.pp_quad_big_plan(M, N, K, ctypes.byref(plan, 0), ctypes.byref(plan, 8)), "pp_quad_big_plan")
+    slices, cols = int(plan[0]), int(plan[1])
+    if layout == nat.PP_QUAD_NK:
+        ldc = codes.stride(1)
+        pos0, pld = elem_base, ldc
+    else:
+        ldc = codes.stride(0)
+        pos0, pld = 0, K
+        if pn:
+            keep = transposed_plug(keep[0], keep[1], elem_base, ldc, K, N)
+            pn = int(keep[0].numel())
+    row_plug = None
+    if pn:
+        idx = keep[0].view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+        keys = (pos0 + torch.arange(N, device=dev, dtype=torch.int64)[:, None] * pld
+                + torch.arange(slices, device=dev, dtype=torch.int64)[None, :] * cols).reshape(-1)
+        keys = torch.cat([keys, torch.tensor([pos0 + N * pld], device=dev, dtype=torch.int64)])
+        row_plug = torch.searchsorted(idx, keys)
+    ws_bytes = L.pp_quad_big_workspace_size(M, N, slices)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = L.pp_quad_big(codes.data_ptr(), layout, ldc, a.data_ptr(), a.stride(0), lut_ptrs, lut_dtype, sc,
+                       keep[0].data_ptr() if pn else None, keep[1].data_ptr() if pn else None, pn,
+                       row_plug.data_ptr() if row_plug is not None else None, pos0, pld, slices, cols,
+                       nat.ptr_array([o.data_ptr() for o in outs]), outs[0].stride(0), M, N, K,
+                       ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    nat.check(rc, "pp_quad_big")
+    del keep, row_plug, ws
+    return outs
+
+
 def _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, elem_base, outs, L, dev):
-    """Decode into fp16 weights s_m * W_m (plug applied), then 4 fp16 GEMMs.  The decode
+    """Decode into fp16 weights s_m * W_m (plug applied), then the fp16 GEMMs.  The decode
     follows the storage: codes with K contiguous (an (N,K) buffer seen as (K,N)) decode
-    into (N,K) weights, multiplied as their transpose, so both its reads and its writes
-    run along memory."""
+    into (N,K) weights, multiplied as their transpose (4 GEMMs), so both its reads and its
+    writes run along memory; (K,N) weights go through one batched GEMM with the activations
+    broadcast over the 4 models (one library call instead of 4: 113 against 177 us for
+    four 1024 x 4096 x 4096 products, measured)."""
     view = codes.t() if codes.stride(0) == 1 and codes.stride(1) != 1 else codes
     R, C = view.shape
     w = torch.empty((4, R, C), dtype=torch.float16, device=dev)
@@ -239,8 +309,12 @@ def _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, elem_base, outs
     rc = L.pp_quad_dequant_f16(view.data_ptr(), view.stride(0), view.stride(1), lut_ptrs, lut_dtype, sc, pi, pv, pn,
                                elem_base, nat.ptr_array([w[m].data_ptr() for m in range(4)]), C, R, stream)
     nat.check(rc, "pp_quad_dequant_f16")
+    if view is codes:
+        out = torch.matmul(a, w)          # (4, M, N): the outputs are its 4 contiguous slices
+        outs[:] = [out[m] for m in range(4)]
+        return
     for m in range(4):
-        torch.matmul(a, w[m] if view is codes else w[m].t(), out=outs[m])
+        torch.matmul(a, w[m].t(), out=outs[m])
 
 
 def _mfma_layout_ok(codes, K):

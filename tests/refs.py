@@ -8,7 +8,8 @@
 * :func:`mfma_reference` / :func:`check_mfma` -- the reference of the matrix-core route:
   weights decoded in float32 on the header LUTs and rounded once to fp16 operands (as the
   reference's ``tl.dot`` takes them, quad_kernels.py:116-126), the float32 dot-product
-  bound, and a normwise check against the exact decode;
+  bound, and a normwise check against the exact decode; :func:`kn_mfma_reference` the same
+  for a (K,N) code array with any LUTs;
 * :func:`dual_pack_host` / :func:`dual_rows_ref` -- the same for a dual stream, tails
   included.
 """
@@ -74,6 +75,38 @@ def mfma_reference(qp, pos0, N, K, x):
         exact.append(xd @ W[m].reshape(N, K).T)
         w16.append(xd @ wh.T)
         bound.append(2.0 ** -18 * (np.abs(xd) @ np.abs(wh).T))
+    return exact, w16, bound
+
+
+def kn_mfma_reference(a, codes_kn, luts, scales, plug_at=None, plug_vals=None, cols=None):
+    """The matrix-core reference for codes given as a (K,N) array with arbitrary 7-table
+    LUTs: float64 products of the exact decode and of the fp16 operands (float32 decode
+    on the LUTs rounded once, plug tuples substituted at (k, n) = plug_at), with the
+    float32 dot-product bound; only output columns ``cols`` when given (row sample)."""
+    codes = np.asarray(codes_kn, np.uint32)
+    if cols is not None:
+        cols = np.asarray(cols, np.int64)
+        codes = codes[:, cols]
+        if plug_at is not None:
+            pos = {int(n): i for i, n in enumerate(cols)}
+            keep = np.array([int(n) in pos for n in plug_at[1]], bool)
+            plug_at = (plug_at[0][keep], np.array([pos[int(n)] for n in plug_at[1][keep]], np.int64))
+            plug_vals = plug_vals[keep]
+    lf = [l.float().cpu().numpy() if torch.is_tensor(l) else np.asarray(l, np.float32) for l in luts]
+    W = olay.quad_dequant(codes, lf, scales)
+    W32 = olay.quad_dequant(codes, lf, dtype=np.float32)
+    ad = np.asarray(a, np.float64)
+    exact, w16, bound = [], [], []
+    for m in range(4):
+        h = W32[m].astype(np.float16)
+        we = W[m].copy()
+        if plug_at is not None:
+            h[plug_at] = plug_vals[:, m]
+            we[plug_at] = plug_vals[:, m].astype(np.float64) * scales[m]
+        w = h.astype(np.float64) * float(np.float32(scales[m]))
+        exact.append(ad @ we)
+        w16.append(ad @ w)
+        bound.append(2.0 ** -18 * (np.abs(ad) @ np.abs(w)))
     return exact, w16, bound
 
 

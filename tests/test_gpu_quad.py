@@ -157,7 +157,7 @@ def test_quad_gemm_real_pack_with_plug_fast_path(M):
     W = oqp.unpack_quad_f64(qp, 0, N * K)                # float64, plug applied, times s_k
     for k in range(4):
         w = W[k].reshape(N, K).T
-        bound = fp16_weight_bound(a.numpy(), w) if M > qk.PREFILL_M else None   # fp16 decode + library GEMM
+        bound = fp16_weight_bound(a.numpy(), w) if M > qk.BIG_MAX_M else None   # fp16 decode + library GEMM
         if bound is not None:
             assert normwise(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), w)) <= 1e-3
         assert_gemv_close(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), w), f"model {k}", bound=bound)
@@ -234,12 +234,12 @@ def test_pack_quad_layer_on_gpu_matches_oracle():
 
 def kn_route(K, N, M):
     """Which kernel quad_bitpacked runs for contiguous (K,N) codes: 'fused' (the (K,N)
-    decode kernel), 'mfma' (codes transposed for the matrix cores) or 'prefill' (fp16
-    decode + library GEMM)."""
+    decode kernel), 'mfma' (codes transposed for the matrix cores, or the fused large-batch
+    kernel at 65-128 tokens) or 'prefill' (fp16 decode + library GEMM)."""
     if M <= 8 or (K % 32 != 0 and M <= qk.KN_MAX_M):
         return "fused"
-    if K % 32 == 0 and M <= (qk.KN_MFMA_MAX_M if N > K else qk.PREFILL_M):
-        return "mfma"
+    if K % 32 == 0 and M <= qk.BIG_MAX_M:
+        return "mfma"      # codes transposed for the matrix cores, or the fused large-batch kernel
     return "prefill"
 
 
