@@ -29,7 +29,10 @@ Other workloads (``--workload``), one JSON line each:
                     polar_kernels.py:153-184): 4096x4096 N(0,1) weights packed by the drop-in
                     pack_quad_layer / quantize_polar_bitpacked, the drop-in operators called
                     as the reference calls them at M = 1, 8, 32, 128, 1024 tokens, beside
-                    torch's fp16 matmul of the unpacked weights (one line per operator).
+                    torch's fp16 matmul of the unpacked weights (one line per operator);
+* ``quadbig``    -- the fused large-batch quad kernel (quad_bitpacked(fused=True)) on the
+                    refbench layer at ``--big-tokens`` tokens, against the matrix cores'
+                    fp16 roofline (one line per batch size).
 
 Single-Linear workloads rotate enough copies of the packed weights (>= 512 MB in total)
 that no launch finds its codes in the 256 MB last-level cache, and time a HIP graph of
@@ -291,15 +294,19 @@ def time_events(launch, steps, warmup):
     return [s.elapsed_time(e) for s, e in zip(starts, ends)], wall
 
 
-def line(metric, achieved, ms, args, dtype, config, traffic=None, cpu=None, extra=None):
+def line(metric, achieved, ms, args, dtype, config, traffic=None, cpu=None, extra=None, traffic_profile=None,
+         bound="hbm"):
+    peak, unit = (PEAK_HBM_GBS, "GB/s") if bound == "hbm" else (PEAK_FP16_TFLOPS, "TFLOP/s")
     out = {
-        "metric": metric, "value": round(achieved, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "metric": metric, "value": round(achieved, 2), "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config,
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic},
+        "roofline": {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+                     "frac": round(achieved / peak, 4), "traffic": traffic},
         "cpu_baseline": cpu,
     }
+    if traffic is not None and traffic_profile:
+        out["roofline"]["traffic_profile"] = os.path.relpath(traffic_profile, ROOT)
     if extra:
         out.update(extra)
     print(json.dumps(out), flush=True)
@@ -365,7 +372,7 @@ def run_quad3b(args, dev, log):
           "layers": args.layers, "projections": len(shapes), "models": 4, "batch": 1,
           "tuples": int(pack.n), "plug_entries": int(pack.plug_idx.numel()),
           "algorithmic_bytes": int(algo), "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2)},
-         traffic=read_pmc_traffic(PMC_SUMMARY["quad3b"]), cpu=cpu)
+         traffic=read_pmc_traffic(PMC_SUMMARY["quad3b"]), cpu=cpu, traffic_profile=PMC_SUMMARY["quad3b"])
 
 
 def run_dual3b(args, dev, log, tails):
@@ -441,7 +448,8 @@ def run_dual3b(args, dev, log, tails):
           "pairs": int(pack.n_codes), "tail_weights": pack.tail_lengths,
           "plug_entries": int(pack.plug_idx.numel()), "algorithmic_bytes": int(algo),
           "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2)},
-         traffic=read_pmc_traffic(PMC_SUMMARY["dual3b"]) if tails else None, cpu=cpu)
+         traffic=read_pmc_traffic(PMC_SUMMARY["dual3b"]) if tails else None, cpu=cpu,
+         traffic_profile=PMC_SUMMARY["dual3b"])
 
 
 # ---------------------------------------------------------------- single Linear layers
@@ -722,8 +730,38 @@ def run_refbench(args, dev, log):
               "value_is": "GB/s of algorithmic bytes at M=1 (HIP events, weights cache-resident)"})
 
 
+def run_quadbig(args, dev, log):
+    """The fused large-batch kernel (quad_big_kernel) on the reference benchmark's layer
+    (4 models of 4096 x 4096 N(0,1) weights packed by pack_quad_layer, (K,N) codes) at
+    ``--big-tokens`` tokens, forced with fused=True at every size; checked against fp16
+    torch.matmul of the original weights, timed with HIP events. The roofline is the
+    matrix cores' (fp16 dense): 8 M K N flops per call."""
+    K = N = 4096
+    g = torch.Generator(device=dev).manual_seed(seed_of(6, 0, 0))
+    ws = [torch.randn(K, N, generator=g, device=dev).to(torch.float16) for _ in range(4)]
+    codes, luts, scales = qk.pack_quad_layer(*ws)
+    for M in args.big_tokens:
+        a = torch.randn(M, K, generator=g, device=dev).to(torch.float16)
+        run = lambda: qk.quad_bitpacked(a, codes, luts, scales, fused=True)
+        for o, w in zip(run(), ws):
+            r = torch.matmul(a, w).float()
+            d = (o.float() - r).abs().max().item()
+            if not d <= 0.05 * r.abs().max().item():
+                raise SystemExit(f"quadbig M={M}: max |diff| {d} vs fp16 matmul")
+        per, _ = time_events(run, args.steps, args.warmup)
+        ms = float(np.mean(per))
+        tflops = 8.0 * M * K * N / (ms * 1e-3) / 1e12
+        log(f"[bench] quadbig M={M}: {ms * 1e3:.1f} us per call -> {tflops:.0f} TFLOP/s")
+        line("TFLOP/s of the fused large-batch quad decode (4 models) on a 4096x4096 layer", tflops, ms, args,
+             "fp16 operands, fp32 sums",
+             {"workload": f"quad_bitpacked(fused=True), 4096x4096 pack_quad_layer codes, {M} tokens", "K": K,
+              "N": N, "models": 4, "tokens": M, "flops_per_call": 8 * M * K * N}, bound="mfma")
+
+
 def run_sweep(args, dev, log):
     for name, N, K in (("gate_proj", 11008, 2048), ("down_proj", 2048, 11008)):
+        if name not in args.sweep_shapes:
+            continue
         pack = quad_linear_pack(N, K, dev, seed_of(4, 0, 0 if name == "gate_proj" else 1))
         for M in args.sweep_tokens:
             run_quad_single(args, dev, log, N, K, M, name, pack=pack)
@@ -738,8 +776,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--workload", default="quad3b",
-                    choices=["quad3b", "dual3b", "dual3b-pad", "dual2048", "quadgate", "sweep", "refbench"])
+                    choices=["quad3b", "dual3b", "dual3b-pad", "dual2048", "quadgate", "sweep", "refbench",
+                             "quadbig"])
+    ap.add_argument("--big-tokens", type=int, nargs="+", default=[128, 1024])
     ap.add_argument("--sweep-tokens", type=int, nargs="+", default=[1, 4, 16, 64])
+    ap.add_argument("--sweep-shapes", nargs="+", default=["gate_proj", "down_proj"],
+                    choices=["gate_proj", "down_proj"])
     ap.add_argument("--cpu-sample-tuples", type=int, default=77_070_336)  # one layer
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quiet", action="store_true")
@@ -771,6 +813,8 @@ def main():
         run_quad_single(args, dev, log, 11008, 2048, 1, "gate_proj")
     elif args.workload == "refbench":
         run_refbench(args, dev, log)
+    elif args.workload == "quadbig":
+        run_quadbig(args, dev, log)
     else:
         run_sweep(args, dev, log)
 

@@ -134,12 +134,16 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
         # decode along the storage: K-contiguous codes (container rows) into (N,K) weights,
         # multiplied as their transpose; the kernel rule's groups need the (K,N) indices
         nk = packed.stride(0) == 1 and packed.stride(1) != 1 and chunk_size > 0
-        w1, w2 = dual_dequant(packed.t() if nk else packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size,
-                              plug=plug, elem_base=elem_base, layout=layout, chunk_size=chunk_size,
-                              dtype=torch.float16)
-        torch.matmul(a_fp16, w1.t() if nk else w1, out=out1)
-        torch.matmul(a_fp16, w2.t() if nk else w2, out=out2)
-        return out1, out2
+        view = packed.t() if nk else packed
+        w = torch.empty((2,) + tuple(view.shape), dtype=torch.float16, device=dev)
+        _dequant_into(view, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug, elem_base, layout,
+                      chunk_size, w[0], w[1])
+        if nk:
+            torch.matmul(a_fp16, w[0].t(), out=out1)
+            torch.matmul(a_fp16, w[1].t(), out=out2)
+            return out1, out2
+        out = torch.matmul(a_fp16, w)       # one batched GEMM over the two models: (2, M, N)
+        return out[0], out[1]
     ws_bytes = L.pp_dual_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), packed.data_ptr(),
                                              packed.stride(0), packed.stride(1), group_size, chunk_size,
                                              int(elem_base), pn, M, N, K)
@@ -171,17 +175,26 @@ def dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases=1024, group
     w2 = torch.empty_like(w1)
     if K * N == 0:
         return w1, w2
+    _dequant_into(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug, elem_base, layout,
+                  chunk_size, w1, w2)
+    return w1, w2
+
+
+def _dequant_into(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug, elem_base, layout,
+                  chunk_size, w1, w2):
+    """Decode a (K,N) code view into the contiguous (K,N) tensors w1, w2 (float32 or fp16)."""
+    K, N = packed.shape
+    dev = packed.device
     lay = _codes_view(packed, layout)
     lut_dt = _lut_dtype(amp_lut, cos_lut, sin_lut)
     pi, pa, pn, keep = _dual_plug(plug, dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
-    fn = nat.lib().pp_dual_dequant if dtype == torch.float32 else nat.lib().pp_dual_dequant_f16
+    fn = nat.lib().pp_dual_dequant if w1.dtype == torch.float32 else nat.lib().pp_dual_dequant_f16
     rc = fn(packed.data_ptr(), lay, packed.stride(0), packed.stride(1), bmax.contiguous().data_ptr(), group_size,
             chunk_size, amp_lut.data_ptr(), amp_lut.numel(), cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases,
             lut_dt, pi, pa, pn, int(elem_base), w1.data_ptr(), w2.data_ptr(), N, K, stream)
     nat.check(rc, "pp_dual_dequant")
     del keep
-    return w1, w2
 
 
 def header_luts(amp_bits=6, phase_bits=10, mu=255.0, device=None):
