@@ -129,19 +129,27 @@ def quad_dequant(codes, luts, scales=None, dtype=np.float64):
     return w
 
 
-def dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, group_size=32):
-    """float64 (K,N) weight pair for kernel-layout codes -- polar_kernels.py:64-79.
+def dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, group_size=32, dtype=np.float64, plug=None):
+    """(K,N) weight pair for kernel-layout codes -- polar_kernels.py:64-79.
 
     ``bmax`` is indexed by ``(k*N + n) // group_size`` over the (K,N)
     row-major flatten, as the reference kernel does (polar_kernels.py:70-71).
+    ``dtype=np.float32`` evaluates the reference's products in float32 (amplitude =
+    amp_lut * bmax, then amplitude * cos and amplitude * sin, each rounded once,
+    polar_kernels.py:72-79): the values it rounds to fp16 before its dot products.
+    ``plug=(k, n, amp)`` replaces the amplitude of those elements (polar_bitpack.py:240-243).
     """
     p = np.asarray(packed).astype(np.int32) + 32768
     K, N = p.shape
     amp_q = (p >> 10) & 0x3F
     ph = p & 0x3FF
     g = (np.arange(K)[:, None] * N + np.arange(N)[None, :]) // group_size
-    amp = np.asarray(amp_lut, np.float64)[amp_q] * np.asarray(bmax, np.float64)[g]
-    return amp * np.asarray(cos_lut, np.float64)[ph], amp * np.asarray(sin_lut, np.float64)[ph]
+    amp = np.asarray(amp_lut, np.float64).astype(dtype)[amp_q] * np.asarray(bmax, np.float64).astype(dtype)[g]
+    if plug is not None:
+        kk, nn, pa = plug
+        amp[kk, nn] = np.asarray(pa, np.float64).astype(dtype)
+    return (amp * np.asarray(cos_lut, np.float64).astype(dtype)[ph],
+            amp * np.asarray(sin_lut, np.float64).astype(dtype)[ph])
 
 
 def gemm_f64(a, w):

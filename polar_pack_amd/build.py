@@ -18,7 +18,7 @@ CSRC = os.path.join(PKG, "csrc")
 LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libpolar_pack.so")
 OBJ_DIR = os.path.join(LIB_DIR, "obj")
-SOURCES = ["capi.hip", "quad.hip", "quad_rows.hip", "quad_mfma.hip", "quad_big.hip", "quad_kn.hip", "dual.hip", "dual_rows.hip", "dual_kn.hip", "noalloc.hip"]
+SOURCES = ["capi.hip", "quad.hip", "quad_rows.hip", "quad_mfma.hip", "quad_big.hip", "quad_kn.hip", "dual.hip", "dual_rows.hip", "dual_kn.hip", "dual_mfma.hip", "noalloc.hip"]
 ARCH = "gfx950"
 
 # Packed FP32 instructions are disabled for all device code (their results have been

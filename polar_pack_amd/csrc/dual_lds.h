@@ -71,4 +71,32 @@ __device__ __forceinline__ void dual_lookup1(const char* lds, uint32_t c, const 
   cs = *reinterpret_cast<const float2*>(lds + DLDS_CS + (((c << 7) & 0x1FF80u) | o.cs));
 }
 
+// Build the tables of a workgroup of NT threads (a multiple of 64) from the caller's LUTs
+// (entries of type E): every LUT load of a thread is issued before its stores, the
+// (cos, sin) rows written as 16-byte units in address order.  For the int16 layout
+// (stored = code ^ 0x8000) amplitude entry a holds amp_lut[a ^ 32].  Ends with a barrier.
+template <int NT, int LAYOUT, typename E>
+__device__ __forceinline__ void dual_tables_of(char* lds, const DualLuts& L) {
+  constexpr int KU = (8192 + NT - 1) / NT;
+  const E* cp = reinterpret_cast<const E*>(L.cs[0]);
+  const E* sp = reinterpret_cast<const E*>(L.cs[1]);
+  float c[KU], s[KU];
+#pragma unroll
+  for (int k = 0; k < KU; ++k) {
+    const int p = (threadIdx.x + k * NT) >> 3;
+    c[k] = p < L.phase_n ? (float)cp[p] : 0.f;
+    s[k] = p < L.phase_n ? (float)sp[p] : 0.f;
+  }
+  if (threadIdx.x < 64) {
+    const int e = LAYOUT == PP_DUAL_I16_OFFSET ? (threadIdx.x ^ 32) : threadIdx.x;
+    *reinterpret_cast<float*>(lds + DLDS_AMP + 4 * threadIdx.x) =
+        e < L.amp_n ? (float)reinterpret_cast<const E*>(L.amp)[e] : 0.f;
+  }
+#pragma unroll
+  for (int k = 0; k < KU; ++k)
+    if (threadIdx.x + k * NT < 8192)
+      *reinterpret_cast<float4*>(lds + DLDS_CS + 16 * (threadIdx.x + k * NT)) = make_float4(c[k], s[k], c[k], s[k]);
+  __syncthreads();
+}
+
 }  // namespace pp

@@ -1,0 +1,410 @@
+// Dual-pack decode GEMM for batches of 9 tokens and more on the matrix cores: one fused
+// pass over the int16 (K,N) codes quantize_polar_bitpacked returns produces both models'
+// outputs
+//   out_m[j, n] = fp16( sum_k x[j, k] * W_m[k, n] ),   W_1 = amp cos, W_2 = amp sin,
+//   amp = amp_lut[amp_q] * bmax[(k*N + n) / group_size]
+// with each weight rounded to fp16 before the product, as the reference's tl.dot takes its
+// operands (polar_kernels.py:60-86), plug amplitudes substituted (polar_bitpack.py:240-243),
+// and no weight written to memory.
+//
+// Work item = 16 output columns n x 16*TT tokens x one K slice, one wavefront,
+// v_mfma_f32_16x16x32_f16 (the A operand holds the weights of 16 columns n at 32
+// consecutive k, the B operand x as stored):
+//  * per 32-row step lane l reads the codes of column n0 + l%16 at rows k0 + 8(l/16) .. +7
+//    (8 two-byte loads, 32-byte runs over 16 lanes) and their 8 group scales, looks up
+//    amplitude and (cos, sin) in the dual LDS tables and rounds the two weights to fp16;
+//  * 2 models x TT token tiles of 16 x 16 fp32 sums stay in registers: two waves per SIMD
+//    (8 per workgroup, one workgroup per CU: the tables take 129 KiB of LDS), so one
+//    wave's decode runs beside the other's products;
+//  * codes, scales and x of the next step load while a step is decoded; the walk runs in
+//    whole pairs of steps with no exit between them (a step past the slice end reads x
+//    through an empty buffer record, i.e. zeros).
+// Plug entries replace the amplitude of their element (the table amplitude times the
+// group scale); positions are read in an (N,K) frame (position ppos0 + n*pld + k: the host
+// moves the (K,N) storage positions there), a window of 4 per lane.  With one K slice a
+// wave writes its fp16 outputs; otherwise it adds its sums into float32 accumulators
+// [m][n][j] with device-scope atomics and dual_mfma_finish_kernel writes the outputs and
+// leaves zeros for the next launch.
+#include "dual_lds.h"
+#include "rows_common.h"
+
+namespace pp {
+
+typedef _Float16 dh8 __attribute__((ext_vector_type(8)));
+typedef float df4 __attribute__((ext_vector_type(4)));
+
+constexpr int DM_NT = 512;       // 8 waves, two per SIMD
+constexpr int DM_WAVES = DM_NT / 64;
+
+struct DualMfmaArgs {
+  const uint16_t* codes;   // row k at codes + k*ldk (int16 (K,N) layout, stored = code ^ 0x8000)
+  int64_t ldk;
+  const f16* x;            // (M, K), row stride x_sm
+  int64_t x_sm;
+  f16* out[2];             // (M, N), row stride o_sm
+  int64_t o_sm;
+  int N, K, M;
+  int tiles, tblocks;      // ceil(N / 16), ceil(M / (16 TT))
+  int slices, ks;          // K slices of ks rows (a multiple of 64)
+  const f16* scales;       // bmax, one per group_size consecutive (k*N + n)
+  int64_t n_groups;
+  int log2gs;
+  DualLuts luts;
+  const uint32_t* plug_idx;   // sorted positions in the (N,K) frame
+  const f16* plug_amp;
+  int64_t plug_n;
+  const int64_t* row_plug;    // [n*slices + s]: first entry of (column n, slice s); N*slices + 1 entries
+  int64_t ppos0, pld;
+  float* acc;              // slices > 1: [2][N][M] float32, zero on entry
+  int xcd_remap;
+  int vec_out;             // outputs 8-byte aligned with o_sm % 4 == 0
+};
+
+template <int TT>
+struct DmStage {
+  uint32_t c[8];           // 8 stored codes of the lane's column (low 16 bits)
+  uint32_t sc[8];          // their group scales (fp16 bits)
+  u32x4 xb[TT];            // 8 fp16 x of token 16t + l%16
+};
+
+// The lane's window of 4 plug entries of its column: rows (INT_MAX past the end, INT_MIN
+// once applied) and amplitudes.
+struct DmPlug {
+  int k[4];
+  float a[4];
+  int64_t next, end;
+};
+
+__device__ __forceinline__ void dplug_load(const DualMfmaArgs& A, DmPlug& P, int64_t rowpos) {
+  const rsrc_t ri = make_rsrc(A.plug_idx, 4u * (uint32_t)A.plug_n);
+  const rsrc_t ra = make_rsrc(A.plug_amp, 2u * (uint32_t)A.plug_n);
+  uint32_t idx[4], am[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t e = P.next + i;
+    const bool has = e < P.end;
+    vload32(idx[i], has ? 4u * (uint32_t)e : OOB, ri);
+    vload16(am[i], has ? 2u * (uint32_t)e : OOB, ra);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    P.k[i] = P.next + i < P.end ? (int)((int64_t)idx[i] - rowpos) : 0x7FFFFFFF;
+    P.a[i] = h2f(am[i]);
+  }
+  P.next += 4;
+}
+
+// Substitute the window's entries in the lane's rows kk .. kk+7 (step rows ks .. ks+31)
+// into the amplitudes; refill a window used up within the step.  Wave-uniform control.
+__device__ __forceinline__ void dplug_patch(const DualMfmaArgs& A, DmPlug& P, int64_t rowpos, int kk, int ks,
+                                            float (&amp)[8]) {
+  for (;;) {
+    int hit = -1;
+#pragma unroll
+    for (int i = 3; i >= 0; --i) hit = (unsigned)(P.k[i] - kk) < 8u ? i : hit;
+    if (__ballot(hit >= 0)) {
+      const int e = hit >= 0 ? (hit == 0 ? P.k[0] : hit == 1 ? P.k[1] : hit == 2 ? P.k[2] : P.k[3]) - kk : -1;
+      const float v = hit == 0 ? P.a[0] : hit == 1 ? P.a[1] : hit == 2 ? P.a[2] : P.a[3];
+#pragma unroll
+      for (int ee = 0; ee < 8; ++ee) amp[ee] = e == ee ? v : amp[ee];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) P.k[i] = hit == i ? (int)0x80000000 : P.k[i];
+      continue;
+    }
+    const bool refill = P.k[3] < ks + 32 && P.next < P.end;
+    if (!__ballot(refill)) break;
+    DmPlug R = P;
+    dplug_load(A, R, rowpos);
+    if (refill) P = R;
+  }
+}
+
+// Issue the loads of the step at row k0 (codes clamped to the last step; x of a step at or
+// past the slice end ke through an empty record).  voc: the lane's code offset (OOB past
+// N), the 8 rows 2*ldk bytes apart in the scalar operand; gbase: group index of (k0 = 0,
+// the lane's column); vox: x offsets per token tile.
+template <int TT>
+__device__ __forceinline__ void dm_issue(const DualMfmaArgs& A, int n0, int n, bool ok, int q, int k0, int ke,
+                                         uint32_t voc, const uint32_t (&vox)[TT], const f16* xblk, int j0,
+                                         DmStage<TT>& S) {
+  const uint32_t xrec = k0 < ke ? 2u * (uint32_t)((int64_t)(A.M - 1 - j0) * A.x_sm + (ke - k0)) : 0u;
+  k0 = min(k0, A.K - 32);
+  const rsrc_t rc = make_rsrc(A.codes + (int64_t)k0 * A.ldk + n0,
+                              2u * (uint32_t)((int64_t)(A.K - 1 - k0) * A.ldk + (A.N - n0)));
+  const int st = (int)(2 * A.ldk);
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    S.c[e] = __builtin_amdgcn_raw_buffer_load_b16(rc, (int)voc, e * st, NT_AUX);
+  const rsrc_t rs = make_rsrc(A.scales, 2u * (uint32_t)A.n_groups);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t g = ((int64_t)(k0 + 8 * q + e) * A.N + n) >> A.log2gs;
+    vload16(S.sc[e], ok ? 2u * (uint32_t)g : OOB, rs);
+  }
+  const rsrc_t rx = make_rsrc(xblk + min(k0, A.K - 32), xrec);
+#pragma unroll
+  for (int t = 0; t < TT; ++t) vload128c(S.xb[t], vox[t], rx);
+}
+
+template <int TT, bool PLUG>
+struct DmRun {
+  const char* lds;
+  DualLane lo;
+  const DualMfmaArgs& A;
+  const f16* xblk;
+  int n0, n, j0, q, ke;
+  bool ok;
+  uint32_t voc;
+  uint32_t vox[TT];
+  int64_t rowpos;
+  DmPlug P;
+  df4 C[2][TT];
+
+  // Consume the step at k0 from cur while the step at k0 + 32 loads into nxt.
+  __device__ __forceinline__ void step(const DmStage<TT>& cur, DmStage<TT>& nxt, int k0) {
+    dm_issue<TT>(A, n0, n, ok, q, k0 + 32, ke, voc, vox, xblk, j0, nxt);
+    float amp[8];
+    float2 cs[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float an;
+      dual_lookup1(lds, cur.c[e] & 0xFFFFu, lo, an, cs[e]);
+      amp[e] = an * h2f(cur.sc[e]);
+    }
+    if constexpr (PLUG) dplug_patch(A, P, rowpos, k0 + 8 * q, k0, amp);
+    dh8 a0, a1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a0[e] = (_Float16)(amp[e] * cs[e].x);
+      a1[e] = (_Float16)(amp[e] * cs[e].y);
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const dh8 b = __builtin_bit_cast(dh8, cur.xb[t]);
+      C[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, C[0][t], 0, 0, 0);
+      C[1][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, C[1][t], 0, 0, 0);
+    }
+  }
+};
+
+template <int TT, bool PLUG>
+__device__ __forceinline__ void dm_body(const char* lds, const DualMfmaArgs& A) {
+  const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+  const DualLane lo = dual_lane(lane);
+  int b = blockIdx.x;
+  if (A.xcd_remap) b = (b & 7) * (int)(gridDim.x >> 3) + (b >> 3);
+  const int64_t gw = (int64_t)b * DM_WAVES + uniform(threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * DM_WAVES;
+  // groups of DM_WAVES column tiles sharing a token block and K slice, one per workgroup
+  const int64_t tgroups = (A.tiles + DM_WAVES - 1) / DM_WAVES;
+  const int64_t items = tgroups * DM_WAVES * A.tblocks * A.slices;
+  for (int64_t it = gw; it < items; it += nw) {
+    const int64_t w = uniform64(it / DM_WAVES);
+    const int tile = (int)(uniform64(w / ((int64_t)A.slices * A.tblocks)) * DM_WAVES + it % DM_WAVES);
+    const int sl = (int)(w % A.slices), tb = (int)((w / A.slices) % A.tblocks);
+    if (tile >= A.tiles) continue;
+    const int n0 = tile * 16, j0 = tb * 16 * TT;
+    const int kb = sl * A.ks, ke = min(A.K, kb + A.ks);
+    const int n = n0 + i;
+    const bool ok = n < A.N;
+    DmRun<TT, PLUG> R{lds, lo, A, A.x + (int64_t)j0 * A.x_sm, n0, n, j0, q, ke, ok};
+    R.voc = ok ? 2u * (uint32_t)(8 * q * A.ldk + i) : OOB;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const int jl = 16 * t + i;
+      R.vox[t] = j0 + jl < A.M ? 2u * (uint32_t)(jl * A.x_sm + 8 * q) : OOB;
+    }
+    if constexpr (PLUG) {
+      R.rowpos = A.ppos0 + (int64_t)n * A.pld;
+      R.P.next = ok ? A.row_plug[(int64_t)n * A.slices + sl] : 0;
+      R.P.end = ok ? A.row_plug[(int64_t)n * A.slices + sl + 1] : 0;
+      dplug_load(A, R.P, R.rowpos);
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) R.C[m][t] = df4{0.f, 0.f, 0.f, 0.f};
+    DmStage<TT> S0, S1;
+    dm_issue<TT>(A, n0, n, ok, q, kb, ke, R.voc, R.vox, R.xblk, j0, S0);
+    for (int k0 = kb; k0 < ke; k0 += 64) {
+      R.step(S0, S1, k0);
+      R.step(S1, S0, k0 + 32);
+    }
+    // epilogue: lane holds columns n0 + 4q + r, r = 0..3, of token j0 + 16t + i
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        const int j = j0 + 16 * t + i;
+        const int nn = n0 + 4 * q;
+        const df4 c = R.C[m][t];
+        if (j >= A.M || nn >= A.N) continue;
+        if (A.slices == 1) {
+          f16* o = A.out[m] + (int64_t)j * A.o_sm + nn;
+          if (A.vec_out && nn + 3 < A.N) {
+            const f16x4 h = {(f16)c[0], (f16)c[1], (f16)c[2], (f16)c[3]};
+            *reinterpret_cast<f16x4*>(o) = h;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (nn + r < A.N) o[r] = (f16)c[r];
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (nn + r < A.N)
+              __hip_atomic_fetch_add(A.acc + ((int64_t)m * A.N + nn + r) * A.M + j, c[r], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+  }
+}
+
+template <int TT>
+__global__ __launch_bounds__(DM_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void dual_mfma_kernel(
+    const DualMfmaArgs A) {
+  __shared__ __attribute__((aligned(16))) char T[DLDS_BYTES];
+  if (A.luts.dtype == PP_F16) dual_tables_of<DM_NT, PP_DUAL_I16_OFFSET, f16>(T, A.luts);
+  else dual_tables_of<DM_NT, PP_DUAL_I16_OFFSET, float>(T, A.luts);
+  if (A.plug_n > 0) dm_body<TT, true>(T, A);
+  else dm_body<TT, false>(T, A);
+}
+
+// Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero (after the item kernel
+// has completed).  Thread = 4 consecutive tokens of one (model, column).
+__global__ __launch_bounds__(256) void dual_mfma_finish_kernel(float* acc, f16* o0, f16* o1, int64_t o_sm, int N,
+                                                               int M) {
+  const int64_t total = 2ll * N * M;
+  const int64_t i0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+  if (i0 >= total) return;
+  float v[4];
+  if (M % 4 == 0) {
+    const float4 t = *reinterpret_cast<const float4*>(acc + i0);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    *reinterpret_cast<float4*>(acc + i0) = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = i0 + e < total ? acc[i0 + e] : 0.f;
+      if (i0 + e < total) acc[i0 + e] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t idx = i0 + e;
+    if (idx >= total) break;
+    const int j = (int)(idx % M);
+    const int64_t mn = idx / M;
+    const int col = (int)(mn % N), m = (int)(mn / N);
+    (m == 0 ? o0 : o1)[(int64_t)j * o_sm + col] = (f16)v[e];
+  }
+}
+
+static int dm_tt(int64_t M) { return M <= 32 ? 2 : M <= 64 ? 4 : 8; }
+
+static void dm_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* cols) {
+  const int64_t waves = (int64_t)device_cu_count() * DM_WAVES;
+  const int64_t units = ((N + 15) / 16) * ((M + 16 * dm_tt(M) - 1) / (16 * dm_tt(M)));
+  int64_t s = std::max<int64_t>(1, std::min<int64_t>(K / 64, waves / std::max<int64_t>(1, units)));
+  const int64_t c = ((K + s - 1) / s + 63) / 64 * 64;   // whole pairs of 32-row steps
+  *cols = c;
+  *slices = (K + c - 1) / c;
+}
+
+}  // namespace pp
+
+using namespace pp;
+
+extern "C" int pp_dual_mfma_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* slice_cols) {
+  PP_REQUIRE(slices != nullptr && slice_cols != nullptr, "null pointer argument");
+  PP_REQUIRE(M >= 1 && N >= 1 && K >= 32, "needs M, N >= 1 and K >= 32");
+  dm_plan(M, N, K, slices, slice_cols);
+  return PP_OK;
+}
+
+extern "C" int64_t pp_dual_mfma_workspace_size(int64_t M, int64_t N, int64_t slices) {
+  if (slices <= 1) return 0;
+  return (2 * N * M * 4 + 255) / 256 * 256;
+}
+
+extern "C" int pp_dual_mfma(const void* codes, int64_t ldk, const void* a, int64_t a_sm, const void* bmax,
+                            int64_t group_size, const void* amp_lut, int amp_n, const void* cos_lut,
+                            const void* sin_lut, int phase_n, int lut_dtype, const uint32_t* plug_idx,
+                            const void* plug_amp, int64_t plug_n, const int64_t* row_plug, int64_t plug_pos0,
+                            int64_t plug_ld, int64_t slices, int64_t slice_cols, void* out1, void* out2,
+                            int64_t o_sm, int64_t M, int64_t N, int64_t K, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  PP_REQUIRE(codes && a && bmax && amp_lut && cos_lut && sin_lut && out1 && out2, "null pointer argument");
+  PP_REQUIRE(lut_dtype == PP_F16 || lut_dtype == PP_F32, "bad lut_dtype");
+  PP_REQUIRE(amp_n >= 1 && amp_n <= 64 && phase_n >= 1 && phase_n <= 1024, "amp_n must be 1..64, phase_n 1..1024");
+  PP_REQUIRE(M >= 1 && N >= 1 && K >= 32 && K % 32 == 0, "needs M, N >= 1 and K a multiple of 32 (N=%lld, K=%lld)",
+             (long long)N, (long long)K);
+  PP_REQUIRE(ldk >= N && aligned(codes, 2), "codes: (K,N) rows of ldk >= N int16 codes");
+  PP_REQUIRE(group_size >= 1 && (group_size & (group_size - 1)) == 0, "group_size must be a power of two");
+  PP_REQUIRE(aligned(a, 16) && (M == 1 || (a_sm >= K && a_sm % 8 == 0)),
+             "activations must be 16-byte aligned with a row stride that is a multiple of 8");
+  PP_REQUIRE(o_sm >= N, "o_sm must be >= N");
+  PP_REQUIRE(slices >= 1 && slice_cols >= 64 && slice_cols % 64 == 0 && slices * slice_cols >= K &&
+                 (slices - 1) * slice_cols < K,
+             "slices x slice_cols must cover K in multiples of 64 rows");
+  PP_REQUIRE(plug_n >= 0 && plug_n < (1ll << 29) && (plug_n == 0 || (plug_idx && plug_amp && row_plug)),
+             "plug arrays are null (or more than 2^29 entries)");
+  const int64_t n_groups = (K * N + group_size - 1) / group_size;
+  PP_REQUIRE(K * ldk * 2 < (1ll << 31) && n_groups * 2 < (1ll << 31) && (M - 1) * a_sm + K < (1ll << 30),
+             "the codes, the scales and the activations must each stay below 2 GiB");
+  const int64_t need = pp_dual_mfma_workspace_size(M, N, slices);
+  PP_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), "workspace too small: need %lld bytes",
+             (long long)need);
+  DualMfmaArgs A = {};
+  A.codes = reinterpret_cast<const uint16_t*>(codes);
+  A.ldk = ldk;
+  A.x = reinterpret_cast<const f16*>(a);
+  A.x_sm = M > 1 ? a_sm : K;
+  A.out[0] = reinterpret_cast<f16*>(out1);
+  A.out[1] = reinterpret_cast<f16*>(out2);
+  A.o_sm = o_sm;
+  A.vec_out = o_sm % 4 == 0 && aligned(out1, 8) && aligned(out2, 8);
+  A.N = (int)N;
+  A.K = (int)K;
+  A.M = (int)M;
+  const int tt = dm_tt(M);
+  A.tiles = (int)((N + 15) / 16);
+  A.tblocks = (int)((M + 16 * tt - 1) / (16 * tt));
+  A.slices = (int)slices;
+  A.ks = (int)slice_cols;
+  A.scales = reinterpret_cast<const f16*>(bmax);
+  A.n_groups = n_groups;
+  int lg = 0;
+  while ((1ll << lg) < group_size) ++lg;
+  A.log2gs = lg;
+  A.luts.amp = amp_lut;
+  A.luts.cs[0] = cos_lut;
+  A.luts.cs[1] = sin_lut;
+  A.luts.amp_n = amp_n;
+  A.luts.phase_n = phase_n;
+  A.luts.dtype = lut_dtype;
+  A.plug_idx = plug_idx;
+  A.plug_amp = reinterpret_cast<const f16*>(plug_amp);
+  A.plug_n = plug_n;
+  A.row_plug = row_plug;
+  A.ppos0 = plug_pos0;
+  A.pld = plug_ld;
+  A.acc = reinterpret_cast<float*>(workspace);
+  const int64_t groups = (int64_t)(A.tiles + DM_WAVES - 1) / DM_WAVES * A.tblocks * slices;
+  const int64_t grid = std::min<int64_t>(device_cu_count(), groups);
+  A.xcd_remap = grid % 8 == 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (tt) {
+    case 2: hipLaunchKernelGGL(dual_mfma_kernel<2>, dim3((unsigned)grid), dim3(DM_NT), 0, st, A); break;
+    case 4: hipLaunchKernelGGL(dual_mfma_kernel<4>, dim3((unsigned)grid), dim3(DM_NT), 0, st, A); break;
+    default: hipLaunchKernelGGL(dual_mfma_kernel<8>, dim3((unsigned)grid), dim3(DM_NT), 0, st, A); break;
+  }
+  PP_LAUNCH_CHECK();
+  if (slices > 1) {
+    const int64_t total = 2 * N * M;
+    hipLaunchKernelGGL(dual_mfma_finish_kernel, dim3((unsigned)((total / 4 + 255) / 256 + 1)), dim3(256), 0, st,
+                       A.acc, A.out[0], A.out[1], o_sm, A.N, A.M);
+    PP_LAUNCH_CHECK();
+  }
+  return PP_OK;
+}

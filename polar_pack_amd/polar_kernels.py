@@ -13,12 +13,13 @@ Same names, arguments, return values and error behaviour as the reference
 * :func:`dual_dequant` -- float32 (or fp16) weights of a code view.
 
 Batches of 1-4 tokens (1-8 on the (K,N) kernel layout) run on the fused decode kernels;
-larger ones decode once into
-fp16 weights (the values the reference's kernel rounds its weights to,
-polar_kernels.py:78-82) and run a library fp16 GEMM (hipBLASLt through torch.matmul).
+5-64 tokens on the (K,N) kernel layout on the matrix-core decode (pp_dual_mfma); larger
+ones decode once into fp16 weights (the values the reference's kernel rounds its weights
+to, polar_kernels.py:78-82) and run a library fp16 GEMM (hipBLASLt through torch.matmul).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -101,8 +102,13 @@ def _dual_plug(plug, device):
 
 
 def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases=1024, group_size=32, *,
-                         plug=None, elem_base=0, layout="i16", chunk_size=0):
-    """2 GEMMs from one packed pass (polar_kernels.py:98-115); returns ``(out1, out2)`` fp16 (M,N)."""
+                         plug=None, elem_base=0, layout="i16", chunk_size=0, fused=None):
+    """2 GEMMs from one packed pass (polar_kernels.py:98-115); returns ``(out1, out2)`` fp16 (M,N).
+
+    ``fused`` (more than 4 tokens on the int16 (K,N) layout, K % 32 == 0): True runs the
+    matrix-core decode at any size, False the fused (K,N) kernel up to 8 tokens and the fp16
+    decode + library GEMM above, None (default) the matrix cores up to DUAL_MFMA_MAX_M
+    tokens."""
     M, K = a_fp16.shape
     K_b, N = packed.shape
     assert K == K_b
@@ -130,6 +136,12 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
     kn = packed.stride(1) == 1 and packed.stride(0) >= N and packed.stride(0) % 8 == 0 and N % 8 == 0 \
         and K % 8 == 0 and chunk_size == 0 and group_size >= 8 and group_size & (group_size - 1) == 0 \
         and packed.data_ptr() % 16 == 0
+    if kn and M > DUAL_MFMA_MIN_M and K % 32 == 0 and layout == "i16" and fused is not False \
+            and (fused or M <= DUAL_MFMA_MAX_M):
+        _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, lut_dt, keep, pn,
+                   int(elem_base), out1, out2, L, dev)
+        del keep
+        return out1, out2
     if M > (KN_MAX_M if kn else FUSED_MAX_M):
         # decode along the storage: K-contiguous codes (container rows) into (N,K) weights,
         # multiplied as their transpose; the kernel rule's groups need the (K,N) indices
@@ -160,7 +172,50 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
 
 
 FUSED_MAX_M = 4   # larger batches decode once and run a library GEMM
-KN_MAX_M = 8      # on the (K,N) kernel layout the fused kernel takes up to 8 tokens
+KN_MAX_M = 8      # on the (K,N) kernel layout the fused kernel takes up to 8 tokens, ...
+DUAL_MFMA_MIN_M = 4    # ... but from 5 tokens (K % 32 == 0) the matrix-core decode (pp_dual_mfma)
+DUAL_MFMA_MAX_M = 64   # runs, up to 64 (4096x4096 layer, events: 8 tokens 35 against 49 us,
+# 32 tokens 41 against 43 us for two fp16 matmuls; from 96 tokens the fp16 decode + one
+# batched GEMM is faster: 52 against 66 us)
+
+
+def _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, lut_dt, keep, pn, elem_base,
+               out1, out2, L, dev):
+    """More than 8 tokens on the int16 (K,N) layout: the matrix-core decode (pp_dual_mfma).
+    Plug positions (k*ldk + n of the storage, relative to elem_base) move to the kernel's
+    (N,K) frame n*K + k and are located per (column, K slice) with searchsorted."""
+    M, K = a.shape
+    N = packed.shape[1]
+    ldk = packed.stride(0)
+    plan = (ctypes.c_int64 * 2)()
+    nat.check(L.pp_dual_mfma_plan(M, N, K, ctypes.byref(plan, 0), ctypes.byref(plan, 8)), "pp_dual_mfma_plan")
+    slices, cols = int(plan[0]), int(plan[1])
+    row_plug = None
+    if pn:
+        p = (keep[0].view(torch.int32).to(torch.int64) & 0xFFFFFFFF) - elem_base
+        k, n = p // ldk, p % ldk
+        ok = (p >= 0) & (k < K) & (n < N)
+        pos = (n * K + k)[ok]
+        order = torch.argsort(pos)
+        pos = pos[order]
+        amps = keep[1][ok][order].contiguous()
+        pn = int(pos.numel())
+        keep = (torch.where(pos >= 2 ** 31, pos - 2 ** 32, pos).to(torch.int32).contiguous(), amps)
+        keys = (torch.arange(N, device=dev, dtype=torch.int64)[:, None] * K
+                + torch.arange(slices, device=dev, dtype=torch.int64)[None, :] * cols).reshape(-1)
+        keys = torch.cat([keys, torch.tensor([N * K], device=dev, dtype=torch.int64)])
+        row_plug = torch.searchsorted(pos, keys)
+    ws_bytes = L.pp_dual_mfma_workspace_size(M, N, slices)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = L.pp_dual_mfma(packed.data_ptr(), ldk, a.data_ptr(), a.stride(0), bmax.data_ptr(), group_size,
+                        amp_lut.data_ptr(), amp_lut.numel(), cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases,
+                        lut_dt, keep[0].data_ptr() if pn else None, keep[1].data_ptr() if pn else None, pn,
+                        row_plug.data_ptr() if row_plug is not None else None, 0, K, slices, cols,
+                        out1.data_ptr(), out2.data_ptr(), out1.stride(0), M, N, K,
+                        ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    nat.check(rc, "pp_dual_mfma")
+    del keep, row_plug, ws
 
 
 def dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases=1024, group_size=32, *, plug=None,

@@ -237,6 +237,40 @@ def test_quad_layer_dequant_float32_mode_is_the_rounded_float64():
     assert a[2][0, 123] == np.float32(rss * luts32[5][q3]) and a[1][0, 123] == np.float32(rs * luts32[3][q2])
 
 
+def test_dual_layer_dequant_float32_mode_and_plug():
+    """The float32 evaluation of the kernel-layout dual decode is the float64 one up to
+    its two product roundings, each value is the explicit float32 chain
+    (amp_lut * bmax) * cos, and a plug amplitude replaces amp_lut * bmax of its element."""
+    K, N = 64, 48
+    rng = np.random.default_rng(8)
+    packed = olay.pack_amp_phase(rng.integers(0, 64, (K, N)), rng.integers(0, 1024, (K, N))).astype(np.int16)
+    bmax = (rng.random((K * N + 31) // 32) * 2 + 0.01).astype(np.float16)
+    i = np.arange(64, dtype=np.float64)
+    amp_lut = ((np.exp(i / 63 * math.log1p(255.0)) - 1) / 255.0).astype(np.float16)
+    ph = np.linspace(-math.pi, math.pi, 1025)[:-1]
+    cos_lut, sin_lut = np.cos(ph).astype(np.float16), np.sin(ph).astype(np.float16)
+    a = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, dtype=np.float32)
+    b = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut)
+    for x, y in zip(a, b):
+        assert x.dtype == np.float32
+        np.testing.assert_allclose(x, y, rtol=2 * 2.0 ** -24, atol=1e-30)
+    k, n = 17, 45
+    p = int(packed[k, n]) + 32768
+    amp = np.float32(np.float32(amp_lut[(p >> 10) & 63]) * np.float32(bmax[(k * N + n) // 32]))
+    assert a[0][k, n] == np.float32(amp * np.float32(cos_lut[p & 1023]))
+    assert a[1][k, n] == np.float32(amp * np.float32(sin_lut[p & 1023]))
+    kk, nn = np.array([3, 17]), np.array([5, 45])
+    pa = np.array([0.25, 1.5], np.float16)
+    c = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, plug=(kk, nn, pa))
+    ph_q = (packed.astype(np.int32) + 32768) & 1023
+    for j in range(2):
+        assert c[0][kk[j], nn[j]] == float(pa[j]) * float(cos_lut[ph_q[kk[j], nn[j]]])
+        assert c[1][kk[j], nn[j]] == float(pa[j]) * float(sin_lut[ph_q[kk[j], nn[j]]])
+    others = np.ones((K, N), bool)
+    others[kk, nn] = False
+    assert np.array_equal(c[0][others], b[0][others])
+
+
 def test_dual_layer_dequant_group_index_and_offset():
     K, N = 5, 40
     rng = np.random.default_rng(2)
