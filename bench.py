@@ -32,7 +32,9 @@ Other workloads (``--workload``), one JSON line each:
                     torch's fp16 matmul of the unpacked weights (one line per operator);
 * ``quadbig``    -- the fused large-batch quad kernel (quad_bitpacked(fused=True)) on the
                     refbench layer at ``--big-tokens`` tokens, against the matrix cores'
-                    fp16 roofline (one line per batch size).
+                    fp16 roofline (one line per batch size);
+* ``dualmfma``   -- the dual matrix-core decode (polar_dual_bitpacked(fused=True)) on the
+                    refbench dual layer at ``--dual-tokens`` tokens, the same roofline.
 
 Single-Linear workloads rotate enough copies of the packed weights (>= 512 MB in total)
 that no launch finds its codes in the 256 MB last-level cache, and time a HIP graph of
@@ -758,6 +760,34 @@ def run_quadbig(args, dev, log):
               "N": N, "models": 4, "tokens": M, "flops_per_call": 8 * M * K * N}, bound="mfma")
 
 
+def run_dualmfma(args, dev, log):
+    """The dual matrix-core decode (pp_dual_mfma) on the reference benchmark's dual layer
+    (2 models of 4096 x 4096 N(0,1) weights packed by quantize_polar_bitpacked, int16 (K,N)
+    codes) at ``--dual-tokens`` tokens, forced with fused=True; checked against fp16
+    torch.matmul of the original weights, timed with HIP events. Roofline: the matrix
+    cores' fp16 dense peak, 4 M K N flops per call."""
+    K = N = 4096
+    g = torch.Generator(device=dev).manual_seed(seed_of(6, 0, 1))
+    ws = [torch.randn(K, N, generator=g, device=dev).to(torch.float16) for _ in range(2)]
+    packed, bmax, amp_lut, cos_lut, sin_lut = pk.quantize_polar_bitpacked(ws[0], ws[1])
+    for M in args.dual_tokens:
+        a = torch.randn(M, K, generator=g, device=dev).to(torch.float16)
+        run = lambda: pk.polar_dual_bitpacked(a, packed, bmax, amp_lut, cos_lut, sin_lut, fused=True)
+        for o, w in zip(run(), ws):
+            r = torch.matmul(a, w).float()
+            d = (o.float() - r).abs().max().item()
+            if not d <= 0.05 * r.abs().max().item():
+                raise SystemExit(f"dualmfma M={M}: max |diff| {d} vs fp16 matmul")
+        per, _ = time_events(run, args.steps, args.warmup)
+        ms = float(np.mean(per))
+        tflops = 4.0 * M * K * N / (ms * 1e-3) / 1e12
+        log(f"[bench] dualmfma M={M}: {ms * 1e3:.1f} us per call -> {tflops:.0f} TFLOP/s")
+        line("TFLOP/s of the dual matrix-core decode (2 models) on a 4096x4096 layer", tflops, ms, args,
+             "fp16 operands, fp32 sums",
+             {"workload": f"polar_dual_bitpacked(fused=True), 4096x4096 quantize_polar_bitpacked codes, {M} tokens",
+              "K": K, "N": N, "models": 2, "tokens": M, "flops_per_call": 4 * M * K * N}, bound="mfma")
+
+
 def run_sweep(args, dev, log):
     for name, N, K in (("gate_proj", 11008, 2048), ("down_proj", 2048, 11008)):
         if name not in args.sweep_shapes:
@@ -777,8 +807,9 @@ def main():
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--workload", default="quad3b",
                     choices=["quad3b", "dual3b", "dual3b-pad", "dual2048", "quadgate", "sweep", "refbench",
-                             "quadbig"])
+                             "quadbig", "dualmfma"])
     ap.add_argument("--big-tokens", type=int, nargs="+", default=[128, 1024])
+    ap.add_argument("--dual-tokens", type=int, nargs="+", default=[8, 32, 64])
     ap.add_argument("--sweep-tokens", type=int, nargs="+", default=[1, 4, 16, 64])
     ap.add_argument("--sweep-shapes", nargs="+", default=["gate_proj", "down_proj"],
                     choices=["gate_proj", "down_proj"])
@@ -815,6 +846,8 @@ def main():
         run_refbench(args, dev, log)
     elif args.workload == "quadbig":
         run_quadbig(args, dev, log)
+    elif args.workload == "dualmfma":
+        run_dualmfma(args, dev, log)
     else:
         run_sweep(args, dev, log)
 

@@ -269,31 +269,6 @@ int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const void* a, i
 int pp_quad_big_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* slice_cols);
 int64_t pp_quad_big_workspace_size(int64_t M, int64_t N, int64_t slices);
 
-/*
- * Dual decode GEMM on the matrix cores for batches (used for more than 8 tokens): the
- * product of polar_dual_bitpacked (polar_kernels.py:27-115) on the int16 (K,N) codes that
- * quantize_polar_bitpacked returns (row k at codes + k*ldk, ldk >= N; stored = code - 32768;
- * group scales bmax[(k*N + n) / group_size], group_size a power of two), each weight rounded
- * to fp16 before the product as the reference's tl.dot takes it, no weight written to
- * memory.  K % 32 == 0.  Plug entries (sorted positions, fp16 amplitudes replacing the
- * table amplitude times the group scale, polar_bitpack.py:240-243) are read in an (N,K)
- * frame: the entry of (column n, row k) has position plug_pos0 + n*plug_ld + k (the host
- * moves the (K,N) storage positions there); row_plug[n*slices + s] (N*slices + 1 entries)
- * is the first entry at or after plug_pos0 + n*plug_ld + s*slice_cols, the last one
- * plug_pos0 + N*plug_ld.  slices / slice_cols from pp_dual_mfma_plan; with slices > 1 the
- * workspace (pp_dual_mfma_workspace_size bytes) holds float32 partial sums: zero before the
- * first call, left zero by every call; calls that share it must not overlap.
- */
-int pp_dual_mfma(const void* codes, int64_t ldk, const void* a, int64_t a_sm, const void* bmax,
-                 int64_t group_size, const void* amp_lut, int amp_n, const void* cos_lut,
-                 const void* sin_lut, int phase_n, int lut_dtype, const uint32_t* plug_idx,
-                 const void* plug_amp, int64_t plug_n, const int64_t* row_plug, int64_t plug_pos0,
-                 int64_t plug_ld, int64_t slices, int64_t slice_cols, void* out1, void* out2,
-                 int64_t o_sm, int64_t M, int64_t N, int64_t K, void* workspace,
-                 int64_t workspace_bytes, void* stream);
-/* K slices for pp_dual_mfma at this shape on the current device. */
-int pp_dual_mfma_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* slice_cols);
-int64_t pp_dual_mfma_workspace_size(int64_t M, int64_t N, int64_t slices);
 
 /* Rows per wavefront task the stream decode uses for M tokens (0 and an error for bad M). */
 int pp_quad_stream_rows(int64_t M);
@@ -372,6 +347,32 @@ int64_t pp_dual_gemm_workspace_size(const void* a, int64_t a_sm, int64_t a_sk,
                                     const void* codes, int64_t c_sk, int64_t c_sn,
                                     int64_t group_size, int64_t chunk_size, int64_t elem_base,
                                     int64_t plug_n, int64_t M, int64_t N, int64_t K);
+
+/*
+ * Dual decode GEMM on the matrix cores for batches (used for 5-64 tokens): the
+ * product of polar_dual_bitpacked (polar_kernels.py:27-115) on the int16 (K,N) codes that
+ * quantize_polar_bitpacked returns (row k at codes + k*ldk, ldk >= N; stored = code - 32768;
+ * group scales bmax[(k*N + n) / group_size], group_size a power of two), each weight rounded
+ * to fp16 before the product as the reference's tl.dot takes it, no weight written to
+ * memory.  K % 32 == 0.  Plug entries (sorted positions, fp16 amplitudes replacing the
+ * table amplitude times the group scale, polar_bitpack.py:240-243) are read in an (N,K)
+ * frame: the entry of (column n, row k) has position plug_pos0 + n*plug_ld + k (the host
+ * moves the (K,N) storage positions there); row_plug[n*slices + s] (N*slices + 1 entries)
+ * is the first entry at or after plug_pos0 + n*plug_ld + s*slice_cols, the last one
+ * plug_pos0 + N*plug_ld.  slices / slice_cols from pp_dual_mfma_plan; with slices > 1 the
+ * workspace (pp_dual_mfma_workspace_size bytes) holds float32 partial sums: zero before the
+ * first call, left zero by every call; calls that share it must not overlap.
+ */
+int pp_dual_mfma(const void* codes, int64_t ldk, const void* a, int64_t a_sm, const void* bmax,
+                 int64_t group_size, const void* amp_lut, int amp_n, const void* cos_lut,
+                 const void* sin_lut, int phase_n, int lut_dtype, const uint32_t* plug_idx,
+                 const void* plug_amp, int64_t plug_n, const int64_t* row_plug, int64_t plug_pos0,
+                 int64_t plug_ld, int64_t slices, int64_t slice_cols, void* out1, void* out2,
+                 int64_t o_sm, int64_t M, int64_t N, int64_t K, void* workspace,
+                 int64_t workspace_bytes, void* stream);
+/* K slices for pp_dual_mfma at this shape on the current device. */
+int pp_dual_mfma_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* slice_cols);
+int64_t pp_dual_mfma_workspace_size(int64_t M, int64_t N, int64_t slices);
 
 /* Dequantise to float32 (w1, w2) over a (K,N) view; parity / debug export.
  * Replaces the decode of unpack_dual_models (polar_bitpack.py:228-247). */
