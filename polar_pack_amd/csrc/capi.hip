@@ -17,6 +17,37 @@ void set_error(const char* fmt, ...) {
   g_last_error = buf;
 }
 
+// The current device's side stream and its fork / join events, created on first use and
+// kept until the process ends; default priority.  side_lock serialises the enqueue of a
+// fork / side launch / join sequence, so that concurrent callers do not cross events.
+std::mutex& side_lock() {
+  static std::mutex mu;
+  return mu;
+}
+
+int side_stream(hipStream_t* side, hipEvent_t* fork, hipEvent_t* join) {
+  struct Side {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+  };
+  static std::mutex mu;
+  static std::vector<Side> cache;
+  int dev = 0;
+  PP_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)cache.size() <= dev) cache.resize(dev + 1);
+  Side& c = cache[dev];
+  if (c.s == nullptr) {
+    PP_HIP(hipStreamCreateWithFlags(&c.s, hipStreamNonBlocking));
+    PP_HIP(hipEventCreateWithFlags(&c.fork, hipEventDisableTiming));
+    PP_HIP(hipEventCreateWithFlags(&c.join, hipEventDisableTiming));
+  }
+  *side = c.s;
+  *fork = c.fork;
+  *join = c.join;
+  return PP_OK;
+}
+
 int device_cu_count() {
   static std::mutex mu;
   static std::vector<int> cache;

@@ -914,6 +914,20 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
   A.M = (int)M;
   A.ws = workspace;
   const bool be = code_layout == PP_DUAL_U16_BE;
+  // With both launches, the tail rows (fp16 streaming, little arithmetic) run on a side
+  // stream beside the row kernel (bound by its decode arithmetic, not by HBM): the two write
+  // disjoint rows and share no workspace.  The side stream forks from and joins back into
+  // the caller's stream, so the call orders like one launch on it.
+  std::unique_lock<std::mutex> side_held;
+  hipStream_t tail_st = st;
+  hipEvent_t join = nullptr;
+  if (n_segs > 0 && n_tail > 0) {
+    hipEvent_t fork = nullptr;
+    if (int rc = side_stream(&tail_st, &fork, &join)) return rc;
+    side_held = std::unique_lock<std::mutex>(side_lock());
+    PP_HIP(hipEventRecord(fork, st));
+    PP_HIP(hipStreamWaitEvent(tail_st, fork, 0));
+  }
   if (n_segs > 0) {
     int rc;
     const int pw = plug_windows;
@@ -936,9 +950,18 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
       T.tail_len[m] = tail_len ? tail_len[m] : 0;
     }
     int rc;
-    if (be) rc = sm == 0 ? dispatch_dual_tail<PP_DUAL_U16_BE, 0>(T, mt, st) : dispatch_dual_tail<PP_DUAL_U16_BE, 1>(T, mt, st);
-    else rc = sm == 0 ? dispatch_dual_tail<PP_DUAL_I16_OFFSET, 0>(T, mt, st)
-                      : dispatch_dual_tail<PP_DUAL_I16_OFFSET, 1>(T, mt, st);
+    if (be) rc = sm == 0 ? dispatch_dual_tail<PP_DUAL_U16_BE, 0>(T, mt, tail_st)
+                         : dispatch_dual_tail<PP_DUAL_U16_BE, 1>(T, mt, tail_st);
+    else rc = sm == 0 ? dispatch_dual_tail<PP_DUAL_I16_OFFSET, 0>(T, mt, tail_st)
+                      : dispatch_dual_tail<PP_DUAL_I16_OFFSET, 1>(T, mt, tail_st);
+    if (join != nullptr) {
+      // join even if the tail launch failed, so the caller's stream never runs ahead of it
+      const hipError_t e1 = hipEventRecord(join, tail_st);
+      const hipError_t e2 = hipStreamWaitEvent(st, join, 0);
+      if (rc) return rc;
+      PP_HIP(e1);
+      PP_HIP(e2);
+    }
     if (rc) return rc;
   }
   return PP_OK;

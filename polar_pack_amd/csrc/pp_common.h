@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/polar_pack.h"
@@ -40,6 +41,10 @@ void set_error(const char* fmt, ...);
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 int device_cu_count();  // cached per device
+// The current device's side stream with a fork and a join event (see capi.hip), and the
+// lock that a fork / side launch / join sequence is enqueued under.
+int side_stream(hipStream_t* side, hipEvent_t* fork, hipEvent_t* join);
+std::mutex& side_lock();
 
 // ---------------------------------------------------------------- device side
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
