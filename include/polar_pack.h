@@ -240,10 +240,11 @@ int64_t pp_quad_mfma_workspace_size(int64_t M, int64_t N, int64_t slices);
 int64_t pp_quad_mfma_waves(int64_t M);
 
 /*
- * Large-batch decode GEMM on the matrix cores (any M >= 1; used for more than 64 tokens):
- * the same product as pp_quad_mfma, fused, replacing the reference's tl.dot path for
- * its prefill batch sizes (quad_kernels.py:53-67, 123-134, 166-189), with no weight
- * written to memory.  Each code word is decoded once per 128 tokens.
+ * Fused decode GEMM on the matrix cores (any M >= 1; used for more than 64 tokens, and
+ * from 9 tokens on PP_QUAD_KN storage): the same product as pp_quad_mfma, replacing the
+ * reference's tl.dot path for its batch sizes (quad_kernels.py:53-67, 123-134, 166-189),
+ * with no weight written to memory.  Each code word is decoded once per block of 16, 32,
+ * 64 or 128 tokens (the smallest that holds M; the plan depends on M).
  *   layout PP_QUAD_NK: codes (N,K) row-major, row n at codes + n*ldc (ldc >= K, a
  *                      multiple of 4, 16-byte aligned): the container stream layout;
  *   layout PP_QUAD_KN: codes (K,N), row k at codes + k*ldc (ldc >= N): the layout

@@ -1,23 +1,24 @@
-// Quad-pack decode GEMM for large batches (more than 64 tokens) on the matrix cores: one
-// fused pass produces the 4 models' outputs
+// Quad-pack decode GEMM on the matrix cores for large batches (more than 64 tokens), and
+// for 9-64 tokens on (K,N) storage: one fused pass produces the 4 models' outputs
 //   out_m[j, n] = fp16( s_m * sum_k x[j, k] * W_m[n, k] )
 // (quad_kernels.py:123-134) with W_m decoded from the codes in registers
 // (quad_kernels.py:103-121, quaternion_packer.py:173-185), the plug table patched into
 // the decoded operands (quaternion_packer.py:187-193), and no weight ever written to
 // memory.
 //
-// Work item = 16 weight rows x 128 tokens x one K slice, one wavefront,
-// v_mfma_f32_16x16x32_f16 (operand layouts as in quad_mfma.hip):
+// Work item = 16 weight rows x TT token tiles of 16 (TT = 1, 2, 4 or 8, the fewest that
+// hold the batch) x one K slice, one wavefront, v_mfma_f32_16x16x32_f16 (operand layouts
+// as in quad_mfma.hip):
 //  * per 32-column step a lane decodes 8 code words of its row (n0 + i, i = lane % 16,
-//    columns k0 + 8(lane/16) .. +7), so each code word is decoded once per 128 tokens and
-//    feeds 4 models x 8 token tiles of products;
+//    columns k0 + 8(lane/16) .. +7), so each code word is decoded once per 16 TT tokens and
+//    feeds 4 models x TT token tiles of products;
 //  * x is the B operand as stored: lane l reads tokens 16t + l%16 at the same 8 columns;
-//  * 4 models x 8 token tiles of 16 x 16 fp32 sums stay in registers, with two buffers
-//    each of codes (loaded a step ahead), of x (loaded a step before the products that
-//    use it) and of decoded operands: a wavefront takes a SIMD's register file (4 waves per
-//    workgroup, one workgroup per CU: the decode tables fill the LDS);
-//  * the products of step s - 1 are issued between the arithmetic of step s (the only
-//    wave on its SIMD has no other wave to overlap them with), after step s's LDS lookups.
+//  * 4 models x TT token tiles of 16 x 16 fp32 sums stay in registers, with G buffers of
+//    codes (loaded G - 1 steps ahead), two of x (loaded a step before the products that
+//    use it) and two of decoded operands (QbCfg: with 8 tiles a wavefront takes a SIMD's
+//    register file, with fewer two share it);
+//  * the products of step s - 1 are issued between the arithmetic of step s, after step
+//    s's LDS lookups (with one tile, step s + 1's).
 // Codes in either storage: (N,K) rows (the stream container, K contiguous: two 16-byte
 // loads per step) or (K,N) (pack_quad_layer, N contiguous: 8 four-byte loads per step,
 // each a 64-byte run over 16 lanes).  Plug positions are read in an (N,K) frame (position
@@ -29,11 +30,28 @@
 
 namespace pp {
 
-constexpr int QB_NT = 256;      // 4 waves, one per SIMD
-constexpr int QB_WAVES = QB_NT / 64;
 constexpr int QB_ROWS = 16;     // weight rows per item
-constexpr int QB_TT = 8;        // 16-token tiles per item
-constexpr int QB_GROUP = 2;     // steps per loop pass (2 code buffers, 2 x buffers, 2 operand sets)
+
+// TT 16-token tiles per item (1, 2, 4 or 8: up to 16, 32, 64 or 128 tokens).  With 8 tiles
+// a wavefront takes a SIMD's register file (4 waves per workgroup, one per SIMD); with up
+// to 4 it fits in half of it (8 waves, two per SIMD, each hiding the other's waits).
+// One workgroup per CU: the decode tables fill the LDS.
+// G: steps per loop pass = code buffers, the codes of a step loaded G - 1 steps before it
+// (2 KiB per wave and step: with few token tiles the decode is short and a wave needs
+// several steps of codes in flight to cover the HBM latency; with 8 the registers allow 2).
+template <int TT> struct QbCfg {
+  static constexpr int WPE = TT == 8 ? 1 : 2;    // waves per SIMD
+  static constexpr int NT = 256 * WPE;
+  static constexpr int WAVES = NT / 64;
+  static constexpr int G = TT <= 2 ? 4 : 2;
+  // LA: look up the codes of step s + 1 in step s, so that a step's arithmetic never waits
+  // on its own lookups (needs the codes two steps ahead, G >= 3, and a second set of
+  // lookup registers: room for it with one token tile)
+  static constexpr bool LA = TT == 1;
+};
+
+// Token tiles per item for a batch of M tokens.
+static inline int qb_tt(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
 
 struct QuadBigArgs {
   const uint32_t* codes;
@@ -58,18 +76,19 @@ struct QuadBigArgs {
 struct QbCodes {
   u32x4 c[2];              // 8 code words of the lane's row
 };
+template <int TT>
 struct QbX {
-  u32x4 xb[QB_TT];         // 8 fp16 x of token 16t + l%16
+  u32x4 xb[TT];            // 8 fp16 x of token 16t + l%16
 };
 
-// Issue the code loads of the step at column k0 (clamped to the last step: a step past the
-// slice end reads valid codes whose products are zero).  voc: the lane's code offset (OOB
-// for a row past N).  (K,N) storage: the 8 columns' rows are 4*ldc bytes apart, an offset
-// carried in the scalar operand.
+// Issue the code loads of the step at column k0, clamped to the slice's last step (ke - 32:
+// a step past the slice end reloads codes just read, whose products are zero).  voc: the
+// lane's code offset (OOB for a row past N).  (K,N) storage: the 8 columns' rows are 4*ldc
+// bytes apart, an offset carried in the scalar operand.
 template <bool KN>
-__device__ __forceinline__ void qb_codes(const QuadBigArgs& A, const uint32_t* ctile, int n0, int k0, uint32_t voc,
-                                         QbCodes& S) {
-  k0 = min(k0, A.K - 32);
+__device__ __forceinline__ void qb_codes(const QuadBigArgs& A, const uint32_t* ctile, int n0, int k0, int ke,
+                                         uint32_t voc, QbCodes& S) {
+  k0 = min(k0, ke - 32);
   if constexpr (!KN) {
     const int nr = min(QB_ROWS, A.N - n0);
     const rsrc_t rc = make_rsrc(ctile + k0, 4u * (uint32_t)((int64_t)(nr - 1) * A.ldc + (A.K - k0)));
@@ -87,12 +106,13 @@ __device__ __forceinline__ void qb_codes(const QuadBigArgs& A, const uint32_t* c
 // Issue the x loads of the step at column k0: vox, the lane's offsets per token tile (OOB
 // past M).  A step at or past the slice end ke (the walk runs whole groups of steps) reads
 // through an empty buffer record, i.e. zeros, so its products add nothing.
-__device__ __forceinline__ void qb_x(const QuadBigArgs& A, int k0, int ke, const uint32_t (&vox)[QB_TT],
-                                     const f16* xblk, int j0, QbX& S) {
+template <int TT>
+__device__ __forceinline__ void qb_x(const QuadBigArgs& A, int k0, int ke, const uint32_t (&vox)[TT],
+                                     const f16* xblk, int j0, QbX<TT>& S) {
   const uint32_t xrec = k0 < ke ? 2u * (uint32_t)((int64_t)(A.M - 1 - j0) * A.x_sm + (ke - k0)) : 0u;
   const rsrc_t rx = make_rsrc(xblk + min(k0, A.K - 32), xrec);
 #pragma unroll
-  for (int t = 0; t < QB_TT; ++t) vload128c(S.xb[t], vox[t], rx);
+  for (int t = 0; t < TT; ++t) vload128c(S.xb[t], vox[t], rx);
 }
 
 // The LDS lookups of 8 code words, issued together, and the arithmetic on them.
@@ -120,7 +140,7 @@ __device__ __forceinline__ void math8(const Look8& o, h8 (&a)[4]) {
   }
 }
 
-template <bool KN, bool PLUG, class L>
+template <int TT, bool KN, bool PLUG, class L>
 struct QbRun {
   const char* lds;
   LaneOff lo;
@@ -129,68 +149,69 @@ struct QbRun {
   const f16* xblk;
   int n0, j0, q, ke;
   uint32_t voc;
-  uint32_t vox[QB_TT];
+  uint32_t vox[TT];
   int64_t rowpos;
   MPlug P;
-  f4 C[4][QB_TT];
+  f4 C[4][TT];
 
-  __device__ __forceinline__ void mfma(const h8 (&a)[4], const QbX& S) {
+  __device__ __forceinline__ void mfma(const h8 (&a)[4], const QbX<TT>& S) {
 #pragma unroll
-    for (int t = 0; t < QB_TT; ++t) {
+    for (int t = 0; t < TT; ++t) {
       const h8 b = __builtin_bit_cast(h8, S.xb[t]);
 #pragma unroll
       for (int m = 0; m < 4; ++m) C[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[m], b, C[m][t], 0, 0, 0);
     }
   }
 
-  // Step at k0: issue the code loads of k0 + 32 into nxt and the x loads of k0 into xnow
-  // (used by the next step), look up cur's codes, then the products of the previous step
-  // (operands aprev, x in xprev) interleaved with the arithmetic of this one into anew.
-  __device__ __forceinline__ void step(const QbCodes& cur, QbCodes& nxt, QbX& xnow, const QbX& xprev,
-                                       const h8 (&aprev)[4], h8 (&anew)[4], int k0) {
-    qb_codes<KN>(A, ctile, n0, k0 + 32, voc, nxt);
+  // Step at k0: issue the code loads of k0 + 32 (G - 1) into nxt and the x loads of k0 into
+  // xnow (used by the next step), the lookups of the codes `look` into lnew (this step's,
+  // or with LA the next step's), then the products of the previous step (operands aprev, x
+  // in xprev) interleaved with the arithmetic of this one (lookups lcur) into anew.
+  __device__ __forceinline__ void step(const QbCodes& look, QbCodes& nxt, QbX<TT>& xnow, const QbX<TT>& xprev,
+                                       const h8 (&aprev)[4], h8 (&anew)[4], Look8& lnew, const Look8& lcur, int k0) {
+    qb_codes<KN>(A, ctile, n0, k0 + 32 * (QbCfg<TT>::G - 1), ke, voc, nxt);
     qb_x(A, k0, ke, vox, xblk, j0, xnow);
-    Look8 lk;
-    look8<L>(lds, lo, cur.c[0], cur.c[1], lk);
+    look8<L>(lds, lo, look.c[0], look.c[1], lnew);
     __builtin_amdgcn_sched_barrier(0);
     mfma(aprev, xprev);
-    math8(lk, anew);
-    // 32 products, 64 arithmetic instructions: one product, then two
+    math8(lcur, anew);
+    // 4 TT products against about 64 arithmetic instructions: one product, then 16 / TT
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 4 * TT; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 16 / TT, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (PLUG) mplug_patch(A.plug, P, rowpos, k0 + 8 * q, k0, anew);
   }
 };
 
-template <bool KN, bool PLUG, class L>
+template <int TT, bool KN, bool PLUG, class L>
 __device__ __forceinline__ void qb_body(const char* lds, const QuadBigArgs& A) {
+  constexpr int WAVES = QbCfg<TT>::WAVES;
   const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
   const LaneOff lo = L::lane(lane);
   int b = blockIdx.x;
   if (A.xcd_remap) b = (b & 7) * (int)(gridDim.x >> 3) + (b >> 3);
-  const int64_t gw = (int64_t)b * QB_WAVES + uniform(threadIdx.x >> 6);
-  const int64_t nw = (int64_t)gridDim.x * QB_WAVES;
-  // Items in groups of QB_WAVES row tiles that share a token block and K slice, one group
+  const int64_t gw = (int64_t)b * WAVES + uniform(threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * WAVES;
+  // Items in groups of WAVES row tiles that share a token block and K slice, one group
   // per workgroup (its waves read the same x, through the CU's L1); groups ordered slice,
   // token block, row tiles, so the workgroups of one XCD (consecutive after the remap)
   // share row tiles (codes) and token blocks (x) through its L2.
-  const int64_t tgroups = (A.tiles + QB_WAVES - 1) / QB_WAVES;
-  const int64_t items = tgroups * QB_WAVES * A.tblocks * A.slices;
+  const int64_t tgroups = (A.tiles + WAVES - 1) / WAVES;
+  const int64_t items = tgroups * WAVES * A.tblocks * A.slices;
   for (int64_t it = gw; it < items; it += nw) {
-    const int64_t w = uniform64(it / QB_WAVES);
-    const int tile = (int)(uniform64(w / ((int64_t)A.slices * A.tblocks)) * QB_WAVES + it % QB_WAVES);
+    const int64_t w = uniform64(it / WAVES);
+    const int tile = (int)(uniform64(w / ((int64_t)A.slices * A.tblocks)) * WAVES + it % WAVES);
     const int sl = (int)(w % A.slices), tb = (int)((w / A.slices) % A.tblocks);
     if (tile >= A.tiles) continue;
-    const int n0 = tile * QB_ROWS, j0 = tb * 16 * QB_TT;
+    const int n0 = tile * QB_ROWS, j0 = tb * 16 * TT;
     const int kb = sl * A.ks, ke = min(A.K, kb + A.ks);
-    QbRun<KN, PLUG, L> R{lds, lo, A, KN ? A.codes + n0 : A.codes + (int64_t)n0 * A.ldc,
-                         A.x + (int64_t)j0 * A.x_sm, n0, j0, q, ke};
+    QbRun<TT, KN, PLUG, L> R{lds, lo, A, KN ? A.codes + n0 : A.codes + (int64_t)n0 * A.ldc,
+                             A.x + (int64_t)j0 * A.x_sm, n0, j0, q, ke};
 #pragma unroll
-    for (int t = 0; t < QB_TT; ++t) {
+    for (int t = 0; t < TT; ++t) {
       const int jl = 16 * t + i;
       R.vox[t] = j0 + jl < A.M ? 2u * (uint32_t)(jl * A.x_sm + 8 * q) : OOB;
     }
@@ -204,34 +225,52 @@ __device__ __forceinline__ void qb_body(const char* lds, const QuadBigArgs& A) {
       R.P.end = ok ? A.row_plug[(int64_t)n * A.slices + sl + 1] : 0;
       mplug_issue(A.plug, R.P, pidx);
     }
-    QbCodes C0, C1;
-    QbX X0, X1;
-    qb_codes<KN>(A, R.ctile, n0, kb, R.voc, C0);
+    constexpr int G = QbCfg<TT>::G;
+    QbCodes C[G];
+    QbX<TT> X0, X1;
+#pragma unroll
+    for (int g = 0; g + 1 < G; ++g) qb_codes<KN>(A, R.ctile, n0, kb + 32 * g, ke, R.voc, C[g]);
     if constexpr (PLUG) mplug_take(R.P, pidx, R.rowpos);
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
-      for (int t = 0; t < QB_TT; ++t) R.C[m][t] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < TT; ++t) R.C[m][t] = f4{0.f, 0.f, 0.f, 0.f};
     // step s reads code buffer s % 2, loads x buffer s % 2 and writes operand set s % 2;
     // the "previous step" of the first one multiplies zeros
     h8 Aa[4], Ab[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) Ab[m] = h8{};
 #pragma unroll
-    for (int t = 0; t < QB_TT; ++t) X1.xb[t] = u32x4{0u, 0u, 0u, 0u};
+    for (int t = 0; t < TT; ++t) X1.xb[t] = u32x4{0u, 0u, 0u, 0u};
     // whole groups of steps with no exit between them, so that each load is issued in the
     // step that starts it (not moved by the compiler towards the block that reads it)
-    int k0 = kb;
-    for (; k0 < ke; k0 += 32 * QB_GROUP) {
-      R.step(C0, C1, X0, X1, Ab, Aa, k0);
-      R.step(C1, C0, X1, X0, Aa, Ab, k0 + 32);
+    if constexpr (QbCfg<TT>::LA) {
+      // step s looks up the codes of step s + 1 into set (s + 1) % 2 and computes on set s % 2
+      Look8 K0, K1;
+      look8<L>(lds, lo, C[0].c[0], C[0].c[1], K0);
+      for (int k0 = kb; k0 < ke; k0 += 32 * G) {
+#pragma unroll
+        for (int g = 0; g < G; g += 2) {
+          R.step(C[(g + 1) % G], C[(g + G - 1) % G], X0, X1, Ab, Aa, K1, K0, k0 + 32 * g);
+          R.step(C[(g + 2) % G], C[g], X1, X0, Aa, Ab, K0, K1, k0 + 32 * (g + 1));
+        }
+      }
+    } else {
+      Look8 K;
+      for (int k0 = kb; k0 < ke; k0 += 32 * G) {
+#pragma unroll
+        for (int g = 0; g < G; g += 2) {
+          R.step(C[g], C[(g + G - 1) % G], X0, X1, Ab, Aa, K, K, k0 + 32 * g);
+          R.step(C[g + 1], C[g], X1, X0, Aa, Ab, K, K, k0 + 32 * (g + 1));
+        }
+      }
     }
     R.mfma(Ab, X1);   // the last step's products
     // epilogue: lane holds rows n0 + 4q + r, r = 0..3, of token j0 + 16t + i
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
-      for (int t = 0; t < QB_TT; ++t) {
+      for (int t = 0; t < TT; ++t) {
         const int j = j0 + 16 * t + i;
         const int nn = n0 + 4 * q;
         const f4 c = R.C[m][t] * A.s[m];
@@ -257,19 +296,25 @@ __device__ __forceinline__ void qb_body(const char* lds, const QuadBigArgs& A) {
   }
 }
 
-template <bool KN>
-__global__ __launch_bounds__(QB_NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void quad_big_kernel(
-    const QuadBigArgs A) {
+template <int TT, bool KN>
+__global__ __launch_bounds__(QbCfg<TT>::NT)
+__attribute__((amdgpu_waves_per_eu(QbCfg<TT>::WPE, QbCfg<TT>::WPE))) void quad_big_kernel(const QuadBigArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t Tb[QLDS_BYTES / 4];
   const char* lds = reinterpret_cast<const char*>(Tb);
-  const bool shared = quad_tables<QB_NT>(Tb, A.luts);
+  const bool shared = quad_tables<QbCfg<TT>::NT>(Tb, A.luts);
   if (A.plug.n > 0) {
-    if (shared) qb_body<KN, true, LayShared>(lds, A);
-    else qb_body<KN, true, LaySplit>(lds, A);
+    if (shared) qb_body<TT, KN, true, LayShared>(lds, A);
+    else qb_body<TT, KN, true, LaySplit>(lds, A);
   } else {
-    if (shared) qb_body<KN, false, LayShared>(lds, A);
-    else qb_body<KN, false, LaySplit>(lds, A);
+    if (shared) qb_body<TT, KN, false, LayShared>(lds, A);
+    else qb_body<TT, KN, false, LaySplit>(lds, A);
   }
+}
+
+template <int TT>
+static void qb_launch(bool kn, int64_t grid, hipStream_t st, const QuadBigArgs& A) {
+  if (kn) hipLaunchKernelGGL((quad_big_kernel<TT, true>), dim3((unsigned)grid), dim3(QbCfg<TT>::NT), 0, st, A);
+  else hipLaunchKernelGGL((quad_big_kernel<TT, false>), dim3((unsigned)grid), dim3(QbCfg<TT>::NT), 0, st, A);
 }
 
 // Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero.  Runs after the
@@ -307,12 +352,18 @@ __global__ __launch_bounds__(256) void quad_big_finish_kernel(float* acc, f16* o
 
 // K slices for an (N, K) product at M tokens: as many whole 32-column slices as keep the
 // items within one per wavefront.
+static int64_t qb_waves(int tt) {
+  return tt == 1 ? QbCfg<1>::WAVES : tt == 2 ? QbCfg<2>::WAVES : tt == 4 ? QbCfg<4>::WAVES : QbCfg<8>::WAVES;
+}
+
 static void qb_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* cols) {
-  const int64_t waves = (int64_t)device_cu_count() * QB_WAVES;
-  const int64_t units = ((N + QB_ROWS - 1) / QB_ROWS) * ((M + 16 * QB_TT - 1) / (16 * QB_TT));
+  const int tt = qb_tt(M);
+  const int64_t waves = (int64_t)device_cu_count() * qb_waves(tt);
+  const int64_t units = ((N + QB_ROWS - 1) / QB_ROWS) * ((M + 16 * tt - 1) / (16 * tt));
   int64_t s = std::max<int64_t>(1, std::min<int64_t>(K / 32, waves / std::max<int64_t>(1, units)));
   const int64_t per = (K + s - 1) / s;
-  int64_t c = (per + 32 * QB_GROUP - 1) / (32 * QB_GROUP) * (32 * QB_GROUP);   // whole groups of steps
+  const int64_t grp = 32 * (tt == 1 ? QbCfg<1>::G : tt == 2 ? QbCfg<2>::G : tt == 4 ? QbCfg<4>::G : QbCfg<8>::G);
+  int64_t c = (per + grp - 1) / grp * grp;   // whole groups of steps
   if ((K + c - 1) / c != s) c = (per + 31) / 32 * 32;
   *cols = c;
   *slices = (K + c - 1) / c;
@@ -380,8 +431,9 @@ extern "C" int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const
   A.N = (int)N;
   A.K = (int)K;
   A.M = (int)M;
+  const int tt = qb_tt(M);
   A.tiles = (int)((N + QB_ROWS - 1) / QB_ROWS);
-  A.tblocks = (int)((M + 16 * QB_TT - 1) / (16 * QB_TT));
+  A.tblocks = (int)((M + 16 * tt - 1) / (16 * tt));
   A.slices = (int)slices;
   A.ks = (int)slice_cols;
   for (int i = 0; i < 7; ++i) A.luts.p[i] = luts[i];
@@ -392,13 +444,18 @@ extern "C" int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const
   A.ppos0 = plug_pos0;
   A.pld = plug_ld;
   A.acc = reinterpret_cast<float*>(workspace);
-  const int64_t groups = (int64_t)(A.tiles + QB_WAVES - 1) / QB_WAVES * A.tblocks * slices;
+  const int64_t wv = qb_waves(tt);
+  const int64_t groups = (int64_t)(A.tiles + wv - 1) / wv * A.tblocks * slices;
   const int64_t cus = device_cu_count();
   int64_t grid = std::min<int64_t>(cus, groups);
   A.xcd_remap = grid % 8 == 0;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (kn) hipLaunchKernelGGL((quad_big_kernel<true>), dim3((unsigned)grid), dim3(QB_NT), 0, st, A);
-  else hipLaunchKernelGGL((quad_big_kernel<false>), dim3((unsigned)grid), dim3(QB_NT), 0, st, A);
+  switch (tt) {
+    case 1: qb_launch<1>(kn, grid, st, A); break;
+    case 2: qb_launch<2>(kn, grid, st, A); break;
+    case 4: qb_launch<4>(kn, grid, st, A); break;
+    default: qb_launch<8>(kn, grid, st, A); break;
+  }
   PP_LAUNCH_CHECK();
   if (slices > 1) {
     const int64_t total = 4 * N * M;

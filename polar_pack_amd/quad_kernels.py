@@ -127,10 +127,12 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
     of the element at storage offset ``idx - elem_base`` of ``codes``; ``idx`` must be
     strictly ascending, as a ``.quadpack`` file stores it (quaternion_packer.py:104-113):
     checked on the host when ``POLAR_PACK_CHECK_PLUG=1``.
-    ``fused`` (batches above 64 tokens on (N,K) or (K,N) storage): True runs the fused
-    large-batch kernel at any size, False decodes fp16 weights and runs a library GEMM,
-    None (default) picks by size (the fused kernel up to BIG_MAX_M tokens, where it is
-    the faster; above, the decode + GEMM, which needs 8 bytes of scratch per code word).
+    ``fused`` (batches above 64 tokens on (N,K) or (K,N) storage, and 9-64 tokens on (K,N)
+    storage): True runs the fused large-batch kernel at any size, False decodes fp16
+    weights and runs a library GEMM above 64 tokens (and transposes (K,N) codes for the
+    matrix-core batch decode at 9-64), None (default) picks by size (the fused kernel up to
+    BIG_MAX_M tokens, where it is the faster; above, the decode + GEMM, which needs 8 bytes
+    of scratch per code word).
     """
     M, K = a.shape
     K_b, N = codes.shape
@@ -152,11 +154,15 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
     pi, pv, pn, keep = _plug_args(plug, dev)
     L = nat.lib()
     kn = _kn_layout_ok(codes, K, N)
-    big = _big_layout(codes, K, N) if M > BIG_MIN_M else None
-    if big is not None and (fused or (fused is None and M <= BIG_MAX_M)):
-        _quad_big(a, codes, big, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
+    lay = _big_layout(codes, K, N) if M > 8 else None
+    # the fused large-batch kernel: above 64 tokens on either storage; from 9 tokens on
+    # (K,N) storage, which the matrix-core batch decode would first have to transpose
+    if lay is not None and (M > BIG_MIN_M or (lay == nat.PP_QUAD_KN and fused is not False)) \
+            and (fused or (fused is None and M <= BIG_MAX_M)):
+        _quad_big(a, codes, lay, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
         del keep
         return outs
+    big = lay if M > BIG_MIN_M else None
     if big is None and kn and 8 < M <= (KN_MFMA_MAX_M if N > K else PREFILL_M) and K % 32 == 0:
         _quad_kn_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
         del keep
@@ -191,12 +197,14 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
 BIG_MIN_M = 64    # larger batches on (N,K) or (K,N) storage run the fused large-batch kernel ...
 BIG_MAX_M = 128   # ... up to this size by default; above, the fp16 decode + one library GEMM is
 # faster (4096x4096 layer, measured: fused 87.5 us at 128 tokens against 128 us for 4 fp16
-# matmuls; at 1024 tokens fused 291 us, decode 32 us + one batched GEMM 113 us)
+# matmuls; at 1024 tokens fused 291 us, decode 32 us + one batched GEMM 113 us).  On (K,N)
+# storage it also takes 9-64 tokens (4096x4096: 33 / 40 / 58 us at 16 / 32 / 64 tokens
+# against 59 / 65 / 84 us for the transpose + matrix-core batch decode)
 PREFILL_M = 128   # other layouts: batches above this decode once and run a library GEMM
 KN_MAX_M = 16     # (K,N) storage, K % 32 != 0: up to two 8-token passes of the fused kernel
-# (K,N) storage, K % 32 == 0: codes transposed to (N,K) for the matrix cores, up to 64
-# tokens, or up to PREFILL_M when N <= K (measured: 4096x4096 and 11008x2048 gain at 65-128
-# tokens, 2048x11008 loses to the fp16 decode + GEMM route there)
+# (K,N) storage, K % 32 == 0, fused=False: codes transposed to (N,K) for the matrix cores, up
+# to 64 tokens, or up to PREFILL_M when N <= K (measured: 4096x4096 and 11008x2048 gain at
+# 65-128 tokens, 2048x11008 loses to the fp16 decode + GEMM route there)
 KN_MFMA_MAX_M = 64
 
 
@@ -255,8 +263,8 @@ def _big_layout(codes, K, N):
 
 
 def _quad_big(a, codes, layout, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
-    """More than 64 tokens on (N,K) or (K,N) storage: the fused large-batch decode
-    (pp_quad_big).  Plug entries are located per (row, K slice) with searchsorted
+    """More than 64 tokens on (N,K) or (K,N) storage, or 9-64 on (K,N): the fused decode
+    on the matrix cores (pp_quad_big).  Plug entries are located per (row, K slice) with searchsorted
     (quaternion_packer.py:188-189); on (K,N) storage they are first moved to the (N,K)
     frame the kernel reads them in."""
     M, K = a.shape

@@ -1,4 +1,5 @@
-"""GPU parity of the fused large-batch quad decode (pp_quad_big, more than 64 tokens;
+"""GPU parity of the fused quad decode on the matrix cores (pp_quad_big: more than 64
+tokens, and 9-64 tokens on (K,N) storage, in blocks of 1, 2, 4 or 8 token tiles of 16;
 forced with ``fused=True`` above the size where the drop-in operator switches to the fp16
 decode + library GEMM) against the float64 oracle: the fp16 operands the matrix cores
 multiply (the float32 decode rounded once, plug tuples substituted, as the reference's
@@ -77,12 +78,13 @@ def test_container_rows_through_the_drop_in(M):
         pos += N * K
 
 
-@pytest.mark.parametrize("M", [65, 192])
+@pytest.mark.parametrize("M", [9, 16, 17, 33, 64, 65, 192])
 @pytest.mark.parametrize("split", [False, True])
 def test_kn_storage_with_plug_and_wider_rows(M, split):
     """(K,N) codes (pack_quad_layer's layout) as a column slice of a wider tensor (row stride
     520 > N = 300): plug entries of the block are moved to the kernel's (N,K) frame and
-    applied, entries in the columns past N are not; fp16 LUTs, shared or split q1/q2."""
+    applied, entries in the columns past N are not; fp16 LUTs, shared or split q1/q2; 9-192
+    tokens (1, 2, 4 and 8 token tiles, partial tiles)."""
     K, N, ldk = 1024, 300, 520
     seed = 500 + M + split
     wide = random_codes((K, ldk), seed)
@@ -133,12 +135,14 @@ def _call_big(x, codes_nk, luts, scales, plug, elem_base, slices, cols, o_sm):
         assert int(torch.count_nonzero(ws)) == 0, "the workspace is not left zero"
 
 
+@pytest.mark.parametrize("M", [12, 30, 64, 150])
 @pytest.mark.parametrize("slices,cols", [(1, 512), (2, 256), (3, 192), (16, 32)])
-def test_explicit_slices_and_odd_output_stride(slices, cols):
+def test_explicit_slices_and_odd_output_stride(slices, cols, M):
     """Every K-slice plan (one slice: direct fp16 stores; more: float32 atomics and the
-    finish pass), N = 70 (a partial 32-row tile), an odd output row stride (no 4-row
+    finish pass; slices shorter than a loop pass of 2 or 4 steps), N = 70 (a partial 16-row
+    tile), 12-150 tokens (1, 2, 4 and 8 token tiles), an odd output row stride (no 4-row
     stores), and the columns past N left untouched."""
-    N, K, M = 70, 512, 150
+    N, K = 70, 512
     ws_ = gen.correlated_models(31, [N * K] * 4)
     qp = oqp.pack_quad(ws_, threshold=0.02)
     base = 96
@@ -146,18 +150,19 @@ def test_explicit_slices_and_odd_output_stride(slices, cols):
     luts = qk.header_luts(qp.r_max, device=DEV)
     plug = (u32((qp.plug_idx.astype(np.int64) + base).astype(np.uint32)).to(DEV),
             torch.from_numpy(qp.plug_vals).to(DEV))
-    x_np = np.random.default_rng(slices).standard_normal((M, K)).astype(np.float16)
+    x_np = np.random.default_rng(slices + M).standard_normal((M, K)).astype(np.float16)
     x = torch.from_numpy(x_np).to(DEV)
     ref = mfma_reference(qp, 0, N, K, x_np)
     for outs, wide in _call_big(x, codes, luts, list(qp.s), plug, base, slices, cols, N + 3):
-        check_mfma(outs, ref, f"slices={slices}")
+        check_mfma(outs, ref, f"slices={slices} M={M}")
         for w in wide:
             assert bool(torch.isnan(w[:, N:]).all()), "a column past N was written"
 
 
 def test_plan_covers_k():
     L = nat.lib()
-    for M, N, K in ((65, 4096, 4096), (1024, 4096, 4096), (128, 11008, 2048), (300, 2048, 11008), (100, 7, 64)):
+    for M, N, K in ((65, 4096, 4096), (1024, 4096, 4096), (128, 11008, 2048), (300, 2048, 11008), (100, 7, 64),
+                    (9, 4096, 4096), (16, 11008, 2048), (32, 2048, 11008), (64, 300, 96)):
         plan = (ctypes.c_int64 * 2)()
         nat.check(L.pp_quad_big_plan(M, N, K, ctypes.byref(plan, 0), ctypes.byref(plan, 8)), "plan")
         s, c = int(plan[0]), int(plan[1])
@@ -183,7 +188,25 @@ def test_full_size_kn_layer_column_sample():
     check_mfma([o[:, torch.from_numpy(cols).to(DEV)] for o in outs], ref, "4096x4096 M=1024")
 
 
-@pytest.mark.parametrize("M,fused", [(100, False), (300, None)])
+@pytest.mark.parametrize("M", [10, 24, 48])
+def test_kn_default_route_small_batches(M):
+    """9-64 tokens on (K,N) storage take the fused kernel by default (no transposed copy of
+    the codes): the matrix cores' fp16-operand bound, plug entries applied."""
+    K, N = 512, 388
+    seed = 950 + M
+    codes = random_codes((K, N), seed)
+    luts, scales = fp16_luts(seed)
+    rng = np.random.default_rng(seed)
+    flat = np.sort(rng.choice(K * N, 300, replace=False))
+    vals = (rng.standard_normal((300, 4)) * 0.5).astype(np.float16)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    outs = qk.quad_bitpacked(torch.from_numpy(a).to(DEV), u32(codes).to(DEV), [l.to(DEV) for l in luts], scales,
+                             plug=(u32(flat.astype(np.uint32)).to(DEV), torch.from_numpy(vals).to(DEV)))
+    ref = kn_mfma_reference(a, codes, luts, scales, (flat // N, flat % N), vals)
+    check_mfma(outs, ref, f"kn default M={M}")
+
+
+@pytest.mark.parametrize("M,fused", [(40, False), (100, False), (300, None)])
 def test_kn_decode_and_batched_gemm_route(M, fused):
     """(K,N) storage through the fp16 decode + one batched library GEMM (the default above
     128 tokens, or fused=False): the fp16-weight bound and normwise 1e-3 against the exact
