@@ -117,19 +117,49 @@ def _waves_per_group(n_waves, device):
 
 
 def split_factors(shapes, n, rows_per_task, n_waves, block=512, positions=None):
-    """(slices, column blocks per slice) per projection, slices being whole blocks of
-    ``block`` columns (the kernel's chunk width): 1 slice when the launch has at least
-    half as many tasks as wavefronts (measured: splitting then costs more in partial-sum
-    traffic and pipeline restarts than it gains), else enough slices for about one item
-    per wavefront."""
+    """(slices, column blocks per slice, at most) per projection, slices being whole blocks
+    of ``block`` columns (the kernel's chunk width), from r = wavefronts / tasks:
+      * r < 1.5: 1 slice (the tasks fill the launch; measured on 11008x2048 at 1 token,
+        1,376 tasks: 26.7 us whole, 31 us in 2 or 4 slices);
+      * 1.5 <= r < 4: 2 slices for projections of at least 8 blocks (2048x11008 at 2
+        tokens: 35.6 us against 37.2 us whole), else 1;
+      * r >= 4: ceil(r / 2) slices, at most one per block (2048x11008 at 1 token: 31.3 us
+        in 4 slices, 32.6 us in 8, 65 us whole; the dual 2048x2048 Linear: 11.0 us in 4,
+        14.0 us whole): about one item per two wavefronts, since every item adds a
+        reduction, partial-sum atomics and a pipeline restart.
+    :func:`slice_bounds` deals the blocks to the slices."""
     proj, _, _ = plan_tasks(shapes, n, rows_per_task, positions)
     K = np.array([int(b) for _, b in shapes], np.int64)
     blocks = np.maximum(1, (K + block - 1) // block)
-    if proj.size == 0 or 2 * proj.size >= n_waves:
-        return np.ones(len(shapes), np.int64), blocks
-    want = -(-n_waves // proj.size)
-    per = -(-blocks // np.minimum(want, blocks))          # blocks per slice
-    return -(-blocks // per), per
+    ones = np.ones(len(shapes), np.int64)
+    if proj.size == 0:
+        return ones, blocks
+    r = n_waves / proj.size
+    if r >= 4:
+        want = np.full(len(shapes), -(-n_waves // (2 * proj.size)), np.int64)
+    elif r >= 1.5:
+        want = np.where(blocks >= 8, 2, 1)
+    else:
+        return ones, blocks
+    parts = np.maximum(1, np.minimum(want, blocks))
+    per = -(-blocks // parts)                              # blocks per slice, at most
+    return parts, per
+
+
+# Planner cost of each item of a split projection, in bytes, on top of the bytes it reads:
+# its reduction, partial-sum atomics and pipeline restart (measured on 2048x11008 at 1-2
+# tokens: 64 KiB balances the waves best, 2-9 % faster than 0).
+SPLIT_ITEM_COST = 65536
+
+
+def slice_bounds(K, parts, block):
+    """Column ranges of the ``parts`` slices of a K-column projection: the ceil(K / block)
+    blocks dealt as evenly as possible (slice s takes blocks [s*B // parts, (s+1)*B //
+    parts)), so that no slice is left with a sliver of the columns (one 256-column slice
+    among 1536-column ones made the planner give its waves six tasks each: 2.2x the
+    time of the others for the same bytes, from the per-task reduction and restart)."""
+    B = max(1, -(-int(K) // block))
+    return [((sl * B // parts) * block, min(int(K), ((sl + 1) * B // parts) * block)) for sl in range(int(parts))]
 
 
 def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=4, split=False, block=512,
@@ -142,7 +172,8 @@ def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=
     chunks (:func:`split_factors`), the
     slices of a projection ordered slice by slice.  The items are dealt to the wavefronts
     in contiguous runs of equal cost (bytes read, plus ``task_cost`` bytes for each item's
-    reduction and stores), or of cost proportional to ``wave_weights``, and each
+    reduction and stores, plus SPLIT_ITEM_COST for an item of a split projection), or of
+    cost proportional to ``wave_weights``, and each
     wavefront's run is cut into segments of one projection and one slice.  The workspace of split launches holds one uint32
     counter per task, then 4*M*N float32 accumulators per split projection.
     """
@@ -163,16 +194,15 @@ def plan_segments(shapes, n, plug_host, n_waves, rows_per_task, M=1, code_bytes=
             ts = tid[proj == p]
             if ts.size == 0:
                 continue
-            for sl in range(int(parts[p])):
-                k0 = sl * int(per[p]) * block
-                k1 = min(int(K[p]), (sl + 1) * int(per[p]) * block) if parts[p] > 1 else int(K[p])
+            for k0, k1 in slice_bounds(K[p], parts[p], block):
                 chunks.append((ts, np.full(ts.size, k0, np.int64), np.full(ts.size, k1, np.int64)))
         it_task = np.concatenate([c[0] for c in chunks])
         it_k0 = np.concatenate([c[1] for c in chunks])
         it_k1 = np.concatenate([c[2] for c in chunks])
     it_proj = proj[it_task]
     width = it_k1 - it_k0
-    ib = code_bytes * nrows[it_task] * width + 2 * M * width + int(task_cost)
+    ib = code_bytes * nrows[it_task] * width + 2 * M * width + int(task_cost) \
+        + np.where(parts[it_proj] > 1, SPLIT_ITEM_COST, 0)
     tb = wave_bounds(ib, n_waves, wave_weights)
     wave = np.searchsorted(tb, np.arange(it_task.size), side="right") - 1
     brk = np.ones(it_task.size, bool)

@@ -110,11 +110,12 @@ def test_container_file_round_trip_and_validation(tmp_path):
         QuadPackFile.read(bad)
 
 
-@pytest.mark.parametrize("shape", [(256, 2048), (64, 11008), (1000, 1000), (512, 1536)])
+@pytest.mark.parametrize("shape", [(256, 2048), (64, 11008), (600, 4100), (512, 1536)])
 @pytest.mark.parametrize("M", [1, 2, 8])
 def test_single_linear_split_k(shape, M):
-    """One projection, its tasks cut into column slices that meet in the workspace: equal
-    to the oracle, on repeated launches, and the workspace is left zero."""
+    """One projection, its tasks cut into column slices that meet in the workspace (K not
+    a multiple of the 512-column chunk, slices of unequal block counts): equal to the
+    oracle, on repeated launches, and the workspace is left zero."""
     N, K = shape
     models = gen.correlated_models(7, [N * K] * 4)
     qp = oqp.pack_quad(models, threshold=0.004)
