@@ -44,10 +44,6 @@ template <int TT> struct QbCfg {
   static constexpr int NT = 256 * WPE;
   static constexpr int WAVES = NT / 64;
   static constexpr int G = TT <= 2 ? 4 : 2;
-  // LA: look up the codes of step s + 1 in step s, so that a step's arithmetic never waits
-  // on its own lookups (needs the codes two steps ahead, G >= 3, and a second set of
-  // lookup registers: room for it with one token tile)
-  static constexpr bool LA = TT == 1;
 };
 
 // Token tiles per item for a batch of M tokens.
@@ -163,18 +159,20 @@ struct QbRun {
     }
   }
 
-  // Step at k0: issue the code loads of k0 + 32 (G - 1) into nxt and the x loads of k0 into
-  // xnow (used by the next step), the lookups of the codes `look` into lnew (this step's,
-  // or with LA the next step's), then the products of the previous step (operands aprev, x
-  // in xprev) interleaved with the arithmetic of this one (lookups lcur) into anew.
-  __device__ __forceinline__ void step(const QbCodes& look, QbCodes& nxt, QbX<TT>& xnow, const QbX<TT>& xprev,
-                                       const h8 (&aprev)[4], h8 (&anew)[4], Look8& lnew, const Look8& lcur, int k0) {
-    qb_codes<KN>(A, ctile, n0, k0 + 32 * (QbCfg<TT>::G - 1), ke, voc, nxt);
+  // Step at k0: issue the x loads of k0 into xnow (used by the next step) and the code
+  // loads of k0 + 32 (G - 1) into nxt, look up cur's codes, then the products of the
+  // previous step (operands aprev, x in xprev) interleaved with the arithmetic of this one
+  // into anew.  x goes first: the wait for it in the next step (the memory counter drains
+  // in issue order) then leaves the code loads issued after it in flight.
+  __device__ __forceinline__ void step(const QbCodes& cur, QbCodes& nxt, QbX<TT>& xnow, const QbX<TT>& xprev,
+                                       const h8 (&aprev)[4], h8 (&anew)[4], int k0) {
     qb_x(A, k0, ke, vox, xblk, j0, xnow);
-    look8<L>(lds, lo, look.c[0], look.c[1], lnew);
+    qb_codes<KN>(A, ctile, n0, k0 + 32 * (QbCfg<TT>::G - 1), ke, voc, nxt);
+    Look8 lk;
+    look8<L>(lds, lo, cur.c[0], cur.c[1], lk);
     __builtin_amdgcn_sched_barrier(0);
     mfma(aprev, xprev);
-    math8(lcur, anew);
+    math8(lk, anew);
     // 4 TT products against about 64 arithmetic instructions: one product, then 16 / TT
 #pragma unroll
     for (int i = 0; i < 4 * TT; ++i) {
@@ -244,25 +242,11 @@ __device__ __forceinline__ void qb_body(const char* lds, const QuadBigArgs& A) {
     for (int t = 0; t < TT; ++t) X1.xb[t] = u32x4{0u, 0u, 0u, 0u};
     // whole groups of steps with no exit between them, so that each load is issued in the
     // step that starts it (not moved by the compiler towards the block that reads it)
-    if constexpr (QbCfg<TT>::LA) {
-      // step s looks up the codes of step s + 1 into set (s + 1) % 2 and computes on set s % 2
-      Look8 K0, K1;
-      look8<L>(lds, lo, C[0].c[0], C[0].c[1], K0);
-      for (int k0 = kb; k0 < ke; k0 += 32 * G) {
+    for (int k0 = kb; k0 < ke; k0 += 32 * G) {
 #pragma unroll
-        for (int g = 0; g < G; g += 2) {
-          R.step(C[(g + 1) % G], C[(g + G - 1) % G], X0, X1, Ab, Aa, K1, K0, k0 + 32 * g);
-          R.step(C[(g + 2) % G], C[g], X1, X0, Aa, Ab, K0, K1, k0 + 32 * (g + 1));
-        }
-      }
-    } else {
-      Look8 K;
-      for (int k0 = kb; k0 < ke; k0 += 32 * G) {
-#pragma unroll
-        for (int g = 0; g < G; g += 2) {
-          R.step(C[g], C[(g + G - 1) % G], X0, X1, Ab, Aa, K, K, k0 + 32 * g);
-          R.step(C[g + 1], C[g], X1, X0, Aa, Ab, K, K, k0 + 32 * (g + 1));
-        }
+      for (int g = 0; g < G; g += 2) {
+        R.step(C[g], C[(g + G - 1) % G], X0, X1, Ab, Aa, k0 + 32 * g);
+        R.step(C[g + 1], C[g], X1, X0, Aa, Ab, k0 + 32 * (g + 1));
       }
     }
     R.mfma(Ab, X1);   // the last step's products
