@@ -136,3 +136,36 @@ def float_array(vals):
     for i, v in enumerate(vals):
         arr[i] = float(v)
     return arr
+
+
+# Zeroed workspaces of the kernels that take one zero on entry and leave it zero (the K-slice
+# accumulators of pp_quad_mfma, pp_quad_big, pp_dual_mfma): one per (device, stream), grown
+# on demand and reused by every call on that stream, since calls on one stream run in order.
+# A call that fails drops its stream's buffer (it may not have been left zero).  Under
+# stream capture every call gets a fresh zeroed buffer, as the graph records it.
+_zero_ws = {}
+
+
+def zero_workspace(dev, nbytes: int):
+    """(buffer, key): a zeroed uint8 device tensor of at least ``nbytes`` bytes for the current
+    stream of ``dev`` (None when nbytes is 0); pass ``key`` to :func:`drop_workspace` if the
+    call using it fails."""
+    import torch
+    if nbytes <= 0:
+        return None, None
+    stream = torch.cuda.current_stream(dev)
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(nbytes, dtype=torch.uint8, device=dev), None
+    key = (torch.device(dev).index, stream.cuda_stream)
+    with _lock:
+        ws = _zero_ws.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
+            _zero_ws[key] = ws
+    return ws, key
+
+
+def drop_workspace(key) -> None:
+    if key is not None:
+        with _lock:
+            _zero_ws.pop(key, None)

@@ -206,7 +206,7 @@ def _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_siz
         keys = torch.cat([keys, torch.tensor([N * K], device=dev, dtype=torch.int64)])
         row_plug = torch.searchsorted(pos, keys)
     ws_bytes = L.pp_dual_mfma_workspace_size(M, N, slices)
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    ws, wkey = nat.zero_workspace(dev, ws_bytes)
     stream = torch.cuda.current_stream(dev).cuda_stream
     rc = L.pp_dual_mfma(packed.data_ptr(), ldk, a.data_ptr(), a.stride(0), bmax.data_ptr(), group_size,
                         amp_lut.data_ptr(), amp_lut.numel(), cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases,
@@ -214,6 +214,8 @@ def _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_siz
                         row_plug.data_ptr() if row_plug is not None else None, 0, K, slices, cols,
                         out1.data_ptr(), out2.data_ptr(), out1.stride(0), M, N, K,
                         ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    if rc:
+        nat.drop_workspace(wkey)
     nat.check(rc, "pp_dual_mfma")
     del keep, row_plug, ws
 

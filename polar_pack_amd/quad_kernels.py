@@ -291,13 +291,15 @@ def _quad_big(a, codes, layout, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, ou
         keys = torch.cat([keys, torch.tensor([pos0 + N * pld], device=dev, dtype=torch.int64)])
         row_plug = torch.searchsorted(idx, keys)
     ws_bytes = L.pp_quad_big_workspace_size(M, N, slices)
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    ws, wkey = nat.zero_workspace(dev, ws_bytes)
     stream = torch.cuda.current_stream(dev).cuda_stream
     rc = L.pp_quad_big(codes.data_ptr(), layout, ldc, a.data_ptr(), a.stride(0), lut_ptrs, lut_dtype, sc,
                        keep[0].data_ptr() if pn else None, keep[1].data_ptr() if pn else None, pn,
                        row_plug.data_ptr() if row_plug is not None else None, pos0, pld, slices, cols,
                        nat.ptr_array([o.data_ptr() for o in outs]), outs[0].stride(0), M, N, K,
                        ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    if rc:
+        nat.drop_workspace(wkey)
     nat.check(rc, "pp_quad_big")
     del keep, row_plug, ws
     return outs
@@ -349,13 +351,15 @@ def _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, 
         keys = torch.cat([keys, torch.tensor([elem_base + N * ldc], device=dev, dtype=torch.int64)])
         row_plug = torch.searchsorted(idx, keys)
     ws_bytes = L.pp_quad_mfma_workspace_size(M, N, slices)
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+    ws, wkey = nat.zero_workspace(dev, ws_bytes)
     stream = torch.cuda.current_stream(dev).cuda_stream
     rc = L.pp_quad_mfma(codes.data_ptr(), ldc, elem_base, a.data_ptr(), a.stride(0), lut_ptrs, lut_dtype, sc,
                         keep[0].data_ptr() if pn else None, keep[1].data_ptr() if pn else None, pn,
                         row_plug.data_ptr() if row_plug is not None else None, slices, cols,
                         nat.ptr_array([o.data_ptr() for o in outs]), outs[0].stride(0), M, N, K,
                         ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    if rc:
+        nat.drop_workspace(wkey)
     nat.check(rc, "pp_quad_mfma")
     del keep, row_plug, ws
     return outs

@@ -229,3 +229,21 @@ def test_kn_decode_and_batched_gemm_route(M, fused):
         assert outs[m].shape == (M, N) and outs[m].is_contiguous()
         assert_gemv_close(got, exact, f"model {m}", bound=fp16_weight_bound(a, W[m]))
         assert normwise(got, exact) <= 1e-3
+
+
+def test_operator_workspace_reused_and_left_zero():
+    """The drop-in operators keep one zeroed K-slice workspace per stream: repeated calls of
+    different sizes (the buffer grows, then is reused) stay correct and leave it zero."""
+    K, N = 1024, 512
+    codes = random_codes((K, N), 77)
+    luts, scales = fp16_luts(77)
+    dl = [l.to(DEV) for l in luts]
+    dc = u32(codes).to(DEV)
+    for M in (12, 40, 12, 64, 20):
+        a = np.random.default_rng(M).standard_normal((M, K)).astype(np.float16)
+        outs = qk.quad_bitpacked(torch.from_numpy(a).to(DEV), dc, dl, scales)
+        check_mfma(outs, kn_mfma_reference(a, codes, luts, scales), f"reuse M={M}")
+    torch.cuda.synchronize()
+    assert nat._zero_ws, "no cached workspace was used"
+    for ws in nat._zero_ws.values():
+        assert int(torch.count_nonzero(ws)) == 0, "a cached workspace is not left zero"
