@@ -11,15 +11,14 @@ Same names, arguments, return values and error behaviour as the reference
   quaternion_packer.py:187-193) and ``elem_base``.
 * :func:`quad_dequant` -- float32 (or fp16) weights of a code view.
 
-Batches: 1-8 tokens run on the fused decode kernels; 9-128 tokens on the matrix-core
-decode when the codes are an (N,K) block seen as (K,N) (the container layout), 9-64
-(9-128 when N <= K) on (K,N) storage after a transpose of the codes (two 8-token fused
-passes up to 16 tokens when K % 32 != 0); larger batches, and more tokens on other
-layouts, decode once into
-fp16 weights (the
-values the reference's kernel rounds its weights to, quad_kernels.py:117-126) and run a
-library fp16 GEMM (hipBLASLt through torch.matmul), where the matmul's compute, not the
-weight stream, bounds the time.
+Batches: 1-8 tokens run on the fused decode kernels; 9-128 tokens on the matrix cores
+with K % 32 == 0: on an (N,K) block seen as (K,N) (the container layout) the batch decode
+to 64 tokens and the fused kernel above, on (K,N) storage the fused kernel on the codes
+as stored (two 8-token fused passes up to 16 tokens when K % 32 != 0); larger batches, and
+more tokens on other layouts, decode once into fp16 weights (the values the reference's
+kernel rounds its weights to, quad_kernels.py:117-126) and run a library fp16 GEMM
+(hipBLASLt through torch.matmul), where the matmul's compute, not the weight stream, bounds
+the time.
 """
 from __future__ import annotations
 
