@@ -141,6 +141,18 @@ int pp_quad_dequant_f16(const uint32_t* codes, int64_t c_sk, int64_t c_sn,
                         void* const* out, int64_t N, int64_t K, void* stream);
 
 /*
+ * The same, transposed: codes (K,N) with unit column stride and row stride c_sk (>= N, a
+ * multiple of 4, 16-byte aligned rows; the layout pack_quad_layer returns) into
+ * out_m[n*K + k] = fp16(s_m * W_m[k, n]), i.e. W_m^T row-major, the operand a library GEMM
+ * takes fastest for x @ W_m.  N % 8 == 0, K % 8 == 0, 16-byte aligned outputs.  Plug
+ * positions as for pp_quad_dequant_f16.  No counterpart in the reference: the fp16 weights
+ * of its tl.dot, laid out for the prefill GEMM that replaces it (quad_kernels.py:166-189).
+ */
+int pp_quad_dequant_f16_t(const uint32_t* codes, int64_t c_sk, const void* const* luts, int lut_dtype,
+                          const float* scales, const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n,
+                          int64_t elem_base, void* const* out, int64_t N, int64_t K, void* stream);
+
+/*
  * Whole-stream decode for 1..8 tokens: one launch over many projections of one
  * .quadpack stream (the grouped whole-step launch).  All tables are device memory
  * prepared by the host once per stream (see polar_pack_amd/stream.py):
@@ -393,6 +405,18 @@ int pp_dual_dequant_f16(const void* codes, int code_layout, int64_t c_sk, int64_
                         int phase_n, int lut_dtype,
                         const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n, int64_t elem_base,
                         void* out1, void* out2, int64_t N, int64_t K, void* stream);
+
+/* The same, transposed: codes (K,N) with unit column stride and row stride c_sk (>= N, a
+ * multiple of 8, 16-byte aligned rows; the layout quantize_polar_bitpacked returns), the
+ * kernel's group rule (k*N + n) / group_size with a power-of-two group_size >= 8, into
+ * out1[n*K + k] = w1[k, n] and out2 likewise (W^T row-major fp16, for the prefill GEMM
+ * that replaces polar_dual_bitpacked_kernel at large batches, polar_kernels.py:165-184).
+ * N % 8 == 0, K % 8 == 0, 16-byte aligned outputs.  No counterpart in the reference. */
+int pp_dual_dequant_f16_t(const void* codes, int code_layout, int64_t c_sk, const void* bmax, int64_t group_size,
+                          const void* amp_lut, int amp_lut_n, const void* cos_lut, const void* sin_lut,
+                          int phase_n, int lut_dtype, const uint32_t* plug_idx, const void* plug_amp,
+                          int64_t plug_n, int64_t elem_base, void* out1, void* out2, int64_t N, int64_t K,
+                          void* stream);
 
 /*
  * Whole-stream dual decode for 1..4 tokens: every projection of a .dualpack stream in

@@ -59,6 +59,7 @@ EXPORTS = {
                                    i64, i64, i64, vp]),
     "pp_quad_dequant": (i32, [vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
     "pp_quad_dequant_f16": (i32, [vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
+    "pp_quad_dequant_f16_t": (i32, [vp, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
     "pp_quad_mfma": (i32, [vp, i64, i64, vp, i64, vp, i32, vp, vp, vp, i64, vp, i64, i64, vp, i64, i64, i64, i64,
                            vp, i64, vp]),
     "pp_quad_mfma_workspace_size": (i64, [i64, i64, i64]),
@@ -90,6 +91,8 @@ EXPORTS = {
                               vp, vp, i64, i64, vp]),
     "pp_dual_dequant_f16": (i32, [vp, i32, i64, i64, vp, i64, i64, vp, i32, vp, vp, i32, i32, vp, vp, i64, i64,
                                   vp, vp, i64, i64, vp]),
+    "pp_dual_dequant_f16_t": (i32, [vp, i32, i64, vp, i64, vp, i32, vp, vp, i32, i32, vp, vp, i64, i64, vp, vp,
+                                    i64, i64, vp]),
 }
 
 _lock = threading.Lock()

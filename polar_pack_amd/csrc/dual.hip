@@ -17,6 +17,7 @@
 //                         quantize_polar_bitpacked returns, in blocks of up to 8 tokens.
 //   dual_dequant_kernel / dual_plug_scatter_kernel / dual_ws_gemm_kernel -- generic path
 //                         and parity export (any strides, both group-index modes).
+#include "dequant_t.h"
 #include "dual_kn.h"
 #include "dual_lds.h"
 
@@ -385,6 +386,7 @@ struct DualPlugScatterArgs {
   DualLuts luts;
   void* out[2];
   int64_t N, K;
+  int64_t o_k, o_n;   // output element of (k, n): k*o_k + n*o_n
 };
 
 template <typename O>
@@ -408,8 +410,55 @@ __global__ void dual_plug_scatter_kernel(const DualPlugScatterArgs A) {
   const float amp = (float)A.plug_amp[j];
   const float c = ph < A.luts.phase_n ? lut_at(A.luts.cs[0], A.luts.dtype, ph) : 0.f;
   const float s = ph < A.luts.phase_n ? lut_at(A.luts.cs[1], A.luts.dtype, ph) : 0.f;
-  reinterpret_cast<O*>(A.out[0])[k * A.N + n] = (O)(amp * c);
-  reinterpret_cast<O*>(A.out[1])[k * A.N + n] = (O)(amp * s);
+  reinterpret_cast<O*>(A.out[0])[k * A.o_k + n * A.o_n] = (O)(amp * c);
+  reinterpret_cast<O*>(A.out[1])[k * A.o_k + n * A.o_n] = (O)(amp * s);
+}
+
+// Transposed decode (dequant_t.h): int16 / big-endian codes (K,N), row stride c_sk (unit
+// column stride), the kernel group rule (k*N + n) / gs with gs a power of two >= 8 ->
+// out_m (N,K) row-major fp16.  8 codes of a row share one group scale.
+struct DualDequantTArgs {
+  const void* codes;
+  int layout;
+  int64_t c_sk;
+  const f16* scales;
+  int log2gs;
+  DualLuts luts;
+  f16* out[2];
+  int64_t N, K;
+};
+
+struct DualDecT {
+  const DualDqLds& T;
+  const DualDequantTArgs& A;
+  __device__ __forceinline__ void decode8(int64_t k, int64_t n, float (&v)[2][8]) const {
+    const u32x4 q = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(A.codes) + k * A.c_sk + n);
+    const float sc = (float)A.scales[(k * A.N + n) >> A.log2gs];
+    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t raw = (w4[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+      const uint32_t code = A.layout == PP_DUAL_U16_BE ? (((raw & 0xFFu) << 8) | (raw >> 8)) : (raw ^ 0x8000u);
+      const float amp = T.amp[(code >> 10) & 63u] * sc;
+      const float2 cs = T.cs[code & 1023u];
+      v[0][i] = amp * cs.x;
+      v[1][i] = amp * cs.y;
+    }
+  }
+};
+
+__global__ __launch_bounds__(DQT_NT) void dual_dequant_t_kernel(const DualDequantTArgs A) {
+  __shared__ DualDqLds T;
+  __shared__ __attribute__((aligned(16))) char tile[2 * DQT_T * 128];
+  const DualLuts& L = A.luts;
+  for (int i = threadIdx.x; i < 1024; i += blockDim.x) {
+    T.cs[i] = i < L.phase_n ? make_float2(lut_at(L.cs[0], L.dtype, i), lut_at(L.cs[1], L.dtype, i))
+                            : make_float2(0.f, 0.f);
+    if (i < 64) T.amp[i] = i < L.amp_n ? lut_at(L.amp, L.dtype, i) : 0.f;
+  }
+  __syncthreads();
+  f16* const out[2] = {A.out[0], A.out[1]};
+  dequant_t_tiles<2>(DualDecT{T, A}, tile, A.N, A.K, out);
 }
 
 struct DualWsGemmArgs {
@@ -612,6 +661,8 @@ static int dual_dequant_to(const void* codes, int code_layout, int64_t c_sk, int
     P.out[1] = out2;
     P.N = N;
     P.K = K;
+    P.o_k = N;
+    P.o_n = 1;
     hipLaunchKernelGGL(dual_plug_scatter_kernel<O>, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0, st, P);
     PP_LAUNCH_CHECK();
   }
@@ -636,6 +687,62 @@ extern "C" int pp_dual_dequant_f16(const void* codes, int code_layout, int64_t c
   return dual_dequant_to<f16>(codes, code_layout, c_sk, c_sn, bmax, group_size, chunk_size, amp_lut, amp_lut_n,
                               cos_lut, sin_lut, phase_n, lut_dtype, plug_idx, plug_amp, plug_n, elem_base, out1,
                               out2, N, K, stream);
+}
+
+extern "C" int pp_dual_dequant_f16_t(const void* codes, int code_layout, int64_t c_sk, const void* bmax,
+                                     int64_t group_size, const void* amp_lut, int amp_lut_n, const void* cos_lut,
+                                     const void* sin_lut, int phase_n, int lut_dtype, const uint32_t* plug_idx,
+                                     const void* plug_amp, int64_t plug_n, int64_t elem_base, void* out1,
+                                     void* out2, int64_t N, int64_t K, void* stream) {
+  if (int rc = dual_common_checks(codes, code_layout, group_size, 0, amp_lut, amp_lut_n, cos_lut, sin_lut, phase_n,
+                                  lut_dtype, plug_n, plug_idx, plug_amp, c_sk, 1, N, K))
+    return rc;
+  PP_REQUIRE(out1 && out2 && bmax, "out / bmax pointers are null");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (N * K == 0) return PP_OK;
+  PP_REQUIRE(N % 8 == 0 && K % 8 == 0 && c_sk >= N && c_sk % 8 == 0 && aligned(codes, 16),
+             "the transposed decode needs N % 8 == 0, K % 8 == 0 and 16-byte aligned code rows "
+             "(row stride >= N, a multiple of 8)");
+  PP_REQUIRE(group_size >= 8 && (group_size & (group_size - 1)) == 0,
+             "the transposed decode needs a power-of-two group_size >= 8");
+  PP_REQUIRE(aligned(out1, 16) && aligned(out2, 16), "outputs must be 16-byte aligned");
+  DualDequantTArgs A;
+  A.codes = codes;
+  A.layout = code_layout;
+  A.c_sk = c_sk;
+  A.scales = reinterpret_cast<const f16*>(bmax);
+  A.log2gs = 0;
+  while ((1ll << A.log2gs) < group_size) ++A.log2gs;
+  A.luts = make_dual_luts(amp_lut, amp_lut_n, cos_lut, sin_lut, phase_n, lut_dtype);
+  A.out[0] = reinterpret_cast<f16*>(out1);
+  A.out[1] = reinterpret_cast<f16*>(out2);
+  A.N = N;
+  A.K = K;
+  const int64_t tiles = ((N + DQT_T - 1) / DQT_T) * ((K + DQT_T - 1) / DQT_T);
+  const int64_t blocks = std::min<int64_t>(tiles, (int64_t)device_cu_count() * 4);
+  hipLaunchKernelGGL(dual_dequant_t_kernel, dim3((unsigned)blocks), dim3(DQT_NT), 0, st, A);
+  PP_LAUNCH_CHECK();
+  if (plug_n > 0) {
+    DualPlugScatterArgs P;
+    P.codes = codes;
+    P.layout = code_layout;
+    P.c_sk = c_sk;
+    P.c_sn = 1;
+    P.elem_base = elem_base;
+    P.plug_idx = plug_idx;
+    P.plug_amp = reinterpret_cast<const f16*>(plug_amp);
+    P.plug_n = plug_n;
+    P.luts = A.luts;
+    P.out[0] = out1;
+    P.out[1] = out2;
+    P.N = N;
+    P.K = K;
+    P.o_k = 1;
+    P.o_n = K;
+    hipLaunchKernelGGL(dual_plug_scatter_kernel<f16>, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0, st, P);
+    PP_LAUNCH_CHECK();
+  }
+  return PP_OK;
 }
 
 extern "C" int pp_dual_gemm(const void* a, int64_t a_sm, int64_t a_sk, const void* codes, int code_layout,

@@ -13,6 +13,7 @@
 //                        (also the parity export pp_quad_dequant), then
 //   quad_ws_gemm_kernel -- a plain GEMM on them (correct for any strides, not a
 //                        performance path).
+#include "dequant_t.h"
 #include "pp_common.h"
 #include "quad_kn.h"
 #include "quad_rows.h"
@@ -103,6 +104,7 @@ struct QuadPlugScatterArgs {
   float s[4];
   void* out[4];
   int64_t N, K;
+  int64_t o_k, o_n;   // output element of (k, n): k*o_k + n*o_n
 };
 
 // Entries are unique positions, so the scatter has no write conflicts.
@@ -121,9 +123,46 @@ __global__ void quad_plug_scatter_kernel(const QuadPlugScatterArgs A) {
     n = off - k * A.c_sk;
   }
   if (k >= A.K || n >= A.N) return;
-  const int64_t e = k * A.N + n;
+  const int64_t e = k * A.o_k + n * A.o_n;
 #pragma unroll
   for (int m = 0; m < 4; ++m) reinterpret_cast<O*>(A.out[m])[e] = (O)((float)A.plug_vals[4 * j + m] * A.s[m]);
+}
+
+// Transposed decode (dequant_t.h): codes (K,N), row stride c_sk (unit column stride) ->
+// out_m (N,K) row-major fp16, s_m applied.
+struct QuadDequantTArgs {
+  const uint32_t* codes;
+  int64_t c_sk;
+  QuadLuts luts;
+  float s[4];
+  f16* out[4];
+  int64_t N, K;
+};
+
+struct QuadDecT {
+  const QuadLds<1, 1>& T;
+  const QuadDequantTArgs& A;
+  __device__ __forceinline__ void decode8(int64_t k, int64_t n, float (&v)[4][8]) const {
+    const uint32_t* p = A.codes + k * A.c_sk + n;
+    const u32x4 q0 = *reinterpret_cast<const u32x4*>(p), q1 = *reinterpret_cast<const u32x4*>(p + 4);
+    const uint32_t cw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float w[4];
+      quad_decode(T, cw[i], 0, 0, w[0], w[1], w[2], w[3]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) v[m][i] = w[m] * A.s[m];
+    }
+  }
+};
+
+__global__ __launch_bounds__(DQT_NT) void quad_dequant_t_kernel(const QuadDequantTArgs A) {
+  __shared__ QuadLds<1, 1> T;
+  __shared__ __attribute__((aligned(16))) char tile[4 * DQT_T * 128];
+  quad_build_lds(T, A.luts);
+  __syncthreads();
+  f16* const out[4] = {A.out[0], A.out[1], A.out[2], A.out[3]};
+  dequant_t_tiles<4>(QuadDecT{T, A}, tile, A.N, A.K, out);
 }
 
 struct QuadWsGemmArgs {
@@ -235,6 +274,8 @@ static int quad_dequant_to(const uint32_t* codes, int64_t c_sk, int64_t c_sn, co
     }
     P.N = N;
     P.K = K;
+    P.o_k = N;
+    P.o_n = 1;
     hipLaunchKernelGGL(quad_plug_scatter_kernel<O>, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0, st, P);
     PP_LAUNCH_CHECK();
   }
@@ -255,6 +296,58 @@ extern "C" int pp_quad_dequant_f16(const uint32_t* codes, int64_t c_sk, int64_t 
                                    int64_t N, int64_t K, void* stream) {
   return quad_dequant_to<f16>(codes, c_sk, c_sn, luts, lut_dtype, scales, plug_idx, plug_vals, plug_n, elem_base,
                               out, N, K, stream);
+}
+
+extern "C" int pp_quad_dequant_f16_t(const uint32_t* codes, int64_t c_sk, const void* const* luts, int lut_dtype,
+                                     const float* scales, const uint32_t* plug_idx, const void* plug_vals,
+                                     int64_t plug_n, int64_t elem_base, void* const* out, int64_t N, int64_t K,
+                                     void* stream) {
+  if (int rc = check_luts(luts, lut_dtype)) return rc;
+  PP_REQUIRE(N >= 0 && K >= 0, "negative shape");
+  PP_REQUIRE(out != nullptr && out[0] && out[1] && out[2] && out[3], "out pointers are null");
+  PP_REQUIRE(scales != nullptr, "scales is null");
+  PP_REQUIRE(plug_n == 0 || (plug_idx && plug_vals), "plug arrays are null");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (N * K == 0) return PP_OK;
+  PP_REQUIRE(codes != nullptr, "codes is null");
+  PP_REQUIRE(N % 8 == 0 && K % 8 == 0 && c_sk >= N && c_sk % 4 == 0 && aligned(codes, 16),
+             "the transposed decode needs N % 8 == 0, K % 8 == 0 and 16-byte aligned code rows "
+             "(row stride >= N, a multiple of 4)");
+  for (int m = 0; m < 4; ++m) PP_REQUIRE(aligned(out[m], 16), "out[%d] must be 16-byte aligned", m);
+  QuadDequantTArgs A;
+  A.codes = codes;
+  A.c_sk = c_sk;
+  A.luts = make_luts(luts, lut_dtype);
+  for (int m = 0; m < 4; ++m) {
+    A.s[m] = scales[m];
+    A.out[m] = reinterpret_cast<f16*>(out[m]);
+  }
+  A.N = N;
+  A.K = K;
+  const int64_t tiles = ((N + DQT_T - 1) / DQT_T) * ((K + DQT_T - 1) / DQT_T);
+  const int64_t blocks = std::min<int64_t>(tiles, (int64_t)device_cu_count() * 4);
+  hipLaunchKernelGGL(quad_dequant_t_kernel, dim3((unsigned)blocks), dim3(DQT_NT), 0, st, A);
+  PP_LAUNCH_CHECK();
+  if (plug_n > 0) {
+    QuadPlugScatterArgs P;
+    P.plug_idx = plug_idx;
+    P.plug_vals = reinterpret_cast<const f16*>(plug_vals);
+    P.plug_n = plug_n;
+    P.elem_base = elem_base;
+    P.c_sk = c_sk;
+    P.c_sn = 1;
+    for (int m = 0; m < 4; ++m) {
+      P.s[m] = scales[m];
+      P.out[m] = out[m];
+    }
+    P.N = N;
+    P.K = K;
+    P.o_k = 1;
+    P.o_n = K;
+    hipLaunchKernelGGL(quad_plug_scatter_kernel<f16>, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0, st, P);
+    PP_LAUNCH_CHECK();
+  }
+  return PP_OK;
 }
 
 extern "C" int pp_quad_gemm(const void* a, int64_t a_sm, int64_t a_sk, const uint32_t* codes, int64_t c_sk,

@@ -143,18 +143,24 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
         del keep
         return out1, out2
     if M > (KN_MAX_M if kn else FUSED_MAX_M):
-        # decode along the storage: K-contiguous codes (container rows) into (N,K) weights,
-        # multiplied as their transpose; the kernel rule's groups need the (K,N) indices
+        # fp16 weights laid out (N,K), the GEMM's fastest right operand, then one batched GEMM
+        # over the two models: K-contiguous codes (container rows) decode along their storage
+        # into it (the kernel rule's groups need the (K,N) indices); (K,N) codes with unit
+        # column stride through the transposing decode; other strides into (K,N) weights
         nk = packed.stride(0) == 1 and packed.stride(1) != 1 and chunk_size > 0
-        view = packed.t() if nk else packed
-        w = torch.empty((2,) + tuple(view.shape), dtype=torch.float16, device=dev)
-        _dequant_into(view, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug, elem_base, layout,
-                      chunk_size, w[0], w[1])
-        if nk:
-            torch.matmul(a_fp16, w[0].t(), out=out1)
-            torch.matmul(a_fp16, w[1].t(), out=out2)
-            return out1, out2
-        out = torch.matmul(a_fp16, w)       # one batched GEMM over the two models: (2, M, N)
+        if kn:
+            w = torch.empty((2, N, K), dtype=torch.float16, device=dev)
+            _dequant_t_into(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug, elem_base,
+                            layout, w[0], w[1])
+        else:
+            view = packed.t() if nk else packed
+            w = torch.empty((2,) + tuple(view.shape), dtype=torch.float16, device=dev)
+            _dequant_into(view, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug, elem_base, layout,
+                          chunk_size, w[0], w[1])
+            if not nk:
+                out = torch.matmul(a_fp16, w)       # (2, M, N)
+                return out[0], out[1]
+        out = torch.matmul(a_fp16, w.transpose(1, 2))
         return out[0], out[1]
     ws_bytes = L.pp_dual_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), packed.data_ptr(),
                                              packed.stride(0), packed.stride(1), group_size, chunk_size,
@@ -251,6 +257,23 @@ def _dequant_into(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_siz
             chunk_size, amp_lut.data_ptr(), amp_lut.numel(), cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases,
             lut_dt, pi, pa, pn, int(elem_base), w1.data_ptr(), w2.data_ptr(), N, K, stream)
     nat.check(rc, "pp_dual_dequant")
+    del keep
+
+
+def _dequant_t_into(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug, elem_base, layout, w1, w2):
+    """Decode (K,N) codes with unit column stride (the kernel's group rule) into the
+    contiguous fp16 (N,K) tensors w1, w2: the weights transposed (pp_dual_dequant_f16_t)."""
+    K, N = packed.shape
+    dev = packed.device
+    lay = _codes_view(packed, layout)
+    lut_dt = _lut_dtype(amp_lut, cos_lut, sin_lut)
+    pi, pa, pn, keep = _dual_plug(plug, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = nat.lib().pp_dual_dequant_f16_t(packed.data_ptr(), lay, packed.stride(0), bmax.contiguous().data_ptr(),
+                                         group_size, amp_lut.data_ptr(), amp_lut.numel(), cos_lut.data_ptr(),
+                                         sin_lut.data_ptr(), num_phases, lut_dt, pi, pa, pn, int(elem_base),
+                                         w1.data_ptr(), w2.data_ptr(), N, K, stream)
+    nat.check(rc, "pp_dual_dequant_f16_t")
     del keep
 
 
