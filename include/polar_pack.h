@@ -278,8 +278,9 @@ int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const void* a, i
                 int64_t plug_pos0, int64_t plug_ld, int64_t slices, int64_t slice_cols,
                 void* const* out, int64_t o_sm, int64_t M, int64_t N, int64_t K,
                 void* workspace, int64_t workspace_bytes, void* stream);
-/* K slices for pp_quad_big at this shape on the current device. */
-int pp_quad_big_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* slice_cols);
+/* K slices for pp_quad_big at this shape and code layout on the current device (any plan
+ * that covers K is valid; this one balances the launch). */
+int pp_quad_big_plan(int64_t M, int64_t N, int64_t K, int layout, int64_t* slices, int64_t* slice_cols);
 int64_t pp_quad_big_workspace_size(int64_t M, int64_t N, int64_t slices);
 
 

@@ -66,7 +66,7 @@ EXPORTS = {
     "pp_quad_mfma_waves": (i64, [i64]),
     "pp_quad_big": (i32, [vp, i32, i64, vp, i64, vp, i32, vp, vp, vp, i64, vp, i64, i64, i64, i64, vp, i64, i64, i64,
                           i64, vp, i64, vp]),
-    "pp_quad_big_plan": (i32, [i64, i64, i64, vp, vp]),
+    "pp_quad_big_plan": (i32, [i64, i64, i64, i32, vp, vp]),
     "pp_quad_big_workspace_size": (i64, [i64, i64, i64]),
     "pp_dual_mfma": (i32, [vp, i64, vp, i64, vp, i64, vp, i32, vp, vp, i32, i32, vp, vp, i64, vp, i64, i64, i64,
                            i64, vp, vp, i64, i64, i64, i64, vp, i64, vp]),

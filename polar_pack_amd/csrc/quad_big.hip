@@ -33,14 +33,17 @@ namespace pp {
 constexpr int QB_ROWS = 16;     // weight rows per item
 
 // TT 16-token tiles per item (1, 2, 4 or 8: up to 16, 32, 64 or 128 tokens).  With 8 tiles
-// a wavefront takes a SIMD's register file (4 waves per workgroup, one per SIMD); with up
-// to 4 it fits in half of it (8 waves, two per SIMD, each hiding the other's waits).
-// One workgroup per CU: the decode tables fill the LDS.
+// a wavefront takes a SIMD's register file (4 waves per workgroup, one per SIMD).  With up
+// to 4 it fits in half of it: on (N,K) rows two waves share a SIMD (8 per workgroup); on
+// (K,N) storage one wave per SIMD with twice the items measured faster (4096 x 4096 at 16 /
+// 32 / 64 tokens: 27 / 32 / 44 against 31 / 39 / 51 us; the second wave of a SIMD ran its
+// items 1.29x slower than the first, and the (K,N) step's 8 four-byte code loads per lane
+// leave less to overlap).  One workgroup per CU: the decode tables fill the LDS.
 // G: steps per loop pass = code buffers, the codes of a step loaded G - 1 steps before it
 // (2 KiB per wave and step: with few token tiles the decode is short and a wave needs
 // several steps of codes in flight to cover the HBM latency; with 8 the registers allow 2).
-template <int TT> struct QbCfg {
-  static constexpr int WPE = TT == 8 ? 1 : 2;    // waves per SIMD
+template <int TT, bool KN> struct QbCfg {
+  static constexpr int WPE = TT == 8 || KN ? 1 : 2;    // waves per SIMD
   static constexpr int NT = 256 * WPE;
   static constexpr int WAVES = NT / 64;
   static constexpr int G = TT <= 2 ? 4 : 2;
@@ -167,7 +170,7 @@ struct QbRun {
   __device__ __forceinline__ void step(const QbCodes& cur, QbCodes& nxt, QbX<TT>& xnow, const QbX<TT>& xprev,
                                        const h8 (&aprev)[4], h8 (&anew)[4], int k0) {
     qb_x(A, k0, ke, vox, xblk, j0, xnow);
-    qb_codes<KN>(A, ctile, n0, k0 + 32 * (QbCfg<TT>::G - 1), ke, voc, nxt);
+    qb_codes<KN>(A, ctile, n0, k0 + 32 * (QbCfg<TT, KN>::G - 1), ke, voc, nxt);
     Look8 lk;
     look8<L>(lds, lo, cur.c[0], cur.c[1], lk);
     __builtin_amdgcn_sched_barrier(0);
@@ -186,7 +189,7 @@ struct QbRun {
 
 template <int TT, bool KN, bool PLUG, class L>
 __device__ __forceinline__ void qb_body(const char* lds, const QuadBigArgs& A) {
-  constexpr int WAVES = QbCfg<TT>::WAVES;
+  constexpr int WAVES = QbCfg<TT, KN>::WAVES;
   const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
   const LaneOff lo = L::lane(lane);
   int b = blockIdx.x;
@@ -223,7 +226,7 @@ __device__ __forceinline__ void qb_body(const char* lds, const QuadBigArgs& A) {
       R.P.end = ok ? A.row_plug[(int64_t)n * A.slices + sl + 1] : 0;
       mplug_issue(A.plug, R.P, pidx);
     }
-    constexpr int G = QbCfg<TT>::G;
+    constexpr int G = QbCfg<TT, KN>::G;
     QbCodes C[G];
     QbX<TT> X0, X1;
 #pragma unroll
@@ -281,11 +284,12 @@ __device__ __forceinline__ void qb_body(const char* lds, const QuadBigArgs& A) {
 }
 
 template <int TT, bool KN>
-__global__ __launch_bounds__(QbCfg<TT>::NT)
-__attribute__((amdgpu_waves_per_eu(QbCfg<TT>::WPE, QbCfg<TT>::WPE))) void quad_big_kernel(const QuadBigArgs A) {
+__global__ __launch_bounds__((QbCfg<TT, KN>::NT))
+__attribute__((amdgpu_waves_per_eu(QbCfg<TT, KN>::WPE, QbCfg<TT, KN>::WPE))) void quad_big_kernel(
+    const QuadBigArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t Tb[QLDS_BYTES / 4];
   const char* lds = reinterpret_cast<const char*>(Tb);
-  const bool shared = quad_tables<QbCfg<TT>::NT>(Tb, A.luts);
+  const bool shared = quad_tables<QbCfg<TT, KN>::NT>(Tb, A.luts);
   if (A.plug.n > 0) {
     if (shared) qb_body<TT, KN, true, LayShared>(lds, A);
     else qb_body<TT, KN, true, LaySplit>(lds, A);
@@ -297,8 +301,8 @@ __attribute__((amdgpu_waves_per_eu(QbCfg<TT>::WPE, QbCfg<TT>::WPE))) void quad_b
 
 template <int TT>
 static void qb_launch(bool kn, int64_t grid, hipStream_t st, const QuadBigArgs& A) {
-  if (kn) hipLaunchKernelGGL((quad_big_kernel<TT, true>), dim3((unsigned)grid), dim3(QbCfg<TT>::NT), 0, st, A);
-  else hipLaunchKernelGGL((quad_big_kernel<TT, false>), dim3((unsigned)grid), dim3(QbCfg<TT>::NT), 0, st, A);
+  if (kn) hipLaunchKernelGGL((quad_big_kernel<TT, true>), dim3((unsigned)grid), dim3(QbCfg<TT, true>::NT), 0, st, A);
+  else hipLaunchKernelGGL((quad_big_kernel<TT, false>), dim3((unsigned)grid), dim3(QbCfg<TT, false>::NT), 0, st, A);
 }
 
 // Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero.  Runs after the
@@ -336,31 +340,48 @@ __global__ __launch_bounds__(256) void quad_big_finish_kernel(float* acc, f16* o
 
 // K slices for an (N, K) product at M tokens: as many whole 32-column slices as keep the
 // items within one per wavefront.
-static int64_t qb_waves(int tt) {
-  return tt == 1 ? QbCfg<1>::WAVES : tt == 2 ? QbCfg<2>::WAVES : tt == 4 ? QbCfg<4>::WAVES : QbCfg<8>::WAVES;
+template <int TT>
+static int64_t qb_waves_of(bool kn) { return kn ? QbCfg<TT, true>::WAVES : QbCfg<TT, false>::WAVES; }
+static int64_t qb_waves(int tt, bool kn) {
+  return tt == 1 ? qb_waves_of<1>(kn) : tt == 2 ? qb_waves_of<2>(kn) : tt == 4 ? qb_waves_of<4>(kn) : qb_waves_of<8>(kn);
 }
 
-static void qb_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* cols) {
+static void qb_plan(int64_t M, int64_t N, int64_t K, bool kn, int64_t* slices, int64_t* cols) {
   const int tt = qb_tt(M);
-  const int64_t waves = (int64_t)device_cu_count() * qb_waves(tt);
-  const int64_t units = ((N + QB_ROWS - 1) / QB_ROWS) * ((M + 16 * tt - 1) / (16 * tt));
-  int64_t s = std::max<int64_t>(1, std::min<int64_t>(K / 32, waves / std::max<int64_t>(1, units)));
-  const int64_t per = (K + s - 1) / s;
-  const int64_t grp = 32 * (tt == 1 ? QbCfg<1>::G : tt == 2 ? QbCfg<2>::G : tt == 4 ? QbCfg<4>::G : QbCfg<8>::G);
-  int64_t c = (per + grp - 1) / grp * grp;   // whole groups of steps
-  if ((K + c - 1) / c != s) c = (per + 31) / 32 * 32;
-  *cols = c;
-  *slices = (K + c - 1) / c;
+  const int64_t cus = device_cu_count(), wv = qb_waves(tt, kn);
+  const int64_t g = tt == 1 ? QbCfg<1, false>::G : tt == 2 ? QbCfg<2, false>::G : tt == 4 ? QbCfg<4, false>::G
+                                                                                    : QbCfg<8, false>::G;
+  const int64_t steps = K / 32;
+  // groups of wv row tiles (one per workgroup and round) for s slices; a launch takes
+  // ceil(groups / CUs) rounds of items of ceil(steps / s) steps (whole loop passes of g),
+  // each with about 4 steps of fixed cost (its first loads, its epilogue); the slice
+  // count with the fewest step-times wins, fewer slices on ties
+  const int64_t tgroups = ((N + QB_ROWS - 1) / QB_ROWS + wv - 1) / wv * ((M + 16 * tt - 1) / (16 * tt));
+  int64_t best = 1, best_cost = -1;
+  for (int64_t s = 1; s <= std::min<int64_t>(steps, 64); ++s) {
+    const int64_t per = (steps + s - 1) / s;
+    if ((steps + per - 1) / per != s) continue;        // s slices of `per` steps do not exist
+    const int64_t rounds = (tgroups * s + cus - 1) / cus;
+    const int64_t cost = rounds * ((per + g - 1) / g * g + 4);
+    if (best_cost < 0 || cost < best_cost) {
+      best = s;
+      best_cost = cost;
+    }
+  }
+  const int64_t per = (steps + best - 1) / best;
+  *cols = 32 * per;
+  *slices = (K + *cols - 1) / *cols;
 }
 
 }  // namespace pp
 
 using namespace pp;
 
-extern "C" int pp_quad_big_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* slice_cols) {
+extern "C" int pp_quad_big_plan(int64_t M, int64_t N, int64_t K, int layout, int64_t* slices, int64_t* slice_cols) {
   PP_REQUIRE(slices != nullptr && slice_cols != nullptr, "null pointer argument");
   PP_REQUIRE(M >= 1 && N >= 1 && K >= 32, "needs M, N >= 1 and K >= 32");
-  qb_plan(M, N, K, slices, slice_cols);
+  PP_REQUIRE(layout == PP_QUAD_NK || layout == PP_QUAD_KN, "layout must be PP_QUAD_NK or PP_QUAD_KN");
+  qb_plan(M, N, K, layout == PP_QUAD_KN, slices, slice_cols);
   return PP_OK;
 }
 
@@ -428,7 +449,7 @@ extern "C" int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const
   A.ppos0 = plug_pos0;
   A.pld = plug_ld;
   A.acc = reinterpret_cast<float*>(workspace);
-  const int64_t wv = qb_waves(tt);
+  const int64_t wv = qb_waves(tt, kn);
   const int64_t groups = (int64_t)(A.tiles + wv - 1) / wv * A.tblocks * slices;
   const int64_t cus = device_cu_count();
   int64_t grid = std::min<int64_t>(cus, groups);

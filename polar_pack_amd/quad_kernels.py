@@ -271,7 +271,7 @@ def _quad_big(a, codes, layout, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, ou
     if a.stride(1) != 1 or a.data_ptr() % 16 or (M > 1 and a.stride(0) % 8):
         a = a.contiguous()
     plan = (ctypes.c_int64 * 2)()
-    nat.check(L.pp_quad_big_plan(M, N, K, ctypes.byref(plan, 0), ctypes.byref(plan, 8)), "pp_quad_big_plan")
+    nat.check(L.pp_quad_big_plan(M, N, K, layout, ctypes.byref(plan, 0), ctypes.byref(plan, 8)), "pp_quad_big_plan")
     slices, cols = int(plan[0]), int(plan[1])
     if layout == nat.PP_QUAD_NK:
         ldc = codes.stride(1)

@@ -164,9 +164,10 @@ def test_plan_covers_k():
     for M, N, K in ((65, 4096, 4096), (1024, 4096, 4096), (128, 11008, 2048), (300, 2048, 11008), (100, 7, 64),
                     (9, 4096, 4096), (16, 11008, 2048), (32, 2048, 11008), (64, 300, 96)):
         plan = (ctypes.c_int64 * 2)()
-        nat.check(L.pp_quad_big_plan(M, N, K, ctypes.byref(plan, 0), ctypes.byref(plan, 8)), "plan")
-        s, c = int(plan[0]), int(plan[1])
-        assert c % 32 == 0 and s * c >= K and (s - 1) * c < K
+        for layout in (nat.PP_QUAD_NK, nat.PP_QUAD_KN):
+            nat.check(L.pp_quad_big_plan(M, N, K, layout, ctypes.byref(plan, 0), ctypes.byref(plan, 8)), "plan")
+            s, c = int(plan[0]), int(plan[1])
+            assert c % 32 == 0 and s * c >= K and (s - 1) * c < K
 
 
 def test_full_size_kn_layer_column_sample():
