@@ -444,6 +444,11 @@ int pp_dual_dequant_f16_t(const void* codes, int code_layout, int64_t c_sk, cons
  * per task, accumulators at acc_off + (m*M + j)*N + row for model m = 0, 1), which must
  * be zero before the first launch and is left zero by each; launches that share it must
  * not overlap.  A null workspace skips split segments.
+ * scale_tab (optional, n_tab fp16 entries from pp_dual_scale_table for the same
+ * projections): with M = 1 and chunk_size % group_size == 0 the row kernel reads each
+ * decode step's group scales from it (one 16-byte load for the 8 rows of a task) instead
+ * of from scales; it requires every projection to have K % group_size == 0, N % 8 == 0
+ * and pos0 % (8 * group_size) == 0.  Null: scales only.
  * Replaces the per-projection polar_dual_bitpacked calls of a decode step
  * (polar_kernels.py:98-115) and the decode of unpack_dual_models
  * (polar_bitpack.py:194-260).
@@ -469,10 +474,27 @@ int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs,
                    void* workspace, const int64_t* task_plug, int64_t n_tasks, int plug_windows,
                    const pp_quad_item* tail_items, int64_t n_tail,
                    int code_layout, const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
+                   const void* scale_tab, int64_t n_tab,
                    const float* amp_lut, const float* cos_lut, const float* sin_lut,
                    const uint32_t* plug_idx, const void* plug_amp, const uint32_t* plug_ent, int64_t plug_n,
                    int64_t n_codes, const void* const* tails, const int64_t* tail_len,
                    int64_t M, void* stream);
+
+/*
+ * Group scales of a dual stream regrouped for pp_dual_stream's scale_tab (built once per
+ * stream plan, on the stream's device): projection i covers stream positions
+ * proj_pos0[i] .. proj_pos0[i] + proj_n[i] * proj_k[i] - 1 (rows of proj_k[i] columns;
+ * proj_pos0 ascending, n_projs entries).  For the rows 8b .. 8b+7 of projection i, which
+ * start at position P = proj_pos0[i] + 8 b proj_k[i],
+ *   tab[P / group_size + 8 j + q] = scales[(P + q proj_k[i]) / group_size + j]
+ * (row 8b + q, column group j); entries outside every projection are copied from scales
+ * (0 at or past n_groups).  n_tab >= the end of the last projection / group_size.
+ * Requirements as for scale_tab above.  No counterpart in the reference: a reordering of
+ * its scale array (polar_bitpack.py:205-211) for the decode's loads.
+ */
+int pp_dual_scale_table(const void* scales, int64_t n_groups, int64_t group_size, const int64_t* proj_pos0,
+                        const int32_t* proj_n, const int32_t* proj_k, int64_t n_projs, void* tab, int64_t n_tab,
+                        void* stream);
 
 /*
  * Plug records of a dual stream (built once per stream plan, on the stream's device):

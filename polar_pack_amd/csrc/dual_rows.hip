@@ -11,10 +11,14 @@
 //
 // Same structure as quad_rows.hip: one workgroup per CU, wavefronts walk segments (runs of
 // full rows of one projection) in tasks of RG rows and chunks of 512 pairs, the next chunk
-// in flight while one is decoded, reduction / stores of a task done in the first step of
-// the next.  Plug corrections go through a three-stage window pipeline (below).  Per lane and row a chunk is one 16-byte load (8 pairs that
-// share one group scale, so the scale multiplies a per-lane partial sum once per 8 pairs)
-// and one 2-byte scale load.
+// (at one token the next two) in flight while one is decoded, reduction / stores of a task
+// done in the first step of the next.  Plug corrections go through a three-stage window
+// pipeline (below).  Per lane and row a chunk is one 16-byte load (8 pairs that share one
+// group scale, so the scale multiplies a per-lane partial sum once per 8 pairs) and one
+// 2-byte scale load; at one token with the scale table (SM = 2, pp_dual_scale_table) one
+// 16-byte load brings the scales of all 8 rows of the task (measured on the 3B-shaped
+// stream: 1.12 -> 1.03 ms per step, the per-row scale loads and their group arithmetic
+// having cost more than the decode's table lookups).
 //
 // LDS tables (129 KiB, dual_lds.h): (cos, sin) of the 1024 phases in 128-byte rows of 16
 // replicas, the 64 amplitudes one per bank.
@@ -45,6 +49,8 @@ struct DualStreamArgs {
   const float* sin_lut;   // [1024]
   const f16* scales;
   int64_t n_groups;
+  const f16* scale_tab;       // SM = 2: the group scales regrouped per task (pp_dual_scale_table)
+  int64_t n_tab;
   int64_t gs, chunk, per_chunk;
   int log2gs;
   const uint32_t* plug_idx;
@@ -98,11 +104,11 @@ struct DualSeg {
   uint32_t* cnt;       // parts > 1: the counters of the segment's tasks
 };
 
-// Group (scale index) of stream position p.  SM = 0: chunk is a multiple of gs, so
+// Group (scale index) of stream position p.  SM = 0 and 2: chunk is a multiple of gs, so
 // groups never restart mid-group and group = p / gs; SM = 1: the general rule.
 template <int SM>
 __device__ __forceinline__ uint32_t dual_group(const DualStreamArgs& A, int64_t p) {
-  if constexpr (SM == 0) {
+  if constexpr (SM != 1) {
     return (uint32_t)(p >> A.log2gs);
   } else {
     const uint32_t pp = (uint32_t)p, ch = (uint32_t)A.chunk;
@@ -114,9 +120,21 @@ __device__ __forceinline__ uint32_t dual_group(const DualStreamArgs& A, int64_t 
 template <int MT, int RG>
 struct DChunk {
   u32x4 q[RG];          // 8 pairs per lane per row
-  uint32_t sc[RG];      // their group scale (fp16 bits)
+  uint32_t sc[RG];      // their group scale (fp16 bits); SM = 2: in sq
+  u32x4 sq;             // SM = 2 (RG = 8): the 8 rows' scales of the lane's group, one fp16 each
   u32x4 xr[MT];         // 8 fp16 activations per lane
 };
+
+// Scale of row r of a chunk (fp16 bits in the low half).
+template <int RG, int SM, int MT>
+__device__ __forceinline__ uint32_t dchunk_scale(const DChunk<MT, RG>& c, int r) {
+  if constexpr (SM == 2) {
+    const uint32_t w = r < 2 ? c.sq.x : r < 4 ? c.sq.y : r < 6 ? c.sq.z : c.sq.w;
+    return (r & 1) ? w >> 16 : w;
+  } else {
+    return c.sc[r];
+  }
+}
 
 template <int MT, int RG, int SM>
 __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const DualSeg& S, int row, int kc,
@@ -129,19 +147,28 @@ __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const Dual
   for (int r = 0; r < RG; ++r) vload128(c.q[r], voff[r], rc);
   const int k = kc + 8 * lane;
   const int64_t base = S.pos0 + first;   // stream position of (row, kc): uniform
+  if constexpr (SM == 2) {
+    // the task's 8 rows start at a multiple of 8 gs positions: their scales of group j
+    // (columns j gs .. j gs + gs - 1 of each row) are the 16 bytes at 8 * (task start / gs + 8 j)
+    static_assert(RG == 8, "the scale table holds 8 rows per cell");
+    const int64_t t0 = (S.pos0 + (int64_t)row * S.ldc) >> A.log2gs;
+    const rsrc_t rt = make_rsrc(A.scale_tab + t0, 2u * (uint32_t)(A.n_tab - t0));
+    vload128(c.sq, 16u * ((uint32_t)k >> A.log2gs), rt);
+  } else {
 #pragma unroll
-  for (int r = 0; r < RG; ++r) {
-    const bool in = (row + r) < S.nrows && k < S.kend;
-    const int64_t br = base + (int64_t)r * S.ldc;
-    uint32_t g;
-    if constexpr (SM == 0) {
-      // group = (br + 8 lane) / gs, split into a uniform part and a small per-lane one
-      const uint32_t U = (uint32_t)(br >> A.log2gs), R = (uint32_t)br & (uint32_t)(A.gs - 1);
-      g = U + ((R + 8u * lane) >> A.log2gs);
-    } else {
-      g = dual_group<1>(A, br + 8 * lane);
+    for (int r = 0; r < RG; ++r) {
+      const bool in = (row + r) < S.nrows && k < S.kend;
+      const int64_t br = base + (int64_t)r * S.ldc;
+      uint32_t g;
+      if constexpr (SM == 0) {
+        // group = (br + 8 lane) / gs, split into a uniform part and a small per-lane one
+        const uint32_t U = (uint32_t)(br >> A.log2gs), R = (uint32_t)br & (uint32_t)(A.gs - 1);
+        g = U + ((R + 8u * lane) >> A.log2gs);
+      } else {
+        g = dual_group<1>(A, br + 8 * lane);
+      }
+      vload16(c.sc[r], in ? 2u * g : OOB, rs);
     }
-    vload16(c.sc[r], in ? 2u * g : OOB, rs);
   }
   if constexpr (MT == 1) {
     // columns past the slice read x = 0, so the codes loaded there add nothing
@@ -153,7 +180,7 @@ __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const Dual
   }
 }
 
-template <int MT, int RG, int LAYOUT>
+template <int MT, int RG, int LAYOUT, int SM>
 __device__ __forceinline__ void dchunk_compute(const char* lds, const DualLane& lo, const DChunk<MT, RG>& c,
                                                float (&acc)[RG][2][MT]) {
   float xv[MT][8];
@@ -190,7 +217,7 @@ __device__ __forceinline__ void dchunk_compute(const char* lds, const DualLane& 
         l1[j] = fmaf(xa, cs[e].x, l1[j]);
         l2[j] = fmaf(xa, cs[e].y, l2[j]);
       }
-    const float sc = h2f(c.sc[r]);
+    const float sc = h2f(dchunk_scale<RG, SM>(c, r));
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
       acc[r][0][j] = fmaf(sc, l1[j], acc[r][0][j]);
@@ -276,12 +303,15 @@ __device__ __forceinline__ void dwin_apply(const char* lds, const DualLane& lo, 
     float2 cs;
     dual_lookup1(lds, dual_half<LAYOUT>(W.aux[w]), lo, an, cs);
     const float d = h2f(W.pa[w]) - an * h2f(W.aux[w] >> 16);
+    float dx[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) dx[j] = d * h2f(W.xk[w][j]);
 #pragma unroll
     for (int q = 0; q < RG; ++q) {
-      const float on = q == W.q[w] ? d : 0.f;
+      const bool on = q == W.q[w];
 #pragma unroll
       for (int j = 0; j < MT; ++j) {
-        const float t = on * h2f(W.xk[w][j]);
+        const float t = on ? dx[j] : 0.f;
         acc[q][0][j] = fmaf(t, cs.x, acc[q][0][j]);
         acc[q][1][j] = fmaf(t, cs.y, acc[q][1][j]);
       }
@@ -465,7 +495,7 @@ struct DualRunner {
     dwin_data<MT, RG, PW, SM>(A, S, s1, I, lane, D);
     dwin_positions<PW>(A, s2, lane, I);
     if (cur.ck == 0 && pend_ti >= 0) finish_pending();
-    dchunk_compute<MT, RG, LAYOUT>(lds, lo, comp, acc);
+    dchunk_compute<MT, RG, LAYOUT, SM>(lds, lo, comp, acc);
     if (cur.ck == nck - 1) {
 #pragma unroll
       for (int r = 0; r < RG; ++r)
@@ -501,12 +531,25 @@ struct DualRunner {
     advance_slot(c3);
     load_range(c3, T);
     // c3 now names step 2; step() turns T into s2 and moves c3 to step 3
-    DChunk<MT, RG> c0, c1;
     Cursor cur = {0, 0};
-    prefetch(c0);
-    for (;;) {
-      if (!step(cur, c0, c1)) break;
-      if (!step(cur, c1, c0)) break;
+    if constexpr (MT == 1) {
+      // one token: two chunks in flight while one is decoded (measured 1-2 % faster on
+      // the 3B stream than one; the registers of more tokens leave room for one)
+      DChunk<MT, RG> c0, c1, c2;
+      prefetch(c0);
+      prefetch(c1);
+      for (;;) {
+        if (!step(cur, c0, c2)) break;
+        if (!step(cur, c1, c0)) break;
+        if (!step(cur, c2, c1)) break;
+      }
+    } else {
+      DChunk<MT, RG> c0, c1;
+      prefetch(c0);
+      for (;;) {
+        if (!step(cur, c0, c1)) break;
+        if (!step(cur, c1, c0)) break;
+      }
     }
     finish_pending();
   }
@@ -779,6 +822,38 @@ __global__ __launch_bounds__(256) void dual_plug_table_kernel(const uint16_t* co
   ent[3 * j + 2] = (uint32_t)__builtin_bit_cast(unsigned short, plug_amp[j]);
 }
 
+// The group scales regrouped for the one-token stream decode: for every projection i
+// (stream positions proj_pos0[i] .. + N_i K_i, rows of K_i columns, K_i % gs == 0,
+// proj_pos0[i] % (8 gs) == 0, N_i % 8 == 0) and every run of 8 rows starting at row 8b,
+// position P = proj_pos0[i] + 8 b K_i: tab[P/gs + 8 j + q] = scales[(P + q K_i)/gs + j], the
+// scale of row 8b + q, column group j.  A decode step then loads the 8 rows' scales of its
+// group in one 16-byte load.  Entries outside every projection copy scales (0 past n_groups).
+__global__ __launch_bounds__(256) void dual_scale_table_kernel(const f16* scales, int64_t n_groups, int log2gs,
+                                                               const int64_t* proj_pos0, const int32_t* proj_n,
+                                                               const int32_t* proj_k, int n_projs, f16* tab,
+                                                               int64_t n_tab) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_tab) return;
+  int64_t src = t;
+  const int64_t p = t << log2gs;   // stream position of group t
+  if (p >= proj_pos0[0]) {
+    int lo = 0, hi = n_projs - 1;   // last projection starting at or before p
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (proj_pos0[mid] <= p) lo = mid;
+      else hi = mid - 1;
+    }
+    const int64_t K = proj_k[lo], gk = K >> log2gs;   // column groups per row
+    const int64_t local = t - (proj_pos0[lo] >> log2gs);
+    if (local < (int64_t)proj_n[lo] * gk) {
+      const int64_t blk = local / (8 * gk), r = local - blk * 8 * gk;
+      const int64_t j = r >> 3, q = r & 7;
+      src = (proj_pos0[lo] >> log2gs) + (blk * 8 + q) * gk + j;
+    }
+  }
+  tab[t] = src < n_groups ? scales[src] : (f16)0.f;
+}
+
 // ------------------------------------------------------------------ host side
 static int dual_stream_mt(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : 4; }
 static int dual_stream_rg(int mt) { return mt == 1 ? DualCfg<1>::RG : mt == 2 ? DualCfg<2>::RG : DualCfg<4>::RG; }
@@ -851,6 +926,22 @@ extern "C" int pp_dual_plug_table(const void* codes, int64_t n_codes, const void
   return PP_OK;
 }
 
+extern "C" int pp_dual_scale_table(const void* scales, int64_t n_groups, int64_t group_size,
+                                   const int64_t* proj_pos0, const int32_t* proj_n, const int32_t* proj_k,
+                                   int64_t n_projs, void* tab, int64_t n_tab, void* stream) {
+  PP_REQUIRE(scales && proj_pos0 && proj_n && proj_k && tab, "null pointer");
+  PP_REQUIRE(n_groups >= 1 && n_tab >= 1 && n_tab < (1ll << 40), "bad n_groups / n_tab");
+  PP_REQUIRE(group_size >= 8 && (group_size & (group_size - 1)) == 0, "group_size must be a power of two >= 8");
+  PP_REQUIRE(n_projs >= 1 && n_projs < (1ll << 30), "bad n_projs");
+  int log2gs = 0;
+  while ((1ll << log2gs) < group_size) ++log2gs;
+  hipLaunchKernelGGL(dual_scale_table_kernel, dim3((unsigned)((n_tab + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const f16*>(scales), n_groups, log2gs,
+                     proj_pos0, proj_n, proj_k, (int)n_projs, reinterpret_cast<f16*>(tab), n_tab);
+  PP_LAUNCH_CHECK();
+  return PP_OK;
+}
+
 extern "C" int pp_dual_stream_chunk(int64_t M) { return M < 1 || M > 4 ? 0 : DPAIRS; }
 
 extern "C" int64_t pp_dual_stream_waves(int64_t M) {
@@ -863,7 +954,8 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
                               int64_t n_tasks,
                               int plug_windows, const pp_quad_item* tail_items,
                               int64_t n_tail, int code_layout, const void* scales, int64_t n_groups,
-                              int64_t group_size, int64_t chunk_size, const float* amp_lut, const float* cos_lut,
+                              int64_t group_size, int64_t chunk_size, const void* scale_tab, int64_t n_tab,
+                              const float* amp_lut, const float* cos_lut,
                               const float* sin_lut, const uint32_t* plug_idx, const void* plug_amp,
                               const uint32_t* plug_ent, int64_t plug_n,
                               int64_t n_codes, const void* const* tails, const int64_t* tail_len, int64_t M,
@@ -881,6 +973,7 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
   PP_REQUIRE(group_size >= 8 && (group_size & (group_size - 1)) == 0,
              "the stream decode needs a power-of-two group_size >= 8");
   PP_REQUIRE(chunk_size >= 8 && chunk_size % 8 == 0, "the stream decode needs chunk_size % 8 == 0");
+  PP_REQUIRE(scale_tab == nullptr || (n_tab >= 1 && 2 * n_tab < (1ll << 31)), "bad scale_tab / n_tab");
   PP_REQUIRE(plug_n >= 0 && (plug_n == 0 || (plug_idx != nullptr && plug_amp != nullptr)), "plug arrays are null");
   PP_REQUIRE(plug_n == 0 || n_segs == 0 || plug_ent != nullptr, "plug_ent is null (build it with pp_dual_plug_table)");
   PP_REQUIRE(M >= 1 && M <= 4, "the dual stream decode takes 1..4 tokens, got %lld", (long long)M);
@@ -900,6 +993,8 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
   A.sin_lut = sin_lut;
   A.scales = reinterpret_cast<const f16*>(scales);
   A.n_groups = n_groups;
+  A.scale_tab = reinterpret_cast<const f16*>(scale_tab);
+  A.n_tab = n_tab;
   A.gs = group_size;
   A.chunk = chunk_size;
   A.per_chunk = (chunk_size + group_size - 1) / group_size;
@@ -931,10 +1026,16 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
   if (n_segs > 0) {
     int rc;
     const int pw = plug_windows;
-    if (be) rc = sm == 0 ? dispatch_dual_stream<PP_DUAL_U16_BE, 0>(A, mt, pw, st)
-                         : dispatch_dual_stream<PP_DUAL_U16_BE, 1>(A, mt, pw, st);
-    else rc = sm == 0 ? dispatch_dual_stream<PP_DUAL_I16_OFFSET, 0>(A, mt, pw, st)
-                      : dispatch_dual_stream<PP_DUAL_I16_OFFSET, 1>(A, mt, pw, st);
+    if (sm == 0 && mt == 1 && scale_tab != nullptr) {
+      rc = be ? launch_dual_stream<1, PP_DUAL_U16_BE, 2>(A, pw, st)
+              : launch_dual_stream<1, PP_DUAL_I16_OFFSET, 2>(A, pw, st);
+    } else if (be) {
+      rc = sm == 0 ? dispatch_dual_stream<PP_DUAL_U16_BE, 0>(A, mt, pw, st)
+                   : dispatch_dual_stream<PP_DUAL_U16_BE, 1>(A, mt, pw, st);
+    } else {
+      rc = sm == 0 ? dispatch_dual_stream<PP_DUAL_I16_OFFSET, 0>(A, mt, pw, st)
+                   : dispatch_dual_stream<PP_DUAL_I16_OFFSET, 1>(A, mt, pw, st);
+    }
     if (rc) return rc;
   }
   if (n_tail > 0) {

@@ -465,10 +465,14 @@ class DualStream:
     8 pairs (a lane reads 8 pairs that share one group scale).  ``split`` as for
     :class:`QuadStream` (column slices for launches with few row tasks, summed in a
     workspace owned by this object: two launches of one DualStream must not overlap).
+    ``scale_table`` (default: where it applies) gives the one-token decode the group scales
+    regrouped per 8-row task (``pp_dual_scale_table``: one load per step for all 8 rows);
+    it applies when M = 1, chunk_size % group_size == 0 and every projection has
+    K % group_size == 0, N % 8 == 0 and a position that is a multiple of 8 * group_size.
     """
 
     def __init__(self, pack, shapes: Sequence[Tuple[int, int]], M: int = 1, plug_windows=None, split: bool = True,
-                 positions=None, wave_weights="slots", task_cost=0):
+                 positions=None, wave_weights="slots", task_cost=0, scale_table=None):
         L = nat.lib()
         self.pack = pack
         self.shapes = [(int(n), int(k)) for n, k in shapes]
@@ -540,6 +544,26 @@ class DualStream:
                                       self.rows_per_item, self.plug_ent.data_ptr(),
                                       torch.cuda.current_stream(dev).cuda_stream)
             nat.check(rc, "pp_dual_plug_table")
+        gs = pack.group_size
+        fits = (self.M == 1 and pack.chunk_size % gs == 0 and len(self.shapes) > 0
+                and all(k % gs == 0 and n % 8 == 0 and int(p) % (8 * gs) == 0
+                        for (n, k), p in zip(self.shapes, self.pos0)))
+        if scale_table and not fits:
+            raise ValueError("the scale table needs M = 1, chunk_size % group_size == 0 and, for every "
+                             "projection, K % group_size == 0, N % 8 == 0 and a position that is a multiple "
+                             "of 8 * group_size")
+        self.scale_tab = None
+        if fits and scale_table is not False:
+            n_tab = max(int(pack.scales.numel()), -(-total // gs))
+            self.scale_tab = torch.empty(n_tab, dtype=torch.float16, device=dev)
+            self._tab_pos0 = torch.tensor(self.pos0, dtype=torch.int64, device=dev)
+            self._tab_n = torch.tensor([n for n, _ in self.shapes], dtype=torch.int32, device=dev)
+            self._tab_k = torch.tensor([k for _, k in self.shapes], dtype=torch.int32, device=dev)
+            rc = L.pp_dual_scale_table(pack.scales.data_ptr(), int(pack.scales.numel()), gs,
+                                       self._tab_pos0.data_ptr(), self._tab_n.data_ptr(), self._tab_k.data_ptr(),
+                                       len(self.shapes), self.scale_tab.data_ptr(), n_tab,
+                                       torch.cuda.current_stream(dev).cuda_stream)
+            nat.check(rc, "pp_dual_scale_table")
         self.projs = None
 
     @classmethod
@@ -601,7 +625,10 @@ class DualStream:
                                       self.plug_windows,
                                       self.tail_items.data_ptr() if self.n_tail else None, self.n_tail,
                                       self.code_layout, pk.scales.data_ptr(), int(pk.scales.numel()),
-                                      pk.group_size, pk.chunk_size, amp.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                      pk.group_size, pk.chunk_size,
+                                      self.scale_tab.data_ptr() if self.scale_tab is not None else None,
+                                      int(self.scale_tab.numel()) if self.scale_tab is not None else 0,
+                                      amp.data_ptr(), cos.data_ptr(), sin.data_ptr(),
                                       pk.plug_idx.data_ptr() if pk.plug_idx.numel() else None,
                                       pk.plug_val.data_ptr() if pk.plug_val.numel() else None,
                                       self.plug_ent.data_ptr(),

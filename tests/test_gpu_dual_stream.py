@@ -27,9 +27,9 @@ def oracle_pairs(dp, tails=None):
     return w1, w2
 
 
-def oracle_outputs(w, xs):
+def oracle_outputs(w, xs, shapes=SHAPES):
     outs, pos = [], 0
-    for (N, K), x in zip(SHAPES, xs):
+    for (N, K), x in zip(shapes, xs):
         per = []
         for m in range(2):
             wm = w[m][pos:pos + N * K].reshape(N, K)
@@ -251,3 +251,94 @@ def test_plug_records(layout, chunk):
     np.testing.assert_array_equal(ent[:, 0], ((row % st.rows_per_item) << 24) | col)
     np.testing.assert_array_equal(ent[:, 1], stored[p] | (dp.scales.view(np.uint16)[g].astype(np.uint32) << 16))
     np.testing.assert_array_equal(ent[:, 2], dp.plug_val.view(np.uint16))
+
+
+# Projections on which the one-token decode reads the regrouped scales (N % 8 == 0,
+# K % 32 == 0, positions multiples of 8 * 32).
+SHAPES_T = [(24, 1024), (8, 2048), (16, 4096), (40, 512), (16, 11008), (8, 64)]
+
+
+def stream_outputs(pack, shapes, M, seed, **kw):
+    st = DualStream(pack, shapes, M=M, **kw)
+    xs_np = [np.random.default_rng(seed + p).standard_normal((M, k)).astype(np.float16)
+             for p, (_, k) in enumerate(shapes)]
+    xs = [torch.from_numpy(x).to(DEV) for x in xs_np]
+    outs = [[torch.full((M, n), float("nan"), dtype=torch.float16, device=DEV) for _ in range(2)] for n, _ in shapes]
+    st.bind(xs, outs)
+    st()
+    torch.cuda.synchronize()
+    return st, xs_np, [[o.float().cpu().numpy() for o in per] for per in outs]
+
+
+@pytest.mark.parametrize("layout", ["u16be", "i16"])
+@pytest.mark.parametrize("chunk", [50_000_000, 4096])     # one chunk; groups restarting every 4096 pairs
+@pytest.mark.parametrize("cap", [0.03, 0.2])
+@pytest.mark.parametrize("split", [False, True])
+def test_dual_stream_scale_table(layout, chunk, cap, split):
+    """One token on projections that admit the regrouped scales: the decode reads them from
+    pp_dual_scale_table's table and matches the oracle, and (without column slices, whose
+    float32 partial sums arrive in any order) the same stream reading the scales array bit
+    for bit."""
+    total = sum(n * k for n, k in SHAPES_T)
+    w1, w2 = gen.correlated_models(23, [total, total - 5000], delta_growth=False)
+    dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=cap, chunk_size=chunk))
+    pack = device_pack(dp, layout)
+    st_t, xs_np, got_t = stream_outputs(pack, SHAPES_T, 1, 3, split=split)
+    st_s, _, got_s = stream_outputs(pack, SHAPES_T, 1, 3, split=split, scale_table=False)
+    assert st_t.scale_tab is not None and st_s.scale_tab is None
+    assert st_t.split == split
+    ref = oracle_outputs(oracle_pairs(dp), xs_np, SHAPES_T)
+    for p in range(len(SHAPES_T)):
+        for m in range(2):
+            assert_gemv_close(got_t[p][m], ref[p][m], f"proj {p} model {m}")
+            if not split:
+                assert np.array_equal(got_t[p][m], got_s[p][m]), f"proj {p} model {m}"
+
+
+def test_dual_stream_scale_table_not_applicable():
+    """Shapes or batches that the regrouped scales do not fit read the scales array; asking
+    for the table there is an error."""
+    n = sum(n * k for n, k in SHAPES_T) + 1000
+    dp = odp.pack_dual(*gen.correlated_models(29, [n, n], delta_growth=False),
+                       odp.DualConfig(plug_cap=0.01, chunk_size=50_000_000))
+    pack = device_pack(dp, "u16be")
+    assert DualStream(pack, SHAPES_T, M=1).scale_tab is not None
+    assert DualStream(pack, SHAPES, M=1).scale_tab is None            # N = 3, 9 and K = 16, 520
+    assert DualStream(pack, SHAPES_T, M=2).scale_tab is None
+    shifted = [8 + sum(a * b for a, b in SHAPES_T[:i]) for i in range(len(SHAPES_T))]
+    assert DualStream(pack, SHAPES_T, M=1, positions=shifted).scale_tab is None
+    with pytest.raises(ValueError):
+        DualStream(pack, SHAPES, M=1, scale_table=True)
+
+
+def test_scale_table_layout():
+    """pp_dual_scale_table against its definition: for rows 8b..8b+7 of a projection
+    (starting at position P), tab[P/gs + 8j + q] = scales[(P + q K)/gs + j]; positions
+    outside every projection (gaps, the end) keep the scales array, 0 past its end."""
+    from polar_pack_amd import _native as nat
+    gs = 32
+    shapes = [(16, 64), (8, 4096), (24, 1024)]
+    pos0 = [256, 256 + 16 * 64 + 512, 256 + 16 * 64 + 512 + 8 * 4096]     # gaps before and between
+    end = pos0[-1] + 24 * 1024
+    n_groups = end // gs - 5                                               # the last rows run past the scales
+    rng = np.random.default_rng(31)
+    scales = rng.standard_normal(n_groups).astype(np.float16)
+    n_tab = end // gs + 7
+    tab = torch.full((n_tab,), float("nan"), dtype=torch.float16, device=DEV)
+    sc_d = torch.from_numpy(scales).to(DEV)
+    p_d = torch.tensor(pos0, dtype=torch.int64, device=DEV)
+    n_d = torch.tensor([n for n, _ in shapes], dtype=torch.int32, device=DEV)
+    k_d = torch.tensor([k for _, k in shapes], dtype=torch.int32, device=DEV)
+    rc = nat.lib().pp_dual_scale_table(sc_d.data_ptr(), n_groups, gs, p_d.data_ptr(), n_d.data_ptr(), k_d.data_ptr(),
+                                       len(shapes), tab.data_ptr(), n_tab, torch.cuda.current_stream().cuda_stream)
+    nat.check(rc, "pp_dual_scale_table")
+    got = tab.cpu().numpy()
+    want = np.concatenate([scales, np.zeros(n_tab - n_groups, np.float16)])
+    for (N, K), p in zip(shapes, pos0):
+        gk = K // gs
+        for r in range(N):
+            for j in range(gk):
+                src = (p + r * K) // gs + j
+                dst = p // gs + (r // 8) * 8 * gk + 8 * j + r % 8
+                want[dst] = scales[src] if src < n_groups else 0
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
