@@ -427,10 +427,11 @@ int pp_dual_dequant_f16_t(const void* codes, int code_layout, int64_t c_sk, cons
  * group rule of the file (group_size, chunk_size: groups restart every chunk);
  * amp_lut / cos_lut / sin_lut are float32 tables from the header (64 / 1024 / 1024
  * entries); plug entries replace the amplitude of a pair by an exact fp16 amplitude.
- * plug_ent (3 words per entry, from pp_dual_plug_table for the same projections and
- * pp_dual_stream_rows(M)) is each entry's record, read with the plug window instead of
- * gathering the entry's code and scale from the stream; the kernel takes the plug
- * amplitudes from it (plug_amp is read by the tail rows).
+ * plug_ent (2 words per entry, from pp_dual_plug_table for the same projections,
+ * pp_dual_stream_rows(M), code layout and amp_lut) is each entry's record, read with the
+ * plug window instead of gathering the entry's code and scale from the stream; the
+ * kernel takes the amplitude corrections from it (plug_amp is read by the tail rows).
+ * Projections need K < 2^19 when plug_n > 0.
  * Positions >= n_codes come from the per-model fp16 tails (tails[m], tail_len[m]): a
  * build-defined extension for streams whose models have different lengths (the file
  * format itself zero-pads the shorter model).
@@ -498,20 +499,24 @@ int pp_dual_scale_table(const void* scales, int64_t n_groups, int64_t group_size
 
 /*
  * Plug records of a dual stream (built once per stream plan, on the stream's device):
- * for entry j at stream position p = plug_idx[j],
- *   ent[3j]   = (row of p in its task of rows_per_task rows) << 24 | column of p,
- *               where projection i covers [proj_pos0[i], proj_pos0[i+1]) with rows of
- *               proj_k[i] < 2^24 columns (proj_pos0 has n_projs + 1 entries), 0 outside;
- *   ent[3j+1] = the stored 16-bit code of pair p (in the codes' layout) | the fp16 bits
- *               of its group scale << 16 (group rule of pp_dual_stream), 0 at or past n_codes;
- *   ent[3j+2] = the fp16 bits of plug_amp[j].
+ * for entry j at stream position p = plug_idx[j], with c the pair's 16-bit code
+ * (amp << 10 | phase, read from codes in code_layout) and s its group scale (group rule
+ * of pp_dual_stream),
+ *   ent[2j]   = column of p | (row of p in its task of rows_per_task <= 8 rows) << 19 |
+ *               phase << 22, where projection i covers [proj_pos0[i], proj_pos0[i+1])
+ *               with rows of proj_k[i] < 2^19 columns (proj_pos0 has n_projs + 1
+ *               entries; column and row 0 outside);
+ *   ent[2j+1] = the float32 bits of d = plug_amp[j] - amp_lut[amp] * s (one rounding),
+ *               the correction the decode adds to the pair's amplitude (0 at or past
+ *               n_codes).
+ * amp_lut is the stream's float32 amplitude table (64 entries, device memory).
  * No counterpart in the reference: an index over its code, scale and plug arrays
  * (polar_bitpack.py:205-211) for the plug correction.
  */
-int pp_dual_plug_table(const void* codes, int64_t n_codes, const void* scales, int64_t n_groups,
-                       int64_t group_size, int64_t chunk_size, const uint32_t* plug_idx, const void* plug_amp,
-                       int64_t plug_n, const int64_t* proj_pos0, const int32_t* proj_k, int64_t n_projs,
-                       int64_t rows_per_task, uint32_t* ent, void* stream);
+int pp_dual_plug_table(const void* codes, int64_t n_codes, int code_layout, const void* scales, int64_t n_groups,
+                       int64_t group_size, int64_t chunk_size, const float* amp_lut, const uint32_t* plug_idx,
+                       const void* plug_amp, int64_t plug_n, const int64_t* proj_pos0, const int32_t* proj_k,
+                       int64_t n_projs, int64_t rows_per_task, uint32_t* ent, void* stream);
 
 #ifdef __cplusplus
 }

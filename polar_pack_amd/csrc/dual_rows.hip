@@ -55,8 +55,8 @@ struct DualStreamArgs {
   int log2gs;
   const uint32_t* plug_idx;
   const f16* plug_amp;
-  const uint32_t* plug_ent;   // per entry 3 words: row in its task << 24 | column; stored code |
-                              // group scale bits << 16; plug amplitude bits
+  const uint32_t* plug_ent;   // per entry 2 words: column | row in its task << 19 | phase << 22;
+                              // the amplitude correction (float32 bits)
   int64_t plug_n;
   const int64_t* task_plug;   // per task: first plug entry in its rows, first entry past them
   int64_t n_tasks;
@@ -227,16 +227,17 @@ __device__ __forceinline__ void dchunk_compute(const char* lds, const DualLane& 
 }
 
 // Plug entries.  The host gives every task its plug range [tlo, thi): the entries whose
-// positions lie in the task's rows, and every entry its 12-byte record plug_ent (row in
-// its task and column, the stored code and group scale of its pair, the plug amplitude),
-// so a window needs one contiguous load and the x gather, and no position arithmetic.  Step ck of a task takes the window of entries
+// positions lie in the task's rows, and every entry its 8-byte record plug_ent (column,
+// row in its task and phase of its pair; the amplitude correction d = plug amplitude -
+// amp_lut[aq] * scale, computed once per plan), so a window needs one contiguous load and
+// the x gather, and no position arithmetic.  Step ck of a task takes the window of entries
 // tlo + 64*PW*ck .. +64*PW (one entry per lane and window, filled from the front); a
 // task with more entries than its steps can take corrects the rest when it finishes.
 // A window passes through three stages, one step apart, so that every load is issued a
 // step before the step that reads it and the number of loads per step is fixed:
 //   step s-2: the entries' records;
 //   step s-1: x at each entry's column;
-//   step s:   acc[row] += (plug amp - amp_lut[aq] * scale) * x * (cos, sin)(phase).
+//   step s:   acc[row] += d * x * (cos, sin)(phase).
 // Lanes without an entry load nothing (reads of 0 make their correction 0).
 
 // Uniform description of the window of one step: its task, its first entry and the
@@ -254,39 +255,36 @@ __device__ __forceinline__ int dslot_cnt(const DSlot& s) {
 
 template <int MT, int PW>
 struct DWin {
-  uint32_t aux[PW], pa[PW];            // stored code | group scale << 16, plug amplitude (16 bits)
+  uint32_t ph[PW], d[PW];              // phase, amplitude correction (float32 bits)
   uint32_t xk[PW][MT];                 // x at the entry's column (fp16 bits)
   int q[PW];                           // row of the entry in its task, -1 for none
 };
 
-typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-
 // Stage 1: the records of the window's entries.
 template <int PW>
-__device__ __forceinline__ void dwin_positions(const DualStreamArgs& A, const DSlot& t, int lane, u32x3 (&ent)[PW]) {
+__device__ __forceinline__ void dwin_positions(const DualStreamArgs& A, const DSlot& t, int lane, u32x2 (&ent)[PW]) {
   const int cnt = dslot_cnt<PW>(t);
-  const uint32_t base = 12u * (uint32_t)t.lo;
-  const rsrc_t r = make_rsrc(A.plug_ent, 12u * (uint32_t)A.plug_n);
+  const uint32_t base = 8u * (uint32_t)t.lo;
+  const rsrc_t r = make_rsrc(A.plug_ent, 8u * (uint32_t)A.plug_n);
 #pragma unroll
   for (int w = 0; w < PW; ++w)
-    ent[w] = __builtin_amdgcn_raw_buffer_load_b96(
-        r, (int)(64 * w + lane < cnt ? base + 12u * (uint32_t)(64 * w + lane) : OOB), 0, 0);
+    vload64(ent[w], 64 * w + lane < cnt ? base + 8u * (uint32_t)(64 * w + lane) : OOB, r);
 }
 
 // Stage 2: per entry its row in the task, and x at its column.
 template <int MT, int RG, int PW, int SM>
 __device__ __forceinline__ void dwin_data(const DualStreamArgs& A, const DualSeg& S, const DSlot& t,
-                                          const u32x3 (&ent)[PW], int lane, DWin<MT, PW>& W) {
+                                          const u32x2 (&ent)[PW], int lane, DWin<MT, PW>& W) {
   const int cnt = dslot_cnt<PW>(t);
 #pragma unroll
   for (int w = 0; w < PW; ++w) {
     const int e = 64 * w + lane;
-    const int row = (int)(ent[w].x >> 24), k = (int)(ent[w].x & 0xFFFFFFu);
+    const int row = (int)((ent[w].x >> 19) & 7u), k = (int)(ent[w].x & 0x7FFFFu);
     // entries of the task's other column slices are theirs
     const bool v = e < cnt && k >= S.kbeg && k < S.kend;
     W.q[w] = v ? row : -1;
-    W.aux[w] = ent[w].y;
-    W.pa[w] = ent[w].z;
+    W.ph[w] = ent[w].x >> 22;
+    W.d[w] = ent[w].y;
 #pragma unroll
     for (int j = 0; j < MT; ++j)
       vload16(W.xk[w][j], (v && j < A.M) ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
@@ -294,15 +292,13 @@ __device__ __forceinline__ void dwin_data(const DualStreamArgs& A, const DualSeg
 }
 
 // Stage 3: the corrections.
-template <int MT, int RG, int PW, int LAYOUT>
+template <int MT, int RG, int PW>
 __device__ __forceinline__ void dwin_apply(const char* lds, const DualLane& lo, const DWin<MT, PW>& W,
                                            float (&acc)[RG][2][MT]) {
 #pragma unroll
   for (int w = 0; w < PW; ++w) {
-    float an;
-    float2 cs;
-    dual_lookup1(lds, dual_half<LAYOUT>(W.aux[w]), lo, an, cs);
-    const float d = h2f(W.pa[w]) - an * h2f(W.aux[w] >> 16);
+    const float2 cs = *reinterpret_cast<const float2*>(lds + DLDS_CS + ((W.ph[w] << 7) | lo.cs));
+    const float d = __uint_as_float(W.d[w]);
     float dx[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) dx[j] = d * h2f(W.xk[w][j]);
@@ -419,7 +415,7 @@ struct DualRunner {
   DSlot s0, s1, s2;          // windows of steps s, s+1, s+2 (s = the step being computed)
   Cursor c3;                 // step s+3, whose task plug range is in flight
   u32x4 T;                   // that range: {tlo lo, tlo hi, thi lo, thi hi}
-  u32x3 I[PW];               // records of the entries of step s+1's window
+  u32x2 I[PW];               // records of the entries of step s+1's window
   DWin<MT, PW> D;            // data of step s's window
 
   __device__ __forceinline__ DualRunner(const char* l, const DualStreamArgs& a, const DualSeg& s, int t0)
@@ -472,11 +468,11 @@ struct DualRunner {
   // Entries of the finished task that its steps could not take, then its outputs.
   __device__ __forceinline__ void finish_pending() {
     for (DSlot t = pend_left; t.rem > 0; t.lo += 64 * PW, t.rem -= 64 * PW) {
-      u32x3 idx[PW];
+      u32x2 idx[PW];
       DWin<MT, PW> W;
       dwin_positions<PW>(A, t, lane, idx);
       dwin_data<MT, RG, PW, SM>(A, S, t, idx, lane, W);
-      dwin_apply<MT, RG, PW, LAYOUT>(lds, lo, W, pend);
+      dwin_apply<MT, RG, PW>(lds, lo, W, pend);
     }
     if (SPLIT && S.parts > 1) dtask_accumulate<MT, RG>(A, S, pend_ti, lane, pend);
     else dtask_write<MT, RG>(A, S, pend_ti, lane, pend);
@@ -491,7 +487,7 @@ struct DualRunner {
     s2 = slot_of(c3, T);
     advance_slot(c3);
     load_range(c3, T);
-    if (dslot_cnt<PW>(s0) > 0) dwin_apply<MT, RG, PW, LAYOUT>(lds, lo, D, acc);
+    if (dslot_cnt<PW>(s0) > 0) dwin_apply<MT, RG, PW>(lds, lo, D, acc);
     dwin_data<MT, RG, PW, SM>(A, S, s1, I, lane, D);
     dwin_positions<PW>(A, s2, lane, I);
     if (cur.ck == 0 && pend_ti >= 0) finish_pending();
@@ -791,8 +787,11 @@ __global__ __launch_bounds__(256) void dual_tail_kernel(const DualTailArgs T) {
 // Records of the plug entries for the stream decode (see DualStreamArgs::plug_ent).
 // Projection p covers stream positions [proj_pos0[p], proj_pos0[p] + N_p * proj_k[p]);
 // proj_pos0 has n_projs + 1 entries (the last one the end of the stream's projections).
-__global__ __launch_bounds__(256) void dual_plug_table_kernel(const uint16_t* codes, int64_t n_codes, const f16* scales,
-                                                              int64_t n_groups, int64_t gs, int64_t chunk,
+// The correction is the one the decode applies to the pair's amplitude, in float32 with
+// one rounding: d = plug_amp - amp_lut[aq] * scale.
+__global__ __launch_bounds__(256) void dual_plug_table_kernel(const uint16_t* codes, int64_t n_codes, int layout,
+                                                              const f16* scales, int64_t n_groups, int64_t gs,
+                                                              int64_t chunk, const float* amp_lut,
                                                               const uint32_t* plug_idx, const f16* plug_amp,
                                                               int64_t plug_n, const int64_t* proj_pos0,
                                                               const int32_t* proj_k, int n_projs, int rows_per_task,
@@ -800,11 +799,15 @@ __global__ __launch_bounds__(256) void dual_plug_table_kernel(const uint16_t* co
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= plug_n) return;
   const int64_t p = plug_idx[j];
-  uint32_t w0 = 0, w1 = 0;
+  uint32_t w0 = 0;
+  float d = 0.f;
   if (p < n_codes) {
     const int64_t g = (p / chunk) * ((chunk + gs - 1) / gs) + (p % chunk) / gs;
-    const uint32_t sc = g < n_groups ? (uint32_t)__builtin_bit_cast(unsigned short, scales[g]) : 0u;
-    w1 = (uint32_t)codes[p] | (sc << 16);
+    const float sc = g < n_groups ? (float)scales[g] : 0.f;
+    const uint32_t st = codes[p];
+    const uint32_t c = layout == PP_DUAL_U16_BE ? (((st & 0xFFu) << 8) | (st >> 8)) : (st ^ 0x8000u);
+    w0 = (c & 0x3FFu) << 22;
+    d = fmaf(-amp_lut[c >> 10], sc, (float)plug_amp[j]);
   }
   if (p >= proj_pos0[0] && p < proj_pos0[n_projs]) {
     int lo = 0, hi = n_projs - 1;                   // last projection starting at or before p
@@ -815,11 +818,10 @@ __global__ __launch_bounds__(256) void dual_plug_table_kernel(const uint16_t* co
     }
     const int64_t local = p - proj_pos0[lo], K = proj_k[lo];
     const int64_t row = local / K;
-    w0 = ((uint32_t)(row % rows_per_task) << 24) | (uint32_t)(local - row * K);
+    w0 |= ((uint32_t)(row % rows_per_task) << 19) | (uint32_t)(local - row * K);
   }
-  ent[3 * j] = w0;
-  ent[3 * j + 1] = w1;
-  ent[3 * j + 2] = (uint32_t)__builtin_bit_cast(unsigned short, plug_amp[j]);
+  ent[2 * j] = w0;
+  ent[2 * j + 1] = __float_as_uint(d);
 }
 
 // The group scales regrouped for the one-token stream decode: for every projection i
@@ -906,21 +908,22 @@ extern "C" int pp_dual_stream_rows(int64_t M) {
   return dual_stream_rg(dual_stream_mt(M));
 }
 
-extern "C" int pp_dual_plug_table(const void* codes, int64_t n_codes, const void* scales, int64_t n_groups,
-                                  int64_t group_size, int64_t chunk_size, const uint32_t* plug_idx,
-                                  const void* plug_amp, int64_t plug_n, const int64_t* proj_pos0,
-                                  const int32_t* proj_k, int64_t n_projs, int64_t rows_per_task, uint32_t* ent,
-                                  void* stream) {
+extern "C" int pp_dual_plug_table(const void* codes, int64_t n_codes, int code_layout, const void* scales,
+                                  int64_t n_groups, int64_t group_size, int64_t chunk_size, const float* amp_lut,
+                                  const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n,
+                                  const int64_t* proj_pos0, const int32_t* proj_k, int64_t n_projs,
+                                  int64_t rows_per_task, uint32_t* ent, void* stream) {
   PP_REQUIRE(plug_n >= 0 && plug_n < (1ll << 28), "the stream decode takes fewer than 2^28 plug entries");
   if (plug_n == 0) return PP_OK;
-  PP_REQUIRE(codes && scales && plug_idx && plug_amp && proj_pos0 && proj_k && ent, "null pointer");
+  PP_REQUIRE(codes && scales && amp_lut && plug_idx && plug_amp && proj_pos0 && proj_k && ent, "null pointer");
+  PP_REQUIRE(code_layout == PP_DUAL_I16_OFFSET || code_layout == PP_DUAL_U16_BE, "bad code_layout");
   PP_REQUIRE(n_codes >= 0 && n_groups >= 1 && group_size >= 1 && chunk_size >= 1, "bad sizes");
   PP_REQUIRE(n_projs >= 1 && n_projs < (1ll << 30), "bad n_projs");
-  PP_REQUIRE(rows_per_task >= 1 && rows_per_task <= 255, "bad rows_per_task");
+  PP_REQUIRE(rows_per_task >= 1 && rows_per_task <= 8, "bad rows_per_task");
   hipLaunchKernelGGL(dual_plug_table_kernel, dim3((unsigned)((plug_n + 255) / 256)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const uint16_t*>(codes), n_codes,
-                     reinterpret_cast<const f16*>(scales), n_groups, group_size, chunk_size, plug_idx,
-                     reinterpret_cast<const f16*>(plug_amp), plug_n, proj_pos0, proj_k, (int)n_projs,
+                     code_layout, reinterpret_cast<const f16*>(scales), n_groups, group_size, chunk_size, amp_lut,
+                     plug_idx, reinterpret_cast<const f16*>(plug_amp), plug_n, proj_pos0, proj_k, (int)n_projs,
                      (int)rows_per_task, ent);
   PP_LAUNCH_CHECK();
   return PP_OK;

@@ -487,8 +487,8 @@ class DualStream:
         if total > longest:
             raise ValueError(f"projections cover {total} positions, the stream holds {longest}")
         for n, k in self.shapes:
-            if k % 8 or k >= 2 ** 24 or n >= 2 ** 31:
-                raise ValueError(f"dual stream decode needs K % 8 == 0 and K < 2^24 (got N={n}, K={k})")
+            if k % 8 or k >= 2 ** 19 or n >= 2 ** 31:
+                raise ValueError(f"dual stream decode needs K % 8 == 0 and K < 2^19 (got N={n}, K={k})")
         if pack.group_size < 8 or pack.group_size & (pack.group_size - 1) or pack.chunk_size % 8:
             raise ValueError("dual stream decode needs a power-of-two group_size >= 8 and chunk_size % 8 == 0")
         plug = pack.plug_host()
@@ -530,16 +530,16 @@ class DualStream:
         self._tail_ptrs = nat.ptr_array([t.data_ptr() if t is not None and t.numel() else 0 for t in tails])
         self._tail_len = (C.c_int64 * 2)(*pack.tail_lengths)
         self.code_layout = nat.PP_DUAL_U16_BE if pack.layout == "u16be" else nat.PP_DUAL_I16_OFFSET
-        # each plug entry's 12-byte record (row in its task, column, stored code and group
-        # scale of its pair, plug amplitude), built once here (pp_dual_plug_table)
+        # each plug entry's 8-byte record (column, row in its task and phase of its pair; its
+        # amplitude correction), built once here (pp_dual_plug_table)
         P = int(pack.plug_idx.numel())
-        self.plug_ent = torch.zeros(max(3 * P, 1), dtype=torch.int32, device=dev)
+        self.plug_ent = torch.zeros(max(2 * P, 1), dtype=torch.int32, device=dev)
         if P:
             self._proj_pos0 = torch.tensor(list(self.pos0) + [total], dtype=torch.int64, device=dev)
             self._proj_k = torch.tensor([k for _, k in self.shapes], dtype=torch.int32, device=dev)
-            rc = L.pp_dual_plug_table(pack.codes.data_ptr(), pack.n_codes, pack.scales.data_ptr(),
+            rc = L.pp_dual_plug_table(pack.codes.data_ptr(), pack.n_codes, self.code_layout, pack.scales.data_ptr(),
                                       int(pack.scales.numel()), pack.group_size, pack.chunk_size,
-                                      pack.plug_idx.data_ptr(), pack.plug_val.data_ptr(), P,
+                                      self.luts[0].data_ptr(), pack.plug_idx.data_ptr(), pack.plug_val.data_ptr(), P,
                                       self._proj_pos0.data_ptr(), self._proj_k.data_ptr(), len(self.shapes),
                                       self.rows_per_item, self.plug_ent.data_ptr(),
                                       torch.cuda.current_stream(dev).cuda_stream)

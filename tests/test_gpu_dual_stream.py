@@ -233,24 +233,25 @@ def test_single_linear_split_k(shape, M):
 @pytest.mark.parametrize("layout", ["u16be", "i16"])
 @pytest.mark.parametrize("chunk", [50_000_000, 1000])
 def test_plug_records(layout, chunk):
-    """pp_dual_plug_table: each entry's row in its task and column, its pair's stored code
-    | its group's fp16 scale bits << 16 (groups restart every chunk, polar_bitpack.py:201-203),
-    and its plug amplitude."""
+    """pp_dual_plug_table: each entry's column, row in its task and phase, and the float32
+    correction d = plug amplitude - amp_lut[aq] * group scale (groups restart every chunk,
+    polar_bitpack.py:201-203), rounded once."""
     w1, w2 = gen.correlated_models(31, [TOTAL, TOTAL], delta_growth=False)
     dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=0.03, chunk_size=chunk))
     pack = device_pack(dp, layout)
     st = DualStream(pack, SHAPES, M=1)
-    stored = pack.codes.cpu().numpy().view(np.uint16).astype(np.uint32)
+    code = odp.from_be_bytes(dp.codes_be).astype(np.uint32)
     p = dp.plug_idx.astype(np.int64)
     g = (p // chunk) * (-(-chunk // dp.group_size)) + (p % chunk) // dp.group_size
     pos0 = np.cumsum([0] + [n * k for n, k in SHAPES])
     proj = np.searchsorted(pos0, p, side="right") - 1
     K = np.array([k for _, k in SHAPES])[proj]
     row, col = (p - pos0[proj]) // K, (p - pos0[proj]) % K
-    ent = st.plug_ent.cpu().numpy().view(np.uint32)[:3 * p.size].reshape(-1, 3)
-    np.testing.assert_array_equal(ent[:, 0], ((row % st.rows_per_item) << 24) | col)
-    np.testing.assert_array_equal(ent[:, 1], stored[p] | (dp.scales.view(np.uint16)[g].astype(np.uint32) << 16))
-    np.testing.assert_array_equal(ent[:, 2], dp.plug_val.view(np.uint16))
+    ent = st.plug_ent.cpu().numpy().view(np.uint32)[:2 * p.size].reshape(-1, 2)
+    np.testing.assert_array_equal(ent[:, 0], col | ((row % st.rows_per_item) << 19) | ((code[p] & 0x3FF) << 22))
+    amp = st.luts[0].cpu().numpy().astype(np.float64)
+    d = dp.plug_val.astype(np.float64) - amp[code[p] >> 10] * dp.scales[g].astype(np.float64)
+    np.testing.assert_array_equal(ent[:, 1], d.astype(np.float32).view(np.uint32))
 
 
 # Projections on which the one-token decode reads the regrouped scales (N % 8 == 0,
