@@ -446,10 +446,10 @@ int pp_dual_dequant_f16_t(const void* codes, int code_layout, int64_t c_sk, cons
  * be zero before the first launch and is left zero by each; launches that share it must
  * not overlap.  A null workspace skips split segments.
  * scale_tab (optional, n_tab fp16 entries from pp_dual_scale_table for the same
- * projections): with M = 1 and chunk_size % group_size == 0 the row kernel reads each
- * decode step's group scales from it (one 16-byte load for the 8 rows of a task) instead
- * of from scales; it requires every projection to have K % group_size == 0, N % 8 == 0
- * and pos0 % (8 * group_size) == 0.  Null: scales only.
+ * projections and R = pp_dual_stream_rows(M)): with chunk_size % group_size == 0 the row
+ * kernel reads each decode step's group scales from it (one load for the R rows of a
+ * task) instead of from scales; it requires every projection to have K % group_size == 0,
+ * N % R == 0 and pos0 % (R * group_size) == 0.  Null: scales only.
  * Replaces the per-projection polar_dual_bitpacked calls of a decode step
  * (polar_kernels.py:98-115) and the decode of unpack_dual_models
  * (polar_bitpack.py:194-260).
@@ -485,17 +485,18 @@ int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs,
  * Group scales of a dual stream regrouped for pp_dual_stream's scale_tab (built once per
  * stream plan, on the stream's device): projection i covers stream positions
  * proj_pos0[i] .. proj_pos0[i] + proj_n[i] * proj_k[i] - 1 (rows of proj_k[i] columns;
- * proj_pos0 ascending, n_projs entries).  For the rows 8b .. 8b+7 of projection i, which
- * start at position P = proj_pos0[i] + 8 b proj_k[i],
- *   tab[P / group_size + 8 j + q] = scales[(P + q proj_k[i]) / group_size + j]
- * (row 8b + q, column group j); entries outside every projection are copied from scales
+ * proj_pos0 ascending, n_projs entries).  With R = rows_per_task (8, 4 or 2:
+ * pp_dual_stream_rows(M)), for the rows Rb .. Rb+R-1 of projection i, which start at
+ * position P = proj_pos0[i] + R b proj_k[i],
+ *   tab[P / group_size + R j + q] = scales[(P + q proj_k[i]) / group_size + j]
+ * (row Rb + q, column group j); entries outside every projection are copied from scales
  * (0 at or past n_groups).  n_tab >= the end of the last projection / group_size.
  * Requirements as for scale_tab above.  No counterpart in the reference: a reordering of
  * its scale array (polar_bitpack.py:205-211) for the decode's loads.
  */
 int pp_dual_scale_table(const void* scales, int64_t n_groups, int64_t group_size, const int64_t* proj_pos0,
-                        const int32_t* proj_n, const int32_t* proj_k, int64_t n_projs, void* tab, int64_t n_tab,
-                        void* stream);
+                        const int32_t* proj_n, const int32_t* proj_k, int64_t n_projs, int64_t rows_per_task,
+                        void* tab, int64_t n_tab, void* stream);
 
 /*
  * Plug records of a dual stream (built once per stream plan, on the stream's device):

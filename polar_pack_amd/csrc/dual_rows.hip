@@ -15,8 +15,8 @@
 // done in the first step of the next.  Plug corrections go through a three-stage window
 // pipeline (below).  Per lane and row a chunk is one 16-byte load (8 pairs that share one
 // group scale, so the scale multiplies a per-lane partial sum once per 8 pairs) and one
-// 2-byte scale load; at one token with the scale table (SM = 2, pp_dual_scale_table) one
-// 16-byte load brings the scales of all 8 rows of the task (measured on the 3B-shaped
+// 2-byte scale load; with the scale table (SM = 2, pp_dual_scale_table) one load brings
+// the scales of all RG rows of the task (16 bytes at one token; measured on the 3B-shaped
 // stream: 1.12 -> 1.03 ms per step, the per-row scale loads and their group arithmetic
 // having cost more than the decode's table lookups).
 //
@@ -121,7 +121,7 @@ template <int MT, int RG>
 struct DChunk {
   u32x4 q[RG];          // 8 pairs per lane per row
   uint32_t sc[RG];      // their group scale (fp16 bits); SM = 2: in sq
-  u32x4 sq;             // SM = 2 (RG = 8): the 8 rows' scales of the lane's group, one fp16 each
+  u32x4 sq;             // SM = 2: the RG rows' scales of the lane's group, one fp16 each
   u32x4 xr[MT];         // 8 fp16 activations per lane
 };
 
@@ -148,12 +148,24 @@ __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const Dual
   const int k = kc + 8 * lane;
   const int64_t base = S.pos0 + first;   // stream position of (row, kc): uniform
   if constexpr (SM == 2) {
-    // the task's 8 rows start at a multiple of 8 gs positions: their scales of group j
-    // (columns j gs .. j gs + gs - 1 of each row) are the 16 bytes at 8 * (task start / gs + 8 j)
-    static_assert(RG == 8, "the scale table holds 8 rows per cell");
+    // the task's RG rows start at a multiple of RG gs positions: their scales of group j
+    // (columns j gs .. j gs + gs - 1 of each row) are the 2 RG bytes at entry
+    // task start / gs + RG j of the table
+    static_assert(RG == 8 || RG == 4 || RG == 2, "scale table cells hold 8, 4 or 2 rows");
     const int64_t t0 = (S.pos0 + (int64_t)row * S.ldc) >> A.log2gs;
     const rsrc_t rt = make_rsrc(A.scale_tab + t0, 2u * (uint32_t)(A.n_tab - t0));
-    vload128(c.sq, 16u * ((uint32_t)k >> A.log2gs), rt);
+    const uint32_t off = 2u * RG * ((uint32_t)k >> A.log2gs);
+    if constexpr (RG == 8) {
+      vload128(c.sq, off, rt);
+    } else if constexpr (RG == 4) {
+      u32x2 v;
+      vload64(v, off, rt);
+      c.sq = u32x4{v.x, v.y, 0u, 0u};
+    } else {
+      uint32_t v;
+      vload32(v, off, rt);
+      c.sq = u32x4{v, 0u, 0u, 0u};
+    }
   } else {
 #pragma unroll
     for (int r = 0; r < RG; ++r) {
@@ -824,15 +836,16 @@ __global__ __launch_bounds__(256) void dual_plug_table_kernel(const uint16_t* co
   ent[2 * j + 1] = __float_as_uint(d);
 }
 
-// The group scales regrouped for the one-token stream decode: for every projection i
-// (stream positions proj_pos0[i] .. + N_i K_i, rows of K_i columns, K_i % gs == 0,
-// proj_pos0[i] % (8 gs) == 0, N_i % 8 == 0) and every run of 8 rows starting at row 8b,
-// position P = proj_pos0[i] + 8 b K_i: tab[P/gs + 8 j + q] = scales[(P + q K_i)/gs + j], the
-// scale of row 8b + q, column group j.  A decode step then loads the 8 rows' scales of its
-// group in one 16-byte load.  Entries outside every projection copy scales (0 past n_groups).
+// The group scales regrouped for the stream decode with R rows per task: for every
+// projection i (stream positions proj_pos0[i] .. + N_i K_i, rows of K_i columns,
+// K_i % gs == 0, proj_pos0[i] % (R gs) == 0, N_i % R == 0) and every run of R rows starting
+// at row R b, position P = proj_pos0[i] + R b K_i: tab[P/gs + R j + q] =
+// scales[(P + q K_i)/gs + j], the scale of row R b + q, column group j.  A decode step then
+// loads the R rows' scales of its group in one load.  Entries outside every projection
+// copy scales (0 past n_groups).
 __global__ __launch_bounds__(256) void dual_scale_table_kernel(const f16* scales, int64_t n_groups, int log2gs,
                                                                const int64_t* proj_pos0, const int32_t* proj_n,
-                                                               const int32_t* proj_k, int n_projs, f16* tab,
+                                                               const int32_t* proj_k, int n_projs, int R, f16* tab,
                                                                int64_t n_tab) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_tab) return;
@@ -848,9 +861,9 @@ __global__ __launch_bounds__(256) void dual_scale_table_kernel(const f16* scales
     const int64_t K = proj_k[lo], gk = K >> log2gs;   // column groups per row
     const int64_t local = t - (proj_pos0[lo] >> log2gs);
     if (local < (int64_t)proj_n[lo] * gk) {
-      const int64_t blk = local / (8 * gk), r = local - blk * 8 * gk;
-      const int64_t j = r >> 3, q = r & 7;
-      src = (proj_pos0[lo] >> log2gs) + (blk * 8 + q) * gk + j;
+      const int64_t blk = local / (R * gk), r = local - blk * R * gk;
+      const int64_t j = r / R, q = r - j * R;
+      src = (proj_pos0[lo] >> log2gs) + (blk * R + q) * gk + j;
     }
   }
   tab[t] = src < n_groups ? scales[src] : (f16)0.f;
@@ -931,16 +944,19 @@ extern "C" int pp_dual_plug_table(const void* codes, int64_t n_codes, int code_l
 
 extern "C" int pp_dual_scale_table(const void* scales, int64_t n_groups, int64_t group_size,
                                    const int64_t* proj_pos0, const int32_t* proj_n, const int32_t* proj_k,
-                                   int64_t n_projs, void* tab, int64_t n_tab, void* stream) {
+                                   int64_t n_projs, int64_t rows_per_task, void* tab, int64_t n_tab, void* stream) {
   PP_REQUIRE(scales && proj_pos0 && proj_n && proj_k && tab, "null pointer");
   PP_REQUIRE(n_groups >= 1 && n_tab >= 1 && n_tab < (1ll << 40), "bad n_groups / n_tab");
   PP_REQUIRE(group_size >= 8 && (group_size & (group_size - 1)) == 0, "group_size must be a power of two >= 8");
   PP_REQUIRE(n_projs >= 1 && n_projs < (1ll << 30), "bad n_projs");
+  PP_REQUIRE(rows_per_task == 8 || rows_per_task == 4 || rows_per_task == 2,
+             "rows_per_task must be pp_dual_stream_rows(M): 8, 4 or 2");
   int log2gs = 0;
   while ((1ll << log2gs) < group_size) ++log2gs;
   hipLaunchKernelGGL(dual_scale_table_kernel, dim3((unsigned)((n_tab + 255) / 256)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const f16*>(scales), n_groups, log2gs,
-                     proj_pos0, proj_n, proj_k, (int)n_projs, reinterpret_cast<f16*>(tab), n_tab);
+                     proj_pos0, proj_n, proj_k, (int)n_projs, (int)rows_per_task, reinterpret_cast<f16*>(tab),
+                     n_tab);
   PP_LAUNCH_CHECK();
   return PP_OK;
 }
@@ -1029,9 +1045,9 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
   if (n_segs > 0) {
     int rc;
     const int pw = plug_windows;
-    if (sm == 0 && mt == 1 && scale_tab != nullptr) {
-      rc = be ? launch_dual_stream<1, PP_DUAL_U16_BE, 2>(A, pw, st)
-              : launch_dual_stream<1, PP_DUAL_I16_OFFSET, 2>(A, pw, st);
+    if (sm == 0 && scale_tab != nullptr) {
+      rc = be ? dispatch_dual_stream<PP_DUAL_U16_BE, 2>(A, mt, pw, st)
+              : dispatch_dual_stream<PP_DUAL_I16_OFFSET, 2>(A, mt, pw, st);
     } else if (be) {
       rc = sm == 0 ? dispatch_dual_stream<PP_DUAL_U16_BE, 0>(A, mt, pw, st)
                    : dispatch_dual_stream<PP_DUAL_U16_BE, 1>(A, mt, pw, st);

@@ -465,10 +465,10 @@ class DualStream:
     8 pairs (a lane reads 8 pairs that share one group scale).  ``split`` as for
     :class:`QuadStream` (column slices for launches with few row tasks, summed in a
     workspace owned by this object: two launches of one DualStream must not overlap).
-    ``scale_table`` (default: where it applies) gives the one-token decode the group scales
-    regrouped per 8-row task (``pp_dual_scale_table``: one load per step for all 8 rows);
-    it applies when M = 1, chunk_size % group_size == 0 and every projection has
-    K % group_size == 0, N % 8 == 0 and a position that is a multiple of 8 * group_size.
+    ``scale_table`` (default: where it applies) gives the decode the group scales regrouped
+    per task of R = ``rows_per_item`` rows (``pp_dual_scale_table``: one load per step for
+    all R rows); it applies when chunk_size % group_size == 0 and every projection has
+    K % group_size == 0, N % R == 0 and a position that is a multiple of R * group_size.
     """
 
     def __init__(self, pack, shapes: Sequence[Tuple[int, int]], M: int = 1, plug_windows=None, split: bool = True,
@@ -544,14 +544,14 @@ class DualStream:
                                       self.rows_per_item, self.plug_ent.data_ptr(),
                                       torch.cuda.current_stream(dev).cuda_stream)
             nat.check(rc, "pp_dual_plug_table")
-        gs = pack.group_size
-        fits = (self.M == 1 and pack.chunk_size % gs == 0 and len(self.shapes) > 0
-                and all(k % gs == 0 and n % 8 == 0 and int(p) % (8 * gs) == 0
+        gs, R = pack.group_size, self.rows_per_item
+        fits = (pack.chunk_size % gs == 0 and len(self.shapes) > 0
+                and all(k % gs == 0 and n % R == 0 and int(p) % (R * gs) == 0
                         for (n, k), p in zip(self.shapes, self.pos0)))
         if scale_table and not fits:
-            raise ValueError("the scale table needs M = 1, chunk_size % group_size == 0 and, for every "
-                             "projection, K % group_size == 0, N % 8 == 0 and a position that is a multiple "
-                             "of 8 * group_size")
+            raise ValueError(f"the scale table needs chunk_size % group_size == 0 and, for every projection, "
+                             f"K % group_size == 0, N % {R} == 0 and a position that is a multiple of "
+                             f"{R} * group_size")
         self.scale_tab = None
         if fits and scale_table is not False:
             n_tab = max(int(pack.scales.numel()), -(-total // gs))
@@ -561,7 +561,7 @@ class DualStream:
             self._tab_k = torch.tensor([k for _, k in self.shapes], dtype=torch.int32, device=dev)
             rc = L.pp_dual_scale_table(pack.scales.data_ptr(), int(pack.scales.numel()), gs,
                                        self._tab_pos0.data_ptr(), self._tab_n.data_ptr(), self._tab_k.data_ptr(),
-                                       len(self.shapes), self.scale_tab.data_ptr(), n_tab,
+                                       len(self.shapes), R, self.scale_tab.data_ptr(), n_tab,
                                        torch.cuda.current_stream(dev).cuda_stream)
             nat.check(rc, "pp_dual_scale_table")
         self.projs = None

@@ -275,8 +275,9 @@ def stream_outputs(pack, shapes, M, seed, **kw):
 @pytest.mark.parametrize("chunk", [50_000_000, 4096])     # one chunk; groups restarting every 4096 pairs
 @pytest.mark.parametrize("cap", [0.03, 0.2])
 @pytest.mark.parametrize("split", [False, True])
-def test_dual_stream_scale_table(layout, chunk, cap, split):
-    """One token on projections that admit the regrouped scales: the decode reads them from
+@pytest.mark.parametrize("M", [1, 2, 3])                  # 8, 4 and 2 rows per task
+def test_dual_stream_scale_table(layout, chunk, cap, split, M):
+    """Projections that admit the regrouped scales: the decode reads them from
     pp_dual_scale_table's table and matches the oracle, and (without column slices, whose
     float32 partial sums arrive in any order) the same stream reading the scales array bit
     for bit."""
@@ -284,8 +285,8 @@ def test_dual_stream_scale_table(layout, chunk, cap, split):
     w1, w2 = gen.correlated_models(23, [total, total - 5000], delta_growth=False)
     dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=cap, chunk_size=chunk))
     pack = device_pack(dp, layout)
-    st_t, xs_np, got_t = stream_outputs(pack, SHAPES_T, 1, 3, split=split)
-    st_s, _, got_s = stream_outputs(pack, SHAPES_T, 1, 3, split=split, scale_table=False)
+    st_t, xs_np, got_t = stream_outputs(pack, SHAPES_T, M, 3, split=split)
+    st_s, _, got_s = stream_outputs(pack, SHAPES_T, M, 3, split=split, scale_table=False)
     assert st_t.scale_tab is not None and st_s.scale_tab is None
     assert st_t.split == split
     ref = oracle_outputs(oracle_pairs(dp), xs_np, SHAPES_T)
@@ -305,16 +306,18 @@ def test_dual_stream_scale_table_not_applicable():
     pack = device_pack(dp, "u16be")
     assert DualStream(pack, SHAPES_T, M=1).scale_tab is not None
     assert DualStream(pack, SHAPES, M=1).scale_tab is None            # N = 3, 9 and K = 16, 520
-    assert DualStream(pack, SHAPES_T, M=2).scale_tab is None
+    assert DualStream(pack, [(26, 1024)], M=2).scale_tab is None      # 26 rows: not whole tasks of 4
+    assert DualStream(pack, [(26, 1024)], M=4).scale_tab is not None  # whole tasks of 2
     shifted = [8 + sum(a * b for a, b in SHAPES_T[:i]) for i in range(len(SHAPES_T))]
     assert DualStream(pack, SHAPES_T, M=1, positions=shifted).scale_tab is None
     with pytest.raises(ValueError):
         DualStream(pack, SHAPES, M=1, scale_table=True)
 
 
-def test_scale_table_layout():
-    """pp_dual_scale_table against its definition: for rows 8b..8b+7 of a projection
-    (starting at position P), tab[P/gs + 8j + q] = scales[(P + q K)/gs + j]; positions
+@pytest.mark.parametrize("R", [8, 4, 2])
+def test_scale_table_layout(R):
+    """pp_dual_scale_table against its definition: for rows Rb..Rb+R-1 of a projection
+    (starting at position P), tab[P/gs + Rj + q] = scales[(P + q K)/gs + j]; positions
     outside every projection (gaps, the end) keep the scales array, 0 past its end."""
     from polar_pack_amd import _native as nat
     gs = 32
@@ -331,7 +334,7 @@ def test_scale_table_layout():
     n_d = torch.tensor([n for n, _ in shapes], dtype=torch.int32, device=DEV)
     k_d = torch.tensor([k for _, k in shapes], dtype=torch.int32, device=DEV)
     rc = nat.lib().pp_dual_scale_table(sc_d.data_ptr(), n_groups, gs, p_d.data_ptr(), n_d.data_ptr(), k_d.data_ptr(),
-                                       len(shapes), tab.data_ptr(), n_tab, torch.cuda.current_stream().cuda_stream)
+                                       len(shapes), R, tab.data_ptr(), n_tab, torch.cuda.current_stream().cuda_stream)
     nat.check(rc, "pp_dual_scale_table")
     got = tab.cpu().numpy()
     want = np.concatenate([scales, np.zeros(n_tab - n_groups, np.float16)])
@@ -340,6 +343,6 @@ def test_scale_table_layout():
         for r in range(N):
             for j in range(gk):
                 src = (p + r * K) // gs + j
-                dst = p // gs + (r // 8) * 8 * gk + 8 * j + r % 8
+                dst = p // gs + (r // R) * R * gk + R * j + r % R
                 want[dst] = scales[src] if src < n_groups else 0
     assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
