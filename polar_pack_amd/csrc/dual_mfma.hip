@@ -12,7 +12,9 @@
 // consecutive k, the B operand x as stored):
 //  * per 32-row step lane l reads the codes of column n0 + l%16 at rows k0 + 8(l/16) .. +7
 //    (8 two-byte loads, 32-byte runs over 16 lanes) and their 8 group scales, looks up
-//    amplitude and (cos, sin) in the dual LDS tables and rounds the two weights to fp16;
+//    amplitude and (cos, sin) in the dual LDS tables and rounds the two weights to fp16
+//    (up to 32 tokens without a plug table, rows of 8 codes are loaded instead and the
+//    weights transposed through LDS: see "Transposing loads" below);
 //  * 2 models x TT token tiles of 16 x 16 fp32 sums stay in registers: two waves per SIMD
 //    (8 per workgroup, one workgroup per CU: the tables take 129 KiB of LDS), so one
 //    wave's decode runs beside the other's products;
@@ -58,12 +60,26 @@ struct DualMfmaArgs {
   float* acc;              // slices > 1: [2][N][M] float32, zero on entry
   int xcd_remap;
   int vec_out;             // outputs 8-byte aligned with o_sm % 4 == 0
+  int gcols;               // transposing loads: N / group_size (group of (k, n) = k gcols + n / gs)
 };
+
+// Transposing loads (2 token tiles, no plug table, N % 16 == 0, N % group_size == 0,
+// 16-byte aligned rows): per 32-row step lane l loads the 8 codes of row k0 + l/2 at columns
+// n0 + 8(l%2) .. +7 (one 16-byte load) and their one group scale, decodes them and writes
+// the 16 fp16 weights of each model into the wave's LDS area transposed ([n][k], rows of
+// DM_TROW bytes); the A operands are then one 16-byte LDS read per model.  This replaces
+// 8 two-byte code loads and 8 scale loads per lane and step.
+constexpr int DM_TROW = 80;                 // bytes per n row (32 k of fp16 + 16 padding: spreads the banks)
+constexpr int DM_TMODEL = 16 * DM_TROW;     // one model's 16 x 32 block
+constexpr int DM_TWAVE = 2 * DM_TMODEL;     // per wave
+constexpr uint32_t DM_LDS_BYTES = DLDS_BYTES + DM_WAVES * DM_TWAVE;
 
 template <int TT>
 struct DmStage {
   uint32_t c[8];           // 8 stored codes of the lane's column (low 16 bits)
   uint32_t sc[8];          // their group scales (fp16 bits)
+  u32x4 cq;                // transposing loads: 8 stored codes of the lane's row
+  uint32_t sq;             // and their group scale
   u32x4 xb[TT];            // 8 fp16 x of token 16t + l%16
 };
 
@@ -123,30 +139,37 @@ __device__ __forceinline__ void dplug_patch(const DualMfmaArgs& A, DmPlug& P, in
 // past the slice end ke through an empty record).  voc: the lane's code offset (OOB past
 // N), the 8 rows 2*ldk bytes apart in the scalar operand; gbase: group index of (k0 = 0,
 // the lane's column); vox: x offsets per token tile.
-template <int TT>
+template <int TT, bool TL>
 __device__ __forceinline__ void dm_issue(const DualMfmaArgs& A, int n0, int n, bool ok, int q, int k0, int ke,
-                                         uint32_t voc, const uint32_t (&vox)[TT], const f16* xblk, int j0,
-                                         DmStage<TT>& S) {
+                                         uint32_t voc, uint32_t vos, const uint32_t (&vox)[TT], const f16* xblk,
+                                         int j0, DmStage<TT>& S) {
   const uint32_t xrec = k0 < ke ? 2u * (uint32_t)((int64_t)(A.M - 1 - j0) * A.x_sm + (ke - k0)) : 0u;
   k0 = min(k0, A.K - 32);
   const rsrc_t rc = make_rsrc(A.codes + (int64_t)k0 * A.ldk + n0,
                               2u * (uint32_t)((int64_t)(A.K - 1 - k0) * A.ldk + (A.N - n0)));
-  const int st = (int)(2 * A.ldk);
+  if constexpr (TL) {
+    // voc: the lane's row and 8 columns; vos: its group in the step's first row
+    S.cq = __builtin_amdgcn_raw_buffer_load_b128(rc, (int)voc, 0, NT_AUX);
+    const int64_t g0 = (int64_t)k0 * A.gcols;
+    vload16(S.sq, vos, make_rsrc(A.scales + g0, 2u * (uint32_t)(A.n_groups - g0)));
+  } else {
+    const int st = (int)(2 * A.ldk);
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
-    S.c[e] = __builtin_amdgcn_raw_buffer_load_b16(rc, (int)voc, e * st, NT_AUX);
-  const rsrc_t rs = make_rsrc(A.scales, 2u * (uint32_t)A.n_groups);
+    for (int e = 0; e < 8; ++e)
+      S.c[e] = __builtin_amdgcn_raw_buffer_load_b16(rc, (int)voc, e * st, NT_AUX);
+    const rsrc_t rs = make_rsrc(A.scales, 2u * (uint32_t)A.n_groups);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int64_t g = ((int64_t)(k0 + 8 * q + e) * A.N + n) >> A.log2gs;
-    vload16(S.sc[e], ok ? 2u * (uint32_t)g : OOB, rs);
+    for (int e = 0; e < 8; ++e) {
+      const int64_t g = ((int64_t)(k0 + 8 * q + e) * A.N + n) >> A.log2gs;
+      vload16(S.sc[e], ok ? 2u * (uint32_t)g : OOB, rs);
+    }
   }
   const rsrc_t rx = make_rsrc(xblk + min(k0, A.K - 32), xrec);
 #pragma unroll
   for (int t = 0; t < TT; ++t) vload128c(S.xb[t], vox[t], rx);
 }
 
-template <int TT, bool PLUG>
+template <int TT, bool PLUG, bool TL>
 struct DmRun {
   const char* lds;
   DualLane lo;
@@ -154,29 +177,62 @@ struct DmRun {
   const f16* xblk;
   int n0, n, j0, q, ke;
   bool ok;
-  uint32_t voc;
+  uint32_t voc, vos;
   uint32_t vox[TT];
+  char* tw;                // TL: the wave's transpose area
+  uint32_t twr, twa;       // TL: the lane's write offset (row k, first of its 8 columns), read offset
   int64_t rowpos;
   DmPlug P;
   df4 C[2][TT];
 
   // Consume the step at k0 from cur while the step at k0 + 32 loads into nxt.
   __device__ __forceinline__ void step(const DmStage<TT>& cur, DmStage<TT>& nxt, int k0) {
-    dm_issue<TT>(A, n0, n, ok, q, k0 + 32, ke, voc, vox, xblk, j0, nxt);
-    float amp[8];
-    float2 cs[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float an;
-      dual_lookup1(lds, cur.c[e] & 0xFFFFu, lo, an, cs[e]);
-      amp[e] = an * h2f(cur.sc[e]);
-    }
-    if constexpr (PLUG) dplug_patch(A, P, rowpos, k0 + 8 * q, k0, amp);
+    dm_issue<TT, TL>(A, n0, n, ok, q, k0 + 32, ke, voc, vos, vox, xblk, j0, nxt);
     dh8 a0, a1;
+    if constexpr (TL) {
+      const float sc = h2f(cur.sq);
+      const uint32_t w4[4] = {cur.cq.x, cur.cq.y, cur.cq.z, cur.cq.w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      a0[e] = (_Float16)(amp[e] * cs[e].x);
-      a1[e] = (_Float16)(amp[e] * cs[e].y);
+      for (int e = 0; e < 4; ++e) {
+        float an[2];
+        float2 cs[2];
+        dual_lookup2<PP_DUAL_I16_OFFSET>(lds, w4[e], lo, an, cs);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float amp = an[h] * sc;
+          // the weights are rounded as the reference rounds them, the float32 product then
+          // fp16: the products are hidden from the compiler, which would otherwise fold
+          // product and conversion into one mixed-precision multiply that rounds once
+          float w1 = amp * cs[h].x, w2 = amp * cs[h].y;
+          asm volatile("" : "+v"(w1), "+v"(w2));
+          const uint32_t o = twr + (2 * e + h) * DM_TROW;
+          *reinterpret_cast<_Float16*>(tw + o) = (_Float16)w1;
+          *reinterpret_cast<_Float16*>(tw + DM_TMODEL + o) = (_Float16)w2;
+        }
+      }
+      // the reads below take values other lanes wrote: wait until the writes are done
+      // (lgkmcnt(0); vmcnt and expcnt left at their maxima, so the loads in flight are not
+      // waited for)
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_wave_barrier();
+      a0 = *reinterpret_cast<const dh8*>(tw + twa);
+      a1 = *reinterpret_cast<const dh8*>(tw + DM_TMODEL + twa);
+      __builtin_amdgcn_wave_barrier();
+    } else {
+      float amp[8];
+      float2 cs[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float an;
+        dual_lookup1(lds, cur.c[e] & 0xFFFFu, lo, an, cs[e]);
+        amp[e] = an * h2f(cur.sc[e]);
+      }
+      if constexpr (PLUG) dplug_patch(A, P, rowpos, k0 + 8 * q, k0, amp);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a0[e] = (_Float16)(amp[e] * cs[e].x);
+        a1[e] = (_Float16)(amp[e] * cs[e].y);
+      }
     }
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
@@ -187,8 +243,8 @@ struct DmRun {
   }
 };
 
-template <int TT, bool PLUG>
-__device__ __forceinline__ void dm_body(const char* lds, const DualMfmaArgs& A) {
+template <int TT, bool PLUG, bool TL>
+__device__ __forceinline__ void dm_body(char* lds, const DualMfmaArgs& A) {
   const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
   const DualLane lo = dual_lane(lane);
   int b = blockIdx.x;
@@ -207,8 +263,18 @@ __device__ __forceinline__ void dm_body(const char* lds, const DualMfmaArgs& A) 
     const int kb = sl * A.ks, ke = min(A.K, kb + A.ks);
     const int n = n0 + i;
     const bool ok = n < A.N;
-    DmRun<TT, PLUG> R{lds, lo, A, A.x + (int64_t)j0 * A.x_sm, n0, n, j0, q, ke, ok};
-    R.voc = ok ? 2u * (uint32_t)(8 * q * A.ldk + i) : OOB;
+    DmRun<TT, PLUG, TL> R{lds, lo, A, A.x + (int64_t)j0 * A.x_sm, n0, n, j0, q, ke, ok};
+    if constexpr (TL) {
+      // lane l: row k0 + l/2 of the step, columns n0 + 8(l%2) .. +7 (N % 16 == 0: all in range)
+      const int kr = lane >> 1, nh = 8 * (lane & 1);
+      R.voc = 2u * (uint32_t)(kr * A.ldk + nh);
+      R.vos = 2u * (uint32_t)(kr * A.gcols + ((n0 + nh) >> A.log2gs));
+      R.tw = lds + DLDS_BYTES + uniform(threadIdx.x >> 6) * DM_TWAVE;
+      R.twr = (uint32_t)(nh * DM_TROW + 2 * kr);
+      R.twa = (uint32_t)(i * DM_TROW + 16 * q);
+    } else {
+      R.voc = ok ? 2u * (uint32_t)(8 * q * A.ldk + i) : OOB;
+    }
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
       const int jl = 16 * t + i;
@@ -225,7 +291,7 @@ __device__ __forceinline__ void dm_body(const char* lds, const DualMfmaArgs& A) 
 #pragma unroll
       for (int t = 0; t < TT; ++t) R.C[m][t] = df4{0.f, 0.f, 0.f, 0.f};
     DmStage<TT> S0, S1;
-    dm_issue<TT>(A, n0, n, ok, q, kb, ke, R.voc, R.vox, R.xblk, j0, S0);
+    dm_issue<TT, TL>(A, n0, n, ok, q, kb, ke, R.voc, R.vos, R.vox, R.xblk, j0, S0);
     for (int k0 = kb; k0 < ke; k0 += 64) {
       R.step(S0, S1, k0);
       R.step(S1, S0, k0 + 32);
@@ -263,11 +329,20 @@ __device__ __forceinline__ void dm_body(const char* lds, const DualMfmaArgs& A) 
 template <int TT>
 __global__ __launch_bounds__(DM_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void dual_mfma_kernel(
     const DualMfmaArgs A) {
-  __shared__ __attribute__((aligned(16))) char T[DLDS_BYTES];
+  __shared__ __attribute__((aligned(16))) char T[DM_LDS_BYTES];
   if (A.luts.dtype == PP_F16) dual_tables_of<DM_NT, PP_DUAL_I16_OFFSET, f16>(T, A.luts);
   else dual_tables_of<DM_NT, PP_DUAL_I16_OFFSET, float>(T, A.luts);
-  if (A.plug_n > 0) dm_body<TT, true>(T, A);
-  else dm_body<TT, false>(T, A);
+  // transposing loads for 2 token tiles (up to 32 tokens): 33.0-33.4 against 35.2-36.7 us
+  // on the 4096 x 4096 layer at 8 tokens; with 4 tiles they measured slower (47 -> 51 us
+  // at 64 tokens), the LDS round trip no longer hidden behind the products
+  if constexpr (TT == 2) {
+    if (A.gcols > 0) {
+      dm_body<TT, false, true>(T, A);
+      return;
+    }
+  }
+  if (A.plug_n > 0) dm_body<TT, true, false>(T, A);
+  else dm_body<TT, false, false>(T, A);
 }
 
 // Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero (after the item kernel
@@ -377,6 +452,10 @@ extern "C" int pp_dual_mfma(const void* codes, int64_t ldk, const void* a, int64
   int lg = 0;
   while ((1ll << lg) < group_size) ++lg;
   A.log2gs = lg;
+  A.gcols = plug_n == 0 && N % 16 == 0 && group_size >= 8 && N % group_size == 0 && ldk % 8 == 0 &&
+                    aligned(codes, 16)
+                ? (int)(N / group_size)
+                : 0;
   A.luts.amp = amp_lut;
   A.luts.cs[0] = cos_lut;
   A.luts.cs[1] = sin_lut;

@@ -42,12 +42,14 @@ def to_dev(*arrs):
 
 @pytest.mark.parametrize("M", [9, 16, 32, 33, 64, 65, 128, 200])
 @pytest.mark.parametrize("K,N,plug,gs", [(1024, 384, 0, 32), (2048, 1000, 500, 32), (512, 4096, 300, 64),
-                                         (96, 40, 40, 8)])
+                                         (96, 40, 40, 8), (256, 512, 0, 64), (512, 400, 0, 32), (128, 64, 0, 8)])
 def test_kernel_layout_matches_oracle(K, N, plug, gs, M):
     """Several shapes (N not a multiple of 16, K = 96: one padded step), group sizes 8-64,
     plug amplitudes at random positions, 9-200 tokens (16-token tiles of 2, 4 or 8; one to
     two token blocks; K slices for the small batches), forced with fused=True above the
-    operator's default range."""
+    operator's default range.  Without plug entries and with N a multiple of 16 and of the
+    group size the kernel loads rows of 8 codes and transposes them through LDS (N = 400
+    with 32-pair groups takes the column loads)."""
     seed = K * 3 + N + plug + M + gs
     packed, bmax, amp_lut, cos_lut, sin_lut = layer(K, N, seed, gs)
     rng = np.random.default_rng(seed)
@@ -91,6 +93,24 @@ def test_wider_row_stride_and_float32_luts(M):
     blk = (pos % ldk) < N
     pl = (pos[blk] // ldk, pos[blk] % ldk, vals[blk])
     check((o1, o2), a, packed_w[:, :N], bmax, *luts32, 32, pl, f"ldk={ldk} M={M}")
+
+
+@pytest.mark.parametrize("M", [20, 70])
+def test_wider_row_stride_row_loads(M):
+    """No plug table, codes as a column slice of a wider tensor (row stride 536 > N = 320):
+    the row loads read the block's 320 columns of each row only."""
+    K, N, ldk = 256, 320, 536
+    seed = 500 + M
+    packed_w, _, amp_lut, cos_lut, sin_lut = layer(K, ldk, seed)
+    rng = np.random.default_rng(seed)
+    bmax = (rng.random((K * N + 31) // 32) * 0.5 + 0.05).astype(np.float16)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    view = torch.from_numpy(packed_w).to(DEV)[:, :N]
+    assert view.stride(0) == ldk
+    o1, o2 = pk.polar_dual_bitpacked(torch.from_numpy(a).to(DEV), view, torch.from_numpy(bmax).to(DEV),
+                                     *[torch.from_numpy(np.asarray(l)).to(DEV) for l in (amp_lut, cos_lut, sin_lut)],
+                                     fused=True)
+    check((o1, o2), a, packed_w[:, :N], bmax, amp_lut, cos_lut, sin_lut, 32, None, f"ldk={ldk} M={M}")
 
 
 @pytest.mark.parametrize("M,fused", [(40, False), (300, True)])
