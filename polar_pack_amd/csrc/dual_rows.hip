@@ -143,8 +143,11 @@ __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const Dual
   const int64_t end = (int64_t)(S.nrows - 1) * S.ldc + S.K;
   const rsrc_t rc = make_rsrc(S.codes + first, 2u * (uint32_t)(end - first));
   const rsrc_t rs = make_rsrc(A.scales, 2u * (uint32_t)A.n_groups);
+  // lanes past the row end read nothing: those codes start the next row, whose own first
+  // chunk reads them (38 MB of the 3B-shaped stream's 11008-pair rows, read twice otherwise)
+  const bool in_row = 8 * lane < S.K - kc;
 #pragma unroll
-  for (int r = 0; r < RG; ++r) vload128(c.q[r], voff[r], rc);
+  for (int r = 0; r < RG; ++r) vload128(c.q[r], in_row ? voff[r] : OOB, rc);
   const int k = kc + 8 * lane;
   const int64_t base = S.pos0 + first;   // stream position of (row, kc): uniform
   if constexpr (SM == 2) {
