@@ -126,10 +126,12 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
     of the element at storage offset ``idx - elem_base`` of ``codes``; ``idx`` must be
     strictly ascending, as a ``.quadpack`` file stores it (quaternion_packer.py:104-113):
     checked on the host when ``POLAR_PACK_CHECK_PLUG=1``.
-    ``fused`` (batches above 64 tokens on (N,K) or (K,N) storage, and 9-64 tokens on (K,N)
-    storage): True runs the fused large-batch kernel at any size, False decodes fp16
-    weights and runs a library GEMM above 64 tokens (and transposes (K,N) codes for the
-    matrix-core batch decode at 9-64), None (default) picks by size (the fused kernel up to
+    ``fused`` (batches above 64 tokens on (N,K) or (K,N) storage, and up to 64 tokens on
+    (K,N) storage): True runs the fused matrix-core kernel at any size (K % 32 == 0), False decodes
+    fp16 weights and runs a library GEMM above 64 tokens (and transposes (K,N) codes for the
+    matrix-core batch decode at 9-64, and keeps the fused row kernel up to 8), None (default)
+    picks by size (on (K,N) storage the fused kernel from 2 or 3 tokens, see
+    ``_kn_big_min_m``, the row kernel with plug entries up to 8; the fused kernel up to
     BIG_MAX_M tokens, where it is the faster; above, the decode + GEMM, which needs 8 bytes
     of scratch per code word).
     """
@@ -153,11 +155,14 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
     pi, pv, pn, keep = _plug_args(plug, dev)
     L = nat.lib()
     kn = _kn_layout_ok(codes, K, N)
-    lay = _big_layout(codes, K, N) if M > 8 else None
-    # the fused large-batch kernel: above 64 tokens on either storage; from 9 tokens on
-    # (K,N) storage, which the matrix-core batch decode would first have to transpose
-    if lay is not None and (M > BIG_MIN_M or (lay == nat.PP_QUAD_KN and fused is not False)) \
-            and (fused or (fused is None and M <= BIG_MAX_M)):
+    lay = _big_layout(codes, K, N) if M > 8 or fused or (M > 1 and pn == 0) else None
+    if lay == nat.PP_QUAD_NK and M <= 8:
+        lay = None
+    # the fused large-batch kernel: above 64 tokens on either storage; on (K,N) storage from
+    # 9 tokens (the matrix-core batch decode would first have to transpose it), and from
+    # 2 or 3 tokens without plug entries (_kn_big_min_m)
+    kn_big = lay == nat.PP_QUAD_KN and (fused or (fused is None and (M > 8 or M >= _kn_big_min_m(K, N))))
+    if lay is not None and (M > BIG_MIN_M or kn_big) and (fused or (fused is None and M <= BIG_MAX_M)):
         _quad_big(a, codes, lay, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
         del keep
         return outs
@@ -191,6 +196,17 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
     nat.check(rc, "pp_quad_gemm")
     del keep
     return outs
+
+
+def _kn_big_min_m(K, N):
+    """Fewest tokens from which (K,N) codes without plug entries take the fused matrix-core
+    kernel instead of the fused (K,N) row kernel (graph-replayed, measured: at 2 / 4 / 8
+    tokens 4096x4096 27.4 / 27.4 / 27.4 against 29.6 / 36.6 / 45.5 us, K x N = 11008x2048
+    32.4 / 32.5 / 32.3 against 34.4 / 42.2 / 53.9 us, 2048x11008 38.4 / 40.6 / 40.7 against
+    33.9 / 41.9 / 56.3 us; at 1 token the row kernel is the faster: 23.3 against 27.6 us on
+    4096x4096).  With plug entries the row kernel keeps up to 8 tokens: the matrix-core kernel
+    would move them to its (N,K) frame on every call."""
+    return 2 if N <= K else 3
 
 
 BIG_MIN_M = 64    # larger batches on (N,K) or (K,N) storage run the fused large-batch kernel ...

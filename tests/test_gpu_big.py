@@ -207,6 +207,42 @@ def test_kn_default_route_small_batches(M):
     check_mfma(outs, ref, f"kn default M={M}")
 
 
+@pytest.mark.parametrize("M,N,plug,fused,big", [(2, 388, False, None, True), (2, 600, False, None, False),
+                                                (3, 600, False, None, True), (5, 388, False, None, True),
+                                                (8, 1000, False, None, True), (4, 388, True, None, False),
+                                                (1, 388, False, True, True), (4, 388, True, True, True)])
+def test_kn_few_tokens_route(monkeypatch, M, N, plug, fused, big):
+    """2-8 tokens on (K,N) storage without plug entries take the fused matrix-core kernel by
+    default (from 2 tokens when N <= K, from 3 when N > K), with plug entries the fused row
+    kernel; fused=True takes the matrix-core kernel at 1 token and with plug entries.  The
+    route taken is recorded; the matrix cores are held to their fp16-operand bound, the row
+    kernel to the float32 decode's bound."""
+    K = 512
+    seed = 970 + 10 * M + N
+    codes = random_codes((K, N), seed)
+    luts, scales = fp16_luts(seed)
+    rng = np.random.default_rng(seed)
+    flat = np.sort(rng.choice(K * N, 250, replace=False)) if plug else None
+    vals = (rng.standard_normal((250, 4)) * 0.5).astype(np.float16) if plug else None
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    taken = []
+    real = qk._quad_big
+    monkeypatch.setattr(qk, "_quad_big", lambda *args: taken.append(1) or real(*args))
+    pl = (u32(flat.astype(np.uint32)).to(DEV), torch.from_numpy(vals).to(DEV)) if plug else None
+    outs = qk.quad_bitpacked(torch.from_numpy(a).to(DEV), u32(codes).to(DEV), [l.to(DEV) for l in luts], scales,
+                             plug=pl, fused=fused)
+    assert bool(taken) == big
+    if big:
+        ref = kn_mfma_reference(a, codes, luts, scales, (flat // N, flat % N) if plug else None, vals)
+        check_mfma(outs, ref, f"kn M={M} N={N}")
+        return
+    W = olay.quad_dequant(codes, [l.float().numpy() for l in luts], scales)
+    for m in range(4):
+        if plug:
+            W[m][flat // N, flat % N] = vals[:, m].astype(np.float64) * scales[m]
+        assert_gemv_close(outs[m].float().cpu().numpy(), a.astype(np.float64) @ W[m], f"model {m}")
+
+
 @pytest.mark.parametrize("M,fused", [(40, False), (100, False), (300, None)])
 def test_kn_decode_and_batched_gemm_route(M, fused):
     """(K,N) storage through the fp16 decode + one batched library GEMM (the default above

@@ -120,9 +120,9 @@ def test_quad_gemm_matches_oracle(K, N, layout, M):
     # product (as the reference's tl.dot); held to the fp16-rounded decode + the fp32
     # dot-product bound (see test_gpu_mfma.py)
     kn_ok = layout == "kn" and N % 4 == 0 and K % 8 == 0
-    # matrix cores: (N,K) rows, or (K,N) storage transposed for them
-    kn_mfma_max = qk.KN_MFMA_MAX_M if N > K else qk.PREFILL_M
-    mfma = M > 8 and K % 32 == 0 and (layout == "nk" or (kn_ok and M <= kn_mfma_max))
+    # matrix cores: (N,K) rows above 8 tokens; (K,N) storage (no plug entries here) from
+    # 2 or 3 tokens, in the fused matrix-core kernel (any column count)
+    mfma = K % 32 == 0 and ((layout == "nk" and M > 8) or (layout == "kn" and M >= qk._kn_big_min_m(K, N)))
     kn = kn_ok and M <= qk.KN_MAX_M and not mfma                          # fused (K,N) passes
     prefill = M > 8 and not mfma and not kn      # fp16 decode + library GEMM
     W32 = olay.quad_dequant(codes, [l.float().numpy() for l in luts], dtype=np.float32) if mfma else None
@@ -232,10 +232,12 @@ def test_pack_quad_layer_on_gpu_matches_oracle():
         np.testing.assert_array_equal(luts[i].cpu().numpy().view(np.uint16), rl[i].view(np.uint16))
 
 
-def kn_route(K, N, M):
+def kn_route(K, N, M, plug):
     """Which kernel quad_bitpacked runs for contiguous (K,N) codes: 'fused' (the (K,N)
-    decode kernel), 'mfma' (codes transposed for the matrix cores, or the fused large-batch
-    kernel at 65-128 tokens) or 'prefill' (fp16 decode + library GEMM)."""
+    decode kernel), 'mfma' (the fused matrix-core kernel: 9-128 tokens, and from 2 or 3
+    tokens without plug entries) or 'prefill' (fp16 decode + library GEMM)."""
+    if K % 32 == 0 and not plug and qk._kn_big_min_m(K, N) <= M <= 8:
+        return "mfma"
     if M <= 8 or (K % 32 != 0 and M <= qk.KN_MAX_M):
         return "fused"
     if K % 32 == 0 and M <= qk.BIG_MAX_M:
@@ -291,7 +293,7 @@ def test_quad_gemm_kn_layout_fast_path(K, N, plug, M):
     if plug:
         kw = dict(plug=(u32(flat + base).to(DEV), torch.from_numpy(vals).to(DEV)), elem_base=base)
     outs = qk.quad_bitpacked(a.to(DEV), u32(codes).to(DEV), [l.to(DEV) for l in luts], scales, **kw)
-    check_route(outs, a, codes, luts, scales, kn_route(K, N, M), (flat // N, flat % N), vals, f"M={M}")
+    check_route(outs, a, codes, luts, scales, kn_route(K, N, M, plug), (flat // N, flat % N), vals, f"M={M}")
 
 
 @pytest.mark.parametrize("M", [4, 40, 200])
@@ -320,7 +322,7 @@ def test_quad_gemm_kn_layout_wider_row_stride(M):
                              plug=(u32((pos + base).astype(np.uint32)).to(DEV), torch.from_numpy(vals).to(DEV)),
                              elem_base=base)
     in_block = (pos % ldk) < N
-    check_route(outs, a, wide[:, :N], luts, scales, kn_route(K, N, M), (pos[in_block] // ldk, pos[in_block] % ldk),
+    check_route(outs, a, wide[:, :N], luts, scales, kn_route(K, N, M, True), (pos[in_block] // ldk, pos[in_block] % ldk),
                 vals[in_block], f"ldk={ldk} M={M}")
 
 
@@ -350,7 +352,7 @@ def test_quad_split_tables_every_route(layout, M):
         view = u32(codes).to(DEV)
         idx = flat
         at = (flat // N, flat % N)
-        route = kn_route(K, N, M)
+        route = kn_route(K, N, M, True)
     else:
         view = u32(np.ascontiguousarray(codes.T)).to(DEV).t()
         nn, kk = flat // K, flat % K          # storage offsets of (N,K) rows
