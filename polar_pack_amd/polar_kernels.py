@@ -105,10 +105,11 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
                          plug=None, elem_base=0, layout="i16", chunk_size=0, fused=None):
     """2 GEMMs from one packed pass (polar_kernels.py:98-115); returns ``(out1, out2)`` fp16 (M,N).
 
-    ``fused`` (more than 4 tokens on the int16 (K,N) layout, K % 32 == 0): True runs the
-    matrix-core decode at any size, False the fused (K,N) kernel up to 8 tokens and the fp16
-    decode + library GEMM above, None (default) the matrix cores up to DUAL_MFMA_MAX_M
-    tokens."""
+    ``fused`` (the int16 (K,N) layout, K % 32 == 0): True runs the matrix-core decode at any
+    size, False the fused (K,N) kernel up to 8 tokens and the fp16 decode + library GEMM
+    above, None (default) the fused (K,N) kernel below ``_dual_mfma_min_m`` tokens (2 when
+    N <= K without plug entries, else 5) and the matrix cores from there up to
+    DUAL_MFMA_MAX_M tokens."""
     M, K = a_fp16.shape
     K_b, N = packed.shape
     assert K == K_b
@@ -136,8 +137,8 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
     kn = packed.stride(1) == 1 and packed.stride(0) >= N and packed.stride(0) % 8 == 0 and N % 8 == 0 \
         and K % 8 == 0 and chunk_size == 0 and group_size >= 8 and group_size & (group_size - 1) == 0 \
         and packed.data_ptr() % 16 == 0
-    if kn and M > DUAL_MFMA_MIN_M and K % 32 == 0 and layout == "i16" and fused is not False \
-            and (fused or M <= DUAL_MFMA_MAX_M):
+    if kn and K % 32 == 0 and layout == "i16" and fused is not False \
+            and (fused or _dual_mfma_min_m(K, N, pn) <= M <= DUAL_MFMA_MAX_M):
         _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, lut_dt, keep, pn,
                    int(elem_base), out1, out2, L, dev)
         del keep
@@ -179,10 +180,21 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
 
 FUSED_MAX_M = 4   # larger batches decode once and run a library GEMM
 KN_MAX_M = 8      # on the (K,N) kernel layout the fused kernel takes up to 8 tokens, ...
-DUAL_MFMA_MIN_M = 4    # ... but from 5 tokens (K % 32 == 0) the matrix-core decode (pp_dual_mfma)
-DUAL_MFMA_MAX_M = 64   # runs, up to 64 (4096x4096 layer, events: 8 tokens 35 against 49 us,
-# 32 tokens 41 against 43 us for two fp16 matmuls; from 96 tokens the fp16 decode + one
-# batched GEMM is faster: 52 against 66 us)
+DUAL_MFMA_MIN_M = 4    # ... but from 5 tokens (K % 32 == 0; earlier, see _dual_mfma_min_m) the
+DUAL_MFMA_MAX_M = 64   # matrix-core decode (pp_dual_mfma) runs, up to 64 (4096x4096 layer,
+# events: 8 tokens 35 against 49 us, 32 tokens 41 against 43 us for two fp16 matmuls; from
+# 96 tokens the fp16 decode + one batched GEMM is faster: 52 against 66 us)
+
+
+def _dual_mfma_min_m(K, N, pn):
+    """Fewest tokens from which int16 (K,N) codes take the matrix-core decode instead of the
+    fused (K,N) kernel: 2 when N <= K without plug entries (graph-replayed, measured at 2 / 3 /
+    4 tokens: 4096x4096 26.0 / 26.7 / 28.3 against 29.6 / 32.8 / 36.6 us, K x N = 11008x2048
+    30.2 / 31.5 / 32.1 against 33.8 / 37.9 / 40.6 us; at 1 token the fused kernel is the
+    faster, 21.8 against 25.2 us on 4096x4096), else 5 (2048x11008: 38.0 / 38.4 / 38.5
+    against 29.6 / 34.6 / 38.1 us; with plug entries the matrix-core decode moves them to
+    its frame on every call)."""
+    return 2 if N <= K and pn == 0 else DUAL_MFMA_MIN_M + 1
 
 
 def _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, lut_dt, keep, pn, elem_base,

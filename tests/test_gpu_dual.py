@@ -22,10 +22,13 @@ def kernel_layout_layer(K, N, seed, dtype=torch.float16):
     return olay.quantize_polar_bitpacked(w1, w2)
 
 
-def prefill_bound(a, w):
-    """More than 4 tokens: fp16 decode + library GEMM, weights rounded to fp16 as the
-    reference's kernel rounds them (polar_kernels.py:78-82)."""
-    return fp16_weight_bound(a, w) if a.shape[0] > pk.FUSED_MAX_M else None
+def prefill_bound(a, w, plug=0, kn=True):
+    """More than 4 tokens, or int16 (K,N) codes (``kn``) on the matrix cores (from 2 tokens
+    when N <= K without plug entries): weights rounded to fp16 as the reference's kernel
+    rounds them (polar_kernels.py:78-82)."""
+    (M, K), N = a.shape, w.shape[1]
+    mfma = kn and K % 32 == 0 and N % 8 == 0 and M >= pk._dual_mfma_min_m(K, N, plug)
+    return fp16_weight_bound(a, w) if M > pk.FUSED_MAX_M or mfma else None
 
 
 def to_dev(*arrs):
@@ -96,7 +99,8 @@ def test_polar_dual_bitpacked_container_stream(chunk, M):
         d1, d2 = odp.decode_pairs_f64(dp, base, base + N * K)
         for o, d in ((o1, d1), (o2, d2)):
             w = d.reshape(N, K).T
-            assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), f"base {base}", bound=prefill_bound(a, w))
+            assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), f"base {base}",
+                              bound=prefill_bound(a, w, kn=False))
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
@@ -144,7 +148,7 @@ def test_polar_dual_bitpacked_kn_fast_path(K, N, plug, M):
     for w, lut in ((W[0], cos_lut), (W[1], sin_lut)):
         w[kk, nn] = vals.astype(np.float64) * np.asarray(lut, np.float64)[ph[kk, nn]]
     for o, w in ((o1, W[0]), (o2, W[1])):
-        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), bound=prefill_bound(a, w))
+        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), bound=prefill_bound(a, w, plug))
 
 
 def test_polar_dual_bitpacked_kn_output_view():

@@ -1,5 +1,5 @@
-"""GPU parity of the dual matrix-core decode (pp_dual_mfma, 5-64 tokens by default on the
-int16 (K,N) layout quantize_polar_bitpacked returns) against the float64 oracle: the fp16
+"""GPU parity of the dual matrix-core decode (pp_dual_mfma, 2-64 tokens by default on the
+int16 (K,N) layout quantize_polar_bitpacked returns, from 5 when N > K or with plug entries) against the float64 oracle: the fp16
 operands the reference's tl.dot takes (the float32 decode (amp_lut * bmax) * cos/sin
 rounded once, plug amplitudes substituted, polar_kernels.py:60-82) within rel 1e-3 plus the
 float32 dot-product bound 2^-18 * sum |w x|, and normwise within 1e-3 of the exact decode."""
@@ -111,6 +111,37 @@ def test_wider_row_stride_row_loads(M):
                                      *[torch.from_numpy(np.asarray(l)).to(DEV) for l in (amp_lut, cos_lut, sin_lut)],
                                      fused=True)
     check((o1, o2), a, packed_w[:, :N], bmax, amp_lut, cos_lut, sin_lut, 32, None, f"ldk={ldk} M={M}")
+
+
+@pytest.mark.parametrize("M,K,N,plug,fused,mfma", [(2, 1024, 512, 0, None, True), (2, 512, 1024, 0, None, False),
+                                                   (4, 512, 1024, 0, None, False), (5, 512, 1024, 0, None, True),
+                                                   (3, 2048, 1000, 0, None, True), (4, 1024, 512, 300, None, False),
+                                                   (1, 1024, 512, 0, True, True), (3, 1024, 512, 300, True, True)])
+def test_few_tokens_route(monkeypatch, M, K, N, plug, fused, mfma):
+    """int16 (K,N) codes: the matrix-core decode from 2 tokens when N <= K without plug
+    entries, from 5 otherwise; fused=True at any size.  The route taken is recorded; the
+    matrix cores are held to their fp16-operand bound, the fused (K,N) kernel to the float32
+    decode's bound."""
+    seed = 40 * M + K + N + plug
+    packed, bmax, amp_lut, cos_lut, sin_lut = layer(K, N, seed)
+    rng = np.random.default_rng(seed)
+    base = 5
+    flat = np.sort(rng.choice(K * N, plug, replace=False)).astype(np.uint32)
+    vals = np.abs(rng.standard_normal(plug) * 0.05).astype(np.float16)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    kw = dict(plug=(u32(flat + base).to(DEV), torch.from_numpy(vals).to(DEV)), elem_base=base) if plug else {}
+    taken = []
+    real = pk._dual_mfma
+    monkeypatch.setattr(pk, "_dual_mfma", lambda *args: taken.append(1) or real(*args))
+    o1, o2 = pk.polar_dual_bitpacked(*to_dev(a, packed, bmax, amp_lut, cos_lut, sin_lut), fused=fused, **kw)
+    assert bool(taken) == mfma
+    pl = (flat // N, flat % N, vals) if plug else None
+    if mfma:
+        check((o1, o2), a, packed, bmax, amp_lut, cos_lut, sin_lut, 32, pl, f"K={K} N={N} M={M}")
+        return
+    W = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut, 32, plug=pl)
+    for o, w in zip((o1, o2), W):
+        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w))
 
 
 @pytest.mark.parametrize("M,fused", [(40, False), (300, True)])
