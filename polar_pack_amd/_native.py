@@ -142,6 +142,15 @@ def float_array(vals):
     return arr
 
 
+def raw_stream(dev) -> int:
+    """The HIP stream handle of ``dev``'s current torch stream (what
+    ``torch.cuda.current_stream(dev).cuda_stream`` returns, without building the stream
+    object: 0.2 against 1.9 us per call)."""
+    import torch
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
+
+
 # Zeroed workspaces of the kernels that take one zero on entry and leave it zero (the K-slice
 # accumulators of pp_quad_mfma, pp_quad_big, pp_dual_mfma): one per (device, stream), grown
 # on demand and reused by every call on that stream, since calls on one stream run in order.
@@ -157,10 +166,10 @@ def zero_workspace(dev, nbytes: int):
     import torch
     if nbytes <= 0:
         return None, None
-    stream = torch.cuda.current_stream(dev)
+    dev = torch.device(dev)
     if torch.cuda.is_current_stream_capturing():
         return torch.zeros(nbytes, dtype=torch.uint8, device=dev), None
-    key = (torch.device(dev).index, stream.cuda_stream)
+    key = (dev.index, raw_stream(dev))
     with _lock:
         ws = _zero_ws.get(key)
         if ws is None or ws.numel() < nbytes:

@@ -116,8 +116,7 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
     dev = _check_device(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut)
     if a_fp16.dtype != torch.float16 or bmax.dtype != torch.float16:
         raise TypeError("a and bmax must be float16")
-    out1 = torch.empty((M, N), dtype=torch.float16, device=dev)
-    out2 = torch.empty_like(out1)
+    out1, out2 = torch.empty((2, M, N), dtype=torch.float16, device=dev).unbind(0)
     if M == 0 or N == 0:
         return out1, out2
     if K == 0:
@@ -167,7 +166,7 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
                                              packed.stride(0), packed.stride(1), group_size, chunk_size,
                                              int(elem_base), pn, M, N, K)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = nat.raw_stream(dev)
     rc = L.pp_dual_gemm(a.data_ptr(), a.stride(0), a.stride(1), packed.data_ptr(), lay, packed.stride(0),
                         packed.stride(1), bmax.data_ptr(), group_size, chunk_size, amp_lut.data_ptr(),
                         amp_lut.numel(), cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases, lut_dt, pi, pa, pn,
@@ -225,7 +224,7 @@ def _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_siz
         row_plug = torch.searchsorted(pos, keys)
     ws_bytes = L.pp_dual_mfma_workspace_size(M, N, slices)
     ws, wkey = nat.zero_workspace(dev, ws_bytes)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = nat.raw_stream(dev)
     rc = L.pp_dual_mfma(packed.data_ptr(), ldk, a.data_ptr(), a.stride(0), bmax.data_ptr(), group_size,
                         amp_lut.data_ptr(), amp_lut.numel(), cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases,
                         lut_dt, keep[0].data_ptr() if pn else None, keep[1].data_ptr() if pn else None, pn,
@@ -263,7 +262,7 @@ def _dequant_into(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_siz
     lay = _codes_view(packed, layout)
     lut_dt = _lut_dtype(amp_lut, cos_lut, sin_lut)
     pi, pa, pn, keep = _dual_plug(plug, dev)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = nat.raw_stream(dev)
     fn = nat.lib().pp_dual_dequant if w1.dtype == torch.float32 else nat.lib().pp_dual_dequant_f16
     rc = fn(packed.data_ptr(), lay, packed.stride(0), packed.stride(1), bmax.contiguous().data_ptr(), group_size,
             chunk_size, amp_lut.data_ptr(), amp_lut.numel(), cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases,
@@ -280,7 +279,7 @@ def _dequant_t_into(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_s
     lay = _codes_view(packed, layout)
     lut_dt = _lut_dtype(amp_lut, cos_lut, sin_lut)
     pi, pa, pn, keep = _dual_plug(plug, dev)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = nat.raw_stream(dev)
     rc = nat.lib().pp_dual_dequant_f16_t(packed.data_ptr(), lay, packed.stride(0), bmax.contiguous().data_ptr(),
                                          group_size, amp_lut.data_ptr(), amp_lut.numel(), cos_lut.data_ptr(),
                                          sin_lut.data_ptr(), num_phases, lut_dt, pi, pa, pn, int(elem_base),

@@ -143,7 +143,8 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
         raise TypeError("a must be float16")
     if codes.dtype not in (torch.uint32, torch.int32):
         raise TypeError("codes must be uint32")
-    outs = [torch.empty((M, N), dtype=torch.float16, device=dev) for _ in range(4)]
+    # the 4 outputs as slices of one allocation (one allocator call instead of 4)
+    outs = list(torch.empty((4, M, N), dtype=torch.float16, device=dev).unbind(0))
     if M == 0 or N == 0:
         return outs
     if K == 0:
@@ -188,7 +189,7 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
     ws_bytes = L.pp_quad_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), codes.data_ptr(),
                                              codes.stride(0), codes.stride(1), pn, M, N, K)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = nat.raw_stream(dev)
     rc = L.pp_quad_gemm(a.data_ptr(), a.stride(0), a.stride(1), codes.data_ptr(), codes.stride(0),
                         codes.stride(1), lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base),
                         nat.ptr_array([o.data_ptr() for o in outs]), outs[0].stride(0), outs[0].stride(1),
@@ -245,7 +246,7 @@ def _quad_kn_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, 
     K, N = codes.shape
     ldk = codes.stride(0)
     cnk = torch.empty((N, K), dtype=torch.int32, device=dev)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = nat.raw_stream(dev)
     nat.check(L.pp_quad_codes_nk(codes.data_ptr(), ldk, K, N, cnk.data_ptr(), stream), "pp_quad_codes_nk")
     view = cnk.view(torch.uint32).t()
     keep2, pn2 = (), 0
@@ -307,7 +308,7 @@ def _quad_big(a, codes, layout, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, ou
         row_plug = torch.searchsorted(idx, keys)
     ws_bytes = L.pp_quad_big_workspace_size(M, N, slices)
     ws, wkey = nat.zero_workspace(dev, ws_bytes)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = nat.raw_stream(dev)
     rc = L.pp_quad_big(codes.data_ptr(), layout, ldc, a.data_ptr(), a.stride(0), lut_ptrs, lut_dtype, sc,
                        keep[0].data_ptr() if pn else None, keep[1].data_ptr() if pn else None, pn,
                        row_plug.data_ptr() if row_plug is not None else None, pos0, pld, slices, cols,
@@ -332,7 +333,7 @@ def _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, elem_base, outs
     M, K = a.shape
     N = codes.shape[1]
     nk = codes.stride(0) == 1 and codes.stride(1) != 1
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = nat.raw_stream(dev)
     if not nk and codes.stride(1) == 1 and codes.stride(0) >= N and codes.stride(0) % 4 == 0 and N % 8 == 0 \
             and K % 8 == 0 and codes.data_ptr() % 16 == 0:
         w = torch.empty((4, N, K), dtype=torch.float16, device=dev)
@@ -379,7 +380,7 @@ def _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, 
         row_plug = torch.searchsorted(idx, keys)
     ws_bytes = L.pp_quad_mfma_workspace_size(M, N, slices)
     ws, wkey = nat.zero_workspace(dev, ws_bytes)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = nat.raw_stream(dev)
     rc = L.pp_quad_mfma(codes.data_ptr(), ldc, elem_base, a.data_ptr(), a.stride(0), lut_ptrs, lut_dtype, sc,
                         keep[0].data_ptr() if pn else None, keep[1].data_ptr() if pn else None, pn,
                         row_plug.data_ptr() if row_plug is not None else None, slices, cols,
@@ -404,7 +405,7 @@ def quad_dequant(codes, luts, scales, *, plug=None, elem_base=0, dtype=torch.flo
         return outs
     lut_ptrs, lut_dtype = _lut_args(luts)
     pi, pv, pn, keep = _plug_args(plug, dev)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = nat.raw_stream(dev)
     fn = nat.lib().pp_quad_dequant if dtype == torch.float32 else nat.lib().pp_quad_dequant_f16
     rc = fn(codes.data_ptr(), codes.stride(0), codes.stride(1), lut_ptrs, lut_dtype, nat.float_array(scales), pi, pv,
             pn, int(elem_base), nat.ptr_array([o.data_ptr() for o in outs]), N, K, stream)

@@ -375,7 +375,7 @@ class QuadStream:
         self.plug_code = torch.empty(max(P, 1), dtype=torch.int32, device=dev)
         if P:
             rc = L.pp_quad_plug_codes(pack.codes.data_ptr(), pack.n, pack.plug_idx.data_ptr(), P,
-                                      self.plug_code.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+                                      self.plug_code.data_ptr(), nat.raw_stream(dev))
             nat.check(rc, "pp_quad_plug_codes")
         self.projs = None
 
@@ -428,7 +428,7 @@ class QuadStream:
         if self.projs is None:
             raise RuntimeError("QuadStream.bind() must be called before launching")
         pk = self.pack
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = nat.raw_stream(self.device)
         rc = nat.lib().pp_quad_stream(self.projs.data_ptr(), len(self.shapes),
                                       self.segs.data_ptr() if self.n_segs else None, self.n_segs,
                                       self.bounds.data_ptr(), self.n_waves,
@@ -542,7 +542,7 @@ class DualStream:
                                       self.luts[0].data_ptr(), pack.plug_idx.data_ptr(), pack.plug_val.data_ptr(), P,
                                       self._proj_pos0.data_ptr(), self._proj_k.data_ptr(), len(self.shapes),
                                       self.rows_per_item, self.plug_ent.data_ptr(),
-                                      torch.cuda.current_stream(dev).cuda_stream)
+                                      nat.raw_stream(dev))
             nat.check(rc, "pp_dual_plug_table")
         gs, R = pack.group_size, self.rows_per_item
         fits = (pack.chunk_size % gs == 0 and len(self.shapes) > 0
@@ -562,7 +562,7 @@ class DualStream:
             rc = L.pp_dual_scale_table(pack.scales.data_ptr(), int(pack.scales.numel()), gs,
                                        self._tab_pos0.data_ptr(), self._tab_n.data_ptr(), self._tab_k.data_ptr(),
                                        len(self.shapes), R, self.scale_tab.data_ptr(), n_tab,
-                                       torch.cuda.current_stream(dev).cuda_stream)
+                                       nat.raw_stream(dev))
             nat.check(rc, "pp_dual_scale_table")
         self.projs = None
 
@@ -615,7 +615,7 @@ class DualStream:
         if self.projs is None:
             raise RuntimeError("DualStream.bind() must be called before launching")
         pk = self.pack
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = nat.raw_stream(self.device)
         amp, cos, sin = self.luts
         rc = nat.lib().pp_dual_stream(self.projs.data_ptr(), len(self.shapes),
                                       self.segs.data_ptr() if self.n_segs else None, self.n_segs,
@@ -727,7 +727,7 @@ class QuadBatch:
         if self.x is None:
             raise RuntimeError("QuadBatch.bind() must be called before launching")
         pk = self.pack
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = nat.raw_stream(self.device)
         rc = nat.lib().pp_quad_mfma(pk.codes.data_ptr() + 4 * self.pos0, self.K, self.pos0, self.x.data_ptr(),
                                     self.x.stride(0), self._lut_ptrs, nat.PP_F32, self._scales,
                                     pk.plug_idx.data_ptr() if pk.plug_idx.numel() else None,

@@ -268,6 +268,26 @@ def test_kn_decode_and_batched_gemm_route(M, fused):
         assert normwise(got, exact) <= 1e-3
 
 
+def test_raw_stream_is_torch_current_stream():
+    """The operators launch on torch's current stream: the handle they read is the one
+    torch reports, also inside a side-stream context, and outputs computed there match."""
+    assert nat.raw_stream(DEV) == torch.cuda.current_stream(DEV).cuda_stream
+    K, N, M = 512, 256, 4
+    codes = random_codes((K, N), 5)
+    luts, scales = fp16_luts(5)
+    a = torch.from_numpy(np.random.default_rng(5).standard_normal((M, K)).astype(np.float16)).to(DEV)
+    cd, ld = u32(codes).to(DEV), [l.to(DEV) for l in luts]
+    ref = qk.quad_bitpacked(a, cd, ld, scales)
+    s = torch.cuda.Stream(DEV)
+    s.wait_stream(torch.cuda.current_stream(DEV))
+    with torch.cuda.stream(s):
+        assert nat.raw_stream(DEV) == s.cuda_stream != torch.cuda.default_stream(DEV).cuda_stream
+        got = qk.quad_bitpacked(a, cd, ld, scales)
+    torch.cuda.current_stream(DEV).wait_stream(s)
+    for g, r in zip(got, ref):
+        assert torch.equal(g, r)
+
+
 def test_operator_workspace_reused_and_left_zero():
     """The drop-in operators keep one zeroed K-slice workspace per stream: repeated calls of
     different sizes (the buffer grows, then is reused) stay correct and leave it zero."""
