@@ -635,10 +635,10 @@ def cpu_single_quad(pack, N, K, M):
 
 
 def run_quad_single(args, dev, log, N, K, M, name, pack=None):
-    """Up to 8 tokens: the fused row decode (QuadStream of one projection); more: the
-    matrix-core batch decode (QuadBatch)."""
+    """Up to 4 tokens: the fused row decode (QuadStream of one projection); more: the
+    matrix-core batch decode (QuadBatch), as quad_bitpacked routes (N,K) rows."""
     pack = pack if pack is not None else quad_linear_pack(N, K, dev, seed_of(2, 0, 0))
-    make = QuadStream if M <= 8 else _batch_as_stream
+    make = QuadStream if M <= qk.ROWS_MAX_M else _batch_as_stream
     st0 = make(pack, [(N, K)], M=M)
     copies = max(2, -(-MALL_BYTES // st0.algorithmic_bytes()))
     sts = rotated_streams(make, pack, [(N, K)], M, copies, dev, quad=True)

@@ -176,7 +176,7 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
         _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base), outs, L, dev)
         del keep
         return outs
-    if M > 8 and not kn:
+    if (M > 8 or (M > ROWS_MAX_M and _mfma_layout_ok(codes, K))) and not kn:
         # the matrix-core path takes up to 64 tokens per launch: larger batches (the
         # reference's prefill sizes, quad_kernels.py:166-189) run in blocks of 64 rows
         for i0 in range(0, M, 64):
@@ -210,6 +210,10 @@ def _kn_big_min_m(K, N):
     return 2 if N <= K else 3
 
 
+ROWS_MAX_M = 4    # (N,K) storage: the row kernel up to this many tokens, the matrix-core batch
+# decode from 5 (K % 32 == 0; gate 11008x2048 / down 2048x11008 with 0.1 % plug entries, rotated
+# copies: 5 tokens 45.4 / 43.9 us against 66.1 / 80.0 us, 8 tokens 45.1 / 43.4 against 66.9 /
+# 79.7; 4 tokens 43.6 / 44.7 against 40.9 / 43.9)
 BIG_MIN_M = 64    # larger batches on (N,K) or (K,N) storage run the fused large-batch kernel ...
 BIG_MAX_M = 128   # ... up to this size by default; above, the fp16 decode + one library GEMM is
 # faster (4096x4096 layer, measured: fused 87.5 us at 128 tokens against 128 us for 4 fp16
@@ -362,7 +366,7 @@ def _mfma_layout_ok(codes, K):
 
 
 def _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
-    """More than 8 tokens: the matrix-core batch decode (pp_quad_mfma), plug starts per
+    """More than ROWS_MAX_M tokens on (N,K) rows: the matrix-core batch decode (pp_quad_mfma), plug starts per
     (row, K slice) found on the device with searchsorted (quaternion_packer.py:188-189)."""
     M, K = a.shape
     N = codes.shape[1]

@@ -120,9 +120,9 @@ def test_quad_gemm_matches_oracle(K, N, layout, M):
     # product (as the reference's tl.dot); held to the fp16-rounded decode + the fp32
     # dot-product bound (see test_gpu_mfma.py)
     kn_ok = layout == "kn" and N % 4 == 0 and K % 8 == 0
-    # matrix cores: (N,K) rows above 8 tokens; (K,N) storage (no plug entries here) from
+    # matrix cores: (N,K) rows above ROWS_MAX_M tokens; (K,N) storage (no plug entries here) from
     # 2 or 3 tokens, in the fused matrix-core kernel (any column count)
-    mfma = K % 32 == 0 and ((layout == "nk" and M > 8) or (layout == "kn" and M >= qk._kn_big_min_m(K, N)))
+    mfma = K % 32 == 0 and ((layout == "nk" and M > qk.ROWS_MAX_M) or (layout == "kn" and M >= qk._kn_big_min_m(K, N)))
     kn = kn_ok and M <= qk.KN_MAX_M and not mfma                          # fused (K,N) passes
     prefill = M > 8 and not mfma and not kn      # fp16 decode + library GEMM
     W32 = olay.quad_dequant(codes, [l.float().numpy() for l in luts], dtype=np.float32) if mfma else None
@@ -157,7 +157,9 @@ def test_quad_gemm_real_pack_with_plug_fast_path(M):
     W = oqp.unpack_quad_f64(qp, 0, N * K)                # float64, plug applied, times s_k
     for k in range(4):
         w = W[k].reshape(N, K).T
-        bound = fp16_weight_bound(a.numpy(), w) if M > qk.BIG_MAX_M else None   # fp16 decode + library GEMM
+        # fp16 weights into the product above ROWS_MAX_M tokens (matrix cores; the fp16 decode
+        # + library GEMM above BIG_MAX_M)
+        bound = fp16_weight_bound(a.numpy(), w) if M > qk.ROWS_MAX_M else None
         if bound is not None:
             assert normwise(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), w)) <= 1e-3
         assert_gemv_close(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), w), f"model {k}", bound=bound)
@@ -358,7 +360,7 @@ def test_quad_split_tables_every_route(layout, M):
         nn, kk = flat // K, flat % K          # storage offsets of (N,K) rows
         idx = flat
         at = (kk, nn)
-        route = "fused" if M <= 8 else "mfma"
+        route = "fused" if M <= qk.ROWS_MAX_M else "mfma"
     a = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
     L = [l.to(DEV) for l in luts]
     outs = qk.quad_bitpacked(a.to(DEV), view, L, scales, plug=(u32(idx).to(DEV), torch.from_numpy(vals).to(DEV)))
