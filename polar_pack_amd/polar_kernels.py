@@ -212,15 +212,14 @@ def _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_siz
         p = (keep[0].view(torch.int32).to(torch.int64) & 0xFFFFFFFF) - elem_base
         k, n = p // ldk, p % ldk
         ok = (p >= 0) & (k < K) & (n < N)
-        pos = (n * K + k)[ok]
-        order = torch.argsort(pos)
-        pos = pos[order]
-        amps = keep[1][ok][order].contiguous()
-        pn = int(pos.numel())
+        # entries outside the K x N block go to position N*K, past every column's search
+        # range: the entry count stays static (no wait on the device; graph-capturable)
+        pos, order = torch.sort(torch.where(ok, n * K + k, N * K))
+        amps = keep[1][order].contiguous()
         keep = (torch.where(pos >= 2 ** 31, pos - 2 ** 32, pos).to(torch.int32).contiguous(), amps)
         keys = (torch.arange(N, device=dev, dtype=torch.int64)[:, None] * K
                 + torch.arange(slices, device=dev, dtype=torch.int64)[None, :] * cols).reshape(-1)
-        keys = torch.cat([keys, torch.tensor([N * K], device=dev, dtype=torch.int64)])
+        keys = torch.cat([keys, keys.new_full((1,), N * K)])
         row_plug = torch.searchsorted(pos, keys)
     ws_bytes = L.pp_dual_mfma_workspace_size(M, N, slices)
     ws, wkey = nat.zero_workspace(dev, ws_bytes)

@@ -231,16 +231,16 @@ KN_MFMA_MAX_M = 64
 def transposed_plug(idx, vals, elem_base, ldk, K, N):
     """Plug entries of a (K,N) code tensor (row stride ``ldk``, positions relative to
     ``elem_base``) moved to its (N,K) transpose: position k*ldk + n becomes n*K + k, entries
-    outside the K x N block dropped, re-sorted (the matrix-core path searches them).
-    Returns (int32 tensor holding the uint32 positions, (P', 4) fp16 values)."""
+    outside the K x N block to N*K (past every row's search range, so the entry count stays
+    that of the input: no wait on the device, and the call can be captured in a graph),
+    re-sorted (the matrix-core path searches them).
+    Returns (int32 tensor holding the uint32 positions, (P, 4) fp16 values)."""
     p = (idx.view(torch.int32).to(torch.int64) & 0xFFFFFFFF) - elem_base
     k, n = p // ldk, p % ldk
     ok = (p >= 0) & (k < K) & (n < N)
-    pos = (n * K + k)[ok]
-    order = torch.argsort(pos)
-    pos = pos[order]
+    pos, order = torch.sort(torch.where(ok, n * K + k, N * K))
     return (torch.where(pos >= 2 ** 31, pos - 2 ** 32, pos).to(torch.int32).contiguous(),
-            vals.reshape(-1, 4)[ok][order].contiguous())
+            vals.reshape(-1, 4)[order].contiguous())
 
 
 def _quad_kn_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
@@ -308,7 +308,7 @@ def _quad_big(a, codes, layout, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, ou
         idx = keep[0].view(torch.int32).to(torch.int64) & 0xFFFFFFFF
         keys = (pos0 + torch.arange(N, device=dev, dtype=torch.int64)[:, None] * pld
                 + torch.arange(slices, device=dev, dtype=torch.int64)[None, :] * cols).reshape(-1)
-        keys = torch.cat([keys, torch.tensor([pos0 + N * pld], device=dev, dtype=torch.int64)])
+        keys = torch.cat([keys, keys.new_full((1,), pos0 + N * pld)])
         row_plug = torch.searchsorted(idx, keys)
     ws_bytes = L.pp_quad_big_workspace_size(M, N, slices)
     ws, wkey = nat.zero_workspace(dev, ws_bytes)
@@ -380,7 +380,7 @@ def _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, 
         idx = keep[0].view(torch.int32).to(torch.int64) & 0xFFFFFFFF
         keys = (elem_base + torch.arange(N, device=dev, dtype=torch.int64)[:, None] * ldc
                 + torch.arange(slices, device=dev, dtype=torch.int64)[None, :] * cols).reshape(-1)
-        keys = torch.cat([keys, torch.tensor([elem_base + N * ldc], device=dev, dtype=torch.int64)])
+        keys = torch.cat([keys, keys.new_full((1,), elem_base + N * ldc)])
         row_plug = torch.searchsorted(idx, keys)
     ws_bytes = L.pp_quad_mfma_workspace_size(M, N, slices)
     ws, wkey = nat.zero_workspace(dev, ws_bytes)

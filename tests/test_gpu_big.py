@@ -288,6 +288,55 @@ def test_raw_stream_is_torch_current_stream():
         assert torch.equal(g, r)
 
 
+def test_operators_with_plug_entries_in_a_graph():
+    """The drop-in operators with plug entries captured in a HIP graph: (N,K) rows on the batch
+    decode (8 tokens) and the fused kernel (100 tokens), (K,N) codes on the fused kernel (16
+    tokens, entries also in the columns past N, which the row stride holds), dual int16 (K,N)
+    codes on the matrix cores (8 tokens).  Every replay, with eager work and
+    synchronizations between them, matches the eager call to one fp16 ulp (K-slice sums
+    are added in any order)."""
+    from polar_pack_amd import polar_kernels as pk
+    rng = np.random.default_rng(31)
+    K, N, ldk = 512, 384, 400
+    luts, scales = fp16_luts(31)
+    L = [l.to(DEV) for l in luts]
+    wide = random_codes((K, ldk), 31)
+    nk = u32(np.ascontiguousarray(wide[:, :N].T)).to(DEV).t()
+    kn = u32(wide).to(DEV)[:, :N]
+    flat_nk = np.sort(rng.choice(K * N, 200, replace=False)).astype(np.uint32)
+    flat_kn = np.sort(rng.choice(K * ldk, 260, replace=False)).astype(np.uint32)
+    v_nk = torch.from_numpy((rng.standard_normal((200, 4)) * 0.5).astype(np.float16)).to(DEV)
+    v_kn = torch.from_numpy((rng.standard_normal((260, 4)) * 0.5).astype(np.float16)).to(DEV)
+    w1, w2 = (torch.from_numpy(w.reshape(K, N)).to(torch.float16) for w in gen.correlated_models(32, [K * N] * 2))
+    dl = [torch.from_numpy(np.ascontiguousarray(t)).to(DEV) for t in olay.quantize_polar_bitpacked(w1, w2)]
+    flat_d = np.sort(rng.choice(K * N, 150, replace=False)).astype(np.uint32)
+    amp_d = torch.from_numpy(np.abs(rng.standard_normal(150) * 0.05).astype(np.float16)).to(DEV)
+    xs = {M: torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).to(DEV) for M in (8, 16, 100)}
+    p_nk, p_kn, p_d = (u32(flat_nk).to(DEV), v_nk), (u32(flat_kn).to(DEV), v_kn), (u32(flat_d).to(DEV), amp_d)
+    calls = [
+        lambda: qk.quad_bitpacked(xs[8], nk, L, scales, plug=p_nk),
+        lambda: qk.quad_bitpacked(xs[100], nk, L, scales, plug=p_nk),
+        lambda: qk.quad_bitpacked(xs[16], kn, L, scales, plug=p_kn),
+        lambda: list(pk.polar_dual_bitpacked(xs[8], *dl, plug=p_d)),
+    ]
+    eager = [[o.clone() for o in c()] for c in calls]
+    for c in calls:                       # warm the workspace caches outside the capture
+        c()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        got = [c() for c in calls]
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for e, o in zip(eager, got):
+            for a, b in zip(e, o):
+                a32, b32 = a.float(), b.float()
+                lim = 2.0 ** -10 * a32.abs() + 2.0 ** -14 * a32.abs().max()     # one fp16 ulp
+                assert bool(((b32 - a32).abs() <= lim).all()), f"replay {rep}"
+        torch.randn(1 << 20, device=DEV).sum().item()     # eager work between the replays
+
+
 def test_operator_workspace_reused_and_left_zero():
     """The drop-in operators keep one zeroed K-slice workspace per stream: repeated calls of
     different sizes (the buffer grows, then is reused) stay correct and leave it zero."""
