@@ -321,6 +321,16 @@ int pp_quad_codes_nk(const uint32_t* codes, int64_t ldk, int64_t K, int64_t N, u
 int pp_quad_plug_codes(const uint32_t* codes, int64_t n_codes, const uint32_t* plug_idx, int64_t plug_n,
                        uint32_t* code, void* stream);
 
+/*
+ * Plug ranges of the matrix-core kernels (pp_quad_mfma, pp_quad_big, pp_dual_mfma):
+ * row_plug[r*slices + s] = the first j with plug_idx[j] >= pos0 + r*pld + s*cols, and
+ * row_plug[rows*slices] = the first j with plug_idx[j] >= pos0 + rows*pld (rows*slices + 1
+ * entries).  plug_idx ascending.  The search the reference's unpacker makes with
+ * torch.searchsorted (quaternion_packer.py:188-189), one launch for every key.
+ */
+int pp_plug_search(const uint32_t* plug_idx, int64_t plug_n, int64_t pos0, int64_t pld, int64_t rows,
+                   int64_t slices, int64_t cols, int64_t* row_plug, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Dual pack: 16-bit [amp 6 | phase 10] -> 2 models.                          */
 /* ------------------------------------------------------------------------ */

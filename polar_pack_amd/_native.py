@@ -77,6 +77,7 @@ EXPORTS = {
     "pp_quad_stream_waves": (i64, [i64]),
     "pp_quad_stream": (i32, [vp, i64, vp, i64, vp, i64, vp, vp, i64, vp, vp, vp, vp, vp, i64, i64, vp, vp, i64, vp]),
     "pp_quad_plug_codes": (i32, [vp, i64, vp, i64, vp, vp]),
+    "pp_plug_search": (i32, [vp, i64, i64, i64, i64, i64, i64, vp, vp]),
     "pp_quad_codes_nk": (i32, [vp, i64, i64, i64, vp, vp]),
     "pp_dual_stream_rows": (i32, [i64]),
     "pp_dual_stream_chunk": (i32, [i64]),
@@ -149,6 +150,18 @@ def raw_stream(dev) -> int:
     import torch
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     return torch._C._cuda_getCurrentRawStream(idx)
+
+
+def plug_search(idx, n: int, pos0: int, pld: int, rows: int, slices: int, cols: int, dev):
+    """int64 device tensor of rows*slices + 1 plug ranges (pp_plug_search): entry
+    r*slices + s is the first j with idx[j] >= pos0 + r*pld + s*cols, the last one the first
+    j with idx[j] >= pos0 + rows*pld; ``idx`` the ascending uint32 positions (int32 or
+    uint32 tensor), one launch."""
+    import torch
+    row_plug = torch.empty(rows * slices + 1, dtype=torch.int64, device=dev)
+    check(lib().pp_plug_search(idx.data_ptr(), n, pos0, pld, rows, slices, cols, row_plug.data_ptr(),
+                               raw_stream(dev)), "pp_plug_search")
+    return row_plug
 
 
 # Zeroed workspaces of the kernels that take one zero on entry and leave it zero (the K-slice

@@ -890,6 +890,40 @@ __global__ __launch_bounds__(256) void quad_plug_code_kernel(const uint32_t* cod
   code[j] = p < n_codes ? codes[p] : 0u;
 }
 
+// row_plug[r*slices + s] = first j with plug_idx[j] >= pos0 + r*pld + s*cols, and
+// row_plug[rows*slices] = first j with plug_idx[j] >= pos0 + rows*pld: one thread per key,
+// a binary search over the ascending uint32 positions.
+__global__ __launch_bounds__(256) void plug_search_kernel(const uint32_t* idx, int64_t n, int64_t pos0, int64_t pld,
+                                                          int64_t rows, int64_t slices, int64_t cols,
+                                                          int64_t* row_plug) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t nk = rows * slices;
+  if (i > nk) return;
+  const int64_t key = i == nk ? pos0 + rows * pld : pos0 + (i / slices) * pld + (i % slices) * cols;
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if ((int64_t)idx[mid] < key) lo = mid + 1;
+    else hi = mid;
+  }
+  row_plug[i] = lo;
+}
+
+extern "C" int pp_plug_search(const uint32_t* plug_idx, int64_t plug_n, int64_t pos0, int64_t pld, int64_t rows,
+                              int64_t slices, int64_t cols, int64_t* row_plug, void* stream) {
+  PP_REQUIRE(plug_n >= 0 && rows >= 0 && slices >= 1 && cols >= 0 && pld >= 0 && pos0 >= 0,
+             "bad sizes (plug_n=%lld rows=%lld slices=%lld)", (long long)plug_n, (long long)rows,
+             (long long)slices);
+  PP_REQUIRE(row_plug != nullptr && (plug_n == 0 || plug_idx != nullptr), "null pointer");
+  PP_REQUIRE(rows * slices < (1ll << 40), "too many keys");
+  const int64_t keys = rows * slices + 1;
+  hipLaunchKernelGGL(plug_search_kernel, dim3((unsigned)((keys + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), plug_idx, plug_n, pos0, pld, rows, slices, cols,
+                     row_plug);
+  PP_LAUNCH_CHECK();
+  return PP_OK;
+}
+
 extern "C" int pp_quad_plug_codes(const uint32_t* codes, int64_t n_codes, const uint32_t* plug_idx, int64_t plug_n,
                                   uint32_t* code, void* stream) {
   PP_REQUIRE(plug_n >= 0 && plug_n < (1ll << 31), "plug_n out of range");

@@ -200,7 +200,7 @@ def _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_siz
                out1, out2, L, dev):
     """More than 8 tokens on the int16 (K,N) layout: the matrix-core decode (pp_dual_mfma).
     Plug positions (k*ldk + n of the storage, relative to elem_base) move to the kernel's
-    (N,K) frame n*K + k and are located per (column, K slice) with searchsorted."""
+    (N,K) frame n*K + k and are located per (column, K slice) (pp_plug_search)."""
     M, K = a.shape
     N = packed.shape[1]
     ldk = packed.stride(0)
@@ -217,10 +217,7 @@ def _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_siz
         pos, order = torch.sort(torch.where(ok, n * K + k, N * K))
         amps = keep[1][order].contiguous()
         keep = (torch.where(pos >= 2 ** 31, pos - 2 ** 32, pos).to(torch.int32).contiguous(), amps)
-        keys = (torch.arange(N, device=dev, dtype=torch.int64)[:, None] * K
-                + torch.arange(slices, device=dev, dtype=torch.int64)[None, :] * cols).reshape(-1)
-        keys = torch.cat([keys, keys.new_full((1,), N * K)])
-        row_plug = torch.searchsorted(pos, keys)
+        row_plug = nat.plug_search(keep[0], pn, 0, K, N, slices, cols, dev)
     ws_bytes = L.pp_dual_mfma_workspace_size(M, N, slices)
     ws, wkey = nat.zero_workspace(dev, ws_bytes)
     stream = nat.raw_stream(dev)

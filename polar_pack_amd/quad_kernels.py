@@ -284,7 +284,7 @@ def _big_layout(codes, K, N):
 
 def _quad_big(a, codes, layout, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
     """More than 64 tokens on (N,K) or (K,N) storage, or 9-64 on (K,N): the fused decode
-    on the matrix cores (pp_quad_big).  Plug entries are located per (row, K slice) with searchsorted
+    on the matrix cores (pp_quad_big).  Plug entries are located per (row, K slice) (pp_plug_search)
     (quaternion_packer.py:188-189); on (K,N) storage they are first moved to the (N,K)
     frame the kernel reads them in."""
     M, K = a.shape
@@ -305,11 +305,7 @@ def _quad_big(a, codes, layout, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, ou
             pn = int(keep[0].numel())
     row_plug = None
     if pn:
-        idx = keep[0].view(torch.int32).to(torch.int64) & 0xFFFFFFFF
-        keys = (pos0 + torch.arange(N, device=dev, dtype=torch.int64)[:, None] * pld
-                + torch.arange(slices, device=dev, dtype=torch.int64)[None, :] * cols).reshape(-1)
-        keys = torch.cat([keys, keys.new_full((1,), pos0 + N * pld)])
-        row_plug = torch.searchsorted(idx, keys)
+        row_plug = nat.plug_search(keep[0], pn, pos0, pld, N, slices, cols, dev)
     ws_bytes = L.pp_quad_big_workspace_size(M, N, slices)
     ws, wkey = nat.zero_workspace(dev, ws_bytes)
     stream = nat.raw_stream(dev)
@@ -367,7 +363,7 @@ def _mfma_layout_ok(codes, K):
 
 def _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
     """More than ROWS_MAX_M tokens on (N,K) rows: the matrix-core batch decode (pp_quad_mfma), plug starts per
-    (row, K slice) found on the device with searchsorted (quaternion_packer.py:188-189)."""
+    (row, K slice) found on the device (pp_plug_search; quaternion_packer.py:188-189)."""
     M, K = a.shape
     N = codes.shape[1]
     ldc = codes.stride(1)
@@ -377,11 +373,7 @@ def _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, 
     slices, cols = mfma_slices(N, K, int(L.pp_quad_mfma_waves(M)))
     row_plug = None
     if pn:
-        idx = keep[0].view(torch.int32).to(torch.int64) & 0xFFFFFFFF
-        keys = (elem_base + torch.arange(N, device=dev, dtype=torch.int64)[:, None] * ldc
-                + torch.arange(slices, device=dev, dtype=torch.int64)[None, :] * cols).reshape(-1)
-        keys = torch.cat([keys, keys.new_full((1,), elem_base + N * ldc)])
-        row_plug = torch.searchsorted(idx, keys)
+        row_plug = nat.plug_search(keep[0], pn, elem_base, ldc, N, slices, cols, dev)
     ws_bytes = L.pp_quad_mfma_workspace_size(M, N, slices)
     ws, wkey = nat.zero_workspace(dev, ws_bytes)
     stream = nat.raw_stream(dev)

@@ -69,7 +69,8 @@ def test_header_luts_closed_form():
 
 def test_transposed_plug_positions():
     """Plug entries of a (K,N) tensor moved to its (N,K) transpose (the matrix-core route
-    for (K,N) storage): positions remapped, out-of-block entries dropped, re-sorted."""
+    for (K,N) storage): positions remapped, out-of-block entries moved to N*K (past every
+    row's range, so the count stays that of the input), re-sorted."""
     import torch
     from polar_pack_amd.quad_kernels import transposed_plug
     K, N, ldk, base = 6, 5, 8, 100
@@ -80,9 +81,12 @@ def test_transposed_plug_positions():
     got_pos, got_vals = transposed_plug(idx, torch.from_numpy(vals), base, ldk, K, N)
     keep = [(p, v) for p, v in zip(pos, vals) if p >= 0 and p // ldk < K and p % ldk < N]
     want = sorted(((p % ldk) * K + p // ldk, tuple(v)) for p, v in keep)
-    assert got_pos.dtype == torch.int32
-    np.testing.assert_array_equal(got_pos.numpy(), [w[0] for w in want])
-    np.testing.assert_array_equal(got_vals.numpy(), np.array([w[1] for w in want], np.float16).reshape(-1, 4))
+    assert got_pos.dtype == torch.int32 and got_pos.numel() == pos.size and got_vals.shape == (pos.size, 4)
+    n_in = len(want)
+    assert 0 < n_in < pos.size
+    np.testing.assert_array_equal(got_pos.numpy()[:n_in], [w[0] for w in want])
+    np.testing.assert_array_equal(got_pos.numpy()[n_in:], N * K)
+    np.testing.assert_array_equal(got_vals.numpy()[:n_in], np.array([w[1] for w in want], np.float16).reshape(-1, 4))
 
 
 def test_pack_quad_device_tails_and_threshold_rule_match_the_oracle():
