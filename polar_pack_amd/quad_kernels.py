@@ -11,11 +11,12 @@ Same names, arguments, return values and error behaviour as the reference
   quaternion_packer.py:187-193) and ``elem_base``.
 * :func:`quad_dequant` -- float32 (or fp16) weights of a code view.
 
-Batches: 1-8 tokens run on the fused decode kernels; 9-128 tokens on the matrix cores
-with K % 32 == 0: on an (N,K) block seen as (K,N) (the container layout) the batch decode
-to 64 tokens and the fused kernel above, on (K,N) storage the fused kernel on the codes
-as stored (two 8-token fused passes up to 16 tokens when K % 32 != 0); larger batches, and
-more tokens on other layouts, decode once into fp16 weights (the values the reference's
+Batches (K % 32 == 0 for the matrix cores): on an (N,K) block seen as (K,N) (the container
+layout) the row kernel to 4 tokens, the matrix-core batch decode at 5-64 and the fused
+matrix-core kernel at 65-128; on (K,N) storage the fused (K,N) row kernel at 1 token (and
+with plug entries up to 8) and the fused matrix-core kernel on the codes as stored from 2
+tokens (3 when N > K) to 128 (two 8-token row passes up to 16 tokens when K % 32 != 0);
+larger batches, and more tokens on other layouts, decode once into fp16 weights (the values the reference's
 kernel rounds its weights to, quad_kernels.py:117-126) and run a library fp16 GEMM
 (hipBLASLt through torch.matmul), where the matmul's compute, not the weight stream, bounds
 the time.
