@@ -58,6 +58,7 @@ sys.path.insert(0, ROOT)
 
 from polar_pack_amd import polar_kernels as pk  # noqa: E402
 from polar_pack_amd import quad_kernels as qk  # noqa: E402
+from polar_pack_amd import routes  # noqa: E402
 from polar_pack_amd.packer import pack_dual_device, pack_quad_device  # noqa: E402
 from polar_pack_amd.stream import DualStream, QuadBatch, QuadStream  # noqa: E402
 
@@ -638,7 +639,8 @@ def run_quad_single(args, dev, log, N, K, M, name, pack=None):
     """Up to 4 tokens: the fused row decode (QuadStream of one projection); more: the
     matrix-core batch decode (QuadBatch), as quad_bitpacked routes (N,K) rows."""
     pack = pack if pack is not None else quad_linear_pack(N, K, dev, seed_of(2, 0, 0))
-    make = QuadStream if M <= qk.ROWS_MAX_M else _batch_as_stream
+    caps = routes.quad_storage(1, K, 0, K, N, 1)            # (N,K) container rows, with plug entries
+    make = QuadStream if routes.quad_route(M, K, N, caps, True) == "rows" else _batch_as_stream
     st0 = make(pack, [(N, K)], M=M)
     copies = max(2, -(-MALL_BYTES // st0.algorithmic_bytes()))
     sts = rotated_streams(make, pack, [(N, K)], M, copies, dev, quad=True)
@@ -709,9 +711,9 @@ def run_refbench(args, dev, log):
                    "speedup_vs_fp16": round(tf / tq, 3), "packed_event_ms": round(ev * 1e3, 4),
                    "gbs_event": round(algo(M) / ev / 1e9, 1)}
             extra = ""
-            if name == "quad" and M > qk.BIG_MIN_M:
+            if name == "quad" and M > 64:
                 # the fused large-batch kernel at every size (the operator's default above
-                # BIG_MAX_M tokens is the fp16 decode + one batched GEMM)
+                # 128 tokens is the fp16 decode + one batched GEMM)
                 fz = lambda: qk.quad_bitpacked(a, codes, luts, scales, fused=True)
                 for o, r in zip(fz(), want):
                     d = (o.float() - r.float()).abs().max().item()

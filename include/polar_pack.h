@@ -96,6 +96,15 @@ int64_t pp_quad_gemm_workspace_size(const void* a, int64_t a_sm, int64_t a_sk,
                                     const uint32_t* codes, int64_t c_sk, int64_t c_sn,
                                     int64_t plug_n, int64_t M, int64_t N, int64_t K);
 
+/* The kernel pp_quad_gemm / pp_dual_gemm runs for these operands (no reference counterpart:
+ * the reference has one kernel per operator): PP_GEMM_ROWS (the fused row decode of (N,K)
+ * rows), PP_GEMM_KN (the fused decode of (K,N) rows with unit column stride), PP_GEMM_GENERIC
+ * (decode into the workspace, then a plain GEMV), 0 for an empty problem.  No device work;
+ * the Python operators' routing table is checked against it. */
+enum pp_gemm_kernel { PP_GEMM_ROWS = 1, PP_GEMM_KN = 2, PP_GEMM_GENERIC = 3 };
+int pp_quad_gemm_kernel(const void* a, int64_t a_sm, int64_t a_sk, const uint32_t* codes, int64_t c_sk,
+                        int64_t c_sn, int64_t M, int64_t N, int64_t K);
+
 /*
  * pp_quad_gemm without a workspace argument, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
@@ -371,6 +380,10 @@ int64_t pp_dual_gemm_workspace_size(const void* a, int64_t a_sm, int64_t a_sk,
                                     const void* codes, int64_t c_sk, int64_t c_sn,
                                     int64_t group_size, int64_t chunk_size, int64_t elem_base,
                                     int64_t plug_n, int64_t M, int64_t N, int64_t K);
+/* The kernel pp_dual_gemm runs for these operands (enum pp_gemm_kernel above). */
+int pp_dual_gemm_kernel(const void* a, int64_t a_sm, int64_t a_sk, const void* codes, int64_t c_sk,
+                        int64_t c_sn, int64_t group_size, int64_t chunk_size, int64_t elem_base,
+                        int64_t M, int64_t N, int64_t K);
 
 /*
  * Dual decode GEMM on the matrix cores for batches (used for 5-64 tokens): the

@@ -5,6 +5,7 @@ The product path has no fallback: if the library is missing or cannot load,
 """
 from __future__ import annotations
 
+import collections
 import ctypes as C
 import os
 import threading
@@ -15,6 +16,7 @@ PP_OK, PP_EINVAL, PP_EHIP, PP_ENOSUPPORT = 0, 1, 2, 3
 PP_F16, PP_F32 = 0, 1
 PP_DUAL_I16_OFFSET, PP_DUAL_U16_BE = 0, 1
 PP_QUAD_NK, PP_QUAD_KN = 0, 1
+PP_GEMM_ROWS, PP_GEMM_KN, PP_GEMM_GENERIC = 1, 2, 3
 PP_ITEM_TAIL = 1
 PP_ITEM_FP16 = 2
 
@@ -55,6 +57,8 @@ EXPORTS = {
     "pp_quad_gemm": (i32, [vp, i64, i64, vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64,
                            i64, i64, i64, vp, i64, vp]),
     "pp_quad_gemm_workspace_size": (i64, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64]),
+    "pp_quad_gemm_kernel": (i32, [vp, i64, i64, vp, i64, i64, i64, i64, i64]),
+    "pp_dual_gemm_kernel": (i32, [vp, i64, i64, vp, i64, i64, i64, i64, i64, i64, i64, i64]),
     "pp_quad_gemm_noalloc": (i32, [vp, i64, i64, vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64,
                                    i64, i64, i64, vp]),
     "pp_quad_dequant": (i32, [vp, i64, i64, vp, i32, vp, vp, vp, i64, i64, vp, i64, i64, vp]),
@@ -167,9 +171,12 @@ def plug_search(idx, n: int, pos0: int, pld: int, rows: int, slices: int, cols: 
 # Zeroed workspaces of the kernels that take one zero on entry and leave it zero (the K-slice
 # accumulators of pp_quad_mfma, pp_quad_big, pp_dual_mfma): one per (device, stream), grown
 # on demand and reused by every call on that stream, since calls on one stream run in order.
-# A call that fails drops its stream's buffer (it may not have been left zero).  Under
-# stream capture every call gets a fresh zeroed buffer, as the graph records it.
-_zero_ws = {}
+# At most ZERO_WS_STREAMS streams per device keep one (least recently used dropped first), so
+# callers that cycle through many streams do not pile up device memory; release_workspaces()
+# drops them all.  A call that fails drops its stream's buffer (it may not have been left
+# zero).  Under stream capture every call gets a fresh zeroed buffer, as the graph records it.
+ZERO_WS_STREAMS = 4
+_zero_ws = collections.OrderedDict()
 
 
 def zero_workspace(dev, nbytes: int):
@@ -188,6 +195,10 @@ def zero_workspace(dev, nbytes: int):
         if ws is None or ws.numel() < nbytes:
             ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
             _zero_ws[key] = ws
+        _zero_ws.move_to_end(key)
+        mine = [k for k in _zero_ws if k[0] == key[0]]
+        for k in mine[:max(0, len(mine) - ZERO_WS_STREAMS)]:
+            del _zero_ws[k]
     return ws, key
 
 
@@ -195,3 +206,10 @@ def drop_workspace(key) -> None:
     if key is not None:
         with _lock:
             _zero_ws.pop(key, None)
+
+
+def release_workspaces() -> None:
+    """Drop every cached K-slice workspace (their memory returns to torch's caching
+    allocator once the calls that used them have completed on their streams)."""
+    with _lock:
+        _zero_ws.clear()

@@ -52,6 +52,13 @@ def _read_array(f, dtype, count, chunk_bytes=1 << 28) -> np.ndarray:
     return out
 
 
+
+def check_ascending(idx: np.ndarray) -> None:
+    """Raise ValueError unless the plug positions are strictly ascending, as both containers
+    store them (quaternion_packer.py:104-113, polar_bitpack.py:154-157)."""
+    if idx.size > 1 and not bool(np.all(idx[1:].astype(np.int64) > idx[:-1].astype(np.int64))):
+        raise ValueError("plug positions must be strictly ascending (as .quadpack / .dualpack files store them)")
+
 @dataclass
 class QuadPackFile:
     """A ``.quadpack`` v2 file's contents (host arrays)."""
@@ -123,14 +130,20 @@ class QuadPackDevice:
     plug_vals: torch.Tensor      # float16 (P, 4)
     tails: List[torch.Tensor]
     plug_idx_host: Optional[np.ndarray] = None
+    plug_checked: bool = False
 
     @property
     def tail_lengths(self):
         return [int(t.numel()) for t in self.tails]
 
     def plug_host(self) -> np.ndarray:
+        """Host copy of the plug positions, checked strictly ascending once (the stream planners
+        slice them with searchsorted)."""
         if self.plug_idx_host is None:
             self.plug_idx_host = self.plug_idx.cpu().view(torch.int32).numpy().view(np.uint32)
+        if not self.plug_checked:
+            check_ascending(self.plug_idx_host)
+            self.plug_checked = True
         return self.plug_idx_host
 
     def to_file(self) -> QuadPackFile:
@@ -235,6 +248,7 @@ class DualPackDevice:
     chunk_size: int = 50_000_000
     tails: List[torch.Tensor] = field(default_factory=list)
     plug_idx_host: Optional[np.ndarray] = None
+    plug_checked: bool = False
 
     @property
     def tail_lengths(self):
@@ -242,6 +256,11 @@ class DualPackDevice:
         return [int(x.numel()) if x is not None else 0 for x in t]
 
     def plug_host(self) -> np.ndarray:
+        """Host copy of the plug positions, checked strictly ascending once (the stream planners
+        slice them with searchsorted)."""
         if self.plug_idx_host is None:
             self.plug_idx_host = self.plug_idx.cpu().view(torch.int32).numpy().view(np.uint32)
+        if not self.plug_checked:
+            check_ascending(self.plug_idx_host)
+            self.plug_checked = True
         return self.plug_idx_host

@@ -745,6 +745,16 @@ extern "C" int pp_dual_dequant_f16_t(const void* codes, int code_layout, int64_t
   return PP_OK;
 }
 
+extern "C" int pp_dual_gemm_kernel(const void* a, int64_t a_sm, int64_t a_sk, const void* codes, int64_t c_sk,
+                                   int64_t c_sn, int64_t group_size, int64_t chunk_size, int64_t elem_base,
+                                   int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (dual_fast_ok(a, a_sm, a_sk, codes, c_sk, c_sn, elem_base, chunk_size, group_size, M, K)) return PP_GEMM_ROWS;
+  if (dual_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, group_size, chunk_size, std::min<int64_t>(M, 8), N, K))
+    return PP_GEMM_KN;
+  return PP_GEMM_GENERIC;
+}
+
 extern "C" int pp_dual_gemm(const void* a, int64_t a_sm, int64_t a_sk, const void* codes, int code_layout,
                             int64_t c_sk, int64_t c_sn, const void* bmax, int64_t group_size, int64_t chunk_size,
                             const void* amp_lut, int amp_lut_n, const void* cos_lut, const void* sin_lut,

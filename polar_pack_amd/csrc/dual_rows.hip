@@ -971,6 +971,34 @@ extern "C" int64_t pp_dual_stream_waves(int64_t M) {
   return (int64_t)device_cu_count() * (dual_stream_nt(dual_stream_mt(M)) / 64);
 }
 
+// Joins a side stream back into the caller's stream on every return after the fork, so the
+// caller's stream never runs ahead of the side stream's work, and a capture that forked it
+// can end (a side stream left unjoined makes ending the capture fail).  finish() joins on
+// the success path and reports the status; the destructor joins on the early returns.
+struct SideJoin {
+  hipEvent_t join = nullptr;
+  hipStream_t side = nullptr, main = nullptr;
+  void arm(hipEvent_t j, hipStream_t s, hipStream_t m) {
+    join = j;
+    side = s;
+    main = m;
+  }
+  int finish() {
+    if (join == nullptr) return PP_OK;
+    const hipEvent_t j = join;
+    join = nullptr;
+    PP_HIP(hipEventRecord(j, side));
+    PP_HIP(hipStreamWaitEvent(main, j, 0));
+    return PP_OK;
+  }
+  ~SideJoin() {
+    if (join != nullptr) {
+      (void)hipEventRecord(join, side);
+      (void)hipStreamWaitEvent(main, join, 0);
+    }
+  }
+};
+
 extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const pp_quad_seg* segs, int64_t n_segs,
                               const int64_t* seg_bounds, int64_t n_waves, void* workspace, const int64_t* task_plug,
                               int64_t n_tasks,
@@ -1037,12 +1065,14 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
   // the caller's stream, so the call orders like one launch on it.
   std::unique_lock<std::mutex> side_held;
   hipStream_t tail_st = st;
-  hipEvent_t join = nullptr;
+  SideJoin joiner;
   if (n_segs > 0 && n_tail > 0) {
-    hipEvent_t fork = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
     if (int rc = side_stream(&tail_st, &fork, &join)) return rc;
     side_held = std::unique_lock<std::mutex>(side_lock());
     PP_HIP(hipEventRecord(fork, st));
+    // from here on every return joins the side stream back (joiner's destructor)
+    joiner.arm(join, tail_st, st);
     PP_HIP(hipStreamWaitEvent(tail_st, fork, 0));
   }
   if (n_segs > 0) {
@@ -1077,15 +1107,7 @@ extern "C" int pp_dual_stream(const pp_dual_proj* projs, int64_t n_projs, const 
                          : dispatch_dual_tail<PP_DUAL_U16_BE, 1>(T, mt, tail_st);
     else rc = sm == 0 ? dispatch_dual_tail<PP_DUAL_I16_OFFSET, 0>(T, mt, tail_st)
                       : dispatch_dual_tail<PP_DUAL_I16_OFFSET, 1>(T, mt, tail_st);
-    if (join != nullptr) {
-      // join even if the tail launch failed, so the caller's stream never runs ahead of it
-      const hipError_t e1 = hipEventRecord(join, tail_st);
-      const hipError_t e2 = hipStreamWaitEvent(st, join, 0);
-      if (rc) return rc;
-      PP_HIP(e1);
-      PP_HIP(e2);
-    }
     if (rc) return rc;
   }
-  return PP_OK;
+  return joiner.finish();
 }

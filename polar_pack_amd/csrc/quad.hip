@@ -350,6 +350,14 @@ extern "C" int pp_quad_dequant_f16_t(const uint32_t* codes, int64_t c_sk, const 
   return PP_OK;
 }
 
+extern "C" int pp_quad_gemm_kernel(const void* a, int64_t a_sm, int64_t a_sk, const uint32_t* codes, int64_t c_sk,
+                                   int64_t c_sn, int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (quad_rows_ok(a, a_sm, a_sk, codes, c_sk, c_sn, M, N, K)) return PP_GEMM_ROWS;
+  if (quad_kn_ok(a, a_sm, a_sk, codes, c_sk, c_sn, std::min<int64_t>(M, 8), N, K)) return PP_GEMM_KN;
+  return PP_GEMM_GENERIC;
+}
+
 extern "C" int pp_quad_gemm(const void* a, int64_t a_sm, int64_t a_sk, const uint32_t* codes, int64_t c_sk,
                             int64_t c_sn, const void* const* luts, int lut_dtype, const float* scales,
                             const uint32_t* plug_idx, const void* plug_vals, int64_t plug_n, int64_t elem_base,

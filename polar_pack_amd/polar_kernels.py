@@ -12,10 +12,12 @@ Same names, arguments, return values and error behaviour as the reference
   group rule, > 0 = the container's stream-position rule).
 * :func:`dual_dequant` -- float32 (or fp16) weights of a code view.
 
-Batches of 1-4 tokens (1-8 on the (K,N) kernel layout) run on the fused decode kernels;
-5-64 tokens on the (K,N) kernel layout on the matrix-core decode (pp_dual_mfma); larger
-ones decode once into fp16 weights (the values the reference's kernel rounds its weights
-to, polar_kernels.py:78-82) and run a library fp16 GEMM (hipBLASLt through torch.matmul).
+The kernel of a call comes from one table, :data:`polar_pack_amd.routes.DUAL_ROUTES`:
+batches of 1-4 tokens (1-8 on the (K,N) kernel layout) run on the fused decode kernels;
+2-64 tokens on the int16 (K,N) kernel layout on the matrix-core decode (pp_dual_mfma);
+larger ones decode once into fp16 weights (the values the reference's kernel rounds its
+weights to, polar_kernels.py:78-82) and run a library fp16 GEMM (hipBLASLt through
+torch.matmul).
 """
 from __future__ import annotations
 
@@ -25,6 +27,7 @@ import math
 import torch
 
 from . import _native as nat
+from . import plugs, routes
 from .quad_kernels import _check_device
 
 _LAYOUTS = {"i16": nat.PP_DUAL_I16_OFFSET, "u16be": nat.PP_DUAL_U16_BE}
@@ -95,9 +98,9 @@ def _dual_plug(plug, device):
     idx, amp = plug
     if idx.dtype not in (torch.uint32, torch.int32) or amp.dtype != torch.float16 or amp.numel() != idx.numel():
         raise TypeError("plug must be (uint32 idx (P,), float16 amplitude (P,))")
-    idx, amp = idx.contiguous(), amp.contiguous()
     if idx.device != device or amp.device != device:
         raise ValueError("plug tensors must be on the codes' device")
+    idx, amp = plugs.ascending(idx.contiguous(), amp.contiguous())
     return idx.data_ptr(), amp.data_ptr(), idx.numel(), (idx, amp)
 
 
@@ -105,11 +108,13 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
                          plug=None, elem_base=0, layout="i16", chunk_size=0, fused=None):
     """2 GEMMs from one packed pass (polar_kernels.py:98-115); returns ``(out1, out2)`` fp16 (M,N).
 
-    ``fused`` (the int16 (K,N) layout, K % 32 == 0): True runs the matrix-core decode at any
-    size, False the fused (K,N) kernel up to 8 tokens and the fp16 decode + library GEMM
-    above, None (default) the fused (K,N) kernel below ``_dual_mfma_min_m`` tokens (2 when
-    N <= K without plug entries, else 5) and the matrix cores from there up to
-    DUAL_MFMA_MAX_M tokens."""
+    ``plug=(idx uint32 (P,), amp fp16 (P,))`` replaces the amplitude of the pair at storage
+    offset ``idx - elem_base`` (polar_bitpack.py:240-243); entries in any order (sorted once
+    per table on the device, :mod:`polar_pack_amd.plugs`).  The kernel is chosen by
+    :data:`polar_pack_amd.routes.DUAL_ROUTES` from the storage of ``packed``, M, the plug table
+    and ``fused`` (the int16 (K,N) layout, K % 32 == 0): True runs the matrix-core decode at
+    any size, False never (the fused (K,N) kernel up to 8 tokens, then the fp16 decode +
+    library GEMM), None (default) picks by size."""
     M, K = a_fp16.shape
     K_b, N = packed.shape
     assert K == K_b
@@ -133,35 +138,36 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
     bmax = bmax.contiguous()
     pi, pa, pn, keep = _dual_plug(plug, dev)
     L = nat.lib()
-    kn = packed.stride(1) == 1 and packed.stride(0) >= N and packed.stride(0) % 8 == 0 and N % 8 == 0 \
-        and K % 8 == 0 and chunk_size == 0 and group_size >= 8 and group_size & (group_size - 1) == 0 \
-        and packed.data_ptr() % 16 == 0
-    if kn and K % 32 == 0 and layout == "i16" and fused is not False \
-            and (fused or _dual_mfma_min_m(K, N, pn) <= M <= DUAL_MFMA_MAX_M):
+    route = dual_call_route(packed, M, layout=layout, group_size=group_size, chunk_size=chunk_size,
+                            elem_base=elem_base, plug_n=pn, fused=fused)
+    if route == "dual_mfma":
         _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, lut_dt, keep, pn,
                    int(elem_base), out1, out2, L, dev)
         del keep
         return out1, out2
-    if M > (KN_MAX_M if kn else FUSED_MAX_M):
+    if route == "prefill":
         # fp16 weights laid out (N,K), the GEMM's fastest right operand, then one batched GEMM
         # over the two models: K-contiguous codes (container rows) decode along their storage
         # into it (the kernel rule's groups need the (K,N) indices); (K,N) codes with unit
         # column stride through the transposing decode; other strides into (K,N) weights
+        kn = "dual_kn" in routes.dual_storage(packed.stride(0), packed.stride(1), packed.data_ptr(), K, N, layout,
+                                              group_size, chunk_size, int(elem_base))
         nk = packed.stride(0) == 1 and packed.stride(1) != 1 and chunk_size > 0
         if kn:
             w = torch.empty((2, N, K), dtype=torch.float16, device=dev)
-            _dequant_t_into(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug, elem_base,
-                            layout, w[0], w[1])
+            _dequant_t_into(packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug,
+                            elem_base, layout, w[0], w[1])
         else:
             view = packed.t() if nk else packed
             w = torch.empty((2,) + tuple(view.shape), dtype=torch.float16, device=dev)
-            _dequant_into(view, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug, elem_base, layout,
-                          chunk_size, w[0], w[1])
+            _dequant_into(view, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, plug, elem_base,
+                          layout, chunk_size, w[0], w[1])
             if not nk:
                 out = torch.matmul(a_fp16, w)       # (2, M, N)
                 return out[0], out[1]
         out = torch.matmul(a_fp16, w.transpose(1, 2))
         return out[0], out[1]
+    # dual_kn, dual_rows, generic: pp_dual_gemm picks among them alike
     ws_bytes = L.pp_dual_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), packed.data_ptr(),
                                              packed.stride(0), packed.stride(1), group_size, chunk_size,
                                              int(elem_base), pn, M, N, K)
@@ -177,23 +183,13 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
     return out1, out2
 
 
-FUSED_MAX_M = 4   # larger batches decode once and run a library GEMM
-KN_MAX_M = 8      # on the (K,N) kernel layout the fused kernel takes up to 8 tokens, ...
-DUAL_MFMA_MIN_M = 4    # ... but from 5 tokens (K % 32 == 0; earlier, see _dual_mfma_min_m) the
-DUAL_MFMA_MAX_M = 64   # matrix-core decode (pp_dual_mfma) runs, up to 64 (4096x4096 layer,
-# events: 8 tokens 35 against 49 us, 32 tokens 41 against 43 us for two fp16 matmuls; from
-# 96 tokens the fp16 decode + one batched GEMM is faster: 52 against 66 us)
-
-
-def _dual_mfma_min_m(K, N, pn):
-    """Fewest tokens from which int16 (K,N) codes take the matrix-core decode instead of the
-    fused (K,N) kernel: 2 when N <= K without plug entries (graph-replayed, measured at 2 / 3 /
-    4 tokens: 4096x4096 26.0 / 26.7 / 28.3 against 29.6 / 32.8 / 36.6 us, K x N = 11008x2048
-    30.2 / 31.5 / 32.1 against 33.8 / 37.9 / 40.6 us; at 1 token the fused kernel is the
-    faster, 21.8 against 25.2 us on 4096x4096), else 5 (2048x11008: 38.0 / 38.4 / 38.5
-    against 29.6 / 34.6 / 38.1 us; with plug entries the matrix-core decode moves them to
-    its frame on every call)."""
-    return 2 if N <= K and pn == 0 else DUAL_MFMA_MIN_M + 1
+def dual_call_route(packed, M, *, layout="i16", group_size=32, chunk_size=0, elem_base=0, plug_n=0, fused=None):
+    """The route (:data:`polar_pack_amd.routes.DUAL_ROUTES`) of a ``polar_dual_bitpacked`` call
+    with these codes, M tokens and ``plug_n`` plug entries."""
+    K, N = packed.shape
+    caps = routes.dual_storage(packed.stride(0), packed.stride(1), packed.data_ptr(), K, N, layout, group_size,
+                               chunk_size, int(elem_base), plug_n)
+    return routes.dual_route(M, K, N, caps, plug_n > 0, fused)
 
 
 def _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, lut_dt, keep, pn, elem_base,

@@ -11,28 +11,28 @@ Same names, arguments, return values and error behaviour as the reference
   quaternion_packer.py:187-193) and ``elem_base``.
 * :func:`quad_dequant` -- float32 (or fp16) weights of a code view.
 
-Batches (K % 32 == 0 for the matrix cores): on an (N,K) block seen as (K,N) (the container
-layout) the row kernel to 4 tokens, the matrix-core batch decode at 5-64 and the fused
-matrix-core kernel at 65-128; on (K,N) storage the fused (K,N) row kernel at 1 token (and
-with plug entries up to 8) and the fused matrix-core kernel on the codes as stored from 2
-tokens (3 when N > K) to 128 (two 8-token row passes up to 16 tokens when K % 32 != 0);
-larger batches, and more tokens on other layouts, decode once into fp16 weights (the values the reference's
-kernel rounds its weights to, quad_kernels.py:117-126) and run a library fp16 GEMM
-(hipBLASLt through torch.matmul), where the matmul's compute, not the weight stream, bounds
-the time.
+The kernel of a call comes from one table, :data:`polar_pack_amd.routes.QUAD_ROUTES`
+(K % 32 == 0 for the matrix cores): on an (N,K) block seen as (K,N) (the container layout)
+the row kernel to 4 tokens, the matrix-core batch decode at 5-64 and the fused matrix-core
+kernel at 65-128; on (K,N) storage the fused (K,N) row kernel at 1 token (and with plug
+entries up to 8) and the fused matrix-core kernel on the codes as stored from 2 tokens (3
+when N > K) to 128 (two 8-token row passes up to 16 tokens when K % 32 != 0); larger
+batches, and more tokens on other layouts, decode once into fp16 weights (the values the
+reference's kernel rounds its weights to, quad_kernels.py:117-126) and run a library fp16
+GEMM (hipBLASLt through torch.matmul), where the matmul's compute, not the weight stream,
+bounds the time.
 """
 from __future__ import annotations
 
 import ctypes
 import math
-import os
 
 import torch
 
 from . import _native as nat
+from . import plugs, routes
 
 MU = 255.0   # quad_kernels.py:13
-_CHECK_PLUG = os.environ.get("POLAR_PACK_CHECK_PLUG", "0") == "1"   # verify plug order (one sync per call)
 
 
 def _u32_words(nq, q1, q2, q3):
@@ -96,14 +96,9 @@ def _plug_args(plug, device):
         raise TypeError("plug index must be uint32 (or int32 holding uint32 bits)")
     if vals.dtype != torch.float16 or vals.numel() != 4 * idx.numel():
         raise TypeError("plug values must be float16 (P, 4)")
-    idx = idx.contiguous()
-    vals = vals.contiguous()
     if idx.device != device or vals.device != device:
         raise ValueError("plug tensors must be on the codes' device")
-    if _CHECK_PLUG and idx.numel() > 1:
-        pos = idx.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
-        if not bool(torch.all(pos[1:] > pos[:-1])):
-            raise ValueError("plug positions must be strictly ascending")
+    idx, vals = plugs.ascending(idx.contiguous(), vals.contiguous())
     return idx.data_ptr(), vals.data_ptr(), idx.numel(), (idx, vals)
 
 
@@ -124,17 +119,14 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
     7 tables of :func:`pack_quad_layer` (fp16 or fp32); ``scales`` 4 floats.
     Returns a list of 4 fp16 (M,N) tensors ``out_k = fp16(s_k * a @ W_k)``.
     ``plug=(idx uint32 (P,), vals fp16 (P,4))`` replaces the normalised tuple
-    of the element at storage offset ``idx - elem_base`` of ``codes``; ``idx`` must be
-    strictly ascending, as a ``.quadpack`` file stores it (quaternion_packer.py:104-113):
-    checked on the host when ``POLAR_PACK_CHECK_PLUG=1``.
-    ``fused`` (batches above 64 tokens on (N,K) or (K,N) storage, and up to 64 tokens on
-    (K,N) storage): True runs the fused matrix-core kernel at any size (K % 32 == 0), False decodes
-    fp16 weights and runs a library GEMM above 64 tokens (and transposes (K,N) codes for the
-    matrix-core batch decode at 9-64, and keeps the fused row kernel up to 8), None (default)
-    picks by size (on (K,N) storage the fused kernel from 2 or 3 tokens, see
-    ``_kn_big_min_m``, the row kernel with plug entries up to 8; the fused kernel up to
-    BIG_MAX_M tokens, where it is the faster; above, the decode + GEMM, which needs 8 bytes
-    of scratch per code word).
+    of the element at storage offset ``idx - elem_base`` of ``codes``, as a ``.quadpack``
+    file's table does (quaternion_packer.py:187-193); entries in any order (sorted once per
+    table on the device, :mod:`polar_pack_amd.plugs`).
+    The kernel is chosen by :data:`polar_pack_amd.routes.QUAD_ROUTES` from the storage of
+    ``codes``, M, the plug table and ``fused``: None (default) picks by size, True runs the
+    fused matrix-core kernel wherever it can (K % 32 == 0), False never runs it (the fp16
+    decode + library GEMM instead above 64 tokens, which needs 8 bytes of scratch per code
+    word).
     """
     M, K = a.shape
     K_b, N = codes.shape
@@ -155,36 +147,39 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
     lut_ptrs, lut_dtype = _lut_args(luts)
     sc = nat.float_array(scales)
     pi, pv, pn, keep = _plug_args(plug, dev)
+    route = quad_call_route(codes, M, pn, fused)
     L = nat.lib()
-    kn = _kn_layout_ok(codes, K, N)
-    lay = _big_layout(codes, K, N) if M > 8 or fused or (M > 1 and pn == 0) else None
-    if lay == nat.PP_QUAD_NK and M <= 8:
-        lay = None
-    # the fused large-batch kernel: above 64 tokens on either storage; on (K,N) storage from
-    # 9 tokens (the matrix-core batch decode would first have to transpose it), and from
-    # 2 or 3 tokens without plug entries (_kn_big_min_m)
-    kn_big = lay == nat.PP_QUAD_KN and (fused or (fused is None and (M > 8 or M >= _kn_big_min_m(K, N))))
-    if lay is not None and (M > BIG_MIN_M or kn_big) and (fused or (fused is None and M <= BIG_MAX_M)):
+    if route in ("big_nk", "big_kn"):
+        lay = nat.PP_QUAD_NK if route == "big_nk" else nat.PP_QUAD_KN
         _quad_big(a, codes, lay, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
-        del keep
-        return outs
-    big = lay if M > BIG_MIN_M else None
-    if big is None and kn and 8 < M <= (KN_MFMA_MAX_M if N > K else PREFILL_M) and K % 32 == 0:
+    elif route == "kn_mfma":
         _quad_kn_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
-        del keep
-        return outs
-    if M > PREFILL_M or big is not None or (M > 8 and not _mfma_layout_ok(codes, K) and not (kn and M <= KN_MAX_M)):
-        _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base), outs, L, dev)
-        del keep
-        return outs
-    if (M > 8 or (M > ROWS_MAX_M and _mfma_layout_ok(codes, K))) and not kn:
-        # the matrix-core path takes up to 64 tokens per launch: larger batches (the
-        # reference's prefill sizes, quad_kernels.py:166-189) run in blocks of 64 rows
-        for i0 in range(0, M, 64):
+    elif route == "mfma":
+        for i0 in range(0, M, 64):        # the matrix-core decode takes up to 64 tokens per launch
             i1 = min(M, i0 + 64)
             _quad_mfma(a[i0:i1], codes, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base),
                        [o[i0:i1] for o in outs], L, dev)
-        return outs
+    elif route == "prefill":
+        _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base), outs, L, dev)
+    else:                                 # rows, kn, generic: pp_quad_gemm picks among them alike
+        _quad_gemm(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base), outs, L, dev)
+    del keep
+    return outs
+
+
+def quad_call_route(codes, M, plug_n=0, fused=None):
+    """The route (:data:`polar_pack_amd.routes.QUAD_ROUTES`) of a ``quad_bitpacked`` call with
+    these codes, M tokens and ``plug_n`` plug entries."""
+    K, N = codes.shape
+    caps = routes.quad_storage(codes.stride(0), codes.stride(1), codes.data_ptr(), K, N, plug_n)
+    return routes.quad_route(M, K, N, caps, plug_n > 0, fused)
+
+
+def _quad_gemm(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, elem_base, outs, L, dev):
+    """pp_quad_gemm: the row kernel on (N,K) rows, the (K,N) row kernel on (K,N) codes (8 tokens
+    per pass), the generic decode + GEMV otherwise."""
+    M, K = a.shape
+    N = codes.shape[1]
     if a.stride(1) != 1 or a.data_ptr() % 16 or (M > 1 and a.stride(0) % 8):
         a = a.contiguous()
     ws_bytes = L.pp_quad_gemm_workspace_size(a.data_ptr(), a.stride(0), a.stride(1), codes.data_ptr(),
@@ -192,41 +187,10 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
     stream = nat.raw_stream(dev)
     rc = L.pp_quad_gemm(a.data_ptr(), a.stride(0), a.stride(1), codes.data_ptr(), codes.stride(0),
-                        codes.stride(1), lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base),
+                        codes.stride(1), lut_ptrs, lut_dtype, sc, pi, pv, pn, elem_base,
                         nat.ptr_array([o.data_ptr() for o in outs]), outs[0].stride(0), outs[0].stride(1),
                         M, N, K, ws.data_ptr() if ws is not None else None, ws_bytes, stream)
     nat.check(rc, "pp_quad_gemm")
-    del keep
-    return outs
-
-
-def _kn_big_min_m(K, N):
-    """Fewest tokens from which (K,N) codes without plug entries take the fused matrix-core
-    kernel instead of the fused (K,N) row kernel (graph-replayed, measured: at 2 / 4 / 8
-    tokens 4096x4096 27.4 / 27.4 / 27.4 against 29.6 / 36.6 / 45.5 us, K x N = 11008x2048
-    32.4 / 32.5 / 32.3 against 34.4 / 42.2 / 53.9 us, 2048x11008 38.4 / 40.6 / 40.7 against
-    33.9 / 41.9 / 56.3 us; at 1 token the row kernel is the faster: 23.3 against 27.6 us on
-    4096x4096).  With plug entries the row kernel keeps up to 8 tokens: the matrix-core kernel
-    would move them to its (N,K) frame on every call."""
-    return 2 if N <= K else 3
-
-
-ROWS_MAX_M = 4    # (N,K) storage: the row kernel up to this many tokens, the matrix-core batch
-# decode from 5 (K % 32 == 0; gate 11008x2048 / down 2048x11008 with 0.1 % plug entries, rotated
-# copies: 5 tokens 45.4 / 43.9 us against 66.1 / 80.0 us, 8 tokens 45.1 / 43.4 against 66.9 /
-# 79.7; 4 tokens 43.6 / 44.7 against 40.9 / 43.9)
-BIG_MIN_M = 64    # larger batches on (N,K) or (K,N) storage run the fused large-batch kernel ...
-BIG_MAX_M = 128   # ... up to this size by default; above, the fp16 decode + one library GEMM is
-# faster (4096x4096 layer, measured: fused 87.5 us at 128 tokens against 128 us for 4 fp16
-# matmuls; at 1024 tokens fused 291 us, decode 32 us + one batched GEMM 113 us).  On (K,N)
-# storage it also takes 9-64 tokens (4096x4096: 33 / 40 / 58 us at 16 / 32 / 64 tokens
-# against 59 / 65 / 84 us for the transpose + matrix-core batch decode)
-PREFILL_M = 128   # other layouts: batches above this decode once and run a library GEMM
-KN_MAX_M = 16     # (K,N) storage, K % 32 != 0: up to two 8-token passes of the fused kernel
-# (K,N) storage, K % 32 == 0, fused=False: codes transposed to (N,K) for the matrix cores, up
-# to 64 tokens, or up to PREFILL_M when N <= K (measured: 4096x4096 and 11008x2048 gain at
-# 65-128 tokens, 2048x11008 loses to the fp16 decode + GEMM route there)
-KN_MFMA_MAX_M = 64
 
 
 def transposed_plug(idx, vals, elem_base, ldk, K, N):
@@ -261,26 +225,6 @@ def _quad_kn_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, 
     for i0 in range(0, a.shape[0], 64):
         i1 = min(a.shape[0], i0 + 64)
         _quad_mfma(a[i0:i1], view, lut_ptrs, lut_dtype, sc, keep2, pn2, 0, [o[i0:i1] for o in outs], L, dev)
-
-
-def _kn_layout_ok(codes, K, N):
-    """Codes (K,N) with unit column stride (as pack_quad_layer returns): the fused (K,N)
-    kernel's layout."""
-    return codes.stride(1) == 1 and codes.stride(0) >= N and codes.stride(0) % 4 == 0 and N % 4 == 0 \
-        and K % 8 == 0 and codes.data_ptr() % 16 == 0
-
-
-def _big_layout(codes, K, N):
-    """The storage the large-batch kernel reads: PP_QUAD_NK for (N,K) rows seen as (K,N)
-    (the stream container), PP_QUAD_KN for (K,N) rows with unit column stride
-    (pack_quad_layer); None for other strides or K % 32 != 0."""
-    if K % 32:
-        return None
-    if _mfma_layout_ok(codes, K):
-        return nat.PP_QUAD_NK
-    if codes.stride(1) == 1 and codes.stride(0) >= N:
-        return nat.PP_QUAD_KN
-    return None
 
 
 def _quad_big(a, codes, layout, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
@@ -356,14 +300,8 @@ def _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, elem_base, outs
     outs[:] = [out[m] for m in range(4)]
 
 
-def _mfma_layout_ok(codes, K):
-    """Codes of an (N,K) row-major block seen as (K,N): the layout the matrix-core path reads."""
-    return codes.stride(0) == 1 and codes.stride(1) >= K and codes.stride(1) % 4 == 0 and K % 32 == 0 \
-        and codes.data_ptr() % 16 == 0
-
-
 def _quad_mfma(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
-    """More than ROWS_MAX_M tokens on (N,K) rows: the matrix-core batch decode (pp_quad_mfma), plug starts per
+    """5-64 tokens on (N,K) rows: the matrix-core batch decode (pp_quad_mfma), plug starts per
     (row, K slice) found on the device (pp_plug_search; quaternion_packer.py:188-189)."""
     M, K = a.shape
     N = codes.shape[1]

@@ -165,3 +165,16 @@ def dual_rows_ref(dp, tails, pos0, K, rows, x):
         for m in range(2):
             res[m][:, i] = xd @ w[m]
     return res
+
+
+def route_class(route):
+    """How a route's products are held to the oracle: ``fused`` (the row kernels and the
+    generic decode: float32 decode, rel 1e-3 against the exact products), ``mfma`` (the matrix
+    cores: fp16 operands, the float32 dot-product bound), ``prefill`` (fp16 decode + library
+    GEMM: the fp16-weight bound)."""
+    if route in ("rows", "kn", "generic", "dual_kn", "dual_rows"):
+        return "fused"
+    if route in ("mfma", "big_nk", "big_kn", "kn_mfma", "dual_mfma"):
+        return "mfma"
+    assert route == "prefill", route
+    return "prefill"

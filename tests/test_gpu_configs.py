@@ -52,6 +52,26 @@ def _sample_rows(plug_host, pos0, N, K, rng, n_random=4, limit=None):
     return np.array(sorted(rows), np.int64), counts
 
 
+def _segment_edges(st):
+    """Per projection, the rows where the stream's planner cuts: the first and last row of
+    every segment of the launch's segment table (so the first and last row of every wave's
+    run, and the rows on either side of every projection boundary inside one wave's run), and
+    the number of such (projection, row) pairs."""
+    edges = {}
+    for g in st.segs_np:
+        p = int(g["proj"])
+        edges.setdefault(p, set()).update({int(g["row0"]), int(g["row1"]) - 1})
+    # a projection boundary inside one wave's run: the last row before it and the first after
+    for w in range(st.n_waves):
+        lo, hi = int(st.bounds_np[w]), int(st.bounds_np[w + 1])
+        for i in range(lo, hi - 1):
+            a, b = st.segs_np[i], st.segs_np[i + 1]
+            if int(a["proj"]) != int(b["proj"]):
+                edges[int(a["proj"])].add(int(a["row1"]) - 1)
+                edges[int(b["proj"])].add(int(b["row0"]))
+    return edges, sum(len(v) for v in edges.values())
+
+
 # ------------------------------------------------------------------ dual 2048x2048 Linear
 
 def test_dual_2048_linear_split_stream_and_drop_in():
@@ -177,10 +197,14 @@ def test_quad_3b_stream_row_sample_and_per_projection():
     torch.cuda.synchronize()
     rng = np.random.default_rng(2026)
     luts = qk.header_luts(pack.r_max, device=DEV)
-    plugged = 0
+    edges, n_edges = _segment_edges(st)
+    plugged = checked_edges = 0
     for p, (N, K) in enumerate(shapes):
         pos0 = int(st.pos0[p])
         rows, counts = _sample_rows(plug, pos0, N, K, rng)
+        edge = edges.get(p, set())
+        rows = np.array(sorted(set(rows.tolist()) | edge), np.int64)
+        checked_edges += len(edge)
         x_np = xs[p].cpu().numpy()
         ref, n_plug = quad_rows_ref(pack, plug, pos0, K, rows, x_np)
         plugged += n_plug
@@ -194,6 +218,9 @@ def test_quad_3b_stream_row_sample_and_per_projection():
             assert_gemv_close(outs[p][m].float().cpu().numpy(), single[m].float().cpu().numpy(),
                               f"projection {p} model {m}: stream vs drop-in")
     assert plugged > 1000
+    # every wave's first and last row and both sides of every projection cut, against the oracle
+    assert checked_edges == n_edges and n_edges >= st.n_waves, (checked_edges, n_edges, st.n_waves)
+    print(f"quad 3B stream: {n_edges} segment-edge rows checked against the float64 oracle")
 
 
 # ------------------------------------------------------------------ dual 3B-shaped heavy-tail stream
@@ -226,9 +253,14 @@ def test_dual_3b_stream_with_tails_row_sample():
     rng = np.random.default_rng(2027)
     n = pack.n_codes
     saw_straddle = saw_tail = saw_past = False
+    edges, n_edges = _segment_edges(st)
+    checked_edges = 0
     for p, (N, K) in enumerate(shapes):
         pos0 = int(st.pos0[p])
         rows, _ = _sample_rows(plug, pos0, N, K, rng, n_random=3)
+        edge = edges.get(p, set())
+        rows = np.array(sorted(set(rows.tolist()) | edge), np.int64)
+        checked_edges += len(edge)
         if pos0 < n < pos0 + N * K:                   # the projection the codes end in
             r = (n - pos0) // K
             extra = [r - 1, r, r + 1, N - 1] if (n - pos0) % K else [r - 1, r, N - 1]
@@ -250,3 +282,5 @@ def test_dual_3b_stream_with_tails_row_sample():
                 assert_gemv_close(outs[p][m].float().cpu().numpy(), single[m].float().cpu().numpy(),
                                   f"projection {p} model {m}: stream vs drop-in")
     assert saw_straddle and saw_tail and saw_past
+    assert checked_edges == n_edges and n_edges >= st.n_waves, (checked_edges, n_edges, st.n_waves)
+    print(f"dual 3B stream: {n_edges} segment-edge rows checked against the float64 oracle")

@@ -22,13 +22,11 @@ def kernel_layout_layer(K, N, seed, dtype=torch.float16):
     return olay.quantize_polar_bitpacked(w1, w2)
 
 
-def prefill_bound(a, w, plug=0, kn=True):
-    """More than 4 tokens, or int16 (K,N) codes (``kn``) on the matrix cores (from 2 tokens
-    when N <= K without plug entries): weights rounded to fp16 as the reference's kernel
-    rounds them (polar_kernels.py:78-82)."""
-    (M, K), N = a.shape, w.shape[1]
-    mfma = kn and K % 32 == 0 and N % 8 == 0 and M >= pk._dual_mfma_min_m(K, N, plug)
-    return fp16_weight_bound(a, w) if M > pk.FUSED_MAX_M or mfma else None
+def prefill_bound(a, w, route):
+    """The matrix-core decode and the fp16 decode + library GEMM (routes ``dual_mfma`` and
+    ``prefill``) multiply weights rounded to fp16, as the reference's kernel rounds them
+    (polar_kernels.py:78-82): held to the fp16-weight bound; the fused row kernels to rel 1e-3."""
+    return fp16_weight_bound(a, w) if route in ("dual_mfma", "prefill") else None
 
 
 def to_dev(*arrs):
@@ -73,11 +71,13 @@ def test_dual_dequant_container_layout_with_plug(chunk):
 def test_polar_dual_bitpacked_kernel_layout(K, N, M):
     packed, bmax, amp_lut, cos_lut, sin_lut = kernel_layout_layer(K, N, 11 * K + N)
     a = np.random.default_rng(M).standard_normal((M, K)).astype(np.float16)
-    o1, o2 = pk.polar_dual_bitpacked(*to_dev(a, packed, bmax, amp_lut, cos_lut, sin_lut))
+    dv = to_dev(a, packed, bmax, amp_lut, cos_lut, sin_lut)
+    o1, o2 = pk.polar_dual_bitpacked(*dv)
+    route = pk.dual_call_route(dv[1], M)
     W = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut)
     for o, w in ((o1, W[0]), (o2, W[1])):
         assert o.shape == (M, N) and o.dtype == torch.float16
-        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), bound=prefill_bound(a, w))
+        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), bound=prefill_bound(a, w, route))
 
 
 @pytest.mark.parametrize("M", [1, 2, 4, 6])
@@ -96,11 +96,13 @@ def test_polar_dual_bitpacked_container_stream(chunk, M):
         view = codes_all[base:base + N * K].reshape(N, K).t()
         o1, o2 = pk.polar_dual_bitpacked(torch.from_numpy(a).to(DEV), view, scales, amp, cs, sn, layout="u16be",
                                          chunk_size=dp.chunk_size, plug=plug, elem_base=base)
+        route = pk.dual_call_route(view, M, layout="u16be", chunk_size=dp.chunk_size, elem_base=base,
+                                   plug_n=plug[0].numel())
         d1, d2 = odp.decode_pairs_f64(dp, base, base + N * K)
         for o, d in ((o1, d1), (o2, d2)):
             w = d.reshape(N, K).T
             assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), f"base {base}",
-                              bound=prefill_bound(a, w, kn=False))
+                              bound=prefill_bound(a, w, route))
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
@@ -141,14 +143,16 @@ def test_polar_dual_bitpacked_kn_fast_path(K, N, plug, M):
     kw = {}
     if plug:
         kw = dict(plug=(u32(flat + base).to(DEV), torch.from_numpy(vals).to(DEV)), elem_base=base)
-    o1, o2 = pk.polar_dual_bitpacked(*to_dev(a, packed, bmax, amp_lut, cos_lut, sin_lut), **kw)
+    dv = to_dev(a, packed, bmax, amp_lut, cos_lut, sin_lut)
+    o1, o2 = pk.polar_dual_bitpacked(*dv, **kw)
+    route = pk.dual_call_route(dv[1], M, elem_base=base, plug_n=plug)
     W = olay.dual_dequant(packed, bmax, amp_lut, cos_lut, sin_lut)
     ph = (packed.astype(np.int32) + 32768) & 1023
     kk, nn = flat // N, flat % N
     for w, lut in ((W[0], cos_lut), (W[1], sin_lut)):
         w[kk, nn] = vals.astype(np.float64) * np.asarray(lut, np.float64)[ph[kk, nn]]
     for o, w in ((o1, W[0]), (o2, W[1])):
-        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), bound=prefill_bound(a, w, plug))
+        assert_gemv_close(o.float().cpu().numpy(), olay.gemm_f64(a, w), bound=prefill_bound(a, w, route))
 
 
 def test_polar_dual_bitpacked_kn_output_view():

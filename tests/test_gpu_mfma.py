@@ -10,6 +10,7 @@ from oracle import layer as olay
 from oracle import quadpack as oqp
 from parity import assert_gemv_close, fp16_weight_bound, normwise
 from polar_pack_amd import quad_kernels as qk
+from refs import route_class
 from polar_pack_amd.container import QuadPackFile
 from polar_pack_amd.stream import QuadBatch
 
@@ -120,7 +121,7 @@ def test_drop_in_operator_takes_the_matrix_cores_for_large_batches(M):
                              plug=(pack.plug_idx, pack.plug_vals), elem_base=pos)
     for m in range(4):
         assert outs[m].shape == (M, N) and outs[m].dtype == torch.float16
-    if M <= qk.BIG_MAX_M:
+    if route_class(qk.quad_call_route(codes, M, pack.plug_idx.numel())) == "mfma":
         check(outs, oracle(qp, pos, N, K, x_np), "drop-in")
         return
     # above: fp16 decode (s_m folded in) + library GEMM, held to the fp16-weight bound

@@ -10,6 +10,8 @@ from oracle import layer as olay
 from oracle import quadpack as oqp
 from parity import fp16_ulp_distance, fp16_weight_bound, normwise, assert_dequant_close, assert_gemv_close
 from polar_pack_amd import quad_kernels as qk
+from polar_pack_amd import routes
+from refs import route_class
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -119,12 +121,8 @@ def test_quad_gemm_matches_oracle(K, N, layout, M):
     # more than 8 tokens on (N,K) rows: the matrix-core path, fp16 weights into the dot
     # product (as the reference's tl.dot); held to the fp16-rounded decode + the fp32
     # dot-product bound (see test_gpu_mfma.py)
-    kn_ok = layout == "kn" and N % 4 == 0 and K % 8 == 0
-    # matrix cores: (N,K) rows above ROWS_MAX_M tokens; (K,N) storage (no plug entries here) from
-    # 2 or 3 tokens, in the fused matrix-core kernel (any column count)
-    mfma = K % 32 == 0 and ((layout == "nk" and M > qk.ROWS_MAX_M) or (layout == "kn" and M >= qk._kn_big_min_m(K, N)))
-    kn = kn_ok and M <= qk.KN_MAX_M and not mfma                          # fused (K,N) passes
-    prefill = M > 8 and not mfma and not kn      # fp16 decode + library GEMM
+    cls = route_class(qk.quad_call_route(view, M))
+    mfma, prefill = cls == "mfma", cls == "prefill"
     W32 = olay.quad_dequant(codes, [l.float().numpy() for l in luts], dtype=np.float32) if mfma else None
     for k in range(4):
         assert outs[k].shape == (M, N) and outs[k].dtype == torch.float16
@@ -151,15 +149,16 @@ def test_quad_gemm_real_pack_with_plug_fast_path(M):
     luts = qk.header_luts(qp.r_max)
     rng = np.random.default_rng(M)
     a = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
-    outs = qk.quad_bitpacked(a.to(DEV), u32(codes_nk).to(DEV).t(), [l.to(DEV) for l in luts], list(qp.s),
+    view = u32(codes_nk).to(DEV).t()
+    outs = qk.quad_bitpacked(a.to(DEV), view, [l.to(DEV) for l in luts], list(qp.s),
                              plug=(u32(qp.plug_idx + base).to(DEV), torch.from_numpy(qp.plug_vals).to(DEV)),
                              elem_base=base)
+    cls = route_class(qk.quad_call_route(view, M, qp.plug_idx.size))
     W = oqp.unpack_quad_f64(qp, 0, N * K)                # float64, plug applied, times s_k
     for k in range(4):
         w = W[k].reshape(N, K).T
-        # fp16 weights into the product above ROWS_MAX_M tokens (matrix cores; the fp16 decode
-        # + library GEMM above BIG_MAX_M)
-        bound = fp16_weight_bound(a.numpy(), w) if M > qk.ROWS_MAX_M else None
+        # fp16 weights into the product on the matrix cores and the fp16 decode + library GEMM
+        bound = fp16_weight_bound(a.numpy(), w) if cls != "fused" else None
         if bound is not None:
             assert normwise(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), w)) <= 1e-3
         assert_gemv_close(outs[k].float().cpu().numpy(), olay.gemm_f64(a.numpy(), w), f"model {k}", bound=bound)
@@ -235,16 +234,10 @@ def test_pack_quad_layer_on_gpu_matches_oracle():
 
 
 def kn_route(K, N, M, plug):
-    """Which kernel quad_bitpacked runs for contiguous (K,N) codes: 'fused' (the (K,N)
-    decode kernel), 'mfma' (the fused matrix-core kernel: 9-128 tokens, and from 2 or 3
-    tokens without plug entries) or 'prefill' (fp16 decode + library GEMM)."""
-    if K % 32 == 0 and not plug and qk._kn_big_min_m(K, N) <= M <= 8:
-        return "mfma"
-    if M <= 8 or (K % 32 != 0 and M <= qk.KN_MAX_M):
-        return "fused"
-    if K % 32 == 0 and M <= qk.BIG_MAX_M:
-        return "mfma"      # codes transposed for the matrix cores, or the fused large-batch kernel
-    return "prefill"
+    """How quad_bitpacked's route for contiguous (K,N) codes is held to the oracle
+    (:func:`refs.route_class` of the routing table's cell)."""
+    caps = routes.quad_storage(N, 1, 0, K, N, 1 if plug else 0)
+    return route_class(routes.quad_route(M, K, N, caps, bool(plug)))
 
 
 def check_route(outs, a, codes, luts, scales, route, plug_at=None, plug_vals=None, what=""):
@@ -360,7 +353,7 @@ def test_quad_split_tables_every_route(layout, M):
         nn, kk = flat // K, flat % K          # storage offsets of (N,K) rows
         idx = flat
         at = (kk, nn)
-        route = "fused" if M <= qk.ROWS_MAX_M else "mfma"
+        route = route_class(qk.quad_call_route(view, M, flat.size))
     a = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
     L = [l.to(DEV) for l in luts]
     outs = qk.quad_bitpacked(a.to(DEV), view, L, scales, plug=(u32(idx).to(DEV), torch.from_numpy(vals).to(DEV)))
