@@ -96,6 +96,29 @@ int64_t pp_quad_gemm_workspace_size(const void* a, int64_t a_sm, int64_t a_sk,
                                     const uint32_t* codes, int64_t c_sk, int64_t c_sn,
                                     int64_t plug_n, int64_t M, int64_t N, int64_t K);
 
+/* One (N,K) Linear of container rows (row n of the codes at codes + n*ldc, as a stream
+ * stores a projection) on the fused row kernel, 1-8 tokens, with a plan made once per codes
+ * and plug table (no reference counterpart: the reference's quad_bitpacked, quad_kernels.py:
+ * 146-159, makes one call per Linear with no state; this is that call with its per-table work
+ * done ahead, which the drop-in operator caches).  The plan:
+ *   wave_plug  pp_quad_rows_plan_size(M) int64 plug starts from pp_quad_rows_plan (null
+ *              without plug entries), for this elem_base, ldc, M, N and K;
+ *   plug_code  each entry's code word from pp_quad_plug_codes (or null: read from the codes);
+ *   workspace  pp_quad_rows_workspace_size(M, N, K) bytes, zero on entry and left zero by
+ *              every launch (null when that is 0): rows with fewer tasks than ~1.5 per
+ *              wavefront are cut into column slices whose sums meet there.
+ * Outputs out[m][i*o_sm + n*o_sn] = fp16(s_m * sum_k a[i*a_sm + k] W_m[n][k]); launches that
+ * share a workspace must not overlap. */
+int64_t pp_quad_rows_plan_size(int64_t M);
+int64_t pp_quad_rows_workspace_size(int64_t M, int64_t N, int64_t K);
+int pp_quad_rows_plan(const uint32_t* plug_idx, int64_t plug_n, int64_t elem_base, int64_t ldc, int64_t M,
+                      int64_t N, int64_t K, int64_t* wave_plug, void* stream);
+int pp_quad_rows(const void* a, int64_t a_sm, const uint32_t* codes, int64_t ldc,
+                 const void* const* luts, int lut_dtype, const float* scales,
+                 const uint32_t* plug_idx, const void* plug_vals, const uint32_t* plug_code, int64_t plug_n,
+                 const int64_t* wave_plug, int64_t elem_base, void* const* out, int64_t o_sm, int64_t o_sn,
+                 int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* The kernel pp_quad_gemm / pp_dual_gemm runs for these operands (no reference counterpart:
  * the reference has one kernel per operator): PP_GEMM_ROWS (the fused row decode of (N,K)
  * rows), PP_GEMM_KN (the fused decode of (K,N) rows with unit column stride), PP_GEMM_GENERIC
@@ -489,6 +512,23 @@ typedef struct pp_dual_proj {
 } pp_dual_proj;
 
 int pp_dual_stream_rows(int64_t M);
+/* One (N,K) Linear of a dual stream on the stream kernel's one-Linear launch (no reference
+ * counterpart: the reference's polar_dual_bitpacked, polar_kernels.py:98-115, makes one call
+ * per Linear; this is that call with the per-stream plan of pp_dual_stream done ahead).
+ * proj: the Linear (its codes, stream position, activations and outputs, as a pp_dual_proj
+ * of pp_dual_stream); task_plug, plug_ent, scale_tab: as pp_dual_stream takes them, for this
+ * one projection (tasks of pp_dual_stream_rows(M) rows numbered from its first row); no
+ * segments and no tails.  The waves find their rows and column slice from the launch shape;
+ * rows with fewer tasks than ~1.5 per wavefront are cut into column slices whose sums meet in
+ * the workspace: pp_dual_rows_workspace_size(M, N, K) bytes, zero on entry, left zero by every
+ * launch (launches sharing it must not overlap). */
+int64_t pp_dual_rows_workspace_size(int64_t M, int64_t N, int64_t K);
+int pp_dual_rows(const pp_dual_proj* proj, const int64_t* task_plug, int plug_windows, int code_layout,
+                 const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
+                 const void* scale_tab, int64_t n_tab, const float* amp_lut, const float* cos_lut,
+                 const float* sin_lut, const uint32_t* plug_idx, const void* plug_amp,
+                 const uint32_t* plug_ent, int64_t plug_n, int64_t M, void* workspace,
+                 int64_t workspace_bytes, void* stream);
 /* Pairs the dual stream decode reads per row and step for M tokens (0 for bad M). */
 int pp_dual_stream_chunk(int64_t M);
 int64_t pp_dual_stream_waves(int64_t M);

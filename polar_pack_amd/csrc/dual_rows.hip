@@ -62,31 +62,48 @@ struct DualStreamArgs {
   int64_t n_tasks;
   int M;
   void* ws;                   // split launches: per-task counters, then float32 accumulators
+  // one-Linear launch (dual_direct_kernel): the projection, its column slices and chunks,
+  // the accumulators [2][M][N] and per-task counters of a sliced launch
+  pp_dual_proj proj;
+  int parts, n_chunks;
+  float* acc;
+  uint32_t* cnt;
 };
 
 // (cos, sin) rows as 16-byte units (two replicas) in address order, so that a wavefront's
 // stores fill consecutive banks; every LUT load of a thread is issued before its stores.
+// In two steps, so that a kernel can issue other loads between the LUT loads and the stores.
 template <int LAYOUT, int NT>
-__device__ __forceinline__ void dual_build_lds(char* lds, const DualStreamArgs& A) {
-  constexpr int KU = (8192 + NT - 1) / NT;
-  float c[KU], s[KU];
+struct DualTableBuild {
+  static constexpr int KU = (8192 + NT - 1) / NT;
+  float c[KU], s[KU], amp;
+  __device__ __forceinline__ void load(const DualStreamArgs& A) {
 #pragma unroll
-  for (int k = 0; k < KU; ++k) {
-    const int u = threadIdx.x + k * NT;
-    if (u < 8192) {
-      c[k] = A.cos_lut[u >> 3];
-      s[k] = A.sin_lut[u >> 3];
+    for (int k = 0; k < KU; ++k) {
+      const int u = threadIdx.x + k * NT;
+      if (u < 8192) {
+        c[k] = A.cos_lut[u >> 3];
+        s[k] = A.sin_lut[u >> 3];
+      }
+    }
+    // the int16 layout stores code ^ 0x8000: entry a holds amplitude a ^ 32
+    if (threadIdx.x < 64) amp = A.amp_lut[LAYOUT == PP_DUAL_I16_OFFSET ? (threadIdx.x ^ 32) : threadIdx.x];
+  }
+  __device__ __forceinline__ void store(char* lds) const {
+    if (threadIdx.x < 64) *reinterpret_cast<float*>(lds + DLDS_AMP + 4 * threadIdx.x) = amp;
+#pragma unroll
+    for (int k = 0; k < KU; ++k) {
+      const int u = threadIdx.x + k * NT;
+      if (u < 8192) *reinterpret_cast<float4*>(lds + DLDS_CS + 16 * u) = make_float4(c[k], s[k], c[k], s[k]);
     }
   }
-  // the int16 layout stores code ^ 0x8000: entry a holds amplitude a ^ 32
-  if (threadIdx.x < 64)
-    *reinterpret_cast<float*>(lds + DLDS_AMP + 4 * threadIdx.x) =
-        A.amp_lut[LAYOUT == PP_DUAL_I16_OFFSET ? (threadIdx.x ^ 32) : threadIdx.x];
-#pragma unroll
-  for (int k = 0; k < KU; ++k) {
-    const int u = threadIdx.x + k * NT;
-    if (u < 8192) *reinterpret_cast<float4*>(lds + DLDS_CS + 16 * u) = make_float4(c[k], s[k], c[k], s[k]);
-  }
+};
+
+template <int LAYOUT, int NT>
+__device__ __forceinline__ void dual_build_lds(char* lds, const DualStreamArgs& A) {
+  DualTableBuild<LAYOUT, NT> b;
+  b.load(A);
+  b.store(lds);
 }
 
 // Uniform state of a segment.
@@ -526,6 +543,52 @@ struct DualRunner {
     return cur.ti < ntask;
   }
 
+  // One-Linear launch, in three parts around the table build: start_ranges() requests the
+  // plug ranges of steps 0-2 (the first thing a wave loads), start_chunks() waits for the
+  // first two, requests the entries of step 0's window and issues the first chunks,
+  // run_started() (after the build) completes the window stages and runs the walk.
+  u32x4 Tr[2];
+  __device__ __forceinline__ void start_ranges() {
+    Cursor c = {0, 0};
+    load_range(c, Tr[0]);
+    advance_slot(c);
+    load_range(c, Tr[1]);
+    advance_slot(c);
+    load_range(c, T);
+    c3 = c;
+  }
+  template <int NPRE, int NB>
+  __device__ __forceinline__ void start_chunks(DChunk<MT, RG> (&cb)[NB]) {
+    s0 = slot_of(Cursor{0, 0}, Tr[0]);
+    Cursor c = {0, 0};
+    advance_slot(c);
+    s1 = slot_of(c, Tr[1]);
+    dwin_positions<PW>(A, s0, lane, I);
+#pragma unroll
+    for (int b = 0; b < NPRE; ++b) prefetch(cb[b]);
+  }
+  __device__ __forceinline__ void run_started_one(DChunk<MT, RG> (&cb)[3]) {
+    dwin_data<MT, RG, PW, SM>(A, S, s0, I, lane, D);
+    dwin_positions<PW>(A, s1, lane, I);
+    Cursor cur = {0, 0};
+    for (;;) {
+      if (!step(cur, cb[0], cb[2])) break;
+      if (!step(cur, cb[1], cb[0])) break;
+      if (!step(cur, cb[2], cb[1])) break;
+    }
+    finish_pending();
+  }
+  __device__ __forceinline__ void run_started_two(DChunk<MT, RG> (&cb)[2]) {
+    dwin_data<MT, RG, PW, SM>(A, S, s0, I, lane, D);
+    dwin_positions<PW>(A, s1, lane, I);
+    Cursor cur = {0, 0};
+    for (;;) {
+      if (!step(cur, cb[0], cb[1])) break;
+      if (!step(cur, cb[1], cb[0])) break;
+    }
+    finish_pending();
+  }
+
   __device__ __forceinline__ void run() {
     if (ntask <= 0 || S.kend <= S.kbeg) return;
     // fill the window stages for steps 0 and 1, the range of step 2 in flight
@@ -619,6 +682,44 @@ __global__ __launch_bounds__(DualCfg<MT>::NT) void dual_stream_kernel(const Dual
     DualRunner<MT, RG, PW, LAYOUT, SM, SPLIT> R(lds, A, S, uniform(g.task0));
     R.run();
   }
+}
+
+// One Linear: wave gw's column slice and task run from the launch shape (direct_item, as
+// the quad row kernel deals them), no segment table.  The wave requests its first plug
+// ranges, then the LUTs, its first window's entries and first chunks, so their round trips
+// run under the table build.
+template <int MT, int PW, int LAYOUT, int SM, bool SPLIT>
+__global__ __launch_bounds__(DualCfg<MT>::NT) void dual_direct_kernel(const DualStreamArgs A) {
+  constexpr int RG = DualCfg<MT>::RG, NT = DualCfg<MT>::NT, WAVES = NT / 64;
+  __shared__ __attribute__((aligned(16))) uint32_t Tb[DLDS_BYTES / 4];
+  char* lds = reinterpret_cast<char*>(Tb);
+  const int64_t gw = (int64_t)blockIdx.x * WAVES + uniform(threadIdx.x >> 6);
+  const int K = uniform(A.proj.K), N = uniform(A.proj.N);
+  const DirectItem d = direct_item<WAVES>((uint32_t)gw, gridDim.x * WAVES, (uint32_t)uniform64(A.n_tasks),
+                                          (uint32_t)uniform(A.parts), (uint32_t)uniform(A.n_chunks), DPAIRS,
+                                          (uint32_t)K);
+  DualSeg S;
+  dual_seg(A.proj, min(d.t0 * RG, N), min(d.t1 * RG, N), A.M, S);
+  S.kbeg = uniform(d.kbeg);
+  S.kend = uniform(d.kend);
+  if (SPLIT && uniform(A.parts) > 1) {
+    S.parts = uniform(A.parts);
+    S.acc = uniform_ptr(A.acc);
+    S.cnt = uniform_ptr(A.cnt) + d.t0;
+  }
+  const bool busy = S.nrows > 0 && S.kend > S.kbeg;
+  DualRunner<MT, RG, PW, LAYOUT, SM, SPLIT> R(lds, A, S, d.t0);
+  if (busy) R.start_ranges();
+  DualTableBuild<LAYOUT, NT> tb;
+  tb.load(A);
+  constexpr int NB = MT == 1 ? 3 : 2;
+  DChunk<MT, RG> cb[NB];
+  if (busy) R.template start_chunks<NB - 1>(cb);
+  tb.store(lds);
+  __syncthreads();
+  if (!busy) return;
+  if constexpr (MT == 1) R.run_started_one(cb);
+  else R.run_started_two(cb);
 }
 
 // ------------------------------------------------------------------ tail rows
@@ -891,6 +992,49 @@ static int launch_dual_stream(const DualStreamArgs& A, int pw, hipStream_t st) {
   return PP_OK;
 }
 
+template <int MT, int LAYOUT, int SM>
+static int launch_dual_direct(const DualStreamArgs& A, int pw, hipStream_t st) {
+  const dim3 grid((unsigned)device_cu_count()), block(DualCfg<MT>::NT);
+  if (A.parts > 1) {
+    if (pw == 1) hipLaunchKernelGGL((dual_direct_kernel<MT, 1, LAYOUT, SM, true>), grid, block, 0, st, A);
+    else hipLaunchKernelGGL((dual_direct_kernel<MT, 2, LAYOUT, SM, true>), grid, block, 0, st, A);
+  } else {
+    if (pw == 1) hipLaunchKernelGGL((dual_direct_kernel<MT, 1, LAYOUT, SM, false>), grid, block, 0, st, A);
+    else hipLaunchKernelGGL((dual_direct_kernel<MT, 2, LAYOUT, SM, false>), grid, block, 0, st, A);
+  }
+  PP_LAUNCH_CHECK();
+  return PP_OK;
+}
+
+template <int LAYOUT, int SM>
+static int dispatch_dual_direct(const DualStreamArgs& A, int mt, int pw, hipStream_t st) {
+  switch (mt) {
+    case 1: return launch_dual_direct<1, LAYOUT, SM>(A, pw, st);
+    case 2: return launch_dual_direct<2, LAYOUT, SM>(A, pw, st);
+    default: return launch_dual_direct<4, LAYOUT, SM>(A, pw, st);
+  }
+}
+
+// One Linear of a dual stream: T tasks and their column slices (direct_parts), the split
+// workspace (per-task counters, 256-byte aligned, then accumulators [2][M][N]).
+struct DualDirectPlan {
+  int mt, rg, parts, n_chunks;
+  int64_t n_tasks, waves, cnt_bytes, split_bytes;
+};
+static DualDirectPlan dual_direct_plan(int64_t M, int64_t N, int64_t K) {
+  DualDirectPlan p;
+  p.mt = M <= 1 ? 1 : M <= 2 ? 2 : 4;
+  p.rg = p.mt == 1 ? DualCfg<1>::RG : p.mt == 2 ? DualCfg<2>::RG : DualCfg<4>::RG;
+  const int nt = p.mt == 1 ? DualCfg<1>::NT : p.mt == 2 ? DualCfg<2>::NT : DualCfg<4>::NT;
+  p.waves = (int64_t)device_cu_count() * (nt / 64);
+  p.n_tasks = (N + p.rg - 1) / p.rg;
+  p.n_chunks = (int)std::max<int64_t>(1, (K + DPAIRS - 1) / DPAIRS);
+  p.parts = direct_parts(p.n_tasks, p.waves, p.n_chunks);
+  p.cnt_bytes = p.parts > 1 ? (p.n_tasks * 4 + 255) / 256 * 256 : 0;
+  p.split_bytes = p.parts > 1 ? p.cnt_bytes + 4 * 2 * M * N : 0;
+  return p;
+}
+
 template <int LAYOUT, int SM>
 static int dispatch_dual_stream(const DualStreamArgs& A, int mt, int pw, hipStream_t st) {
   switch (mt) {
@@ -969,6 +1113,85 @@ extern "C" int pp_dual_stream_chunk(int64_t M) { return M < 1 || M > 4 ? 0 : DPA
 extern "C" int64_t pp_dual_stream_waves(int64_t M) {
   if (M < 1 || M > 4) return 0;
   return (int64_t)device_cu_count() * (dual_stream_nt(dual_stream_mt(M)) / 64);
+}
+
+extern "C" int64_t pp_dual_rows_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > 4 || N < 1 || K < 1) return 0;
+  return dual_direct_plan(M, N, K).split_bytes;
+}
+
+extern "C" int pp_dual_rows(const pp_dual_proj* proj, const int64_t* task_plug, int plug_windows, int code_layout,
+                            const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
+                            const void* scale_tab, int64_t n_tab, const float* amp_lut, const float* cos_lut,
+                            const float* sin_lut, const uint32_t* plug_idx, const void* plug_amp,
+                            const uint32_t* plug_ent, int64_t plug_n, int64_t M, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  PP_REQUIRE(proj != nullptr, "proj is null");
+  const pp_dual_proj P = *proj;
+  PP_REQUIRE(P.codes && P.x && P.out[0] && P.out[1], "null pointer in proj");
+  PP_REQUIRE(P.N >= 1 && P.K >= 8 && P.K % 8 == 0 && P.K < (1 << 19) && P.ldc >= P.K && P.ldc % 8 == 0,
+             "the dual row decode needs K % 8 == 0, K < 2^19 and ldc >= K, a multiple of 8");
+  PP_REQUIRE(aligned(P.codes, 16) && aligned(P.x, 16) && P.pos0 >= 0 && P.pos0 % 8 == 0,
+             "codes and activations must be 16-byte aligned, the position a multiple of 8");
+  PP_REQUIRE(M >= 1 && M <= 4 && (M == 1 || (P.x_sm >= P.K && P.x_sm % 8 == 0)) && (M == 1 || P.o_sm >= P.N),
+             "the dual row decode takes 1..4 tokens (activation rows a multiple of 8 apart)");
+  PP_REQUIRE(2 * ((int64_t)(P.N - 1) * P.ldc + P.K) < (1ll << 31) && (M - 1) * P.x_sm + P.K < (1ll << 30) &&
+                 (M - 1) * P.o_sm + P.N < (1ll << 30),
+             "a Linear's codes, activations and outputs must each stay below 2 GiB");
+  PP_REQUIRE(plug_windows == 1 || plug_windows == 2, "plug_windows must be 1 or 2");
+  PP_REQUIRE(code_layout == PP_DUAL_I16_OFFSET || code_layout == PP_DUAL_U16_BE, "bad code_layout");
+  PP_REQUIRE(amp_lut && cos_lut && sin_lut && task_plug, "lut pointers or task_plug are null");
+  PP_REQUIRE(scales != nullptr && n_groups >= 1 && 2 * n_groups < (1ll << 31), "bad scales / n_groups");
+  PP_REQUIRE(group_size >= 8 && (group_size & (group_size - 1)) == 0,
+             "the dual row decode needs a power-of-two group_size >= 8");
+  PP_REQUIRE(chunk_size >= 8 && chunk_size % 8 == 0, "the dual row decode needs chunk_size % 8 == 0");
+  PP_REQUIRE(scale_tab == nullptr || (n_tab >= 1 && 2 * n_tab < (1ll << 31)), "bad scale_tab / n_tab");
+  PP_REQUIRE(plug_n >= 0 && plug_n < (1ll << 28) && (plug_n == 0 || (plug_idx && plug_amp && plug_ent)),
+             "plug arrays are null (plug_ent from pp_dual_plug_table)");
+  const int sm = chunk_size % group_size == 0 ? (scale_tab != nullptr ? 2 : 0) : 1;
+  PP_REQUIRE(sm != 2 || chunk_size % group_size == 0, "the scale table needs chunk_size % group_size == 0");
+  const DualDirectPlan p = dual_direct_plan(M, P.N, P.K);
+  PP_REQUIRE(p.waves < (1 << 16), "the one-Linear launch deals at most 65,535 wavefronts");
+  PP_REQUIRE(p.split_bytes == 0 || (workspace != nullptr && workspace_bytes >= p.split_bytes),
+             "workspace too small: need %lld bytes (pp_dual_rows_workspace_size), zero on entry",
+             (long long)p.split_bytes);
+  DualStreamArgs A = {};
+  A.amp_lut = amp_lut;
+  A.cos_lut = cos_lut;
+  A.sin_lut = sin_lut;
+  A.scales = reinterpret_cast<const f16*>(scales);
+  A.n_groups = n_groups;
+  A.scale_tab = reinterpret_cast<const f16*>(scale_tab);
+  A.n_tab = n_tab;
+  A.gs = group_size;
+  A.chunk = chunk_size;
+  A.per_chunk = (chunk_size + group_size - 1) / group_size;
+  A.log2gs = 0;
+  while ((1ll << A.log2gs) < group_size) ++A.log2gs;
+  A.plug_idx = plug_idx;
+  A.plug_amp = reinterpret_cast<const f16*>(plug_amp);
+  A.plug_ent = plug_ent;
+  A.plug_n = plug_n;
+  A.task_plug = task_plug;
+  A.n_tasks = p.n_tasks;
+  A.M = (int)M;
+  A.proj = P;
+  A.parts = p.parts;
+  A.n_chunks = p.n_chunks;
+  if (p.parts > 1) {
+    A.cnt = reinterpret_cast<uint32_t*>(workspace);
+    A.acc = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.cnt_bytes);
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool be = code_layout == PP_DUAL_U16_BE;
+  if (sm == 2)
+    return be ? dispatch_dual_direct<PP_DUAL_U16_BE, 2>(A, p.mt, plug_windows, st)
+              : dispatch_dual_direct<PP_DUAL_I16_OFFSET, 2>(A, p.mt, plug_windows, st);
+  if (sm == 0)
+    return be ? dispatch_dual_direct<PP_DUAL_U16_BE, 0>(A, p.mt, plug_windows, st)
+              : dispatch_dual_direct<PP_DUAL_I16_OFFSET, 0>(A, p.mt, plug_windows, st);
+  return be ? dispatch_dual_direct<PP_DUAL_U16_BE, 1>(A, p.mt, plug_windows, st)
+            : dispatch_dual_direct<PP_DUAL_I16_OFFSET, 1>(A, p.mt, plug_windows, st);
 }
 
 // Joins a side stream back into the caller's stream on every return after the fork, so the

@@ -115,32 +115,45 @@ __device__ __forceinline__ void lookup(const char* lds, uint32_t cw, const LaneO
 }
 
 // Build the tables of a workgroup (all NT threads; NT a multiple of 256) from the 7
-// header LUTs (256 entries each, of type E) into T (QLDS_BYTES).  Returns true for the
-// shared layout (the t1 and t2 tables equal), false for the split one.  Every load of
-// the shared layout is issued before the layout check.
+// header LUTs (256 entries each, of type E) into T (QLDS_BYTES), in two steps so that a
+// kernel can issue other loads between them: load() issues every LUT load of the shared
+// layout (and those of the layout check), finish() checks the layout across the workgroup,
+// stores the tables and waits for them; it returns true for the shared layout (the t1 and
+// t2 tables equal), false for the split one.
+template <int NT, typename E>
+struct QuadTableBuild {
+  static_assert(NT % 256 == 0, "the table build takes a multiple of 256 threads");
+  float v[4];
+  LayShared::Units<NT> U;
+  __device__ __forceinline__ void load(const QuadLuts& luts) {
+    const int e = threadIdx.x & 255;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = lut_val<E>(luts, 1 + i, e);
+    U.template load<E>(luts);
+  }
+  __device__ __forceinline__ bool finish(uint32_t* T, const QuadLuts& luts) {
+    char* lds = reinterpret_cast<char*>(T);
+    const bool same = __float_as_uint(v[0]) == __float_as_uint(v[2]) && __float_as_uint(v[1]) == __float_as_uint(v[3]);
+    // workgroup-wide AND through the (not yet built) table memory: the tables fill all
+    // of LDS, so there is no room for a separate flag
+    if (threadIdx.x == 0) T[0] = 0u;
+    __syncthreads();
+    if (!same) T[0] = 1u;
+    __syncthreads();
+    const bool shared = T[0] == 0u;
+    __syncthreads();
+    if (shared) U.store(lds);
+    else LaySplit::build<NT, E>(lds, luts);
+    __syncthreads();
+    return shared;
+  }
+};
+
 template <int NT, typename E>
 __device__ __forceinline__ bool quad_tables_of(uint32_t* T, const QuadLuts& luts) {
-  static_assert(NT % 256 == 0, "the table build takes a multiple of 256 threads");
-  char* lds = reinterpret_cast<char*>(T);
-  const int e = threadIdx.x & 255;
-  float v[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = lut_val<E>(luts, 1 + i, e);
-  LayShared::Units<NT> U;
-  U.template load<E>(luts);
-  const bool same = __float_as_uint(v[0]) == __float_as_uint(v[2]) && __float_as_uint(v[1]) == __float_as_uint(v[3]);
-  // workgroup-wide AND through the (not yet built) table memory: the tables fill all
-  // of LDS, so there is no room for a separate flag
-  if (threadIdx.x == 0) T[0] = 0u;
-  __syncthreads();
-  if (!same) T[0] = 1u;
-  __syncthreads();
-  const bool shared = T[0] == 0u;
-  __syncthreads();
-  if (shared) U.store(lds);
-  else LaySplit::build<NT, E>(lds, luts);
-  __syncthreads();
-  return shared;
+  QuadTableBuild<NT, E> b;
+  b.load(luts);
+  return b.finish(T, luts);
 }
 
 template <int NT>

@@ -74,11 +74,14 @@ template <> struct RowsCfg<4> { static constexpr int RG = PP_ROWS4_RG, NSEG = PP
 template <> struct RowsCfg<8> { static constexpr int RG = 1, NSEG = 2, NT = 512; };
 
 struct QuadRowsArgs {
-  // single-projection front end (segs == nullptr): wave w owns row tasks
-  // [w*n_tasks/n_waves, (w+1)*n_tasks/n_waves) of `proj`
+  // one-Linear front end (segs == nullptr): the tasks of `proj`, cut into `parts` column
+  // slices of whole chunks, dealt to the waves by direct_item
   pp_quad_proj proj;
   int64_t o_sn;
   int64_t n_tasks;
+  int parts, n_chunks;       // column slices; chunks of the K columns
+  float* acc;                // parts > 1: accumulators [4][M][N] (zero on entry, left zero)
+  uint32_t* cnt;             // parts > 1: one arrival counter per task (zero on entry, left zero)
   const int64_t* wave_plug;  // plug start of each wave's first row (n_waves + 1), or null
   // stream front end
   const pp_quad_proj* projs;
@@ -568,6 +571,22 @@ struct SegRunner {
     }
     finish_pending();
   }
+
+  // The same walk when the caller has already issued the first chunk into c0 (with this
+  // runner's lane offsets): the first task's plug positions are requested, then the loop.
+  __device__ __forceinline__ void run_issued(Chunk<MT, RG, NSEG>& c0) {
+    Chunk<MT, RG, NSEG> c1;
+    Cursor cur = {0, 0};
+    vload32(P.idx, 4u * lane, plug_idx_rsrc(A, pc));
+    Cursor nx = lc;                    // the load cursor past the first chunk, as prefetch(c0) leaves it
+    advance(nx);
+    if (nx.ti < ntask) lc = nx;
+    for (;;) {
+      if (!step(cur, c0, c1)) break;
+      if (!step(cur, c1, c0)) break;
+    }
+    finish_pending();
+  }
 };
 
 // Segment context of rows [row0, row1) of projection P.  Every field goes through
@@ -605,18 +624,6 @@ __device__ __forceinline__ void seg_ctx(const pp_quad_proj& P, int64_t o_sn, int
 template <int MT, class L, bool SPLIT>
 __device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A, int64_t gw, int64_t s0, int64_t s1) {
   constexpr int RG = RowsCfg<MT>::RG, NSEG = RowsCfg<MT>::NSEG;
-  constexpr int WAVES = RowsCfg<MT>::NT / 64;
-  const int64_t nw = (int64_t)gridDim.x * WAVES;
-  if (A.segs == nullptr) {
-    const int64_t t0 = gw * A.n_tasks / nw, t1 = (gw + 1) * A.n_tasks / nw;
-    const int row0 = (int)std::min<int64_t>(t0 * RG, A.proj.N), row1 = (int)std::min<int64_t>(t1 * RG, A.proj.N);
-    if (row1 <= row0) return;
-    SegCtx S;
-    seg_ctx(A.proj, A.o_sn, row0, row1, A.M, S);
-    SegRunner<MT, RG, NSEG, L, false> R(lds, A, S, A.wave_plug ? uniform64(A.wave_plug[gw]) : 0);
-    R.run();
-    return;
-  }
   for (int64_t si = s0; si < s1; ++si) {
     const pp_quad_seg g = A.segs[si];
     SegCtx S;
@@ -636,15 +643,74 @@ __device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A
   }
 }
 
+// The one-Linear front end.  Its first chunk needs no descriptor, so the wave issues it
+// before the table build and the round trip to HBM runs under the build: first the plug
+// start of its first row (so that waiting for it waits for nothing else), then the LUT
+// loads, then the first chunk; the build waits for the LUT values only.
+template <int MT, typename E, bool SPLIT>
+__device__ __forceinline__ void direct_body(uint32_t* T, const QuadRowsArgs& A, int64_t gw) {
+  constexpr int RG = RowsCfg<MT>::RG, NSEG = RowsCfg<MT>::NSEG, NT = RowsCfg<MT>::NT;
+  const int lane = threadIdx.x & 63;
+  const int64_t W = (int64_t)gridDim.x * (NT / 64);
+  u32x2 wp = {0u, 0u};
+  if (A.wave_plug != nullptr) vload64(wp, 8u * (uint32_t)gw, make_rsrc(A.wave_plug, 8u * (uint32_t)(W + 1)));
+  QuadTableBuild<NT, E> tb;
+  tb.load(A.luts);
+  const int K = uniform(A.proj.K), N = uniform(A.proj.N);
+  const DirectItem d = direct_item<NT / 64>((uint32_t)gw, (uint32_t)W, (uint32_t)uniform64(A.n_tasks),
+                                           (uint32_t)uniform(A.parts), (uint32_t)uniform(A.n_chunks), NSEG * QSEG,
+                                           (uint32_t)K);
+  SegCtx S;
+  seg_ctx(A.proj, A.o_sn, min(d.t0 * RG, N), min(d.t1 * RG, N), A.M, S);
+  S.kbeg = uniform(d.kbeg);
+  S.kend = uniform(d.kend);
+  if (SPLIT && uniform(A.parts) > 1) {
+    S.parts = uniform(A.parts);
+    S.acc = uniform_ptr(A.acc);
+    S.cnt = uniform_ptr(A.cnt) + d.t0;
+  }
+  const bool busy = S.nrows > 0 && S.kend > S.kbeg;
+  uint32_t voff[RG];
+#pragma unroll
+  for (int r = 0; r < RG; ++r) voff[r] = 4u * (uint32_t)(r * S.ldc) + 16u * lane;
+  Chunk<MT, RG, NSEG> c0;
+  if (busy) chunk_issue<MT, RG, NSEG>(S, 0, S.kbeg, voff, lane, c0);   // 1 us faster than after the build
+  const bool shared = tb.finish(T, A.luts);
+  if (!busy) return;
+  // the caller's plan, kept inside the table whatever it holds (a stale plan must not send
+  // the plug loads outside it)
+  const int64_t pc = std::min<int64_t>(std::max<int64_t>(uniform64((int64_t)(((uint64_t)wp[1] << 32) | wp[0])), 0),
+                                       A.plug_n);
+  const char* lds = reinterpret_cast<const char*>(T);
+  if (shared) {
+    SegRunner<MT, RG, NSEG, LayShared, SPLIT> R(lds, A, S, pc);
+    R.run_issued(c0);
+  } else {
+    SegRunner<MT, RG, NSEG, LaySplit, SPLIT> R(lds, A, S, pc);
+    R.run_issued(c0);
+  }
+}
+
+// The whole-stream launch (segments from the planner's tables).
 template <int MT, bool SPLIT>
 __global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_rows_kernel(const QuadRowsArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t T[QLDS_BYTES / 4];
   const char* lds = reinterpret_cast<const char*>(T);
   const int64_t gw = (int64_t)blockIdx.x * (RowsCfg<MT>::NT / 64) + uniform(threadIdx.x >> 6);
   SegRange sr;
-  if (A.segs != nullptr) sr.issue(A.seg_bounds, gw, (int64_t)gridDim.x * (RowsCfg<MT>::NT / 64));
+  sr.issue(A.seg_bounds, gw, (int64_t)gridDim.x * (RowsCfg<MT>::NT / 64));
   if (quad_tables<RowsCfg<MT>::NT>(T, A.luts)) rows_body<MT, LayShared, SPLIT>(lds, A, gw, sr.lo(), sr.hi());
   else rows_body<MT, LaySplit, SPLIT>(lds, A, gw, sr.lo(), sr.hi());
+}
+
+// One Linear (segs == nullptr): a kernel of its own, so that the whole-stream kernel keeps
+// its register allocation.
+template <int MT, bool SPLIT>
+__global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_direct_kernel(const QuadRowsArgs A) {
+  __shared__ __attribute__((aligned(16))) uint32_t T[QLDS_BYTES / 4];
+  const int64_t gw = (int64_t)blockIdx.x * (RowsCfg<MT>::NT / 64) + uniform(threadIdx.x >> 6);
+  if (A.luts.dtype == PP_F16) direct_body<MT, f16, SPLIT>(T, A, gw);
+  else direct_body<MT, float, SPLIT>(T, A, gw);
 }
 
 // ------------------------------------------------------------------ tail rows
@@ -737,13 +803,22 @@ __global__ __launch_bounds__(256) void quad_tail_kernel(const QuadTailArgs A) {
   }
 }
 
-// Plug start of each wave's first row: first entry with idx >= pos0 + row(g)*ldc, where
-// wave g starts at task g*n_tasks/n_waves (rows_per_task rows each).
+// Plug start of each wave's first row (one-Linear front end): the first entry with
+// idx >= pos0 + row*ldc, row the first row of direct_item(g); entry n_waves: the end of the
+// rows.  One thread per wave, a binary search over the ascending positions.
+template <int G>
 __global__ void wave_plug_kernel(const uint32_t* plug_idx, int64_t plug_n, int64_t pos0, int64_t ldc,
-                                 int rows_per_task, int64_t n_tasks, int64_t n_waves, int N, int64_t* wave_plug) {
+                                 int rows_per_task, int64_t n_tasks, int parts, int n_chunks, int chunk, int K,
+                                 int64_t n_waves, int N, int64_t* wave_plug) {
   const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (g > n_waves) return;
-  const int64_t row = std::min<int64_t>(g * n_tasks / n_waves * rows_per_task, N);
+  int64_t row = N;
+  if (g < n_waves)
+    row = std::min<int64_t>((int64_t)direct_item<G>((uint32_t)g, (uint32_t)n_waves, (uint32_t)n_tasks, (uint32_t)parts,
+                                                     (uint32_t)n_chunks, (uint32_t)chunk, (uint32_t)K)
+                                    .t0 *
+                                rows_per_task,
+                            N);
   const int64_t key = pos0 + row * ldc;
   int64_t lo = 0, hi = plug_n;
   while (lo < hi) {
@@ -777,6 +852,15 @@ static int cfg_waves(int mt) {
 template <bool SPLIT>
 static void launch_rows_t(const QuadRowsArgs& A, int mt, hipStream_t st) {
   const unsigned grid = (unsigned)device_cu_count();
+  if (A.segs == nullptr) {
+    switch (mt) {
+      case 1: hipLaunchKernelGGL((quad_direct_kernel<1, SPLIT>), dim3(grid), dim3(RowsCfg<1>::NT), 0, st, A); break;
+      case 2: hipLaunchKernelGGL((quad_direct_kernel<2, SPLIT>), dim3(grid), dim3(RowsCfg<2>::NT), 0, st, A); break;
+      case 4: hipLaunchKernelGGL((quad_direct_kernel<4, SPLIT>), dim3(grid), dim3(RowsCfg<4>::NT), 0, st, A); break;
+      default: hipLaunchKernelGGL((quad_direct_kernel<8, SPLIT>), dim3(grid), dim3(RowsCfg<8>::NT), 0, st, A); break;
+    }
+    return;
+  }
   switch (mt) {
     case 1: hipLaunchKernelGGL((quad_rows_kernel<1, SPLIT>), dim3(grid), dim3(RowsCfg<1>::NT), 0, st, A); break;
     case 2: hipLaunchKernelGGL((quad_rows_kernel<2, SPLIT>), dim3(grid), dim3(RowsCfg<2>::NT), 0, st, A); break;
@@ -785,9 +869,10 @@ static void launch_rows_t(const QuadRowsArgs& A, int mt, hipStream_t st) {
   }
 }
 
-// The stream launch with a workspace runs the kernel that also takes split segments.
+// The stream launch with a workspace, and a one-Linear launch cut into column slices, run
+// the kernel that also takes split segments.
 static int launch_rows(const QuadRowsArgs& A, int mt, hipStream_t st) {
-  if (A.ws != nullptr) launch_rows_t<true>(A, mt, st);
+  if (A.segs != nullptr ? A.ws != nullptr : A.parts > 1) launch_rows_t<true>(A, mt, st);
   else launch_rows_t<false>(A, mt, st);
   PP_LAUNCH_CHECK();
   return PP_OK;
@@ -808,24 +893,43 @@ bool quad_rows_ok(const void* a, int64_t a_sm, int64_t a_sk, const uint32_t* cod
          N * c_sn < (1ll << 29) && (M - 1) * a_sm + K < (1ll << 30);
 }
 
-int64_t quad_rows_workspace(int64_t M, int64_t N, int64_t plug_n) {
-  if (plug_n <= 0) return 0;
-  const int mt = round_mt(M);
-  const int64_t waves = (int64_t)device_cu_count() * cfg_waves(mt);
-  return ((waves + 1) * 8 + 255) / 256 * 256;
+static int cfg_chunk(int mt) {
+  switch (mt) {
+    case 1: return RowsCfg<1>::NSEG * QSEG;
+    case 2: return RowsCfg<2>::NSEG * QSEG;
+    case 4: return RowsCfg<4>::NSEG * QSEG;
+    default: return RowsCfg<8>::NSEG * QSEG;
+  }
 }
 
-int quad_rows_single(const void* a, int64_t a_sm, const uint32_t* codes, int64_t ldc, const void* const* luts,
-                     int lut_dtype, const float* scales, const uint32_t* plug_idx, const void* plug_vals,
-                     int64_t plug_n, int64_t elem_base, void* const* out, int64_t o_sm, int64_t o_sn, int64_t M,
-                     int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, hipStream_t st) {
-  const int mt = round_mt(M);
-  const int rg = cfg_rg(mt);
-  const int64_t waves = (int64_t)device_cu_count() * cfg_waves(mt);
-  const int64_t need = quad_rows_workspace(M, N, plug_n);
-  PP_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr), "workspace too small: need %lld bytes",
-             (long long)need);
-  QuadRowsArgs A = {};
+// How one Linear runs on the row kernel: T tasks of rg rows, cut into `parts` column slices
+// of whole chunks when the tasks are too few for the launch's W wavefronts (direct_parts:
+// gate 11008x2048 at one token, 1,376 tasks, runs whole rows; down 2048x11008 in 4 slices).
+// The split workspace holds one arrival counter per task (256-byte aligned), then float32
+// accumulators [4][M][N].
+struct DirectPlan {
+  int mt, rg, chunk, parts, n_chunks;
+  int64_t n_tasks, waves, cnt_bytes, split_bytes;
+};
+static DirectPlan direct_plan(int64_t M, int64_t N, int64_t K, bool split) {
+  DirectPlan p;
+  p.mt = round_mt(M);
+  p.rg = cfg_rg(p.mt);
+  p.chunk = cfg_chunk(p.mt);
+  p.waves = (int64_t)device_cu_count() * cfg_waves(p.mt);
+  p.n_tasks = (N + p.rg - 1) / p.rg;
+  p.n_chunks = (int)std::max<int64_t>(1, (K + p.chunk - 1) / p.chunk);
+  p.parts = split ? direct_parts(p.n_tasks, p.waves, p.n_chunks) : 1;
+  p.cnt_bytes = p.parts > 1 ? (p.n_tasks * 4 + 255) / 256 * 256 : 0;
+  p.split_bytes = p.parts > 1 ? p.cnt_bytes + 4 * 4 * M * N : 0;
+  return p;
+}
+
+static void direct_args(QuadRowsArgs& A, const DirectPlan& p, const void* a, int64_t a_sm, const uint32_t* codes,
+                        int64_t ldc, const void* const* luts, int lut_dtype, const float* scales,
+                        const uint32_t* plug_idx, const void* plug_vals, const uint32_t* plug_code, int64_t plug_n,
+                        int64_t elem_base, void* const* out, int64_t o_sm, int64_t o_sn, int64_t M, int64_t N,
+                        int64_t K) {
   A.proj.codes = codes;
   A.proj.ldc = ldc;
   A.proj.pos0 = elem_base;
@@ -836,21 +940,56 @@ int quad_rows_single(const void* a, int64_t a_sm, const uint32_t* codes, int64_t
   A.proj.N = (int32_t)N;
   A.proj.K = (int32_t)K;
   A.o_sn = o_sn;
-  A.n_tasks = (N + rg - 1) / rg;
+  A.n_tasks = p.n_tasks;
+  A.parts = p.parts;
+  A.n_chunks = p.n_chunks;
   A.luts = make_luts(luts, lut_dtype);
   for (int m = 0; m < 4; ++m) A.s[m] = scales[m];
   A.plug_idx = plug_idx;
   A.plug_vals = reinterpret_cast<const f16*>(plug_vals);
+  A.plug_code = plug_code;
   A.plug_n = plug_n;
   A.M = (int)M;
+}
+
+static int launch_wave_plug(const DirectPlan& p, const uint32_t* plug_idx, int64_t plug_n, int64_t elem_base,
+                            int64_t ldc, int64_t N, int64_t K, int64_t* wave_plug, hipStream_t st) {
+  static_assert(RowsCfg<1>::NT == RowsCfg<2>::NT && RowsCfg<1>::NT == RowsCfg<4>::NT && RowsCfg<1>::NT == RowsCfg<8>::NT,
+                "one workgroup size for the one-Linear launches");
+  hipLaunchKernelGGL(wave_plug_kernel<RowsCfg<1>::NT / 64>, dim3((unsigned)((p.waves + 1 + 255) / 256)), dim3(256), 0,
+                     st, plug_idx, plug_n, elem_base, ldc, p.rg, p.n_tasks, p.parts, p.n_chunks, p.chunk, (int)K,
+                     p.waves, (int)N, wave_plug);
+  PP_LAUNCH_CHECK();
+  return PP_OK;
+}
+
+int64_t quad_rows_workspace(int64_t M, int64_t N, int64_t plug_n) {
+  if (plug_n <= 0) return 0;
+  const int mt = round_mt(M);
+  const int64_t waves = (int64_t)device_cu_count() * cfg_waves(mt);
+  return ((waves + 1) * 8 + 255) / 256 * 256;
+}
+
+// pp_quad_gemm's route: whole rows (any workspace content; the plug starts are found in
+// the workspace by a first launch).
+int quad_rows_single(const void* a, int64_t a_sm, const uint32_t* codes, int64_t ldc, const void* const* luts,
+                     int lut_dtype, const float* scales, const uint32_t* plug_idx, const void* plug_vals,
+                     int64_t plug_n, int64_t elem_base, void* const* out, int64_t o_sm, int64_t o_sn, int64_t M,
+                     int64_t N, int64_t K, void* workspace, int64_t workspace_bytes, hipStream_t st) {
+  const DirectPlan p = direct_plan(M, N, K, false);
+  PP_REQUIRE(p.waves < (1 << 16), "the one-Linear launch deals at most 65,535 wavefronts");
+  const int64_t need = quad_rows_workspace(M, N, plug_n);
+  PP_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr), "workspace too small: need %lld bytes",
+             (long long)need);
+  QuadRowsArgs A = {};
+  direct_args(A, p, a, a_sm, codes, ldc, luts, lut_dtype, scales, plug_idx, plug_vals, nullptr, plug_n, elem_base,
+              out, o_sm, o_sn, M, N, K);
   if (plug_n > 0) {
     int64_t* wp = reinterpret_cast<int64_t*>(workspace);
-    hipLaunchKernelGGL(wave_plug_kernel, dim3((unsigned)((waves + 1 + 255) / 256)), dim3(256), 0, st, plug_idx,
-                       plug_n, elem_base, ldc, rg, A.n_tasks, waves, (int)N, wp);
-    PP_LAUNCH_CHECK();
+    if (int rc = launch_wave_plug(p, plug_idx, plug_n, elem_base, ldc, N, K, wp, st)) return rc;
     A.wave_plug = wp;
   }
-  return launch_rows(A, mt, st);
+  return launch_rows(A, p.mt, st);
 }
 
 }  // namespace pp
@@ -878,6 +1017,57 @@ extern "C" int pp_quad_stream_chunk(int64_t M) {
 extern "C" int64_t pp_quad_stream_waves(int64_t M) {
   if (M < 1 || M > 8) return 0;
   return (int64_t)device_cu_count() * cfg_waves(round_mt(M));
+}
+
+extern "C" int64_t pp_quad_rows_plan_size(int64_t M) {
+  if (M < 1 || M > 8) return 0;
+  return (int64_t)device_cu_count() * cfg_waves(round_mt(M)) + 1;
+}
+
+extern "C" int64_t pp_quad_rows_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > 8 || N < 1 || K < 1) return 0;
+  return direct_plan(M, N, K, true).split_bytes;
+}
+
+extern "C" int pp_quad_rows_plan(const uint32_t* plug_idx, int64_t plug_n, int64_t elem_base, int64_t ldc, int64_t M,
+                                 int64_t N, int64_t K, int64_t* wave_plug, void* stream) {
+  PP_REQUIRE(M >= 1 && M <= 8, "the row kernel takes 1..8 tokens, got %lld", (long long)M);
+  PP_REQUIRE(N >= 1 && K >= 1 && ldc >= K && N < (1ll << 31) && K < (1ll << 31), "bad shape");
+  PP_REQUIRE(plug_n >= 0 && (plug_n == 0 || plug_idx != nullptr) && wave_plug != nullptr, "null pointer argument");
+  const DirectPlan p = direct_plan(M, N, K, true);
+  PP_REQUIRE(p.waves < (1 << 16), "the one-Linear launch deals at most 65,535 wavefronts");
+  return launch_wave_plug(p, plug_idx, plug_n, elem_base, ldc, N, K, wave_plug, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int pp_quad_rows(const void* a, int64_t a_sm, const uint32_t* codes, int64_t ldc, const void* const* luts,
+                            int lut_dtype, const float* scales, const uint32_t* plug_idx, const void* plug_vals,
+                            const uint32_t* plug_code, int64_t plug_n, const int64_t* wave_plug, int64_t elem_base,
+                            void* const* out, int64_t o_sm, int64_t o_sn, int64_t M, int64_t N, int64_t K,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
+  PP_REQUIRE(luts != nullptr && scales != nullptr && out != nullptr, "null pointer argument");
+  for (int i = 0; i < 7; ++i) PP_REQUIRE(luts[i] != nullptr, "lut %d is null", i);
+  for (int m = 0; m < 4; ++m) PP_REQUIRE(out[m] != nullptr, "out[%d] is null", m);
+  PP_REQUIRE(lut_dtype == PP_F16 || lut_dtype == PP_F32, "bad lut_dtype");
+  PP_REQUIRE(quad_rows_ok(a, a_sm, 1, codes, 1, ldc, M, N, K),
+             "the row kernel needs 1..8 tokens of contiguous fp16 activations (8-byte aligned, row stride a "
+             "multiple of 4) and 16-byte aligned (N,K) rows of ldc >= K words (a multiple of 4)");
+  PP_REQUIRE(N < (1ll << 31) && o_sn >= 1 && (M == 1 || o_sm >= 1), "bad output strides");
+  PP_REQUIRE(plug_n >= 0 && (plug_n == 0 || (plug_idx && plug_vals && wave_plug)),
+             "plug entries need plug_idx, plug_vals and a wave_plug plan (pp_quad_rows_plan)");
+  const DirectPlan p = direct_plan(M, N, K, true);
+  PP_REQUIRE(p.waves < (1 << 16), "the one-Linear launch deals at most 65,535 wavefronts");
+  PP_REQUIRE(p.split_bytes == 0 || (workspace != nullptr && workspace_bytes >= p.split_bytes),
+             "workspace too small: need %lld bytes (pp_quad_rows_workspace_size), zero on entry",
+             (long long)p.split_bytes);
+  QuadRowsArgs A = {};
+  direct_args(A, p, a, a_sm, codes, ldc, luts, lut_dtype, scales, plug_idx, plug_vals, plug_code, plug_n, elem_base,
+              out, o_sm, o_sn, M, N, K);
+  A.wave_plug = plug_n > 0 ? wave_plug : nullptr;
+  if (p.parts > 1) {
+    A.cnt = reinterpret_cast<uint32_t*>(workspace);
+    A.acc = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.cnt_bytes);
+  }
+  return launch_rows(A, p.mt, reinterpret_cast<hipStream_t>(stream));
 }
 
 // Side table of the plug entries: code[j] = the code word at stream position plug_idx[j]

@@ -137,4 +137,55 @@ struct Cursor {
   int ti, ck;
 };
 
+// One-Linear launches (quad_rows.hip, dual_rows.hip): wave gw's column slice and run of row
+// tasks, from the launch shape alone (no descriptor to read).  The slices take whole chunks,
+// dealt as evenly as possible (slice s: chunks [s*C/parts, (s+1)*C/parts)); the waves are dealt
+// to the slices alike (slice s: waves [s*W/parts, (s+1)*W/parts)).  A slice with at least as
+// many tasks as waves gives its j-th wave q or q + 1 of its T tasks (q = T / nw, the first
+// T % nw waves one more); one with fewer gives each workgroup the tasks an even spread gives
+// its waves, one per wave from its lowest slot (slots 0 .. G/2-1 are on distinct SIMDs).
+// 32-bit arithmetic (W < 2^16, T < 2^31, parts * C < 2^31): the wave computes this before
+// issuing its first chunk, and 64-bit divisions there cost ~1,200 instructions.
+struct DirectItem {
+  int t0, t1, kbeg, kend;
+};
+template <int G>
+__device__ __host__ __forceinline__ DirectItem direct_item(uint32_t gw, uint32_t W, uint32_t T, uint32_t parts,
+                                                           uint32_t n_chunks, uint32_t chunk, uint32_t K) {
+  const uint32_t s = ((gw + 1) * parts - 1) / W;      // the slice whose waves hold gw
+  const uint32_t w0 = s * W / parts, w1 = (s + 1) * W / parts;
+  const uint32_t j = gw - w0, nw = w1 - w0;
+  DirectItem d;
+  if (T >= nw) {
+    const uint32_t q = T / nw, r = T - q * nw;
+    d.t0 = (int)(j * q + std::min(j, r));
+    d.t1 = d.t0 + (int)(q + (j < r ? 1u : 0u));
+  } else {
+    // each workgroup takes the tasks an even spread gives its waves, on its lowest slots
+    // (gate_proj 11008x2048 at one token, 1,376 tasks for 2,048 waves: 22.9 us; 23.0 with the
+    // tasks spread over the slots too; 27.6 with all first half-waves taken before any second
+    // one, which gives a third of the workgroups twice the tasks of the rest)
+    const uint32_t g0 = gw / G * G;
+    const uint32_t a = std::max(g0, w0) - w0, b = std::min(g0 + G, w1) - w0;
+    const uint32_t fa = a * T / nw, fb = b * T / nw, p = j - a;
+    d.t0 = (int)std::min(fa + p, fb);
+    d.t1 = (int)std::min(fa + p + 1, fb);
+  }
+  d.kbeg = (int)(s * n_chunks / parts * chunk);
+  d.kend = (int)std::min<uint32_t>(K, (s + 1) * n_chunks / parts * chunk);
+  return d;
+}
+
+// Column slices of one Linear's T row tasks for W wavefronts and C chunks (the stream
+// planner's rule, stream.split_factors): r = W / T; r < 1.5 whole rows; 1.5 <= r < 4 two
+// slices when K holds at least 8 chunks; r >= 4 ceil(r / 2) slices, at most one per chunk.
+inline int direct_parts(int64_t T, int64_t W, int64_t C) {
+  int64_t want = 1;
+  if (T > 0) {
+    if (W >= 4 * T) want = (W + 2 * T - 1) / (2 * T);
+    else if (2 * W >= 3 * T) want = C >= 8 ? 2 : 1;
+  }
+  return (int)std::max<int64_t>(1, std::min<int64_t>(want, C));
+}
+
 }  // namespace pp

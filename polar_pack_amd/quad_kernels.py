@@ -24,8 +24,11 @@ bounds the time.
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 import math
+import threading
+import weakref
 
 import torch
 
@@ -33,6 +36,7 @@ from . import _native as nat
 from . import plugs, routes
 
 MU = 255.0   # quad_kernels.py:13
+_plans_lock = threading.Lock()
 
 
 def _u32_words(nq, q1, q2, q3):
@@ -161,7 +165,9 @@ def quad_bitpacked(a, codes, luts, scales, *, plug=None, elem_base=0, fused=None
                        [o[i0:i1] for o in outs], L, dev)
     elif route == "prefill":
         _quad_prefill(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base), outs, L, dev)
-    else:                                 # rows, kn, generic: pp_quad_gemm picks among them alike
+    elif route == "rows":
+        _quad_rows(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, int(elem_base), outs, L, dev)
+    else:                                 # kn, generic: pp_quad_gemm picks among them alike
         _quad_gemm(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, int(elem_base), outs, L, dev)
     del keep
     return outs
@@ -173,6 +179,71 @@ def quad_call_route(codes, M, plug_n=0, fused=None):
     K, N = codes.shape
     caps = routes.quad_storage(codes.stride(0), codes.stride(1), codes.data_ptr(), K, N, plug_n)
     return routes.quad_route(M, K, N, caps, plug_n > 0, fused)
+
+
+# Plans of the row kernel's one-Linear launches (pp_quad_rows): per plug table (the sorted
+# copy plugs.ascending returns, checked by identity and version), position, shape and token
+# count, the range [lo, hi) of the table's entries inside the Linear's rows and each
+# wavefront's first entry (pp_quad_rows_plan over that range).  Made once, on the first call
+# outside stream capture (finding the range reads two numbers back from the device).
+_ROWS_PLANS = collections.OrderedDict()
+_ROWS_PLANS_MAX = 2048
+
+
+def _rows_plan(idx, pn, elem_base, ldc, M, N, K, L, dev):
+    """(lo, hi, wave_plug) for the plug entries of an (N,K) Linear at ``elem_base``."""
+    key = (id(idx), elem_base, ldc, M, N, K)
+    with _plans_lock:
+        hit = _ROWS_PLANS.get(key)
+        if hit is not None:
+            ref, ver, plan = hit
+            if ref() is idx and idx._version == ver:
+                _ROWS_PLANS.move_to_end(key)
+                return plan
+    capturing = torch.cuda.is_current_stream_capturing()
+    if capturing:
+        lo, hi = 0, pn                    # no host read-back under capture: the whole table
+    else:
+        pos = idx.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+        bounds = torch.tensor([elem_base, elem_base + (N - 1) * ldc + K], dtype=torch.int64, device=dev)
+        lo, hi = (int(v) for v in torch.searchsorted(pos, bounds).tolist())
+    wave_plug = torch.empty(int(L.pp_quad_rows_plan_size(M)), dtype=torch.int64, device=dev)
+    if hi > lo:
+        nat.check(L.pp_quad_rows_plan(idx.data_ptr() + 4 * lo, hi - lo, elem_base, ldc, M, N, K, wave_plug.data_ptr(),
+                                      nat.raw_stream(dev)), "pp_quad_rows_plan")
+    plan = (lo, hi, wave_plug)
+    if not capturing:
+        with _plans_lock:
+            _ROWS_PLANS[key] = (weakref.ref(idx), idx._version, plan)
+            while len(_ROWS_PLANS) > _ROWS_PLANS_MAX:
+                _ROWS_PLANS.popitem(last=False)
+    return plan
+
+
+def _quad_rows(a, codes, lut_ptrs, lut_dtype, sc, keep, pn, elem_base, outs, L, dev):
+    """(N,K) rows at 1-8 tokens: the row kernel's one-Linear launch (pp_quad_rows), with its
+    plan (the Linear's slice of the plug table and each wavefront's first entry) cached per
+    plug table, and column slices meeting in the stream's zeroed workspace."""
+    M, K = a.shape
+    N = codes.shape[1]
+    ldc = codes.stride(1)
+    if a.stride(1) != 1 or a.data_ptr() % 16 or (M > 1 and a.stride(0) % 8):
+        a = a.contiguous()
+    lo = hi = 0
+    wave_plug = None
+    if pn:
+        lo, hi, wave_plug = _rows_plan(keep[0], pn, elem_base, ldc, M, N, K, L, dev)
+    ws_bytes = L.pp_quad_rows_workspace_size(M, N, K)
+    ws, wkey = nat.zero_workspace(dev, ws_bytes)
+    n = hi - lo
+    rc = L.pp_quad_rows(a.data_ptr(), a.stride(0), codes.data_ptr(), ldc, lut_ptrs, lut_dtype, sc,
+                        keep[0].data_ptr() + 4 * lo if n else None, keep[1].data_ptr() + 8 * lo if n else None,
+                        None, n, wave_plug.data_ptr() if n else None, elem_base,
+                        nat.ptr_array([o.data_ptr() for o in outs]), outs[0].stride(0), outs[0].stride(1),
+                        M, N, K, ws.data_ptr() if ws is not None else None, ws_bytes, nat.raw_stream(dev))
+    if rc:
+        nat.drop_workspace(wkey)
+    nat.check(rc, "pp_quad_rows")
 
 
 def _quad_gemm(a, codes, lut_ptrs, lut_dtype, sc, pi, pv, pn, elem_base, outs, L, dev):

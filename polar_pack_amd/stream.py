@@ -327,10 +327,14 @@ class QuadStream:
     workspace owned by this object (so two launches of one QuadStream must not overlap).
     ``wave_weights``: per-wave shares of the work ("slots": :func:`slot_weights`; None:
     equal bytes); ``task_cost``: bytes charged per task for its reduction and stores.
+    ``one_linear``: a single projection wholly inside the codes runs the row kernel's
+    one-Linear launch (``pp_quad_rows``: the waves find their rows and column slice from the
+    launch shape, with no segment table to read), except at one token with column slices,
+    where the segment plan measured faster; False keeps the segment plan.
     """
 
     def __init__(self, pack: QuadPackDevice, shapes: Sequence[Tuple[int, int]], M: int = 1, split: bool = True,
-                 positions=None, wave_weights="slots", task_cost=0):
+                 positions=None, wave_weights="slots", task_cost=0, one_linear: bool = True):
         L = nat.lib()
         self.pack = pack
         self.shapes = [(int(n), int(k)) for n, k in shapes]
@@ -349,6 +353,18 @@ class QuadStream:
                 raise ValueError(f"stream decode needs K % 4 == 0 (got N={n}, K={k})")
         plug = pack.plug_host()
         self.n_waves = int(L.pp_quad_stream_waves(self.M))
+        # one Linear wholly inside the codes: the row kernel's one-Linear launch (pp_quad_rows),
+        # which needs no segment table (its waves find their rows from the launch shape).  At one
+        # token with column slices the segment plan is kept: measured interleaved, down_proj
+        # 2048x11008 at one token 30.3 us on the segment plan against 34-35 us on the one-Linear
+        # launch, whatever its deal; gate_proj (whole rows) 22.9 against 25.3 us, and down at 2 / 4
+        # tokens 28.3 / 31.7 against 34.3 / 39.9 us, go to the one-Linear launch
+        sliced_one_token = self.M == 1 and self.shapes and \
+            int(L.pp_quad_rows_workspace_size(self.M, *self.shapes[0])) > 0
+        self.direct = one_linear and len(self.shapes) == 1 and total <= pack.n and split and not sliced_one_token
+        if self.direct:
+            self._plan_direct(plug)
+            return
         if isinstance(wave_weights, str) and wave_weights == "slots":
             wave_weights = slot_weights(self.n_waves, _waves_per_group(self.n_waves, self.device))
         self.segs_np, self.bounds_np, ws_bytes = plan_segments(
@@ -377,6 +393,35 @@ class QuadStream:
             rc = L.pp_quad_plug_codes(pack.codes.data_ptr(), pack.n, pack.plug_idx.data_ptr(), P,
                                       self.plug_code.data_ptr(), nat.raw_stream(dev))
             nat.check(rc, "pp_quad_plug_codes")
+        self.projs = None
+
+    def _plan_direct(self, plug):
+        """The plan of a one-Linear launch: the Linear's slice of the plug table, each
+        wavefront's first entry in it (pp_quad_rows_plan), the entries' code words
+        (pp_quad_plug_codes) and the zeroed column-slice workspace."""
+        L = nat.lib()
+        pk, dev = self.pack, self.device
+        (N, K), pos0 = self.shapes[0], int(self.pos0[0])
+        self.plug_lo = int(np.searchsorted(plug, pos0, side="left"))
+        self.plug_hi = int(np.searchsorted(plug, pos0 + N * K, side="left"))
+        n = self.plug_hi - self.plug_lo
+        stream = nat.raw_stream(dev)
+        self.wave_plug = torch.zeros(int(L.pp_quad_rows_plan_size(self.M)), dtype=torch.int64, device=dev)
+        self.plug_code = torch.zeros(max(n, 1), dtype=torch.int32, device=dev)
+        if n:
+            idx = pk.plug_idx.data_ptr() + 4 * self.plug_lo
+            nat.check(L.pp_quad_rows_plan(idx, n, pos0, K, self.M, N, K, self.wave_plug.data_ptr(), stream),
+                      "pp_quad_rows_plan")
+            nat.check(L.pp_quad_plug_codes(pk.codes.data_ptr(), pk.n, idx, n, self.plug_code.data_ptr(), stream),
+                      "pp_quad_plug_codes")
+        ws_bytes = int(L.pp_quad_rows_workspace_size(self.M, N, K))
+        self.workspace = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
+        self._ws_bytes = ws_bytes
+        self.split = ws_bytes > 0
+        self.n_segs = self.n_tail = 0
+        self.luts = header_luts(pk.r_max, device=dev)
+        self._lut_ptrs = nat.ptr_array([t.data_ptr() for t in self.luts])
+        self._scales = nat.float_array(pk.s)
         self.projs = None
 
     @classmethod
@@ -423,10 +468,30 @@ class QuadStream:
             tab[p]["K"] = K
         self.projs = torch.from_numpy(tab.view(np.uint8).copy()).to(self.device)
         self._bound = (xs, outs)          # keep the buffers alive while bound
+        if self.direct:
+            self._out_ptrs = nat.ptr_array([t.data_ptr() for t in outs[0]])
+
+    def _call_direct(self):
+        pk = self.pack
+        (N, K), pos0 = self.shapes[0], int(self.pos0[0])
+        xs, outs = self._bound
+        n = self.plug_hi - self.plug_lo
+        rc = nat.lib().pp_quad_rows(xs[0].data_ptr(), xs[0].stride(0), pk.codes.data_ptr() + 4 * pos0, K,
+                                    self._lut_ptrs, nat.PP_F32, self._scales,
+                                    pk.plug_idx.data_ptr() + 4 * self.plug_lo if n else None,
+                                    pk.plug_vals.data_ptr() + 8 * self.plug_lo if n else None,
+                                    self.plug_code.data_ptr() if n else None, n,
+                                    self.wave_plug.data_ptr() if n else None, pos0, self._out_ptrs,
+                                    outs[0][0].stride(0), 1, self.M, N, K,
+                                    self.workspace.data_ptr() if self.workspace is not None else None,
+                                    self._ws_bytes, nat.raw_stream(self.device))
+        nat.check(rc, "pp_quad_rows")
 
     def __call__(self):
         if self.projs is None:
             raise RuntimeError("QuadStream.bind() must be called before launching")
+        if self.direct:
+            return self._call_direct()
         pk = self.pack
         stream = nat.raw_stream(self.device)
         rc = nat.lib().pp_quad_stream(self.projs.data_ptr(), len(self.shapes),
@@ -469,10 +534,13 @@ class DualStream:
     per task of R = ``rows_per_item`` rows (``pp_dual_scale_table``: one load per step for
     all R rows); it applies when chunk_size % group_size == 0 and every projection has
     K % group_size == 0, N % R == 0 and a position that is a multiple of R * group_size.
+    ``one_linear``: a single projection wholly inside the codes runs the stream kernel's
+    one-Linear launch (``pp_dual_rows``: no segment table; its column slices meet in a
+    workspace sized by ``pp_dual_rows_workspace_size``); False keeps the segment plan.
     """
 
     def __init__(self, pack, shapes: Sequence[Tuple[int, int]], M: int = 1, plug_windows=None, split: bool = True,
-                 positions=None, wave_weights="slots", task_cost=0, scale_table=None):
+                 positions=None, wave_weights="slots", task_cost=0, scale_table=None, one_linear: bool = True):
         L = nat.lib()
         self.pack = pack
         self.shapes = [(int(n), int(k)) for n, k in shapes]
@@ -500,8 +568,13 @@ class DualStream:
             block=int(L.pp_dual_stream_chunk(self.M)), positions=self.positions, wave_weights=wave_weights,
             task_cost=task_cost)
         self.split = bool(np.any(self.segs_np["parts"] > 1))
+        self.direct = one_linear and len(self.shapes) == 1 and total <= pack.n_codes and split
+        if self.direct:
+            ws_bytes = int(L.pp_dual_rows_workspace_size(self.M, *self.shapes[0]))
+            self.split = ws_bytes > 0
         # split launches: counters + accumulators, zero once here, left zero by every launch
         self.workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=self.device) if ws_bytes else None
+        self._ws_bytes = ws_bytes
         tails = list(pack.tails) + [None] * (2 - len(pack.tails))
         aligned = pack.n_codes % 8 == 0 and all(t is None or t.numel() == 0 or t.data_ptr() % 16 == 0
                                                 for t in tails)
@@ -610,10 +683,29 @@ class DualStream:
             tab[p]["K"] = K
         self.projs = torch.from_numpy(tab.view(np.uint8).copy()).to(self.device)
         self._bound = (xs, outs)
+        if self.direct:
+            self._proj = nat.DualProj.from_buffer_copy(tab[0].tobytes())
+
+    def _call_direct(self):
+        pk = self.pack
+        amp, cos, sin = self.luts
+        P = int(pk.plug_idx.numel())
+        rc = nat.lib().pp_dual_rows(C.byref(self._proj), self.task_plug.data_ptr(), self.plug_windows,
+                                    self.code_layout, pk.scales.data_ptr(), int(pk.scales.numel()), pk.group_size,
+                                    pk.chunk_size, self.scale_tab.data_ptr() if self.scale_tab is not None else None,
+                                    int(self.scale_tab.numel()) if self.scale_tab is not None else 0,
+                                    amp.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                    pk.plug_idx.data_ptr() if P else None, pk.plug_val.data_ptr() if P else None,
+                                    self.plug_ent.data_ptr() if P else None, P, self.M,
+                                    self.workspace.data_ptr() if self.workspace is not None else None,
+                                    self._ws_bytes, nat.raw_stream(self.device))
+        nat.check(rc, "pp_dual_rows")
 
     def __call__(self):
         if self.projs is None:
             raise RuntimeError("DualStream.bind() must be called before launching")
+        if self.direct:
+            return self._call_direct()
         pk = self.pack
         stream = nat.raw_stream(self.device)
         amp, cos, sin = self.luts

@@ -203,16 +203,19 @@ def test_dual_stream_fp16_tail_rows(M):
 
 
 
+@pytest.mark.parametrize("one_linear", [True, False])
 @pytest.mark.parametrize("shape", [(256, 2048), (64, 11008), (1000, 1000), (2048, 520)])
 @pytest.mark.parametrize("M", [1, 2, 4])
-def test_single_linear_split_k(shape, M):
-    """One projection whose tasks are cut into column slices that meet in the workspace:
-    equal to the oracle on repeated launches, and the workspace is left zero."""
+def test_single_linear_split_k(shape, M, one_linear):
+    """One projection whose tasks are cut into column slices that meet in the workspace, on
+    the one-Linear launch (pp_dual_rows) and on the segment plan: equal to the oracle on
+    repeated launches, and the workspace is left zero."""
     N, K = shape
     w1, w2 = gen.correlated_models(19, [N * K, N * K], delta_growth=False)
     dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=0.01, chunk_size=50_000_000))
     pack = device_pack(dp, "i16")
-    st = DualStream(pack, [shape], M=M)
+    st = DualStream(pack, [shape], M=M, one_linear=one_linear)
+    assert st.direct == one_linear
     # slices when the launch has fewer than half as many row tasks as wavefronts
     assert st.split == (K > 512 and 2 * -(-N // st.rows_per_item) < st.n_waves)
     assert (st.workspace is not None) == st.split

@@ -110,18 +110,21 @@ def test_container_file_round_trip_and_validation(tmp_path):
         QuadPackFile.read(bad)
 
 
+@pytest.mark.parametrize("one_linear", [True, False])
 @pytest.mark.parametrize("shape", [(256, 2048), (64, 11008), (600, 4100), (512, 1536)])
 @pytest.mark.parametrize("M", [1, 2, 8])
-def test_single_linear_split_k(shape, M):
+def test_single_linear_split_k(shape, M, one_linear):
     """One projection, its tasks cut into column slices that meet in the workspace (K not
-    a multiple of the 512-column chunk, slices of unequal block counts): equal to the
-    oracle, on repeated launches, and the workspace is left zero."""
+    a multiple of the 512-column chunk, slices of unequal block counts), on the one-Linear
+    launch (pp_quad_rows) and on the segment plan: equal to the oracle, on repeated
+    launches, and the workspace is left zero."""
     N, K = shape
     models = gen.correlated_models(7, [N * K] * 4)
     qp = oqp.pack_quad(models, threshold=0.004)
     pack = QuadPackFile(n=qp.n, s=qp.s, r_max=qp.r_max, codes=qp.codes, plug_idx=qp.plug_idx,
                         plug_vals=qp.plug_vals).to_device(DEV)
-    st = QuadStream(pack, [shape], M=M)
+    st = QuadStream(pack, [shape], M=M, one_linear=one_linear)
+    assert st.direct == (one_linear and M > 1)     # sliced at one token: the segment plan
     assert st.split and st.workspace is not None
     x_np = np.random.default_rng(5).standard_normal((M, K)).astype(np.float16)
     xs = [torch.from_numpy(x_np).to(DEV)]
