@@ -68,7 +68,9 @@ PEAK_FP16_TFLOPS = 2500.0
 LAYER = [("q_proj", 2048, 2048), ("k_proj", 256, 2048), ("v_proj", 256, 2048), ("o_proj", 2048, 2048),
          ("gate_proj", 11008, 2048), ("up_proj", 11008, 2048), ("down_proj", 2048, 11008)]
 PMC_SUMMARY = {"quad3b": os.path.join(ROOT, "profiles", "quad_stream_3b_pmc.md"),
-               "dual3b": os.path.join(ROOT, "profiles", "dual_stream_3b_pmc.md")}
+               "dual3b": os.path.join(ROOT, "profiles", "dual_stream_3b_pmc.md"),
+               "dual2048": os.path.join(ROOT, "profiles", "dual_linear_2048_direct.md"),
+               "quadgate": os.path.join(ROOT, "profiles", "quad_linear_gate_direct.md")}
 MALL_BYTES = 512 << 20
 
 
@@ -520,7 +522,8 @@ def run_dual2048(args, dev, log):
     line("achieved HBM GB/s (% of peak) + us per dual-pack 2048x2048 Linear, batch 1", achieved, ms, args, "fp32",
          {"workload": "dual-pack Linear 2048x2048, 2 models, batch 1", "N": N, "K": K, "models": 2, "batch": 1,
           "plug_entries": int(pack.plug_idx.numel()), "rotated_copies": copies, "algorithmic_bytes": int(algo),
-          "us_per_linear": round(ms * 1e3, 3), "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2)}, cpu=cpu)
+          "us_per_linear": round(ms * 1e3, 3), "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2)}, cpu=cpu,
+         traffic=read_pmc_traffic(PMC_SUMMARY["dual2048"]), traffic_profile=PMC_SUMMARY["dual2048"])
 
 
 def sanity_dual_single(entry, pack, dev):
@@ -658,7 +661,9 @@ def run_quad_single(args, dev, log, N, K, M, name, pack=None):
           "models": 4, "batch": M, "plug_entries": int(pack.plug_idx.numel()), "rotated_copies": copies,
           "algorithmic_bytes": int(algo), "us_per_linear": round(ms * 1e3, 3),
           "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2), "tflops": round(tflops, 3),
-          "pct_of_fp16_mfma_peak": round(100 * tflops / PEAK_FP16_TFLOPS, 3)}, cpu=cpu)
+          "pct_of_fp16_mfma_peak": round(100 * tflops / PEAK_FP16_TFLOPS, 3)}, cpu=cpu,
+         **({"traffic": read_pmc_traffic(PMC_SUMMARY["quadgate"]), "traffic_profile": PMC_SUMMARY["quadgate"]}
+            if (N, K, M) == (11008, 2048, 1) and args.workload == "quadgate" else {}))
     return pack
 
 
