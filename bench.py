@@ -34,7 +34,9 @@ Other workloads (``--workload``), one JSON line each:
                     refbench layer at ``--big-tokens`` tokens, against the matrix cores'
                     fp16 roofline (one line per batch size);
 * ``dualmfma``   -- the dual matrix-core decode (polar_dual_bitpacked(fused=True)) on the
-                    refbench dual layer at ``--dual-tokens`` tokens, the same roofline.
+                    refbench dual layer at ``--dual-tokens`` tokens, the same roofline;
+* ``dualrows``   -- polar_dual_bitpacked on .dualpack (N,K) rows (2048x2048, gate, down) at
+                    ``--rows-tokens`` tokens: the default route against fused=False.
 
 Single-Linear workloads rotate enough copies of the packed weights (>= 512 MB in total)
 that no launch finds its codes in the 256 MB last-level cache, and time a HIP graph of
@@ -795,6 +797,57 @@ def run_dualmfma(args, dev, log):
               "K": K, "N": N, "models": 2, "tokens": M, "flops_per_call": 4 * M * K * N}, bound="mfma")
 
 
+def run_dualrows(args, dev, log):
+    """polar_dual_bitpacked on (N,K) rows of a .dualpack stream (the reference's (K,N) view of
+    the container), 2048x2048, gate 11008x2048 and down 2048x11008, at ``--rows-tokens``:
+    the default route (the container-row matrix-core decode from 1 token, 3 when N > K, to
+    64) against ``fused=False`` (the row kernel to 4 tokens, then the fp16 decode + library
+    GEMM), per Linear: each graph replays every rotated copy of the codes once (the MALL
+    holds none of them), no plug table; checked against the fp16 decode + fp16 matmul."""
+    for name, N, K in (("2048", 2048, 2048), ("gate", 11008, 2048), ("down", 2048, 11008)):
+        g = torch.Generator(device=dev).manual_seed(seed_of(7, 0, N + K))
+        w0 = student_t(N * K, 5, 0.02, g, dev)
+        w1 = (w0 + torch.randn(N * K, generator=g, device=dev) * 0.002).to(torch.float16)
+        w2 = (w0 + torch.randn(N * K, generator=g, device=dev) * 0.002).to(torch.float16)
+        pack = pack_dual_device(w1, w2, plug_cap=0.001, select="norm")
+        del w0, w1, w2
+        amp, cs, sn = pk.header_luts(pack.amp_bits, pack.phase_bits, pack.mu, device=dev)
+        copies = max(2, -(-MALL_BYTES // (2 * N * K)))
+        views = [(pack.codes if c == 0 else pack.codes.clone())[:N * K].reshape(N, K).t() for c in range(copies)]
+        wref = pk.dual_dequant(views[0], pack.scales, amp, cs, sn, layout=pack.layout, chunk_size=pack.chunk_size,
+                               dtype=torch.float16)
+        for M in args.rows_tokens:
+            times = {}
+            for fused in (None, False):
+                route = pk.dual_call_route(views[0], M, layout=pack.layout, chunk_size=pack.chunk_size, fused=fused)
+                xs = [torch.randn(M, K, generator=g, device=dev).to(torch.float16) for _ in views]
+                fs = [(lambda v=v, x=x: pk.polar_dual_bitpacked(x, v, pack.scales, amp, cs, sn, layout=pack.layout,
+                                                                chunk_size=pack.chunk_size, fused=fused))
+                      for v, x in zip(views, xs)]
+                for o, w in zip(fs[0](), wref):
+                    r = torch.matmul(xs[0], w).float()
+                    d = (o.float() - r).abs().max().item()
+                    if not d <= 2e-2 * r.abs().max().item():
+                        raise SystemExit(f"dualrows {name} M={M} route {route}: max |diff| {d} vs fp16 matmul")
+                graph = graph_of(fs)
+                per, _ = time_events(graph.replay, args.steps, args.warmup)
+                times[fused] = (route, float(np.median(per)) / len(fs))
+                del graph
+            route, ms = times[None]
+            algo = 2 * N * K + 2 * -(-N * K // pack.group_size) + 2 * M * K + 4 * M * N
+            achieved = algo / (ms * 1e-3) / 1e9
+            log(f"[bench] dual rows {name} {N}x{K} M={M}: {route} {ms * 1e3:.2f} us per Linear, "
+                f"{times[False][0]} {times[False][1] * 1e3:.2f} us")
+            line(f"achieved HBM GB/s (% of peak) + us per dual-pack container-row Linear {N}x{K}, {M} token(s)",
+                 achieved, ms, args, "fp16 operands, fp32 sums",
+                 {"workload": f"polar_dual_bitpacked on .dualpack (N,K) rows {N}x{K}, 2 models, {M} token(s)",
+                  "N": N, "K": K, "models": 2, "tokens": M, "route": route, "rotated_copies": copies,
+                  "algorithmic_bytes": int(algo), "us_per_linear": round(ms * 1e3, 3),
+                  "fused_false_route": times[False][0], "fused_false_us": round(times[False][1] * 1e3, 3)})
+        del views, pack, wref
+        torch.cuda.empty_cache()
+
+
 def run_sweep(args, dev, log):
     for name, N, K in (("gate_proj", 11008, 2048), ("down_proj", 2048, 11008)):
         if name not in args.sweep_shapes:
@@ -814,10 +867,11 @@ def main():
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--workload", default="quad3b",
                     choices=["quad3b", "dual3b", "dual3b-pad", "dual2048", "quadgate", "sweep", "refbench",
-                             "quadbig", "dualmfma"])
+                             "quadbig", "dualmfma", "dualrows"])
     ap.add_argument("--big-tokens", type=int, nargs="+", default=[128, 1024])
     ap.add_argument("--dual-tokens", type=int, nargs="+", default=[8, 32, 64])
     ap.add_argument("--sweep-tokens", type=int, nargs="+", default=[1, 4, 16, 64])
+    ap.add_argument("--rows-tokens", type=int, nargs="+", default=[1, 4, 16, 64])
     ap.add_argument("--sweep-shapes", nargs="+", default=["gate_proj", "down_proj"],
                     choices=["gate_proj", "down_proj"])
     ap.add_argument("--cpu-sample-tuples", type=int, default=77_070_336)  # one layer
@@ -855,6 +909,8 @@ def main():
         run_quadbig(args, dev, log)
     elif args.workload == "dualmfma":
         run_dualmfma(args, dev, log)
+    elif args.workload == "dualrows":
+        run_dualrows(args, dev, log)
     else:
         run_sweep(args, dev, log)
 

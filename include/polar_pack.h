@@ -434,6 +434,29 @@ int pp_dual_mfma(const void* codes, int64_t ldk, const void* a, int64_t a_sm, co
 int pp_dual_mfma_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* slice_cols);
 int64_t pp_dual_mfma_workspace_size(int64_t M, int64_t N, int64_t slices);
 
+/*
+ * The same product over (N,K) rows of a .dualpack stream (the reference's (K,N) view of
+ * the container with c_sk == 1, polar_kernels.py:27-115 over unpack_dual_models' layout,
+ * polar_bitpack.py:228-247): row n at codes + n*ldc (ldc >= K, a multiple of 8, codes
+ * 16-byte aligned), pairs in the file's byte order (PP_DUAL_U16_BE) or the int16 layout;
+ * group scales by the container rule on the stream position p = elem_base + n*ldc + k:
+ * g = (p / chunk_size) * ceil(chunk_size / group_size) + (p % chunk_size) / group_size,
+ * scales[0 .. n_groups).  elem_base % 8 == 0, group_size a power of two >= 8, chunk_size a
+ * multiple of 8 in [32, 2^30), K % 32 == 0.  Plug entries are stream positions (sorted);
+ * row_plug[n*slices + s] (N*slices + 1 entries) is the first entry at or after elem_base +
+ * n*ldc + s*slice_cols, the last one at or after elem_base + N*ldc.  slices / slice_cols
+ * from pp_dual_mfma_plan, workspace as pp_dual_mfma's (pp_dual_mfma_workspace_size).  No
+ * counterpart kernel in the reference (its container path unpacks to fp16 weights first);
+ * used for 5-64 tokens.
+ */
+int pp_dual_nk_mfma(const void* codes, int code_layout, int64_t ldc, int64_t elem_base, const void* a,
+                    int64_t a_sm, const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
+                    const void* amp_lut, int amp_n, const void* cos_lut, const void* sin_lut, int phase_n,
+                    int lut_dtype, const uint32_t* plug_idx, const void* plug_amp, int64_t plug_n,
+                    const int64_t* row_plug, int64_t slices, int64_t slice_cols, void* out1, void* out2,
+                    int64_t o_sm, int64_t M, int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                    void* stream);
+
 /* Dequantise to float32 (w1, w2) over a (K,N) view; parity / debug export.
  * Replaces the decode of unpack_dual_models (polar_bitpack.py:228-247). */
 int pp_dual_dequant(const void* codes, int code_layout, int64_t c_sk, int64_t c_sn,

@@ -80,6 +80,8 @@ EXPORTS = {
     "pp_dual_mfma": (i32, [vp, i64, vp, i64, vp, i64, vp, i32, vp, vp, i32, i32, vp, vp, i64, vp, i64, i64, i64,
                            i64, vp, vp, i64, i64, i64, i64, vp, i64, vp]),
     "pp_dual_mfma_plan": (i32, [i64, i64, i64, vp, vp]),
+    "pp_dual_nk_mfma": (i32, [vp, i32, i64, i64, vp, i64, vp, i64, i64, i64, vp, i32, vp, vp, i32, i32, vp, vp, i64,
+                              vp, i64, i64, vp, vp, i64, i64, i64, i64, vp, i64, vp]),
     "pp_dual_mfma_workspace_size": (i64, [i64, i64, i64]),
     "pp_quad_stream_rows": (i32, [i64]),
     "pp_quad_stream_chunk": (i32, [i64]),

@@ -91,7 +91,8 @@ struct DmPlug {
   int64_t next, end;
 };
 
-__device__ __forceinline__ void dplug_load(const DualMfmaArgs& A, DmPlug& P, int64_t rowpos) {
+template <class Args>
+__device__ __forceinline__ void dplug_load(const Args& A, DmPlug& P, int64_t rowpos) {
   const rsrc_t ri = make_rsrc(A.plug_idx, 4u * (uint32_t)A.plug_n);
   const rsrc_t ra = make_rsrc(A.plug_amp, 2u * (uint32_t)A.plug_n);
   uint32_t idx[4], am[4];
@@ -112,7 +113,8 @@ __device__ __forceinline__ void dplug_load(const DualMfmaArgs& A, DmPlug& P, int
 
 // Substitute the window's entries in the lane's rows kk .. kk+7 (step rows ks .. ks+31)
 // into the amplitudes; refill a window used up within the step.  Wave-uniform control.
-__device__ __forceinline__ void dplug_patch(const DualMfmaArgs& A, DmPlug& P, int64_t rowpos, int kk, int ks,
+template <class Args>
+__device__ __forceinline__ void dplug_patch(const Args& A, DmPlug& P, int64_t rowpos, int kk, int ks,
                                             float (&amp)[8]) {
   for (;;) {
     int hit = -1;
@@ -375,6 +377,224 @@ __global__ __launch_bounds__(256) void dual_mfma_finish_kernel(float* acc, f16* 
   }
 }
 
+// ------------------------------------------------------------ (N,K) container rows
+// The same product over the rows of a .dualpack stream: codes (N,K) row-major (row n at
+// codes + n*ldc, K contiguous), 16-bit pairs in the file's byte order (or the int16
+// layout), group scales by the container rule on the stream position p = elem_base +
+// n*ldc + k: g = (p / chunk) * ceil(chunk / gs) + (p % chunk) / gs (polar_bitpack.py:201-203,
+// 224-238).  Per 32-column step lane l reads row n0 + l%16 at columns k0 + 8(l/16) .. +7:
+// one 16-byte load of 8 codes, which is the A operand's own layout (no transpose), and one
+// group scale (elem_base, ldc, the chunk size and gs are multiples of 8, so the 8 codes
+// share a group).  The lane keeps the chunk index and offset of its next load position and
+// advances them by 32 per step: no division in the loop.  Plug entries are stream
+// positions; the window logic, slices, epilogue and finish pass are dual_mfma_kernel's.
+struct DualNkArgs {
+  const uint16_t* codes;   // row n at codes + n*ldc
+  int64_t ldc;
+  int64_t elem_base;       // stream position of (row 0, column 0)
+  const f16* x;            // (M, K), row stride x_sm
+  int64_t x_sm;
+  f16* out[2];             // (M, N), row stride o_sm
+  int64_t o_sm;
+  int N, K, M;
+  int tiles, tblocks;      // ceil(N / 16), ceil(M / (16 TT))
+  int slices, ks;          // K slices of ks columns (a multiple of 64)
+  const f16* scales;       // the stream's group scales
+  int64_t n_groups;
+  int chunk;               // chunk size (>= 32, a multiple of 8)
+  int64_t gpc;             // groups per chunk, ceil(chunk / gs)
+  int log2gs;
+  DualLuts luts;
+  const uint32_t* plug_idx;   // sorted stream positions
+  const f16* plug_amp;
+  int64_t plug_n;
+  const int64_t* row_plug;    // [n*slices + s]: first entry of (row n, slice s); N*slices + 1 entries
+  float* acc;              // slices > 1: [2][N][M] float32, zero on entry
+  int xcd_remap;
+  int vec_out;
+};
+
+template <int TT>
+struct DnStage {
+  u32x4 c;                 // 8 stored codes of the lane's row
+  uint32_t sc;             // their group scale (fp16 bits)
+  u32x4 xb[TT];            // 8 fp16 x of token 16t + l%16
+};
+
+// The chunk index and offset of a lane's position.
+struct DnPos {
+  int64_t c;
+  int r;
+  __device__ __forceinline__ void set(int64_t p, int chunk) {
+    c = p / chunk;
+    r = (int)(p - c * chunk);
+  }
+  __device__ __forceinline__ void advance32(int chunk) {   // chunk >= 32
+    r += 32;
+    const bool w = r >= chunk;
+    r = w ? r - chunk : r;
+    c += w ? 1 : 0;
+  }
+};
+
+// Issue the loads of the step at column k0 (codes clamped to the last step; x of a step at
+// or past the slice end ke through an empty record) and advance the scale position.
+template <int TT>
+__device__ __forceinline__ void dn_issue(const DualNkArgs& A, const uint16_t* ctile, int nrows, uint32_t voc, bool ok,
+                                         DnPos& pos, int k0, int ke, const uint32_t (&vox)[TT], const f16* xblk,
+                                         int j0, DnStage<TT>& S) {
+  const uint32_t xrec = k0 < ke ? 2u * (uint32_t)((int64_t)(A.M - 1 - j0) * A.x_sm + (ke - k0)) : 0u;
+  k0 = min(k0, A.K - 32);
+  const rsrc_t rc = make_rsrc(ctile + k0, 2u * (uint32_t)((int64_t)(nrows - 1) * A.ldc + (A.K - k0)));
+  S.c = __builtin_amdgcn_raw_buffer_load_b128(rc, (int)voc, 0, NT_AUX);
+  const int64_t g = pos.c * A.gpc + (pos.r >> A.log2gs);
+  vload16(S.sc, ok ? 2u * (uint32_t)g : OOB, make_rsrc(A.scales, 2u * (uint32_t)A.n_groups));
+  pos.advance32(A.chunk);
+  const rsrc_t rx = make_rsrc(xblk + k0, xrec);
+#pragma unroll
+  for (int t = 0; t < TT; ++t) vload128c(S.xb[t], vox[t], rx);
+}
+
+template <int TT, int LAYOUT, bool PLUG>
+struct DnRun {
+  const char* lds;
+  DualLane lo;
+  const DualNkArgs& A;
+  const uint16_t* ctile;
+  const f16* xblk;
+  int nrows, j0, q, ke;
+  bool ok;
+  uint32_t voc;
+  uint32_t vox[TT];
+  DnPos pos;
+  int64_t rowpos;
+  DmPlug P;
+  df4 C[2][TT];
+
+  // Consume the step at k0 from cur while the step at k0 + 32 loads into nxt.
+  __device__ __forceinline__ void step(const DnStage<TT>& cur, DnStage<TT>& nxt, int k0) {
+    dn_issue<TT>(A, ctile, nrows, voc, ok, pos, k0 + 32, ke, vox, xblk, j0, nxt);
+    const float sc = h2f(cur.sc);
+    const uint32_t w4[4] = {cur.c.x, cur.c.y, cur.c.z, cur.c.w};
+    float amp[8];
+    float2 cs[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float an[2];
+      float2 c2[2];
+      dual_lookup2<LAYOUT>(lds, w4[e], lo, an, c2);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        amp[2 * e + h] = an[h] * sc;
+        cs[2 * e + h] = c2[h];
+      }
+    }
+    if constexpr (PLUG) dplug_patch(A, P, rowpos, k0 + 8 * q, k0, amp);
+    dh8 a0, a1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // the float32 product, then fp16, as the reference rounds the weights: hidden from the
+      // compiler, which would otherwise fold product and conversion into one multiply
+      float w1 = amp[e] * cs[e].x, w2 = amp[e] * cs[e].y;
+      asm volatile("" : "+v"(w1), "+v"(w2));
+      a0[e] = (_Float16)w1;
+      a1[e] = (_Float16)w2;
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const dh8 b = __builtin_bit_cast(dh8, cur.xb[t]);
+      C[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b, C[0][t], 0, 0, 0);
+      C[1][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b, C[1][t], 0, 0, 0);
+    }
+  }
+};
+
+template <int TT, int LAYOUT, bool PLUG>
+__device__ __forceinline__ void dn_body(const char* lds, const DualNkArgs& A) {
+  const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+  const DualLane lo = dual_lane(lane);
+  int b = blockIdx.x;
+  if (A.xcd_remap) b = (b & 7) * (int)(gridDim.x >> 3) + (b >> 3);
+  const int64_t gw = (int64_t)b * DM_WAVES + uniform(threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * DM_WAVES;
+  // groups of DM_WAVES row tiles sharing a token block and K slice, one per workgroup
+  const int64_t tgroups = (A.tiles + DM_WAVES - 1) / DM_WAVES;
+  const int64_t items = tgroups * DM_WAVES * A.tblocks * A.slices;
+  for (int64_t it = gw; it < items; it += nw) {
+    const int64_t w = uniform64(it / DM_WAVES);
+    const int tile = (int)(uniform64(w / ((int64_t)A.slices * A.tblocks)) * DM_WAVES + it % DM_WAVES);
+    const int sl = (int)(w % A.slices), tb = (int)((w / A.slices) % A.tblocks);
+    if (tile >= A.tiles) continue;
+    const int n0 = tile * 16, j0 = tb * 16 * TT;
+    const int kb = sl * A.ks, ke = min(A.K, kb + A.ks);
+    const int n = n0 + i;
+    const bool ok = n < A.N;
+    const int nrows = min(16, A.N - n0);
+    DnRun<TT, LAYOUT, PLUG> R{lds, lo, A, A.codes + (int64_t)n0 * A.ldc, A.x + (int64_t)j0 * A.x_sm, nrows, j0, q,
+                              ke, ok};
+    R.voc = ok ? 2u * (uint32_t)(i * A.ldc + 8 * q) : OOB;
+    R.rowpos = A.elem_base + (int64_t)min(n, A.N - 1) * A.ldc;
+    R.pos.set(R.rowpos + kb + 8 * q, A.chunk);
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const int jl = 16 * t + i;
+      R.vox[t] = j0 + jl < A.M ? 2u * (uint32_t)(jl * A.x_sm + 8 * q) : OOB;
+    }
+    if constexpr (PLUG) {
+      R.P.next = ok ? A.row_plug[(int64_t)n * A.slices + sl] : 0;
+      R.P.end = ok ? A.row_plug[(int64_t)n * A.slices + sl + 1] : 0;
+      dplug_load(A, R.P, R.rowpos);
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) R.C[m][t] = df4{0.f, 0.f, 0.f, 0.f};
+    DnStage<TT> S0, S1;
+    dn_issue<TT>(A, R.ctile, nrows, R.voc, ok, R.pos, kb, ke, R.vox, R.xblk, j0, S0);
+    for (int k0 = kb; k0 < ke; k0 += 64) {
+      R.step(S0, S1, k0);
+      R.step(S1, S0, k0 + 32);
+    }
+    // epilogue: lane holds rows n0 + 4q + r, r = 0..3, of token j0 + 16t + i
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        const int j = j0 + 16 * t + i;
+        const int nn = n0 + 4 * q;
+        const df4 c = R.C[m][t];
+        if (j >= A.M || nn >= A.N) continue;
+        if (A.slices == 1) {
+          f16* o = A.out[m] + (int64_t)j * A.o_sm + nn;
+          if (A.vec_out && nn + 3 < A.N) {
+            const f16x4 h = {(f16)c[0], (f16)c[1], (f16)c[2], (f16)c[3]};
+            *reinterpret_cast<f16x4*>(o) = h;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (nn + r < A.N) o[r] = (f16)c[r];
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (nn + r < A.N)
+              __hip_atomic_fetch_add(A.acc + ((int64_t)m * A.N + nn + r) * A.M + j, c[r], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+  }
+}
+
+template <int TT, int LAYOUT>
+__global__ __launch_bounds__(DM_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void dual_nk_mfma_kernel(
+    const DualNkArgs A) {
+  __shared__ __attribute__((aligned(16))) char T[DLDS_BYTES];
+  if (A.luts.dtype == PP_F16) dual_tables_of<DM_NT, LAYOUT, f16>(T, A.luts);
+  else dual_tables_of<DM_NT, LAYOUT, float>(T, A.luts);
+  if (A.plug_n > 0) dn_body<TT, LAYOUT, true>(T, A);
+  else dn_body<TT, LAYOUT, false>(T, A);
+}
+
 static int dm_tt(int64_t M) { return M <= 32 ? 2 : M <= 64 ? 4 : 8; }
 
 static void dm_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* cols) {
@@ -478,6 +698,95 @@ extern "C" int pp_dual_mfma(const void* codes, int64_t ldk, const void* a, int64
     case 4: hipLaunchKernelGGL(dual_mfma_kernel<4>, dim3((unsigned)grid), dim3(DM_NT), 0, st, A); break;
     default: hipLaunchKernelGGL(dual_mfma_kernel<8>, dim3((unsigned)grid), dim3(DM_NT), 0, st, A); break;
   }
+  PP_LAUNCH_CHECK();
+  if (slices > 1) {
+    const int64_t total = 2 * N * M;
+    hipLaunchKernelGGL(dual_mfma_finish_kernel, dim3((unsigned)((total / 4 + 255) / 256 + 1)), dim3(256), 0, st,
+                       A.acc, A.out[0], A.out[1], o_sm, A.N, A.M);
+    PP_LAUNCH_CHECK();
+  }
+  return PP_OK;
+}
+
+extern "C" int pp_dual_nk_mfma(const void* codes, int code_layout, int64_t ldc, int64_t elem_base, const void* a,
+                               int64_t a_sm, const void* scales, int64_t n_groups, int64_t group_size,
+                               int64_t chunk_size, const void* amp_lut, int amp_n, const void* cos_lut,
+                               const void* sin_lut, int phase_n, int lut_dtype, const uint32_t* plug_idx,
+                               const void* plug_amp, int64_t plug_n, const int64_t* row_plug, int64_t slices,
+                               int64_t slice_cols, void* out1, void* out2, int64_t o_sm, int64_t M, int64_t N,
+                               int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
+  PP_REQUIRE(codes && a && scales && amp_lut && cos_lut && sin_lut && out1 && out2, "null pointer argument");
+  PP_REQUIRE(code_layout == PP_DUAL_U16_BE || code_layout == PP_DUAL_I16_OFFSET, "bad code_layout");
+  PP_REQUIRE(lut_dtype == PP_F16 || lut_dtype == PP_F32, "bad lut_dtype");
+  PP_REQUIRE(amp_n >= 1 && amp_n <= 64 && phase_n >= 1 && phase_n <= 1024, "amp_n must be 1..64, phase_n 1..1024");
+  PP_REQUIRE(M >= 1 && N >= 1 && N < (1ll << 30) && K >= 32 && K % 32 == 0,
+             "needs M, N >= 1 and K a multiple of 32 (N=%lld, K=%lld)", (long long)N, (long long)K);
+  PP_REQUIRE(ldc >= K && ldc % 8 == 0 && aligned(codes, 16) && elem_base >= 0 && elem_base % 8 == 0,
+             "codes: 16-byte aligned (N,K) rows of ldc >= K pairs, ldc and elem_base multiples of 8");
+  PP_REQUIRE(group_size >= 8 && (group_size & (group_size - 1)) == 0, "group_size must be a power of two >= 8");
+  PP_REQUIRE(chunk_size >= 32 && chunk_size % 8 == 0 && chunk_size < (1ll << 30),
+             "chunk_size must be a multiple of 8 in [32, 2^30)");
+  PP_REQUIRE(n_groups >= 1 && n_groups < (1ll << 30), "n_groups must be in [1, 2^30)");
+  PP_REQUIRE(aligned(a, 16) && (M == 1 || (a_sm >= K && a_sm % 8 == 0)),
+             "activations must be 16-byte aligned with a row stride that is a multiple of 8");
+  PP_REQUIRE(o_sm >= N, "o_sm must be >= N");
+  PP_REQUIRE(slices >= 1 && slice_cols >= 64 && slice_cols % 64 == 0 && slices * slice_cols >= K &&
+                 (slices - 1) * slice_cols < K,
+             "slices x slice_cols must cover K in multiples of 64 columns");
+  PP_REQUIRE(plug_n >= 0 && plug_n < (1ll << 29) && (plug_n == 0 || (plug_idx && plug_amp && row_plug)),
+             "plug arrays are null (or more than 2^29 entries)");
+  PP_REQUIRE(16 * ldc * 2 < (1ll << 31) && (M - 1) * a_sm + K < (1ll << 30),
+             "a row tile's codes and the activations must each stay below 2 GiB");
+  const int64_t need = pp_dual_mfma_workspace_size(M, N, slices);
+  PP_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), "workspace too small: need %lld bytes",
+             (long long)need);
+  DualNkArgs A = {};
+  A.codes = reinterpret_cast<const uint16_t*>(codes);
+  A.ldc = ldc;
+  A.elem_base = elem_base;
+  A.x = reinterpret_cast<const f16*>(a);
+  A.x_sm = M > 1 ? a_sm : K;
+  A.out[0] = reinterpret_cast<f16*>(out1);
+  A.out[1] = reinterpret_cast<f16*>(out2);
+  A.o_sm = o_sm;
+  A.vec_out = o_sm % 4 == 0 && aligned(out1, 8) && aligned(out2, 8);
+  A.N = (int)N;
+  A.K = (int)K;
+  A.M = (int)M;
+  const int tt = dm_tt(M);
+  A.tiles = (int)((N + 15) / 16);
+  A.tblocks = (int)((M + 16 * tt - 1) / (16 * tt));
+  A.slices = (int)slices;
+  A.ks = (int)slice_cols;
+  A.scales = reinterpret_cast<const f16*>(scales);
+  A.n_groups = n_groups;
+  A.chunk = (int)chunk_size;
+  A.gpc = (chunk_size + group_size - 1) / group_size;
+  int lg = 0;
+  while ((1ll << lg) < group_size) ++lg;
+  A.log2gs = lg;
+  A.luts.amp = amp_lut;
+  A.luts.cs[0] = cos_lut;
+  A.luts.cs[1] = sin_lut;
+  A.luts.amp_n = amp_n;
+  A.luts.phase_n = phase_n;
+  A.luts.dtype = lut_dtype;
+  A.plug_idx = plug_idx;
+  A.plug_amp = reinterpret_cast<const f16*>(plug_amp);
+  A.plug_n = plug_n;
+  A.row_plug = row_plug;
+  A.acc = reinterpret_cast<float*>(workspace);
+  const int64_t groups = (int64_t)(A.tiles + DM_WAVES - 1) / DM_WAVES * A.tblocks * slices;
+  const int64_t grid = std::min<int64_t>(device_cu_count(), groups);
+  A.xcd_remap = grid % 8 == 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool be = code_layout == PP_DUAL_U16_BE;
+  using KernelFn = void (*)(DualNkArgs);
+  static const KernelFn kernels[3][2] = {
+      {dual_nk_mfma_kernel<2, PP_DUAL_I16_OFFSET>, dual_nk_mfma_kernel<2, PP_DUAL_U16_BE>},
+      {dual_nk_mfma_kernel<4, PP_DUAL_I16_OFFSET>, dual_nk_mfma_kernel<4, PP_DUAL_U16_BE>},
+      {dual_nk_mfma_kernel<8, PP_DUAL_I16_OFFSET>, dual_nk_mfma_kernel<8, PP_DUAL_U16_BE>}};
+  hipLaunchKernelGGL(kernels[tt == 2 ? 0 : tt == 4 ? 1 : 2][be ? 1 : 0], dim3((unsigned)grid), dim3(DM_NT), 0, st, A);
   PP_LAUNCH_CHECK();
   if (slices > 1) {
     const int64_t total = 2 * N * M;

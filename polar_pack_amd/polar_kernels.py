@@ -14,8 +14,8 @@ Same names, arguments, return values and error behaviour as the reference
 
 The kernel of a call comes from one table, :data:`polar_pack_amd.routes.DUAL_ROUTES`:
 batches of 1-4 tokens (1-8 on the (K,N) kernel layout) run on the fused decode kernels;
-2-64 tokens on the int16 (K,N) kernel layout on the matrix-core decode (pp_dual_mfma);
-larger ones decode once into fp16 weights (the values the reference's kernel rounds its
+2-64 tokens on the int16 (K,N) kernel layout on the matrix-core decode (pp_dual_mfma), 5-64
+on container (N,K) rows on its (N,K) form (pp_dual_nk_mfma); larger ones decode once into fp16 weights (the values the reference's kernel rounds its
 weights to, polar_kernels.py:78-82) and run a library fp16 GEMM (hipBLASLt through
 torch.matmul).
 """
@@ -112,9 +112,9 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
     offset ``idx - elem_base`` (polar_bitpack.py:240-243); entries in any order (sorted once
     per table on the device, :mod:`polar_pack_amd.plugs`).  The kernel is chosen by
     :data:`polar_pack_amd.routes.DUAL_ROUTES` from the storage of ``packed``, M, the plug table
-    and ``fused`` (the int16 (K,N) layout, K % 32 == 0): True runs the matrix-core decode at
-    any size, False never (the fused (K,N) kernel up to 8 tokens, then the fp16 decode +
-    library GEMM), None (default) picks by size."""
+    and ``fused`` (the int16 (K,N) layout or container rows, K % 32 == 0): True runs the
+    matrix-core decode at any size, False never (the fused row kernels up to 4 or 8 tokens,
+    then the fp16 decode + library GEMM), None (default) picks by size."""
     M, K = a_fp16.shape
     K_b, N = packed.shape
     assert K == K_b
@@ -143,6 +143,11 @@ def polar_dual_bitpacked(a_fp16, packed, bmax, amp_lut, cos_lut, sin_lut, num_ph
     if route == "dual_mfma":
         _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, lut_dt, keep, pn,
                    int(elem_base), out1, out2, L, dev)
+        del keep
+        return out1, out2
+    if route == "dual_nk_mfma":
+        _dual_nk_mfma(a, packed, lay, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_size, chunk_size, lut_dt,
+                      keep, pn, int(elem_base), out1, out2, L, dev)
         del keep
         return out1, out2
     if route == "prefill":
@@ -226,6 +231,33 @@ def _dual_mfma(a, packed, bmax, amp_lut, cos_lut, sin_lut, num_phases, group_siz
     if rc:
         nat.drop_workspace(wkey)
     nat.check(rc, "pp_dual_mfma")
+    del keep, row_plug, ws
+
+
+def _dual_nk_mfma(a, packed, lay, scales, amp_lut, cos_lut, sin_lut, num_phases, group_size, chunk_size, lut_dt,
+                  keep, pn, elem_base, out1, out2, L, dev):
+    """5-64 tokens on (N,K) container rows: the matrix-core decode (pp_dual_nk_mfma), plug
+    starts per (row, K slice) found on the device (pp_plug_search; polar_bitpack.py:240-243)."""
+    M, K = a.shape
+    N = packed.shape[1]
+    ldc = packed.stride(1)
+    plan = (ctypes.c_int64 * 2)()
+    nat.check(L.pp_dual_mfma_plan(M, N, K, ctypes.byref(plan, 0), ctypes.byref(plan, 8)), "pp_dual_mfma_plan")
+    slices, cols = int(plan[0]), int(plan[1])
+    row_plug = nat.plug_search(keep[0], pn, elem_base, ldc, N, slices, cols, dev) if pn else None
+    ws_bytes = L.pp_dual_mfma_workspace_size(M, N, slices)
+    ws, wkey = nat.zero_workspace(dev, ws_bytes)
+    stream = nat.raw_stream(dev)
+    rc = L.pp_dual_nk_mfma(packed.data_ptr(), lay, ldc, elem_base, a.data_ptr(), a.stride(0), scales.data_ptr(),
+                           scales.numel(), group_size, chunk_size, amp_lut.data_ptr(), amp_lut.numel(),
+                           cos_lut.data_ptr(), sin_lut.data_ptr(), num_phases, lut_dt,
+                           keep[0].data_ptr() if pn else None, keep[1].data_ptr() if pn else None, pn,
+                           row_plug.data_ptr() if row_plug is not None else None, slices, cols, out1.data_ptr(),
+                           out2.data_ptr(), out1.stride(0), M, N, K, ws.data_ptr() if ws is not None else None,
+                           ws_bytes, stream)
+    if rc:
+        nat.drop_workspace(wkey)
+    nat.check(rc, "pp_dual_nk_mfma")
     del keep, row_plug, ws
 
 

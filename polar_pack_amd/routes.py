@@ -31,6 +31,7 @@ Dual kernels (polar_kernels.py:14-115):
 * ``dual_mfma``  matrix-core decode of the int16 (K,N) kernel layout (``pp_dual_mfma``)
 * ``dual_kn``    fused row decode of (K,N) codes, 8 tokens per pass (``pp_dual_gemm``)
 * ``dual_rows``  fused row decode of container (N,K) rows, 1-4 tokens (``pp_dual_gemm``)
+* ``dual_nk_mfma`` matrix-core decode of container (N,K) rows (``pp_dual_nk_mfma``)
 * ``prefill`` / ``generic`` as for quad.
 
 The token boundaries are measured crossovers (graph-replayed GPU times on the reference's
@@ -152,11 +153,23 @@ def quad_route(M: int, K: int, N: int, caps: FrozenSet[str], has_plug: bool, fus
 
 
 # ------------------------------------------------------------------------------- dual
+def dual_nk_mfma_min_m(K: int, N: int, has_plug: bool) -> int:
+    """First token count of the container-row matrix-core decode by default: 1, or 3 when
+    N > K (there the row kernel is faster at 1-2 tokens)."""
+    return 3 if N > K else 1
+
+
 DUAL_ROUTES = (
     Route("dual_mfma", 1, INF, fused=(True,)),
     # from 96 tokens the fp16 decode + one batched GEMM is faster (4096x4096: 52 against 66 us)
     Route("dual_mfma", dual_mfma_min_m, 64, fused=(None,)),
+    Route("dual_nk_mfma", 1, INF, fused=(True,)),
     Route("dual_kn", 1, 8),
+    # container rows, no plug table, graph-replayed per Linear: 2048x2048 at 1 token 12.8
+    # against 16.1 us on the row kernel, 2048x11008 25.6 against 80.2; 11008x2048 (N > K) at
+    # 1-2 tokens 33.1 / 31.3 against 22.7 / 27.4 us, at 3 tokens 32.0 against 51.7; above 64
+    # tokens the fp16 decode + GEMM wins on 2048x2048 (32.7 against 61.5 us at 65)
+    Route("dual_nk_mfma", dual_nk_mfma_min_m, 64, fused=(None,)),
     Route("dual_rows", 1, 4),
     Route("generic", 1, 4),
     Route("prefill", 1, INF),
@@ -167,7 +180,7 @@ def dual_storage(c_sk: int, c_sn: int, ptr: int, K: int, N: int, layout: str, gr
                  elem_base: int, plug_n: int = 0) -> FrozenSet[str]:
     """Kernels that can read dual codes of the (K,N) view with strides (c_sk, c_sn) at device
     address ``ptr`` (dual_kn.hip dual_kn_ok, dual.hip dual_fast_ok, dual_mfma.hip
-    pp_dual_mfma)."""
+    pp_dual_mfma and pp_dual_nk_mfma)."""
     caps = {"prefill", "generic"}
     a16 = _aligned(ptr, 16)
     gs_ok = group_size >= 8 and group_size & (group_size - 1) == 0
@@ -182,6 +195,9 @@ def dual_storage(c_sk: int, c_sn: int, ptr: int, K: int, N: int, layout: str, gr
     if c_sk == 1 and c_sn % 8 == 0 and c_sn >= K and K % 8 == 0 and K > 0 and a16 and chunk_size > 0 \
             and chunk_size % 8 == 0 and gs_ok and elem_base % 8 == 0:
         caps.add("dual_rows")
+        if K % 32 == 0 and 32 <= chunk_size < (1 << 30) and 32 * c_sn < (1 << 31) and N < (1 << 30) \
+                and plug_n < (1 << 29):
+            caps.add("dual_nk_mfma")
     return frozenset(caps)
 
 

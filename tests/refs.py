@@ -174,7 +174,7 @@ def route_class(route):
     GEMM: the fp16-weight bound)."""
     if route in ("rows", "kn", "generic", "dual_kn", "dual_rows"):
         return "fused"
-    if route in ("mfma", "big_nk", "big_kn", "kn_mfma", "dual_mfma"):
+    if route in ("mfma", "big_nk", "big_kn", "kn_mfma", "dual_mfma", "dual_nk_mfma"):
         return "mfma"
     assert route == "prefill", route
     return "prefill"

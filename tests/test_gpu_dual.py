@@ -23,10 +23,11 @@ def kernel_layout_layer(K, N, seed, dtype=torch.float16):
 
 
 def prefill_bound(a, w, route):
-    """The matrix-core decode and the fp16 decode + library GEMM (routes ``dual_mfma`` and
-    ``prefill``) multiply weights rounded to fp16, as the reference's kernel rounds them
-    (polar_kernels.py:78-82): held to the fp16-weight bound; the fused row kernels to rel 1e-3."""
-    return fp16_weight_bound(a, w) if route in ("dual_mfma", "prefill") else None
+    """The matrix-core decodes and the fp16 decode + library GEMM (routes ``dual_mfma``,
+    ``dual_nk_mfma`` and ``prefill``) multiply weights rounded to fp16, as the reference's
+    kernel rounds them (polar_kernels.py:78-82): held to the fp16-weight bound; the fused row
+    kernels to rel 1e-3."""
+    return fp16_weight_bound(a, w) if route in ("dual_mfma", "dual_nk_mfma", "prefill") else None
 
 
 def to_dev(*arrs):

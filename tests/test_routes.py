@@ -96,7 +96,12 @@ DUAL_TABLE = [
     (dkn(2048, 512), (False, True), False, "dual_kn:1-8 prefill:9-"),
     (dict(dkn(2048, 512), layout="u16be"), (False, True), None, "dual_kn:1-8 prefill:9-"),
     (dkn(2056, 512), (False, True), None, "dual_kn:1-8 prefill:9-"),            # K % 32 != 0
-    (dnk(2048, 512), (False, True), None, "dual_rows:1-4 prefill:5-"),          # .dualpack rows
+    (dnk(2048, 512), (False, True), None, "dual_nk_mfma:1-64 prefill:65-"),     # .dualpack rows, N <= K
+    (dnk(512, 2048), (False, True), None, "dual_rows:1-2 dual_nk_mfma:3-64 prefill:65-"),   # N > K
+    (dnk(2048, 512), (False, True), True, "dual_nk_mfma:1-"),
+    (dnk(2048, 512), (False, True), False, "dual_rows:1-4 prefill:5-"),
+    (dict(dnk(2048, 512), chunk_size=24), (False, True), None, "dual_rows:1-4 prefill:5-"),   # chunks < 32 pairs
+    (dnk(2056, 512), (False, True), None, "dual_rows:1-4 prefill:5-"),          # K % 32 != 0
     (dnk(2048, 512, elem_base=4), (False, True), None, "generic:1-4 prefill:5-"),
     # K * ldk * 2 >= 2^31 bytes: neither the matrix cores nor the (K,N) kernel address it
     (dkn(16384, 65536), (False, True), None, "generic:1-4 prefill:5-"),
