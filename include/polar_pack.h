@@ -106,11 +106,14 @@ int64_t pp_quad_gemm_workspace_size(const void* a, int64_t a_sm, int64_t a_sk,
  *   plug_code  each entry's code word from pp_quad_plug_codes (or null: read from the codes);
  *   workspace  pp_quad_rows_workspace_size(M, N, K) bytes, zero on entry and left zero by
  *              every launch (null when that is 0): rows with fewer tasks than ~1.5 per
- *              wavefront are cut into column slices whose sums meet there.
+ *              wavefront are cut into pp_quad_rows_parts(M, N, K) column slices; when that is
+ *              a power of two dividing a workgroup's waves, a task's slices are waves of one
+ *              workgroup and meet in LDS (no workspace), otherwise they meet there.
  * Outputs out[m][i*o_sm + n*o_sn] = fp16(s_m * sum_k a[i*a_sm + k] W_m[n][k]); launches that
  * share a workspace must not overlap. */
 int64_t pp_quad_rows_plan_size(int64_t M);
 int64_t pp_quad_rows_workspace_size(int64_t M, int64_t N, int64_t K);
+int pp_quad_rows_parts(int64_t M, int64_t N, int64_t K);
 int pp_quad_rows_plan(const uint32_t* plug_idx, int64_t plug_n, int64_t elem_base, int64_t ldc, int64_t M,
                       int64_t N, int64_t K, int64_t* wave_plug, void* stream);
 int pp_quad_rows(const void* a, int64_t a_sm, const uint32_t* codes, int64_t ldc,
@@ -546,6 +549,10 @@ int pp_dual_stream_rows(int64_t M);
  * the workspace: pp_dual_rows_workspace_size(M, N, K) bytes, zero on entry, left zero by every
  * launch (launches sharing it must not overlap). */
 int64_t pp_dual_rows_workspace_size(int64_t M, int64_t N, int64_t K);
+/* K parts of pp_dual_rows at this shape (1: whole rows).  When a power of two that divides a
+ * workgroup's waves, a task's parts are waves of one workgroup and their sums meet in LDS
+ * (no workspace: pp_dual_rows_workspace_size is 0); otherwise they meet in the workspace. */
+int pp_dual_rows_parts(int64_t M, int64_t N, int64_t K);
 int pp_dual_rows(const pp_dual_proj* proj, const int64_t* task_plug, int plug_windows, int code_layout,
                  const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
                  const void* scale_tab, int64_t n_tab, const float* amp_lut, const float* cos_lut,

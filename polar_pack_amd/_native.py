@@ -60,6 +60,7 @@ EXPORTS = {
     "pp_quad_gemm_kernel": (i32, [vp, i64, i64, vp, i64, i64, i64, i64, i64]),
     "pp_quad_rows_plan_size": (i64, [i64]),
     "pp_quad_rows_workspace_size": (i64, [i64, i64, i64]),
+    "pp_quad_rows_parts": (i32, [i64, i64, i64]),
     "pp_quad_rows_plan": (i32, [vp, i64, i64, i64, i64, i64, i64, vp, vp]),
     "pp_quad_rows": (i32, [vp, i64, vp, i64, vp, i32, vp, vp, vp, vp, i64, vp, i64, vp, i64, i64, i64, i64, i64,
                            vp, i64, vp]),
@@ -97,6 +98,7 @@ EXPORTS = {
                              vp, vp, vp, vp, vp, vp, i64, i64, vp, vp, i64, vp]),
     "pp_dual_scale_table": (i32, [vp, i64, i64, vp, vp, vp, i64, i64, vp, i64, vp]),
     "pp_dual_rows_workspace_size": (i64, [i64, i64, i64]),
+    "pp_dual_rows_parts": (i32, [i64, i64, i64]),
     "pp_dual_rows": (i32, [vp, vp, i32, i32, vp, i64, i64, i64, vp, i64, vp, vp, vp, vp, vp, vp, i64, i64, vp, i64,
                            vp]),
     "pp_dual_plug_table": (i32, [vp, i64, i32, vp, i64, i64, i64, vp, vp, vp, i64, vp, vp, i64, i64, vp, vp]),

@@ -68,6 +68,7 @@ struct DualStreamArgs {
   int parts, n_chunks;
   float* acc;
   uint32_t* cnt;
+  int wg_parts;               // 1: a task's parts are waves of one workgroup, summed in LDS
 };
 
 // (cos, sin) rows as 16-byte units (two replicas) in address order, so that a wavefront's
@@ -119,6 +120,7 @@ struct DualSeg {
   int parts, N, row0;  // slices of its rows; the projection's rows; the first row
   float* acc;          // parts > 1: the projection's accumulators [2][M][N]
   uint32_t* cnt;       // parts > 1: the counters of the segment's tasks
+  float* red;          // parts meeting in LDS: the wave's 64 reduced sums
 };
 
 // Group (scale index) of stream position p.  SM = 0 and 2: chunk is a multiple of gs, so
@@ -354,6 +356,21 @@ struct DReduced {
   bool wr;
 };
 
+// The (row, model, token) lane `lane` holds after the reduction below, and whether it writes.
+template <int MT, int RG>
+__device__ __forceinline__ DReduced dred_slot(const DualStreamArgs& A, const DualSeg& S, int ti, int lane) {
+  constexpr int LNV = Log2<RG * 2 * MT>::v;
+  DReduced o;
+  o.y = 0.f;
+  const int idx = lane >> (6 - LNV);
+  o.r = idx / (2 * MT);
+  o.m = (idx / MT) & 1;
+  o.j = idx % MT;
+  const int nr = min(RG, S.nrows - ti * RG);
+  o.wr = (lane & ((1 << (6 - LNV)) - 1)) == 0 && o.r < nr && o.j < A.M;
+  return o;
+}
+
 template <int MT, int RG>
 __device__ __forceinline__ DReduced dtask_reduce(const DualStreamArgs& A, const DualSeg& S, int ti, int lane,
                                                  float (&acc)[RG][2][MT]) {
@@ -367,14 +384,8 @@ __device__ __forceinline__ DReduced dtask_reduce(const DualStreamArgs& A, const 
     for (int m = 0; m < 2; ++m)
 #pragma unroll
       for (int j = 0; j < MT; ++j) v[(r * 2 + m) * MT + j] = acc[r][m][j];
-  DReduced o;
+  DReduced o = dred_slot<MT, RG>(A, S, ti, lane);
   o.y = wave_transpose_reduce<LNV>(v, lane);
-  const int idx = lane >> (6 - LNV);
-  o.r = idx / (2 * MT);
-  o.m = (idx / MT) & 1;
-  o.j = idx % MT;
-  const int nr = min(RG, S.nrows - ti * RG);
-  o.wr = (lane & ((1 << (6 - LNV)) - 1)) == 0 && o.r < nr && o.j < A.M;
   return o;
 }
 
@@ -506,7 +517,8 @@ struct DualRunner {
       dwin_data<MT, RG, PW, SM>(A, S, t, idx, lane, W);
       dwin_apply<MT, RG, PW>(lds, lo, W, pend);
     }
-    if (SPLIT && S.parts > 1) dtask_accumulate<MT, RG>(A, S, pend_ti, lane, pend);
+    if (SPLIT && S.red != nullptr) S.red[lane] = dtask_reduce<MT, RG>(A, S, pend_ti, lane, pend).y;
+    else if (SPLIT && S.parts > 1) dtask_accumulate<MT, RG>(A, S, pend_ti, lane, pend);
     else dtask_write<MT, RG>(A, S, pend_ti, lane, pend);
     pend_ti = -1;
   }
@@ -652,6 +664,7 @@ __device__ __forceinline__ void dual_seg(const pp_dual_proj& P, int row0, int ro
   S.row0 = row0;
   S.acc = nullptr;
   S.cnt = nullptr;
+  S.red = nullptr;
 }
 
 template <int MT, int PW, int LAYOUT, int SM, bool SPLIT>
@@ -688,24 +701,39 @@ __global__ __launch_bounds__(DualCfg<MT>::NT) void dual_stream_kernel(const Dual
 // the quad row kernel deals them), no segment table.  The wave requests its first plug
 // ranges, then the LUTs, its first window's entries and first chunks, so their round trips
 // run under the table build.
-template <int MT, int PW, int LAYOUT, int SM, bool SPLIT>
+// PARTS: 0 whole rows; 1 K parts meeting through the workspace; 2 a task's parts are
+// consecutive waves of one workgroup (wg_item), each parks its reduced sums in LDS and, after a
+// barrier every wave of the workgroup reaches, the part-0 wave adds them and writes the outputs
+// (no workspace, no atomics).
+template <int MT, int PW, int LAYOUT, int SM, int PARTS>
 __global__ __launch_bounds__(DualCfg<MT>::NT) void dual_direct_kernel(const DualStreamArgs A) {
   constexpr int RG = DualCfg<MT>::RG, NT = DualCfg<MT>::NT, WAVES = NT / 64;
-  __shared__ __attribute__((aligned(16))) uint32_t Tb[DLDS_BYTES / 4];
+  constexpr bool SPLIT = PARTS != 0;
+  __shared__ __attribute__((aligned(16))) uint32_t Tb[(DLDS_BYTES + (PARTS == 2 ? 256 * WAVES : 0)) / 4];
   char* lds = reinterpret_cast<char*>(Tb);
-  const int64_t gw = (int64_t)blockIdx.x * WAVES + uniform(threadIdx.x >> 6);
+  const int wave = uniform(threadIdx.x >> 6);
+  const int64_t gw = (int64_t)blockIdx.x * WAVES + wave;
   const int K = uniform(A.proj.K), N = uniform(A.proj.N);
-  const DirectItem d = direct_item<WAVES>((uint32_t)gw, gridDim.x * WAVES, (uint32_t)uniform64(A.n_tasks),
-                                          (uint32_t)uniform(A.parts), (uint32_t)uniform(A.n_chunks), DPAIRS,
-                                          (uint32_t)K);
+  constexpr bool wg = PARTS == 2;
+  const uint32_t parts = (uint32_t)uniform(A.parts);
+  const DirectItem d = wg ? wg_item<WAVES>(blockIdx.x, gridDim.x, (uint32_t)wave, (uint32_t)uniform64(A.n_tasks), parts,
+                                           (uint32_t)uniform(A.n_chunks), DPAIRS, (uint32_t)K)
+                          : direct_item<WAVES>((uint32_t)gw, gridDim.x * WAVES, (uint32_t)uniform64(A.n_tasks), parts,
+                                               (uint32_t)uniform(A.n_chunks), DPAIRS, (uint32_t)K);
   DualSeg S;
   dual_seg(A.proj, min(d.t0 * RG, N), min(d.t1 * RG, N), A.M, S);
   S.kbeg = uniform(d.kbeg);
   S.kend = uniform(d.kend);
-  if (SPLIT && uniform(A.parts) > 1) {
-    S.parts = uniform(A.parts);
-    S.acc = uniform_ptr(A.acc);
-    S.cnt = uniform_ptr(A.cnt) + d.t0;
+  S.red = nullptr;
+  float* red = reinterpret_cast<float*>(lds + DLDS_BYTES);
+  if (SPLIT && parts > 1) {
+    S.parts = (int)parts;
+    if (wg) {
+      S.red = red + 64 * wave;
+    } else {
+      S.acc = uniform_ptr(A.acc);
+      S.cnt = uniform_ptr(A.cnt) + d.t0;
+    }
   }
   const bool busy = S.nrows > 0 && S.kend > S.kbeg;
   DualRunner<MT, RG, PW, LAYOUT, SM, SPLIT> R(lds, A, S, d.t0);
@@ -717,9 +745,24 @@ __global__ __launch_bounds__(DualCfg<MT>::NT) void dual_direct_kernel(const Dual
   if (busy) R.template start_chunks<NB - 1>(cb);
   tb.store(lds);
   __syncthreads();
-  if (!busy) return;
-  if constexpr (MT == 1) R.run_started_one(cb);
-  else R.run_started_two(cb);
+  if constexpr (!wg) {
+    if (!busy) return;
+    if constexpr (MT == 1) R.run_started_one(cb);
+    else R.run_started_two(cb);
+  } else {
+    if (busy) {
+      if constexpr (MT == 1) R.run_started_one(cb);
+      else R.run_started_two(cb);
+    }
+    __syncthreads();   // every wave of the workgroup: the parked sums are in LDS
+    const int lane = threadIdx.x & 63;
+    if (busy && wave % (int)parts == 0) {
+      DReduced o = dred_slot<MT, RG>(A, S, 0, lane);
+      float y = 0.f;
+      for (int p = 0; p < (int)parts; ++p) y += red[64 * (wave + p) + lane];
+      dtask_store<RG>(A, S, 0, o, y);
+    }
+  }
 }
 
 // ------------------------------------------------------------------ tail rows
@@ -995,12 +1038,15 @@ static int launch_dual_stream(const DualStreamArgs& A, int pw, hipStream_t st) {
 template <int MT, int LAYOUT, int SM>
 static int launch_dual_direct(const DualStreamArgs& A, int pw, hipStream_t st) {
   const dim3 grid((unsigned)device_cu_count()), block(DualCfg<MT>::NT);
-  if (A.parts > 1) {
-    if (pw == 1) hipLaunchKernelGGL((dual_direct_kernel<MT, 1, LAYOUT, SM, true>), grid, block, 0, st, A);
-    else hipLaunchKernelGGL((dual_direct_kernel<MT, 2, LAYOUT, SM, true>), grid, block, 0, st, A);
+  if (A.parts > 1 && A.wg_parts) {
+    if (pw == 1) hipLaunchKernelGGL((dual_direct_kernel<MT, 1, LAYOUT, SM, 2>), grid, block, 0, st, A);
+    else hipLaunchKernelGGL((dual_direct_kernel<MT, 2, LAYOUT, SM, 2>), grid, block, 0, st, A);
+  } else if (A.parts > 1) {
+    if (pw == 1) hipLaunchKernelGGL((dual_direct_kernel<MT, 1, LAYOUT, SM, 1>), grid, block, 0, st, A);
+    else hipLaunchKernelGGL((dual_direct_kernel<MT, 2, LAYOUT, SM, 1>), grid, block, 0, st, A);
   } else {
-    if (pw == 1) hipLaunchKernelGGL((dual_direct_kernel<MT, 1, LAYOUT, SM, false>), grid, block, 0, st, A);
-    else hipLaunchKernelGGL((dual_direct_kernel<MT, 2, LAYOUT, SM, false>), grid, block, 0, st, A);
+    if (pw == 1) hipLaunchKernelGGL((dual_direct_kernel<MT, 1, LAYOUT, SM, 0>), grid, block, 0, st, A);
+    else hipLaunchKernelGGL((dual_direct_kernel<MT, 2, LAYOUT, SM, 0>), grid, block, 0, st, A);
   }
   PP_LAUNCH_CHECK();
   return PP_OK;
@@ -1019,6 +1065,7 @@ static int dispatch_dual_direct(const DualStreamArgs& A, int mt, int pw, hipStre
 // workspace (per-task counters, 256-byte aligned, then accumulators [2][M][N]).
 struct DualDirectPlan {
   int mt, rg, parts, n_chunks;
+  bool wg;                 // the parts meet in LDS (no workspace)
   int64_t n_tasks, waves, cnt_bytes, split_bytes;
 };
 static DualDirectPlan dual_direct_plan(int64_t M, int64_t N, int64_t K) {
@@ -1030,8 +1077,9 @@ static DualDirectPlan dual_direct_plan(int64_t M, int64_t N, int64_t K) {
   p.n_tasks = (N + p.rg - 1) / p.rg;
   p.n_chunks = (int)std::max<int64_t>(1, (K + DPAIRS - 1) / DPAIRS);
   p.parts = direct_parts(p.n_tasks, p.waves, p.n_chunks);
-  p.cnt_bytes = p.parts > 1 ? (p.n_tasks * 4 + 255) / 256 * 256 : 0;
-  p.split_bytes = p.parts > 1 ? p.cnt_bytes + 4 * 2 * M * N : 0;
+  p.wg = wg_parts_ok(p.n_tasks, p.waves, p.parts, nt / 64);
+  p.cnt_bytes = p.parts > 1 && !p.wg ? (p.n_tasks * 4 + 255) / 256 * 256 : 0;
+  p.split_bytes = p.parts > 1 && !p.wg ? p.cnt_bytes + 4 * 2 * M * N : 0;
   return p;
 }
 
@@ -1115,6 +1163,11 @@ extern "C" int64_t pp_dual_stream_waves(int64_t M) {
   return (int64_t)device_cu_count() * (dual_stream_nt(dual_stream_mt(M)) / 64);
 }
 
+extern "C" int pp_dual_rows_parts(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > 4 || N < 1 || K < 1) return 0;
+  return dual_direct_plan(M, N, K).parts;
+}
+
 extern "C" int64_t pp_dual_rows_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || M > 4 || N < 1 || K < 1) return 0;
   return dual_direct_plan(M, N, K).split_bytes;
@@ -1178,7 +1231,8 @@ extern "C" int pp_dual_rows(const pp_dual_proj* proj, const int64_t* task_plug, 
   A.proj = P;
   A.parts = p.parts;
   A.n_chunks = p.n_chunks;
-  if (p.parts > 1) {
+  A.wg_parts = p.wg ? 1 : 0;
+  if (p.parts > 1 && !p.wg) {
     A.cnt = reinterpret_cast<uint32_t*>(workspace);
     A.acc = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + p.cnt_bytes);
   }

@@ -80,6 +80,7 @@ struct QuadRowsArgs {
   int64_t o_sn;
   int64_t n_tasks;
   int parts, n_chunks;       // column slices; chunks of the K columns
+  int wg_parts;              // 1: a task's slices are waves of one workgroup, summed in LDS
   float* acc;                // parts > 1: accumulators [4][M][N] (zero on entry, left zero)
   uint32_t* cnt;             // parts > 1: one arrival counter per task (zero on entry, left zero)
   const int64_t* wave_plug;  // plug start of each wave's first row (n_waves + 1), or null
@@ -114,6 +115,7 @@ struct SegCtx {
   int N;              // rows of the projection (accumulator stride)
   float* acc;         // parts > 1: the projection's accumulators
   uint32_t* cnt;      // parts > 1: counter of the segment's first task
+  bool park;          // slices meeting in LDS: the runner keeps its reduced sum (SegRunner::parked)
 };
 
 template <int MT, int RG, int NSEG>
@@ -381,6 +383,21 @@ struct Reduced {
   bool wr;       // this lane writes it
 };
 
+// The (row, model, token) lane `lane` holds after the reduction below, and whether it writes.
+template <int MT, int RG>
+__device__ __forceinline__ Reduced<MT, RG> task_slot(const QuadRowsArgs& A, const SegCtx& S, int ti, int lane) {
+  constexpr int LNV = Log2<RG * 4 * MT>::v;
+  Reduced<MT, RG> o;
+  o.y = 0.f;
+  const int idx = lane >> (6 - LNV);
+  o.r = idx / (4 * MT);
+  o.m = (idx / MT) & 3;
+  o.j = idx % MT;
+  const int nr = min(RG, S.nrows - ti * RG);
+  o.wr = (lane & ((1 << (6 - LNV)) - 1)) == 0 && o.r < nr && o.j < A.M;
+  return o;
+}
+
 template <int MT, int RG>
 __device__ __forceinline__ Reduced<MT, RG> task_reduce(const QuadRowsArgs& A, const SegCtx& S, int ti, int lane,
                                                        float (&acc)[RG][4][MT]) {
@@ -394,14 +411,8 @@ __device__ __forceinline__ Reduced<MT, RG> task_reduce(const QuadRowsArgs& A, co
     for (int m = 0; m < 4; ++m)
 #pragma unroll
       for (int j = 0; j < MT; ++j) v[(r * 4 + m) * MT + j] = acc[r][m][j];
-  Reduced<MT, RG> o;
+  Reduced<MT, RG> o = task_slot<MT, RG>(A, S, ti, lane);
   o.y = wave_transpose_reduce<LNV>(v, lane);
-  const int idx = lane >> (6 - LNV);
-  o.r = idx / (4 * MT);
-  o.m = (idx / MT) & 3;
-  o.j = idx % MT;
-  const int nr = min(RG, S.nrows - ti * RG);
-  o.wr = (lane & ((1 << (6 - LNV)) - 1)) == 0 && o.r < nr && o.j < A.M;
   return o;
 }
 
@@ -490,9 +501,10 @@ struct SegRunner {
   PlugSt<MT> P;            // plug entries of the pending task (then of the current one)
   int64_t pc;
   Cursor lc;               // next chunk to load
+  float parked;            // S.park: the last task's reduced (unscaled) sum of this lane
 
   __device__ __forceinline__ SegRunner(const char* l, const QuadRowsArgs& a, const SegCtx& s, int64_t plug_lo)
-      : lds(l), A(a), S(s), pend_ti(-1), pc(plug_lo) {
+      : lds(l), A(a), S(s), pend_ti(-1), pc(plug_lo), parked(0.f) {
     lane = threadIdx.x & 63;
     lo = L::lane(lane);
     nck = (S.kend - S.kbeg + CHUNK - 1) / CHUNK;
@@ -523,7 +535,8 @@ struct SegRunner {
   __device__ __forceinline__ void finish_pending() {
     plug_end<MT, RG, L>(lds, lo, A, S, pend_ti, lane, pc, P, pend);
     if constexpr (SPLIT) {
-      if (S.parts > 1) task_accumulate<MT, RG>(A, S, pend_ti, lane, pend);
+      if (S.park) parked = task_reduce<MT, RG>(A, S, pend_ti, lane, pend).y;
+      else if (S.parts > 1) task_accumulate<MT, RG>(A, S, pend_ti, lane, pend);
       else task_write<MT, RG>(A, S, pend_ti, lane, pend);
     } else {
       task_write<MT, RG>(A, S, pend_ti, lane, pend);
@@ -618,6 +631,7 @@ __device__ __forceinline__ void seg_ctx(const pp_quad_proj& P, int64_t o_sn, int
   S.N = uniform(P.N);
   S.acc = nullptr;
   S.cnt = nullptr;
+  S.park = false;
 }
 
 // Wave gw of the launch; [s0, s1) its segments (stream front end).
@@ -647,27 +661,39 @@ __device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A
 // before the table build and the round trip to HBM runs under the build: first the plug
 // start of its first row (so that waiting for it waits for nothing else), then the LUT
 // loads, then the first chunk; the build waits for the LUT values only.
-template <int MT, typename E, bool SPLIT>
+// PARTS: 0 whole rows; 1 column slices meeting through the workspace; 2 a task's slices are
+// consecutive waves of one workgroup (wg_item): each keeps its reduced sums, and after every
+// wave of the workgroup is done with the tables (a barrier) they go into the table memory,
+// where after a second barrier the slice-0 wave adds them and writes the outputs.
+template <int MT, typename E, int PARTS>
 __device__ __forceinline__ void direct_body(uint32_t* T, const QuadRowsArgs& A, int64_t gw) {
-  constexpr int RG = RowsCfg<MT>::RG, NSEG = RowsCfg<MT>::NSEG, NT = RowsCfg<MT>::NT;
+  constexpr int RG = RowsCfg<MT>::RG, NSEG = RowsCfg<MT>::NSEG, NT = RowsCfg<MT>::NT, WAVES = NT / 64;
+  constexpr bool SPLIT = PARTS != 0, WG = PARTS == 2;
   const int lane = threadIdx.x & 63;
-  const int64_t W = (int64_t)gridDim.x * (NT / 64);
+  const int64_t W = (int64_t)gridDim.x * WAVES;
   u32x2 wp = {0u, 0u};
   if (A.wave_plug != nullptr) vload64(wp, 8u * (uint32_t)gw, make_rsrc(A.wave_plug, 8u * (uint32_t)(W + 1)));
   QuadTableBuild<NT, E> tb;
   tb.load(A.luts);
   const int K = uniform(A.proj.K), N = uniform(A.proj.N);
-  const DirectItem d = direct_item<NT / 64>((uint32_t)gw, (uint32_t)W, (uint32_t)uniform64(A.n_tasks),
-                                           (uint32_t)uniform(A.parts), (uint32_t)uniform(A.n_chunks), NSEG * QSEG,
-                                           (uint32_t)K);
+  const uint32_t parts = (uint32_t)uniform(A.parts);
+  const int wave = (int)(gw - (int64_t)blockIdx.x * WAVES);
+  const DirectItem d = WG ? wg_item<WAVES>(blockIdx.x, gridDim.x, (uint32_t)wave, (uint32_t)uniform64(A.n_tasks), parts,
+                                           (uint32_t)uniform(A.n_chunks), NSEG * QSEG, (uint32_t)K)
+                          : direct_item<WAVES>((uint32_t)gw, (uint32_t)W, (uint32_t)uniform64(A.n_tasks), parts,
+                                               (uint32_t)uniform(A.n_chunks), NSEG * QSEG, (uint32_t)K);
   SegCtx S;
   seg_ctx(A.proj, A.o_sn, min(d.t0 * RG, N), min(d.t1 * RG, N), A.M, S);
   S.kbeg = uniform(d.kbeg);
   S.kend = uniform(d.kend);
-  if (SPLIT && uniform(A.parts) > 1) {
-    S.parts = uniform(A.parts);
-    S.acc = uniform_ptr(A.acc);
-    S.cnt = uniform_ptr(A.cnt) + d.t0;
+  if (SPLIT && parts > 1) {
+    S.parts = (int)parts;
+    if (WG) {
+      S.park = true;
+    } else {
+      S.acc = uniform_ptr(A.acc);
+      S.cnt = uniform_ptr(A.cnt) + d.t0;
+    }
   }
   const bool busy = S.nrows > 0 && S.kend > S.kbeg;
   uint32_t voff[RG];
@@ -676,18 +702,36 @@ __device__ __forceinline__ void direct_body(uint32_t* T, const QuadRowsArgs& A, 
   Chunk<MT, RG, NSEG> c0;
   if (busy) chunk_issue<MT, RG, NSEG>(S, 0, S.kbeg, voff, lane, c0);   // 1 us faster than after the build
   const bool shared = tb.finish(T, A.luts);
-  if (!busy) return;
+  if (!WG && !busy) return;
   // the caller's plan, kept inside the table whatever it holds (a stale plan must not send
   // the plug loads outside it)
   const int64_t pc = std::min<int64_t>(std::max<int64_t>(uniform64((int64_t)(((uint64_t)wp[1] << 32) | wp[0])), 0),
                                        A.plug_n);
   const char* lds = reinterpret_cast<const char*>(T);
-  if (shared) {
-    SegRunner<MT, RG, NSEG, LayShared, SPLIT> R(lds, A, S, pc);
-    R.run_issued(c0);
-  } else {
-    SegRunner<MT, RG, NSEG, LaySplit, SPLIT> R(lds, A, S, pc);
-    R.run_issued(c0);
+  float y = 0.f;
+  if (busy) {
+    if (shared) {
+      SegRunner<MT, RG, NSEG, LayShared, SPLIT> R(lds, A, S, pc);
+      R.run_issued(c0);
+      y = R.parked;
+    } else {
+      SegRunner<MT, RG, NSEG, LaySplit, SPLIT> R(lds, A, S, pc);
+      R.run_issued(c0);
+      y = R.parked;
+    }
+  }
+  if constexpr (WG) {
+    float* red = reinterpret_cast<float*>(T);
+    __syncthreads();   // every wave of the workgroup is done with the tables
+    red[64 * wave + lane] = y;
+    __syncthreads();
+    if (busy && wave % (int)parts == 0) {
+      Reduced<MT, RG> o = task_slot<MT, RG>(A, S, 0, lane);
+      float t = 0.f;
+      for (int p = 0; p < (int)parts; ++p) t += red[64 * (wave + p) + lane];
+      const float val[4] = {t * A.s[0], t * A.s[1], t * A.s[2], t * A.s[3]};
+      task_store<MT, RG>(A, S, 0, o, val);
+    }
   }
 }
 
@@ -704,13 +748,13 @@ __global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_rows_kernel(const QuadRo
 }
 
 // One Linear (segs == nullptr): a kernel of its own, so that the whole-stream kernel keeps
-// its register allocation.
-template <int MT, bool SPLIT>
+// its register allocation.  PARTS as direct_body.
+template <int MT, int PARTS>
 __global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_direct_kernel(const QuadRowsArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t T[QLDS_BYTES / 4];
   const int64_t gw = (int64_t)blockIdx.x * (RowsCfg<MT>::NT / 64) + uniform(threadIdx.x >> 6);
-  if (A.luts.dtype == PP_F16) direct_body<MT, f16, SPLIT>(T, A, gw);
-  else direct_body<MT, float, SPLIT>(T, A, gw);
+  if (A.luts.dtype == PP_F16) direct_body<MT, f16, PARTS>(T, A, gw);
+  else direct_body<MT, float, PARTS>(T, A, gw);
 }
 
 // ------------------------------------------------------------------ tail rows
@@ -809,16 +853,18 @@ __global__ __launch_bounds__(256) void quad_tail_kernel(const QuadTailArgs A) {
 template <int G>
 __global__ void wave_plug_kernel(const uint32_t* plug_idx, int64_t plug_n, int64_t pos0, int64_t ldc,
                                  int rows_per_task, int64_t n_tasks, int parts, int n_chunks, int chunk, int K,
-                                 int64_t n_waves, int N, int64_t* wave_plug) {
+                                 int64_t n_waves, int N, int wg, int64_t* wave_plug) {
   const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (g > n_waves) return;
   int64_t row = N;
-  if (g < n_waves)
-    row = std::min<int64_t>((int64_t)direct_item<G>((uint32_t)g, (uint32_t)n_waves, (uint32_t)n_tasks, (uint32_t)parts,
-                                                     (uint32_t)n_chunks, (uint32_t)chunk, (uint32_t)K)
-                                    .t0 *
-                                rows_per_task,
-                            N);
+  if (g < n_waves) {
+    const DirectItem d = wg ? wg_item<G>((uint32_t)(g / G), (uint32_t)(n_waves / G), (uint32_t)(g % G),
+                                         (uint32_t)n_tasks, (uint32_t)parts, (uint32_t)n_chunks, (uint32_t)chunk,
+                                         (uint32_t)K)
+                            : direct_item<G>((uint32_t)g, (uint32_t)n_waves, (uint32_t)n_tasks, (uint32_t)parts,
+                                             (uint32_t)n_chunks, (uint32_t)chunk, (uint32_t)K);
+    row = std::min<int64_t>((int64_t)d.t0 * rows_per_task, N);
+  }
   const int64_t key = pos0 + row * ldc;
   int64_t lo = 0, hi = plug_n;
   while (lo < hi) {
@@ -849,16 +895,23 @@ static int cfg_waves(int mt) {
   }
 }
 
+template <int PARTS>
+static void launch_direct_t(const QuadRowsArgs& A, int mt, hipStream_t st) {
+  const unsigned grid = (unsigned)device_cu_count();
+  switch (mt) {
+    case 1: hipLaunchKernelGGL((quad_direct_kernel<1, PARTS>), dim3(grid), dim3(RowsCfg<1>::NT), 0, st, A); break;
+    case 2: hipLaunchKernelGGL((quad_direct_kernel<2, PARTS>), dim3(grid), dim3(RowsCfg<2>::NT), 0, st, A); break;
+    case 4: hipLaunchKernelGGL((quad_direct_kernel<4, PARTS>), dim3(grid), dim3(RowsCfg<4>::NT), 0, st, A); break;
+    default: hipLaunchKernelGGL((quad_direct_kernel<8, PARTS>), dim3(grid), dim3(RowsCfg<8>::NT), 0, st, A); break;
+  }
+}
+
 template <bool SPLIT>
 static void launch_rows_t(const QuadRowsArgs& A, int mt, hipStream_t st) {
   const unsigned grid = (unsigned)device_cu_count();
   if (A.segs == nullptr) {
-    switch (mt) {
-      case 1: hipLaunchKernelGGL((quad_direct_kernel<1, SPLIT>), dim3(grid), dim3(RowsCfg<1>::NT), 0, st, A); break;
-      case 2: hipLaunchKernelGGL((quad_direct_kernel<2, SPLIT>), dim3(grid), dim3(RowsCfg<2>::NT), 0, st, A); break;
-      case 4: hipLaunchKernelGGL((quad_direct_kernel<4, SPLIT>), dim3(grid), dim3(RowsCfg<4>::NT), 0, st, A); break;
-      default: hipLaunchKernelGGL((quad_direct_kernel<8, SPLIT>), dim3(grid), dim3(RowsCfg<8>::NT), 0, st, A); break;
-    }
+    if (SPLIT && A.wg_parts) launch_direct_t<2>(A, mt, st);
+    else launch_direct_t<SPLIT ? 1 : 0>(A, mt, st);
     return;
   }
   switch (mt) {
@@ -909,6 +962,7 @@ static int cfg_chunk(int mt) {
 // accumulators [4][M][N].
 struct DirectPlan {
   int mt, rg, chunk, parts, n_chunks;
+  bool wg;                 // the slices meet in LDS (no workspace)
   int64_t n_tasks, waves, cnt_bytes, split_bytes;
 };
 static DirectPlan direct_plan(int64_t M, int64_t N, int64_t K, bool split) {
@@ -920,8 +974,9 @@ static DirectPlan direct_plan(int64_t M, int64_t N, int64_t K, bool split) {
   p.n_tasks = (N + p.rg - 1) / p.rg;
   p.n_chunks = (int)std::max<int64_t>(1, (K + p.chunk - 1) / p.chunk);
   p.parts = split ? direct_parts(p.n_tasks, p.waves, p.n_chunks) : 1;
-  p.cnt_bytes = p.parts > 1 ? (p.n_tasks * 4 + 255) / 256 * 256 : 0;
-  p.split_bytes = p.parts > 1 ? p.cnt_bytes + 4 * 4 * M * N : 0;
+  p.wg = wg_parts_ok(p.n_tasks, p.waves, p.parts, cfg_waves(p.mt));
+  p.cnt_bytes = p.parts > 1 && !p.wg ? (p.n_tasks * 4 + 255) / 256 * 256 : 0;
+  p.split_bytes = p.parts > 1 && !p.wg ? p.cnt_bytes + 4 * 4 * M * N : 0;
   return p;
 }
 
@@ -943,6 +998,7 @@ static void direct_args(QuadRowsArgs& A, const DirectPlan& p, const void* a, int
   A.n_tasks = p.n_tasks;
   A.parts = p.parts;
   A.n_chunks = p.n_chunks;
+  A.wg_parts = p.wg ? 1 : 0;
   A.luts = make_luts(luts, lut_dtype);
   for (int m = 0; m < 4; ++m) A.s[m] = scales[m];
   A.plug_idx = plug_idx;
@@ -958,7 +1014,7 @@ static int launch_wave_plug(const DirectPlan& p, const uint32_t* plug_idx, int64
                 "one workgroup size for the one-Linear launches");
   hipLaunchKernelGGL(wave_plug_kernel<RowsCfg<1>::NT / 64>, dim3((unsigned)((p.waves + 1 + 255) / 256)), dim3(256), 0,
                      st, plug_idx, plug_n, elem_base, ldc, p.rg, p.n_tasks, p.parts, p.n_chunks, p.chunk, (int)K,
-                     p.waves, (int)N, wave_plug);
+                     p.waves, (int)N, p.wg ? 1 : 0, wave_plug);
   PP_LAUNCH_CHECK();
   return PP_OK;
 }
@@ -1027,6 +1083,11 @@ extern "C" int64_t pp_quad_rows_plan_size(int64_t M) {
 extern "C" int64_t pp_quad_rows_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M < 1 || M > 8 || N < 1 || K < 1) return 0;
   return direct_plan(M, N, K, true).split_bytes;
+}
+
+extern "C" int pp_quad_rows_parts(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || M > 8 || N < 1 || K < 1) return 0;
+  return direct_plan(M, N, K, true).parts;
 }
 
 extern "C" int pp_quad_rows_plan(const uint32_t* plug_idx, int64_t plug_n, int64_t elem_base, int64_t ldc, int64_t M,

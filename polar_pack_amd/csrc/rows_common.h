@@ -176,6 +176,27 @@ __device__ __host__ __forceinline__ DirectItem direct_item(uint32_t gw, uint32_t
   return d;
 }
 
+// The K parts of a task in one workgroup (parts divides G, T * parts <= W): wave w of
+// workgroup b takes part w % parts of task b + grid * (w / parts), so every workgroup gets a
+// task before any gets two and the parts' sums can meet in the workgroup's LDS.
+template <int G>
+__device__ __host__ __forceinline__ DirectItem wg_item(uint32_t block, uint32_t grid, uint32_t wave, uint32_t T,
+                                                       uint32_t parts, uint32_t n_chunks, uint32_t chunk, uint32_t K) {
+  const uint32_t s = wave % parts, t = block + grid * (wave / parts);
+  DirectItem d;
+  d.t0 = (int)std::min(t, T);
+  d.t1 = (int)std::min(t + 1, T);
+  d.kbeg = (int)(s * n_chunks / parts * chunk);
+  d.kend = (int)std::min<uint32_t>(K, (s + 1) * n_chunks / parts * chunk);
+  return d;
+}
+
+// Whether the K parts of a one-Linear launch meet in LDS (wg_item) rather than through the
+// workspace: a power of two that divides the workgroup's waves, one task per part group.
+inline bool wg_parts_ok(int64_t T, int64_t W, int parts, int waves_per_wg) {
+  return parts > 1 && waves_per_wg % parts == 0 && (parts & (parts - 1)) == 0 && T * parts <= W;
+}
+
 // Column slices of one Linear's T row tasks for W wavefronts and C chunks (the stream
 // planner's rule, stream.split_factors): r = W / T; r < 1.5 whole rows; 1.5 <= r < 4 two
 // slices when K holds at least 8 chunks; r >= 4 ceil(r / 2) slices, at most one per chunk.

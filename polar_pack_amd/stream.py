@@ -417,7 +417,7 @@ class QuadStream:
         ws_bytes = int(L.pp_quad_rows_workspace_size(self.M, N, K))
         self.workspace = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
         self._ws_bytes = ws_bytes
-        self.split = ws_bytes > 0
+        self.split = int(L.pp_quad_rows_parts(self.M, N, K)) > 1
         self.n_segs = self.n_tail = 0
         self.luts = header_luts(pk.r_max, device=dev)
         self._lut_ptrs = nat.ptr_array([t.data_ptr() for t in self.luts])
@@ -570,8 +570,9 @@ class DualStream:
         self.split = bool(np.any(self.segs_np["parts"] > 1))
         self.direct = one_linear and len(self.shapes) == 1 and total <= pack.n_codes and split
         if self.direct:
+            # K parts meet in LDS when a workgroup holds a task's parts, else in the workspace
             ws_bytes = int(L.pp_dual_rows_workspace_size(self.M, *self.shapes[0]))
-            self.split = ws_bytes > 0
+            self.split = int(L.pp_dual_rows_parts(self.M, *self.shapes[0])) > 1
         # split launches: counters + accumulators, zero once here, left zero by every launch
         self.workspace = torch.zeros(ws_bytes, dtype=torch.uint8, device=self.device) if ws_bytes else None
         self._ws_bytes = ws_bytes

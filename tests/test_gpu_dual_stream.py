@@ -218,7 +218,7 @@ def test_single_linear_split_k(shape, M, one_linear):
     assert st.direct == one_linear
     # slices when the launch has fewer than half as many row tasks as wavefronts
     assert st.split == (K > 512 and 2 * -(-N // st.rows_per_item) < st.n_waves)
-    assert (st.workspace is not None) == st.split
+    assert st.workspace is None or st.split
     x_np = np.random.default_rng(23).standard_normal((M, K)).astype(np.float16)
     outs = [[torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV) for _ in range(2)]]
     st.bind([torch.from_numpy(x_np).to(DEV)], outs)

@@ -11,7 +11,9 @@ from oracle import dualpack as odp
 from oracle import quadpack as oqp
 from parity import assert_gemv_close, fp16_weight_bound
 from polar_pack_amd.container import DualPackFile, QuadPackFile
+from polar_pack_amd import polar_kernels as pk
 from polar_pack_amd.linear import DualPackedLinear, QuadPackedLinear, replace_model_weights
+from refs import route_class
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -27,13 +29,15 @@ def mlp():
     return m.to(DEV).to(torch.float16)
 
 
-def run_and_check(model, weights, x_np, fused_max):
+def run_and_check(model, weights, x_np, fp16):
     """Layer by layer: each packed layer against the oracle's float64 product on the
-    input it actually received (the previous layer's fp16 output).  Batches above the
-    fused kernels' reach feed fp16 weights to the dot product, as the reference's kernels
-    do: held to the fp16-weight bound there."""
+    input it actually received (the previous layer's fp16 output).  The routes that feed
+    fp16 weights to the dot product, as the reference's kernels do (``fp16``: one flag per
+    layer, from the operator's routing table), are held to the fp16-weight bound."""
+    flags = iter(fp16)
+
     def bound(a, w):
-        return fp16_weight_bound(a, w.T) if a.shape[0] > fused_max else None
+        return fp16_weight_bound(a, w.T) if next(flags) else None
     x = torch.from_numpy(x_np).to(DEV)
     h1 = model[0](x)
     assert_gemv_close(h1.float().cpu().numpy(), x_np.astype(np.float64) @ weights[0].T, "layer 0",
@@ -65,7 +69,7 @@ def test_quad_packed_mlp_every_model(M):
         assert replace_model_weights(model, pack, LAYERS, model_index=k) == 2
         assert isinstance(model[0], QuadPackedLinear) and isinstance(model[2], QuadPackedLinear)
         weights = [W[k][:96 * 256].reshape(96, 256), W[k][96 * 256:].reshape(40, 96)]
-        run_and_check(model, weights, x_np, 8)
+        run_and_check(model, weights, x_np, (M > 8, M > 8))
     # all four models from one pass: the per-model layers' outputs (split-K sums may
     # meet in another order between launches, so equal to the GEMV tolerance, not bitwise)
     both = QuadPackedLinear(pack, 96, 256, 0)
@@ -99,7 +103,11 @@ def test_dual_packed_mlp(layout, M):
         assert replace_model_weights(model, pack, LAYERS, model_index=k) == 2
         assert isinstance(model[0], DualPackedLinear)
         weights = [d[k][:96 * 256].reshape(96, 256), d[k][96 * 256:].reshape(40, 96)]
-        run_and_check(model, weights, x_np, 4)
+        fp16 = [route_class(pk.dual_call_route(layer.codes, M, layout=pack.layout, group_size=pack.group_size,
+                                               chunk_size=pack.chunk_size, elem_base=layer.pos0,
+                                               plug_n=pack.plug_idx.numel())) != "fused"
+                for layer in (model[0], model[2])]
+        run_and_check(model, weights, x_np, fp16)
 
 
 def test_projection_outside_the_coded_stream_is_rejected():
