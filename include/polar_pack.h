@@ -553,8 +553,17 @@ int64_t pp_dual_rows_workspace_size(int64_t M, int64_t N, int64_t K);
  * workgroup's waves, a task's parts are waves of one workgroup and their sums meet in LDS
  * (no workspace: pp_dual_rows_workspace_size is 0); otherwise they meet in the workspace. */
 int pp_dual_rows_parts(int64_t M, int64_t N, int64_t K);
-int pp_dual_rows(const pp_dual_proj* proj, const int64_t* task_plug, int plug_windows, int code_layout,
-                 const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
+/* The one-Linear launch's per-task plug records (no reference counterpart: a re-layout of
+ * pp_dual_plug_table's records): task t's records plug_ent[task_plug[2t] .. task_plug[2t+1])
+ * copied to out[t * task_cap ..] (8 bytes each), null records after them; task_cap must be
+ * at least every task's entry count.  out holds n_tasks * task_cap records. */
+int pp_dual_task_entries(const uint32_t* plug_ent, int64_t plug_n, const int64_t* task_plug, int64_t n_tasks,
+                         int64_t task_cap, uint32_t* out, void* stream);
+/* task_cap 0: plug_ent holds pp_dual_plug_table's records and task_plug their ranges per task;
+ * task_cap > 0: plug_ent holds pp_dual_task_entries' task_cap records per task (task_plug
+ * may be null), so a wave loads its task's records without first loading their range. */
+int pp_dual_rows(const pp_dual_proj* proj, const int64_t* task_plug, int64_t task_cap, int plug_windows,
+                 int code_layout, const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
                  const void* scale_tab, int64_t n_tab, const float* amp_lut, const float* cos_lut,
                  const float* sin_lut, const uint32_t* plug_idx, const void* plug_amp,
                  const uint32_t* plug_ent, int64_t plug_n, int64_t M, void* workspace,

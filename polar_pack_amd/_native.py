@@ -99,8 +99,9 @@ EXPORTS = {
     "pp_dual_scale_table": (i32, [vp, i64, i64, vp, vp, vp, i64, i64, vp, i64, vp]),
     "pp_dual_rows_workspace_size": (i64, [i64, i64, i64]),
     "pp_dual_rows_parts": (i32, [i64, i64, i64]),
-    "pp_dual_rows": (i32, [vp, vp, i32, i32, vp, i64, i64, i64, vp, i64, vp, vp, vp, vp, vp, vp, i64, i64, vp, i64,
-                           vp]),
+    "pp_dual_rows": (i32, [vp, vp, i64, i32, i32, vp, i64, i64, i64, vp, i64, vp, vp, vp, vp, vp, vp, i64, i64, vp,
+                           i64, vp]),
+    "pp_dual_task_entries": (i32, [vp, i64, vp, i64, i64, vp, vp]),
     "pp_dual_plug_table": (i32, [vp, i64, i32, vp, i64, i64, i64, vp, vp, vp, i64, vp, vp, i64, i64, vp, vp]),
     "pp_dual_gemm": (i32, [vp, i64, i64, vp, i32, i64, i64, vp, i64, i64, vp, i32, vp, vp, i32, i32,
                            vp, vp, i64, i64, vp, vp, i64, i64, i64, i64, i64, vp, i64, vp]),

@@ -60,6 +60,9 @@ struct DualStreamArgs {
   int64_t plug_n;
   const int64_t* task_plug;   // per task: first plug entry in its rows, first entry past them
   int64_t n_tasks;
+  int64_t task_cap;           // > 0: plug_ent holds task_cap records per task (task t's entries
+                              // from t * task_cap, null records after them) and plug_n is its
+                              // length; task_plug is not read (one-Linear launch)
   int M;
   void* ws;                   // split launches: per-task counters, then float32 accumulators
   // one-Linear launch (dual_direct_kernel): the projection, its column slices and chunks,
@@ -155,16 +158,17 @@ __device__ __forceinline__ uint32_t dchunk_scale(const DChunk<MT, RG>& c, int r)
   }
 }
 
+// live = false (a buffer filled past the wave's last chunk): every load reads nothing.
 template <int MT, int RG, int SM>
 __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const DualSeg& S, int row, int kc,
-                                             const uint32_t (&voff)[RG], int lane, DChunk<MT, RG>& c) {
+                                             const uint32_t (&voff)[RG], int lane, bool live, DChunk<MT, RG>& c) {
   const int64_t first = (int64_t)row * S.ldc + kc;
   const int64_t end = (int64_t)(S.nrows - 1) * S.ldc + S.K;
   const rsrc_t rc = make_rsrc(S.codes + first, 2u * (uint32_t)(end - first));
   const rsrc_t rs = make_rsrc(A.scales, 2u * (uint32_t)A.n_groups);
   // lanes past the row end read nothing: those codes start the next row, whose own first
   // chunk reads them (38 MB of the 3B-shaped stream's 11008-pair rows, read twice otherwise)
-  const bool in_row = 8 * lane < S.K - kc;
+  const bool in_row = live && 8 * lane < S.K - kc;
 #pragma unroll
   for (int r = 0; r < RG; ++r) vload128(c.q[r], in_row ? voff[r] : OOB, rc);
   const int k = kc + 8 * lane;
@@ -176,7 +180,7 @@ __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const Dual
     static_assert(RG == 8 || RG == 4 || RG == 2, "scale table cells hold 8, 4 or 2 rows");
     const int64_t t0 = (S.pos0 + (int64_t)row * S.ldc) >> A.log2gs;
     const rsrc_t rt = make_rsrc(A.scale_tab + t0, 2u * (uint32_t)(A.n_tab - t0));
-    const uint32_t off = 2u * RG * ((uint32_t)k >> A.log2gs);
+    const uint32_t off = live ? 2u * RG * ((uint32_t)k >> A.log2gs) : OOB;
     if constexpr (RG == 8) {
       vload128(c.sq, off, rt);
     } else if constexpr (RG == 4) {
@@ -191,7 +195,7 @@ __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const Dual
   } else {
 #pragma unroll
     for (int r = 0; r < RG; ++r) {
-      const bool in = (row + r) < S.nrows && k < S.kend;
+      const bool in = live && (row + r) < S.nrows && k < S.kend;
       const int64_t br = base + (int64_t)r * S.ldc;
       uint32_t g;
       if constexpr (SM == 0) {
@@ -207,10 +211,11 @@ __device__ __forceinline__ void dchunk_issue(const DualStreamArgs& A, const Dual
   if constexpr (MT == 1) {
     // columns past the slice read x = 0, so the codes loaded there add nothing
     const rsrc_t rx = make_rsrc(S.x + kc, 2u * (uint32_t)(S.kend - kc));
-    vload128c(c.xr[0], 16u * lane, rx);
+    vload128c(c.xr[0], live ? 16u * lane : OOB, rx);
   } else {
 #pragma unroll
-    for (int j = 0; j < MT; ++j) vload128c(c.xr[j], k < S.kend ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
+    for (int j = 0; j < MT; ++j)
+      vload128c(c.xr[j], live && k < S.kend ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
   }
 }
 
@@ -455,6 +460,7 @@ struct DualRunner {
   int pend_ti;
   DSlot pend_left;           // entries of the parked task left after its last step
   Cursor lc;                 // chunk to prefetch
+  bool lc_live;              // false once every chunk of the wave is issued
   DSlot s0, s1, s2;          // windows of steps s, s+1, s+2 (s = the step being computed)
   Cursor c3;                 // step s+3, whose task plug range is in flight
   u32x4 T;                   // that range: {tlo lo, tlo hi, thi lo, thi hi}
@@ -468,6 +474,7 @@ struct DualRunner {
     nck = (S.kend - S.kbeg + DPAIRS - 1) / DPAIRS;
     ntask = (S.nrows + RG - 1) / RG;
     lc = {0, 0};
+    lc_live = true;
 #pragma unroll
     for (int r = 0; r < RG; ++r) voff[r] = 2u * (uint32_t)(r * S.ldc) + 16u * lane;
     dzero<MT, RG>(acc);
@@ -484,15 +491,26 @@ struct DualRunner {
     if (c.ti < ntask) advance(c);
   }
 
+  // Ranges come from task_plug, one load per task; with per-task records (task_cap > 0) a
+  // task's range is its block of the array, known without a load.
   __device__ __forceinline__ void load_range(const Cursor& c, u32x4& t) const {
+    if (uniform64(A.task_cap) > 0) {
+      t = u32x4{0u, 0u, 0u, 0u};
+      return;
+    }
     vload128(t, c.ti < ntask ? 16u * (uint32_t)(task0 + c.ti) : OOB,
              make_rsrc(A.task_plug, 16u * (uint32_t)A.n_tasks));
   }
   __device__ __forceinline__ DSlot slot_of(const Cursor& c, const u32x4& t) const {
-    const int64_t tlo =
-        (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane(t.y) << 32) | __builtin_amdgcn_readfirstlane(t.x));
-    const int64_t thi =
-        (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane(t.w) << 32) | __builtin_amdgcn_readfirstlane(t.z));
+    const int64_t cap = uniform64(A.task_cap);
+    int64_t tlo, thi;
+    if (cap > 0) {
+      tlo = (int64_t)(task0 + c.ti) * cap;
+      thi = c.ti < ntask ? min(tlo + cap, (int64_t)A.plug_n) : tlo;
+    } else {
+      tlo = (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane(t.y) << 32) | __builtin_amdgcn_readfirstlane(t.x));
+      thi = (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane(t.w) << 32) | __builtin_amdgcn_readfirstlane(t.z));
+    }
     DSlot s;
     s.ti = c.ti;
     s.lo = tlo + (int64_t)(64 * PW) * c.ck;
@@ -502,10 +520,11 @@ struct DualRunner {
   }
 
   __device__ __forceinline__ void prefetch(DChunk<MT, RG>& c) {
-    dchunk_issue<MT, RG, SM>(A, S, lc.ti * RG, S.kbeg + lc.ck * DPAIRS, voff, lane, c);
+    dchunk_issue<MT, RG, SM>(A, S, lc.ti * RG, S.kbeg + lc.ck * DPAIRS, voff, lane, lc_live, c);
     Cursor nx = lc;
     advance(nx);
     if (nx.ti < ntask) lc = nx;
+    else lc_live = false;
   }
 
   // Entries of the finished task that its steps could not take, then its outputs.
@@ -523,19 +542,20 @@ struct DualRunner {
     pend_ti = -1;
   }
 
-  // prefetch | range of step s+2, range load for s+3 | corrections of step s | data loads
-  // for s+1 | positions for s+2 | [first chunk] finish the previous task | decode |
-  // [last chunk] park the sums
+  // prefetch | range of step s+2, range load for s+3 | [first chunk] finish the previous
+  // task | decode | corrections of step s | data loads for s+1 | positions for s+2 | [last
+  // chunk] park the sums.  The corrections follow the decode, so that a wave with a single
+  // step decodes while its entries' activations are in flight.
   __device__ __forceinline__ bool step(Cursor& cur, DChunk<MT, RG>& comp, DChunk<MT, RG>& pref) {
     prefetch(pref);
     s2 = slot_of(c3, T);
     advance_slot(c3);
     load_range(c3, T);
+    if (cur.ck == 0 && pend_ti >= 0) finish_pending();
+    dchunk_compute<MT, RG, LAYOUT, SM>(lds, lo, comp, acc);
     if (dslot_cnt<PW>(s0) > 0) dwin_apply<MT, RG, PW>(lds, lo, D, acc);
     dwin_data<MT, RG, PW, SM>(A, S, s1, I, lane, D);
     dwin_positions<PW>(A, s2, lane, I);
-    if (cur.ck == 0 && pend_ti >= 0) finish_pending();
-    dchunk_compute<MT, RG, LAYOUT, SM>(lds, lo, comp, acc);
     if (cur.ck == nck - 1) {
 #pragma unroll
       for (int r = 0; r < RG; ++r)
@@ -943,6 +963,20 @@ __global__ __launch_bounds__(256) void dual_tail_kernel(const DualTailArgs T) {
   }
 }
 
+// The one-Linear launch's per-task records: task t's entries ent[task_plug[2t] ..
+// task_plug[2t+1]) copied to out[t * cap ..], null records (column 0x7FFFF, past any K the
+// decode takes, and a zero correction) after them.
+__global__ __launch_bounds__(256) void dual_task_entries_kernel(const uint32_t* ent, int64_t plug_n,
+                                                                const int64_t* task_plug, int64_t n_tasks,
+                                                                int64_t cap, uint32_t* out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_tasks * cap) return;
+  const int64_t t = i / cap, src = task_plug[2 * t] + (i - t * cap);
+  const bool has = src < task_plug[2 * t + 1] && src < plug_n;
+  out[2 * i] = has ? ent[2 * src] : 0x7FFFFu;
+  out[2 * i + 1] = has ? ent[2 * src + 1] : 0u;
+}
+
 // Records of the plug entries for the stream decode (see DualStreamArgs::plug_ent).
 // Projection p covers stream positions [proj_pos0[p], proj_pos0[p] + N_p * proj_k[p]);
 // proj_pos0 has n_projs + 1 entries (the last one the end of the stream's projections).
@@ -1173,7 +1207,20 @@ extern "C" int64_t pp_dual_rows_workspace_size(int64_t M, int64_t N, int64_t K) 
   return dual_direct_plan(M, N, K).split_bytes;
 }
 
-extern "C" int pp_dual_rows(const pp_dual_proj* proj, const int64_t* task_plug, int plug_windows, int code_layout,
+extern "C" int pp_dual_task_entries(const uint32_t* plug_ent, int64_t plug_n, const int64_t* task_plug,
+                                    int64_t n_tasks, int64_t task_cap, uint32_t* out, void* stream) {
+  PP_REQUIRE(plug_n >= 1 && plug_n < (1ll << 28), "pp_dual_task_entries takes 1 .. 2^28 - 1 plug entries");
+  PP_REQUIRE(n_tasks >= 1 && task_cap >= 1 && n_tasks * task_cap < (1ll << 28),
+             "n_tasks * task_cap must lie in 1 .. 2^28 - 1");
+  PP_REQUIRE(plug_ent && task_plug && out, "null pointer");
+  hipLaunchKernelGGL(dual_task_entries_kernel, dim3((unsigned)((n_tasks * task_cap + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), plug_ent, plug_n, task_plug, n_tasks, task_cap, out);
+  PP_LAUNCH_CHECK();
+  return PP_OK;
+}
+
+extern "C" int pp_dual_rows(const pp_dual_proj* proj, const int64_t* task_plug, int64_t task_cap,
+                            int plug_windows, int code_layout,
                             const void* scales, int64_t n_groups, int64_t group_size, int64_t chunk_size,
                             const void* scale_tab, int64_t n_tab, const float* amp_lut, const float* cos_lut,
                             const float* sin_lut, const uint32_t* plug_idx, const void* plug_amp,
@@ -1193,7 +1240,8 @@ extern "C" int pp_dual_rows(const pp_dual_proj* proj, const int64_t* task_plug, 
              "a Linear's codes, activations and outputs must each stay below 2 GiB");
   PP_REQUIRE(plug_windows == 1 || plug_windows == 2, "plug_windows must be 1 or 2");
   PP_REQUIRE(code_layout == PP_DUAL_I16_OFFSET || code_layout == PP_DUAL_U16_BE, "bad code_layout");
-  PP_REQUIRE(amp_lut && cos_lut && sin_lut && task_plug, "lut pointers or task_plug are null");
+  PP_REQUIRE(amp_lut && cos_lut && sin_lut && (task_plug || task_cap > 0), "lut pointers or task_plug are null");
+  PP_REQUIRE(task_cap >= 0, "task_cap must be 0 (plug ranges in task_plug) or the records per task");
   PP_REQUIRE(scales != nullptr && n_groups >= 1 && 2 * n_groups < (1ll << 31), "bad scales / n_groups");
   PP_REQUIRE(group_size >= 8 && (group_size & (group_size - 1)) == 0,
              "the dual row decode needs a power-of-two group_size >= 8");
@@ -1227,6 +1275,11 @@ extern "C" int pp_dual_rows(const pp_dual_proj* proj, const int64_t* task_plug, 
   A.plug_n = plug_n;
   A.task_plug = task_plug;
   A.n_tasks = p.n_tasks;
+  if (task_cap > 0) {
+    PP_REQUIRE(p.n_tasks * task_cap < (1ll << 28), "n_tasks * task_cap must stay below 2^28");
+    A.task_cap = task_cap;
+    A.plug_n = plug_n > 0 ? p.n_tasks * task_cap : 0;
+  }
   A.M = (int)M;
   A.proj = P;
   A.parts = p.parts;

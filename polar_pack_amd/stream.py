@@ -618,6 +618,22 @@ class DualStream:
                                       self.rows_per_item, self.plug_ent.data_ptr(),
                                       nat.raw_stream(dev))
             nat.check(rc, "pp_dual_plug_table")
+        # one-Linear launch: each task's records in a block of the same size (the largest
+        # task's count; pp_dual_task_entries), so that a wave loads its records without first
+        # loading their range.  Kept while the blocks hold at most 4x the records (or 64K);
+        # a projection without entries passes none (task_cap 1, every window empty).
+        self.task_cap, self.task_ent = 0, None
+        if self.direct:
+            cnt = self.task_plug_np[:, 1] - self.task_plug_np[:, 0]
+            cap = int(cnt.max()) if cnt.size else 0
+            if cap == 0:
+                self.task_cap = 1
+            elif self.n_tasks * cap <= max(4 * P, 1 << 16):
+                self.task_ent = torch.empty(2 * self.n_tasks * cap, dtype=torch.int32, device=dev)
+                rc = L.pp_dual_task_entries(self.plug_ent.data_ptr(), P, self.task_plug.data_ptr(), self.n_tasks, cap,
+                                            self.task_ent.data_ptr(), nat.raw_stream(dev))
+                nat.check(rc, "pp_dual_task_entries")
+                self.task_cap = cap
         gs, R = pack.group_size, self.rows_per_item
         fits = (pack.chunk_size % gs == 0 and len(self.shapes) > 0
                 and all(k % gs == 0 and n % R == 0 and int(p) % (R * gs) == 0
@@ -691,13 +707,17 @@ class DualStream:
         pk = self.pack
         amp, cos, sin = self.luts
         P = int(pk.plug_idx.numel())
-        rc = nat.lib().pp_dual_rows(C.byref(self._proj), self.task_plug.data_ptr(), self.plug_windows,
+        if self.task_cap > 0:
+            ent, P = (self.task_ent, P) if self.task_ent is not None else (None, 0)
+        else:
+            ent = self.plug_ent
+        rc = nat.lib().pp_dual_rows(C.byref(self._proj), self.task_plug.data_ptr(), self.task_cap, self.plug_windows,
                                     self.code_layout, pk.scales.data_ptr(), int(pk.scales.numel()), pk.group_size,
                                     pk.chunk_size, self.scale_tab.data_ptr() if self.scale_tab is not None else None,
                                     int(self.scale_tab.numel()) if self.scale_tab is not None else 0,
                                     amp.data_ptr(), cos.data_ptr(), sin.data_ptr(),
                                     pk.plug_idx.data_ptr() if P else None, pk.plug_val.data_ptr() if P else None,
-                                    self.plug_ent.data_ptr() if P else None, P, self.M,
+                                    ent.data_ptr() if P else None, P, self.M,
                                     self.workspace.data_ptr() if self.workspace is not None else None,
                                     self._ws_bytes, nat.raw_stream(self.device))
         nat.check(rc, "pp_dual_rows")

@@ -233,6 +233,50 @@ def test_single_linear_split_k(shape, M, one_linear):
             assert int(torch.count_nonzero(st.workspace)) == 0
 
 
+@pytest.mark.parametrize("shape,cap", [((256, 2048), 0.01), ((512, 2048), 0.001), ((64, 11008), 0.05),
+                                       ((1000, 1000), 0.0)])
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_single_linear_task_records(shape, cap, M):
+    """The one-Linear launch reading each task's plug records from a block of its own
+    (pp_dual_task_entries: the task's records in order, null records after them) and from the
+    records' ranges (task_cap 0): equal to the oracle, and to each other bit for bit where no
+    column slices meet through atomics."""
+    N, K = shape
+    w1, w2 = gen.correlated_models(41, [N * K, N * K], delta_growth=False)
+    dp = odp.pack_dual(w1, w2, odp.DualConfig(plug_cap=cap, chunk_size=50_000_000))
+    pack = device_pack(dp, "u16be")
+    st = DualStream(pack, [shape], M=M)
+    assert st.direct and st.task_cap >= 1
+    P = dp.plug_idx.size
+    cnt = st.task_plug_np[:, 1] - st.task_plug_np[:, 0]
+    if P:
+        assert st.task_cap == cnt.max()
+        blk = st.task_ent.cpu().numpy().view(np.uint32).reshape(st.n_tasks, st.task_cap, 2)
+        ent = st.plug_ent.cpu().numpy().view(np.uint32).reshape(-1, 2)
+        for t in range(st.n_tasks):
+            lo, hi = st.task_plug_np[t]
+            np.testing.assert_array_equal(blk[t, :hi - lo], ent[lo:hi])
+            assert np.all(blk[t, hi - lo:, 0] == 0x7FFFF) and np.all(blk[t, hi - lo:, 1] == 0)
+    else:
+        assert st.task_ent is None
+    x_np = np.random.default_rng(43).standard_normal((M, K)).astype(np.float16)
+    outs = [[torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV) for _ in range(2)]]
+    st.bind([torch.from_numpy(x_np).to(DEV)], outs)
+    w = odp.decode_pairs_f64(dp, 0, N * K)
+    got = {}
+    for mode, tc in (("blocks", st.task_cap), ("ranges", 0)):
+        st.task_cap = tc
+        st()
+        torch.cuda.synchronize()
+        got[mode] = [o.float().cpu().numpy() for o in outs[0]]
+        for m in range(2):
+            ref = x_np.astype(np.float64) @ w[m].reshape(N, K).T
+            assert_gemv_close(got[mode][m], ref, f"{mode} model {m}")
+    if st.workspace is None:
+        for m in range(2):
+            np.testing.assert_array_equal(got["blocks"][m], got["ranges"][m])
+
+
 @pytest.mark.parametrize("layout", ["u16be", "i16"])
 @pytest.mark.parametrize("chunk", [50_000_000, 1000])
 def test_plug_records(layout, chunk):
