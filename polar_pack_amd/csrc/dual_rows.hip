@@ -599,6 +599,28 @@ struct DualRunner {
 #pragma unroll
     for (int b = 0; b < NPRE; ++b) prefetch(cb[b]);
   }
+  // A wave of one task and one chunk (the usual one-Linear shape) in straight-line code:
+  // the activations of its corrections are requested, the chunk decoded while they are in
+  // flight (its codes arrived before the table barrier), then the corrections applied;
+  // entries past the first window are taken when the task finishes.
+  __device__ __forceinline__ void run_started_single(const DChunk<MT, RG>& c) {
+    dwin_data<MT, RG, PW, SM>(A, S, s0, I, lane, D);
+    dchunk_compute<MT, RG, LAYOUT, SM>(lds, lo, c, acc);
+    // unconditional (an empty window adds zeros), so that the activation loads are not
+    // moved into a branch after the decode
+    dwin_apply<MT, RG, PW>(lds, lo, D, acc);
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int j = 0; j < MT; ++j) pend[r][m][j] = acc[r][m][j];
+    pend_ti = 0;
+    pend_left = s0;
+    pend_left.lo += 64 * PW;
+    pend_left.rem = s0.rem > 64 * PW ? s0.rem - 64 * PW : 0;
+    finish_pending();
+  }
   __device__ __forceinline__ void run_started_one(DChunk<MT, RG> (&cb)[3]) {
     dwin_data<MT, RG, PW, SM>(A, S, s0, I, lane, D);
     dwin_positions<PW>(A, s1, lane, I);
@@ -724,17 +746,18 @@ __global__ __launch_bounds__(DualCfg<MT>::NT) void dual_stream_kernel(const Dual
 // PARTS: 0 whole rows; 1 K parts meeting through the workspace; 2 a task's parts are
 // consecutive waves of one workgroup (wg_item), each parks its reduced sums in LDS and, after a
 // barrier every wave of the workgroup reaches, the part-0 wave adds them and writes the outputs
-// (no workspace, no atomics).
+// (no workspace, no atomics); 3 as 2 with one chunk per part (parts == chunks), run in
+// straight-line code (run_started_single).
 template <int MT, int PW, int LAYOUT, int SM, int PARTS>
 __global__ __launch_bounds__(DualCfg<MT>::NT) void dual_direct_kernel(const DualStreamArgs A) {
   constexpr int RG = DualCfg<MT>::RG, NT = DualCfg<MT>::NT, WAVES = NT / 64;
   constexpr bool SPLIT = PARTS != 0;
-  __shared__ __attribute__((aligned(16))) uint32_t Tb[(DLDS_BYTES + (PARTS == 2 ? 256 * WAVES : 0)) / 4];
+  __shared__ __attribute__((aligned(16))) uint32_t Tb[(DLDS_BYTES + (PARTS >= 2 ? 256 * WAVES : 0)) / 4];
   char* lds = reinterpret_cast<char*>(Tb);
   const int wave = uniform(threadIdx.x >> 6);
   const int64_t gw = (int64_t)blockIdx.x * WAVES + wave;
   const int K = uniform(A.proj.K), N = uniform(A.proj.N);
-  constexpr bool wg = PARTS == 2;
+  constexpr bool wg = PARTS >= 2;
   const uint32_t parts = (uint32_t)uniform(A.parts);
   const DirectItem d = wg ? wg_item<WAVES>(blockIdx.x, gridDim.x, (uint32_t)wave, (uint32_t)uniform64(A.n_tasks), parts,
                                            (uint32_t)uniform(A.n_chunks), DPAIRS, (uint32_t)K)
@@ -771,7 +794,8 @@ __global__ __launch_bounds__(DualCfg<MT>::NT) void dual_direct_kernel(const Dual
     else R.run_started_two(cb);
   } else {
     if (busy) {
-      if constexpr (MT == 1) R.run_started_one(cb);
+      if constexpr (PARTS == 3) R.run_started_single(cb[0]);
+      else if constexpr (MT == 1) R.run_started_one(cb);
       else R.run_started_two(cb);
     }
     __syncthreads();   // every wave of the workgroup: the parked sums are in LDS
@@ -1072,7 +1096,10 @@ static int launch_dual_stream(const DualStreamArgs& A, int pw, hipStream_t st) {
 template <int MT, int LAYOUT, int SM>
 static int launch_dual_direct(const DualStreamArgs& A, int pw, hipStream_t st) {
   const dim3 grid((unsigned)device_cu_count()), block(DualCfg<MT>::NT);
-  if (A.parts > 1 && A.wg_parts) {
+  if (MT == 1 && A.parts > 1 && A.wg_parts && A.parts == A.n_chunks) {
+    if (pw == 1) hipLaunchKernelGGL((dual_direct_kernel<MT, 1, LAYOUT, SM, 3>), grid, block, 0, st, A);
+    else hipLaunchKernelGGL((dual_direct_kernel<MT, 2, LAYOUT, SM, 3>), grid, block, 0, st, A);
+  } else if (A.parts > 1 && A.wg_parts) {
     if (pw == 1) hipLaunchKernelGGL((dual_direct_kernel<MT, 1, LAYOUT, SM, 2>), grid, block, 0, st, A);
     else hipLaunchKernelGGL((dual_direct_kernel<MT, 2, LAYOUT, SM, 2>), grid, block, 0, st, A);
   } else if (A.parts > 1) {
