@@ -133,25 +133,28 @@ struct Chunk {
 // codes resource = rows [row, nrows) from column kc, num_records ends at column K of
 // the segment's last row, so rows past the segment and columns past K of the last row
 // read 0; columns past K of other rows read the next row's codes, which meet a zero x.
+// live = false: the same instructions, every load reading nothing (a buffer filled past the
+// wave's last chunk; kc must still name a chunk of the segment).
 template <int MT, int RG, int NSEG>
 __device__ __forceinline__ void chunk_issue(const SegCtx& S, int row, int kc, const uint32_t (&voff)[RG], int lane,
-                                            Chunk<MT, RG, NSEG>& c) {
+                                            Chunk<MT, RG, NSEG>& c, bool live = true) {
   const int64_t first = (int64_t)row * S.ldc + kc;
   const int64_t end = (int64_t)(S.nrows - 1) * S.ldc + S.K;   // one past the last code
-  const rsrc_t rc = make_rsrc(S.codes + first, 4u * (uint32_t)(end - first));
+  // not live: empty resources (a scalar choice, no per-lane offsets to select)
+  const rsrc_t rc = make_rsrc(S.codes + first, live ? 4u * (uint32_t)(end - first) : 0u);
 #pragma unroll
   for (int r = 0; r < RG; ++r)
 #pragma unroll
     for (int s = 0; s < NSEG; ++s) vload128(c.q[r][s], voff[r] + 1024u * s, rc);
   if constexpr (MT == 1) {
-    const rsrc_t rx = make_rsrc(S.x + kc, 2u * (uint32_t)(S.kend - kc));   // past kend: reads 0
+    const rsrc_t rx = make_rsrc(S.x + kc, live ? 2u * (uint32_t)(S.kend - kc) : 0u);   // past kend: reads 0
 #pragma unroll
     for (int s = 0; s < NSEG; ++s) vload64(c.xr[0][s], 8u * lane + 512u * s, rx);
   } else {
 #pragma unroll
     for (int s = 0; s < NSEG; ++s) {
       const int k = kc + s * QSEG + 4 * lane;
-      const bool valid = k < S.kend;
+      const bool valid = live && k < S.kend;
 #pragma unroll
       for (int j = 0; j < MT; ++j) vload64(c.xr[j][s], valid ? 2u * (uint32_t)(j * S.x_sm + k) : OOB, S.rx);
     }
@@ -585,6 +588,42 @@ struct SegRunner {
     finish_pending();
   }
 
+  // Chunk ck of the wave's only task into c (past the last chunk: the last chunk's
+  // addresses, nothing read).
+  __device__ __forceinline__ void issue_one(Chunk<MT, RG, NSEG>& c, int ck) const {
+    chunk_issue<MT, RG, NSEG>(S, 0, S.kbeg + min(ck, nck - 1) * CHUNK, voff, lane, c, ck < nck);
+  }
+
+  // A wave with one task (one-Linear launches with no more tasks per column slice than
+  // waves): the caller issued chunks 0 and 1 into c0, c1 and the plug positions (idx)
+  // before the table build; three buffers deep, so two chunks are in flight while one is
+  // decoded (no pending task, whose sums would take the third buffer's registers).
+  __device__ __forceinline__ void run_one(Chunk<MT, RG, NSEG>& c0, Chunk<MT, RG, NSEG>& c1, uint32_t idx) {
+    Chunk<MT, RG, NSEG> c2;
+    P.idx = idx;
+    plug_begin<MT, RG>(A, S, 0, lane, pc, P);
+    int ck = 0;
+    for (;;) {
+      issue_one(c2, ck + 2);
+      chunk_compute<MT, RG, NSEG, L>(lds, lo, c0, acc);
+      if (++ck >= nck) break;
+      issue_one(c0, ck + 2);
+      chunk_compute<MT, RG, NSEG, L>(lds, lo, c1, acc);
+      if (++ck >= nck) break;
+      issue_one(c1, ck + 2);
+      chunk_compute<MT, RG, NSEG, L>(lds, lo, c2, acc);
+      if (++ck >= nck) break;
+    }
+    plug_end<MT, RG, L>(lds, lo, A, S, 0, lane, pc, P, acc);
+    if constexpr (SPLIT) {
+      if (S.park) parked = task_reduce<MT, RG>(A, S, 0, lane, acc).y;
+      else if (S.parts > 1) task_accumulate<MT, RG>(A, S, 0, lane, acc);
+      else task_write<MT, RG>(A, S, 0, lane, acc);
+    } else {
+      task_write<MT, RG>(A, S, 0, lane, acc);
+    }
+  }
+
   // The same walk when the caller has already issued the first chunk into c0 (with this
   // runner's lane offsets): the first task's plug positions are requested, then the loop.
   __device__ __forceinline__ void run_issued(Chunk<MT, RG, NSEG>& c0) {
@@ -665,7 +704,9 @@ __device__ __forceinline__ void rows_body(const char* lds, const QuadRowsArgs& A
 // consecutive waves of one workgroup (wg_item): each keeps its reduced sums, and after every
 // wave of the workgroup is done with the tables (a barrier) they go into the table memory,
 // where after a second barrier the slice-0 wave adds them and writes the outputs.
-template <int MT, typename E, int PARTS>
+// ONE: every wave has at most one task (SegRunner::run_one): its first two chunks and its
+// plug positions are requested before the build.
+template <int MT, typename E, int PARTS, bool ONE>
 __device__ __forceinline__ void direct_body(uint32_t* T, const QuadRowsArgs& A, int64_t gw) {
   constexpr int RG = RowsCfg<MT>::RG, NSEG = RowsCfg<MT>::NSEG, NT = RowsCfg<MT>::NT, WAVES = NT / 64;
   constexpr bool SPLIT = PARTS != 0, WG = PARTS == 2;
@@ -699,24 +740,32 @@ __device__ __forceinline__ void direct_body(uint32_t* T, const QuadRowsArgs& A, 
   uint32_t voff[RG];
 #pragma unroll
   for (int r = 0; r < RG; ++r) voff[r] = 4u * (uint32_t)(r * S.ldc) + 16u * lane;
-  Chunk<MT, RG, NSEG> c0;
+  Chunk<MT, RG, NSEG> c0, c1;
   if (busy) chunk_issue<MT, RG, NSEG>(S, 0, S.kbeg, voff, lane, c0);   // 1 us faster than after the build
-  const bool shared = tb.finish(T, A.luts);
-  if (!WG && !busy) return;
+  if (ONE && busy) {
+    const int k1 = S.kbeg + NSEG * QSEG;
+    chunk_issue<MT, RG, NSEG>(S, 0, k1 < S.kend ? k1 : S.kbeg, voff, lane, c1, k1 < S.kend);
+  }
   // the caller's plan, kept inside the table whatever it holds (a stale plan must not send
   // the plug loads outside it)
   const int64_t pc = std::min<int64_t>(std::max<int64_t>(uniform64((int64_t)(((uint64_t)wp[1] << 32) | wp[0])), 0),
                                        A.plug_n);
+  uint32_t idx0 = 0;
+  if (ONE && busy) vload32(idx0, 4u * lane, plug_idx_rsrc(A, pc));
+  const bool shared = tb.finish(T, A.luts);
+  if (!WG && !busy) return;
   const char* lds = reinterpret_cast<const char*>(T);
   float y = 0.f;
   if (busy) {
     if (shared) {
       SegRunner<MT, RG, NSEG, LayShared, SPLIT> R(lds, A, S, pc);
-      R.run_issued(c0);
+      if constexpr (ONE) R.run_one(c0, c1, idx0);
+      else R.run_issued(c0);
       y = R.parked;
     } else {
       SegRunner<MT, RG, NSEG, LaySplit, SPLIT> R(lds, A, S, pc);
-      R.run_issued(c0);
+      if constexpr (ONE) R.run_one(c0, c1, idx0);
+      else R.run_issued(c0);
       y = R.parked;
     }
   }
@@ -749,12 +798,12 @@ __global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_rows_kernel(const QuadRo
 
 // One Linear (segs == nullptr): a kernel of its own, so that the whole-stream kernel keeps
 // its register allocation.  PARTS as direct_body.
-template <int MT, int PARTS>
+template <int MT, int PARTS, bool ONE = false>
 __global__ __launch_bounds__(RowsCfg<MT>::NT) void quad_direct_kernel(const QuadRowsArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t T[QLDS_BYTES / 4];
   const int64_t gw = (int64_t)blockIdx.x * (RowsCfg<MT>::NT / 64) + uniform(threadIdx.x >> 6);
-  if (A.luts.dtype == PP_F16) direct_body<MT, f16, PARTS>(T, A, gw);
-  else direct_body<MT, float, PARTS>(T, A, gw);
+  if (A.luts.dtype == PP_F16) direct_body<MT, f16, PARTS, ONE>(T, A, gw);
+  else direct_body<MT, float, PARTS, ONE>(T, A, gw);
 }
 
 // ------------------------------------------------------------------ tail rows
@@ -898,8 +947,15 @@ static int cfg_waves(int mt) {
 template <int PARTS>
 static void launch_direct_t(const QuadRowsArgs& A, int mt, hipStream_t st) {
   const unsigned grid = (unsigned)device_cu_count();
+  // at most one task per wave: a task per column slice per wave at most (direct_item deals
+  // each slice's tasks over its >= W / parts waves; wg_item gives a wave one task)
+  const int64_t W = (int64_t)grid * (RowsCfg<1>::NT / 64);
+  const bool one = PARTS == 2 || A.n_tasks <= W / std::max(1, A.parts);
   switch (mt) {
-    case 1: hipLaunchKernelGGL((quad_direct_kernel<1, PARTS>), dim3(grid), dim3(RowsCfg<1>::NT), 0, st, A); break;
+    case 1:
+      if (one) hipLaunchKernelGGL((quad_direct_kernel<1, PARTS, true>), dim3(grid), dim3(RowsCfg<1>::NT), 0, st, A);
+      else hipLaunchKernelGGL((quad_direct_kernel<1, PARTS>), dim3(grid), dim3(RowsCfg<1>::NT), 0, st, A);
+      break;
     case 2: hipLaunchKernelGGL((quad_direct_kernel<2, PARTS>), dim3(grid), dim3(RowsCfg<2>::NT), 0, st, A); break;
     case 4: hipLaunchKernelGGL((quad_direct_kernel<4, PARTS>), dim3(grid), dim3(RowsCfg<4>::NT), 0, st, A); break;
     default: hipLaunchKernelGGL((quad_direct_kernel<8, PARTS>), dim3(grid), dim3(RowsCfg<8>::NT), 0, st, A); break;
@@ -965,6 +1021,18 @@ struct DirectPlan {
   bool wg;                 // the slices meet in LDS (no workspace)
   int64_t n_tasks, waves, cnt_bytes, split_bytes;
 };
+// Slices of a Linear with at least 4 waves per task: as many as fill the waves, a power of
+// two up to a workgroup's waves so that they meet in LDS (down 2048x11008 at one token:
+// 8 slices of 1,376 columns, 26.4 us, against 4 slices, 28.3); otherwise direct_parts.
+static int quad_direct_parts(int64_t T, int64_t W, int64_t C, int waves_per_wg) {
+  if (T > 0 && W >= 4 * T) {
+    int p = 1;
+    while (2 * p <= waves_per_wg && 2 * p * T <= W && 2 * p <= C) p *= 2;
+    if (p > 1) return p;
+  }
+  return direct_parts(T, W, C);
+}
+
 static DirectPlan direct_plan(int64_t M, int64_t N, int64_t K, bool split) {
   DirectPlan p;
   p.mt = round_mt(M);
@@ -973,7 +1041,7 @@ static DirectPlan direct_plan(int64_t M, int64_t N, int64_t K, bool split) {
   p.waves = (int64_t)device_cu_count() * cfg_waves(p.mt);
   p.n_tasks = (N + p.rg - 1) / p.rg;
   p.n_chunks = (int)std::max<int64_t>(1, (K + p.chunk - 1) / p.chunk);
-  p.parts = split ? direct_parts(p.n_tasks, p.waves, p.n_chunks) : 1;
+  p.parts = split ? quad_direct_parts(p.n_tasks, p.waves, p.n_chunks, cfg_waves(p.mt)) : 1;
   p.wg = wg_parts_ok(p.n_tasks, p.waves, p.parts, cfg_waves(p.mt));
   p.cnt_bytes = p.parts > 1 && !p.wg ? (p.n_tasks * 4 + 255) / 256 * 256 : 0;
   p.split_bytes = p.parts > 1 && !p.wg ? p.cnt_bytes + 4 * 4 * M * N : 0;
