@@ -131,9 +131,13 @@ struct QuadTableBuild {
     for (int i = 0; i < 4; ++i) v[i] = lut_val<E>(luts, 1 + i, e);
     U.template load<E>(luts);
   }
-  __device__ __forceinline__ bool finish(uint32_t* T, const QuadLuts& luts) {
+  // Whether this thread's q1 and q2 entries agree (waits for the first LUT loads only).
+  __device__ __forceinline__ bool same() const {
+    return __float_as_uint(v[0]) == __float_as_uint(v[2]) && __float_as_uint(v[1]) == __float_as_uint(v[3]);
+  }
+  __device__ __forceinline__ bool finish(uint32_t* T, const QuadLuts& luts) { return finish(T, luts, same()); }
+  __device__ __forceinline__ bool finish(uint32_t* T, const QuadLuts& luts, bool same) {
     char* lds = reinterpret_cast<char*>(T);
-    const bool same = __float_as_uint(v[0]) == __float_as_uint(v[2]) && __float_as_uint(v[1]) == __float_as_uint(v[3]);
     // workgroup-wide AND through the (not yet built) table memory: the tables fill all
     // of LDS, so there is no room for a separate flag
     if (threadIdx.x == 0) T[0] = 0u;

@@ -602,17 +602,21 @@ struct SegRunner {
     Chunk<MT, RG, NSEG> c2;
     P.idx = idx;
     plug_begin<MT, RG>(A, S, 0, lane, pc, P);
+    // whole rounds of three chunks with no exit between them (an exit inside the round
+    // makes the compiler wait for both chunks in flight at the round's first decode), then
+    // the 0-2 chunks left, already in c0 and c1
     int ck = 0;
-    for (;;) {
+    for (; ck + 3 <= nck; ck += 3) {
       issue_one(c2, ck + 2);
       chunk_compute<MT, RG, NSEG, L>(lds, lo, c0, acc);
-      if (++ck >= nck) break;
-      issue_one(c0, ck + 2);
+      issue_one(c0, ck + 3);
       chunk_compute<MT, RG, NSEG, L>(lds, lo, c1, acc);
-      if (++ck >= nck) break;
-      issue_one(c1, ck + 2);
+      issue_one(c1, ck + 4);
       chunk_compute<MT, RG, NSEG, L>(lds, lo, c2, acc);
-      if (++ck >= nck) break;
+    }
+    if (ck < nck) {
+      chunk_compute<MT, RG, NSEG, L>(lds, lo, c0, acc);
+      if (ck + 1 < nck) chunk_compute<MT, RG, NSEG, L>(lds, lo, c1, acc);
     }
     plug_end<MT, RG, L>(lds, lo, A, S, 0, lane, pc, P, acc);
     if constexpr (SPLIT) {
@@ -742,17 +746,20 @@ __device__ __forceinline__ void direct_body(uint32_t* T, const QuadRowsArgs& A, 
   for (int r = 0; r < RG; ++r) voff[r] = 4u * (uint32_t)(r * S.ldc) + 16u * lane;
   Chunk<MT, RG, NSEG> c0, c1;
   if (busy) chunk_issue<MT, RG, NSEG>(S, 0, S.kbeg, voff, lane, c0);   // 1 us faster than after the build
-  if (ONE && busy) {
-    const int k1 = S.kbeg + NSEG * QSEG;
-    chunk_issue<MT, RG, NSEG>(S, 0, k1 < S.kend ? k1 : S.kbeg, voff, lane, c1, k1 < S.kend);
-  }
   // the caller's plan, kept inside the table whatever it holds (a stale plan must not send
   // the plug loads outside it)
   const int64_t pc = std::min<int64_t>(std::max<int64_t>(uniform64((int64_t)(((uint64_t)wp[1] << 32) | wp[0])), 0),
                                        A.plug_n);
   uint32_t idx0 = 0;
   if (ONE && busy) vload32(idx0, 4u * lane, plug_idx_rsrc(A, pc));
-  const bool shared = tb.finish(T, A.luts);
+  const bool same = tb.same();
+  if (ONE && busy) {
+    // the second chunk once the first LUT values are back (issued with the first, gate
+    // 11008x2048 built its tables 4.9 us after entry; 4.7 this way, both 25.1-26.2 us)
+    const int k1 = S.kbeg + NSEG * QSEG;
+    chunk_issue<MT, RG, NSEG>(S, 0, k1 < S.kend ? k1 : S.kbeg, voff, lane, c1, k1 < S.kend);
+  }
+  const bool shared = tb.finish(T, A.luts, same);
   if (!WG && !busy) return;
   const char* lds = reinterpret_cast<const char*>(T);
   float y = 0.f;
