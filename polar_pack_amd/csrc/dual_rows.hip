@@ -542,20 +542,21 @@ struct DualRunner {
     pend_ti = -1;
   }
 
-  // prefetch | range of step s+2, range load for s+3 | [first chunk] finish the previous
-  // task | decode | corrections of step s | data loads for s+1 | positions for s+2 | [last
-  // chunk] park the sums.  The corrections follow the decode, so that a wave with a single
-  // step decodes while its entries' activations are in flight.
-  __device__ __forceinline__ bool step(Cursor& cur, DChunk<MT, RG>& comp, DChunk<MT, RG>& pref) {
-    prefetch(pref);
+  // range of step s+2, range load for s+3 | corrections of step s | data loads for s+1 |
+  // positions for s+2 | [first chunk] finish the previous task | prefetch | decode | [last
+  // chunk] park the sums.  The prefetch is the step's last load: every load the next step
+  // waits for (range, data, positions) was issued before it, so with three buffers the
+  // chunk it requests is first waited for two steps later (the buffer counter is in order).
+  __device__ __forceinline__ void step(Cursor& cur, DChunk<MT, RG>& comp, DChunk<MT, RG>& pref) {
     s2 = slot_of(c3, T);
     advance_slot(c3);
     load_range(c3, T);
-    if (cur.ck == 0 && pend_ti >= 0) finish_pending();
-    dchunk_compute<MT, RG, LAYOUT, SM>(lds, lo, comp, acc);
     if (dslot_cnt<PW>(s0) > 0) dwin_apply<MT, RG, PW>(lds, lo, D, acc);
     dwin_data<MT, RG, PW, SM>(A, S, s1, I, lane, D);
     dwin_positions<PW>(A, s2, lane, I);
+    if (cur.ck == 0 && pend_ti >= 0) finish_pending();
+    prefetch(pref);
+    dchunk_compute<MT, RG, LAYOUT, SM>(lds, lo, comp, acc);
     if (cur.ck == nck - 1) {
 #pragma unroll
       for (int r = 0; r < RG; ++r)
@@ -572,7 +573,32 @@ struct DualRunner {
     s0 = s1;
     s1 = s2;
     advance(cur);
-    return cur.ti < ntask;
+  }
+
+  // The walk's ntask * nck steps over NB rotating buffers (cb[0 .. NB-2] already issued):
+  // whole rounds of NB steps with no exit inside a round (an exit inside makes the
+  // compiler's count of loads in flight at the round's first decode conservative, so it
+  // waits for the chunks the round has in flight), then the steps left.
+  template <int NB>
+  __device__ __forceinline__ void walk(DChunk<MT, RG> (&cb)[NB]) {
+    const int n = ntask * nck;
+    Cursor cur = {0, 0};
+    int i = 0;
+    if constexpr (NB == 3) {
+      for (; i + 3 <= n; i += 3) {
+        step(cur, cb[0], cb[2]);
+        step(cur, cb[1], cb[0]);
+        step(cur, cb[2], cb[1]);
+      }
+      if (i < n) step(cur, cb[0], cb[2]);
+      if (i + 1 < n) step(cur, cb[1], cb[0]);
+    } else {
+      for (; i + 2 <= n; i += 2) {
+        step(cur, cb[0], cb[1]);
+        step(cur, cb[1], cb[0]);
+      }
+      if (i < n) step(cur, cb[0], cb[1]);
+    }
   }
 
   // One-Linear launch, in three parts around the table build: start_ranges() requests the
@@ -624,22 +650,13 @@ struct DualRunner {
   __device__ __forceinline__ void run_started_one(DChunk<MT, RG> (&cb)[3]) {
     dwin_data<MT, RG, PW, SM>(A, S, s0, I, lane, D);
     dwin_positions<PW>(A, s1, lane, I);
-    Cursor cur = {0, 0};
-    for (;;) {
-      if (!step(cur, cb[0], cb[2])) break;
-      if (!step(cur, cb[1], cb[0])) break;
-      if (!step(cur, cb[2], cb[1])) break;
-    }
+    walk<3>(cb);
     finish_pending();
   }
   __device__ __forceinline__ void run_started_two(DChunk<MT, RG> (&cb)[2]) {
     dwin_data<MT, RG, PW, SM>(A, S, s0, I, lane, D);
     dwin_positions<PW>(A, s1, lane, I);
-    Cursor cur = {0, 0};
-    for (;;) {
-      if (!step(cur, cb[0], cb[1])) break;
-      if (!step(cur, cb[1], cb[0])) break;
-    }
+    walk<2>(cb);
     finish_pending();
   }
 
@@ -659,25 +676,17 @@ struct DualRunner {
     advance_slot(c3);
     load_range(c3, T);
     // c3 now names step 2; step() turns T into s2 and moves c3 to step 3
-    Cursor cur = {0, 0};
     if constexpr (MT == 1) {
       // one token: two chunks in flight while one is decoded (measured 1-2 % faster on
       // the 3B stream than one; the registers of more tokens leave room for one)
-      DChunk<MT, RG> c0, c1, c2;
-      prefetch(c0);
-      prefetch(c1);
-      for (;;) {
-        if (!step(cur, c0, c2)) break;
-        if (!step(cur, c1, c0)) break;
-        if (!step(cur, c2, c1)) break;
-      }
+      DChunk<MT, RG> cb[3];
+      prefetch(cb[0]);
+      prefetch(cb[1]);
+      walk<3>(cb);
     } else {
-      DChunk<MT, RG> c0, c1;
-      prefetch(c0);
-      for (;;) {
-        if (!step(cur, c0, c1)) break;
-        if (!step(cur, c1, c0)) break;
-      }
+      DChunk<MT, RG> cb[2];
+      prefetch(cb[0]);
+      walk<2>(cb);
     }
     finish_pending();
   }
