@@ -46,21 +46,43 @@ __device__ __forceinline__ void mplug_take(MPlug& P, const uint32_t (&idx)[4], i
 }
 
 // Decode 8 code words into the fp16 A operands of the 4 models (each tuple rounded
-// once, as soon as it is decoded: the fp32 values are not kept).
+// once, as soon as it is decoded: the fp32 values are not kept).  The table reads of a
+// group of GT tuples are issued before the arithmetic of the previous group (scheduling
+// fences keep them there), so a wave has up to 8 GT reads in flight instead of waiting
+// for each tuple's four reads in turn.
+#ifndef PP_MFMA_GT
+#define PP_MFMA_GT 2
+#endif
 template <class L>
 __device__ __forceinline__ void decode8(const char* lds, const LaneOff& lo, const u32x4& c0, const u32x4& c1,
                                         h8 (&a)[4]) {
   const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  constexpr int GT = PP_MFMA_GT, NG = 8 / GT;
+  static_assert(8 % GT == 0, "the group must divide 8 tuples");
+  float r[2][GT];
+  float2 ta[2][GT], tb[2][GT], tc[2][GT];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float r;
-    float2 ta, tb, tc;
-    lookup<L>(lds, cw[e], lo, r, ta, tb, tc);
-    const float rs = r * ta.y, rss = rs * tb.y;
-    a[0][e] = (_Float16)(r * ta.x);
-    a[1][e] = (_Float16)(rs * tb.x);
-    a[2][e] = (_Float16)(rss * tc.x);
-    a[3][e] = (_Float16)(rss * tc.y);
+  for (int u = 0; u < GT; ++u) lookup<L>(lds, cw[u], lo, r[0][u], ta[0][u], tb[0][u], tc[0][u]);
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    if (g + 1 < NG) {
+#pragma unroll
+      for (int u = 0; u < GT; ++u) {
+        const int b = (g + 1) & 1;
+        lookup<L>(lds, cw[(g + 1) * GT + u], lo, r[b][u], ta[b][u], tb[b][u], tc[b][u]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < GT; ++u) {
+      const int b = g & 1, e = g * GT + u;
+      const float rs = r[b][u] * ta[b][u].y, rss = rs * tb[b][u].y;
+      a[0][e] = (_Float16)(r[b][u] * ta[b][u].x);
+      a[1][e] = (_Float16)(rs * tb[b][u].x);
+      a[2][e] = (_Float16)(rss * tc[b][u].x);
+      a[3][e] = (_Float16)(rss * tc[b][u].y);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
