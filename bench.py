@@ -73,6 +73,13 @@ PMC_SUMMARY = {"quad3b": os.path.join(ROOT, "profiles", "quad_stream_3b_pmc.md")
                "dual3b": os.path.join(ROOT, "profiles", "dual_stream_3b_pmc.md"),
                "dual2048": os.path.join(ROOT, "profiles", "dual_linear_2048_direct.md"),
                "quadgate": os.path.join(ROOT, "profiles", "quad_linear_gate_direct.md")}
+# The sources of the kernels each summary measured: a summary's traffic is used only while
+# their digest equals the one it records (kernel_sources_sha256), so a kernel changed after
+# its profile reports traffic null until the profile is taken again.
+_QUAD_ROWS_SRC = ["quad_rows.hip", "quad_rows.h", "quad_lds.h", "rows_common.h", "pp_common.h"]
+_DUAL_ROWS_SRC = ["dual_rows.hip", "dual_lds.h", "rows_common.h", "pp_common.h"]
+PMC_SOURCES = {"quad3b": _QUAD_ROWS_SRC, "quadgate": _QUAD_ROWS_SRC, "dual3b": _DUAL_ROWS_SRC,
+               "dual2048": _DUAL_ROWS_SRC}
 MALL_BYTES = 512 << 20
 
 
@@ -272,14 +279,36 @@ def cpu_baseline_dual(pack, shapes, sample_pairs, xs=None, outs=None):
             "worst_normwise": worst}
 
 
-def read_pmc_traffic(path):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE), if committed."""
+def kernel_sources_sha256(names):
+    """sha256 over the named files of polar_pack_amd/csrc, in the order given."""
+    import hashlib
+    h = hashlib.sha256()
+    for n in names:
+        with open(os.path.join(ROOT, "polar_pack_amd", "csrc", n), "rb") as f:
+            h.update(n.encode() + b"\0" + f.read())
+    return h.hexdigest()
+
+
+def read_pmc_traffic(path, sources=None):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE), if
+    committed and, when ``sources`` names the kernel's files, taken of those sources as they
+    are now (the summary's kernel_sources_sha256); None otherwise."""
     try:
         text = open(path).read()
     except (OSError, TypeError):
         return None
     m = re.search(r"traffic_bytes_per_launch\s*[=:]\s*([0-9.eE+]+)", text)
-    return float(m.group(1)) if m else None
+    if not m:
+        return None
+    if sources is not None:
+        h = re.search(r"kernel_sources_sha256\s*[=:]\s*([0-9a-f]{64})", text)
+        if not h or h.group(1) != kernel_sources_sha256(sources):
+            return None
+    return float(m.group(1))
+
+
+def pmc_traffic(workload):
+    return read_pmc_traffic(PMC_SUMMARY[workload], PMC_SOURCES[workload])
 
 
 def time_events(launch, steps, warmup):
@@ -379,7 +408,7 @@ def run_quad3b(args, dev, log):
           "layers": args.layers, "projections": len(shapes), "models": 4, "batch": 1,
           "tuples": int(pack.n), "plug_entries": int(pack.plug_idx.numel()),
           "algorithmic_bytes": int(algo), "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2)},
-         traffic=read_pmc_traffic(PMC_SUMMARY["quad3b"]), cpu=cpu, traffic_profile=PMC_SUMMARY["quad3b"])
+         traffic=pmc_traffic("quad3b"), cpu=cpu, traffic_profile=PMC_SUMMARY["quad3b"])
 
 
 def run_dual3b(args, dev, log, tails):
@@ -455,7 +484,7 @@ def run_dual3b(args, dev, log, tails):
           "pairs": int(pack.n_codes), "tail_weights": pack.tail_lengths,
           "plug_entries": int(pack.plug_idx.numel()), "algorithmic_bytes": int(algo),
           "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2)},
-         traffic=read_pmc_traffic(PMC_SUMMARY["dual3b"]) if tails else None, cpu=cpu,
+         traffic=pmc_traffic("dual3b") if tails else None, cpu=cpu,
          traffic_profile=PMC_SUMMARY["dual3b"])
 
 
@@ -525,7 +554,7 @@ def run_dual2048(args, dev, log):
          {"workload": "dual-pack Linear 2048x2048, 2 models, batch 1", "N": N, "K": K, "models": 2, "batch": 1,
           "plug_entries": int(pack.plug_idx.numel()), "rotated_copies": copies, "algorithmic_bytes": int(algo),
           "us_per_linear": round(ms * 1e3, 3), "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2)}, cpu=cpu,
-         traffic=read_pmc_traffic(PMC_SUMMARY["dual2048"]), traffic_profile=PMC_SUMMARY["dual2048"])
+         traffic=pmc_traffic("dual2048"), traffic_profile=PMC_SUMMARY["dual2048"])
 
 
 def sanity_dual_single(entry, pack, dev):
@@ -664,7 +693,7 @@ def run_quad_single(args, dev, log, N, K, M, name, pack=None):
           "algorithmic_bytes": int(algo), "us_per_linear": round(ms * 1e3, 3),
           "pct_of_peak": round(100 * achieved / PEAK_HBM_GBS, 2), "tflops": round(tflops, 3),
           "pct_of_fp16_mfma_peak": round(100 * tflops / PEAK_FP16_TFLOPS, 3)}, cpu=cpu,
-         **({"traffic": read_pmc_traffic(PMC_SUMMARY["quadgate"]), "traffic_profile": PMC_SUMMARY["quadgate"]}
+         **({"traffic": pmc_traffic("quadgate"), "traffic_profile": PMC_SUMMARY["quadgate"]}
             if (N, K, M) == (11008, 2048, 1) and args.workload == "quadgate" else {}))
     return pack
 
