@@ -299,6 +299,199 @@ __attribute__((amdgpu_waves_per_eu(QbCfg<TT, KN>::WPE, QbCfg<TT, KN>::WPE))) voi
   }
 }
 
+// ---------------------------------------------------------------- producer/consumer form
+// From PP_QB_PC_MIN tokens: a workgroup of 8 waves takes an item of 32 weight rows x 256
+// tokens x one K slice.  Waves 0-3 decode (producers) and waves 4-7 multiply (consumers),
+// one of each per SIMD, so a SIMD's VALU decode and its matrix products come from two
+// waves and run side by side (the one-wave form issues them in turn).  Per super-step of
+// 64 columns, producer p decodes row tile p % 2 at column half p / 2 (8 code words per
+// lane, as above) into LDS as the MFMA A operands of the 4 models; consumer c multiplies
+// the previous super-step's 2 x 2 x 4 operands with its 4 token tiles of x (tokens
+// 64c .. 64c + 63 of the block).  Each code word is decoded once per 256 tokens.  The
+// tables take the split layout (128 KiB, any LUTs), the two operand buffers the rest.
+#ifndef PP_QB_PC_MIN
+#define PP_QB_PC_MIN 256
+#endif
+constexpr int PC_ROWS = 32, PC_TT = 4, PC_TOK = 256, PC_NT = 512;
+constexpr int PC_G = 4;                                   // code buffers of a producer
+constexpr uint32_t PC_ABUF = 0x20000, PC_ABYTES = 0x4000; // [rt 2][kh 2][m 4][lane 64] x 16 B
+static_assert(PC_ABUF + 2 * PC_ABYTES <= QLDS_BYTES, "the operand buffers must fit beside the tables");
+
+__device__ __forceinline__ uint32_t pc_aoff(int buf, int rt, int kh, int m, int lane) {
+  return PC_ABUF + (uint32_t)buf * PC_ABYTES + (uint32_t)((((rt * 2 + kh) * 4 + m) * 64 + lane) * 16);
+}
+
+// An item's super-steps, rounded up to whole rounds of 4 (the producers' code buffers and
+// the consumers' x buffers rotate with the super-step; super-steps past the slice read
+// zero x, so their products add nothing).
+__device__ __forceinline__ int pc_steps(int kb, int ke) { return ((ke - kb + 63) / 64 + 3) / 4 * 4; }
+
+template <bool KN, bool PLUG>
+__device__ __forceinline__ void pc_producer(char* lds, const QuadBigArgs& A, int p, int n0b, int kb, int ke, int sl) {
+  const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+  const int rt = p & 1, kh = p >> 1;
+  const int n0 = n0b + 16 * rt;
+  const LaneOff lo = LaySplit::lane(lane);
+  const int n = n0 + i;
+  const bool ok = n < A.N;
+  const uint32_t voc = !ok ? OOB : KN ? 4u * (uint32_t)(8 * q * A.ldc + i) : 4u * (uint32_t)(i * A.ldc + 8 * q);
+  // a row tile past N (the second of a 32-row block at the end): resources based on the
+  // last row, every lane out of range (nothing read)
+  const int n0c = min(n0, A.N - 1);
+  const uint32_t* ctile = KN ? A.codes + n0c : A.codes + (int64_t)n0c * A.ldc;
+  MPlug P;
+  int64_t rowpos = 0;
+  uint32_t pidx[4];
+  if constexpr (PLUG) {
+    rowpos = A.ppos0 + (int64_t)n * A.pld;
+    P.next = ok ? A.row_plug[(int64_t)n * A.slices + sl] : 0;
+    P.end = ok ? A.row_plug[(int64_t)n * A.slices + sl + 1] : 0;
+    mplug_issue(A.plug, P, pidx);
+  }
+  const int ns = pc_steps(kb, ke);
+  QbCodes C[PC_G];
+#pragma unroll
+  for (int g = 0; g + 1 < PC_G; ++g) qb_codes<KN>(A, ctile, n0c, kb + 64 * g + 32 * kh, ke, voc, C[g]);
+  if constexpr (PLUG) mplug_take(P, pidx, rowpos);
+  // super-step s: decode C[s % G] into operand buffer s % 2
+  auto decode = [&](const QbCodes& c, int s) {
+    Look8 lk;
+    look8<LaySplit>(lds, lo, c.c[0], c.c[1], lk);
+    h8 a[4];
+    math8(lk, a);
+    const int k0 = kb + 64 * s + 32 * kh;
+    if constexpr (PLUG) mplug_patch(A.plug, P, rowpos, k0 + 8 * q, k0, a);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) *reinterpret_cast<h8*>(lds + pc_aoff(s & 1, rt, kh, m, lane)) = a[m];
+  };
+  // C[k % G] holds super-step k.  Prologue: super-step 0 into operand buffer 0, its code
+  // buffer refilled with super-step G.
+  qb_codes<KN>(A, ctile, n0c, kb + 64 * (PC_G - 1) + 32 * kh, ke, voc, C[PC_G - 1]);
+  decode(C[0], 0);
+  qb_codes<KN>(A, ctile, n0c, kb + 64 * PC_G + 32 * kh, ke, voc, C[0]);
+  __syncthreads();
+  for (int s = 0; s < ns; s += PC_G) {
+#pragma unroll
+    for (int g = 0; g < PC_G; ++g) {
+      // while the consumers multiply super-step s + g (operand buffer (s + g) % 2), decode
+      // d = s + g + 1 into the other buffer and refill its code buffer with d + G
+      const int d = s + g + 1;
+      decode(C[(g + 1) % PC_G], d);
+      qb_codes<KN>(A, ctile, n0c, kb + 64 * (d + PC_G) + 32 * kh, ke, voc, C[(g + 1) % PC_G]);
+      __syncthreads();
+    }
+  }
+}
+
+template <bool KN>
+__device__ __forceinline__ void pc_consumer(const char* lds, const QuadBigArgs& A, int c, int n0b, int j0b, int kb,
+                                            int ke) {
+  const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+  const int j0 = j0b + 16 * PC_TT * c;
+  const f16* xblk = A.x + (int64_t)min(j0, A.M - 1) * A.x_sm;
+  uint32_t vox[PC_TT];
+#pragma unroll
+  for (int t = 0; t < PC_TT; ++t) {
+    const int jl = 16 * t + i;
+    vox[t] = j0 + jl < A.M ? 2u * (uint32_t)(jl * A.x_sm + 8 * q) : OOB;
+  }
+  const int jx = min(j0, A.M - 1);
+  const int ns = pc_steps(kb, ke);
+  f4 Cacc[2][4][PC_TT];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int t = 0; t < PC_TT; ++t) Cacc[rt][m][t] = f4{0.f, 0.f, 0.f, 0.f};
+  QbX<PC_TT> X[2][2];   // [buffer][column half]
+  auto loadx = [&](QbX<PC_TT>(&xb)[2], int s) {
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) qb_x<PC_TT>(A, kb + 64 * s + 32 * kh, ke, vox, xblk, jx, xb[kh]);
+  };
+  auto multiply = [&](const QbX<PC_TT>(&xb)[2], int s) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const h8 a = *reinterpret_cast<const h8*>(lds + pc_aoff(s & 1, rt, kh, m, lane));
+#pragma unroll
+          for (int t = 0; t < PC_TT; ++t)
+            Cacc[rt][m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8, xb[kh].xb[t]),
+                                                                    Cacc[rt][m][t], 0, 0, 0);
+        }
+  };
+  loadx(X[0], 0);
+  __syncthreads();
+  for (int s = 0; s < ns; s += 2) {
+    loadx(X[1], s + 1);
+    multiply(X[0], s);
+    __syncthreads();
+    loadx(X[0], s + 2);
+    multiply(X[1], s + 1);
+    __syncthreads();
+  }
+  // lane holds rows n0b + 16 rt + 4q + r, r = 0..3, of token j0 + 16t + i
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int t = 0; t < PC_TT; ++t) {
+        const int j = j0 + 16 * t + i;
+        const int nn = n0b + 16 * rt + 4 * q;
+        const f4 v = Cacc[rt][m][t] * A.s[m];
+        if (j >= A.M || nn >= A.N) continue;
+        if (A.slices == 1) {
+          f16* o = A.out[m] + (int64_t)j * A.o_sm + nn;
+          if (A.vec_out && nn + 3 < A.N) {
+            const f16x4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+            *reinterpret_cast<f16x4*>(o) = h;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (nn + r < A.N) o[r] = (f16)v[r];
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (nn + r < A.N)
+              __hip_atomic_fetch_add(A.acc + ((int64_t)m * A.N + nn + r) * A.M + j, v[r], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+}
+
+template <bool KN>
+__global__ __launch_bounds__(PC_NT) void quad_big_pc_kernel(const QuadBigArgs A) {
+  __shared__ __attribute__((aligned(16))) uint32_t Tb[QLDS_BYTES / 4];
+  char* lds = reinterpret_cast<char*>(Tb);
+  if (A.luts.dtype == PP_F16) LaySplit::build<PC_NT, f16>(lds, A.luts);
+  else LaySplit::build<PC_NT, float>(lds, A.luts);
+  __syncthreads();
+  const int wave = uniform(threadIdx.x >> 6);
+  int b = blockIdx.x;
+  if (A.xcd_remap) b = (b & 7) * (int)(gridDim.x >> 3) + (b >> 3);
+  // items ordered slice, token block, row block: consecutive workgroups (one XCD after
+  // the remap) share token blocks (x) and slices
+  const int64_t items = (int64_t)A.tiles * A.tblocks * A.slices;
+  for (int64_t it = b; it < items; it += gridDim.x) {
+    const int rb = (int)uniform64(it % A.tiles);
+    const int64_t w = it / A.tiles;
+    const int tb = (int)uniform64(w % A.tblocks), sl = (int)uniform64(w / A.tblocks);
+    const int n0b = rb * PC_ROWS, j0b = tb * PC_TOK;
+    const int kb = sl * A.ks, ke = min(A.K, kb + A.ks);
+    if (wave < 4) {
+      if (A.plug.n > 0) pc_producer<KN, true>(lds, A, wave, n0b, kb, ke, sl);
+      else pc_producer<KN, false>(lds, A, wave, n0b, kb, ke, sl);
+    } else {
+      pc_consumer<KN>(lds, A, wave - 4, n0b, j0b, kb, ke);
+    }
+  }
+}
+
 template <int TT>
 static void qb_launch(bool kn, int64_t grid, hipStream_t st, const QuadBigArgs& A) {
   if (kn) hipLaunchKernelGGL((quad_big_kernel<TT, true>), dim3((unsigned)grid), dim3(QbCfg<TT, true>::NT), 0, st, A);
@@ -346,7 +539,30 @@ static int64_t qb_waves(int tt, bool kn) {
   return tt == 1 ? qb_waves_of<1>(kn) : tt == 2 ? qb_waves_of<2>(kn) : tt == 4 ? qb_waves_of<4>(kn) : qb_waves_of<8>(kn);
 }
 
+// The producer/consumer form: items of 32 rows x 256 tokens; s slices of `per` 32-column
+// steps take ceil(items / CUs) rounds of ceil(per / 2) super-steps (rounded to whole rounds
+// of 4) plus about 4 of fixed cost; the fewest super-step-times win, fewer slices on ties.
+static void pc_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* cols) {
+  const int64_t cus = device_cu_count(), steps = K / 32;
+  const int64_t groups = (N + PC_ROWS - 1) / PC_ROWS * ((M + PC_TOK - 1) / PC_TOK);
+  int64_t best = 1, best_cost = -1;
+  for (int64_t s = 1; s <= std::min<int64_t>(steps, 64); ++s) {
+    const int64_t per = (steps + s - 1) / s;
+    if ((steps + per - 1) / per != s) continue;
+    const int64_t rounds = (groups * s + cus - 1) / cus;
+    const int64_t cost = rounds * (((per + 1) / 2 + 3) / 4 * 4 + 4);
+    if (best_cost < 0 || cost < best_cost) {
+      best = s;
+      best_cost = cost;
+    }
+  }
+  const int64_t per = (steps + best - 1) / best;
+  *cols = 32 * per;
+  *slices = (K + *cols - 1) / *cols;
+}
+
 static void qb_plan(int64_t M, int64_t N, int64_t K, bool kn, int64_t* slices, int64_t* cols) {
+  if (M >= PP_QB_PC_MIN) return pc_plan(M, N, K, slices, cols);
   const int tt = qb_tt(M);
   const int64_t cus = device_cu_count(), wv = qb_waves(tt, kn);
   const int64_t g = tt == 1 ? QbCfg<1, false>::G : tt == 2 ? QbCfg<2, false>::G : tt == 4 ? QbCfg<4, false>::G
@@ -449,17 +665,27 @@ extern "C" int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const
   A.ppos0 = plug_pos0;
   A.pld = plug_ld;
   A.acc = reinterpret_cast<float*>(workspace);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (M >= PP_QB_PC_MIN) {
+    A.tiles = (int)((N + PC_ROWS - 1) / PC_ROWS);
+    A.tblocks = (int)((M + PC_TOK - 1) / PC_TOK);
+    const int64_t items = (int64_t)A.tiles * A.tblocks * slices;
+    const int64_t grid = std::min<int64_t>(device_cu_count(), items);
+    A.xcd_remap = grid % 8 == 0;
+    if (kn) hipLaunchKernelGGL(quad_big_pc_kernel<true>, dim3((unsigned)grid), dim3(PC_NT), 0, st, A);
+    else hipLaunchKernelGGL(quad_big_pc_kernel<false>, dim3((unsigned)grid), dim3(PC_NT), 0, st, A);
+  } else {
   const int64_t wv = qb_waves(tt, kn);
   const int64_t groups = (int64_t)(A.tiles + wv - 1) / wv * A.tblocks * slices;
   const int64_t cus = device_cu_count();
   int64_t grid = std::min<int64_t>(cus, groups);
   A.xcd_remap = grid % 8 == 0;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (tt) {
     case 1: qb_launch<1>(kn, grid, st, A); break;
     case 2: qb_launch<2>(kn, grid, st, A); break;
     case 4: qb_launch<4>(kn, grid, st, A); break;
     default: qb_launch<8>(kn, grid, st, A); break;
+  }
   }
   PP_LAUNCH_CHECK();
   if (slices > 1) {
