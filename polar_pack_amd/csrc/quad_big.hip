@@ -314,8 +314,11 @@ __attribute__((amdgpu_waves_per_eu(QbCfg<TT, KN>::WPE, QbCfg<TT, KN>::WPE))) voi
 #endif
 constexpr int PC_ROWS = 32, PC_TT = 4, PC_TOK = 256, PC_NT = 512;
 constexpr int PC_G = 4;                                   // code buffers of a producer
-constexpr uint32_t PC_ABUF = 0x20000, PC_ABYTES = 0x4000; // [rt 2][kh 2][m 4][lane 64] x 16 B
-static_assert(PC_ABUF + 2 * PC_ABYTES <= QLDS_BYTES, "the operand buffers must fit beside the tables");
+// The operand buffers come first in LDS, so that every operand access is one lane base plus
+// an immediate offset (below 64 KiB); the tables follow.
+constexpr uint32_t PC_ABUF = 0, PC_ABYTES = 0x4000;       // [rt 2][kh 2][m 4][lane 64] x 16 B
+constexpr uint32_t PC_TABLES = 2 * PC_ABYTES;
+static_assert(PC_TABLES + 0x20000 <= QLDS_BYTES, "the split tables must fit after the operand buffers");
 
 __device__ __forceinline__ uint32_t pc_aoff(int buf, int rt, int kh, int m, int lane) {
   return PC_ABUF + (uint32_t)buf * PC_ABYTES + (uint32_t)((((rt * 2 + kh) * 4 + m) * 64 + lane) * 16);
@@ -356,7 +359,7 @@ __device__ __forceinline__ void pc_producer(char* lds, const QuadBigArgs& A, int
   // super-step s: decode C[s % G] into operand buffer s % 2
   auto decode = [&](const QbCodes& c, int s) {
     Look8 lk;
-    look8<LaySplit>(lds, lo, c.c[0], c.c[1], lk);
+    look8<LaySplit>(lds + PC_TABLES, lo, c.c[0], c.c[1], lk);
     h8 a[4];
     math8(lk, a);
     const int k0 = kb + 64 * s + 32 * kh;
@@ -425,11 +428,15 @@ __device__ __forceinline__ void pc_consumer(const char* lds, const QuadBigArgs& 
   };
   loadx(X[0], 0);
   __syncthreads();
+  // The fences keep the next super-step's x loads issued ahead of this one's products, so
+  // the products wait only for their own x.
   for (int s = 0; s < ns; s += 2) {
     loadx(X[1], s + 1);
+    __builtin_amdgcn_sched_barrier(0);
     multiply(X[0], s);
     __syncthreads();
     loadx(X[0], s + 2);
+    __builtin_amdgcn_sched_barrier(0);
     multiply(X[1], s + 1);
     __syncthreads();
   }
@@ -468,8 +475,8 @@ template <bool KN>
 __global__ __launch_bounds__(PC_NT) void quad_big_pc_kernel(const QuadBigArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t Tb[QLDS_BYTES / 4];
   char* lds = reinterpret_cast<char*>(Tb);
-  if (A.luts.dtype == PP_F16) LaySplit::build<PC_NT, f16>(lds, A.luts);
-  else LaySplit::build<PC_NT, float>(lds, A.luts);
+  if (A.luts.dtype == PP_F16) LaySplit::build<PC_NT, f16>(lds + PC_TABLES, A.luts);
+  else LaySplit::build<PC_NT, float>(lds + PC_TABLES, A.luts);
   __syncthreads();
   const int wave = uniform(threadIdx.x >> 6);
   int b = blockIdx.x;
