@@ -302,9 +302,9 @@ int64_t pp_quad_mfma_waves(int64_t M);
  * of the (K,N) storage there and sorts them).  row_plug[n*slices + s] (N*slices + 1
  * entries) is the first entry at or after plug_pos0 + n*plug_ld + s*slice_cols, the last
  * one plug_pos0 + N*plug_ld.  slices / slice_cols come from pp_quad_big_plan; with
- * slices > 1 the workspace (pp_quad_big_workspace_size bytes) holds float32 partial sums:
- * zero before the first call, left zero by every call; calls that share it must not
- * overlap.  No counterpart kernel in the reference.
+ * slices > 1 the workspace (pp_quad_big_workspace_size bytes, 16-byte aligned) holds
+ * float32 partial sums: zero before the first call, left zero by every call; calls that
+ * share it must not overlap.  No counterpart kernel in the reference.
  */
 enum pp_quad_layout { PP_QUAD_NK = 0, PP_QUAD_KN = 1 };
 int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const void* a, int64_t a_sm,

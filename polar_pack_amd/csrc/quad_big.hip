@@ -1,22 +1,22 @@
-// Quad-pack decode GEMM on the matrix cores for large batches (more than 64 tokens), and
-// for 9-64 tokens on (K,N) storage: one fused pass produces the 4 models' outputs
+// Quad-pack decode GEMM on the matrix cores for large batches (more than 64 tokens, the
+// producer/consumer form below), and for 1-64 tokens on (K,N) storage: one fused pass
+// produces the 4 models' outputs
 //   out_m[j, n] = fp16( s_m * sum_k x[j, k] * W_m[n, k] )
 // (quad_kernels.py:123-134) with W_m decoded from the codes in registers
 // (quad_kernels.py:103-121, quaternion_packer.py:173-185), the plug table patched into
 // the decoded operands (quaternion_packer.py:187-193), and no weight ever written to
 // memory.
 //
-// Work item = 16 weight rows x TT token tiles of 16 (TT = 1, 2, 4 or 8, the fewest that
-// hold the batch) x one K slice, one wavefront, v_mfma_f32_16x16x32_f16 (operand layouts
-// as in quad_mfma.hip):
+// Up to 64 tokens, work item = 16 weight rows x TT token tiles of 16 (TT = 1, 2 or 4, the
+// fewest that hold the batch) x one K slice, one wavefront, v_mfma_f32_16x16x32_f16
+// (operand layouts as in quad_mfma.hip):
 //  * per 32-column step a lane decodes 8 code words of its row (n0 + i, i = lane % 16,
 //    columns k0 + 8(lane/16) .. +7), so each code word is decoded once per 16 TT tokens and
 //    feeds 4 models x TT token tiles of products;
 //  * x is the B operand as stored: lane l reads tokens 16t + l%16 at the same 8 columns;
 //  * 4 models x TT token tiles of 16 x 16 fp32 sums stay in registers, with G buffers of
 //    codes (loaded G - 1 steps ahead), two of x (loaded a step before the products that
-//    use it) and two of decoded operands (QbCfg: with 8 tiles a wavefront takes a SIMD's
-//    register file, with fewer two share it);
+//    use it) and two of decoded operands (QbCfg);
 //  * the products of step s - 1 are issued between the arithmetic of step s, after step
 //    s's LDS lookups (with one tile, step s + 1's).
 // Codes in either storage: (N,K) rows (the stream container, K contiguous: two 16-byte
@@ -32,25 +32,24 @@ namespace pp {
 
 constexpr int QB_ROWS = 16;     // weight rows per item
 
-// TT 16-token tiles per item (1, 2, 4 or 8: up to 16, 32, 64 or 128 tokens).  With 8 tiles
-// a wavefront takes a SIMD's register file (4 waves per workgroup, one per SIMD).  With up
-// to 4 it fits in half of it: on (N,K) rows two waves share a SIMD (8 per workgroup); on
+// TT 16-token tiles per item (1, 2 or 4: up to 16, 32 or 64 tokens).  A wavefront fits in
+// half of a SIMD's register file: on (N,K) rows two waves share a SIMD (8 per workgroup); on
 // (K,N) storage one wave per SIMD with twice the items measured faster (4096 x 4096 at 16 /
 // 32 / 64 tokens: 27 / 32 / 44 against 31 / 39 / 51 us; the second wave of a SIMD ran its
 // items 1.29x slower than the first, and the (K,N) step's 8 four-byte code loads per lane
 // leave less to overlap).  One workgroup per CU: the decode tables fill the LDS.
 // G: steps per loop pass = code buffers, the codes of a step loaded G - 1 steps before it
 // (2 KiB per wave and step: with few token tiles the decode is short and a wave needs
-// several steps of codes in flight to cover the HBM latency; with 8 the registers allow 2).
+// several steps of codes in flight to cover the HBM latency).
 template <int TT, bool KN> struct QbCfg {
-  static constexpr int WPE = TT == 8 || KN ? 1 : 2;    // waves per SIMD
+  static constexpr int WPE = KN ? 1 : 2;               // waves per SIMD
   static constexpr int NT = 256 * WPE;
   static constexpr int WAVES = NT / 64;
   static constexpr int G = TT <= 2 ? 4 : 2;
 };
 
 // Token tiles per item for a batch of M tokens.
-static inline int qb_tt(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
+static inline int qb_tt(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
 
 struct QuadBigArgs {
   const uint32_t* codes;
@@ -300,19 +299,19 @@ __attribute__((amdgpu_waves_per_eu(QbCfg<TT, KN>::WPE, QbCfg<TT, KN>::WPE))) voi
 }
 
 // ---------------------------------------------------------------- producer/consumer form
-// From PP_QB_PC_MIN tokens: a workgroup of 8 waves takes an item of 32 weight rows x 256
-// tokens x one K slice.  Waves 0-3 decode (producers) and waves 4-7 multiply (consumers),
+// From 65 tokens: a workgroup of 8 waves takes an item of 32 weight rows x a block of 64 TT
+// tokens (TT = 2 or 4, pc_tt) x one K slice.  Waves 0-3 decode (producers) and waves 4-7
+// multiply (consumers),
 // one of each per SIMD, so a SIMD's VALU decode and its matrix products come from two
 // waves and run side by side (the one-wave form issues them in turn).  Per super-step of
 // 64 columns, producer p decodes row tile p % 2 at column half p / 2 (8 code words per
 // lane, as above) into LDS as the MFMA A operands of the 4 models; consumer c multiplies
-// the previous super-step's 2 x 2 x 4 operands with its 4 token tiles of x (tokens
-// 64c .. 64c + 63 of the block).  Each code word is decoded once per 256 tokens.  The
-// tables take the split layout (128 KiB, any LUTs), the two operand buffers the rest.
-#ifndef PP_QB_PC_MIN
-#define PP_QB_PC_MIN 256
-#endif
-constexpr int PC_ROWS = 32, PC_TT = 4, PC_TOK = 256, PC_NT = 512;
+// the previous super-step's 2 x 2 x 4 operands with its TT token tiles of x (tokens
+// 16 TT c .. 16 TT (c + 1) - 1 of the block).  Each code word is decoded once per 64 TT
+// tokens.  The tables take the split layout (128 KiB, any LUTs), the two operand buffers
+// the rest.
+constexpr int64_t PC_MIN_M = 65;
+constexpr int PC_ROWS = 32, PC_NT = 512;
 constexpr int PC_G = 4;                                   // code buffers of a producer
 // The operand buffers come first in LDS, so that every operand access is one lane base plus
 // an immediate offset (below 64 KiB); the tables follow.
@@ -386,45 +385,56 @@ __device__ __forceinline__ void pc_producer(char* lds, const QuadBigArgs& A, int
   }
 }
 
-template <bool KN>
+template <bool KN, int TT>
 __device__ __forceinline__ void pc_consumer(const char* lds, const QuadBigArgs& A, int c, int n0b, int j0b, int kb,
                                             int ke) {
   const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
-  const int j0 = j0b + 16 * PC_TT * c;
+  const int j0 = j0b + 16 * TT * c;
   const f16* xblk = A.x + (int64_t)min(j0, A.M - 1) * A.x_sm;
-  uint32_t vox[PC_TT];
+  uint32_t vox[TT];
 #pragma unroll
-  for (int t = 0; t < PC_TT; ++t) {
+  for (int t = 0; t < TT; ++t) {
     const int jl = 16 * t + i;
     vox[t] = j0 + jl < A.M ? 2u * (uint32_t)(jl * A.x_sm + 8 * q) : OOB;
   }
   const int jx = min(j0, A.M - 1);
   const int ns = pc_steps(kb, ke);
-  f4 Cacc[2][4][PC_TT];
+  f4 Cacc[2][4][TT];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
-      for (int t = 0; t < PC_TT; ++t) Cacc[rt][m][t] = f4{0.f, 0.f, 0.f, 0.f};
-  QbX<PC_TT> X[2][2];   // [buffer][column half]
-  auto loadx = [&](QbX<PC_TT>(&xb)[2], int s) {
+      for (int t = 0; t < TT; ++t) Cacc[rt][m][t] = f4{0.f, 0.f, 0.f, 0.f};
+  QbX<TT> X[2][2];   // [buffer][column half]
+  auto loadx = [&](QbX<TT>(&xb)[2], int s) {
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) qb_x<PC_TT>(A, kb + 64 * s + 32 * kh, ke, vox, xblk, jx, xb[kh]);
+    for (int kh = 0; kh < 2; ++kh) qb_x<TT>(A, kb + 64 * s + 32 * kh, ke, vox, xblk, jx, xb[kh]);
   };
-  auto multiply = [&](const QbX<PC_TT>(&xb)[2], int s) {
+  // The 16 operands of a super-step are read in 4 groups (row tile, column half) of the 4
+  // models; group g + 1 is requested before group g's products, so the products do not
+  // wait on LDS.
+  auto multiply = [&](const QbX<TT>(&xb)[2], int s) {
+    h8 a[2][4];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int m = 0; m < 4; ++m) a[0][m] = *reinterpret_cast<const h8*>(lds + pc_aoff(s & 1, 0, 0, m, lane));
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
+    for (int g = 0; g < 4; ++g) {
+      const int rt = g >> 1, kh = g & 1;
+      if (g < 3) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const h8 a = *reinterpret_cast<const h8*>(lds + pc_aoff(s & 1, rt, kh, m, lane));
+        for (int m = 0; m < 4; ++m)
+          a[(g + 1) & 1][m] = *reinterpret_cast<const h8*>(lds + pc_aoff(s & 1, (g + 1) >> 1, (g + 1) & 1, m, lane));
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int t = 0; t < PC_TT; ++t)
-            Cacc[rt][m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8, xb[kh].xb[t]),
-                                                                    Cacc[rt][m][t], 0, 0, 0);
-        }
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+          Cacc[rt][m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[g & 1][m], __builtin_bit_cast(h8, xb[kh].xb[t]),
+                                                                  Cacc[rt][m][t], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
   loadx(X[0], 0);
   __syncthreads();
@@ -446,7 +456,7 @@ __device__ __forceinline__ void pc_consumer(const char* lds, const QuadBigArgs& 
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
-      for (int t = 0; t < PC_TT; ++t) {
+      for (int t = 0; t < TT; ++t) {
         const int j = j0 + 16 * t + i;
         const int nn = n0b + 16 * rt + 4 * q;
         const f4 v = Cacc[rt][m][t] * A.s[m];
@@ -471,7 +481,7 @@ __device__ __forceinline__ void pc_consumer(const char* lds, const QuadBigArgs& 
       }
 }
 
-template <bool KN>
+template <bool KN, int TT>
 __global__ __launch_bounds__(PC_NT) void quad_big_pc_kernel(const QuadBigArgs A) {
   __shared__ __attribute__((aligned(16))) uint32_t Tb[QLDS_BYTES / 4];
   char* lds = reinterpret_cast<char*>(Tb);
@@ -488,13 +498,13 @@ __global__ __launch_bounds__(PC_NT) void quad_big_pc_kernel(const QuadBigArgs A)
     const int rb = (int)uniform64(it % A.tiles);
     const int64_t w = it / A.tiles;
     const int tb = (int)uniform64(w % A.tblocks), sl = (int)uniform64(w / A.tblocks);
-    const int n0b = rb * PC_ROWS, j0b = tb * PC_TOK;
+    const int n0b = rb * PC_ROWS, j0b = tb * 64 * TT;
     const int kb = sl * A.ks, ke = min(A.K, kb + A.ks);
     if (wave < 4) {
       if (A.plug.n > 0) pc_producer<KN, true>(lds, A, wave, n0b, kb, ke, sl);
       else pc_producer<KN, false>(lds, A, wave, n0b, kb, ke, sl);
     } else {
-      pc_consumer<KN>(lds, A, wave - 4, n0b, j0b, kb, ke);
+      pc_consumer<KN, TT>(lds, A, wave - 4, n0b, j0b, kb, ke);
     }
   }
 }
@@ -506,34 +516,56 @@ static void qb_launch(bool kn, int64_t grid, hipStream_t st, const QuadBigArgs& 
 }
 
 // Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero.  Runs after the
-// item kernel has completed, so its atomics are visible to plain loads.  Thread = 4
-// consecutive tokens of one (model, row).
+// item kernel has completed, so its atomics are visible to plain loads.  (The items add
+// into [m][n][j], where a wave's atomics for one row of its tile cover 16 consecutive
+// tokens; the outputs are [j][n].)  A workgroup takes 64 rows x 64 tokens of one model and
+// transposes them through LDS, so its loads, clears and stores each run along a row.
+constexpr int QF_T = 64;
 __global__ __launch_bounds__(256) void quad_big_finish_kernel(float* acc, f16* o0, f16* o1, f16* o2, f16* o3,
-                                                              int64_t o_sm, int N, int M) {
-  const int64_t total = 4ll * N * M;
-  const int64_t i0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
-  if (i0 >= total) return;
-  float v[4];
-  if (M % 4 == 0) {
-    const float4 t = *reinterpret_cast<const float4*>(acc + i0);
-    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-    *reinterpret_cast<float4*>(acc + i0) = make_float4(0.f, 0.f, 0.f, 0.f);
-  } else {
+                                                              int64_t o_sm, int N, int M, bool vec) {
+  __shared__ float tile[QF_T][QF_T + 1];
+  const int tn = (N + QF_T - 1) / QF_T, tj = (M + QF_T - 1) / QF_T;
+  const int m = blockIdx.x / (tn * tj), r = blockIdx.x % (tn * tj);
+  const int n0 = (r / tj) * QF_T, j0 = (r % tj) * QF_T;
+  const int t = threadIdx.x, c4 = 4 * (t & 15), r16 = t >> 4;
+  float* a = acc + (int64_t)m * N * M;
+  const bool full = n0 + QF_T <= N && j0 + QF_T <= M && M % 4 == 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = i0 + e < total ? acc[i0 + e] : 0.f;
-      if (i0 + e < total) acc[i0 + e] = 0.f;
+  for (int p = 0; p < QF_T / 16; ++p) {
+    const int n = n0 + 16 * p + r16;
+    float* src = a + (int64_t)n * M + j0 + c4;
+    float v[4];
+    if (full) {
+      const float4 x = *reinterpret_cast<const float4*>(src);
+      *reinterpret_cast<float4*>(src) = make_float4(0.f, 0.f, 0.f, 0.f);
+      v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool in = n < N && j0 + c4 + e < M;
+        v[e] = in ? src[e] : 0.f;
+        if (in) src[e] = 0.f;
+      }
     }
-  }
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int64_t idx = i0 + e;
-    if (idx >= total) break;
-    const int j = (int)(idx % M);
-    const int64_t mn = idx / M;
-    const int row = (int)(mn % N), m = (int)(mn / N);
-    f16* o = m == 0 ? o0 : m == 1 ? o1 : m == 2 ? o2 : o3;
-    o[(int64_t)j * o_sm + row] = (f16)v[e];
+    for (int e = 0; e < 4; ++e) tile[16 * p + r16][c4 + e] = v[e];
+  }
+  __syncthreads();
+  f16* o = m == 0 ? o0 : m == 1 ? o1 : m == 2 ? o2 : o3;
+#pragma unroll
+  for (int p = 0; p < QF_T / 16; ++p) {
+    const int j = j0 + 16 * p + r16, n = n0 + c4;
+    if (j >= M) continue;
+    f16* dst = o + (int64_t)j * o_sm + n;
+    const f16x4 h = {(f16)tile[c4][16 * p + r16], (f16)tile[c4 + 1][16 * p + r16], (f16)tile[c4 + 2][16 * p + r16],
+                     (f16)tile[c4 + 3][16 * p + r16]};
+    if (vec && n + 3 < N) {
+      *reinterpret_cast<f16x4*>(dst) = h;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < N) dst[e] = h[e];
+    }
   }
 }
 
@@ -543,16 +575,30 @@ __global__ __launch_bounds__(256) void quad_big_finish_kernel(float* acc, f16* o
 template <int TT>
 static int64_t qb_waves_of(bool kn) { return kn ? QbCfg<TT, true>::WAVES : QbCfg<TT, false>::WAVES; }
 static int64_t qb_waves(int tt, bool kn) {
-  return tt == 1 ? qb_waves_of<1>(kn) : tt == 2 ? qb_waves_of<2>(kn) : tt == 4 ? qb_waves_of<4>(kn) : qb_waves_of<8>(kn);
+  return tt == 1 ? qb_waves_of<1>(kn) : tt == 2 ? qb_waves_of<2>(kn) : qb_waves_of<4>(kn);
 }
 
-// The producer/consumer form: items of 32 rows x 256 tokens.  K is cut into slices only
-// when the items would leave more than half the CUs idle, into as few as fill them: the
-// slices' sums go through float32 atomics and a second launch (gate 11008x2048 at 256
-// tokens: 214 us with 2 slices, 344 items, against one slice).
+// Token tiles per consumer of the producer/consumer form: blocks of 128 tokens (TT = 2) to
+// 255 tokens, and above where 256-token blocks would leave half the CUs idle while 128-token
+// ones fill them; 256 otherwise.  A super-step of 128 tokens takes ~2/3 of one of 256
+// (4096x4096 at 256 tokens: 65 against 98 us with 256-token blocks in 2 K slices; at 128 /
+// 192: 57 / 64 against 83 / 117 us on the one-wave form; 11008x2048 rows at 128 / 192: 110
+// / 153 against 163 / 223; but 11008x2048 at 256 tokens 156 against 128, 2048x11008 165
+// against 122, 4096x4096 at 384 121 against 98).
+static int pc_tt(int64_t M, int64_t N) {
+  if (M < 256) return 2;
+  const int64_t cus = device_cu_count(), rb = (N + PC_ROWS - 1) / PC_ROWS;
+  const int64_t g4 = rb * ((M + 255) / 256), g2 = rb * ((M + 127) / 128);
+  return 2 * g4 <= cus && g2 >= cus ? 2 : 4;
+}
+
+// The producer/consumer form's K slices: only when the items would leave more than half
+// the CUs idle, into as few as fill them: the slices' sums go through float32 atomics and a
+// second launch (gate 11008x2048 at 256 tokens: 214 us with 2 slices, 344 items, against
+// one slice).
 static void pc_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* cols) {
-  const int64_t cus = device_cu_count(), steps = K / 32;
-  const int64_t groups = (N + PC_ROWS - 1) / PC_ROWS * ((M + PC_TOK - 1) / PC_TOK);
+  const int64_t cus = device_cu_count(), steps = K / 32, tok = 64 * pc_tt(M, N);
+  const int64_t groups = (N + PC_ROWS - 1) / PC_ROWS * ((M + tok - 1) / tok);
   int64_t s = 1;
   if (2 * groups <= cus) s = std::min<int64_t>(steps, (cus + groups - 1) / groups);
   const int64_t per = (steps + s - 1) / s;
@@ -561,11 +607,10 @@ static void pc_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* c
 }
 
 static void qb_plan(int64_t M, int64_t N, int64_t K, bool kn, int64_t* slices, int64_t* cols) {
-  if (M >= PP_QB_PC_MIN) return pc_plan(M, N, K, slices, cols);
+  if (M >= PC_MIN_M) return pc_plan(M, N, K, slices, cols);
   const int tt = qb_tt(M);
   const int64_t cus = device_cu_count(), wv = qb_waves(tt, kn);
-  const int64_t g = tt == 1 ? QbCfg<1, false>::G : tt == 2 ? QbCfg<2, false>::G : tt == 4 ? QbCfg<4, false>::G
-                                                                                    : QbCfg<8, false>::G;
+  const int64_t g = tt == 1 ? QbCfg<1, false>::G : tt == 2 ? QbCfg<2, false>::G : QbCfg<4, false>::G;
   const int64_t steps = K / 32;
   // groups of wv row tiles (one per workgroup and round) for s slices; a launch takes
   // ceil(groups / CUs) rounds of items of ceil(steps / s) steps (whole loop passes of g),
@@ -636,6 +681,7 @@ extern "C" int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const
   const int64_t need = pp_quad_big_workspace_size(M, N, slices);
   PP_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), "workspace too small: need %lld bytes",
              (long long)need);
+  PP_REQUIRE(need == 0 || aligned(workspace, 16), "the workspace must be 16-byte aligned");
   QuadBigArgs A = {};
   A.codes = codes;
   A.ldc = ldc;
@@ -665,14 +711,21 @@ extern "C" int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const
   A.pld = plug_ld;
   A.acc = reinterpret_cast<float*>(workspace);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (M >= PP_QB_PC_MIN) {
+  if (M >= PC_MIN_M) {
+    const int ptt = pc_tt(M, N);
     A.tiles = (int)((N + PC_ROWS - 1) / PC_ROWS);
-    A.tblocks = (int)((M + PC_TOK - 1) / PC_TOK);
+    A.tblocks = (int)((M + 64 * ptt - 1) / (64 * ptt));
     const int64_t items = (int64_t)A.tiles * A.tblocks * slices;
     const int64_t grid = std::min<int64_t>(device_cu_count(), items);
     A.xcd_remap = grid % 8 == 0;
-    if (kn) hipLaunchKernelGGL(quad_big_pc_kernel<true>, dim3((unsigned)grid), dim3(PC_NT), 0, st, A);
-    else hipLaunchKernelGGL(quad_big_pc_kernel<false>, dim3((unsigned)grid), dim3(PC_NT), 0, st, A);
+    const dim3 g((unsigned)grid), b(PC_NT);
+    if (ptt == 2) {
+      if (kn) hipLaunchKernelGGL((quad_big_pc_kernel<true, 2>), g, b, 0, st, A);
+      else hipLaunchKernelGGL((quad_big_pc_kernel<false, 2>), g, b, 0, st, A);
+    } else {
+      if (kn) hipLaunchKernelGGL((quad_big_pc_kernel<true, 4>), g, b, 0, st, A);
+      else hipLaunchKernelGGL((quad_big_pc_kernel<false, 4>), g, b, 0, st, A);
+    }
   } else {
   const int64_t wv = qb_waves(tt, kn);
   const int64_t groups = (int64_t)(A.tiles + wv - 1) / wv * A.tblocks * slices;
@@ -682,15 +735,14 @@ extern "C" int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const
   switch (tt) {
     case 1: qb_launch<1>(kn, grid, st, A); break;
     case 2: qb_launch<2>(kn, grid, st, A); break;
-    case 4: qb_launch<4>(kn, grid, st, A); break;
-    default: qb_launch<8>(kn, grid, st, A); break;
+    default: qb_launch<4>(kn, grid, st, A); break;
   }
   }
   PP_LAUNCH_CHECK();
   if (slices > 1) {
-    const int64_t total = 4 * N * M;
-    hipLaunchKernelGGL(quad_big_finish_kernel, dim3((unsigned)((total / 4 + 255) / 256 + 1)), dim3(256), 0, st,
-                       A.acc, A.out[0], A.out[1], A.out[2], A.out[3], o_sm, A.N, A.M);
+    const int64_t tiles = 4 * ((N + QF_T - 1) / QF_T) * ((M + QF_T - 1) / QF_T);
+    hipLaunchKernelGGL(quad_big_finish_kernel, dim3((unsigned)tiles), dim3(256), 0, st, A.acc, A.out[0], A.out[1],
+                       A.out[2], A.out[3], o_sm, A.N, A.M, (bool)A.vec_out);
     PP_LAUNCH_CHECK();
   }
   return PP_OK;

@@ -16,7 +16,7 @@ The kernel of a call comes from one table, :data:`polar_pack_amd.routes.QUAD_ROU
 the row kernel to 4 tokens, the matrix-core batch decode at 5-64 and the fused matrix-core
 kernel at 65-128; on (K,N) storage the fused (K,N) row kernel at 1 token (and with plug
 entries up to 8) and the fused matrix-core kernel on the codes as stored from 2 tokens (3
-when N > K) to 128 (two 8-token row passes up to 16 tokens when K % 32 != 0); larger
+when N > K) to 256 (two 8-token row passes up to 16 tokens when K % 32 != 0); larger
 batches, and more tokens on other layouts, decode once into fp16 weights (the values the
 reference's kernel rounds its weights to, quad_kernels.py:117-126) and run a library fp16
 GEMM (hipBLASLt through torch.matmul), where the matmul's compute, not the weight stream,

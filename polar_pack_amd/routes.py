@@ -20,7 +20,7 @@ Quad kernels (the reference's one fused kernel, quad_kernels.py:53-159, at every
 * ``kn``       fused row decode of (K,N) codes with unit column stride (``pack_quad_layer``),
                8 tokens per pass (``pp_quad_gemm`` -> ``quad_kn_kernel``)
 * ``mfma``     matrix-core batch decode of (N,K) rows, 1-64 tokens per launch (``pp_quad_mfma``)
-* ``big_nk``   fused matrix-core kernel on (N,K) rows, blocks of 16-128 tokens (``pp_quad_big``)
+* ``big_nk``   fused matrix-core kernel on (N,K) rows, blocks of 16-256 tokens (``pp_quad_big``)
 * ``big_kn``   the same kernel on (K,N) codes as stored
 * ``kn_mfma``  (K,N) codes transposed into (N,K) rows, then ``mfma`` (``fused=False`` only)
 * ``prefill``  fp16 decode + one batched library GEMM (hipBLASLt through ``torch.matmul``)
@@ -93,8 +93,9 @@ QUAD_ROUTES = (
     Route("rows", 1, 4),
     Route("mfma", 5, 64),
     Route("rows", 5, 8),                                   # K % 32 != 0: no matrix cores
-    # 65-128 tokens: the fused kernel (4096x4096: 87.5 us at 128 tokens against 128 us for
-    # four fp16 matmuls); above, the fp16 decode + one batched GEMM unless fused=True
+    # 65-128 tokens: the fused kernel (11008x2048 / 2048x11008, 0.1 % plug: 106-108 / 87-90
+    # us against 113-115 / 114-121 us for the fp16 decode + one batched GEMM at 65-128
+    # tokens; 150 / 156 against 116 / 149 at 192); above, the decode + GEMM unless fused=True
     Route("big_nk", 65, 128, fused=(None,)),
     Route("big_nk", 65, INF, fused=(True,)),
     # (K,N) codes (pack_quad_layer): the fused kernel at any size when asked for
@@ -103,8 +104,10 @@ QUAD_ROUTES = (
     # move the entries to its (N,K) frame on every call)
     Route("kn", 1, 1),
     Route("kn", 1, 8, plug=(True,)),
-    Route("big_kn", kn_big_min_m, 128, plug=(False,), fused=(None,)),
-    Route("big_kn", 9, 128, plug=(True,), fused=(None,)),
+    # to 256 tokens (4096x4096 at 65 / 128 / 192 / 256: 55 / 58 / 63 / 68 us against 64 / 64
+    # / 73 / 80 us for the fp16 decode + one batched GEMM; at 320 96 against 81)
+    Route("big_kn", kn_big_min_m, 256, plug=(False,), fused=(None,)),
+    Route("big_kn", 9, 256, plug=(True,), fused=(None,)),
     # fused=False on (K,N): transposed copy + batch decode (4096x4096 16 / 32 / 64 tokens 59
     # / 65 / 84 us, against 33 / 40 / 58 us on the fused kernel)
     Route("kn_mfma", 9, 64, fused=(False,)),

@@ -17,11 +17,11 @@ from test_gpu_quad import check_route, fp16_luts, random_codes, u32
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
-SCAN = range(1, 141)
+SCAN = range(1, 300)
 
 
 def boundary_ms(route_of):
-    """1, then M - 1 and M at every token count M where the route changes (up to 140)."""
+    """1, then M - 1 and M at every token count M where the route changes (up to 299)."""
     ms = {1}
     prev = route_of(1)
     for M in SCAN:

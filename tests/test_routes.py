@@ -53,15 +53,15 @@ QUAD_TABLE = [
     (nk(2056, 512), (False, True), None, "rows:1-8 prefill:9-"),                 # K % 32 != 0
     (nk(2056, 512), (False, True), True, "rows:1-8 prefill:9-"),
     (nk(2048, 512, ptr=8), (False, True), None, "generic:1-8 prefill:9-"),        # not 16-byte aligned
-    (kn(2048, 512), (False,), None, "kn:1-1 big_kn:2-128 prefill:129-"),           # N <= K
-    (kn(512, 2048), (False,), None, "kn:1-2 big_kn:3-128 prefill:129-"),           # N > K
-    (kn(2048, 512), (True,), None, "kn:1-8 big_kn:9-128 prefill:129-"),
-    (kn(512, 2048), (True,), None, "kn:1-8 big_kn:9-128 prefill:129-"),
+    (kn(2048, 512), (False,), None, "kn:1-1 big_kn:2-256 prefill:257-"),           # N <= K
+    (kn(512, 2048), (False,), None, "kn:1-2 big_kn:3-256 prefill:257-"),           # N > K
+    (kn(2048, 512), (True,), None, "kn:1-8 big_kn:9-256 prefill:257-"),
+    (kn(512, 2048), (True,), None, "kn:1-8 big_kn:9-256 prefill:257-"),
     (kn(2048, 512), (False, True), True, "big_kn:1-"),
     (kn(2048, 512), (False, True), False, "kn:1-8 kn_mfma:9-64 prefill:65-"),
     (kn(2056, 512), (False, True), None, "kn:1-16 prefill:17-"),                  # K % 32 != 0
     (kn(2056, 512), (False, True), True, "kn:1-16 prefill:17-"),
-    ((512, 1, 256, 2048, 510), (False,), None, "generic:1-1 big_kn:2-128 prefill:129-"),   # N % 4 != 0
+    ((512, 1, 256, 2048, 510), (False,), None, "generic:1-1 big_kn:2-256 prefill:257-"),   # N % 4 != 0
     ((3000, 2, 256, 2048, 512), (False, True), None, "generic:1-8 prefill:9-"),    # no unit stride
     # lm_head-sized (K,N) codes: K * ldk >= 2^29 words is past the fused kernel's 2 GiB record,
     # so it stays on the (K,N) row kernel, then the decode + GEMM
