@@ -347,34 +347,12 @@ __global__ __launch_bounds__(DM_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
   else dm_body<TT, false, false>(T, A);
 }
 
-// Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero (after the item kernel
-// has completed).  Thread = 4 consecutive tokens of one (model, column).
+// Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero (finish_tile).
 __global__ __launch_bounds__(256) void dual_mfma_finish_kernel(float* acc, f16* o0, f16* o1, int64_t o_sm, int N,
-                                                               int M) {
-  const int64_t total = 2ll * N * M;
-  const int64_t i0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
-  if (i0 >= total) return;
-  float v[4];
-  if (M % 4 == 0) {
-    const float4 t = *reinterpret_cast<const float4*>(acc + i0);
-    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-    *reinterpret_cast<float4*>(acc + i0) = make_float4(0.f, 0.f, 0.f, 0.f);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = i0 + e < total ? acc[i0 + e] : 0.f;
-      if (i0 + e < total) acc[i0 + e] = 0.f;
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int64_t idx = i0 + e;
-    if (idx >= total) break;
-    const int j = (int)(idx % M);
-    const int64_t mn = idx / M;
-    const int col = (int)(mn % N), m = (int)(mn / N);
-    (m == 0 ? o0 : o1)[(int64_t)j * o_sm + col] = (f16)v[e];
-  }
+                                                               int M, bool vec) {
+  int m, n0, j0;
+  finish_coords(N, M, m, n0, j0);
+  finish_tile(acc + (int64_t)m * N * M, m == 0 ? o0 : o1, o_sm, N, M, n0, j0, vec);
 }
 
 // ------------------------------------------------------------ (N,K) container rows
@@ -650,6 +628,7 @@ extern "C" int pp_dual_mfma(const void* codes, int64_t ldk, const void* a, int64
   const int64_t need = pp_dual_mfma_workspace_size(M, N, slices);
   PP_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), "workspace too small: need %lld bytes",
              (long long)need);
+  PP_REQUIRE(need == 0 || aligned(workspace, 16), "the workspace must be 16-byte aligned");
   DualMfmaArgs A = {};
   A.codes = reinterpret_cast<const uint16_t*>(codes);
   A.ldk = ldk;
@@ -700,9 +679,8 @@ extern "C" int pp_dual_mfma(const void* codes, int64_t ldk, const void* a, int64
   }
   PP_LAUNCH_CHECK();
   if (slices > 1) {
-    const int64_t total = 2 * N * M;
-    hipLaunchKernelGGL(dual_mfma_finish_kernel, dim3((unsigned)((total / 4 + 255) / 256 + 1)), dim3(256), 0, st,
-                       A.acc, A.out[0], A.out[1], o_sm, A.N, A.M);
+    hipLaunchKernelGGL(dual_mfma_finish_kernel, dim3((unsigned)finish_tiles(2, N, M)), dim3(256), 0, st, A.acc,
+                       A.out[0], A.out[1], o_sm, A.N, A.M, o_sm % 4 == 0 && aligned(out1, 8) && aligned(out2, 8));
     PP_LAUNCH_CHECK();
   }
   return PP_OK;
@@ -740,6 +718,7 @@ extern "C" int pp_dual_nk_mfma(const void* codes, int code_layout, int64_t ldc, 
   const int64_t need = pp_dual_mfma_workspace_size(M, N, slices);
   PP_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), "workspace too small: need %lld bytes",
              (long long)need);
+  PP_REQUIRE(need == 0 || aligned(workspace, 16), "the workspace must be 16-byte aligned");
   DualNkArgs A = {};
   A.codes = reinterpret_cast<const uint16_t*>(codes);
   A.ldc = ldc;
@@ -789,9 +768,8 @@ extern "C" int pp_dual_nk_mfma(const void* codes, int code_layout, int64_t ldc, 
   hipLaunchKernelGGL(kernels[tt == 2 ? 0 : tt == 4 ? 1 : 2][be ? 1 : 0], dim3((unsigned)grid), dim3(DM_NT), 0, st, A);
   PP_LAUNCH_CHECK();
   if (slices > 1) {
-    const int64_t total = 2 * N * M;
-    hipLaunchKernelGGL(dual_mfma_finish_kernel, dim3((unsigned)((total / 4 + 255) / 256 + 1)), dim3(256), 0, st,
-                       A.acc, A.out[0], A.out[1], o_sm, A.N, A.M);
+    hipLaunchKernelGGL(dual_mfma_finish_kernel, dim3((unsigned)finish_tiles(2, N, M)), dim3(256), 0, st, A.acc,
+                       A.out[0], A.out[1], o_sm, A.N, A.M, o_sm % 4 == 0 && aligned(out1, 8) && aligned(out2, 8));
     PP_LAUNCH_CHECK();
   }
   return PP_OK;

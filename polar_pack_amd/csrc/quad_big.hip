@@ -515,58 +515,13 @@ static void qb_launch(bool kn, int64_t grid, hipStream_t st, const QuadBigArgs& 
   else hipLaunchKernelGGL((quad_big_kernel<TT, false>), dim3((unsigned)grid), dim3(QbCfg<TT, false>::NT), 0, st, A);
 }
 
-// Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero.  Runs after the
-// item kernel has completed, so its atomics are visible to plain loads.  (The items add
-// into [m][n][j], where a wave's atomics for one row of its tile cover 16 consecutive
-// tokens; the outputs are [j][n].)  A workgroup takes 64 rows x 64 tokens of one model and
-// transposes them through LDS, so its loads, clears and stores each run along a row.
-constexpr int QF_T = 64;
+// Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero (finish_tile).
 __global__ __launch_bounds__(256) void quad_big_finish_kernel(float* acc, f16* o0, f16* o1, f16* o2, f16* o3,
                                                               int64_t o_sm, int N, int M, bool vec) {
-  __shared__ float tile[QF_T][QF_T + 1];
-  const int tn = (N + QF_T - 1) / QF_T, tj = (M + QF_T - 1) / QF_T;
-  const int m = blockIdx.x / (tn * tj), r = blockIdx.x % (tn * tj);
-  const int n0 = (r / tj) * QF_T, j0 = (r % tj) * QF_T;
-  const int t = threadIdx.x, c4 = 4 * (t & 15), r16 = t >> 4;
-  float* a = acc + (int64_t)m * N * M;
-  const bool full = n0 + QF_T <= N && j0 + QF_T <= M && M % 4 == 0;
-#pragma unroll
-  for (int p = 0; p < QF_T / 16; ++p) {
-    const int n = n0 + 16 * p + r16;
-    float* src = a + (int64_t)n * M + j0 + c4;
-    float v[4];
-    if (full) {
-      const float4 x = *reinterpret_cast<const float4*>(src);
-      *reinterpret_cast<float4*>(src) = make_float4(0.f, 0.f, 0.f, 0.f);
-      v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool in = n < N && j0 + c4 + e < M;
-        v[e] = in ? src[e] : 0.f;
-        if (in) src[e] = 0.f;
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) tile[16 * p + r16][c4 + e] = v[e];
-  }
-  __syncthreads();
+  int m, n0, j0;
+  finish_coords(N, M, m, n0, j0);
   f16* o = m == 0 ? o0 : m == 1 ? o1 : m == 2 ? o2 : o3;
-#pragma unroll
-  for (int p = 0; p < QF_T / 16; ++p) {
-    const int j = j0 + 16 * p + r16, n = n0 + c4;
-    if (j >= M) continue;
-    f16* dst = o + (int64_t)j * o_sm + n;
-    const f16x4 h = {(f16)tile[c4][16 * p + r16], (f16)tile[c4 + 1][16 * p + r16], (f16)tile[c4 + 2][16 * p + r16],
-                     (f16)tile[c4 + 3][16 * p + r16]};
-    if (vec && n + 3 < N) {
-      *reinterpret_cast<f16x4*>(dst) = h;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (n + e < N) dst[e] = h[e];
-    }
-  }
+  finish_tile(acc + (int64_t)m * N * M, o, o_sm, N, M, n0, j0, vec);
 }
 
 
@@ -740,9 +695,8 @@ extern "C" int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const
   }
   PP_LAUNCH_CHECK();
   if (slices > 1) {
-    const int64_t tiles = 4 * ((N + QF_T - 1) / QF_T) * ((M + QF_T - 1) / QF_T);
-    hipLaunchKernelGGL(quad_big_finish_kernel, dim3((unsigned)tiles), dim3(256), 0, st, A.acc, A.out[0], A.out[1],
-                       A.out[2], A.out[3], o_sm, A.N, A.M, (bool)A.vec_out);
+    hipLaunchKernelGGL(quad_big_finish_kernel, dim3((unsigned)finish_tiles(4, N, M)), dim3(256), 0, st, A.acc,
+                       A.out[0], A.out[1], A.out[2], A.out[3], o_sm, A.N, A.M, (bool)A.vec_out);
     PP_LAUNCH_CHECK();
   }
   return PP_OK;

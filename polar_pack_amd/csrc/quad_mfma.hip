@@ -225,36 +225,12 @@ __global__ __launch_bounds__(MfCfg<T>::NT) void quad_mfma_kernel(const QuadMfmaA
   else mfma_body<T, LaySplit>(lds, A);
 }
 
-// Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero.  This launch starts
-// after the tile kernel has completed, so its atomics are visible to plain loads and
-// plain stores clear the sums for the next launch: each thread takes 4 consecutive sums
-// (M % 4 == 0: one 16-byte load; otherwise one at a time).
-__global__ __launch_bounds__(256) void quad_mfma_finish_kernel(const QuadMfmaArgs A) {
-  const int64_t total = 4ll * A.N * A.M;
-  const int64_t i0 = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
-  if (i0 >= total) return;
-  float v[4];
-  if (A.M % 4 == 0) {
-    const float4 t = *reinterpret_cast<const float4*>(A.acc + i0);
-    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-    *reinterpret_cast<float4*>(A.acc + i0) = make_float4(0.f, 0.f, 0.f, 0.f);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = i0 + e < total ? A.acc[i0 + e] : 0.f;
-      if (i0 + e < total) A.acc[i0 + e] = 0.f;
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int64_t i = i0 + e;
-    if (i >= total) break;
-    const int j = (int)(i % A.M);
-    const int64_t mn = i / A.M;
-    const int row = (int)(mn % A.N), m = (int)(mn / A.N);
-    f16* o = m == 0 ? A.out[0] : m == 1 ? A.out[1] : m == 2 ? A.out[2] : A.out[3];
-    o[(int64_t)j * A.o_sm + row] = (f16)v[e];
-  }
+// Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero (finish_tile).
+__global__ __launch_bounds__(256) void quad_mfma_finish_kernel(const QuadMfmaArgs A, bool vec) {
+  int m, n0, j0;
+  finish_coords(A.N, A.M, m, n0, j0);
+  f16* o = m == 0 ? A.out[0] : m == 1 ? A.out[1] : m == 2 ? A.out[2] : A.out[3];
+  finish_tile(A.acc + (int64_t)m * A.N * A.M, o, A.o_sm, A.N, A.M, n0, j0, vec);
 }
 
 static int mfma_tiles_t(int64_t M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
@@ -307,6 +283,7 @@ extern "C" int pp_quad_mfma(const uint32_t* codes, int64_t ldc, int64_t elem_bas
   const int64_t need = pp_quad_mfma_workspace_size(M, N, slices);
   PP_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need),
              "workspace too small: need %lld bytes", (long long)need);
+  PP_REQUIRE(need == 0 || aligned(workspace, 16), "the workspace must be 16-byte aligned");
   QuadMfmaArgs A = {};
   A.codes = codes;
   A.ldc = ldc;
@@ -340,8 +317,8 @@ extern "C" int pp_quad_mfma(const uint32_t* codes, int64_t ldc, int64_t elem_bas
   }
   PP_LAUNCH_CHECK();
   if (slices > 1) {
-    const int64_t total = 4 * N * M;
-    hipLaunchKernelGGL(quad_mfma_finish_kernel, dim3((unsigned)((total / 4 + 255) / 256 + 1)), dim3(256), 0, st, A);
+    hipLaunchKernelGGL(quad_mfma_finish_kernel, dim3((unsigned)finish_tiles(4, N, M)), dim3(256), 0, st, A,
+                       finish_vec(out, 4, o_sm));
     PP_LAUNCH_CHECK();
   }
   return PP_OK;
