@@ -1,15 +1,15 @@
-// Quad-pack decode GEMM on the matrix cores for large batches (more than 64 tokens, the
-// producer/consumer form below), and for 1-64 tokens on (K,N) storage: one fused pass
-// produces the 4 models' outputs
+// Quad-pack decode GEMM on the matrix cores for large batches (more than 64 tokens, and 33-64
+// on (K,N) storage: the producer/consumer form below), and for fewer tokens on (K,N)
+// storage: one fused pass produces the 4 models' outputs
 //   out_m[j, n] = fp16( s_m * sum_k x[j, k] * W_m[n, k] )
 // (quad_kernels.py:123-134) with W_m decoded from the codes in registers
 // (quad_kernels.py:103-121, quaternion_packer.py:173-185), the plug table patched into
 // the decoded operands (quaternion_packer.py:187-193), and no weight ever written to
 // memory.
 //
-// Up to 64 tokens, work item = 16 weight rows x TT token tiles of 16 (TT = 1, 2 or 4, the
-// fewest that hold the batch) x one K slice, one wavefront, v_mfma_f32_16x16x32_f16
-// (operand layouts as in quad_mfma.hip):
+// The one-wave form (to 64 tokens on (N,K) rows, to 32 on (K,N) codes): work item = 16
+// weight rows x TT token tiles of 16 (TT = 1, 2 or 4, the fewest that hold the batch) x one
+// K slice, one wavefront, v_mfma_f32_16x16x32_f16 (operand layouts as in quad_mfma.hip):
 //  * per 32-column step a lane decodes 8 code words of its row (n0 + i, i = lane % 16,
 //    columns k0 + 8(lane/16) .. +7), so each code word is decoded once per 16 TT tokens and
 //    feeds 4 models x TT token tiles of products;
@@ -299,10 +299,10 @@ __attribute__((amdgpu_waves_per_eu(QbCfg<TT, KN>::WPE, QbCfg<TT, KN>::WPE))) voi
 }
 
 // ---------------------------------------------------------------- producer/consumer form
-// From 65 tokens: a workgroup of 8 waves takes an item of 32 weight rows x a block of 64 TT
-// tokens (TT = 2 or 4, pc_tt) x one K slice.  Waves 0-3 decode (producers) and waves 4-7
-// multiply (consumers),
-// one of each per SIMD, so a SIMD's VALU decode and its matrix products come from two
+// From 65 tokens (33 on (K,N) codes, pc_use): a workgroup of 8 waves takes an item of 32
+// weight rows x a block of 64 TT tokens (TT = 1, 2 or 4, pc_tt) x one K slice.  Waves 0-3
+// decode (producers) and waves 4-7 multiply (consumers), one of each per SIMD, so a SIMD's
+// VALU decode and its matrix products come from two
 // waves and run side by side (the one-wave form issues them in turn).  Per super-step of
 // 64 columns, producer p decodes row tile p % 2 at column half p / 2 (8 code words per
 // lane, as above) into LDS as the MFMA A operands of the 4 models; consumer c multiplies
@@ -310,7 +310,12 @@ __attribute__((amdgpu_waves_per_eu(QbCfg<TT, KN>::WPE, QbCfg<TT, KN>::WPE))) voi
 // 16 TT c .. 16 TT (c + 1) - 1 of the block).  Each code word is decoded once per 64 TT
 // tokens.  The tables take the split layout (128 KiB, any LUTs), the two operand buffers
 // the rest.
-constexpr int64_t PC_MIN_M = 65;
+// (K,N) codes at 33-64 tokens: 64-token blocks measured faster than the one-wave form
+// (4096x4096 / K x N = 2048x11008 / 11008x2048 at 48 tokens 37.5 / 55 / 44 against 42 / 73 /
+// 50 us, at 64 38 / 56 / 45 against 45 / 80 / 56; from 16 to 32 tokens they tie or lose:
+// 4096x4096 at 16 tokens 35 against 31 us).  On (N,K) rows the one-wave form is kept to
+// 64 tokens (the drop-in operator takes pp_quad_mfma there).
+static bool pc_use(int64_t M, bool kn) { return M >= 65 || (kn && M >= 33); }
 constexpr int PC_ROWS = 32, PC_NT = 512;
 constexpr int PC_G = 4;                                   // code buffers of a producer
 // The operand buffers come first in LDS, so that every operand access is one lane base plus
@@ -533,14 +538,15 @@ static int64_t qb_waves(int tt, bool kn) {
   return tt == 1 ? qb_waves_of<1>(kn) : tt == 2 ? qb_waves_of<2>(kn) : qb_waves_of<4>(kn);
 }
 
-// Token tiles per consumer of the producer/consumer form: blocks of 128 tokens (TT = 2) to
-// 255 tokens, and above where 256-token blocks would leave half the CUs idle while 128-token
+// Token tiles per consumer of the producer/consumer form: blocks of 64 tokens (TT = 1) to
+// 64 tokens, of 128 (TT = 2) to 255 tokens, and above where 256-token blocks would leave half the CUs idle while 128-token
 // ones fill them; 256 otherwise.  A super-step of 128 tokens takes ~2/3 of one of 256
 // (4096x4096 at 256 tokens: 65 against 98 us with 256-token blocks in 2 K slices; at 128 /
 // 192: 57 / 64 against 83 / 117 us on the one-wave form; 11008x2048 rows at 128 / 192: 110
 // / 153 against 163 / 223; but 11008x2048 at 256 tokens 156 against 128, 2048x11008 165
 // against 122, 4096x4096 at 384 121 against 98).
 static int pc_tt(int64_t M, int64_t N) {
+  if (M <= 64) return 1;
   if (M < 256) return 2;
   const int64_t cus = device_cu_count(), rb = (N + PC_ROWS - 1) / PC_ROWS;
   const int64_t g4 = rb * ((M + 255) / 256), g2 = rb * ((M + 127) / 128);
@@ -562,7 +568,7 @@ static void pc_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* c
 }
 
 static void qb_plan(int64_t M, int64_t N, int64_t K, bool kn, int64_t* slices, int64_t* cols) {
-  if (M >= PC_MIN_M) return pc_plan(M, N, K, slices, cols);
+  if (pc_use(M, kn)) return pc_plan(M, N, K, slices, cols);
   const int tt = qb_tt(M);
   const int64_t cus = device_cu_count(), wv = qb_waves(tt, kn);
   const int64_t g = tt == 1 ? QbCfg<1, false>::G : tt == 2 ? QbCfg<2, false>::G : QbCfg<4, false>::G;
@@ -666,7 +672,7 @@ extern "C" int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const
   A.pld = plug_ld;
   A.acc = reinterpret_cast<float*>(workspace);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (M >= PC_MIN_M) {
+  if (pc_use(M, kn)) {
     const int ptt = pc_tt(M, N);
     A.tiles = (int)((N + PC_ROWS - 1) / PC_ROWS);
     A.tblocks = (int)((M + 64 * ptt - 1) / (64 * ptt));
@@ -674,7 +680,10 @@ extern "C" int pp_quad_big(const uint32_t* codes, int layout, int64_t ldc, const
     const int64_t grid = std::min<int64_t>(device_cu_count(), items);
     A.xcd_remap = grid % 8 == 0;
     const dim3 g((unsigned)grid), b(PC_NT);
-    if (ptt == 2) {
+    if (ptt == 1) {
+      if (kn) hipLaunchKernelGGL((quad_big_pc_kernel<true, 1>), g, b, 0, st, A);
+      else hipLaunchKernelGGL((quad_big_pc_kernel<false, 1>), g, b, 0, st, A);
+    } else if (ptt == 2) {
       if (kn) hipLaunchKernelGGL((quad_big_pc_kernel<true, 2>), g, b, 0, st, A);
       else hipLaunchKernelGGL((quad_big_pc_kernel<false, 2>), g, b, 0, st, A);
     } else {

@@ -84,7 +84,8 @@ def test_kn_storage_with_plug_and_wider_rows(M, split):
     """(K,N) codes (pack_quad_layer's layout) as a column slice of a wider tensor (row stride
     520 > N = 300): plug entries of the block are moved to the kernel's (N,K) frame and
     applied, entries in the columns past N are not; fp16 LUTs, shared or split q1/q2; 9-192
-    tokens (1, 2, 4 and 8 token tiles, partial tiles)."""
+    tokens (the one-wave form's 1 and 2 token tiles to 32 tokens, the producer/consumer
+    form's 64- and 128-token blocks above, partial tiles and blocks)."""
     K, N, ldk = 1024, 300, 520
     seed = 500 + M + split
     wide = random_codes((K, ldk), seed)
@@ -135,13 +136,15 @@ def _call_big(x, codes_nk, luts, scales, plug, elem_base, slices, cols, o_sm):
         assert int(torch.count_nonzero(ws)) == 0, "the workspace is not left zero"
 
 
-@pytest.mark.parametrize("M", [12, 30, 64, 150])
+@pytest.mark.parametrize("M", [12, 30, 64, 150, 300])
 @pytest.mark.parametrize("slices,cols", [(1, 512), (2, 256), (3, 192), (16, 32)])
 def test_explicit_slices_and_odd_output_stride(slices, cols, M):
     """Every K-slice plan (one slice: direct fp16 stores; more: float32 atomics and the
-    finish pass; slices shorter than a loop pass of 2 or 4 steps), N = 70 (a partial 16-row
-    tile), 12-150 tokens (1, 2, 4 and 8 token tiles), an odd output row stride (no 4-row
-    stores), and the columns past N left untouched."""
+    finish pass; slices shorter than a loop pass of 2 or 4 steps, or than a 64-column
+    super-step), N = 70 (a partial 16-row tile, a partial 32-row block), 12-300 tokens (the
+    one-wave form's 1, 2 and 4 token tiles to 64 tokens on these (N,K) rows, the
+    producer/consumer form's 128- and 256-token blocks above), an odd output row stride (no
+    4-row stores), and the columns past N left untouched."""
     N, K = 70, 512
     ws_ = gen.correlated_models(31, [N * K] * 4)
     qp = oqp.pack_quad(ws_, threshold=0.02)
