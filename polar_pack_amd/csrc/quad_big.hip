@@ -218,7 +218,7 @@ __device__ __forceinline__ void qb_body(const char* lds, const QuadBigArgs& A) {
     const int n = n0 + i;
     const bool ok = n < A.N;
     R.voc = !ok ? OOB : KN ? 4u * (uint32_t)(8 * q * A.ldc + i) : 4u * (uint32_t)(i * A.ldc + 8 * q);
-    uint32_t pidx[4];
+    uint32_t pidx[MPW];
     if constexpr (PLUG) {
       R.rowpos = A.ppos0 + (int64_t)n * A.pld;
       R.P.next = ok ? A.row_plug[(int64_t)n * A.slices + sl] : 0;
@@ -348,7 +348,7 @@ __device__ __forceinline__ void pc_producer(char* lds, const QuadBigArgs& A, int
   const uint32_t* ctile = KN ? A.codes + n0c : A.codes + (int64_t)n0c * A.ldc;
   MPlug P;
   int64_t rowpos = 0;
-  uint32_t pidx[4];
+  uint32_t pidx[MPW];
   if constexpr (PLUG) {
     rowpos = A.ppos0 + (int64_t)n * A.pld;
     P.next = ok ? A.row_plug[(int64_t)n * A.slices + sl] : 0;
@@ -367,9 +367,9 @@ __device__ __forceinline__ void pc_producer(char* lds, const QuadBigArgs& A, int
     h8 a[4];
     math8(lk, a);
     const int k0 = kb + 64 * s + 32 * kh;
-    if constexpr (PLUG) mplug_patch(A.plug, P, rowpos, k0 + 8 * q, k0, a);
 #pragma unroll
     for (int m = 0; m < 4; ++m) *reinterpret_cast<h8*>(lds + pc_aoff(s & 1, rt, kh, m, lane)) = a[m];
+    if constexpr (PLUG) mplug_patch_lds(A.plug, P, rowpos, k0 + 8 * q, k0, lds + pc_aoff(s & 1, rt, kh, 0, lane), 1024u);
   };
   // C[k % G] holds super-step k.  Prologue: super-step 0 into operand buffer 0, its code
   // buffer refilled with super-step G.
