@@ -164,7 +164,7 @@ __device__ __forceinline__ void mfma_body(const char* lds, const QuadMfmaArgs& A
     P.next = rowok && A.plug_n > 0 ? A.row_plug[(int64_t)n * A.slices + sl] : 0;
     P.end = rowok && A.plug_n > 0 ? A.row_plug[(int64_t)n * A.slices + sl + 1] : 0;
     const int64_t rowpos = A.pos0 + (int64_t)n * A.ldc;
-    uint32_t pidx[4];
+    uint32_t pidx[MPW];
     mplug_issue(PlugSrc{A.plug_idx, A.plug_vals, A.plug_n}, P, pidx);
     MStage<T> s0, s1;
     mstage_issue<T>(A, ctile, nrows, voc, vox, kb, s0);
