@@ -347,6 +347,219 @@ __global__ __launch_bounds__(DM_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
   else dm_body<TT, false, false>(T, A);
 }
 
+// ------------------------------------------------------------ producer/consumer form
+// From 65 tokens on the rows the transposing loads take (no plug table, N % 16 == 0, N a
+// multiple of the group size, 16-byte aligned rows): a workgroup of 8 waves takes 64 output
+// columns x a block of 64 TT tokens (TT = 2 or 4, dpc_tt) x one K slice.  Waves 0-3 decode
+// (producers): per 32-row super-step wave p loads column tile p's 16 columns x 32 rows (lane
+// l: row l/2, columns 8(l%2) .. +7, one 16-byte load and one group scale, codes loaded
+// DPC_G super-steps ahead), decodes them as the transposing loads do and stores the two
+// models' fp16 weights transposed into LDS as the MFMA A operands.  Waves 4-7 multiply
+// (consumers): wave c takes the TT token tiles 16 TT c .. of the block with the previous
+// super-step's 4 x 2 operands.  One of each per SIMD, so a SIMD's decode and its products
+// come from two waves; two 8 KiB operand buffers alternate with one barrier per
+// super-step.  Each code is decoded once per 64 TT tokens (the one-wave form: once per 16
+// TT, with its x reloaded by every 16-column tile).
+constexpr int DPC_COLS = 64, DPC_G = 4, DPC_NT = 512;
+constexpr uint32_t DPC_ABUF = DLDS_BYTES, DPC_ABYTES = 0x2000;   // [tile 4][model 2][lane 64] x 16 B
+constexpr uint32_t DPC_LDS = DPC_ABUF + 2 * DPC_ABYTES;
+static_assert(DPC_LDS <= 160 * 1024, "the tables and both operand buffers must fit in LDS");
+
+__device__ __forceinline__ uint32_t dpc_aoff(int buf, int ct, int m, int lane) {
+  return DPC_ABUF + (uint32_t)buf * DPC_ABYTES + (uint32_t)(((ct * 2 + m) * 64 + lane) * 16);
+}
+
+// Super-steps of a slice, rounded up to whole rounds of DPC_G (the producers' code
+// buffers rotate with the super-step; super-steps past the slice read zero codes and x).
+__device__ __forceinline__ int dpc_steps(int kb, int ke) { return ((ke - kb + 31) / 32 + DPC_G - 1) / DPC_G * DPC_G; }
+
+struct DpcCodes {
+  u32x4 c;                 // 8 stored codes of the lane's row
+  uint32_t sc;             // their group scale (fp16 bits)
+};
+
+__device__ __forceinline__ void dpc_load(const DualMfmaArgs& A, int n0, bool ok, int k0, int ke, uint32_t voc,
+                                         uint32_t vos, DpcCodes& C) {
+  const bool live = ok && k0 < ke;
+  const int kc = min(k0, A.K - 32);
+  const rsrc_t rc = make_rsrc(A.codes + (int64_t)kc * A.ldk + n0,
+                              live ? 2u * (uint32_t)((int64_t)(A.K - 1 - kc) * A.ldk + (A.N - n0)) : 0u);
+  C.c = __builtin_amdgcn_raw_buffer_load_b128(rc, (int)voc, 0, NT_AUX);
+  const int64_t g0 = (int64_t)kc * A.gcols;
+  vload16(C.sc, vos, make_rsrc(A.scales + g0, live ? 2u * (uint32_t)(A.n_groups - g0) : 0u));
+}
+
+__device__ __forceinline__ void dpc_producer(char* lds, const DualMfmaArgs& A, int p, int n0b, int kb, int ke) {
+  const int lane = threadIdx.x & 63;
+  const DualLane lo = dual_lane(lane);
+  const int kr = lane >> 1, nh = 8 * (lane & 1);
+  const int n0 = n0b + 16 * p;
+  const bool ok = n0 < A.N;              // N % 16 == 0: a column tile is whole or past N
+  const uint32_t voc = 2u * (uint32_t)(kr * A.ldk + nh);
+  const uint32_t vos = 2u * (uint32_t)(kr * A.gcols + ((min(n0, A.N - 16) + nh) >> A.log2gs));
+  // the lane's 8 weights of row kr go to operand lanes nh + j + 16 (kr / 8), element kr % 8
+  const uint32_t wofs = (uint32_t)((nh + 16 * (kr >> 3)) * 16 + 2 * (kr & 7));
+  const int ns = dpc_steps(kb, ke);
+  DpcCodes C[DPC_G];
+#pragma unroll
+  for (int g = 0; g + 1 < DPC_G; ++g) dpc_load(A, n0, ok, kb + 32 * g, ke, voc, vos, C[g]);
+  auto decode = [&](const DpcCodes& c, int s) {
+    const float sc = h2f(c.sc);
+    const uint32_t w4[4] = {c.c.x, c.c.y, c.c.z, c.c.w};
+    char* dst = lds + dpc_aoff(s & 1, p, 0, 0) + wofs;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float an[2];
+      float2 cs[2];
+      dual_lookup2<PP_DUAL_I16_OFFSET>(lds, w4[e], lo, an, cs);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float amp = an[h] * sc;
+        // the float32 product, then fp16, as the reference rounds its operands (hidden from
+        // the compiler, which would fold the two into one mixed-precision multiply)
+        float w1 = amp * cs[h].x, w2 = amp * cs[h].y;
+        asm volatile("" : "+v"(w1), "+v"(w2));
+        *reinterpret_cast<_Float16*>(dst + 16 * (2 * e + h)) = (_Float16)w1;
+        *reinterpret_cast<_Float16*>(dst + 1024 + 16 * (2 * e + h)) = (_Float16)w2;
+      }
+    }
+  };
+  // C[k % G] holds super-step k.  Prologue: super-step 0 into operand buffer 0, its code
+  // buffer refilled with super-step G.
+  dpc_load(A, n0, ok, kb + 32 * (DPC_G - 1), ke, voc, vos, C[DPC_G - 1]);
+  decode(C[0], 0);
+  dpc_load(A, n0, ok, kb + 32 * DPC_G, ke, voc, vos, C[0]);
+  __syncthreads();
+  for (int s = 0; s < ns; s += DPC_G) {
+#pragma unroll
+    for (int g = 0; g < DPC_G; ++g) {
+      // while the consumers multiply super-step s + g, decode d = s + g + 1 into the other
+      // operand buffer and refill its code buffer with d + G
+      const int d = s + g + 1;
+      decode(C[(g + 1) % DPC_G], d);
+      dpc_load(A, n0, ok, kb + 32 * (d + DPC_G), ke, voc, vos, C[(g + 1) % DPC_G]);
+      __syncthreads();
+    }
+  }
+}
+
+template <int TT>
+__device__ __forceinline__ void dpc_consumer(const char* lds, const DualMfmaArgs& A, int c, int n0b, int j0b, int kb,
+                                             int ke) {
+  const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+  const int j0 = j0b + 16 * TT * c;
+  const int jx = min(j0, A.M - 1);
+  const f16* xblk = A.x + (int64_t)jx * A.x_sm;
+  uint32_t vox[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const int jl = 16 * t + i;
+    vox[t] = j0 + jl < A.M ? 2u * (uint32_t)(jl * A.x_sm + 8 * q) : OOB;
+  }
+  const int ns = dpc_steps(kb, ke);
+  df4 Cacc[4][2][TT];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) Cacc[ct][m][t] = df4{0.f, 0.f, 0.f, 0.f};
+  u32x4 X[2][TT];
+  auto loadx = [&](u32x4(&xb)[TT], int s) {
+    const int k0 = kb + 32 * s;
+    const uint32_t rec = k0 < ke ? 2u * (uint32_t)((int64_t)(A.M - 1 - jx) * A.x_sm + (ke - k0)) : 0u;
+    const rsrc_t rx = make_rsrc(xblk + min(k0, A.K - 32), rec);
+#pragma unroll
+    for (int t = 0; t < TT; ++t) vload128c(xb[t], vox[t], rx);
+  };
+  // the 8 operands of a super-step are read in 4 pairs (column tile) of the 2 models; pair
+  // ct + 1 is requested before pair ct's products
+  auto multiply = [&](const u32x4(&xb)[TT], int s) {
+    dh8 a[2][2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) a[0][m] = *reinterpret_cast<const dh8*>(lds + dpc_aoff(s & 1, 0, m, lane));
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      if (ct < 3) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+          a[(ct + 1) & 1][m] = *reinterpret_cast<const dh8*>(lds + dpc_aoff(s & 1, ct + 1, m, lane));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+          Cacc[ct][m][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ct & 1][m], __builtin_bit_cast(dh8, xb[t]),
+                                                                  Cacc[ct][m][t], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  loadx(X[0], 0);
+  __syncthreads();
+  // the fences keep the next super-step's x loads issued ahead of this one's products
+  for (int s = 0; s < ns; s += 2) {
+    loadx(X[1], s + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    multiply(X[0], s);
+    __syncthreads();
+    loadx(X[0], s + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    multiply(X[1], s + 1);
+    __syncthreads();
+  }
+  // lane holds columns n0b + 16 ct + 4q + r, r = 0..3, of token j0 + 16t + i
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        const int j = j0 + 16 * t + i;
+        const int nn = n0b + 16 * ct + 4 * q;
+        const df4 v = Cacc[ct][m][t];
+        if (j >= A.M || nn >= A.N) continue;
+        if (A.slices == 1) {
+          f16* o = A.out[m] + (int64_t)j * A.o_sm + nn;
+          if (A.vec_out) {    // N % 16 == 0: the 4 columns are in range
+            const f16x4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+            *reinterpret_cast<f16x4*>(o) = h;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[r] = (f16)v[r];
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            __hip_atomic_fetch_add(A.acc + ((int64_t)m * A.N + nn + r) * A.M + j, v[r], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+}
+
+template <int TT>
+__global__ __launch_bounds__(DPC_NT) void dual_pc_kernel(const DualMfmaArgs A) {
+  __shared__ __attribute__((aligned(16))) char T[DPC_LDS];
+  if (A.luts.dtype == PP_F16) dual_tables_of<DPC_NT, PP_DUAL_I16_OFFSET, f16>(T, A.luts);
+  else dual_tables_of<DPC_NT, PP_DUAL_I16_OFFSET, float>(T, A.luts);
+  const int wave = uniform(threadIdx.x >> 6);
+  int b = blockIdx.x;
+  if (A.xcd_remap) b = (b & 7) * (int)(gridDim.x >> 3) + (b >> 3);
+  // items ordered slice, token block, column block: consecutive workgroups (one XCD after
+  // the remap) share token blocks (x) and slices
+  const int cblocks = (A.N + DPC_COLS - 1) / DPC_COLS;
+  const int64_t items = (int64_t)cblocks * A.tblocks * A.slices;
+  for (int64_t it = b; it < items; it += gridDim.x) {
+    const int cb = (int)uniform64(it % cblocks);
+    const int64_t w = it / cblocks;
+    const int tb = (int)uniform64(w % A.tblocks), sl = (int)uniform64(w / A.tblocks);
+    const int n0b = cb * DPC_COLS, j0b = tb * 64 * TT;
+    const int kb = sl * A.ks, ke = min(A.K, kb + A.ks);
+    if (wave < 4) dpc_producer(T, A, wave, n0b, kb, ke);
+    else dpc_consumer<TT>(T, A, wave - 4, n0b, j0b, kb, ke);
+  }
+}
+
 // Sliced launches: out_m[j, n] = fp16(acc[m][n][j]), acc left zero (finish_tile).
 __global__ __launch_bounds__(256) void dual_mfma_finish_kernel(float* acc, f16* o0, f16* o1, int64_t o_sm, int N,
                                                                int M, bool vec) {
@@ -575,7 +788,32 @@ __global__ __launch_bounds__(DM_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 
 static int dm_tt(int64_t M) { return M <= 32 ? 2 : M <= 64 ? 4 : 8; }
 
+// Token tiles per consumer of the producer/consumer form: 128-token blocks (TT = 2) to 255
+// tokens, and above where 256-token blocks would fill at most half the CUs while 128-token
+// ones fill them all; 256 otherwise.
+static int dpc_tt(int64_t M, int64_t N) {
+  if (M < 256) return 2;
+  const int64_t cus = device_cu_count(), cb = (N + DPC_COLS - 1) / DPC_COLS;
+  const int64_t g4 = cb * ((M + 255) / 256), g2 = cb * ((M + 127) / 128);
+  return 2 * g4 <= cus && g2 >= cus ? 2 : 4;
+}
+
+// Its K slices: only when the items would leave more than half the CUs idle, into as few as
+// fill them (whole pairs of 32-row steps).
+static void dpc_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* cols) {
+  const int64_t cus = device_cu_count(), tok = 64 * dpc_tt(M, N);
+  const int64_t groups = (N + DPC_COLS - 1) / DPC_COLS * ((M + tok - 1) / tok);
+  int64_t s = 1;
+  if (2 * groups <= cus) s = std::max<int64_t>(1, std::min<int64_t>(K / 64, (cus + groups - 1) / groups));
+  const int64_t c = ((K + s - 1) / s + 63) / 64 * 64;
+  *cols = c;
+  *slices = (K + c - 1) / c;
+}
+
+// From 65 tokens the plan is the producer/consumer form's (the one-wave form, which takes
+// plug tables and the other layouts at these sizes, runs any plan).
 static void dm_plan(int64_t M, int64_t N, int64_t K, int64_t* slices, int64_t* cols) {
+  if (M >= 65) return dpc_plan(M, N, K, slices, cols);
   const int64_t waves = (int64_t)device_cu_count() * DM_WAVES;
   const int64_t units = ((N + 15) / 16) * ((M + 16 * dm_tt(M) - 1) / (16 * dm_tt(M)));
   int64_t s = std::max<int64_t>(1, std::min<int64_t>(K / 64, waves / std::max<int64_t>(1, units)));
@@ -668,14 +906,24 @@ extern "C" int pp_dual_mfma(const void* codes, int64_t ldk, const void* a, int64
   A.ppos0 = plug_pos0;
   A.pld = plug_ld;
   A.acc = reinterpret_cast<float*>(workspace);
-  const int64_t groups = (int64_t)(A.tiles + DM_WAVES - 1) / DM_WAVES * A.tblocks * slices;
-  const int64_t grid = std::min<int64_t>(device_cu_count(), groups);
-  A.xcd_remap = grid % 8 == 0;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  switch (tt) {
-    case 2: hipLaunchKernelGGL(dual_mfma_kernel<2>, dim3((unsigned)grid), dim3(DM_NT), 0, st, A); break;
-    case 4: hipLaunchKernelGGL(dual_mfma_kernel<4>, dim3((unsigned)grid), dim3(DM_NT), 0, st, A); break;
-    default: hipLaunchKernelGGL(dual_mfma_kernel<8>, dim3((unsigned)grid), dim3(DM_NT), 0, st, A); break;
+  if (M >= 65 && A.gcols > 0) {
+    const int ptt = dpc_tt(M, N);
+    A.tblocks = (int)((M + 64 * ptt - 1) / (64 * ptt));
+    const int64_t items = (N + DPC_COLS - 1) / DPC_COLS * A.tblocks * slices;
+    const int64_t grid = std::min<int64_t>(device_cu_count(), items);
+    A.xcd_remap = grid % 8 == 0;
+    if (ptt == 2) hipLaunchKernelGGL(dual_pc_kernel<2>, dim3((unsigned)grid), dim3(DPC_NT), 0, st, A);
+    else hipLaunchKernelGGL(dual_pc_kernel<4>, dim3((unsigned)grid), dim3(DPC_NT), 0, st, A);
+  } else {
+    const int64_t groups = (int64_t)(A.tiles + DM_WAVES - 1) / DM_WAVES * A.tblocks * slices;
+    const int64_t grid = std::min<int64_t>(device_cu_count(), groups);
+    A.xcd_remap = grid % 8 == 0;
+    switch (tt) {
+      case 2: hipLaunchKernelGGL(dual_mfma_kernel<2>, dim3((unsigned)grid), dim3(DM_NT), 0, st, A); break;
+      case 4: hipLaunchKernelGGL(dual_mfma_kernel<4>, dim3((unsigned)grid), dim3(DM_NT), 0, st, A); break;
+      default: hipLaunchKernelGGL(dual_mfma_kernel<8>, dim3((unsigned)grid), dim3(DM_NT), 0, st, A); break;
+    }
   }
   PP_LAUNCH_CHECK();
   if (slices > 1) {

@@ -40,16 +40,19 @@ def to_dev(*arrs):
     return [torch.from_numpy(np.ascontiguousarray(x)).to(DEV) for x in arrs]
 
 
-@pytest.mark.parametrize("M", [9, 16, 32, 33, 64, 65, 128, 200])
+@pytest.mark.parametrize("M", [9, 16, 32, 33, 64, 65, 128, 200, 300])
 @pytest.mark.parametrize("K,N,plug,gs", [(1024, 384, 0, 32), (2048, 1000, 500, 32), (512, 4096, 300, 64),
-                                         (96, 40, 40, 8), (256, 512, 0, 64), (512, 400, 0, 32), (128, 64, 0, 8)])
+                                         (96, 40, 40, 8), (256, 512, 0, 64), (512, 400, 0, 32), (128, 64, 0, 8),
+                                         (320, 208, 0, 16)])
 def test_kernel_layout_matches_oracle(K, N, plug, gs, M):
     """Several shapes (N not a multiple of 16, K = 96: one padded step), group sizes 8-64,
-    plug amplitudes at random positions, 9-200 tokens (16-token tiles of 2, 4 or 8; one to
+    plug amplitudes at random positions, 9-300 tokens (16-token tiles of 2, 4 or 8; one to
     two token blocks; K slices for the small batches), forced with fused=True above the
     operator's default range.  Without plug entries and with N a multiple of 16 and of the
     group size the kernel loads rows of 8 codes and transposes them through LDS (N = 400
-    with 32-pair groups takes the column loads)."""
+    with 32-pair groups takes the column loads); from 65 tokens those rows go to the
+    producer/consumer workgroups (64-column blocks: N = 208 ends in a partial block, K = 320
+    in K slices of whole and partial super-steps; 128- and 256-token blocks)."""
     seed = K * 3 + N + plug + M + gs
     packed, bmax, amp_lut, cos_lut, sin_lut = layer(K, N, seed, gs)
     rng = np.random.default_rng(seed)
