@@ -361,12 +361,20 @@ __global__ __launch_bounds__(DM_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 // super-step.  Each code is decoded once per 64 TT tokens (the one-wave form: once per 16
 // TT, with its x reloaded by every 16-column tile).
 constexpr int DPC_COLS = 64, DPC_G = 4, DPC_NT = 512;
-constexpr uint32_t DPC_ABUF = DLDS_BYTES, DPC_ABYTES = 0x2000;   // [tile 4][model 2][lane 64] x 16 B
+// An operand block (one column tile, one model) holds lane l's 16 bytes at slot l + l / 8
+// (16 bytes of padding after every 8 lanes), so the producers' 2-byte stores of one
+// instruction, which go to lanes 8 and 16 apart, fall in different banks.
+#ifndef PP_DPC_PAD
+#define PP_DPC_PAD 1
+#endif
+constexpr uint32_t DPC_MBLK = PP_DPC_PAD ? 72 * 16 : 64 * 16;
+constexpr uint32_t DPC_ABUF = DLDS_BYTES, DPC_ABYTES = 8 * DPC_MBLK;   // [tile 4][model 2] blocks
 constexpr uint32_t DPC_LDS = DPC_ABUF + 2 * DPC_ABYTES;
 static_assert(DPC_LDS <= 160 * 1024, "the tables and both operand buffers must fit in LDS");
 
+__device__ __forceinline__ uint32_t dpc_slot(int lane) { return 16u * (uint32_t)(lane + (PP_DPC_PAD ? lane >> 3 : 0)); }
 __device__ __forceinline__ uint32_t dpc_aoff(int buf, int ct, int m, int lane) {
-  return DPC_ABUF + (uint32_t)buf * DPC_ABYTES + (uint32_t)(((ct * 2 + m) * 64 + lane) * 16);
+  return DPC_ABUF + (uint32_t)buf * DPC_ABYTES + (uint32_t)(ct * 2 + m) * DPC_MBLK + dpc_slot(lane);
 }
 
 // Super-steps of a slice, rounded up to whole rounds of DPC_G (the producers' code
@@ -398,7 +406,8 @@ __device__ __forceinline__ void dpc_producer(char* lds, const DualMfmaArgs& A, i
   const uint32_t voc = 2u * (uint32_t)(kr * A.ldk + nh);
   const uint32_t vos = 2u * (uint32_t)(kr * A.gcols + ((min(n0, A.N - 16) + nh) >> A.log2gs));
   // the lane's 8 weights of row kr go to operand lanes nh + j + 16 (kr / 8), element kr % 8
-  const uint32_t wofs = (uint32_t)((nh + 16 * (kr >> 3)) * 16 + 2 * (kr & 7));
+  // (j < 8: their slots are consecutive)
+  const uint32_t wofs = dpc_slot(nh + 16 * (kr >> 3)) + 2u * (uint32_t)(kr & 7);
   const int ns = dpc_steps(kb, ke);
   DpcCodes C[DPC_G];
 #pragma unroll
@@ -420,7 +429,7 @@ __device__ __forceinline__ void dpc_producer(char* lds, const DualMfmaArgs& A, i
         float w1 = amp * cs[h].x, w2 = amp * cs[h].y;
         asm volatile("" : "+v"(w1), "+v"(w2));
         *reinterpret_cast<_Float16*>(dst + 16 * (2 * e + h)) = (_Float16)w1;
-        *reinterpret_cast<_Float16*>(dst + 1024 + 16 * (2 * e + h)) = (_Float16)w2;
+        *reinterpret_cast<_Float16*>(dst + DPC_MBLK + 16 * (2 * e + h)) = (_Float16)w2;
       }
     }
   };

@@ -14,8 +14,10 @@ Same names, arguments, return values and error behaviour as the reference
 
 The kernel of a call comes from one table, :data:`polar_pack_amd.routes.DUAL_ROUTES`:
 batches of 1-4 tokens (1-8 on the (K,N) kernel layout) run on the fused decode kernels;
-2-64 tokens on the int16 (K,N) kernel layout on the matrix-core decode (pp_dual_mfma), 5-64
-on container (N,K) rows on its (N,K) form (pp_dual_nk_mfma); larger ones decode once into fp16 weights (the values the reference's kernel rounds its
+2-64 tokens on the int16 (K,N) kernel layout on the matrix-core decode (pp_dual_mfma; to 128
+without a plug table on rows it loads 8 codes at a time, its producer/consumer form from 65),
+5-64 on container (N,K) rows on its (N,K) form (pp_dual_nk_mfma); larger ones decode once
+into fp16 weights (the values the reference's kernel rounds its
 weights to, polar_kernels.py:78-82) and run a library fp16 GEMM (hipBLASLt through
 torch.matmul).
 """

@@ -56,13 +56,14 @@ class Route:
     m_hi: int                                             # inclusive
     plug: Tuple[bool, ...] = ANY_PLUG
     fused: Tuple[Optional[bool], ...] = ANY_FUSED
+    cap: Optional[str] = None                             # a further capability the storage must have
 
     def lo(self, K: int, N: int, has_plug: bool) -> int:
         return self.m_lo(K, N, has_plug) if callable(self.m_lo) else self.m_lo
 
     def matches(self, caps: FrozenSet[str], M: int, K: int, N: int, has_plug: bool, fused) -> bool:
-        return (self.kernel in caps and has_plug in self.plug and fused in self.fused
-                and self.lo(K, N, has_plug) <= M <= self.m_hi)
+        return (self.kernel in caps and (self.cap is None or self.cap in caps) and has_plug in self.plug
+                and fused in self.fused and self.lo(K, N, has_plug) <= M <= self.m_hi)
 
 
 def kn_big_min_m(K: int, N: int, has_plug: bool) -> int:
@@ -166,6 +167,10 @@ DUAL_ROUTES = (
     Route("dual_mfma", 1, INF, fused=(True,)),
     # from 96 tokens the fp16 decode + one batched GEMM is faster (4096x4096: 52 against 66 us)
     Route("dual_mfma", dual_mfma_min_m, 64, fused=(None,)),
+    # 65-128 tokens on the rows its producer/consumer form reads (no plug table, N a multiple
+    # of 16 and of the group size, 16-byte rows): 4096x4096 at 65 / 128 / 192 tokens 46 / 43 /
+    # 60 us against 53 / 53 / 54 us for the fp16 decode + one batched GEMM
+    Route("dual_mfma", 65, 128, plug=(False,), fused=(None,), cap="dual_pc"),
     Route("dual_nk_mfma", 1, INF, fused=(True,)),
     Route("dual_kn", 1, 8),
     # container rows, no plug table, graph-replayed per Linear: 2048x2048 at 1 token 12.8
@@ -195,6 +200,10 @@ def dual_storage(c_sk: int, c_sn: int, ptr: int, K: int, N: int, layout: str, gr
     if kn and layout == "i16" and K % 32 == 0 and K * c_sk * 2 < (1 << 31) and n_groups * 2 < (1 << 31) \
             and plug_n < (1 << 29):
         caps.add("dual_mfma")
+        # rows of 8 codes per 16-byte load (pp_dual_mfma's transposing loads and its
+        # producer/consumer form): dual_mfma.hip's gcols condition
+        if plug_n == 0 and N % 16 == 0 and N % group_size == 0 and c_sk % 8 == 0 and a16:
+            caps.add("dual_pc")
     if c_sk == 1 and c_sn % 8 == 0 and c_sn >= K and K % 8 == 0 and K > 0 and a16 and chunk_size > 0 \
             and chunk_size % 8 == 0 and gs_ok and elem_base % 8 == 0:
         caps.add("dual_rows")

@@ -89,9 +89,11 @@ def dnk(K, N, ptr=256, elem_base=0):
 
 
 DUAL_TABLE = [
-    (dkn(2048, 512), (False,), None, "dual_kn:1-1 dual_mfma:2-64 prefill:65-"),
+    (dkn(2048, 512), (False,), None, "dual_kn:1-1 dual_mfma:2-128 prefill:129-"),
+    (dkn(2048, 520), (False,), None, "dual_kn:1-1 dual_mfma:2-64 prefill:65-"),      # N % 16 != 0
     (dkn(2048, 512), (True,), None, "dual_kn:1-4 dual_mfma:5-64 prefill:65-"),
-    (dkn(512, 2048), (False, True), None, "dual_kn:1-4 dual_mfma:5-64 prefill:65-"),
+    (dkn(512, 2048), (False,), None, "dual_kn:1-4 dual_mfma:5-128 prefill:129-"),
+    (dkn(512, 2048), (True,), None, "dual_kn:1-4 dual_mfma:5-64 prefill:65-"),
     (dkn(2048, 512), (False, True), True, "dual_mfma:1-"),
     (dkn(2048, 512), (False, True), False, "dual_kn:1-8 prefill:9-"),
     (dict(dkn(2048, 512), layout="u16be"), (False, True), None, "dual_kn:1-8 prefill:9-"),
