@@ -360,7 +360,10 @@ __global__ __launch_bounds__(DM_NT) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 // come from two waves; two 8 KiB operand buffers alternate with one barrier per
 // super-step.  Each code is decoded once per 64 TT tokens (the one-wave form: once per 16
 // TT, with its x reloaded by every 16-column tile).
-constexpr int DPC_COLS = 64, DPC_G = 4, DPC_NT = 512;
+#ifndef PP_DPC_G
+#define PP_DPC_G 4
+#endif
+constexpr int DPC_COLS = 64, DPC_G = PP_DPC_G, DPC_NT = 512;
 // An operand block (one column tile, one model) holds lane l's 16 bytes at slot l + l / 8
 // (16 bytes of padding after every 8 lanes), so the producers' 2-byte stores of one
 // instruction, which go to lanes 8 and 16 apart, fall in different banks.

@@ -317,7 +317,10 @@ __attribute__((amdgpu_waves_per_eu(QbCfg<TT, KN>::WPE, QbCfg<TT, KN>::WPE))) voi
 // 64 tokens (the drop-in operator takes pp_quad_mfma there).
 static bool pc_use(int64_t M, bool kn) { return M >= 65 || (kn && M >= 33); }
 constexpr int PC_ROWS = 32, PC_NT = 512;
-constexpr int PC_G = 4;                                   // code buffers of a producer
+#ifndef PP_PC_G
+#define PP_PC_G 4
+#endif
+constexpr int PC_G = PP_PC_G;                             // code buffers of a producer
 // The operand buffers come first in LDS, so that every operand access is one lane base plus
 // an immediate offset (below 64 KiB); the tables follow.
 constexpr uint32_t PC_ABUF = 0, PC_ABYTES = 0x4000;       // [rt 2][kh 2][m 4][lane 64] x 16 B
@@ -328,10 +331,10 @@ __device__ __forceinline__ uint32_t pc_aoff(int buf, int rt, int kh, int m, int 
   return PC_ABUF + (uint32_t)buf * PC_ABYTES + (uint32_t)((((rt * 2 + kh) * 4 + m) * 64 + lane) * 16);
 }
 
-// An item's super-steps, rounded up to whole rounds of 4 (the producers' code buffers and
+// An item's super-steps, rounded up to whole rounds of PC_G (the producers' code buffers and
 // the consumers' x buffers rotate with the super-step; super-steps past the slice read
 // zero x, so their products add nothing).
-__device__ __forceinline__ int pc_steps(int kb, int ke) { return ((ke - kb + 63) / 64 + 3) / 4 * 4; }
+__device__ __forceinline__ int pc_steps(int kb, int ke) { return ((ke - kb + 63) / 64 + PC_G - 1) / PC_G * PC_G; }
 
 template <bool KN, bool PLUG>
 __device__ __forceinline__ void pc_producer(char* lds, const QuadBigArgs& A, int p, int n0b, int kb, int ke, int sl) {
