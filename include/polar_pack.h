@@ -412,7 +412,8 @@ int pp_dual_gemm_kernel(const void* a, int64_t a_sm, int64_t a_sk, const void* c
                         int64_t M, int64_t N, int64_t K);
 
 /*
- * Dual decode GEMM on the matrix cores for batches (used for 5-64 tokens): the
+ * Dual decode GEMM on the matrix cores for batches (used for 5-64 tokens, and to 128 on
+ * rows of the layout below): the
  * product of polar_dual_bitpacked (polar_kernels.py:27-115) on the int16 (K,N) codes that
  * quantize_polar_bitpacked returns (row k at codes + k*ldk, ldk >= N; stored = code - 32768;
  * group scales bmax[(k*N + n) / group_size], group_size a power of two), each weight rounded
@@ -424,7 +425,10 @@ int pp_dual_gemm_kernel(const void* a, int64_t a_sm, int64_t a_sk, const void* c
  * is the first entry at or after plug_pos0 + n*plug_ld + s*slice_cols, the last one
  * plug_pos0 + N*plug_ld.  slices / slice_cols from pp_dual_mfma_plan; with slices > 1 the
  * workspace (pp_dual_mfma_workspace_size bytes) holds float32 partial sums: zero before the
- * first call, left zero by every call; calls that share it must not overlap.
+ * first call, left zero by every call; calls that share it must not overlap (16-byte
+ * aligned).  From 65 tokens, without plug entries, with N a multiple of 16 and of
+ * group_size and 16-byte aligned rows, the product runs on producer/consumer workgroups;
+ * pp_dual_mfma_plan then returns their plan (any valid plan is accepted either way).
  */
 int pp_dual_mfma(const void* codes, int64_t ldk, const void* a, int64_t a_sm, const void* bmax,
                  int64_t group_size, const void* amp_lut, int amp_n, const void* cos_lut,
