@@ -28,6 +28,7 @@
 // [m][n][j] with device-scope atomics and dual_mfma_finish_kernel writes the outputs and
 // leaves zeros for the next launch.
 #include "dual_lds.h"
+#include "finish_tile.h"
 #include "rows_common.h"
 
 namespace pp {

@@ -5,6 +5,7 @@
 #pragma once
 
 #include "quad_lds.h"
+#include "finish_tile.h"
 #include "rows_common.h"
 
 namespace pp {
