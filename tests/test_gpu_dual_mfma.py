@@ -3,6 +3,8 @@ int16 (K,N) layout quantize_polar_bitpacked returns, from 5 when N > K or with p
 operands the reference's tl.dot takes (the float32 decode (amp_lut * bmax) * cos/sin
 rounded once, plug amplitudes substituted, polar_kernels.py:60-82) within rel 1e-3 plus the
 float32 dot-product bound 2^-18 * sum |w x|, and normwise within 1e-3 of the exact decode."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -10,6 +12,7 @@ import torch
 import gen
 from oracle import layer as olay
 from parity import assert_gemv_close, fp16_weight_bound, normwise
+from polar_pack_amd import _native as nat
 from polar_pack_amd import polar_kernels as pk
 
 pytestmark = pytest.mark.gpu
@@ -96,6 +99,39 @@ def test_wider_row_stride_and_float32_luts(M):
     blk = (pos % ldk) < N
     pl = (pos[blk] // ldk, pos[blk] % ldk, vals[blk])
     check((o1, o2), a, packed_w[:, :N], bmax, *luts32, 32, pl, f"ldk={ldk} M={M}")
+
+
+@pytest.mark.parametrize("M", [96, 300])
+def test_producer_consumer_float32_luts_odd_output_stride(M):
+    """The producer/consumer form (65 tokens and more, no plug table, N a multiple of 16 and
+    of the group size) with float32 LUTs (its tables built from them) and outputs that are
+    column slices of wider buffers (no 4-column stores); the columns past N untouched."""
+    K, N, gs = 384, 144, 16
+    seed = 900 + M
+    packed, bmax, amp_lut, cos_lut, sin_lut = layer(K, N, seed, gs)
+    luts32 = [np.asarray(l, np.float32) for l in (amp_lut, cos_lut, sin_lut)]
+    a = np.random.default_rng(seed).standard_normal((M, K)).astype(np.float16)
+    wide = [torch.full((M, N + 3), float("nan"), dtype=torch.float16, device=DEV) for _ in range(2)]
+    o1, o2 = (w[:, :N] for w in wide)
+    L = nat.lib()
+    slices, cols = (ctypes.c_int64 * 1)(), (ctypes.c_int64 * 1)()
+    nat.check(L.pp_dual_mfma_plan(M, N, K, slices, cols), "pp_dual_mfma_plan")
+    s_, c_ = int(slices[0]), int(cols[0])
+    ws_bytes = L.pp_dual_mfma_workspace_size(M, N, s_)
+    ws = torch.zeros(max(ws_bytes, 16), dtype=torch.uint8, device=DEV)
+    dv = to_dev(a, packed, bmax, *luts32)
+    for rep in range(2):   # the second call reuses the workspace the first left zero
+        rc = L.pp_dual_mfma(dv[1].data_ptr(), N, dv[0].data_ptr(), K, dv[2].data_ptr(), gs, dv[3].data_ptr(),
+                            dv[3].numel(), dv[4].data_ptr(), dv[5].data_ptr(), dv[4].numel(), nat.PP_F32, None, None,
+                            0, None, 0, K, s_, c_, o1.data_ptr(), o2.data_ptr(), N + 3, M, N, K, ws.data_ptr(),
+                            ws_bytes, torch.cuda.current_stream(DEV).cuda_stream)
+        nat.check(rc, "pp_dual_mfma")
+        torch.cuda.synchronize()
+        check((o1, o2), a, packed, bmax, *luts32, gs, None, f"float32 LUTs M={M} rep={rep}")
+        for w in wide:
+            assert bool(torch.isnan(w[:, N:]).all()), "a column past N was written"
+    if ws_bytes:
+        assert int(torch.count_nonzero(ws)) == 0, "the workspace is not left zero"
 
 
 @pytest.mark.parametrize("M", [20, 70])
