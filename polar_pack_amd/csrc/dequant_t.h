@@ -21,20 +21,35 @@ __device__ __forceinline__ uint32_t dqt_off(int n, int k) {
   return (uint32_t)n * 128u + ((((uint32_t)k >> 3) ^ (((uint32_t)n >> 3) & 7u)) << 4) + (((uint32_t)k & 7u) << 1);
 }
 
-// Tiles of the (K, N) code matrix; D.decode8(k, n, v) fills v[m][i] for codes (k, n + i),
-// i < 8 (fp32, final scale applied).  N % 8 == 0 and K % 8 == 0, outputs 16-byte aligned.
+// Tiles of the (K, N) code matrix.  D::load(k, n) fetches what codes (k, n + i), i < 8, need
+// from memory (a D::Raw); D::decode(raw, v) turns it into v[m][i] (fp32, final scale
+// applied).  The next tile's loads are issued before this tile's LDS reads and output
+// stores, so their latency hides behind the stores.  N % 8 == 0 and K % 8 == 0, outputs
+// 16-byte aligned.
 template <int NM, class D>
 __device__ __forceinline__ void dequant_t_tiles(const D& dec, char* tile, int64_t N, int64_t K, f16* const (&out)[NM]) {
   const int t = threadIdx.x;
   const int64_t tn = (N + DQT_T - 1) / DQT_T, tiles = tn * ((K + DQT_T - 1) / DQT_T);
+  const int n8 = (t & 7) * 8;
+  typename D::Raw raw[2];
+  auto fetch = [&](int64_t ti) {
+    if (ti >= tiles) return;
+    const int64_t k0 = (ti / tn) * DQT_T, n0 = (ti % tn) * DQT_T;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int kr = (t >> 3) + 32 * p;
+      if (k0 + kr < K && n0 + n8 < N) raw[p] = dec.load(k0 + kr, n0 + n8);
+    }
+  };
+  fetch(blockIdx.x);
   for (int64_t ti = blockIdx.x; ti < tiles; ti += gridDim.x) {
     const int64_t k0 = (ti / tn) * DQT_T, n0 = (ti % tn) * DQT_T;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      const int kr = (t >> 3) + 32 * p, n8 = (t & 7) * 8;
+      const int kr = (t >> 3) + 32 * p;
       if (k0 + kr < K && n0 + n8 < N) {
         float v[NM][8];
-        dec.decode8(k0 + kr, n0 + n8, v);
+        dec.decode(raw[p], v);
 #pragma unroll
         for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -43,6 +58,7 @@ __device__ __forceinline__ void dequant_t_tiles(const D& dec, char* tile, int64_
       }
     }
     __syncthreads();
+    fetch(ti + gridDim.x);
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll

@@ -142,10 +142,15 @@ struct QuadDequantTArgs {
 struct QuadDecT {
   const QuadLds<1, 1>& T;
   const QuadDequantTArgs& A;
-  __device__ __forceinline__ void decode8(int64_t k, int64_t n, float (&v)[4][8]) const {
+  struct Raw {
+    u32x4 q0, q1;
+  };
+  __device__ __forceinline__ Raw load(int64_t k, int64_t n) const {
     const uint32_t* p = A.codes + k * A.c_sk + n;
-    const u32x4 q0 = *reinterpret_cast<const u32x4*>(p), q1 = *reinterpret_cast<const u32x4*>(p + 4);
-    const uint32_t cw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    return Raw{*reinterpret_cast<const u32x4*>(p), *reinterpret_cast<const u32x4*>(p + 4)};
+  }
+  __device__ __forceinline__ void decode(const Raw& r, float (&v)[4][8]) const {
+    const uint32_t cw[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float w[4];
@@ -325,6 +330,7 @@ extern "C" int pp_quad_dequant_f16_t(const uint32_t* codes, int64_t c_sk, const 
   A.N = N;
   A.K = K;
   const int64_t tiles = ((N + DQT_T - 1) / DQT_T) * ((K + DQT_T - 1) / DQT_T);
+  // 39 KiB of LDS a workgroup: four fit a CU
   const int64_t blocks = std::min<int64_t>(tiles, (int64_t)device_cu_count() * 4);
   hipLaunchKernelGGL(quad_dequant_t_kernel, dim3((unsigned)blocks), dim3(DQT_NT), 0, st, A);
   PP_LAUNCH_CHECK();
