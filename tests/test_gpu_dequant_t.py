@@ -1,6 +1,7 @@
 """GPU parity of the transposing fp16 decodes (pp_quad_dequant_f16_t, pp_dual_dequant_f16_t:
 (K,N) codes -> weights (N,K) for the prefill GEMM) against the (K,N) decodes they transpose,
-bit for bit, with plug entries, partial 64 x 64 tiles and a row stride wider than N; and the
+bit for bit, with plug entries, partial 64 x 64 tiles, a row stride wider than N and more
+tiles than the grid has workgroups; and the
 drop-in operators' prefill routes against the float64 oracle."""
 import numpy as np
 import pytest
@@ -81,6 +82,54 @@ def test_dual_transposed_decode_is_the_transpose(K, N, ldk, plug, gs):
     torch.cuda.synchronize()
     for m in range(2):
         assert torch.equal(got[m].view(torch.int16), ref[m].t().contiguous().view(torch.int16)), f"model {m}"
+
+
+@pytest.mark.parametrize("K,N,ldk", [(4096, 4096, 4096), (4104, 2056, 2064)])
+def test_transposed_decode_many_tiles_per_workgroup(K, N, ldk):
+    """Thousands of 64 x 64 tiles, more than the grid's workgroups: each workgroup walks
+    several, loading the next tile's codes while it stores the current one."""
+    rng = np.random.default_rng(K + N)
+    L = nat.lib()
+    st = torch.cuda.current_stream(DEV).cuda_stream
+    # quad: any uint32 word is a code
+    ws = [torch.from_numpy(w.reshape(64, 64)).to(torch.float16) for w in gen.correlated_models(7, [4096] * 4)]
+    _, luts, scales = olay.pack_quad_layer(*ws)
+    luts = [torch.from_numpy(l).to(DEV) for l in luts]
+    lut_ptrs, lut_dtype = qk._lut_args(luts)
+    codes = torch.randint(-2 ** 31, 2 ** 31, (K, ldk), dtype=torch.int64, device=DEV).to(torch.int32)[:, :N]
+    ref = torch.full((4, K, N), float("nan"), dtype=torch.float16, device=DEV)
+    got = torch.full((4, N, K), float("nan"), dtype=torch.float16, device=DEV)
+    sc = nat.float_array(scales)
+    nat.check(L.pp_quad_dequant_f16(codes.data_ptr(), ldk, 1, lut_ptrs, lut_dtype, sc, None, None, 0, 0,
+                                    nat.ptr_array([ref[m].data_ptr() for m in range(4)]), N, K, st), "quad ref")
+    nat.check(L.pp_quad_dequant_f16_t(codes.data_ptr(), ldk, lut_ptrs, lut_dtype, sc, None, None, 0, 0,
+                                      nat.ptr_array([got[m].data_ptr() for m in range(4)]), N, K, st), "quad t")
+    torch.cuda.synchronize()
+    for m in range(4):
+        assert torch.equal(got[m].view(torch.int16), ref[m].t().contiguous().view(torch.int16)), f"quad model {m}"
+    del ref, got, codes
+    # dual: a quantized 256 x 256 block tiled over the layer (valid amplitude indices),
+    # random positive group scales
+    gs = 32
+    w1, w2 = (torch.from_numpy(w.reshape(256, 256)).to(torch.float16) for w in gen.correlated_models(11, [65536] * 2))
+    packed, _, amp_lut, cos_lut, sin_lut = olay.quantize_polar_bitpacked(w1, w2, group_size=gs)
+    wide = np.tile(np.asarray(packed), (K // 256 + 1, ldk // 256 + 1))[:K, :ldk]
+    codes = torch.from_numpy(np.ascontiguousarray(wide)).to(DEV)[:, :N]
+    bmax = (np.abs(rng.standard_normal(K * N // gs)) * 0.05 + 0.01).astype(np.float16)
+    dl = [torch.from_numpy(np.asarray(x)).to(DEV) for x in (bmax, amp_lut, cos_lut, sin_lut)]
+    ref = torch.full((2, K, N), float("nan"), dtype=torch.float16, device=DEV)
+    got = torch.full((2, N, K), float("nan"), dtype=torch.float16, device=DEV)
+    nat.check(L.pp_dual_dequant_f16(codes.data_ptr(), nat.PP_DUAL_I16_OFFSET, ldk, 1, dl[0].data_ptr(), gs, 0,
+                                    dl[1].data_ptr(), dl[1].numel(), dl[2].data_ptr(), dl[3].data_ptr(), 1024,
+                                    nat.PP_F16, None, None, 0, 0, ref[0].data_ptr(), ref[1].data_ptr(), N, K, st),
+              "dual ref")
+    nat.check(L.pp_dual_dequant_f16_t(codes.data_ptr(), nat.PP_DUAL_I16_OFFSET, ldk, dl[0].data_ptr(), gs,
+                                      dl[1].data_ptr(), dl[1].numel(), dl[2].data_ptr(), dl[3].data_ptr(), 1024,
+                                      nat.PP_F16, None, None, 0, 0, got[0].data_ptr(), got[1].data_ptr(), N, K, st),
+              "dual t")
+    torch.cuda.synchronize()
+    for m in range(2):
+        assert torch.equal(got[m].view(torch.int16), ref[m].t().contiguous().view(torch.int16)), f"dual model {m}"
 
 
 def test_transposed_decode_rejects_bad_shapes():
